@@ -1,0 +1,110 @@
+/*
+ * wsl_lora.h — C ABI of the MI355X (gfx950) fused LoRA linear library (libwsl.so).
+ *
+ * The reference (muchanem/weightshared_torchtitan) has no native boundary for this
+ * path: the LoRA linear is three nn.Linear calls plus a mul and an add inside
+ * Attention.forward. Each entry point below names the reference code it replaces.
+ *
+ * Conventions shared by every entry point:
+ *   - Row-major matrices with an explicit leading dimension (elements between rows);
+ *     the inner dimension is contiguous. Shapes follow nn.Linear: y = x . W^T.
+ *   - The caller owns every buffer. Nothing here allocates or frees device memory;
+ *     scratch space is passed in (see wsl_lora_linear_workspace_bytes).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and is
+ *     stream-ordered. No entry point synchronizes the host.
+ *   - Return value: WSL_OK (0) or a negative WSL_E_* code. Nothing throws across the
+ *     ABI. wsl_last_error() returns a thread-local description of the last failure.
+ *   - bf16 is bfloat16 (1-8-7); fp8 is OCP float8_e4m3fn (bias 7, max 448, no inf).
+ */
+#ifndef WSL_LORA_H
+#define WSL_LORA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WSL_OK 0
+#define WSL_E_INVALID_ARG (-1) /* null pointer where one is required, bad enum   */
+#define WSL_E_SHAPE (-2)       /* negative / inconsistent sizes or leading dims   */
+#define WSL_E_DTYPE (-3)       /* unsupported w_dtype                             */
+#define WSL_E_ALIGN (-4)       /* pointer or leading dimension misaligned         */
+#define WSL_E_WORKSPACE (-5)   /* workspace missing or smaller than required      */
+#define WSL_E_DEVICE (-6)      /* no HIP device, or device is not gfx950          */
+#define WSL_E_LAUNCH (-7)      /* a kernel launch failed                          */
+
+/* Storage type of the base weight W. */
+#define WSL_DTYPE_BF16 0
+#define WSL_DTYPE_FP8_E4M3 1
+
+/* Largest LoRA rank the kernels accept. */
+#define WSL_MAX_RANK 256
+
+/*
+ * Bytes of scratch memory wsl_lora_linear_fwd needs for this problem (may be 0).
+ * Pure host function: touches no device.
+ */
+int wsl_lora_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r,
+                                    int32_t w_dtype, size_t* bytes);
+
+/*
+ * Fused LoRA linear:  y[M,N] = (x . W^T) * diag(w_scale) + scale * (x . A^T) . B^T
+ *
+ * Replaces, for one projection, the reference's
+ *   base  = nn.Linear(K, N)(x)                       torchtitan/models/llama3/model/model.py:257-273,392-394
+ *   delta = w_b(w_a(x)) * (alpha / rank)             torchtitan/models/llama3/model/model.py:189-192
+ *   y     = broadcast_add(base, delta)  (g = 1 case) torchtitan/models/llama3/model/model.py:111-145,396-398
+ *
+ *   x        [M,K] bf16, row stride ldx.
+ *   w        [N,K] bf16 (w_dtype = WSL_DTYPE_BF16) or fp8 e4m3fn (WSL_DTYPE_FP8_E4M3),
+ *            row stride ldw. May be NULL: then y is the LoRA delta alone (the
+ *            reference LoRAModule.forward).
+ *   w_scale  [N] fp32 per-output-channel dequantisation scale. Required for fp8,
+ *            must be NULL for bf16.
+ *   a        [r,K] bf16 (LoRAModule.w_a.weight), row stride lda.
+ *   b        [N,r] bf16 (LoRAModule.w_b.weight), row stride ldb.
+ *            r = 0 (a, b ignored) gives the plain linear.
+ *   scale    LoRA scale s = alpha / rank (2.0 under the reference's alpha = 2*rank).
+ *   y        [M,N] bf16 output, row stride ldy. Must not alias any input.
+ *   Accumulation is fp32. x . A^T is rounded once to bf16 after scaling by s.
+ *   M may be 0 (no work). K >= 1, N >= 1, 0 <= r <= WSL_MAX_RANK.
+ */
+int wsl_lora_linear_fwd(const void* x, int64_t ldx,
+                        const void* w, int64_t ldw, int32_t w_dtype, const float* w_scale,
+                        const void* a, int64_t lda,
+                        const void* b, int64_t ldb,
+                        float scale,
+                        void* y, int64_t ldy,
+                        int64_t M, int64_t N, int64_t K, int64_t r,
+                        void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/*
+ * Factorized embedding:  out[t, :] = E[ids[t], :] . P^T      (k -> hidden)
+ *
+ * Replaces the reference's token embedding nn.Embedding(vocab, dim)
+ * (torchtitan/models/llama3/model/model.py:561, torchtitan/experiments/qwen3/model/model.py:350)
+ * with a rank-k factorisation: E [vocab,k] bf16 (row stride lde), P [hidden,k] bf16
+ * (row stride ldp, nn.Linear(k, hidden).weight layout). out [n_ids, hidden] bf16,
+ * row stride ldo. ids are int64; an id outside [0, vocab) sets that row to zero
+ * (the kernel never reads out of bounds). k <= 1024.
+ */
+int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
+                                 const void* emb, int64_t lde, int64_t vocab, int64_t k,
+                                 const void* proj, int64_t ldp, int64_t hidden,
+                                 void* out, int64_t ldo,
+                                 void* stream);
+
+/* Thread-local, NUL-terminated description of the last error ("" if none). */
+const char* wsl_last_error(void);
+
+/* Library ABI version (major * 100 + minor). */
+int wsl_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WSL_LORA_H */

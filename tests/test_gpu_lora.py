@@ -1,0 +1,247 @@
+"""GPU parity of the fused LoRA linear (prefill, decode and generic paths) against the
+CPU oracle, plus size-independent properties at the benchmark shapes.
+
+Bar: max|y - y_ref| / max|y_ref| <= 1e-2 for the bf16 path and
+<= 3e-2 for the fp8-base path, y_ref = float64 oracle on the same bf16-rounded inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lora_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+FP8_TOL = 3e-2
+
+
+def _inputs(M, N, K, r, seed=0, has_w=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16() if has_w else None
+    A = (torch.randn(r, K, generator=g) * 0.02).bfloat16() if r else None
+    B = (torch.randn(N, r, generator=g) * 0.02).bfloat16() if r else None
+    return x, W, A, B
+
+
+def _np(t):
+    return None if t is None else t.float().numpy()
+
+
+def _gpu(t, dev):
+    return None if t is None else t.to(dev)
+
+
+def _run(dev, x, W, A, B, s, w_scale=None):
+    import weightshared_torchtitan_amd as wsl
+    y = wsl.lora_linear(_gpu(x, dev), _gpu(W, dev), _gpu(A, dev), _gpu(B, dev), s,
+                        w_scale=_gpu(w_scale, dev))
+    torch.cuda.synchronize()
+    return y.cpu()
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+PREFILL_CASES = [
+    # M, N, K, r, s, has_w
+    (2048, 1024, 1024, 16, 2.0, True),   # BASELINE config 1 shape
+    (512, 2048, 1024, 32, 2.0, True),
+    (300, 520, 192, 24, 2.0, True),      # M, N tails, odd rank
+    (256, 256, 64, 8, 2.0, True),        # reference default rank 8, one K tile
+    (1000, 768, 512, 64, 2.0, True),     # largest in-kernel rank
+    (640, 512, 256, 128, 1.0, True),     # pre-pass rank, scale 1
+    (320, 384, 256, 256, 2.0, True),     # WSL_MAX_RANK
+    (384, 1024, 512, 0, 2.0, True),      # plain linear
+    (400, 640, 320, 32, 2.0, False),     # delta only (LoRAModule.forward)
+    (65, 1024, 1024, 32, 2.0, True),     # just above the decode cut-over
+]
+
+
+@pytest.mark.parametrize("M,N,K,r,s,has_w", PREFILL_CASES)
+def test_prefill_parity(gpu, M, N, K, r, s, has_w):
+    _say(f"[prefill] M={M} N={N} K={K} r={r} s={s} has_w={has_w}")
+    x, W, A, B = _inputs(M, N, K, r, seed=M + N + K + r, has_w=has_w)
+    y = _run(gpu, x, W, A, B, s)
+    ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), s)
+    err = O.max_rel_err(y.float().numpy(), ref)
+    _say(f"  max_rel_err={err:.3e}")
+    assert np.isfinite(err) and err <= BF16_TOL
+
+
+DECODE_CASES = [
+    (1, 2048, 2048, 64, 2.0, True),
+    (8, 2048, 2048, 64, 2.0, True),
+    (32, 1024, 2048, 64, 2.0, True),
+    (64, 6144, 2048, 64, 2.0, True),
+    (64, 2048, 6144, 64, 2.0, True),
+    (3, 1000, 1024, 16, 2.0, True),      # N not a multiple of the row group
+    (17, 512, 512, 8, 2.0, True),
+    (49, 768, 1024, 40, 2.0, True),
+    (8, 4096, 256, 0, 2.0, True),        # r = 0, direct-write path
+    (5, 640, 1024, 32, 2.0, False),      # delta only
+    (16, 1024, 1024, 256, 2.0, True),    # max rank
+]
+
+
+@pytest.mark.parametrize("M,N,K,r,s,has_w", DECODE_CASES)
+def test_decode_parity(gpu, M, N, K, r, s, has_w):
+    _say(f"[decode] M={M} N={N} K={K} r={r} s={s} has_w={has_w}")
+    x, W, A, B = _inputs(M, N, K, r, seed=7 * M + N + K + r, has_w=has_w)
+    y = _run(gpu, x, W, A, B, s)
+    ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), s)
+    err = O.max_rel_err(y.float().numpy(), ref)
+    _say(f"  max_rel_err={err:.3e}")
+    assert np.isfinite(err) and err <= BF16_TOL
+
+
+GENERIC_CASES = [
+    (70, 100, 100, 5, 2.0),    # K % 64 != 0, odd rank -> generic path
+    (3, 33, 40, 3, 2.0),       # tiny decode-size, odd everything
+    (129, 64, 72, 12, 2.0),
+]
+
+
+@pytest.mark.parametrize("M,N,K,r,s", GENERIC_CASES)
+def test_generic_parity(gpu, M, N, K, r, s):
+    _say(f"[generic] M={M} N={N} K={K} r={r}")
+    x, W, A, B = _inputs(M, N, K, r, seed=11 + M)
+    y = _run(gpu, x, W, A, B, s)
+    ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), s)
+    err = O.max_rel_err(y.float().numpy(), ref)
+    _say(f"  max_rel_err={err:.3e}")
+    assert err <= BF16_TOL
+
+
+def test_strided_inputs(gpu):
+    """Leading dimensions larger than K (views into wider buffers)."""
+    import weightshared_torchtitan_amd as wsl
+    _say("[strided] M=300 N=256 K=256 r=16, ldx=ldw=320")
+    g = torch.Generator().manual_seed(5)
+    xb = torch.randn(300, 320, generator=g).bfloat16()
+    wb = (torch.randn(256, 320, generator=g) * 0.02).bfloat16()
+    A = (torch.randn(16, 256, generator=g) * 0.02).bfloat16()
+    B = (torch.randn(256, 16, generator=g) * 0.02).bfloat16()
+    x, W = xb[:, :256], wb[:, :256]
+    y = wsl.lora_linear(xb.to(gpu)[:, :256], wb.to(gpu)[:, :256], A.to(gpu), B.to(gpu), 2.0)
+    ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), 2.0)
+    assert O.max_rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
+
+
+def test_golden_vectors_on_gpu(gpu):
+    """The brute-force fixtures, run through the HIP kernels (generic/decode paths)."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "lora_small.npz"), allow_pickle=False)
+    for name in g["names"]:
+        x = torch.from_numpy(g[f"{name}_x"]).bfloat16()
+        W = torch.from_numpy(g[f"{name}_W"]).bfloat16() if g[f"{name}_W"].shape[0] else None
+        A = torch.from_numpy(g[f"{name}_A"]).bfloat16() if g[f"{name}_A"].shape[0] else None
+        B = torch.from_numpy(g[f"{name}_B"]).bfloat16() if A is not None else None
+        _say(f"[golden] {name} x{tuple(x.shape)}")
+        y = _run(gpu, x, W, A, B, float(g[f"{name}_s"]))
+        assert O.max_rel_err(y.float().numpy(), g[f"{name}_y"]) <= BF16_TOL, str(name)
+
+
+# ------------------------------------------------------------------ fp8 base
+@pytest.mark.parametrize("M,N,K", [(16, 1024, 4096), (512, 1024, 1024), (4, 512, 2048)])
+def test_fp8_base_parity(gpu, M, N, K):
+    from weightshared_torchtitan_amd import quantize_fp8_per_channel
+    _say(f"[fp8] M={M} N={N} K={K} r=128 s=1")
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    Wf = torch.randn(N, K, generator=g) * 0.02
+    A = (torch.randn(128, K, generator=g) * 0.02).bfloat16()
+    B = (torch.randn(N, 128, generator=g) * 0.02).bfloat16()
+    q, sc = quantize_fp8_per_channel(Wf)
+    y = _run(gpu, x, q, A, B, 1.0, w_scale=sc).float().numpy()
+    ref = O.lora_linear(_np(x), Wf.numpy(), _np(A), _np(B), 1.0)
+    err = O.max_rel_err(y, ref)
+    wdq = O.dequantize_fp8(q.view(torch.uint8).numpy(), sc.numpy())
+    err_dq = O.max_rel_err(y, O.lora_linear(_np(x), wdq, _np(A), _np(B), 1.0))
+    _say(f"  vs fp32 W: {err:.3e}   vs dequantised W: {err_dq:.3e}")
+    assert err <= FP8_TOL
+    assert err_dq <= BF16_TOL
+
+
+def test_fp8_decode_table_on_gpu(gpu):
+    """Every finite e4m3fn code through the kernel's decoder: x = e_k one-hot rows."""
+    _say("[fp8 table] K=256 one-hot")
+    codes = torch.tensor([c for c in range(256) if c not in (0x7F, 0xFF)], dtype=torch.uint8)
+    n = codes.numel()
+    K = 256
+    q = torch.zeros(n, K, dtype=torch.uint8)
+    q[:, 0] = codes
+    x = torch.zeros(1, K, dtype=torch.bfloat16)
+    x[0, 0] = 1.0
+    y = _run(gpu, x, q.view(torch.float8_e4m3fn), None, None, 0.0, w_scale=torch.ones(n))
+    expect = O.fp8_e4m3_decode(codes.numpy())
+    np.testing.assert_array_equal(y.float().numpy()[0], expect.astype(np.float32))
+
+
+# ------------------------------------------------------------------ properties at benchmark size
+def test_properties_at_benchmark_shape(gpu):
+    """Config-2 gate/up projection (M=8192, N=3072, K=1024, r=32): determinism, row
+    independence, B = 0 reducing to the plain linear, linearity in the scale."""
+    import weightshared_torchtitan_amd as wsl
+    _say("[props] M=8192 N=3072 K=1024 r=32")
+    M, N, K, r = 8192, 3072, 1024, 32
+    x, W, A, B = (t.to(gpu) for t in _inputs(M, N, K, r, seed=99))
+    y1 = wsl.lora_linear(x, W, A, B, 2.0)
+    y2 = wsl.lora_linear(x, W, A, B, 2.0)
+    assert torch.equal(y1, y2), "not deterministic"
+    ys = wsl.lora_linear(x[1024:1536], W, A, B, 2.0)
+    assert torch.equal(ys, y1[1024:1536]), "rows not independent"
+    y0 = wsl.lora_linear(x, W, A, torch.zeros_like(B), 2.0)
+    yp = wsl.lora_linear(x, W, None, None, 0.0)
+    assert torch.equal(y0, yp), "B = 0 must equal the plain linear"
+    ya = wsl.lora_linear(x, W, A, B, 1.0).float()
+    yb = wsl.lora_linear(x, W, A, B, 3.0).float()
+    d1 = ya - yp.float()
+    d3 = yb - yp.float()
+    rel = ((d3 - 3 * d1).abs().max() / (3 * d1).abs().max()).item()
+    _say(f"  linearity residual {rel:.3e}")
+    assert rel < 5e-2
+    # spot-check 64 rows against the oracle at full K
+    rows = torch.arange(0, M, M // 64)
+    ref = O.lora_linear(_np(x[rows].cpu()), _np(W.cpu()), _np(A.cpu()), _np(B.cpu()), 2.0)
+    assert O.max_rel_err(y1[rows].float().cpu().numpy(), ref) <= BF16_TOL
+
+
+def test_decode_matches_prefill_path(gpu):
+    """The same rows through the decode (M <= 64) and prefill (M > 64) kernels agree."""
+    import weightshared_torchtitan_amd as wsl
+    _say("[decode vs prefill] N=2048 K=2048 r=64")
+    x, W, A, B = (t.to(gpu) for t in _inputs(128, 2048, 2048, 64, seed=3))
+    big = wsl.lora_linear(x, W, A, B, 2.0).float()
+    small = wsl.lora_linear(x[:8], W, A, B, 2.0).float()
+    rel = ((big[:8] - small).abs().max() / big[:8].abs().max()).item()
+    assert rel < 1e-2
+
+
+# ------------------------------------------------------------------ factorized embedding
+def test_factorized_embedding_golden(gpu):
+    import os
+    import weightshared_torchtitan_amd as wsl
+    _say("[embedding golden]")
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "embedding_small.npz"), allow_pickle=False)
+    E = torch.from_numpy(g["E"]).bfloat16().to(gpu)
+    P = torch.from_numpy(g["P"]).bfloat16().to(gpu)
+    out = wsl.factorized_embedding(torch.from_numpy(g["ids"]).to(gpu), E, P).float().cpu().numpy()
+    assert O.max_rel_err(out, g["out"]) <= BF16_TOL
+    assert np.all(out[3] == 0) and np.all(out[5] == 0)  # out-of-range ids
+
+
+@pytest.mark.parametrize("n_tok", [8, 4096])
+def test_factorized_embedding_benchmark_shape(gpu, n_tok):
+    import weightshared_torchtitan_amd as wsl
+    _say(f"[embedding] V=151936 k=256 H=1024 tokens={n_tok}")
+    g = torch.Generator().manual_seed(n_tok)
+    V, k, H = 151936, 256, 1024
+    E = (torch.randn(V, k, generator=g) * 0.02).bfloat16()
+    P = (torch.randn(H, k, generator=g) * 0.02).bfloat16()
+    ids = torch.randint(0, V, (n_tok,), generator=g)
+    out = wsl.factorized_embedding(ids.to(gpu), E.to(gpu), P.to(gpu)).float().cpu().numpy()
+    ref = O.factorized_embedding(ids.numpy(), _np(E), _np(P))
+    assert O.max_rel_err(out, ref) <= BF16_TOL

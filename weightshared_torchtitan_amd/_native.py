@@ -1,0 +1,117 @@
+"""ctypes binding of libwsl.so (the C ABI declared in include/wsl_lora.h).
+
+torch is imported first so that the process-wide HIP runtime is the one PyTorch-ROCm
+ships; libwsl then binds to that same runtime. There is no fallback: if the library is
+missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads the HIP runtime libwsl links against)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwsl.so")
+
+WSL_OK = 0
+WSL_E_INVALID_ARG = -1
+WSL_E_SHAPE = -2
+WSL_E_DTYPE = -3
+WSL_E_ALIGN = -4
+WSL_E_WORKSPACE = -5
+WSL_E_DEVICE = -6
+WSL_E_LAUNCH = -7
+
+WSL_DTYPE_BF16 = 0
+WSL_DTYPE_FP8_E4M3 = 1
+WSL_MAX_RANK = 256
+
+# Every symbol include/wsl_lora.h declares.
+EXPORTED = (
+    "wsl_lora_linear_workspace_bytes",
+    "wsl_lora_linear_fwd",
+    "wsl_factorized_embedding_fwd",
+    "wsl_last_error",
+    "wsl_version",
+)
+
+_lib = None
+_lock = threading.Lock()
+
+_c_i64 = ctypes.c_int64
+_c_vp = ctypes.c_void_p
+
+
+class WSLError(RuntimeError):
+    """A libwsl call failed on the device side (workspace, device, launch)."""
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.wsl_version.restype = ctypes.c_int
+    lib.wsl_version.argtypes = []
+    lib.wsl_last_error.restype = ctypes.c_char_p
+    lib.wsl_last_error.argtypes = []
+    lib.wsl_lora_linear_workspace_bytes.restype = ctypes.c_int
+    lib.wsl_lora_linear_workspace_bytes.argtypes = [
+        _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]
+    lib.wsl_lora_linear_fwd.restype = ctypes.c_int
+    lib.wsl_lora_linear_fwd.argtypes = [
+        _c_vp, _c_i64,                   # x, ldx
+        _c_vp, _c_i64, ctypes.c_int32, _c_vp,  # w, ldw, w_dtype, w_scale
+        _c_vp, _c_i64,                   # a, lda
+        _c_vp, _c_i64,                   # b, ldb
+        ctypes.c_float,                  # scale
+        _c_vp, _c_i64,                   # y, ldy
+        _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
+        _c_vp, ctypes.c_size_t,          # workspace, bytes
+        _c_vp,                           # stream
+    ]
+    lib.wsl_factorized_embedding_fwd.restype = ctypes.c_int
+    lib.wsl_factorized_embedding_fwd.argtypes = [
+        _c_vp, _c_i64,                   # ids, n_ids
+        _c_vp, _c_i64, _c_i64, _c_i64,   # emb, lde, vocab, k
+        _c_vp, _c_i64, _c_i64,           # proj, ldp, hidden
+        _c_vp, _c_i64,                   # out, ldo
+        _c_vp,                           # stream
+    ]
+
+
+def lib() -> ctypes.CDLL:
+    """Returns the loaded library, loading it on first use. Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"libwsl.so not found at {LIB_PATH}; build it with "
+                    "`python -m weightshared_torchtitan_amd.build` (hipcc, gfx950)")
+            handle = ctypes.CDLL(LIB_PATH)
+            _declare(handle)
+            _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().wsl_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int, what: str) -> None:
+    """Maps a WSL_E_* code to the matching Python exception."""
+    if rc == WSL_OK:
+        return
+    msg = f"{what}: {last_error()} (code {rc})"
+    if rc in (WSL_E_INVALID_ARG, WSL_E_SHAPE, WSL_E_ALIGN):
+        raise ValueError(msg)
+    if rc == WSL_E_DTYPE:
+        raise TypeError(msg)
+    raise WSLError(msg)
+
+
+def workspace_bytes(M: int, N: int, K: int, r: int, w_dtype: int) -> int:
+    out = ctypes.c_size_t(0)
+    check(lib().wsl_lora_linear_workspace_bytes(M, N, K, r, w_dtype, ctypes.byref(out)),
+          "wsl_lora_linear_workspace_bytes")
+    return int(out.value)

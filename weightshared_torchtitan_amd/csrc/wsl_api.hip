@@ -1,0 +1,192 @@
+// C ABI of libwsl (declared in include/wsl_lora.h): argument validation, the one-time
+// device check, and dispatch to the prefill / decode / generic kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/wsl_lora.h"
+#include "wsl_common.h"
+
+namespace {
+
+thread_local char g_err[512] = {0};
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_err() { g_err[0] = 0; }
+
+// Checks once per device that it is a gfx950 part (the kernels are built for it only).
+int check_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(WSL_E_DEVICE, "hipGetDevice failed: %s", hipGetErrorString(e));
+  static std::mutex mu;
+  static int checked[64] = {0};  // 0 unknown, 1 ok, -1 bad
+  if (dev < 0 || dev >= 64) return fail(WSL_E_DEVICE, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(mu);
+  if (checked[dev] == 0) {
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return fail(WSL_E_DEVICE, "hipGetDeviceProperties failed: %s", hipGetErrorString(e));
+    checked[dev] = (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ? 1 : -1;
+    if (checked[dev] < 0) {
+      return fail(WSL_E_DEVICE, "device %d is %s; libwsl is built for gfx950 only", dev, prop.gcnArchName);
+    }
+  }
+  if (checked[dev] < 0) return fail(WSL_E_DEVICE, "device %d is not gfx950", dev);
+  return WSL_OK;
+}
+
+enum class Path { kNone, kPrefill, kDecode, kGeneric };
+
+Path choose_path(const wsl::LoraArgs& p) {
+  if (p.M == 0) return Path::kNone;
+  if (p.M <= wsl::kDecodeMaxM && wsl::decode_supported(p)) return Path::kDecode;
+  if (wsl::prefill_supported(p)) return Path::kPrefill;
+  return Path::kGeneric;
+}
+
+size_t generic_ws(int64_t M, int64_t r) { return (size_t)(M * r * 2); }
+
+size_t workspace_for(const wsl::LoraArgs& p) {
+  switch (choose_path(p)) {
+    case Path::kDecode: return wsl::decode_workspace_bytes(p.M, p.N, p.K, p.r, p.w_dtype);
+    case Path::kPrefill: return wsl::prefill_workspace_bytes(p.M, p.N, p.K, p.r, p.w_dtype);
+    case Path::kGeneric: return generic_ws(p.M, p.r);
+    default: return 0;
+  }
+}
+
+// Upper bound over the paths a problem of this size can take (the path also depends on
+// pointer alignment, which the size query does not see).
+size_t workspace_upper_bound(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
+  size_t b = generic_ws(M, r);
+  size_t pf = wsl::prefill_workspace_bytes(M, N, K, r, w_dtype);
+  if (pf > b) b = pf;
+  if (M >= 1 && M <= wsl::kDecodeMaxM) {
+    size_t d = wsl::decode_workspace_bytes(M, N, K, r, w_dtype);
+    if (d > b) b = d;
+  }
+  return b;
+}
+
+int validate_sizes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t w_dtype) {
+  if (M < 0) return fail(WSL_E_SHAPE, "M must be >= 0 (got %lld)", (long long)M);
+  if (N < 1) return fail(WSL_E_SHAPE, "N must be >= 1 (got %lld)", (long long)N);
+  if (K < 1) return fail(WSL_E_SHAPE, "K must be >= 1 (got %lld)", (long long)K);
+  if (r < 0 || r > WSL_MAX_RANK)
+    return fail(WSL_E_SHAPE, "rank r must be in [0, %d] (got %lld)", WSL_MAX_RANK, (long long)r);
+  if (M > ((int64_t)1 << 31) || N > ((int64_t)1 << 31) || K > ((int64_t)1 << 31))
+    return fail(WSL_E_SHAPE, "M, N, K must each be below 2^31");
+  if (w_dtype != WSL_DTYPE_BF16 && w_dtype != WSL_DTYPE_FP8_E4M3)
+    return fail(WSL_E_DTYPE, "unsupported w_dtype %d", (int)w_dtype);
+  return WSL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wsl_version(void) { return 100; }
+
+const char* wsl_last_error(void) { return g_err; }
+
+int wsl_lora_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t w_dtype,
+                                    size_t* bytes) {
+  clear_err();
+  if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
+  int rc = validate_sizes(M, N, K, r, w_dtype);
+  if (rc != WSL_OK) return rc;
+  *bytes = workspace_upper_bound(M, N, K, r, w_dtype);
+  return WSL_OK;
+}
+
+int wsl_lora_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+                        const float* w_scale, const void* a, int64_t lda, const void* b,
+                        int64_t ldb, float scale, void* y, int64_t ldy, int64_t M, int64_t N,
+                        int64_t K, int64_t r, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  clear_err();
+  int rc = validate_sizes(M, N, K, r, w_dtype);
+  if (rc != WSL_OK) return rc;
+  if (M > 0 && x == nullptr) return fail(WSL_E_INVALID_ARG, "x must not be NULL");
+  if (M > 0 && y == nullptr) return fail(WSL_E_INVALID_ARG, "y must not be NULL");
+  if (w == nullptr && r == 0) return fail(WSL_E_INVALID_ARG, "w is NULL and r == 0: nothing to compute");
+  if (r > 0 && (a == nullptr || b == nullptr)) return fail(WSL_E_INVALID_ARG, "r > 0 needs a and b");
+  if (w != nullptr && w_dtype == WSL_DTYPE_FP8_E4M3 && w_scale == nullptr)
+    return fail(WSL_E_INVALID_ARG, "fp8 w needs w_scale");
+  if (w_dtype == WSL_DTYPE_BF16 && w_scale != nullptr)
+    return fail(WSL_E_INVALID_ARG, "w_scale is only valid with an fp8 w");
+  if (ldx < K) return fail(WSL_E_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
+  if (w != nullptr && ldw < K) return fail(WSL_E_SHAPE, "ldw (%lld) < K (%lld)", (long long)ldw, (long long)K);
+  if (r > 0 && lda < K) return fail(WSL_E_SHAPE, "lda (%lld) < K (%lld)", (long long)lda, (long long)K);
+  if (r > 0 && ldb < r) return fail(WSL_E_SHAPE, "ldb (%lld) < r (%lld)", (long long)ldb, (long long)r);
+  if (ldy < N) return fail(WSL_E_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
+  if (((uintptr_t)x & 1) || ((uintptr_t)y & 1) || ((uintptr_t)a & 1) || ((uintptr_t)b & 1) ||
+      ((uintptr_t)w_scale & 3) || (w_dtype == WSL_DTYPE_BF16 && ((uintptr_t)w & 1)))
+    return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
+
+  wsl::LoraArgs p;
+  p.x = x; p.ldx = ldx;
+  p.w = w; p.ldw = ldw; p.w_dtype = w_dtype; p.w_scale = w_scale;
+  p.a = a; p.lda = lda; p.b = b; p.ldb = ldb;
+  p.scale = scale;
+  p.y = y; p.ldy = ldy;
+  p.M = M; p.N = N; p.K = K; p.r = r;
+  p.ws = workspace; p.ws_bytes = workspace_bytes;
+  p.stream = reinterpret_cast<hipStream_t>(stream);
+  p.gather = nullptr; p.gather_rows = 0;
+
+  Path path = choose_path(p);
+  if (path == Path::kNone) return WSL_OK;
+  size_t need = workspace_for(p);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if (need > 0 && ((uintptr_t)workspace & 15))
+    return fail(WSL_E_ALIGN, "workspace must be 16-byte aligned");
+  rc = check_device();
+  if (rc != WSL_OK) return rc;
+
+  hipError_t e;
+  switch (path) {
+    case Path::kDecode: e = wsl::launch_decode(p); break;
+    case Path::kPrefill: e = wsl::launch_prefill(p); break;
+    default: e = wsl::launch_generic(p); break;
+  }
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
+int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids, const void* emb, int64_t lde,
+                                 int64_t vocab, int64_t k, const void* proj, int64_t ldp,
+                                 int64_t hidden, void* out, int64_t ldo, void* stream) {
+  clear_err();
+  if (n_ids < 0) return fail(WSL_E_SHAPE, "n_ids must be >= 0");
+  if (vocab < 1 || k < 1 || hidden < 1) return fail(WSL_E_SHAPE, "vocab, k and hidden must be >= 1");
+  if (k > 1024) return fail(WSL_E_SHAPE, "k must be <= 1024 (got %lld)", (long long)k);
+  if (n_ids > ((int64_t)1 << 31) || hidden > ((int64_t)1 << 31) || vocab > ((int64_t)1 << 40))
+    return fail(WSL_E_SHAPE, "sizes out of range");
+  if (n_ids == 0) return WSL_OK;
+  if (ids == nullptr || emb == nullptr || proj == nullptr || out == nullptr)
+    return fail(WSL_E_INVALID_ARG, "ids, emb, proj and out must not be NULL");
+  if (lde < k || ldp < k || ldo < hidden) return fail(WSL_E_SHAPE, "leading dimension too small");
+  if (((uintptr_t)ids & 7) || ((uintptr_t)emb & 1) || ((uintptr_t)proj & 1) || ((uintptr_t)out & 1))
+    return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
+  int rc = check_device();
+  if (rc != WSL_OK) return rc;
+  hipError_t e = wsl::launch_factorized_embedding(ids, n_ids, emb, lde, vocab, k, proj, ldp, hidden,
+                                                  out, ldo, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
+}  // extern "C"

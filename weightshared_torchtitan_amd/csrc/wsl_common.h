@@ -1,0 +1,111 @@
+// Shared device-side types and helpers for the gfx950 kernels of libwsl.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wsl {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+// Storage type tags (match WSL_DTYPE_* in include/wsl_lora.h).
+enum : int { kBF16 = 0, kFP8 = 1 };
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// Two fp32 -> packed bf16x2 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+
+// Four OCP e4m3fn bytes (packed in one dword, byte 0 first) -> 4 bf16 in two dwords.
+// gfx950's v_cvt_pk_f32_fp8 decodes the OCP format; every e4m3fn value is exactly
+// representable in bf16, so truncating the fp32 result is exact.
+template <bool HIGH_HALF>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t q) {
+  auto f = __builtin_amdgcn_cvt_pk_f32_fp8((int)q, HIGH_HALF);
+  return (__float_as_uint(f[0]) >> 16) | (__float_as_uint(f[1]) & 0xffff0000u);
+}
+
+// 16 fp8 (one 16-byte chunk) -> 16 bf16 (two 16-byte chunks).
+__device__ __forceinline__ void fp8x16_to_bf16x16(const u32x4_t& q, u32x4_t& lo, u32x4_t& hi);
+
+__device__ __forceinline__ void fp8x16_to_bf16x16(const u32x4_t& q, u32x4_t& lo, u32x4_t& hi) {
+  lo = u32x4_t{fp8x2_to_bf16x2<false>(q[0]), fp8x2_to_bf16x2<true>(q[0]),
+               fp8x2_to_bf16x2<false>(q[1]), fp8x2_to_bf16x2<true>(q[1])};
+  hi = u32x4_t{fp8x2_to_bf16x2<false>(q[2]), fp8x2_to_bf16x2<true>(q[2]),
+               fp8x2_to_bf16x2<false>(q[3]), fp8x2_to_bf16x2<true>(q[3])};
+}
+
+// 8 fp8 (two dwords) -> 8 bf16 (one 16-byte chunk).
+__device__ __forceinline__ u32x4_t fp8x8_to_bf16x8(uint32_t q0, uint32_t q1) {
+  return u32x4_t{fp8x2_to_bf16x2<false>(q0), fp8x2_to_bf16x2<true>(q0),
+                 fp8x2_to_bf16x2<false>(q1), fp8x2_to_bf16x2<true>(q1)};
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ u32x4_t ld_global_16(const void* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+__device__ __forceinline__ u32x4_t zero_u32x4() {
+  u32x4_t z = {0u, 0u, 0u, 0u};
+  return z;
+}
+
+}  // namespace wsl
+
+// Host-side launch helpers shared by the translation units of libwsl.
+namespace wsl {
+
+struct LoraArgs {
+  const void* x; int64_t ldx;
+  const void* w; int64_t ldw; int w_dtype; const float* w_scale;
+  const void* a; int64_t lda;
+  const void* b; int64_t ldb;
+  float scale;
+  void* y; int64_t ldy;
+  int64_t M, N, K, r;
+  void* ws; size_t ws_bytes;
+  hipStream_t stream;
+  // Optional row gather on x: row m of x is row gather[m] of a [gather_rows, ldx] table;
+  // ids outside [0, gather_rows) read as zero rows. Used by the factorized embedding.
+  const int64_t* gather; int64_t gather_rows;
+};
+
+// Each launcher returns hipSuccess or the launch error.
+hipError_t launch_prefill(const LoraArgs& p);
+size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
+bool prefill_supported(const LoraArgs& p);
+
+hipError_t launch_decode(const LoraArgs& p);
+size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
+bool decode_supported(const LoraArgs& p);
+
+hipError_t launch_generic(const LoraArgs& p);
+
+hipError_t launch_factorized_embedding(const int64_t* ids, int64_t n_ids, const void* emb,
+                                       int64_t lde, int64_t vocab, int64_t k, const void* proj,
+                                       int64_t ldp, int64_t hidden, void* out, int64_t ldo,
+                                       hipStream_t stream);
+
+// Largest M routed to the decode-shaped (skinny) kernels.
+constexpr int64_t kDecodeMaxM = 64;
+
+}  // namespace wsl

@@ -1,0 +1,327 @@
+"""Weight-shared Qwen3 decoder whose every projection is the fused LoRA linear.
+
+Layer l runs base block b(l) (one of ``n_unique_blocks`` sets of q/k/v/o/gate/up/down
+weights and norms, shared by n_layers / n_unique_blocks layers) plus its own rank-r
+LoRA adapters on all seven projections. Tokens enter through a factorized embedding
+E [vocab, k] . P^T and leave through the tied head (h . P) . E^T.
+
+Block semantics follow the reference's Qwen3 block:
+  attention with q/k RMSNorm, HF-style RoPE and GQA   torchtitan/experiments/qwen3/model/model.py:167-218
+  SwiGLU feed-forward                                  :250-251
+  pre-norm residual block                              :296-314
+Cross-layer sharing, the factorized embedding and LoRA on all projections are the
+configuration this path serves; the reference applies LoRA to q/k/v only
+(torchtitan/models/llama3/model/model.py:302-324).
+
+Decoding keeps a KV cache (the reference re-runs the full prefix each step,
+scripts/generate/_generation.py:43) and can replay one decode step as a HIP graph.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+from .lora import LoRAModule
+
+PROJS = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
+
+
+@dataclass
+class SharedQwen3Args:
+    dim: int = 1024
+    n_layers: int = 28
+    n_unique_blocks: int = 4
+    n_heads: int = 16
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    hidden_dim: int = 3072
+    vocab_size: int = 151936
+    embed_rank: int = 256
+    lora_rank: int = 32
+    lora_scale: Optional[float] = None  # None: alpha / rank with alpha = 2 * rank
+    norm_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    max_seq_len: int = 1024
+    block_map: str = "cyclic"  # "cyclic": b(l) = l % n_unique; "contiguous": l // (n_layers / n_unique)
+
+    def block_of(self, layer: int) -> int:
+        if self.block_map == "cyclic":
+            return layer % self.n_unique_blocks
+        if self.block_map == "contiguous":
+            return layer // (self.n_layers // self.n_unique_blocks)
+        raise ValueError(f"unknown block_map {self.block_map!r}")
+
+    def proj_shapes(self) -> dict:
+        """(out, in) of each projection."""
+        q = self.n_heads * self.head_dim
+        kv = self.n_kv_heads * self.head_dim
+        return {"wq": (q, self.dim), "wk": (kv, self.dim), "wv": (kv, self.dim), "wo": (self.dim, q),
+                "w1": (self.hidden_dim, self.dim), "w3": (self.hidden_dim, self.dim),
+                "w2": (self.dim, self.hidden_dim)}
+
+
+def qwen3_0p6b_shared() -> SharedQwen3Args:
+    """The benchmark configuration: Qwen3-0.6B dims, 28 layers from 4 unique blocks."""
+    return SharedQwen3Args()
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x):
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class _Attention(nn.Module):
+    def __init__(self, a: SharedQwen3Args):
+        super().__init__()
+        sh = a.proj_shapes()
+        for name in ("wq", "wk", "wv", "wo"):
+            out, inp = sh[name]
+            setattr(self, name, nn.Linear(inp, out, bias=False))
+        self.q_norm = RMSNorm(a.head_dim, a.norm_eps)
+        self.k_norm = RMSNorm(a.head_dim, a.norm_eps)
+
+
+class _FeedForward(nn.Module):
+    def __init__(self, a: SharedQwen3Args):
+        super().__init__()
+        sh = a.proj_shapes()
+        for name in ("w1", "w2", "w3"):
+            out, inp = sh[name]
+            setattr(self, name, nn.Linear(inp, out, bias=False))
+
+
+class SharedBlockBase(nn.Module):
+    """The shared (base) weights of one unique block."""
+
+    def __init__(self, a: SharedQwen3Args):
+        super().__init__()
+        self.attention = _Attention(a)
+        self.feed_forward = _FeedForward(a)
+        self.attention_norm = RMSNorm(a.dim, a.norm_eps)
+        self.ffn_norm = RMSNorm(a.dim, a.norm_eps)
+
+    def base(self, name: str) -> nn.Linear:
+        return getattr(self.attention if name in ("wq", "wk", "wv", "wo") else self.feed_forward, name)
+
+
+class LayerLoRA(nn.Module):
+    """Per-layer adapters: one LoRAModule per projection."""
+
+    def __init__(self, a: SharedQwen3Args):
+        super().__init__()
+        for name, (out, inp) in a.proj_shapes().items():
+            setattr(self, name, LoRAModule(inp, out, rank=a.lora_rank, scale=a.lora_scale))
+
+
+class FactorizedEmbedding(nn.Module):
+    """E [vocab, k] and P = proj.weight [dim, k]: embed(ids) = E[ids] . P^T."""
+
+    def __init__(self, vocab: int, rank: int, dim: int):
+        super().__init__()
+        self.emb = nn.Parameter(torch.empty(vocab, rank))
+        self.proj = nn.Linear(rank, dim, bias=False)
+        self._pt = None
+        self._pt_key = None
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        return ops.factorized_embedding(ids, self.emb, self.proj.weight)
+
+    def proj_t(self) -> torch.Tensor:
+        """P^T [k, dim] contiguous, cached while P is unchanged."""
+        w = self.proj.weight
+        key = (w.data_ptr(), w._version)
+        if self._pt is None or self._pt_key != key:
+            self._pt = w.detach().t().contiguous()
+            self._pt_key = key
+        return self._pt
+
+    def tied_logits(self, h: torch.Tensor) -> torch.Tensor:
+        """(h . P) . E^T as two fused-linear calls (r = 0): [.., dim] -> [.., k] -> [.., vocab]."""
+        z = ops.lora_linear(h, self.proj_t(), None, None, 0.0)
+        return ops.lora_linear(z, self.emb, None, None, 0.0)
+
+
+class KVCache:
+    """Per-layer K (stored transposed, [b, kv_heads, head_dim, L]) and V ([b, kv_heads, L, head_dim])."""
+
+    def __init__(self, a: SharedQwen3Args, batch: int, max_len: int, device, dtype=torch.bfloat16):
+        self.k_t = torch.zeros(a.n_layers, batch, a.n_kv_heads, a.head_dim, max_len, device=device, dtype=dtype)
+        self.v = torch.zeros(a.n_layers, batch, a.n_kv_heads, max_len, a.head_dim, device=device, dtype=dtype)
+        self.max_len = max_len
+
+
+def _rope_cache(head_dim: int, max_seq_len: int, theta: float) -> torch.Tensor:
+    freqs = 1.0 / (theta ** (torch.arange(0, head_dim, 2)[: head_dim // 2].float() / head_dim))
+    t = torch.arange(max_seq_len, dtype=freqs.dtype)
+    idx = torch.outer(t, freqs).float()
+    f = torch.cat([idx, idx], dim=-1)
+    return torch.cat([f.cos(), f.sin()], dim=-1)
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+class SharedQwen3(nn.Module):
+    def __init__(self, a: SharedQwen3Args):
+        super().__init__()
+        if a.n_layers % a.n_unique_blocks != 0:
+            raise ValueError("n_layers must be a multiple of n_unique_blocks")
+        self.args = a
+        self.tok_embeddings = FactorizedEmbedding(a.vocab_size, a.embed_rank, a.dim)
+        self.base_blocks = nn.ModuleList([SharedBlockBase(a) for _ in range(a.n_unique_blocks)])
+        self.layer_loras = nn.ModuleList([LayerLoRA(a) for _ in range(a.n_layers)])
+        self.norm = RMSNorm(a.dim, a.norm_eps)
+        self.register_buffer("rope", _rope_cache(a.head_dim, a.max_seq_len, a.rope_theta), persistent=False)
+
+    # ------------------------------------------------------------------ init
+    @torch.no_grad()
+    def init_random(self, seed: int = 0, std: float = 0.02) -> None:
+        """Every weight matrix ~ N(0, std^2) (LoRA B non-zero), norms = 1, drawn on the CPU
+        from one seeded generator in parameter order, then copied to the module's device."""
+        g = torch.Generator().manual_seed(seed)
+        for name, p in self.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.copy_((torch.randn(p.shape, generator=g) * std).to(p.dtype))
+
+    # ------------------------------------------------------------------ helpers
+    def _proj(self, layer: int, name: str, x: torch.Tensor) -> torch.Tensor:
+        base = self.base_blocks[self.args.block_of(layer)].base(name)
+        lora = getattr(self.layer_loras[layer], name)
+        return ops.lora_linear(x, base.weight, lora.w_a.weight, lora.w_b.weight, lora.scale)
+
+    def _rope(self, x: torch.Tensor, rc: torch.Tensor) -> torch.Tensor:
+        hd = x.shape[-1]
+        cos = rc[..., :hd].to(x.dtype)
+        sin = rc[..., hd:].to(x.dtype)
+        return x * cos + _rotate_half(x) * sin
+
+    def _ffn(self, layer: int, h: torch.Tensor) -> torch.Tensor:
+        blk = self.base_blocks[self.args.block_of(layer)]
+        x = blk.ffn_norm(h)
+        g = self._proj(layer, "w1", x)
+        u = self._proj(layer, "w3", x)
+        return h + self._proj(layer, "w2", F.silu(g) * u)
+
+    # ------------------------------------------------------------------ prefill
+    def forward(self, tokens: torch.Tensor, cache: Optional[KVCache] = None) -> torch.Tensor:
+        """Full-sequence causal forward from position 0 -> logits [b, s, vocab].
+        Fills `cache` (positions 0..s-1) when given."""
+        a = self.args
+        b, s = tokens.shape
+        h = self.tok_embeddings(tokens)
+        rc = self.rope[:s].view(1, s, 1, 2 * a.head_dim)
+        rep = a.n_heads // a.n_kv_heads
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        for l in range(a.n_layers):
+            blk = self.base_blocks[a.block_of(l)]
+            x = blk.attention_norm(h)
+            xq = self._proj(l, "wq", x).view(b, s, a.n_heads, a.head_dim)
+            xk = self._proj(l, "wk", x).view(b, s, a.n_kv_heads, a.head_dim)
+            xv = self._proj(l, "wv", x).view(b, s, a.n_kv_heads, a.head_dim)
+            xq = self._rope(blk.attention.q_norm(xq), rc)
+            xk = self._rope(blk.attention.k_norm(xk), rc)
+            if cache is not None:
+                cache.k_t[l, :, :, :, :s] = xk.permute(0, 2, 3, 1)
+                cache.v[l, :, :, :s] = xv.transpose(1, 2)
+            kk = xk.repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
+            vv = xv.repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                o = F.scaled_dot_product_attention(xq.transpose(1, 2).contiguous(), kk, vv, is_causal=True)
+            o = o.transpose(1, 2).reshape(b, s, a.n_heads * a.head_dim)
+            h = h + self._proj(l, "wo", o)
+            h = self._ffn(l, h)
+        h = self.norm(h)
+        return self.tok_embeddings.tied_logits(h)
+
+    # ------------------------------------------------------------------ decode
+    def decode_step(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        """One greedy step at position `pos` (0-d int64 device tensor) -> logits [b, vocab].
+        Shape-static and host-sync-free, so it can be captured in a HIP graph."""
+        a = self.args
+        b = token.shape[0]
+        L = cache.max_len
+        rep = a.n_heads // a.n_kv_heads
+        h = self.tok_embeddings(token.view(b, 1))  # [b, 1, dim]
+        rc = self.rope.index_select(0, pos.view(1)).view(1, 1, 1, 2 * a.head_dim)
+        masked = (torch.arange(L, device=token.device) > pos).view(1, 1, 1, L)
+        sm_scale = a.head_dim ** -0.5
+        for l in range(a.n_layers):
+            blk = self.base_blocks[a.block_of(l)]
+            x = blk.attention_norm(h)
+            xq = self._proj(l, "wq", x).view(b, 1, a.n_heads, a.head_dim)
+            xk = self._proj(l, "wk", x).view(b, 1, a.n_kv_heads, a.head_dim)
+            xv = self._proj(l, "wv", x).view(b, 1, a.n_kv_heads, a.head_dim)
+            xq = self._rope(blk.attention.q_norm(xq), rc)
+            xk = self._rope(blk.attention.k_norm(xk), rc)
+            cache.k_t[l].index_copy_(3, pos.view(1), xk.view(b, a.n_kv_heads, a.head_dim, 1))
+            cache.v[l].index_copy_(2, pos.view(1), xv.view(b, a.n_kv_heads, 1, a.head_dim))
+            q = xq.view(b, a.n_kv_heads, rep, a.head_dim)
+            scores = torch.matmul(q, cache.k_t[l]).float() * sm_scale  # [b, kv, rep, L]
+            scores = scores.masked_fill(masked, float("-inf"))
+            probs = torch.softmax(scores, dim=-1).to(cache.v.dtype)
+            o = torch.matmul(probs, cache.v[l])  # [b, kv, rep, hd]
+            h = h + self._proj(l, "wo", o.reshape(b, 1, a.n_heads * a.head_dim))
+            h = self._ffn(l, h)
+        h = self.norm(h)
+        return self.tok_embeddings.tied_logits(h).view(b, -1)
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True):
+        """Greedy decoding with a KV cache. Returns (new tokens [b, n_new], timings dict)."""
+        b, s = prompt.shape
+        dev = prompt.device
+        cache = KVCache(self.args, b, s + n_new, dev)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t2 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        logits = self.forward(prompt, cache)[:, -1]
+        tok = logits.argmax(-1).view(b, 1)
+        t1.record()
+        out = torch.empty(b, n_new, dtype=torch.int64, device=dev)
+        out[:, 0] = tok[:, 0]
+        pos = torch.full((), s, dtype=torch.int64, device=dev)
+        tok_buf = tok.clone()
+        if use_graph and n_new > 1:
+            # warm up outside the graph (kernel selection, allocator), then capture one step
+            stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                _ = self.decode_step(tok_buf, pos, cache)
+            torch.cuda.current_stream().wait_stream(stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                g_logits = self.decode_step(tok_buf, pos, cache)
+                g_next = g_logits.argmax(-1).view(b, 1)
+            # the warm-up wrote position s; the first replay rewrites it identically
+            for i in range(1, n_new):
+                graph.replay()
+                out[:, i] = g_next[:, 0]
+                tok_buf.copy_(g_next)
+                pos.add_(1)
+        else:
+            for i in range(1, n_new):
+                logits = self.decode_step(tok_buf, pos, cache)
+                nxt = logits.argmax(-1).view(b, 1)
+                out[:, i] = nxt[:, 0]
+                tok_buf.copy_(nxt)
+                pos.add_(1)
+        t2.record()
+        t2.synchronize()
+        return out, {"prefill_ms": t0.elapsed_time(t1), "decode_ms": t1.elapsed_time(t2)}
