@@ -1,0 +1,302 @@
+"""Benchmark of the fused LoRA linear on one MI355X.
+
+Headline (the JSON line's `value`): BASELINE config 2 — Qwen3-0.6B-shaped prefill
+projections in bf16, M = 8192 tokens, 7 projections x 28 layers per step, one shared
+base weight set, per-layer rank-32 LoRA (scale 2). A step is one pass over the 196
+projections, captured once as a HIP graph and replayed. value = algorithmic TFLOP/s,
+FLOPs = sum over launches of 2*M*(N*K + r*(K+N)).
+
+Also reported (same JSON line, key "extra"): config 3 decode GB/s (cold and warm
+weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
+projections, and the CPU baseline (the reference's fp32 arithmetic on host cores).
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+METRIC = "fused-LoRA linear TFLOP/s (% MFMA peak); weight-shared Qwen3 decode tok/s"
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+
+# (name, N, K) of the seven projections, as functions of (hidden, q_out, kv_out, ffn)
+def proj_shapes(hidden, q_out, kv_out, ffn):
+    return [("wq", q_out, hidden), ("wk", kv_out, hidden), ("wv", kv_out, hidden),
+            ("wo", hidden, q_out), ("w1", ffn, hidden), ("w3", ffn, hidden), ("w2", hidden, ffn)]
+
+
+QWEN3_0P6B = proj_shapes(1024, 2048, 1024, 3072)
+QWEN3_1P7B = proj_shapes(2048, 2048, 1024, 6144)
+QWEN3_8B = proj_shapes(4096, 4096, 1024, 12288)
+
+
+def lora_flops(M, N, K, r):
+    return 2.0 * M * (N * K + r * (K + N))
+
+
+def lora_bytes(M, N, K, r, w_bytes=2, scales=False):
+    return 2 * M * K + w_bytes * N * K + (4 * N if scales else 0) + 2 * r * K + 2 * N * r + 2 * M * N
+
+
+class ProjectionStack:
+    """Inputs of `layers` x 7 projections: one x per distinct K, `copies` sets of shared
+    base weights (layer l uses copy l % copies), per-layer LoRA A/B. Drawn from one seeded
+    generator in the order x, W (per copy, per projection), then A, B layer-major."""
+
+    def __init__(self, shapes, M, r, layers, dev, seed=0, copies=1, fp8=False, scale=2.0):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.shapes, self.M, self.r, self.layers, self.copies, self.scale = shapes, M, r, layers, copies, scale
+        self.fp8 = fp8
+        self.x = {}
+        for _, _, K in shapes:
+            if K not in self.x:
+                self.x[K] = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        self.W, self.S = [], []
+        for _ in range(copies):
+            wl, sl = [], []
+            for _, N, K in shapes:
+                w = torch.randn(N, K, device=dev, generator=g) * 0.02
+                if fp8:
+                    from weightshared_torchtitan_amd import quantize_fp8_per_channel
+                    q, s = quantize_fp8_per_channel(w)
+                    wl.append(q)
+                    sl.append(s)
+                else:
+                    wl.append(w.bfloat16())
+                    sl.append(None)
+                del w
+            self.W.append(wl)
+            self.S.append(sl)
+        self.A, self.B = [], []
+        for _ in range(layers):
+            al, bl = [], []
+            for _, N, K in shapes:
+                al.append((torch.randn(r, K, device=dev, generator=g) * 0.02).bfloat16() if r else None)
+                bl.append((torch.randn(N, r, device=dev, generator=g) * 0.02).bfloat16() if r else None)
+            self.A.append(al)
+            self.B.append(bl)
+
+    def run(self):
+        from weightshared_torchtitan_amd import lora_linear
+        for l in range(self.layers):
+            c = l % self.copies
+            for p, (_, N, K) in enumerate(self.shapes):
+                lora_linear(self.x[K], self.W[c][p], self.A[l][p], self.B[l][p], self.scale, w_scale=self.S[c][p])
+
+    def flops(self):
+        return self.layers * sum(lora_flops(self.M, N, K, self.r) for _, N, K in self.shapes)
+
+    def bytes(self):
+        wb = 1 if self.fp8 else 2
+        return self.layers * sum(lora_bytes(self.M, N, K, self.r, wb, self.fp8) for _, N, K in self.shapes)
+
+
+def graph_of(fn):
+    """Captures fn() once as a HIP graph (after one eager warm-up on a side stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_replays(graph, steps, warmup):
+    """Mean ms per replay over `steps` replays, bracketed by synchronize + HIP events on
+    the stream the replays run on."""
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+# ------------------------------------------------------------------------------ configs
+def bench_c2(dev, steps, warmup):
+    st = ProjectionStack(QWEN3_0P6B, M=8192, r=32, layers=28, dev=dev, seed=2)
+    g = graph_of(st.run)
+    ms = time_replays(g, steps, warmup)
+    del g
+    return st.flops(), ms
+
+
+def bench_c2_1p7b(dev, steps, warmup):
+    st = ProjectionStack(QWEN3_1P7B, M=8192, r=32, layers=4, dev=dev, seed=21)
+    g = graph_of(st.run)
+    ms = time_replays(g, steps, warmup)
+    del g, st
+    torch.cuda.empty_cache()
+    return ms
+
+
+def bench_c3(dev, steps, warmup):
+    out = {}
+    for M in (1, 8, 32, 64):
+        row = {}
+        for label, copies in (("cold", 6), ("warm", 1)):
+            st = ProjectionStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=copies)
+            g = graph_of(st.run)
+            ms = time_replays(g, steps, warmup)
+            row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
+                          "frac_hbm": round(st.bytes() / ms / 1e6 / HBM_PEAK_GBS, 4)}
+            del g, st
+            torch.cuda.empty_cache()
+        out[f"M={M}"] = row
+    return out
+
+
+def bench_c5(dev, steps, warmup):
+    out = {}
+    for M in (16, 4096):
+        copies = 3 if M == 16 else 1
+        st = ProjectionStack(QWEN3_8B, M=M, r=128, layers=4 if M == 16 else 1, dev=dev, seed=5,
+                             copies=copies, fp8=True, scale=1.0)
+        g = graph_of(st.run)
+        ms = time_replays(g, steps, warmup)
+        base = st.layers * sum(2.0 * M * N * K for _, N, K in st.shapes)
+        lora = st.flops() - base
+        t_min = base / (FP8_PEAK_TFLOPS * 1e12) + lora / (BF16_PEAK_TFLOPS * 1e12)
+        out[f"M={M}"] = {"ms": round(ms, 4), "TFLOP/s": round(st.flops() / ms / 1e9, 1),
+                         "GB/s": round(st.bytes() / ms / 1e6, 1),
+                         "frac_mixed_mfma_roofline": round(t_min * 1e3 / ms, 4),
+                         "frac_hbm": round(st.bytes() / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        del g, st
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_c4(dev):
+    from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3, qwen3_0p6b_shared
+    args = qwen3_0p6b_shared()
+    args.max_seq_len = 1024
+    model = SharedQwen3(args).to(dev)
+    model.init_random(seed=4)
+    model = model.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, args.vocab_size, (8, 512), generator=g).to(dev)
+    model.generate(prompt[:, :16], 4)  # warm-up (allocations, kernel load)
+    torch.cuda.synchronize()
+    toks, t = model.generate(prompt, 256)
+    n_new = 256
+    res = {"batch": 8, "prompt": 512, "new_tokens": n_new,
+           "decode_tok_s": round(8 * n_new / (t["decode_ms"] / 1e3), 1),
+           "prefill_ms": round(t["prefill_ms"], 2), "decode_ms": round(t["decode_ms"], 2),
+           "reference_formula_tok_s": round(8 * (512 + n_new) / ((t["prefill_ms"] + t["decode_ms"]) / 1e3), 1)}
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(seconds=10.0):
+    """The reference's fp32 CPU arithmetic (F.linear(x,W) + F.linear(F.linear(x,A),B)*s),
+    timed on host cores over a bounded sample of the config-2 projections."""
+    from oracle.qwen3_ref import reference_lora_linear
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    M = 8192
+    xs = {K: torch.randn(M, K, generator=g) for _, _, K in QWEN3_0P6B}
+    Ws = [torch.randn(N, K, generator=g) * 0.02 for _, N, K in QWEN3_0P6B]
+    As = [torch.randn(32, K, generator=g) * 0.02 for _, _, K in QWEN3_0P6B]
+    Bs = [torch.randn(N, 32, generator=g) * 0.02 for _, N, _ in QWEN3_0P6B]
+    reference_lora_linear(xs[1024][:256], Ws[0], As[0], Bs[0], 2.0)  # warm-up
+    flops, n = 0.0, 0
+    t0 = time.perf_counter()
+    while True:
+        p = n % 7
+        _, N, K = QWEN3_0P6B[p]
+        reference_lora_linear(xs[K], Ws[p], As[p], Bs[p], 2.0)
+        flops += lora_flops(M, N, K, 32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 7:
+            break
+    return {"value": round(flops / el / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{n} config-2 projections (M=8192, hidden 1024, r=32) in fp32, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the fused LoRA linear is row-independent; see the sharding design).", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    import weightshared_torchtitan_amd  # noqa: F401  (loads libwsl; fails loudly if missing)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.synchronize()
+    flops, ms = bench_c2(dev, args.steps, args.warmup)
+    tflops = flops / ms / 1e9
+    launches = 7 * 28
+    res = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (x ~ N(0,1); W, A, B ~ N(0, 0.02^2); seeded)",
+        "config": {"workload": "config 2: Qwen3-0.6B prefill projections, M=8192, 7 proj x 28 layers, "
+                               "one shared base W set, per-layer rank-32 LoRA, scale 2",
+                   "M": 8192, "hidden": 1024, "rank": 32, "layers": 28, "projections": 7},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "prefill_kernel (196 launches per step, one per projection)",
+                     "avg_launch_us": round(ms * 1e3 / launches, 3)},
+    }
+    extra = {}
+    if not args.no_extra:
+        ms17 = bench_c2_1p7b(dev, args.steps, args.warmup)
+        f17 = 4 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_1P7B)
+        extra["c2_qwen3_1.7b_prefill"] = {"TFLOP/s": round(f17 / ms17 / 1e9, 1),
+                                          "frac_mfma": round(f17 / ms17 / 1e9 / BF16_PEAK_TFLOPS, 4),
+                                          "ms_per_4_layers": round(ms17, 4)}
+        extra["c3_qwen3_1.7b_decode"] = bench_c3(dev, args.steps, args.warmup)
+        extra["c5_qwen3_8b_fp8_base"] = bench_c5(dev, args.steps, args.warmup)
+        extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)
+        res["extra"] = extra
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

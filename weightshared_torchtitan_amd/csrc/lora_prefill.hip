@@ -2,20 +2,36 @@
 //
 //   y[M,N] = (x . W^T) * diag(w_scale) + T . B^T,   T = bf16(s * x . A^T)
 //
-// One workgroup (4 waves, 256 threads) owns a 256(n) x 256(m) output tile; each wave
-// owns 128 x 128 of it as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16 (fp32 accumulate).
-// K is walked in 64-wide tiles staged through swizzled, double-buffered LDS.
+// Tiling. A workgroup of 8 waves (two per SIMD) owns a BM(m) x BN(n) output tile,
+// split over its waves as a WNW x WMW grid of wave tiles; a wave tile is a grid of
+// v_mfma_f32_32x32x16_bf16 blocks with fp32 accumulators. Two configurations:
+//   256 x 256, 128(n) x 64(m) per wave;
+//   128 x 256, 64 x 64 per wave — used when 256-row tiles would leave CUs idle.
+// (A 4-wave 256 x 256 tile with 128 x 128 per wave measured slower on these shapes:
+// one wave per SIMD leaves LDS latency exposed, and rank blocks overflow the AGPRs.)
+// K is walked in 64-wide tiles through two LDS buffers filled by
+// global_load_lds_dwordx4 (global memory -> LDS without passing through VGPRs; lane i
+// of a wave instruction lands at the wave-uniform LDS base + 16*i, so the XOR swizzle of
+// the LDS rows is applied by permuting the global source addresses). The barrier sits
+// in the middle of each K tile: the fragments of the tile's last k step are read before
+// it, so it frees the buffer for the fill of tile k+2, and the first fragments of tile
+// k+1 are read while the last MFMAs of tile k run. Fragments are double-buffered in
+// registers across k steps. An fp8 base weight is staged through registers, where it
+// is decoded to bf16.
 //
-// LoRA fusion (rank r <= 64): while the x tile of a K step is LDS-resident, the same
-// x fragments also feed x . A^T for the workgroup's 256 rows (the rank-r
-// down-projection, computed once per workgroup, never written to HBM). After the K
-// loop T is scaled, rounded to bf16 and parked in LDS, and the rank-r up-projection
-// T . B^T accumulates into the same accumulator registers as x . W^T.
-// For r > 64, T comes from a pre-pass kernel (workspace) and is consumed the same way.
+// LoRA fusion (rank r <= 64). The rank-r down-projection rides on the main loop: the x
+// fragments a wave already holds for x . W^T also feed x . A^T, so T is computed once
+// per workgroup from the LDS-resident x tile and never touches HBM. After the K loop T
+// is scaled by s, rounded to bf16 and parked in LDS, and the up-projection T . B^T
+// accumulates into the same accumulator registers as x . W^T; its B slice is filled
+// into the idle LDS buffer while the last K tile is multiplied. For r > 64 a pre-pass
+// writes T to the workspace and the kernel consumes it the same way.
 //
-// The MFMA "A" operand is the W tile (rows n) and the "B" operand the x tile (rows m),
-// so each lane ends with 4 consecutive n of one m per accumulator group: the bf16
-// result leaves as 8-byte stores.
+// The MFMA "A" operand is the W tile (rows n) and "B" the x tile (rows m): each lane
+// ends with 4 consecutive n of one m per accumulator group, stored as 8-byte writes.
+//
+// Workgroups are dispatched round-robin over the 8 XCDs; the tile order remaps them so
+// that each XCD works on a compact group of m x n tiles and its L2 serves the reuse.
 //
 // Reference arithmetic being fused: torchtitan/models/llama3/model/model.py:189-192
 // (LoRAModule.forward), :392-398 (base projection + broadcast_add with g = 1).
@@ -24,22 +40,36 @@
 namespace wsl {
 namespace {
 
-constexpr int BM = 256;   // m rows per workgroup tile
-constexpr int BN = 256;   // n rows per workgroup tile
-constexpr int BK = 64;    // K per LDS stage
-constexpr int NT = 256;   // threads per workgroup
 constexpr int RIN = 64;   // largest rank whose down-projection runs inside the kernel
-constexpr int ROW_BYTES = BK * 2;                  // 128 B per LDS row (8 chunks of 16 B)
-constexpr int TILE_BYTES = 256 * ROW_BYTES;        // 32 KB for a 256-row operand tile
-constexpr int RANK_A_BYTES = RIN * ROW_BYTES;      // 8 KB for the rank-A K slice
-constexpr int STAGE_BYTES = 2 * TILE_BYTES + RANK_A_BYTES;  // 72 KB
-constexpr int LDS_BYTES = 2 * STAGE_BYTES;                  // 144 KB (gfx950: 160 KB / CU)
+constexpr int BK = 64;    // K per LDS buffer
+constexpr int ROWB = 128; // bytes per LDS row (BK bf16)
+constexpr int KK = 4;     // MFMA k steps per K tile
+constexpr int N_XCD = 8;
+constexpr int GROUP_M = 8;
 
-// Byte offset of 16-byte chunk `c` (0..7) of LDS row `row`. XOR swizzle: the 8 rows a
-// group of lanes touches at one chunk index land in 8 distinct bank groups.
-__device__ __forceinline__ int lds_off(int row, int c) {
-  return row * ROW_BYTES + ((c ^ (row & 7)) << 4);
-}
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int BM_, int BN_, int WNW_, int NW_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int NW = NW_, NT = NW_ * 64;     // waves, threads
+  static constexpr int WNW = WNW_, WMW = NW_ / WNW_;  // waves along n and m
+  static constexpr int TN = BN / WNW, TM = BM / WMW;  // wave tile
+  static constexpr int NI = TN / 32, MJ = TM / 32;    // MFMA blocks per wave
+  static constexpr int XB = BM * ROWB, WB = BN * ROWB;
+  static constexpr int NXI = XB / 1024 / NW;          // direct-fill instructions per wave
+  static constexpr int NWI = WB / 1024 / NW;
+  static constexpr int NBI = BN * ROWB / 1024 / NW;   // fills of a [BN][64] B slice
+  static_assert(NXI >= 1 && NWI >= 1 && NBI >= 1, "tile too small for the direct-fill split");
+};
+
+// Byte offset of 16-byte chunk `c` (0..7) of LDS row `row` (128-byte rows). XOR swizzle:
+// the 8 rows that 8 consecutive lanes read at one chunk index fall in distinct banks.
+__device__ __forceinline__ int lds_off(int row, int c) { return row * ROWB + ((c ^ (row & 7)) << 4); }
+
+// Chunk a lane fetches in a direct fill: the fill writes lane i to LDS slot i%8 of row
+// (group*8 + i/8), which holds global chunk (i%8) ^ (row%8) = (i%8) ^ (i/8).
+__device__ __forceinline__ int fill_chunk(int lane) { return (lane & 7) ^ ((lane >> 3) & 7); }
 
 __device__ __forceinline__ u32x4_t lds_read16(const char* base, int off) {
   return *reinterpret_cast<const u32x4_t*>(base + off);
@@ -48,8 +78,28 @@ __device__ __forceinline__ void lds_write16(char* base, int off, u32x4_t v) {
   *reinterpret_cast<u32x4_t*>(base + off) = v;
 }
 
-template <int WDT, bool HAS_W, bool IN_T, bool GATHER>
-__global__ void __launch_bounds__(NT, 1)
+// One wave instruction: 8 LDS rows starting at row grp*8 of `lds_tile` from `src`
+// (this lane's 16 source bytes).
+__device__ __forceinline__ void direct_fill(char* lds_tile, int grp, const void* src) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(lds_tile + grp * 1024), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0) with expcnt/lgkmcnt left unconstrained (gfx9 encoding).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+// Workgroup barrier of the K loop. Its vmcnt wait is explicit, so it must not carry the
+// release fence of __syncthreads(), which would also wait for the fill in flight.
+// This wave's LDS reads are complete (lgkmcnt(0)) before it, and the empty asm keeps
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
+__global__ void __launch_bounds__(C::NT, 1)
 prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const int64_t* __restrict__ gidx, int64_t grows,
                const void* __restrict__ w, int64_t ldw, const float* __restrict__ w_scale,
@@ -57,205 +107,313 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const uint16_t* __restrict__ tg, int64_t ldt,
                const uint16_t* __restrict__ bm, int64_t ldb, float s,
                uint16_t* __restrict__ y, int64_t ldy,
-               int M, int N, int K, int r, int tiles_m) {
-  __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
+               int M, int N, int K, int r, int tiles_m, int tiles_n) {
+  constexpr bool W8 = HAS_W && WDT == kFP8;
+  constexpr bool WDIRECT = HAS_W && WDT == kBF16;
+  constexpr bool LORA = RB > 0 || EXT_T;
+  constexpr int NT = C::NT;
+  constexpr int AB = RB * 32 * ROWB;         // rank-A slice of a K tile
+  constexpr int STAGE = C::XB + C::WB + AB;  // one of the two ring buffers
+  static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+  static_assert(C::BM * ROWB + 16384 <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wi = wave & 1;   // n half of the tile
-  const int wj = wave >> 1;  // m half of the tile
+  // wave index as a scalar: the LDS bases of the direct fills (M0) derive from it
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave % C::WNW;
+  const int wm = wave / C::WNW;
   const int l32 = lane & 31;
   const int lh = lane >> 5;
 
-  const int tile = blockIdx.x;
-  const int tm = tile % tiles_m;
-  const int tn = tile / tiles_m;
-  const int m0 = tm * BM;
-  const int n0 = tn * BN;
+  // ---- XCD-aware, grouped tile order ----
+  const int G = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if (G % N_XCD == 0) t = (t % N_XCD) * (G / N_XCD) + t / N_XCD;
+  const int group_size = GROUP_M * tiles_n;
+  const int first_m = (t / group_size) * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (t % group_size) % gm;
+  const int tn = (t % group_size) / gm;
+  const int m0 = tm * C::BM;
+  const int n0 = tn * C::BN;
 
-  // ---- global -> register staging (8 chunks per operand tile per thread) ----
-  // chunk id = i*256 + tid  ->  row = i*32 + tid/8, chunk = tid%8
-  const int ld_c = tid & 7;
-  const int ld_r = tid >> 3;
-  u32x4_t stx[8];
-  u32x4_t stw[8];
-  u32x4_t sta[2];
-
-  const int rpad32 = IN_T ? ((r + 31) & ~31) : 0;  // rank rows computed in-kernel
-
-  auto load_stage = [&](int k0) {
+  // ---- sources of this wave's direct fills: uniform tile base + 32-bit lane offset ----
+  const int fc = fill_chunk(lane);
+  const char* xbase = reinterpret_cast<const char*>(GATHER ? x : x + (int64_t)m0 * ldx);
+  uint32_t xoff[C::NXI];
+  const uint16_t* xg[GATHER ? C::NXI : 1];  // gathered rows keep 64-bit row pointers
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int row = m0 + i * 32 + ld_r;
-      row = row < M ? row : M - 1;
-      if constexpr (GATHER) {
-        const int64_t id = gidx[row];
-        stx[i] = (id >= 0 && id < grows) ? ld_global_16(x + id * ldx + k0 + ld_c * 8) : zero_u32x4();
-      } else {
-        stx[i] = ld_global_16(x + (int64_t)row * ldx + k0 + ld_c * 8);
-      }
+  for (int i = 0; i < C::NXI; ++i) {
+    const int row = (wave * C::NXI + i) * 8 + (lane >> 3);
+    const int gr = min(m0 + row, M - 1);
+    if constexpr (GATHER) {
+      const int64_t id = gidx[gr];
+      xg[i] = x + ((id >= 0 && id < grows) ? id : 0) * ldx + fc * 8;  // bad ids: zeroed at the store
+      xoff[i] = 0;
+    } else {
+      xoff[i] = (uint32_t)((gr - m0) * ldx * 2 + fc * 16);
     }
-    if constexpr (HAS_W) {
-      if constexpr (WDT == kBF16) {
-        const uint16_t* wp = reinterpret_cast<const uint16_t*>(w);
+  }
+  const char* wbase = reinterpret_cast<const char*>(w) + (WDIRECT ? (int64_t)n0 * ldw * 2 : 0);
+  uint32_t woff[C::NWI];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          int row = n0 + i * 32 + ld_r;
-          row = row < N ? row : N - 1;
-          stw[i] = ld_global_16(wp + (int64_t)row * ldw + k0 + ld_c * 8);
-        }
-      } else {
-        // fp8: 64 bytes per row = 4 chunks of 16 fp8; thread handles rows i*64 + tid/4
-        const uint8_t* wp = reinterpret_cast<const uint8_t*>(w);
+  for (int i = 0; i < C::NWI; ++i) {
+    const int row = (wave * C::NWI + i) * 8 + (lane >> 3);
+    woff[i] = (uint32_t)((min(n0 + row, N - 1) - n0) * ldw * 2 + fc * 16);
+  }
+  // rank-A slice: RB*32 rows = RB*4 fills, one per wave for waves < RB*4 (rows >= r read
+  // row r-1 and are zeroed before the MFMA)
+  constexpr int NAI = RB * 4;
+  uint32_t aoff = 0;
+  if constexpr (RB > 0) aoff = (uint32_t)(min(wave * 8 + (lane >> 3), r - 1) * lda * 2 + fc * 16);
+  // fp8 W: BN rows x 64 B per K tile, 16 fp8 per chunk
+  constexpr int W8C = W8 ? C::BN * 4 / NT : 1;  // chunks per thread
+  const uint8_t* w8row[W8C];
+  if constexpr (W8) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          int row = n0 + i * 64 + (tid >> 2);
-          row = row < N ? row : N - 1;
-          u32x4_t q = ld_global_16(wp + (int64_t)row * ldw + k0 + (tid & 3) * 16);
-          fp8x16_to_bf16x16(q, stw[2 * i], stw[2 * i + 1]);
-        }
-      }
-    }
-    if constexpr (IN_T) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        int row = i * 32 + ld_r;
-        sta[i] = (row < r) ? ld_global_16(a + (int64_t)row * lda + k0 + ld_c * 8) : zero_u32x4();
-      }
-    }
-  };
-
-  auto store_stage = [&](int stage) {
-    char* sx = lds + stage * STAGE_BYTES;
-    char* sw = sx + TILE_BYTES;
-    char* sa = sw + TILE_BYTES;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) lds_write16(sx, lds_off(i * 32 + ld_r, ld_c), stx[i]);
-    if constexpr (HAS_W) {
-      if constexpr (WDT == kBF16) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lds_write16(sw, lds_off(i * 32 + ld_r, ld_c), stw[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          int row = i * 64 + (tid >> 2);
-          int c = (tid & 3) * 2;
-          lds_write16(sw, lds_off(row, c), stw[2 * i]);
-          lds_write16(sw, lds_off(row, c + 1), stw[2 * i + 1]);
-        }
-      }
-    }
-    if constexpr (IN_T) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        int row = i * 32 + ld_r;
-        if (row < rpad32) lds_write16(sa, lds_off(row, ld_c), sta[i]);
-      }
-    }
-  };
-
-  f32x16_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  f32x16_t acct[2][2];  // [rank block][m block] of this wave's 64 T rows
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acct[i][j][v] = 0.f;
-
-  constexpr bool RUN_K = HAS_W || IN_T;
-  if constexpr (RUN_K) {
-    const int nk = K / BK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int stage = kt & 1;
-      if (kt + 1 < nk) load_stage((kt + 1) * BK);
-      const char* sx = lds + stage * STAGE_BYTES;
-      const char* sw = sx + TILE_BYTES;
-      const char* sa = sw + TILE_BYTES;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int c = kk * 2 + lh;
-        bf16x8_t xf[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          xf[j] = as_bf16x8(lds_read16(sx, lds_off(wj * 128 + j * 32 + l32, c)));
-        if constexpr (HAS_W) {
-          bf16x8_t wf[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            wf[i] = as_bf16x8(lds_read16(sw, lds_off(wi * 128 + i * 32 + l32, c)));
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
-        }
-        if constexpr (IN_T) {
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
-            if (rb * 32 < rpad32) {
-              bf16x8_t af = as_bf16x8(lds_read16(sa, lds_off(rb * 32 + l32, c)));
-#pragma unroll
-              for (int jj = 0; jj < 2; ++jj)
-                acct[rb][jj] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, xf[2 * wi + jj], acct[rb][jj], 0, 0, 0);
-            }
-          }
-        }
-      }
-      if (kt + 1 < nk) store_stage(stage ^ 1);
-      __syncthreads();
+    for (int i = 0; i < W8C; ++i) {
+      const int id = i * NT + tid;
+      w8row[i] = reinterpret_cast<const uint8_t*>(w) + (int64_t)min(n0 + (id >> 2), N - 1) * ldw + (id & 3) * 16;
     }
   }
 
-  // ---- per-output-channel dequantisation scale (fp8 base) ----
-  if constexpr (HAS_W && WDT == kFP8) {
+  auto issue = [&](int stage, int k0) {
+    char* sx = lds + stage * STAGE;
+    char* sw = sx + C::XB;
+    char* sa = sw + C::WB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < C::NXI; ++i) {
+      if constexpr (GATHER) direct_fill(sx, wave * C::NXI + i, xg[i] + k0);
+      else direct_fill(sx, wave * C::NXI + i, xbase + k0 * 2 + xoff[i]);
+    }
+    if constexpr (WDIRECT) {
+#pragma unroll
+      for (int i = 0; i < C::NWI; ++i) direct_fill(sw, wave * C::NWI + i, wbase + k0 * 2 + woff[i]);
+    }
+    if constexpr (RB > 0) {
+      if (wave < NAI) direct_fill(sa, wave, reinterpret_cast<const char*>(a) + k0 * 2 + aoff);
+    }
+  };
+  // B slice [BN][64 ranks from rk0] into `dst`. Lanes past rank r read a finite element
+  // of their own row instead; T is zero at those ranks, so they contribute nothing.
+  auto issue_b = [&](char* dst, int rk0) {
+#pragma unroll
+    for (int i = 0; i < C::NBI; ++i) {
+      const int grp = wave * C::NBI + i;
+      const int row = grp * 8 + (lane >> 3);
+      const int kr = rk0 + fc * 8;
+      const uint16_t* src = bm + (int64_t)min(n0 + row, N - 1) * ldb + (kr < r ? kr : 0);
+      direct_fill(dst, grp, src);
+    }
+  };
+
+  u32x4_t w8stage[W8C];
+  auto load_w8 = [&](int k0) {
+    if constexpr (W8) {
+#pragma unroll
+      for (int i = 0; i < W8C; ++i) w8stage[i] = ld_global_16(w8row[i] + k0);
+    }
+  };
+  auto store_w8 = [&](int stage) {
+    if constexpr (W8) {
+      char* sw = lds + stage * STAGE + C::XB;
+#pragma unroll
+      for (int i = 0; i < W8C; ++i) {
+        const int id = i * NT + tid;
+        const int row = id >> 2, c = (id & 3) * 2;
+        u32x4_t lo, hi;
+        fp8x16_to_bf16x16(w8stage[i], lo, hi);
+        lds_write16(sw, lds_off(row, c), lo);
+        lds_write16(sw, lds_off(row, c + 1), hi);
+      }
+    }
+  };
+
+  // ---- T work split: TBLK (m block, rank block) pairs per m strip, shared by WNW waves ----
+  constexpr int TBLK = C::MJ * RB;
+  constexpr int TPW = (RB == 0) ? 0 : (TBLK >= C::WNW ? TBLK / C::WNW : 1);  // blocks per wave
+  constexpr int KSPLIT = (RB == 0 || TBLK >= C::WNW) ? 1 : C::WNW / TBLK;   // waves per block
+  static_assert(RB == 0 || TBLK % C::WNW == 0 || C::WNW % TBLK == 0, "T split");
+  static_assert(KSPLIT <= 2, "T partial hand-off covers two phases");
+  const int t_first = (KSPLIT == 1) ? wn * TPW : wn % TBLK;  // first T block of this wave
+  const int t_phase = (KSPLIT == 1) ? 0 : wn / TBLK;          // k-step phase (KSPLIT > 1)
+
+  f32x16_t acc[C::NI][C::MJ];
+#pragma unroll
+  for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+    for (int j = 0; j < C::MJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  constexpr int TPWX = TPW > 0 ? TPW : 1;
+  f32x16_t acct[TPWX];
+#pragma unroll
+  for (int q = 0; q < TPWX; ++q)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acct[q][v] = 0.f;
+  bool tlive[TPWX];  // rank rows of the T block exist (rows >= r multiply by zero)
+  int tj[TPWX], trb[TPWX];
+#pragma unroll
+  for (int q = 0; q < TPWX; ++q) {
+    const int b = t_first + q;
+    tj[q] = b % C::MJ;
+    trb[q] = b / C::MJ;
+    tlive[q] = trb[q] * 32 + l32 < r;
+  }
+
+  // Fragments of one 16-wide k step: x rows (MFMA B operand), W rows and rank-A rows
+  // (A operand).
+  struct Frags {
+    u32x4_t x[C::MJ];
+    u32x4_t w[C::NI];
+    u32x4_t a[TPWX];
+  };
+  auto frag_load = [&](int stage, int kk, Frags& f) {
+    const char* sx = lds + stage * STAGE;
+    const char* sw = sx + C::XB;
+    const char* sa = sw + C::WB;
+    const int c = kk * 2 + lh;
+#pragma unroll
+    for (int j = 0; j < C::MJ; ++j) f.x[j] = lds_read16(sx, lds_off(wm * C::TM + j * 32 + l32, c));
+    if constexpr (HAS_W) {
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i) f.w[i] = lds_read16(sw, lds_off(wn * C::TN + i * 32 + l32, c));
+    }
+    if constexpr (RB > 0) {
+      if (KSPLIT == 1 || t_phase == (kk % KSPLIT)) {
+#pragma unroll
+        for (int q = 0; q < TPW; ++q) {
+          const u32x4_t av = lds_read16(sa, lds_off(trb[q] * 32 + l32, c));
+          f.a[q] = tlive[q] ? av : zero_u32x4();
+        }
+      }
+    }
+  };
+  auto frag_mma = [&](const Frags& f, int kk) {
+    if constexpr (HAS_W) {
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::MJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f.w[i]), as_bf16x8(f.x[j]), acc[i][j], 0, 0, 0);
+    }
+    if constexpr (RB > 0) {
+      if (KSPLIT == 1 || t_phase == (kk % KSPLIT)) {
+#pragma unroll
+        for (int q = 0; q < TPW; ++q) {
+          u32x4_t xt = f.x[0];
+#pragma unroll
+          for (int j = 1; j < C::MJ; ++j) xt = (tj[q] == j) ? f.x[j] : xt;  // whole-vector select
+          acct[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f.a[q]), as_bf16x8(xt), acct[q], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  const int nk = K / BK;
+  // The last K tile runs from buffer (nk-1)&1; the B slice of the LoRA phase is filled
+  // into the other one while it does.
+  char* lora_t = lds + ((nk - 1) & 1) * STAGE;
+  char* lora_b = lds + (nk & 1) * STAGE;
+
+  constexpr bool RUN_K = HAS_W || RB > 0;
+  if constexpr (RUN_K) {
+    issue(0, 0);
+    load_w8(0);
+    wait_vm0();
+    store_w8(0);
+    ring_barrier();
+    if (nk > 1) {
+      issue(1, BK);
+      load_w8(BK);
+    }
+    if constexpr (LORA) {
+      if (nk == 1) issue_b(lora_b, 0);
+    }
+    Frags cur;
+    frag_load(0, 0, cur);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+#pragma unroll
+      for (int kk = 0; kk < KK - 1; ++kk) {
+        Frags nxt;
+        frag_load(buf, kk + 1, nxt);
+        frag_mma(cur, kk);
+        cur = nxt;
+      }
+      if (kt + 1 < nk) {
+        wait_vm0();          // tile kt+1 has landed (the only fill in flight)
+        store_w8(buf ^ 1);   // fp8 base: decoded tile kt+1 into its buffer
+        ring_barrier();      // all fragments of tile kt are read; tile kt+1 visible
+        if (kt + 2 < nk) {
+          issue(buf, (kt + 2) * BK);
+          load_w8((kt + 2) * BK);
+        } else if constexpr (LORA) {
+          issue_b(lora_b, 0);  // kt + 2 == nk: buffer `buf` is lora_b
+        }
+      }
+      // One code path for the last k step of every tile keeps the accumulators in one
+      // register class. After the last tile this read of the idle buffer is discarded.
+      Frags nxt;
+      frag_load(buf ^ 1, 0, nxt);
+      frag_mma(cur, KK - 1);
+      cur = nxt;
+    }
+    __syncthreads();  // every wave is done with the ring before the LDS is reused
+  } else if constexpr (LORA) {
+    issue_b(lora_b, 0);
+  }
+
+  // ---- per-output-channel dequantisation scale (fp8 base) ----
+  if constexpr (W8) {
+#pragma unroll
+    for (int i = 0; i < C::NI; ++i) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          int n = n0 + wi * 128 + i * 32 + g * 8 + lh * 4 + e;
-          float sc = w_scale[n < N ? n : N - 1];
+          const int n = n0 + wn * C::TN + i * 32 + g * 8 + lh * 4 + e;
+          const float sc = w_scale[min(n, N - 1)];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j][g * 4 + e] *= sc;
+          for (int j = 0; j < C::MJ; ++j) acc[i][j][g * 4 + e] *= sc;
         }
       }
     }
   }
 
   // ---- LoRA up-projection: acc[n][m] += sum_j B[n][j] * T[m][j] in 64-rank chunks ----
-  if (r > 0) {
-    char* st = lds;               // T chunk  [256 m][64 ranks]
-    char* sb = lds + TILE_BYTES;  // B chunk  [256 n][64 ranks]
-    if constexpr (IN_T) {
-      // Park bf16(s * T) for this wave's 64 m rows (m block 2*wi + jj of half wj).
+  if constexpr (LORA) {
+    char* st = lora_t;                   // T chunk [BM m][64 ranks]
+    char* sp = lora_t + C::BM * ROWB;    // fp32 T partials of split k steps (16 KB)
+    char* sb = lora_b;                   // B chunk [BN n][64 ranks]
+    if constexpr (RB > 0) {
+      if constexpr (KSPLIT > 1) {
+        // phase-1 waves hand their partial sums to the phase-0 wave of the same block
+        float* part = reinterpret_cast<float*>(sp);
+        const int slot = (wm * TBLK + t_first) * 64 + lane;
+        if (t_phase == 1) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
+          for (int v = 0; v < 16; ++v) part[slot * 16 + v] = acct[0][v];
+        }
+        __syncthreads();
+        if (t_phase == 0) {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const int mrow = wj * 128 + (2 * wi + jj) * 32 + l32;
+          for (int v = 0; v < 16; ++v) acct[0][v] += part[slot * 16 + v];
+        }
+      }
+      if (t_phase == 0) {
+        // park bf16(s * T): rows wm*TM + tj*32 + l32, ranks trb*32 + 8g + 4*lh + e
+#pragma unroll
+        for (int q = 0; q < TPW; ++q) {
+          const int mrow = wm * C::TM + tj[q] * 32 + l32;
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            // ranks rb*32 + 8g + 4*lh + e, e = 0..3  -> 8 contiguous bytes of chunk rb*4+g
-            uint32_t lo = pack_bf16x2(s * acct[rb][jj][g * 4 + 0], s * acct[rb][jj][g * 4 + 1]);
-            uint32_t hi = pack_bf16x2(s * acct[rb][jj][g * 4 + 2], s * acct[rb][jj][g * 4 + 3]);
             uint2 v;
-            v.x = lo;
-            v.y = hi;
-            *reinterpret_cast<uint2*>(st + lds_off(mrow, rb * 4 + g) + lh * 8) = v;
+            v.x = pack_bf16x2(s * acct[q][g * 4 + 0], s * acct[q][g * 4 + 1]);
+            v.y = pack_bf16x2(s * acct[q][g * 4 + 2], s * acct[q][g * 4 + 3]);
+            *reinterpret_cast<uint2*>(st + lds_off(mrow, trb[q] * 4 + g) + lh * 8) = v;
           }
         }
       }
@@ -263,41 +421,32 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int nrc = (r + 63) / 64;
     for (int rc = 0; rc < nrc; ++rc) {
       const int rk0 = rc * 64;
-      // B chunk: rows n0.., ranks rk0 + ld_c*8 (masked beyond r)
+      if (rc > 0) issue_b(sb, rk0);
+      if constexpr (EXT_T) {
+        constexpr int TCH = C::BM * 8 / NT;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int row = n0 + i * 32 + ld_r;
-        row = row < N ? row : N - 1;
-        int kr = rk0 + ld_c * 8;
-        u32x4_t v = (kr < r) ? ld_global_16(bm + (int64_t)row * ldb + kr) : zero_u32x4();
-        lds_write16(sb, lds_off(i * 32 + ld_r, ld_c), v);
-      }
-      if constexpr (!IN_T) {
-        // T chunk from the pre-pass workspace (zero-padded to ldt columns)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          int row = m0 + i * 32 + ld_r;
-          row = row < M ? row : M - 1;
-          lds_write16(st, lds_off(i * 32 + ld_r, ld_c),
-                      ld_global_16(tg + (int64_t)row * ldt + rk0 + ld_c * 8));
+        for (int i = 0; i < TCH; ++i) {
+          const int id = i * NT + tid;
+          const int row = id >> 3, kr = rk0 + (id & 7) * 8;
+          const u32x4_t v = (kr < r) ? ld_global_16(tg + (int64_t)min(m0 + row, M - 1) * ldt + kr) : zero_u32x4();
+          lds_write16(st, lds_off(row, id & 7), v);
         }
       }
+      wait_vm0();
       __syncthreads();
       const int rem = r - rk0;
       const int nkk = rem >= 64 ? 4 : (rem + 15) / 16;
       for (int kk = 0; kk < nkk; ++kk) {
         const int c = kk * 2 + lh;
-        bf16x8_t tf[4], bf[4];
+        bf16x8_t tf[C::MJ], bf[C::NI];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          tf[j] = as_bf16x8(lds_read16(st, lds_off(wj * 128 + j * 32 + l32, c)));
+        for (int j = 0; j < C::MJ; ++j) tf[j] = as_bf16x8(lds_read16(st, lds_off(wm * C::TM + j * 32 + l32, c)));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          bf[i] = as_bf16x8(lds_read16(sb, lds_off(wi * 128 + i * 32 + l32, c)));
+        for (int i = 0; i < C::NI; ++i) bf[i] = as_bf16x8(lds_read16(sb, lds_off(wn * C::TN + i * 32 + l32, c)));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < C::NI; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < C::MJ; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[i], tf[j], acc[i][j], 0, 0, 0);
       }
       __syncthreads();
@@ -306,45 +455,46 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
   // ---- store: lane holds y[m][n..n+3] for m = col, n = 8g + 4*lh + (0..3) ----
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + wj * 128 + j * 32 + l32;
+  for (int j = 0; j < C::MJ; ++j) {
+    const int m = m0 + wm * C::TM + j * 32 + l32;
     if (m >= M) continue;
+    float keep = 1.f;
+    if constexpr (GATHER) {
+      const int64_t id = gidx[m];
+      keep = (id >= 0 && id < grows) ? 1.f : 0.f;  // out-of-range ids give zero rows
+    }
     uint16_t* yr = y + (int64_t)m * ldy;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < C::NI; ++i) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wi * 128 + i * 32 + g * 8 + lh * 4;
-        const f32x16_t& c = acc[i][j];
+        const int n = n0 + wn * C::TN + i * 32 + g * 8 + lh * 4;
+        const f32x16_t& cc = acc[i][j];
         if (n + 3 < N) {
           uint2 v;
-          v.x = pack_bf16x2(c[g * 4 + 0], c[g * 4 + 1]);
-          v.y = pack_bf16x2(c[g * 4 + 2], c[g * 4 + 3]);
+          v.x = pack_bf16x2(keep * cc[g * 4 + 0], keep * cc[g * 4 + 1]);
+          v.y = pack_bf16x2(keep * cc[g * 4 + 2], keep * cc[g * 4 + 3]);
           *reinterpret_cast<uint2*>(yr + n) = v;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (n + e < N) yr[n + e] = f32_to_bf16_bits(c[g * 4 + e]);
+            if (n + e < N) yr[n + e] = f32_to_bf16_bits(keep * cc[g * 4 + e]);
         }
       }
     }
   }
 }
 
-// T[m][j] = bf16(s * x[m] . A[j]) for j < r, 0 for r <= j < ldt. One thread per (m, j).
-// Pre-pass for ranks above the in-kernel limit.
+// T[m][j] = bf16(s * x[m] . A[j]), one thread per (m, j): pre-pass for ranks above the
+// in-kernel limit (row stride ldt).
 __global__ void __launch_bounds__(256) down_pad_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                        const uint16_t* __restrict__ a, int64_t lda,
                                                        float s, uint16_t* __restrict__ t,
                                                        int64_t ldt, int64_t M, int64_t K,
                                                        int64_t r) {
   int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= M * ldt) return;
-  int64_t m = idx / ldt, j = idx % ldt;
-  if (j >= r) {
-    t[idx] = 0;
-    return;
-  }
+  if (idx >= M * r) return;
+  int64_t m = idx / r, j = idx % r;
   const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(x + m * ldx);
   const u32x4_t* ar = reinterpret_cast<const u32x4_t*>(a + j * lda);
   float acc = 0.f;
@@ -356,28 +506,67 @@ __global__ void __launch_bounds__(256) down_pad_kernel(const uint16_t* __restric
       acc += bf16_bits_to_f32(xv[q] >> 16) * bf16_bits_to_f32(av[q] >> 16);
     }
   }
-  t[idx] = f32_to_bf16_bits(s * acc);
+  t[m * ldt + j] = f32_to_bf16_bits(s * acc);
 }
 
-template <int WDT, bool HAS_W, bool IN_T, bool GATHER = false>
-hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
-  const int tiles_m = (int)((p.M + BM - 1) / BM);
-  const int tiles_n = (int)((p.N + BN - 1) / BN);
-  prefill_kernel<WDT, HAS_W, IN_T, GATHER><<<dim3(tiles_m * tiles_n), dim3(NT), 0, p.stream>>>(
+using CfgBig = Cfg<256, 256, 2, 8>;   // 8 waves, 128(n) x 64(m) per wave
+using CfgTall = Cfg<128, 256, 4, 8>;  // 8 waves, 64 x 64 per wave
+
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
+hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+  const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
+  const int tiles_n = (int)((p.N + C::BN - 1) / C::BN);
+  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER><<<dim3(tiles_m * tiles_n), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale,
-      reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m);
+      reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Fraction of the 256 CUs kept busy over the launch's waves of workgroups.
+double wave_efficiency(int64_t tiles) {
+  const int64_t waves = (tiles + 255) / 256;
+  return (double)tiles / (double)(waves * 256);
+}
+
+// 128-row tiles trade register reuse for occupancy; used when they fill the chip better.
+bool use_tall(const LoraArgs& p) {
+  const int64_t tn = (p.N + 255) / 256;
+  const double big = wave_efficiency(((p.M + 255) / 256) * tn);
+  const double tall = wave_efficiency(((p.M + 127) / 128) * tn) * 0.85;
+  return tall > big;
+}
+
+template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER = false>
+hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+  // Two in-kernel rank blocks do not fit beside the 128 x 128 accumulators of the
+  // 4-wave tile; those ranks use the 8-wave configuration.
+  if constexpr (RB == 2) {
+    return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+  } else {
+    return use_tall(p) ? launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt)
+                       : launch_cfg<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+  }
+}
+
+template <int WDT, bool HAS_W>
+hipError_t launch_rank(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+  if (p.r == 0) return launch_variant<WDT, HAS_W, 0, false>(p, nullptr, 0);
+  if (p.r <= 32) return launch_variant<WDT, HAS_W, 1, false>(p, nullptr, 0);
+  if (p.r <= RIN) return launch_variant<WDT, HAS_W, 2, false>(p, nullptr, 0);
+  return launch_variant<WDT, HAS_W, 0, true>(p, tg, ldt);
+}
+
+bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
 }  // namespace
 
 bool prefill_supported(const LoraArgs& p) {
   if (p.K % BK != 0) return false;
   if (p.M > (int64_t)1 << 30 || p.N > (int64_t)1 << 30 || p.K > (int64_t)1 << 30) return false;
+  // 32-bit lane offsets of the direct fills cover a 256-row tile of x and W
+  if (p.ldx > ((int64_t)1 << 22) || p.ldw > ((int64_t)1 << 22) || p.lda > ((int64_t)1 << 22)) return false;
   if (!aligned16(p.x) || p.ldx % 8 != 0) return false;
   if (p.w != nullptr) {
     if (!aligned16(p.w)) return false;
@@ -396,23 +585,21 @@ bool prefill_supported(const LoraArgs& p) {
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
   (void)N; (void)K; (void)w_dtype;
   if (r <= RIN) return 0;
-  const int64_t ldt = (r + 63) / 64 * 64;
-  return (size_t)(M * ldt * 2);
+  return (size_t)(M * r * 2);
 }
 
 hipError_t launch_prefill(const LoraArgs& p) {
   if (p.gather != nullptr) {
     // factorized embedding: gathered x rows, bf16 base, no LoRA term
-    return launch_variant<kBF16, true, false, true>(p, nullptr, 0);
+    return launch_variant<kBF16, true, 0, false, true>(p, nullptr, 0);
   }
   const bool has_w = p.w != nullptr;
-  const bool in_t = p.r > 0 && p.r <= RIN;
   const uint16_t* tg = nullptr;
   int64_t ldt = 0;
   if (p.r > RIN) {
-    ldt = (p.r + 63) / 64 * 64;
+    ldt = p.r;
     uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
-    int64_t n = p.M * ldt;
+    const int64_t n = p.M * p.r;
     down_pad_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, p.stream>>>(
         reinterpret_cast<const uint16_t*>(p.x), p.ldx, reinterpret_cast<const uint16_t*>(p.a),
         p.lda, p.scale, t, ldt, p.M, p.K, p.r);
@@ -420,16 +607,9 @@ hipError_t launch_prefill(const LoraArgs& p) {
     if (e != hipSuccess) return e;
     tg = t;
   }
-  if (p.w_dtype == kFP8 && has_w) {
-    return in_t ? launch_variant<kFP8, true, true>(p, tg, ldt)
-                : launch_variant<kFP8, true, false>(p, tg, ldt);
-  }
-  if (has_w) {
-    return in_t ? launch_variant<kBF16, true, true>(p, tg, ldt)
-                : launch_variant<kBF16, true, false>(p, tg, ldt);
-  }
-  return in_t ? launch_variant<kBF16, false, true>(p, tg, ldt)
-              : launch_variant<kBF16, false, false>(p, tg, ldt);
+  if (has_w && p.w_dtype == kFP8) return launch_rank<kFP8, true>(p, tg, ldt);
+  if (has_w) return launch_rank<kBF16, true>(p, tg, ldt);
+  return launch_rank<kBF16, false>(p, tg, ldt);
 }
 
 }  // namespace wsl
