@@ -55,12 +55,18 @@ Path choose_path(const wsl::LoraArgs& p) {
   return Path::kGeneric;
 }
 
-size_t generic_ws(int64_t M, int64_t r) { return (size_t)(M * r * 2); }
+// Workspace layout: kCounterBytes of arrival counters (decode path), then the path's
+// scratch. The prefill and generic paths place their scratch after the prefix, so the
+// counters stay zero whichever path a call takes.
+size_t generic_ws(int64_t M, int64_t r) { return wsl::kCounterBytes + (size_t)(M * r * 2); }
+size_t prefill_ws(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
+  return wsl::kCounterBytes + wsl::prefill_workspace_bytes(M, N, K, r, w_dtype);
+}
 
 size_t workspace_for(const wsl::LoraArgs& p) {
   switch (choose_path(p)) {
     case Path::kDecode: return wsl::decode_workspace_bytes(p.M, p.N, p.K, p.r, p.w_dtype);
-    case Path::kPrefill: return wsl::prefill_workspace_bytes(p.M, p.N, p.K, p.r, p.w_dtype);
+    case Path::kPrefill: return prefill_ws(p.M, p.N, p.K, p.r, p.w_dtype);
     case Path::kGeneric: return generic_ws(p.M, p.r);
     default: return 0;
   }
@@ -70,7 +76,7 @@ size_t workspace_for(const wsl::LoraArgs& p) {
 // pointer alignment, which the size query does not see).
 size_t workspace_upper_bound(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
   size_t b = generic_ws(M, r);
-  size_t pf = wsl::prefill_workspace_bytes(M, N, K, r, w_dtype);
+  size_t pf = prefill_ws(M, N, K, r, w_dtype);
   if (pf > b) b = pf;
   if (M >= 1 && M <= wsl::kDecodeMaxM) {
     size_t d = wsl::decode_workspace_bytes(M, N, K, r, w_dtype);
@@ -148,15 +154,19 @@ int wsl_lora_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, 
 
   Path path = choose_path(p);
   if (path == Path::kNone) return WSL_OK;
-  size_t need = workspace_for(p);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+  const size_t need = workspace_for(p);
+  if (workspace == nullptr || workspace_bytes < need)
     return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
-  if (need > 0 && ((uintptr_t)workspace & 15))
-    return fail(WSL_E_ALIGN, "workspace must be 16-byte aligned");
+  if ((uintptr_t)workspace & 255)
+    return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
   rc = check_device();
   if (rc != WSL_OK) return rc;
 
   hipError_t e;
+  if (path != Path::kDecode) {
+    p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes;
+    p.ws_bytes = workspace_bytes - wsl::kCounterBytes;
+  }
   switch (path) {
     case Path::kDecode: e = wsl::launch_decode(p); break;
     case Path::kPrefill: e = wsl::launch_prefill(p); break;

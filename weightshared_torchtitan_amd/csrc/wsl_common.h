@@ -41,8 +41,6 @@ __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t q) {
 }
 
 // 16 fp8 (one 16-byte chunk) -> 16 bf16 (two 16-byte chunks).
-__device__ __forceinline__ void fp8x16_to_bf16x16(const u32x4_t& q, u32x4_t& lo, u32x4_t& hi);
-
 __device__ __forceinline__ void fp8x16_to_bf16x16(const u32x4_t& q, u32x4_t& lo, u32x4_t& hi) {
   lo = u32x4_t{fp8x2_to_bf16x2<false>(q[0]), fp8x2_to_bf16x2<true>(q[0]),
                fp8x2_to_bf16x2<false>(q[1]), fp8x2_to_bf16x2<true>(q[1])};
@@ -107,5 +105,10 @@ hipError_t launch_factorized_embedding(const int64_t* ids, int64_t n_ids, const 
 
 // Largest M routed to the decode-shaped (skinny) kernels.
 constexpr int64_t kDecodeMaxM = 64;
+
+// Every workspace starts with this many bytes of arrival counters. They must be zero
+// when the workspace is first used; every launch leaves them zero. Path-specific
+// scratch follows the prefix.
+constexpr size_t kCounterBytes = 65536;
 
 }  // namespace wsl

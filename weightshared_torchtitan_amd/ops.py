@@ -48,6 +48,25 @@ def _check_device(*ts: Optional[torch.Tensor]) -> torch.device:
     return dev
 
 
+_WS_MIN_BYTES = 16 << 20
+_workspaces: dict = {}
+
+
+def workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """The persistent scratch buffer of (device, stream).
+
+    libwsl requires its workspace to be zero-filled before first use (the leading
+    arrival counters of the decode kernels) and leaves it that way, so one zero-filled
+    buffer per stream is reused by every call on that stream; it only grows.
+    """
+    key = (dev.index, stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(2 * nbytes, _WS_MIN_BYTES), dtype=torch.uint8, device=dev)
+        _workspaces[key] = buf
+    return buf
+
+
 def _out_features(w: Optional[torch.Tensor], b: Optional[torch.Tensor]) -> int:
     if w is not None:
         return w.shape[0]
@@ -99,8 +118,8 @@ def lora_linear_op(x: torch.Tensor, w: Optional[torch.Tensor], w_scale: Optional
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     if M > 0:
         ws_bytes = _native.workspace_bytes(M, N, K, r, w_dtype)
-        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev) if ws_bytes else None
         stream = torch.cuda.current_stream(dev).cuda_stream
+        ws = workspace(dev, stream, ws_bytes)
         with torch.cuda.device(dev):
             rc = _native.lib().wsl_lora_linear_fwd(
                 x2.data_ptr(), x2.stride(0),
@@ -110,7 +129,9 @@ def lora_linear_op(x: torch.Tensor, w: Optional[torch.Tensor], w_scale: Optional
                 float(scale),
                 y.data_ptr(), y.stride(0),
                 M, N, K, r,
-                _dev_ptr(ws), ws_bytes, stream)
+                ws.data_ptr(), ws.numel(), stream)
+        if rc != _native.WSL_OK:
+            _workspaces.pop((dev.index, stream), None)  # a failed launch may leave counters set
         _native.check(rc, "wsl_lora_linear_fwd")
     return y.reshape(*lead, N)
 
