@@ -11,12 +11,19 @@ weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
 projections, and the CPU baseline (the reference's fp32 arithmetic on host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
+                      [--only c2|c3|c4|c5] [--copy-calibration]
+
+--only runs one section and prints its JSON alone (for profiling one workload).
+--copy-calibration first runs a plain device copy of COPY_BYTES bytes (three launches),
+the reference point against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are
+scaled to HBM bytes.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -30,6 +37,8 @@ METRIC = "fused-LoRA linear TFLOP/s (% MFMA peak); weight-shared Qwen3 decode to
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 FP8_PEAK_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+COPY_BYTES = 256 << 20      # size of the calibration copy (--copy-calibration)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "prefill_kernel_c2_hbm_traffic.md")
 
 # (name, N, K) of the seven projections, as functions of (hidden, q_out, kv_out, ffn)
 def proj_shapes(hidden, q_out, kv_out, ffn):
@@ -239,6 +248,28 @@ def cpu_baseline(seconds=10.0):
             "sample": f"{n} config-2 projections (M=8192, hidden 1024, r=32) in fp32, {el:.1f} s"}
 
 
+def measured_traffic():
+    """HBM bytes per prefill launch at config 2, as recorded from the rocprofv3
+    FETCH_SIZE + WRITE_SIZE passes (line `traffic_bytes_per_launch: N`), else None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def copy_calibration(dev):
+    """A plain copy of COPY_BYTES bytes, three times: reads and writes COPY_BYTES each."""
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,6 +277,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5"), default=None)
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -258,6 +291,14 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.synchronize()
+    if args.copy_calibration:
+        copy_calibration(dev)
+    if args.only is not None and args.only != "c2":
+        fn = {"c3": lambda: bench_c3(dev, args.steps, args.warmup),
+              "c4": lambda: bench_c4(dev),
+              "c5": lambda: bench_c5(dev, args.steps, args.warmup)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
+        return
     flops, ms = bench_c2(dev, args.steps, args.warmup)
     tflops = flops / ms / 1e9
     launches = 7 * 28
@@ -278,12 +319,12 @@ def main():
                                "one shared base W set, per-layer rank-32 LoRA, scale 2",
                    "M": 8192, "hidden": 1024, "rank": 32, "layers": 28, "projections": 7},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": measured_traffic(),
                      "kernel": "prefill_kernel (196 launches per step, one per projection)",
                      "avg_launch_us": round(ms * 1e3 / launches, 3)},
     }
     extra = {}
-    if not args.no_extra:
+    if not args.no_extra and args.only is None:
         ms17 = bench_c2_1p7b(dev, args.steps, args.warmup)
         f17 = 4 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_1P7B)
         extra["c2_qwen3_1.7b_prefill"] = {"TFLOP/s": round(f17 / ms17 / 1e9, 1),
@@ -293,7 +334,7 @@ def main():
         extra["c5_qwen3_8b_fp8_base"] = bench_c5(dev, args.steps, args.warmup)
         extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)
         res["extra"] = extra
-    if not args.no_cpu:
+    if not args.no_cpu and args.only is None:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
 

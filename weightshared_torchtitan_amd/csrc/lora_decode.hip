@@ -142,11 +142,10 @@ __device__ __forceinline__ void load_t(const DecodeArgs& p, float* tl, int nthre
   }
 }
 
-// y[m][row] = bf16(w_scale[row] * v + T[m] . B[row]).
-__device__ __forceinline__ void finish_one(const DecodeArgs& p, const float* tl, int m, int row, float v) {
+// y[m][row] = bf16(w_scale[row] * v + T[m] . B[row]); tr is the row T[m] (fp32 values).
+__device__ __forceinline__ void finish_one(const DecodeArgs& p, const float* tr, int m, int row, float v) {
   float out = (p.w_scale != nullptr) ? v * p.w_scale[row] : v;
   if (p.r > 0) {
-    const float* tr = tl + m * p.r;
     const uint16_t* br = p.b + (int64_t)row * p.ldb;
     for (int j0 = 0; j0 < p.r; j0 += 8) {
       const u32x4_t bv = ld_global_16(br + j0);
@@ -235,26 +234,28 @@ stream_kernel(DecodeArgs p) {
     const int m = q / nrow, rl = q % nrow;
     const float v = sums[rl * MC + m];
     if constexpr (ROLE == kRoleY) {
-      finish_one(p, tl, m, row0 + rl, v);
+      finish_one(p, tl + m * p.r, m, row0 + rl, v);
     } else {
       p.part[((int64_t)ks * p.M + m) * p.rows + row0 + rl] = v;
     }
   }
 }
 
-// K2: y = bf16(w_scale * sum_s P[s] + T . B^T) over RT rows per workgroup.
+// K2: y = bf16(w_scale * sum_s P[s] + T . B^T); one thread per (m, n), blockIdx.y = m.
 __global__ void __launch_bounds__(RT) reduce_kernel(DecodeArgs p, int splits) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  float* tl = reinterpret_cast<float*>(smem);
-  load_t(p, tl, RT);
+  __shared__ float tl[256];  // T[m][0..r), r <= 256
+  const int m = blockIdx.y;
+  for (int j = threadIdx.x; j < p.r; j += RT) {
+    float v = 0.f;
+    for (int sp = 0; sp < p.tsplits; ++sp) v += p.tpart[((int64_t)sp * p.M + m) * p.r + j];
+    tl[j] = bf16_bits_to_f32(f32_to_bf16_bits(p.s * v));
+  }
   __syncthreads();
   const int n = blockIdx.x * RT + threadIdx.x;
   if (n >= p.rows) return;
-  for (int m = 0; m < p.M; ++m) {
-    float v = 0.f;
-    for (int sp = 0; sp < splits; ++sp) v += p.part[((int64_t)sp * p.M + m) * p.rows + n];
-    finish_one(p, tl, m, n, v);
-  }
+  float v = 0.f;
+  for (int sp = 0; sp < splits; ++sp) v += p.part[((int64_t)sp * p.M + m) * p.rows + n];
+  finish_one(p, tl, m, n, v);
 }
 
 struct Split {
@@ -407,7 +408,7 @@ hipError_t launch_decode(const LoraArgs& p) {
   hipError_t e = fp8 ? dispatch<kFP8, kRolePartial>(y, pl.mb, pl.nr, pl.y.groups, pl.y.splits, 0, p.stream)
                      : dispatch<kBF16, kRolePartial>(y, pl.mb, pl.nr, pl.y.groups, pl.y.splits, 0, p.stream);
   if (e != hipSuccess) return e;
-  reduce_kernel<<<dim3((unsigned)((p.N + RT - 1) / RT)), dim3(RT), (size_t)p.M * p.r * 4, p.stream>>>(y, pl.y.splits);
+  reduce_kernel<<<dim3((unsigned)((p.N + RT - 1) / RT), (unsigned)p.M), dim3(RT), 0, p.stream>>>(y, pl.y.splits);
   return hipGetLastError();
 }
 
