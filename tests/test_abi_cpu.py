@@ -1,0 +1,175 @@
+"""The C ABI without a GPU: libwsl.so loads, exports every symbol include/wsl_lora.h
+declares, and rejects bad arguments with the documented WSL_E_* codes before it touches
+a device. No call here launches a kernel; pointers passed are never dereferenced on the
+host (validation fails first)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from weightshared_torchtitan_amd import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wsl_lora.h")
+
+needs_lib = pytest.mark.skipif(not os.path.exists(N.LIB_PATH),
+                               reason="libwsl.so not built (run __graft_entry__.build())")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wsl_[a-z0-9_]+)\s*\(", text)))
+
+
+def _header_defines():
+    out = {}
+    for name, val in re.findall(r"#define\s+(WSL_[A-Z0-9_]+)\s+\(?(-?\d+)\)?", open(HEADER).read()):
+        out[name] = int(val)
+    return out
+
+
+def test_binding_lists_every_header_function():
+    assert sorted(N.EXPORTED) == _header_functions()
+
+
+def test_python_constants_match_header():
+    d = _header_defines()
+    for name in ("WSL_OK", "WSL_E_INVALID_ARG", "WSL_E_SHAPE", "WSL_E_DTYPE", "WSL_E_ALIGN",
+                 "WSL_E_WORKSPACE", "WSL_E_DEVICE", "WSL_E_LAUNCH", "WSL_DTYPE_BF16",
+                 "WSL_DTYPE_FP8_E4M3", "WSL_MAX_RANK"):
+        assert getattr(N, name) == d[name], name
+
+
+@needs_lib
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(N.LIB_PATH)
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+
+
+@needs_lib
+def test_version_and_empty_error():
+    lib = N.lib()
+    assert lib.wsl_version() == 100
+    sz = ctypes.c_size_t()
+    assert lib.wsl_lora_linear_workspace_bytes(16, 64, 64, 8, 0, ctypes.byref(sz)) == N.WSL_OK
+    assert N.last_error() == ""
+
+
+@needs_lib
+@pytest.mark.parametrize("M,Nn,K,r,dt,code", [
+    (-1, 64, 64, 8, 0, N.WSL_E_SHAPE),
+    (4, 0, 64, 8, 0, N.WSL_E_SHAPE),
+    (4, 64, 0, 8, 0, N.WSL_E_SHAPE),
+    (4, 64, 64, -1, 0, N.WSL_E_SHAPE),
+    (4, 64, 64, 257, 0, N.WSL_E_SHAPE),
+    (4, 64, 64, 8, 7, N.WSL_E_DTYPE),
+])
+def test_workspace_query_rejects_bad_sizes(M, Nn, K, r, dt, code):
+    sz = ctypes.c_size_t()
+    assert N.lib().wsl_lora_linear_workspace_bytes(M, Nn, K, r, dt, ctypes.byref(sz)) == code
+    assert N.last_error() != ""
+
+
+@needs_lib
+def test_workspace_query_null_out_pointer():
+    assert N.lib().wsl_lora_linear_workspace_bytes(4, 64, 64, 8, 0, None) == N.WSL_E_INVALID_ARG
+
+
+@needs_lib
+@pytest.mark.parametrize("M", [1, 8, 64, 65, 8192])
+def test_workspace_includes_counter_prefix(M):
+    # Every path's scratch sits after the WSL_COUNTER_BYTES prefix.
+    b = N.workspace_bytes(M, 2048, 2048, 64, N.WSL_DTYPE_BF16)
+    assert b >= _header_defines()["WSL_COUNTER_BYTES"]
+    # r > 64 on the prefill path materialises T [M, r] bf16
+    big = N.workspace_bytes(M, 2048, 2048, 128, N.WSL_DTYPE_BF16)
+    assert big >= b
+
+
+P = 0x100000  # a 256-aligned fake device address; never dereferenced
+
+
+def _fwd(**kw):
+    a = dict(x=P, ldx=64, w=P, ldw=64, w_dtype=0, w_scale=None, a=P, lda=64, b=P, ldb=8,
+             scale=2.0, y=P, ldy=64, M=4, N=64, K=64, r=8, ws=P, ws_bytes=1 << 24, stream=None)
+    a.update(kw)
+    return N.lib().wsl_lora_linear_fwd(a["x"], a["ldx"], a["w"], a["ldw"], a["w_dtype"], a["w_scale"],
+                                       a["a"], a["lda"], a["b"], a["ldb"], a["scale"], a["y"], a["ldy"],
+                                       a["M"], a["N"], a["K"], a["r"], a["ws"], a["ws_bytes"], a["stream"])
+
+
+@needs_lib
+@pytest.mark.parametrize("kw,code", [
+    (dict(x=None), N.WSL_E_INVALID_ARG),
+    (dict(y=None), N.WSL_E_INVALID_ARG),
+    (dict(w=None, r=0), N.WSL_E_INVALID_ARG),
+    (dict(a=None), N.WSL_E_INVALID_ARG),
+    (dict(w_dtype=1), N.WSL_E_INVALID_ARG),          # fp8 without w_scale
+    (dict(w_scale=P), N.WSL_E_INVALID_ARG),          # w_scale with bf16 w
+    (dict(ldx=63), N.WSL_E_SHAPE),
+    (dict(ldw=63), N.WSL_E_SHAPE),
+    (dict(lda=63), N.WSL_E_SHAPE),
+    (dict(ldb=7), N.WSL_E_SHAPE),
+    (dict(ldy=63), N.WSL_E_SHAPE),
+    (dict(r=300), N.WSL_E_SHAPE),
+    (dict(w_dtype=5), N.WSL_E_DTYPE),
+    (dict(x=P + 1), N.WSL_E_ALIGN),
+    (dict(y=P + 1), N.WSL_E_ALIGN),
+    (dict(ws=None), N.WSL_E_WORKSPACE),
+    (dict(ws_bytes=16), N.WSL_E_WORKSPACE),
+    (dict(ws=P + 128), N.WSL_E_ALIGN),
+])
+def test_fwd_validation_codes(kw, code):
+    assert _fwd(**kw) == code
+    assert N.last_error() != ""
+
+
+@needs_lib
+def test_fwd_empty_batch_is_a_no_op():
+    assert _fwd(M=0, x=None, y=None, ws=None, ws_bytes=0) == N.WSL_OK
+
+
+@needs_lib
+def test_embedding_validation_codes():
+    lib = N.lib()
+    ok = dict(ids=P, n=4, emb=P, lde=16, V=100, k=16, proj=P, ldp=16, H=32, out=P, ldo=32)
+
+    def call(**kw):
+        a = dict(ok)
+        a.update(kw)
+        return lib.wsl_factorized_embedding_fwd(a["ids"], a["n"], a["emb"], a["lde"], a["V"], a["k"],
+                                                a["proj"], a["ldp"], a["H"], a["out"], a["ldo"], None)
+
+    assert call(n=-1) == N.WSL_E_SHAPE
+    assert call(k=2048) == N.WSL_E_SHAPE
+    assert call(lde=8) == N.WSL_E_SHAPE
+    assert call(ids=None) == N.WSL_E_INVALID_ARG
+    assert call(ids=P + 4) == N.WSL_E_ALIGN
+    assert call(n=0, ids=None) == N.WSL_OK
+
+
+def test_python_maps_codes_to_exceptions():
+    with pytest.raises(ValueError):
+        N.check(N.WSL_E_SHAPE, "x")
+    with pytest.raises(TypeError):
+        N.check(N.WSL_E_DTYPE, "x")
+    with pytest.raises(N.WSLError):
+        N.check(N.WSL_E_LAUNCH, "x")
+    N.check(N.WSL_OK, "x")
+
+
+def test_ops_refuse_cpu_tensors():
+    # No CPU fallback: the product path raises on host tensors.
+    import torch
+
+    from weightshared_torchtitan_amd import ops
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    w = torch.zeros(32, 64, dtype=torch.bfloat16)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        ops.lora_linear(x, w)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        ops.factorized_embedding(torch.zeros(3, dtype=torch.int64), torch.zeros(10, 8, dtype=torch.bfloat16),
+                                 torch.zeros(16, 8, dtype=torch.bfloat16))

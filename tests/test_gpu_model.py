@@ -1,0 +1,79 @@
+"""The weight-shared Qwen3 model on the GPU against the CPU oracle (oracle/qwen3_ref.py)
+on a small configuration whose shapes reach the prefill, decode and embedding kernels.
+
+Whole-model bf16 logits are compared with the fp32 oracle by max|d| / max|ref|. Greedy
+tokens are checked step by step against the oracle's no-cache forward of the same prefix
+(scripts/generate/_generation.py:43 re-runs the prefix): the model's token must be one
+whose oracle logit is within the bf16 tolerance of the oracle's maximum, so near-ties do
+not make the test flaky and a wrong cache or position fails it."""
+import pytest
+import torch
+
+from oracle import qwen3_ref as Q
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 3e-2  # whole-model bf16 vs fp32, max|d| / max|ref|
+
+
+def small_args():
+    from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3Args
+    return SharedQwen3Args(dim=256, n_layers=4, n_unique_blocks=2, n_heads=4, n_kv_heads=2, head_dim=64,
+                           hidden_dim=512, vocab_size=1000, embed_rank=64, lora_rank=16, max_seq_len=128)
+
+
+def build(gpu, seed=0):
+    from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3
+    a = small_args()
+    m = SharedQwen3(a)
+    m.init_random(seed=seed, std=0.05)
+    m = m.to(gpu).to(torch.bfloat16)
+    p = {k: v.detach().float().cpu() for k, v in m.named_parameters()}
+    return a, m, p
+
+
+def rel(x, ref):
+    return ((x.float().cpu() - ref).abs().max() / ref.abs().max()).item()
+
+
+@pytest.mark.parametrize("seq", [12, 40])  # M = 24 (decode kernels) and 80 (prefill kernels)
+def test_forward_logits_match_oracle(gpu, seq):
+    a, m, p = build(gpu, seed=1)
+    g = torch.Generator().manual_seed(seq)
+    toks = torch.randint(0, a.vocab_size, (2, seq), generator=g)
+    with torch.no_grad():
+        got = m(toks.to(gpu))
+    ref = Q.reference_forward(p, a, toks)
+    assert rel(got, ref) <= LOGIT_TOL
+
+
+def test_cached_decode_matches_no_cache_greedy(gpu):
+    a, m, p = build(gpu, seed=2)
+    g = torch.Generator().manual_seed(5)
+    prompt = torch.randint(0, a.vocab_size, (2, 9), generator=g)
+    n_new = 6
+    with torch.no_grad():
+        new, _ = m.generate(prompt.to(gpu), n_new, use_graph=True)
+    new = new.cpu()
+    toks = prompt
+    for i in range(n_new):
+        ref = Q.reference_forward(p, a, toks)[:, -1]  # [b, vocab]
+        tol = LOGIT_TOL * ref.abs().max(dim=-1).values
+        chosen = ref.gather(1, new[:, i:i + 1])[:, 0]
+        assert bool((chosen >= ref.max(dim=-1).values - tol).all()), f"step {i}"
+        toks = torch.cat([toks, new[:, i:i + 1]], 1)
+
+
+def test_decode_step_logits_match_oracle(gpu):
+    # One cached step (graph-free) against the oracle's full-prefix forward.
+    from weightshared_torchtitan_amd.qwen3_shared import KVCache
+    a, m, p = build(gpu, seed=3)
+    g = torch.Generator().manual_seed(6)
+    toks = torch.randint(0, a.vocab_size, (2, 11), generator=g)
+    cache = KVCache(a, 2, 16, gpu)
+    with torch.no_grad():
+        m(toks[:, :10].to(gpu), cache)
+        pos = torch.full((), 10, dtype=torch.int64, device=gpu)
+        got = m.decode_step(toks[:, 10:11].to(gpu), pos, cache)
+    ref = Q.reference_forward(p, a, toks)[:, -1]
+    assert rel(got, ref) <= LOGIT_TOL
