@@ -83,6 +83,9 @@ DECODE_CASES = [
     (8, 4096, 256, 0, 2.0, True),        # r = 0, direct-write path
     (5, 640, 1024, 32, 2.0, False),      # delta only
     (16, 1024, 1024, 256, 2.0, True),    # max rank
+    (33, 1000, 2048, 24, 2.0, True),     # 32-row groups with an N tail, partial rank group
+    (64, 1000, 6144, 24, 2.0, True),     # six-way K split with tails
+    (1, 2048, 6144, 128, 1.0, True),     # one token, long K, rank 128
 ]
 
 
@@ -248,25 +251,44 @@ def test_factorized_embedding_benchmark_shape(gpu, n_tok):
 
 
 # ------------------------------------------------------------------ decode workspace contract
-def test_decode_counters_return_to_zero_and_deterministic(gpu):
-    """The split-K decode path leaves its arrival counters zero and sums slices in a fixed
-    order: repeated calls are bitwise identical."""
-    import weightshared_torchtitan_amd as wsl
+def _check_counters(gpu, calls_before, calls_after):
+    """Arrival counters (words 16..) are back to zero; the 64-bit launch counter advanced
+    by exactly 2^20 per decode launch."""
     from weightshared_torchtitan_amd import ops
+    ws = ops.workspace(gpu, torch.cuda.current_stream(gpu).cuda_stream, 0)
+    assert int(ws[64:65536].count_nonzero()) == 0, "arrival counters not restored to zero"
+    launch = int(ws[:8].cpu().numpy().view(np.uint64)[0])
+    if calls_before is not None:
+        assert launch - calls_before == (calls_after << 20)
+    return launch
+
+
+def test_decode_counters_return_to_zero_and_deterministic(gpu):
+    """The split-K decode path leaves its arrival counters zero, advances the launch
+    counter by one unit per launch and sums slices in a fixed order: repeated calls are
+    bitwise identical."""
+    import weightshared_torchtitan_amd as wsl
     _say("[decode counters] M=8 N=2048 K=6144 r=64")
     x, W, A, B = (t.to(gpu) for t in _inputs(8, 2048, 6144, 64, seed=17))
+    wsl.lora_linear(x, W, A, B, 2.0)
+    torch.cuda.synchronize()
+    before = _check_counters(gpu, None, 0)
     ys = [wsl.lora_linear(x, W, A, B, 2.0) for _ in range(3)]
     torch.cuda.synchronize()
     assert all(torch.equal(ys[0], v) for v in ys[1:])
-    ws = ops.workspace(gpu, torch.cuda.current_stream(gpu).cuda_stream, 0)
-    assert int(ws[:65536].count_nonzero()) == 0, "arrival counters not restored to zero"
+    _check_counters(gpu, before, 3)
+    x2, W2, A2, B2 = (t.to(gpu) for t in _inputs(64, 1000, 6144, 24, seed=18))
+    wsl.lora_linear(x2, W2, A2, B2, 2.0)
+    torch.cuda.synchronize()
+    _check_counters(gpu, before, 4)
 
 
-def test_decode_in_graph_replays_match_eager(gpu):
+@pytest.mark.parametrize("M,N,K,r", [(4, 1024, 2048, 32), (64, 2048, 6144, 64)])
+def test_decode_in_graph_replays_match_eager(gpu, M, N, K, r):
     """Captured decode calls replay correctly several times (counters reset per replay)."""
     import weightshared_torchtitan_amd as wsl
-    _say("[decode graph] M=4 N=1024 K=2048 r=32, 3 replays")
-    x, W, A, B = (t.to(gpu) for t in _inputs(4, 1024, 2048, 32, seed=23))
+    _say(f"[decode graph] M={M} N={N} K={K} r={r}, 3 replays")
+    x, W, A, B = (t.to(gpu) for t in _inputs(M, N, K, r, seed=23))
     eager = wsl.lora_linear(x, W, A, B, 2.0)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -282,3 +304,24 @@ def test_decode_in_graph_replays_match_eager(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
         wsl.lora_linear(x, W, A, B, 2.0)  # eager work on the default stream between replays
+
+
+@pytest.mark.parametrize("M,N,K,r", [(1, 2048, 2048, 64), (40, 1000, 6144, 24)])
+def test_decode_t_wait_fallback(gpu, M, N, K, r, monkeypatch):
+    """With the T wait bound forced to zero from the host, every W workgroup computes T
+    itself: the result stays within tolerance and the counters still return to zero."""
+    import weightshared_torchtitan_amd as wsl
+    _say(f"[decode T fallback] M={M} N={N} K={K} r={r}")
+    x, W, A, B = _inputs(M, N, K, r, seed=29)
+    xg, Wg, Ag, Bg = (t.to(gpu) for t in (x, W, A, B))
+    normal = wsl.lora_linear(xg, Wg, Ag, Bg, 2.0).float()
+    monkeypatch.setenv("WSL_DECODE_SPIN_LIMIT", "0")
+    forced = wsl.lora_linear(xg, Wg, Ag, Bg, 2.0).float()
+    torch.cuda.synchronize()
+    monkeypatch.delenv("WSL_DECODE_SPIN_LIMIT")
+    ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), 2.0)
+    assert O.max_rel_err(forced.cpu().numpy(), ref) <= BF16_TOL
+    assert ((forced - normal).abs().max() / normal.abs().max()).item() < 1e-2
+    _check_counters(gpu, None, 0)
+    again = wsl.lora_linear(xg, Wg, Ag, Bg, 2.0).float()  # the normal path still works after it
+    assert torch.equal(again, normal)

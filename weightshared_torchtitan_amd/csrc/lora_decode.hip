@@ -1,36 +1,67 @@
 // Decode-shaped (M <= 64 tokens) fused LoRA linear for gfx950.
 //
-// At small M a projection is a stream over W (N*K elements); the MFMA units are nearly
-// idle and the design goal is HBM bandwidth. Launches:
+// At small M a projection is a stream over W (N*K elements): the MFMA units are nearly
+// idle and the goal is HBM bandwidth, i.e. bytes in flight from the first cycle and as
+// few dependent memory round trips and launches as possible. One launch does all of it:
 //
-//  K0  P_T[s][m][j] = x[m] . A[j] over K slice s           (the r rows of A)
-//  K1  y[m][n] = bf16(w_scale[n] * x[m] . W[n] + T[m] . B[n])  (the N rows of W)
-//      with T[m][j] = bf16(s * sum_s P_T[s][m][j])
-//  K2  only when K1 splits K: sums K1's fp32 partials and finishes the rows as above.
+//   T workgroups  (blockIdx.x < nT, dispatched first): 16 rows of A each over one K
+//                 slice -> T[m][j] = bf16(s * x[m] . A[j]), published to the workspace.
+//   W workgroups  (the rest): 16*NR rows of W over one K slice -> base sums, then
+//                 y[m][n] = bf16(w_scale[n] * base + T[m] . B[n]).
 //
-// K0 and K1 are one row-group kernel: a workgroup (8 waves) owns 16*NR rows and one K
-// slice; each lane streams 64 contiguous bytes of a row per step (16 rows x 4 lane
-// groups per wave, waves interleaved over K), the slice of x is staged in LDS (only
-// the M real rows, plus one zero row that stands in for the MFMA padding), and
-// v_mfma_f32_16x16x32_bf16 forms the dot products. Wave partial sums are reduced
-// through LDS. K is split only as far as the x slice must fit the 160 KB LDS; the
-// partial sums of a split then go through K2 instead of any cross-workgroup hand-off
-// (a device-scope fence on this part writes back and invalidates a whole XCD's L2).
+// A workgroup (8 waves) stages its slice of x into LDS with direct global->LDS loads
+// (no VGPRs, XOR-swizzled rows), and its B rows likewise, while the first PD K steps of
+// its W rows are already in flight into registers. Each lane streams 64 contiguous bytes
+// of a row per step (16 rows x 4 lane groups per wave, waves interleaved over K) and
+// v_mfma_f32_16x16x32_bf16 forms the dot products. Wave sums are reduced through LDS.
+// The up-projection T . B^T of the epilogue is r/32 more MFMAs per 16x16 output block.
+//
+// Cross-workgroup hand-offs (T to the W workgroups; the partial sums of a K split to
+// the last of its workgroups) go through the workspace with agent-scope atomic loads
+// and stores, which are coherent across the XCDs' L2s without the whole-L2 write-back
+// and invalidate that a device-scope fence costs on this part; where data precedes a
+// counter, an s_waitcnt vmcnt(0) orders it ahead of the increment.
+//
+// T needs no counter: each element is published as one 64-bit word (launch tag << 16 |
+// bf16 bits), so a reader knows an element is this launch's by its tag. The tag is the
+// launch ordinal + 1, read from a 64-bit launch counter in the workspace prefix: every
+// workgroup adds C / total at exit (workgroup 0 also adds C % total), so each launch
+// adds exactly C; a workgroup reads the counter when it starts, before its own
+// addition, so floor(count / C) is the ordinal of the running launch for every one of
+// its workgroups. The per-group counters of a K split are reset by their last arriver.
+// Every launch therefore leaves the prefix in a valid state without a final barrier.
+// A W workgroup waits for T with a bounded poll (T workgroups never wait on anything
+// and are dispatched first); past the bound it computes T itself, so the launch always
+// drains.
 //
 // fp8 base rows are decoded to bf16 in registers (v_cvt_pk_f32_fp8). Reference
 // arithmetic: the decode loop runs the same projections at small M
 // (scripts/generate/_generation.py:35-80 calling
 // torchtitan/models/llama3/model/model.py:189-192,392-398).
+#include <cstdlib>
+
 #include "wsl_common.h"
 
 namespace wsl {
 namespace {
 
-constexpr int DT = 512;                   // threads per streaming workgroup (8 waves)
+constexpr int DT = 512;                     // threads per workgroup (8 waves)
 constexpr int NWV = DT / 64;
-constexpr int64_t LDS_MAX = 160 * 1024;   // gfx950 LDS per workgroup
-constexpr int64_t XS_MAX = LDS_MAX - 16 * 1024;  // x slice budget (rest: reduction)
-constexpr int RT = 256;                   // threads of the reduce kernel
+constexpr int64_t LDS_MAX = 160 * 1024;     // gfx950 LDS per workgroup
+constexpr int64_t BL_MAX = 32 * 256 * 2;    // B rows of one group: 32 rows x r32 <= 256
+constexpr int64_t XS_MAX = LDS_MAX - BL_MAX - 1024;
+
+// Words of the workspace prefix: a 64-bit launch counter, then 32-bit arrival counters.
+constexpr int CNT_LAUNCH = 0;  // 64-bit, words 0-1
+constexpr int CNT_TG = 16;     // [16] arrivals per T group (K split)
+constexpr int CNT_YG = 64;     // [..] arrivals per W group (K split)
+constexpr int kCounterWords = (int)(kCounterBytes / 4);
+constexpr uint64_t kLaunchUnit = 1ull << 20;  // C: what one launch adds to the counter
+constexpr uint64_t kTagMask = (1ull << 48) - 1;
+
+constexpr int kDefaultSpin = 1 << 16;  // polls of the T counter before computing T locally
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Elements of K one lane covers per step (64 bytes of the row) and per wave step.
 template <int WDT> struct Geo {
@@ -38,167 +69,222 @@ template <int WDT> struct Geo {
   static constexpr int WAVE_K = 4 * LANE_K;  // 4 lane groups
 };
 
-// x slice staged in LDS: rows 0..M-1 of x, then one zero row (index M) read by the
-// MFMA lanes of padding columns; row stride kc*2 + 16 bytes (bank spread).
-__device__ __forceinline__ int xs_row(int m, int M) { return m < M ? m : M; }
-__device__ __forceinline__ int xs_off(int row, int k, int xs_stride) { return row * xs_stride + k * 2; }
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
 
-// One row group (NR blocks of 16 rows) of a [rows, K] bf16/fp8 matrix against x^T over
-// the local K range [0, kc) starting at global column kbeg.
-template <int WDT, int NR, int MB>
-__device__ __forceinline__ void row_group_dot(const void* __restrict__ wmat, int64_t ldw, int rows,
-                                              int row0, int kbeg, int kc, int M, const char* xs,
-                                              int xs_stride, f32x4_t (&acc)[NR][MB]) {
-  using G = Geo<WDT>;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int l16 = lane & 15;
-  const int grp = lane >> 4;
-  const int nsteps = kc / G::WAVE_K;
+// Workgroup barrier without the fence of __syncthreads() (which would also wait for
+// the W loads still in flight); the empty asm keeps LDS accesses on their side.
+__device__ __forceinline__ void plain_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
-  int64_t rowoff[NR];
-#pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    const int rr = row0 + i * 16 + l16;
-    rowoff[i] = (int64_t)(rr < rows ? rr : rows - 1) * ldw;
-  }
-  int xrow[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) xrow[mb] = xs_row(mb * 16 + l16, M);
+// x slice in LDS: rows 0..M-1, kc bf16 each, 16-byte chunk c of row m stored at chunk
+// c ^ (m & 15) (kc is a multiple of 128, so the XOR stays inside the row). The 16 lanes
+// that read one chunk index of 16 different rows hit 16 distinct bank groups.
+__device__ __forceinline__ int xs_off(int row, int k, int kc) {
+  return row * kc * 2 + (((k >> 3) ^ (row & 15)) << 4);
+}
 
-  for (int st = wave; st < nsteps; st += NWV) {
-    const int kl = st * G::WAVE_K + grp * G::LANE_K;  // local k of this lane's run
-    const int kg = kbeg + kl;
-    u32x4_t wv[NR][4];
-#pragma unroll
-    for (int i = 0; i < NR; ++i) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if constexpr (WDT == kBF16) {
-          wv[i][u] = ld_global_16(reinterpret_cast<const uint16_t*>(wmat) + rowoff[i] + kg + u * 8);
-        } else {
-          wv[i][u] = ld_global_16(reinterpret_cast<const uint8_t*>(wmat) + rowoff[i] + kg + u * 16);
-        }
-      }
+// Direct global->LDS fill of x[0..M)[kbeg .. kbeg+kc): the wave instruction j writes
+// LDS bytes [1024 j, 1024 j + 1024), lane i the 16 bytes at 1024 j + 16 i.
+__device__ __forceinline__ void fill_x(char* xs, const uint16_t* __restrict__ x, int64_t ldx,
+                                       int M, int kbeg, int kc, int wave, int lane) {
+  const int cpr = kc >> 3;  // chunks per row
+  const int total = M * cpr;
+  for (int j = wave; j * 64 < total; j += NWV) {
+    const int p = j * 64 + lane;
+    if (p < total) {
+      const int row = p / cpr;
+      const int c = (p - row * cpr) ^ (row & 15);
+      const void* src = x + (int64_t)row * ldx + kbeg + c * 8;
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(xs + j * 1024), 16, 0, 0);
     }
-    if constexpr (WDT == kBF16) {
+  }
+}
+
+// Direct fill of the B rows of a W group: bl[rl][0..r32) for rows row0 + rl (rows past N
+// repeat row N-1; chunks past r repeat chunk 0 of the row: finite values that meet the
+// zero padding of T).
+__device__ __forceinline__ void fill_b(char* bl, const uint16_t* __restrict__ b, int64_t ldb,
+                                       int rows, int row0, int nrows, int r, int r32,
+                                       int wave, int lane) {
+  const int cpr = r32 >> 3;
+  const int total = rows * cpr;
+  for (int j = wave; j * 64 < total; j += NWV) {
+    const int p = j * 64 + lane;
+    if (p < total) {
+      const int rl = p / cpr;
+      int c = p - rl * cpr;
+      if (c * 8 >= r) c = 0;
+      const int row = min(row0 + rl, nrows - 1);
+      const void* src = b + (int64_t)row * ldb + c * 8;
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(bl + j * 1024), 16, 0, 0);
+    }
+  }
+}
+
+template <int WDT, int NR>
+__device__ __forceinline__ void load_step(u32x4_t (&wv)[NR][4], const void* __restrict__ wmat,
+                                          const int64_t (&rowoff)[NR], int kg) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if constexpr (WDT == kBF16)
+        wv[i][u] = ld_global_16(reinterpret_cast<const uint16_t*>(wmat) + rowoff[i] + kg + u * 8);
+      else
+        wv[i][u] = ld_global_16(reinterpret_cast<const uint8_t*>(wmat) + rowoff[i] + kg + u * 16);
+    }
+}
+
+template <int WDT, int NR, int MB>
+__device__ __forceinline__ void mma_step(const u32x4_t (&wv)[NR][4], const char* xs, int kc,
+                                         const int (&xrow)[MB], int kl, f32x4_t (&acc)[NR][MB]) {
+  if constexpr (WDT == kBF16) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      bf16x8_t xf[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        xf[mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xs + xs_off(xrow[mb], kl + u * 8, kc)));
+#pragma unroll
+      for (int i = 0; i < NR; ++i)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[i][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[i][u]), xf[mb], acc[i][mb], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
         bf16x8_t xf[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
-          xf[mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xs + xs_off(xrow[mb], kl + u * 8, xs_stride)));
+          xf[mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xs + xs_off(xrow[mb], kl + u * 16 + h * 8, kc)));
 #pragma unroll
-        for (int i = 0; i < NR; ++i)
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-            acc[i][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[i][u]), xf[mb], acc[i][mb], 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          bf16x8_t xf[MB];
+        for (int i = 0; i < NR; ++i) {
+          const u32x4_t wb = fp8x8_to_bf16x8(wv[i][u][2 * h], wv[i][u][2 * h + 1]);
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb)
-            xf[mb] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xs + xs_off(xrow[mb], kl + u * 16 + h * 8, xs_stride)));
-#pragma unroll
-          for (int i = 0; i < NR; ++i) {
-            const u32x4_t wb = fp8x8_to_bf16x8(wv[i][u][2 * h], wv[i][u][2 * h + 1]);
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-              acc[i][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wb), xf[mb], acc[i][mb], 0, 0, 0);
-          }
+            acc[i][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wb), xf[mb], acc[i][mb], 0, 0, 0);
         }
       }
     }
   }
 }
 
-// Role of a streaming launch.
-enum Role : int { kRoleT = 0, kRoleY = 1, kRolePartial = 2 };
-
 struct DecodeArgs {
   const uint16_t* x; int64_t ldx;
-  const void* mat; int64_t ldm;    // A (role T) or W (roles Y, partial)
-  int rows;                        // r or N
-  int M, kc;
-  float* part;                     // role T / partial: [splits][M][rows] fp32 sums
-  // finishing (role Y and the reduce kernel):
-  const float* tpart; int tsplits; // K0's partials [tsplits][M][r]
-  float s;                         // LoRA scale
-  const float* w_scale;
-  const uint16_t* b; int64_t ldb; int r;
+  const void* w; int64_t ldw; const float* w_scale;
+  const uint16_t* a; int64_t lda;
+  const uint16_t* b; int64_t ldb;
   uint16_t* y; int64_t ldy;
+  float s;
+  int M, N, K, r, r32;
+  int gT, kst, kct;   // T groups (16 rows of A), K split and slice
+  int gY, ksy, kcy;   // W groups (16*NR rows of W), K split and slice
+  int flag_off;       // LDS byte offset of the broadcast word
+  unsigned* cnt;      // counter prefix of the workspace
+  uint64_t* tfin;     // T [M][r]: tag << 16 | bf16 bits
+  float* tpart;       // [gT][kst][M][16]
+  float* ypart;       // [gY][ksy][M][16*NR]
+  int spin;           // polls of the T counter before the local fallback
 };
 
-// T[m][j] = bf16(s * sum_s P_T[s][m][j]) into LDS (fp32 values), m < M, j < r.
-__device__ __forceinline__ void load_t(const DecodeArgs& p, float* tl, int nthreads) {
-  for (int q = threadIdx.x; q < p.M * p.r; q += nthreads) {
-    float v = 0.f;
-    for (int sp = 0; sp < p.tsplits; ++sp) v += p.tpart[(int64_t)sp * p.M * p.r + q];
-    tl[q] = bf16_bits_to_f32(f32_to_bf16_bits(p.s * v));
-  }
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
+  return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned add_agent(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// y[m][row] = bf16(w_scale[row] * v + T[m] . B[row]); tr is the row T[m] (fp32 values).
-__device__ __forceinline__ void finish_one(const DecodeArgs& p, const float* tr, int m, int row, float v) {
-  float out = (p.w_scale != nullptr) ? v * p.w_scale[row] : v;
-  if (p.r > 0) {
-    const uint16_t* br = p.b + (int64_t)row * p.ldb;
-    for (int j0 = 0; j0 < p.r; j0 += 8) {
-      const u32x4_t bv = ld_global_16(br + j0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        out += tr[j0 + 2 * q] * bf16_bits_to_f32(bv[q] & 0xffffu);
-        out += tr[j0 + 2 * q + 1] * bf16_bits_to_f32(bv[q] >> 16);
-      }
-    }
-  }
-  p.y[(int64_t)m * p.ldy + row] = f32_to_bf16_bits(out);
-}
-
-template <int WDT, int NR, int MB, int ROLE>
-__global__ void __launch_bounds__(DT)
-stream_kernel(DecodeArgs p) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  constexpr int ROWS = 16 * NR;
+// Sums over one K slice of a group of 16*NR rows of `mat` against x (whose fill into
+// smem this wave has issued just before), reduced over the waves into sums[row][m]
+// (LDS, fp32, stride 16*MB). The x slice's LDS is reused for the reduction.
+template <int WDT, int NR, int MB>
+__device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
+                                           int kbeg, int kc, int M, char* smem, float* sums) {
+  using G = Geo<WDT>;
+  constexpr int PD = NR == 1 ? 4 : 2;   // K steps in flight per wave
+  constexpr int LPS = NR * 4;           // loads per step
   constexpr int MC = 16 * MB;
   constexpr int PER_LANE = NR * MB * 4;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int g = blockIdx.x;
-  const int ks = blockIdx.y;
-  const int kbeg = ks * p.kc;
-  const int row0 = g * ROWS;
-  const int xs_stride = p.kc * 2 + 16;
-  char* xs = smem;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15;
+  const int grp = lane >> 4;
+  const int nsteps = kc / G::WAVE_K;
+  const int my = nsteps > wave ? (nsteps - wave + NWV - 1) / NWV : 0;
 
-  // Stage x[0..M)[kbeg .. kbeg+kc) and the zero row M.
-  const int chunks_per_row = p.kc / 8;
-  const int nchunks = (p.M + 1) * chunks_per_row;
-  for (int c = tid; c < nchunks; c += DT) {
-    const int m = c / chunks_per_row;
-    const int kk = (c % chunks_per_row) * 8;
-    const u32x4_t v = (m < p.M) ? ld_global_16(p.x + (int64_t)m * p.ldx + kbeg + kk) : zero_u32x4();
-    *reinterpret_cast<u32x4_t*>(xs + xs_off(m, kk, xs_stride)) = v;
-  }
-  __syncthreads();
+  int64_t rowoff[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) rowoff[i] = (int64_t)min(row0 + i * 16 + l16, nrows - 1) * ldm;
+  int xrow[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) xrow[mb] = min(mb * 16 + l16, M - 1);
+
+  u32x4_t wv[PD][NR][4];
+#pragma unroll
+  for (int q = 0; q < PD; ++q)
+    if (q < my) load_step<WDT, NR>(wv[q], mat, rowoff, kbeg + (wave + q * NWV) * G::WAVE_K + grp * G::LANE_K);
 
   f32x4_t acc[NR][MB];
 #pragma unroll
   for (int i = 0; i < NR; ++i)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[i][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  row_group_dot<WDT, NR, MB>(p.mat, p.ldm, p.rows, row0, kbeg, p.kc, p.M, xs, xs_stride, acc);
 
-  // Cross-wave reduction through LDS into sums[row][m] (fp32, ROWS x MC).
+  // The x / B fills were issued before the W loads: wait until only the W loads are
+  // outstanding, then for every wave's fills.
+  const int npf = my < PD ? my : PD;
+  if (npf == 0) wait_vm<0>();
+  else if (npf == 1) wait_vm<LPS>();
+  else if (npf == 2) wait_vm<2 * LPS>();
+  else if constexpr (PD == 4) {
+    if (npf == 3) wait_vm<3 * LPS>();
+    else wait_vm<4 * LPS>();
+  }
+  plain_barrier();
+
+  for (int i0 = 0; i0 < my; i0 += PD) {
+#pragma unroll
+    for (int q = 0; q < PD; ++q) {
+      const int i = i0 + q;
+      if (i < my) {
+        const int kl = (wave + i * NWV) * G::WAVE_K + grp * G::LANE_K;
+        mma_step<WDT, NR, MB>(wv[q], smem, kc, xrow, kl, acc);
+        if (i + PD < my)
+          load_step<WDT, NR>(wv[q], mat, rowoff, kbeg + (wave + (i + PD) * NWV) * G::WAVE_K + grp * G::LANE_K);
+      }
+    }
+  }
+
+  // Cross-wave reduction (the x slice is dead: its LDS is reused).
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
-  float* sums = red + (NWV - 1) * PER_LANE * 64;
-  float* tl = sums + ROWS * MC;  // T [M][r] (role Y)
   if (wave > 0) {
 #pragma unroll
     for (int i = 0; i < NR; ++i)
@@ -210,150 +296,290 @@ stream_kernel(DecodeArgs p) {
   }
   __syncthreads();
   if (wave == 0) {
-    const int l16 = lane & 15;
-    const int grp = lane >> 4;
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
+    for (int i = 0; i < NR; ++i)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         f32x4_t v = acc[i][mb];
-        for (int wv = 0; wv < NWV - 1; ++wv)
+        for (int w2 = 0; w2 < NWV - 1; ++w2)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += red[(wv * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane];
+          for (int e = 0; e < 4; ++e) v[e] += red[(w2 * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane];
         // D[row][m]: lane holds m = l16, rows grp*4 + e of block i
 #pragma unroll
         for (int e = 0; e < 4; ++e) sums[(i * 16 + grp * 4 + e) * MC + mb * 16 + l16] = v[e];
       }
-    }
   }
-  if constexpr (ROLE == kRoleY) load_t(p, tl, DT);
   __syncthreads();
-
-  const int nrow = min(ROWS, p.rows - row0);
-  for (int q = tid; q < nrow * p.M; q += DT) {
-    const int m = q / nrow, rl = q % nrow;
-    const float v = sums[rl * MC + m];
-    if constexpr (ROLE == kRoleY) {
-      finish_one(p, tl + m * p.r, m, row0 + rl, v);
-    } else {
-      p.part[((int64_t)ks * p.M + m) * p.rows + row0 + rl] = v;
-    }
-  }
 }
 
-// K2: y = bf16(w_scale * sum_s P[s] + T . B^T); one thread per (m, n), blockIdx.y = m.
-__global__ void __launch_bounds__(RT) reduce_kernel(DecodeArgs p, int splits) {
-  __shared__ float tl[256];  // T[m][0..r), r <= 256
-  const int m = blockIdx.y;
-  for (int j = threadIdx.x; j < p.r; j += RT) {
+// The K split of a group: publish this workgroup's partial sums; the last arriver sums
+// all partials in split order (so the result does not depend on arrival order) into
+// `sums` and returns true. With one split, returns true at once.
+template <int ROWS, int MC>
+__device__ __forceinline__ bool split_reduce(float* sums, float* part, unsigned* cnt, int ks, int ksplit,
+                                             int M, int* flag) {
+  if (ksplit == 1) return true;
+  const int tid = threadIdx.x;
+  const int n = M * ROWS;
+  for (int q = tid; q < n; q += DT) {
+    const int m = q / ROWS, rl = q % ROWS;
+    st_agent(part + (int64_t)ks * n + q, sums[rl * MC + m]);
+  }
+  wait_vm<0>();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned old = add_agent(cnt, 1u);
+    const bool last = old == (unsigned)(ksplit - 1);
+    if (last) st_agent(cnt, 0u);  // every other split has arrived: reset for the next launch
+    *flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (*flag == 0) return false;
+  for (int q = tid; q < n; q += DT) {
     float v = 0.f;
-    for (int sp = 0; sp < p.tsplits; ++sp) v += p.tpart[((int64_t)sp * p.M + m) * p.r + j];
-    tl[j] = bf16_bits_to_f32(f32_to_bf16_bits(p.s * v));
+    for (int s2 = 0; s2 < ksplit; ++s2) v += ld_agent(part + (int64_t)s2 * n + q);
+    const int m = q / ROWS, rl = q % ROWS;
+    sums[rl * MC + m] = v;
   }
   __syncthreads();
-  const int n = blockIdx.x * RT + threadIdx.x;
-  if (n >= p.rows) return;
-  float v = 0.f;
-  for (int sp = 0; sp < splits; ++sp) v += p.part[((int64_t)sp * p.M + m) * p.rows + n];
-  finish_one(p, tl, m, n, v);
+  return true;
 }
 
-struct Split {
-  int splits, kc, groups;
-};
+// T[m][j] (bf16) into LDS tl[m][0..r32) (row stride r32 + 8 elements), zero for m >= M
+// or j >= r. Polls (bounded) until every element carries this launch's tag; past the
+// bound computes T itself from x and A.
+template <int MC>
+__device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint64_t tag, int* flag) {
+  const int tid = threadIdx.x;
+  const int tls = p.r32 + 8;
+  for (int q = tid; q < MC * tls; q += DT) tl[q] = 0;
+  const int n = p.M * p.r;
+  bool ok = false;
+  for (int it = 0;; ++it) {
+    if (tid == 0) *flag = 0;
+    __syncthreads();
+    for (int q = tid; q < n; q += DT) {
+      const uint64_t v = ld_agent(p.tfin + q);
+      if ((v >> 16) != tag) *flag = 1;
+      const int m = q / p.r, j = q % p.r;
+      tl[m * tls + j] = (uint16_t)(v & 0xffffu);
+    }
+    __syncthreads();
+    ok = *flag == 0;
+    __syncthreads();  // every thread has read the flag before it is cleared again
+    if (ok || it >= p.spin) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (!ok) {
+    for (int q = tid; q < n; q += DT) {
+      const int m = q / p.r, j = q % p.r;
+      const uint16_t* xr = p.x + (int64_t)m * p.ldx;
+      const uint16_t* ar = p.a + (int64_t)j * p.lda;
+      float acc = 0.f;
+      for (int k = 0; k < p.K; k += 8) {
+        const u32x4_t xv = ld_global_16(xr + k), av = ld_global_16(ar + k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc += bf16_bits_to_f32(xv[e] & 0xffffu) * bf16_bits_to_f32(av[e] & 0xffffu);
+          acc += bf16_bits_to_f32(xv[e] >> 16) * bf16_bits_to_f32(av[e] >> 16);
+        }
+      }
+      tl[m * tls + j] = f32_to_bf16_bits(p.s * acc);
+    }
+  }
+  __syncthreads();
+}
+
+template <int WDT, int NR, int MB>
+__global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  constexpr int ROWS = 16 * NR;
+  constexpr int MC = 16 * MB;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nT = p.gT * p.kst;
+  const int bid = blockIdx.x;
+  int* flag = reinterpret_cast<int*>(smem + p.flag_off);
+  uint64_t* launch = reinterpret_cast<uint64_t*>(p.cnt + CNT_LAUNCH);
+  // This launch's tag (see the file comment); read before this workgroup's exit addition.
+  const uint64_t tag = (ld_agent(launch) / kLaunchUnit + 1) & kTagMask;
+
+  if (bid < nT) {
+    // ---------------- T workgroup: 16 rows of A over one K slice
+    const int g = bid / p.kst, ks = bid % p.kst;
+    const int kbeg = ks * p.kct;
+    constexpr int RED_T = (NWV - 1) * MB * 4 * 64 * 4;
+    float* sums = reinterpret_cast<float*>(smem + RED_T);
+    fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
+    slice_sums<kBF16, 1, MB>(p.a, p.lda, p.r, g * 16, kbeg, p.kct, p.M, smem, sums);
+    if (split_reduce<16, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * 16, p.cnt + CNT_TG + g, ks,
+                             p.kst, p.M, flag)) {
+      for (int q = tid; q < p.M * 16; q += DT) {
+        const int m = q >> 4, rl = q & 15, j = g * 16 + rl;
+        if (j < p.r) st_agent(p.tfin + m * p.r + j, (tag << 16) | f32_to_bf16_bits(p.s * sums[rl * MC + m]));
+      }
+    }
+  } else {
+    // ---------------- W workgroup: 16*NR rows of W over one K slice
+    const int yb = bid - nT;
+    const int g = yb / p.ksy, ks = yb % p.ksy;
+    const int kbeg = ks * p.kcy;
+    const int row0 = g * ROWS;
+    constexpr int RED = (NWV - 1) * NR * MB * 4 * 64 * 4;
+    const int xs_bytes = p.M * p.kcy * 2;
+    const int post = RED + ROWS * MC * 4 + MC * (p.r32 + 8) * 2;
+    char* bl = smem + (xs_bytes > post ? xs_bytes : post);
+    float* sums = reinterpret_cast<float*>(smem + RED);
+    uint16_t* tl = reinterpret_cast<uint16_t*>(smem + RED + ROWS * MC * 4);
+    fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kcy, wave, lane);
+    if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
+    slice_sums<WDT, NR, MB>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
+    if (split_reduce<ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, p.cnt + CNT_YG + g, ks,
+                               p.ksy, p.M, flag)) {
+      if (p.r > 0) gather_t<MC>(p, tl, tag, flag);
+      // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
+      const int l16 = lane & 15, grp = lane >> 4;
+      const int tls = p.r32 + 8;
+      for (int blk = wave; blk < NR * MB; blk += NWV) {
+        const int i = blk / MB, mb = blk % MB;
+        f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+        for (int j0 = 0; j0 < p.r; j0 += 32) {
+          const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(bl + ((i * 16 + l16) * p.r32 + j0 + grp * 8) * 2);
+          const u32x4_t tv = *reinterpret_cast<const u32x4_t*>(tl + (mb * 16 + l16) * tls + j0 + grp * 8);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(bv), as_bf16x8(tv), d, 0, 0, 0);
+        }
+        // d: lane holds token m = mb*16 + l16, rows i*16 + grp*4 + e
+        const int m = mb * 16 + l16;
+        const int n0 = row0 + i * 16 + grp * 4;
+        if (m < p.M) {
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int n = n0 + e;
+            float v = sums[(i * 16 + grp * 4 + e) * MC + m];
+            if (p.w_scale != nullptr && n < p.N) v *= p.w_scale[n];
+            o[e] = v + d[e];
+          }
+          uint16_t* yr = p.y + (int64_t)m * p.ldy;
+          if (n0 + 3 < p.N) {
+            uint2 pk;
+            pk.x = pack_bf16x2(o[0], o[1]);
+            pk.y = pack_bf16x2(o[2], o[3]);
+            *reinterpret_cast<uint2*>(yr + n0) = pk;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n0 + e < p.N) yr[n0 + e] = f32_to_bf16_bits(o[e]);
+          }
+        }
+      }
+    }
+  }
+
+  // Exit: this workgroup's share of the launch's C (the tag was consumed above).
+  if (tid == 0) {
+    const uint64_t total = (uint64_t)(nT + p.gY * p.ksy);
+    const uint64_t share = kLaunchUnit / total + (bid == 0 ? kLaunchUnit % total : 0);
+    __hip_atomic_fetch_add(launch, share, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 
 int wave_k_of(int wdt) { return wdt == kFP8 ? 256 : 128; }
 
-int64_t xs_bytes(int64_t M, int64_t kc) { return (M + 1) * (kc * 2 + 16); }
-
-// The smallest K split whose x slice fits the LDS budget (each slice a whole number of
-// wave steps).
-Split plan_split(int64_t rows, int64_t K, int64_t M, int nr, int wdt) {
-  Split sp;
-  sp.groups = (int)((rows + 16 * nr - 1) / (16 * nr));
-  const int wk = wave_k_of(wdt);
-  int64_t s = 1;
-  while (xs_bytes(M, K / s) > XS_MAX && K % (s * 2 * wk) == 0) s *= 2;
-  sp.splits = (int)s;
-  sp.kc = (int)(K / s);
-  return sp;
+// Smallest K split whose x slice (M rows) fits the LDS budget, each slice a whole number
+// of wave steps; 0 if none.
+int fit_split(int64_t M, int64_t K, int wave_k) {
+  for (int64_t s = 1; s * wave_k <= K; ++s) {
+    if (K % s != 0 || (K / s) % wave_k != 0) continue;
+    if (M * (K / s) * 2 <= XS_MAX) return (int)s;
+  }
+  return 0;
 }
 
 struct DecodePlan {
-  int mb, nr;
-  Split t, y;
-  size_t off_pt, off_py, total;
+  int mb, nr, rows, r32;
+  int gT, kst, kct;
+  int gY, ksy, kcy;
+  size_t off_t, off_pt, off_py, total;
+  size_t flag_off, smem;
+  bool ok;
 };
 
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
-  DecodePlan pl;
+  DecodePlan pl{};
   pl.mb = (int)((M + 15) / 16);
   if (pl.mb < 1) pl.mb = 1;
   pl.nr = pl.mb >= 3 ? 2 : 1;
-  pl.y = plan_split(N, K, M, pl.nr, wdt);
-  if (r > 0) pl.t = plan_split(r, K, M, 1, kBF16);
-  else pl.t = Split{1, (int)K, 0};
-  size_t off = kCounterBytes;  // the decode path keeps no counters; the prefix is reserved
+  pl.rows = 16 * pl.nr;
+  pl.r32 = (int)((r + 31) / 32 * 32);
+  pl.ksy = fit_split(M, K, wave_k_of(wdt));
+  pl.kcy = pl.ksy > 0 ? (int)(K / pl.ksy) : 0;
+  pl.gY = (int)((N + pl.rows - 1) / pl.rows);
+  if (r > 0) {
+    pl.gT = (int)((r + 15) / 16);
+    pl.kst = fit_split(M, K, wave_k_of(kBF16));
+    pl.kct = pl.kst > 0 ? (int)(K / pl.kst) : 0;
+  } else {
+    pl.gT = 0;
+    pl.kst = 1;
+    pl.kct = (int)K;
+  }
+  pl.ok = pl.ksy > 0 && pl.kst > 0 && CNT_YG + pl.gY <= kCounterWords &&
+          (uint64_t)pl.gT * pl.kst + (uint64_t)pl.gY * pl.ksy < kLaunchUnit;
+  size_t off = kCounterBytes;
+  pl.off_t = off;
+  off += (size_t)M * r * 8;
+  off = (off + 255) & ~(size_t)255;
   pl.off_pt = off;
-  off += (size_t)pl.t.splits * M * r * 4;
+  if (pl.kst > 1) off += (size_t)pl.gT * pl.kst * M * 16 * 4;
   off = (off + 255) & ~(size_t)255;
   pl.off_py = off;
-  if (pl.y.splits > 1) off += (size_t)pl.y.splits * M * N * 4;
+  if (pl.ksy > 1) off += (size_t)pl.gY * pl.ksy * M * pl.rows * 4;
   pl.total = off;
+  // LDS: max(x slice, reduction + sums + T) + B rows, then the broadcast word.
+  const size_t xs = (size_t)M * (pl.kcy > pl.kct ? pl.kcy : pl.kct) * 2;
+  const size_t red = (size_t)(NWV - 1) * pl.nr * pl.mb * 4 * 64 * 4;
+  const size_t post = red + (size_t)pl.rows * 16 * pl.mb * 4 + (size_t)16 * pl.mb * (pl.r32 + 8) * 2;
+  pl.flag_off = (xs > post ? xs : post) + (size_t)pl.rows * pl.r32 * 2;
+  pl.smem = pl.flag_off + 16;
+  if (pl.smem > (size_t)LDS_MAX) pl.ok = false;
   return pl;
 }
 
-size_t stream_smem(int64_t M, int kc, int nr, int mb, int r) {
-  const size_t xs = (size_t)xs_bytes(M, kc);
-  const size_t red = (size_t)((NWV - 1) * nr * mb * 4 * 64 + 16 * nr * 16 * mb + M * r) * 4;
-  return xs > red ? xs : red;
-}
-
-bool plan_ok(const DecodePlan& pl, int64_t M, int64_t r) {
-  if (xs_bytes(M, pl.y.kc) > XS_MAX) return false;
-  if (pl.t.groups > 0 && xs_bytes(M, pl.t.kc) > XS_MAX) return false;
-  return stream_smem(M, pl.y.kc, pl.nr, pl.mb, (int)r) <= (size_t)LDS_MAX &&
-         (size_t)M * r * 4 <= 65536;
-}
-
-template <class KernelT>
-void allow_lds(KernelT kernel) {
-  // Raise the dynamic LDS limit of this kernel to the gfx950 maximum (idempotent).
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
-}
-
-template <int WDT, int NR, int MB, int ROLE>
-hipError_t launch_stream(const DecodeArgs& a, int groups, int splits, int r, hipStream_t st) {
-  static bool ready = false;  // set once per instantiation; the attribute is per kernel
+template <int WDT, int NR, int MB>
+hipError_t launch_one(const DecodeArgs& a, int grid, size_t smem, hipStream_t st) {
+  static bool ready = false;  // the attribute is per kernel; setting it twice is harmless
   if (!ready) {
-    allow_lds(stream_kernel<WDT, NR, MB, ROLE>);
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<WDT, NR, MB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
+    if (e != hipSuccess) return e;
     ready = true;
   }
-  const size_t sm = stream_smem(a.M, a.kc, NR, MB, r);
-  stream_kernel<WDT, NR, MB, ROLE><<<dim3((unsigned)groups, (unsigned)splits), dim3(DT), sm, st>>>(a);
+  decode_kernel<WDT, NR, MB><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a);
   return hipGetLastError();
 }
 
-template <int WDT, int ROLE>
-hipError_t dispatch(const DecodeArgs& a, int mb, int nr, int groups, int splits, int r, hipStream_t st) {
+template <int WDT>
+hipError_t dispatch(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
   if (nr == 1) {
-    switch (mb) {
-      case 1: return launch_stream<WDT, 1, 1, ROLE>(a, groups, splits, r, st);
-      case 2: return launch_stream<WDT, 1, 2, ROLE>(a, groups, splits, r, st);
-      case 3: return launch_stream<WDT, 1, 3, ROLE>(a, groups, splits, r, st);
-      default: return launch_stream<WDT, 1, 4, ROLE>(a, groups, splits, r, st);
-    }
+    if (mb == 1) return launch_one<WDT, 1, 1>(a, grid, smem, st);
+    return launch_one<WDT, 1, 2>(a, grid, smem, st);
   }
-  switch (mb) {
-    case 1: return launch_stream<WDT, 2, 1, ROLE>(a, groups, splits, r, st);
-    case 2: return launch_stream<WDT, 2, 2, ROLE>(a, groups, splits, r, st);
-    case 3: return launch_stream<WDT, 2, 3, ROLE>(a, groups, splits, r, st);
-    default: return launch_stream<WDT, 2, 4, ROLE>(a, groups, splits, r, st);
-  }
+  if (mb == 3) return launch_one<WDT, 2, 3>(a, grid, smem, st);
+  return launch_one<WDT, 2, 4>(a, grid, smem, st);
 }
 
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+// Poll bound of the T wait; WSL_DECODE_SPIN_LIMIT overrides it (a test uses 0 to run the
+// local fallback).
+int spin_limit() {
+  const char* e = std::getenv("WSL_DECODE_SPIN_LIMIT");
+  if (e == nullptr || *e == 0) return kDefaultSpin;
+  const long v = std::strtol(e, nullptr, 10);
+  return v < 0 ? 0 : (v > (1L << 30) ? (1 << 30) : (int)v);
+}
 
 }  // namespace
 
@@ -365,12 +591,13 @@ bool decode_supported(const LoraArgs& p) {
   if (p.K % wave_k_of(p.w_dtype) != 0) return false;
   if (!aligned16(p.x) || p.ldx % 8 != 0) return false;
   if (!aligned16(p.w) || p.ldw % (fp8 ? 16 : 8) != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(p.y) & 7u) != 0 || p.ldy % 4 != 0) return false;
   if (p.r > 0) {
     if (p.r % 8 != 0) return false;
     if (!aligned16(p.a) || p.lda % 8 != 0) return false;
     if (!aligned16(p.b) || p.ldb % 8 != 0) return false;
   }
-  return plan_ok(plan_decode(p.M, p.N, p.K, p.r, p.w_dtype), p.M, p.r);
+  return plan_decode(p.M, p.N, p.K, p.r, p.w_dtype).ok;
 }
 
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
@@ -380,36 +607,25 @@ size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_
 hipError_t launch_decode(const LoraArgs& p) {
   const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
   char* ws = reinterpret_cast<char*>(p.ws);
-  float* tpart = reinterpret_cast<float*>(ws + pl.off_pt);
-  if (p.r > 0) {
-    DecodeArgs t{};
-    t.x = reinterpret_cast<const uint16_t*>(p.x); t.ldx = p.ldx;
-    t.mat = p.a; t.ldm = p.lda; t.rows = (int)p.r;
-    t.M = (int)p.M; t.kc = pl.t.kc;
-    t.part = tpart;
-    hipError_t e = dispatch<kBF16, kRoleT>(t, pl.mb, 1, pl.t.groups, pl.t.splits, 0, p.stream);
-    if (e != hipSuccess) return e;
-  }
-  DecodeArgs y{};
-  y.x = reinterpret_cast<const uint16_t*>(p.x); y.ldx = p.ldx;
-  y.mat = p.w; y.ldm = p.ldw; y.rows = (int)p.N;
-  y.M = (int)p.M; y.kc = pl.y.kc;
-  y.part = reinterpret_cast<float*>(ws + pl.off_py);
-  y.tpart = tpart; y.tsplits = pl.t.splits; y.s = p.scale;
-  y.w_scale = p.w_scale;
-  y.b = reinterpret_cast<const uint16_t*>(p.b); y.ldb = p.ldb; y.r = (int)p.r;
-  y.y = reinterpret_cast<uint16_t*>(p.y); y.ldy = p.ldy;
-  const bool fp8 = p.w_dtype == kFP8;
-  const int r = (int)p.r;
-  if (pl.y.splits == 1) {
-    return fp8 ? dispatch<kFP8, kRoleY>(y, pl.mb, pl.nr, pl.y.groups, 1, r, p.stream)
-               : dispatch<kBF16, kRoleY>(y, pl.mb, pl.nr, pl.y.groups, 1, r, p.stream);
-  }
-  hipError_t e = fp8 ? dispatch<kFP8, kRolePartial>(y, pl.mb, pl.nr, pl.y.groups, pl.y.splits, 0, p.stream)
-                     : dispatch<kBF16, kRolePartial>(y, pl.mb, pl.nr, pl.y.groups, pl.y.splits, 0, p.stream);
-  if (e != hipSuccess) return e;
-  reduce_kernel<<<dim3((unsigned)((p.N + RT - 1) / RT), (unsigned)p.M), dim3(RT), 0, p.stream>>>(y, pl.y.splits);
-  return hipGetLastError();
+  DecodeArgs a{};
+  a.x = reinterpret_cast<const uint16_t*>(p.x); a.ldx = p.ldx;
+  a.w = p.w; a.ldw = p.ldw; a.w_scale = p.w_scale;
+  a.a = reinterpret_cast<const uint16_t*>(p.a); a.lda = p.lda;
+  a.b = reinterpret_cast<const uint16_t*>(p.b); a.ldb = p.ldb;
+  a.y = reinterpret_cast<uint16_t*>(p.y); a.ldy = p.ldy;
+  a.s = p.scale;
+  a.M = (int)p.M; a.N = (int)p.N; a.K = (int)p.K; a.r = (int)p.r; a.r32 = pl.r32;
+  a.gT = pl.gT; a.kst = pl.kst; a.kct = pl.kct;
+  a.gY = pl.gY; a.ksy = pl.ksy; a.kcy = pl.kcy;
+  a.flag_off = (int)pl.flag_off;
+  a.cnt = reinterpret_cast<unsigned*>(ws);
+  a.tfin = reinterpret_cast<uint64_t*>(ws + pl.off_t);
+  a.tpart = reinterpret_cast<float*>(ws + pl.off_pt);
+  a.ypart = reinterpret_cast<float*>(ws + pl.off_py);
+  a.spin = spin_limit();
+  const int grid = pl.gT * pl.kst + pl.gY * pl.ksy;
+  return p.w_dtype == kFP8 ? dispatch<kFP8>(a, pl.mb, pl.nr, grid, pl.smem, p.stream)
+                           : dispatch<kBF16>(a, pl.mb, pl.nr, grid, pl.smem, p.stream);
 }
 
 }  // namespace wsl

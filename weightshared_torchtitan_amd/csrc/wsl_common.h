@@ -106,9 +106,9 @@ hipError_t launch_factorized_embedding(const int64_t* ids, int64_t n_ids, const 
 // Largest M routed to the decode-shaped (skinny) kernels.
 constexpr int64_t kDecodeMaxM = 64;
 
-// Every workspace starts with this many bytes of arrival counters. They must be zero
-// when the workspace is first used; every launch leaves them zero. Path-specific
-// scratch follows the prefix.
+// Every workspace starts with this many bytes of counters (a launch counter and arrival
+// counters of the decode path). They must be zero when the workspace is first used;
+// every launch leaves them valid for the next. Path-specific scratch follows the prefix.
 constexpr size_t kCounterBytes = 65536;
 
 }  // namespace wsl

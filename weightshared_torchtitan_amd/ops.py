@@ -56,8 +56,9 @@ def workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     """The persistent scratch buffer of (device, stream).
 
     libwsl requires its workspace to be zero-filled before first use (the leading
-    arrival counters of the decode kernels) and leaves it that way, so one zero-filled
-    buffer per stream is reused by every call on that stream; it only grows.
+    counters of the decode kernels) and keeps those counters valid across calls, so one
+    zero-filled buffer per stream is reused by every call on that stream; it only grows
+    (a grown buffer starts zeroed again).
     """
     key = (dev.index, stream)
     buf = _workspaces.get(key)
@@ -131,7 +132,7 @@ def lora_linear_op(x: torch.Tensor, w: Optional[torch.Tensor], w_scale: Optional
                 M, N, K, r,
                 ws.data_ptr(), ws.numel(), stream)
         if rc != _native.WSL_OK:
-            _workspaces.pop((dev.index, stream), None)  # a failed launch may leave counters set
+            _workspaces.pop((dev.index, stream), None)  # a failed launch may leave counters mid-update
         _native.check(rc, "wsl_lora_linear_fwd")
     return y.reshape(*lead, N)
 
