@@ -105,7 +105,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const void* __restrict__ w, int64_t ldw, const float* __restrict__ w_scale,
                const uint16_t* __restrict__ a, int64_t lda,
                const uint16_t* __restrict__ tg, int64_t ldt,
-               const uint16_t* __restrict__ bm, int64_t ldb, float s,
+               const uint16_t* __restrict__ bm, int64_t ldb, float s, float yscale,
                uint16_t* __restrict__ y, int64_t ldy,
                int M, int N, int K, int r, int tiles_m, int tiles_n) {
   constexpr bool W8 = HAS_W && WDT == kFP8;
@@ -458,10 +458,10 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   for (int j = 0; j < C::MJ; ++j) {
     const int m = m0 + wm * C::TM + j * 32 + l32;
     if (m >= M) continue;
-    float keep = 1.f;
+    float keep = yscale;
     if constexpr (GATHER) {
       const int64_t id = gidx[m];
-      keep = (id >= 0 && id < grows) ? 1.f : 0.f;  // out-of-range ids give zero rows
+      if (id < 0 || id >= grows) keep = 0.f;  // out-of-range ids give zero rows
     }
     uint16_t* yr = y + (int64_t)m * ldy;
 #pragma unroll
@@ -485,30 +485,6 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   }
 }
 
-// T[m][j] = bf16(s * x[m] . A[j]), one thread per (m, j): pre-pass for ranks above the
-// in-kernel limit (row stride ldt).
-__global__ void __launch_bounds__(256) down_pad_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                       const uint16_t* __restrict__ a, int64_t lda,
-                                                       float s, uint16_t* __restrict__ t,
-                                                       int64_t ldt, int64_t M, int64_t K,
-                                                       int64_t r) {
-  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= M * r) return;
-  int64_t m = idx / r, j = idx % r;
-  const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(x + m * ldx);
-  const u32x4_t* ar = reinterpret_cast<const u32x4_t*>(a + j * lda);
-  float acc = 0.f;
-  for (int64_t kc = 0; kc < K / 8; ++kc) {
-    u32x4_t xv = xr[kc], av = ar[kc];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      acc += bf16_bits_to_f32(xv[q] & 0xffffu) * bf16_bits_to_f32(av[q] & 0xffffu);
-      acc += bf16_bits_to_f32(xv[q] >> 16) * bf16_bits_to_f32(av[q] >> 16);
-    }
-  }
-  t[m * ldt + j] = f32_to_bf16_bits(s * acc);
-}
-
 using CfgBig = Cfg<256, 256, 2, 8>;   // 8 waves, 128(n) x 64(m) per wave
 using CfgTall = Cfg<128, 256, 4, 8>;  // 8 waves, 64 x 64 per wave
 
@@ -519,7 +495,7 @@ hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
   prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER><<<dim3(tiles_m * tiles_n), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
-      reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale,
+      reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
       reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n);
   return hipGetLastError();
 }
@@ -597,13 +573,15 @@ hipError_t launch_prefill(const LoraArgs& p) {
   const uint16_t* tg = nullptr;
   int64_t ldt = 0;
   if (p.r > RIN) {
+    // Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by this same kernel run
+    // as a plain GEMM with A in the place of W (N = r) and s applied before rounding.
     ldt = p.r;
     uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
-    const int64_t n = p.M * p.r;
-    down_pad_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, p.stream>>>(
-        reinterpret_cast<const uint16_t*>(p.x), p.ldx, reinterpret_cast<const uint16_t*>(p.a),
-        p.lda, p.scale, t, ldt, p.M, p.K, p.r);
-    hipError_t e = hipGetLastError();
+    LoraArgs q = p;
+    q.w = p.a; q.ldw = p.lda; q.w_dtype = kBF16; q.w_scale = nullptr;
+    q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0;
+    q.N = p.r; q.y = t; q.ldy = ldt; q.yscale = p.scale;
+    const hipError_t e = launch_rank<kBF16, true>(q, nullptr, 0);
     if (e != hipSuccess) return e;
     tg = t;
   }

@@ -85,6 +85,9 @@ struct LoraArgs {
   // Optional row gather on x: row m of x is row gather[m] of a [gather_rows, ldx] table;
   // ids outside [0, gather_rows) read as zero rows. Used by the factorized embedding.
   const int64_t* gather; int64_t gather_rows;
+  // Factor applied to the fp32 result before the bf16 rounding of y (prefill path; the
+  // rank pre-pass uses it to store bf16(s * x . A^T)).
+  float yscale = 1.f;
 };
 
 // Each launcher returns hipSuccess or the launch error.
