@@ -63,13 +63,15 @@ struct Cfg {
   static_assert(NXI >= 1 && NWI >= 1 && NBI >= 1, "tile too small for the direct-fill split");
 };
 
-// Byte offset of 16-byte chunk `c` (0..7) of LDS row `row` (128-byte rows). XOR swizzle:
-// the 8 rows that 8 consecutive lanes read at one chunk index fall in distinct banks.
-__device__ __forceinline__ int lds_off(int row, int c) { return row * ROWB + ((c ^ (row & 7)) << 4); }
+// Byte offset of 16-byte chunk `c` (0..7) of LDS row `row` (128-byte rows). XOR swizzle
+// with row bits 1..3: a ds_read_b128 is served 16 lanes (256 bytes, all 64 banks) at a
+// time, and the 16 consecutive rows those lanes read at one chunk index then cover all
+// 16 bank groups (row parity picks the half of the banks, the XOR the 16-byte slot).
+__device__ __forceinline__ int lds_off(int row, int c) { return row * ROWB + ((c ^ ((row >> 1) & 7)) << 4); }
 
-// Chunk a lane fetches in a direct fill: the fill writes lane i to LDS slot i%8 of row
-// (group*8 + i/8), which holds global chunk (i%8) ^ (row%8) = (i%8) ^ (i/8).
-__device__ __forceinline__ int fill_chunk(int lane) { return (lane & 7) ^ ((lane >> 3) & 7); }
+// Chunk a lane fetches in direct fill number `grp`: the fill writes lane i to LDS slot
+// i%8 of row R = grp*8 + i/8, which holds global chunk (i%8) ^ ((R >> 1) & 7).
+__device__ __forceinline__ int fill_chunk(int lane, int grp) { return (lane & 7) ^ (((grp & 1) << 2) | (lane >> 4)); }
 
 __device__ __forceinline__ u32x4_t lds_read16(const char* base, int off) {
   return *reinterpret_cast<const u32x4_t*>(base + off);
@@ -140,7 +142,6 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   const int n0 = tn * C::BN;
 
   // ---- sources of this wave's direct fills: uniform tile base + 32-bit lane offset ----
-  const int fc = fill_chunk(lane);
   const char* xbase = reinterpret_cast<const char*>(GATHER ? x : x + (int64_t)m0 * ldx);
   uint32_t xoff[C::NXI];
   const uint16_t* xg[GATHER ? C::NXI : 1];  // gathered rows keep 64-bit row pointers
@@ -150,10 +151,10 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int gr = min(m0 + row, M - 1);
     if constexpr (GATHER) {
       const int64_t id = gidx[gr];
-      xg[i] = x + ((id >= 0 && id < grows) ? id : 0) * ldx + fc * 8;  // bad ids: zeroed at the store
+      xg[i] = x + ((id >= 0 && id < grows) ? id : 0) * ldx + fill_chunk(lane, wave * C::NXI + i) * 8;  // bad ids: zeroed at the store
       xoff[i] = 0;
     } else {
-      xoff[i] = (uint32_t)((gr - m0) * ldx * 2 + fc * 16);
+      xoff[i] = (uint32_t)((gr - m0) * ldx * 2 + fill_chunk(lane, wave * C::NXI + i) * 16);
     }
   }
   const char* wbase = reinterpret_cast<const char*>(w) + (WDIRECT ? (int64_t)n0 * ldw * 2 : 0);
@@ -161,13 +162,13 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
   for (int i = 0; i < C::NWI; ++i) {
     const int row = (wave * C::NWI + i) * 8 + (lane >> 3);
-    woff[i] = (uint32_t)((min(n0 + row, N - 1) - n0) * ldw * 2 + fc * 16);
+    woff[i] = (uint32_t)((min(n0 + row, N - 1) - n0) * ldw * 2 + fill_chunk(lane, wave * C::NWI + i) * 16);
   }
   // rank-A slice: RB*32 rows = RB*4 fills, one per wave for waves < RB*4 (rows >= r read
   // row r-1 and are zeroed before the MFMA)
   constexpr int NAI = RB * 4;
   uint32_t aoff = 0;
-  if constexpr (RB > 0) aoff = (uint32_t)(min(wave * 8 + (lane >> 3), r - 1) * lda * 2 + fc * 16);
+  if constexpr (RB > 0) aoff = (uint32_t)(min(wave * 8 + (lane >> 3), r - 1) * lda * 2 + fill_chunk(lane, wave) * 16);
   // fp8 W: BN rows x 64 B per K tile, 16 fp8 per chunk
   constexpr int W8C = W8 ? C::BN * 4 / NT : 1;  // chunks per thread
   const uint8_t* w8row[W8C];
@@ -203,7 +204,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     for (int i = 0; i < C::NBI; ++i) {
       const int grp = wave * C::NBI + i;
       const int row = grp * 8 + (lane >> 3);
-      const int kr = rk0 + fc * 8;
+      const int kr = rk0 + fill_chunk(lane, grp) * 8;
       const uint16_t* src = bm + (int64_t)min(n0 + row, N - 1) * ldb + (kr < r ? kr : 0);
       direct_fill(dst, grp, src);
     }
@@ -312,6 +313,22 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   };
 
+  // Interleave the MFMAs of the current k step with the LDS reads of the next one, so
+  // the reads are issued early and their latency hides behind the MFMAs (left to
+  // itself the scheduler sinks each read next to its use).
+  auto interleave = [&]() {
+    constexpr int NMF = (HAS_W ? C::NI * C::MJ : 0) + TPW;
+    constexpr int NRD = C::MJ + (HAS_W ? C::NI : 0) + TPW;
+    constexpr int PAIRS = NMF < NRD ? NMF : NRD;
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    if constexpr (NMF > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS, 0);
+    if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
+  };
+
   const int nk = K / BK;
   // The last K tile runs from buffer (nk-1)&1; the B slice of the LoRA phase is filled
   // into the other one while it does.
@@ -341,6 +358,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         Frags nxt;
         frag_load(buf, kk + 1, nxt);
         frag_mma(cur, kk);
+        interleave();
         cur = nxt;
       }
       if (kt + 1 < nk) {
@@ -359,6 +377,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       Frags nxt;
       frag_load(buf ^ 1, 0, nxt);
       frag_mma(cur, KK - 1);
+      interleave();
       cur = nxt;
     }
     __syncthreads();  // every wave is done with the ring before the LDS is reused
