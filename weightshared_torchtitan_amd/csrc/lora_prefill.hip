@@ -28,7 +28,8 @@
 // writes T to the workspace and the kernel consumes it the same way.
 //
 // The MFMA "A" operand is the W tile (rows n) and "B" the x tile (rows m): each lane
-// ends with 4 consecutive n of one m per accumulator group, stored as 8-byte writes.
+// ends with 4 consecutive n of one m per accumulator group; the tile is staged through
+// LDS and written back as whole rows.
 //
 // Workgroups are dispatched round-robin over the 8 XCDs; the tile order remaps them so
 // that each XCD works on a compact group of m x n tiles and its L2 serves the reuse.
@@ -116,9 +117,11 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   constexpr int NT = C::NT;
   constexpr int AB = RB * 32 * ROWB;         // rank-A slice of a K tile
   constexpr int STAGE = C::XB + C::WB + AB;  // one of the two ring buffers
-  static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+  constexpr int OS = C::BN * 2 + 16;          // LDS row stride of the staged output tile
+  constexpr int LDS_BYTES = (2 * STAGE > C::BM * OS) ? 2 * STAGE : C::BM * OS;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert(C::BM * ROWB + 16384 <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -472,34 +475,51 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
 
-  // ---- store: lane holds y[m][n..n+3] for m = col, n = 8g + 4*lh + (0..3) ----
+  // ---- store. The accumulators hold 4 consecutive n of one m per lane and group, i.e.
+  // 16-byte pieces of 32 different rows per wave instruction; written straight to y
+  // they reach L2 as partial lines. The tile is staged through LDS (row stride OS) and
+  // written back row-contiguously, 16 bytes per lane.
+  char* ot = lds;  // the ring is idle: the last barrier above ended every LDS use
 #pragma unroll
   for (int j = 0; j < C::MJ; ++j) {
-    const int m = m0 + wm * C::TM + j * 32 + l32;
-    if (m >= M) continue;
+    const int mr = wm * C::TM + j * 32 + l32;
     float keep = yscale;
     if constexpr (GATHER) {
-      const int64_t id = gidx[m];
+      const int64_t id = gidx[min(m0 + mr, M - 1)];
       if (id < 0 || id >= grows) keep = 0.f;  // out-of-range ids give zero rows
     }
-    uint16_t* yr = y + (int64_t)m * ldy;
 #pragma unroll
     for (int i = 0; i < C::NI; ++i) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * C::TN + i * 32 + g * 8 + lh * 4;
+        const int nc = wn * C::TN + i * 32 + g * 8 + lh * 4;
         const f32x16_t& cc = acc[i][j];
-        if (n + 3 < N) {
-          uint2 v;
-          v.x = pack_bf16x2(keep * cc[g * 4 + 0], keep * cc[g * 4 + 1]);
-          v.y = pack_bf16x2(keep * cc[g * 4 + 2], keep * cc[g * 4 + 3]);
-          *reinterpret_cast<uint2*>(yr + n) = v;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < N) yr[n + e] = f32_to_bf16_bits(keep * cc[g * 4 + e]);
-        }
+        uint2 v;
+        v.x = pack_bf16x2(keep * cc[g * 4 + 0], keep * cc[g * 4 + 1]);
+        v.y = pack_bf16x2(keep * cc[g * 4 + 2], keep * cc[g * 4 + 3]);
+        *reinterpret_cast<uint2*>(ot + mr * OS + nc * 2) = v;
       }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = C::BN / 8;  // 16-byte chunks per tile row
+  const bool a16 = ((reinterpret_cast<uintptr_t>(y) & 15u) == 0) && ((ldy & 7) == 0);
+#pragma unroll 4
+  for (int q = tid; q < C::BM * CPR; q += NT) {
+    const int row = q / CPR, c = q % CPR;
+    const int m = m0 + row, n = n0 + c * 8;
+    if (m >= M || n >= N) continue;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ot + row * OS + c * 16);
+    uint16_t* dst = y + (int64_t)m * ldy + n;
+    if (n + 8 <= N) {
+      if (a16) {
+        *reinterpret_cast<u32x4_t*>(dst) = v;
+      } else {
+        reinterpret_cast<uint2*>(dst)[0] = uint2{v[0], v[1]};
+        reinterpret_cast<uint2*>(dst)[1] = uint2{v[2], v[3]};
+      }
+    } else {
+      for (int e = 0; e < N - n; ++e) dst[e] = (uint16_t)(v[e >> 1] >> ((e & 1) * 16));
     }
   }
 }
