@@ -1,0 +1,71 @@
+/*
+ * wsl_decode.h — decode-step kernels of the weight-shared Qwen3 harness (libwsl.so).
+ *
+ * These have no counterpart at the reference's boundary: the reference runs them as torch
+ * ops inside its Qwen3 block (torchtitan/experiments/qwen3/model/model.py:167-218,
+ * 250-251, 296-314) and re-runs the whole prefix every generated token
+ * (scripts/generate/_generation.py:43). Here one token step keeps a KV cache, and the
+ * work between two fused LoRA projections is one launch each. Conventions as in
+ * wsl_lora.h: device pointers, bf16 tensors, explicit leading dimensions, work enqueued on
+ * `stream`, return WSL_OK or a negative WSL_E_* code (wsl_decode_last_error() describes
+ * the last failure of these entry points). Arithmetic is fp32 with one rounding to bf16
+ * per output.
+ *
+ * KV cache layout (one layer): k_cache, v_cache [batch, n_kv_heads, cache_len, head_dim].
+ * `pos` is a device int64 scalar (the position of the token being decoded), so a step can
+ * be captured once in a HIP graph and replayed with pos advanced on the device.
+ */
+#ifndef WSL_DECODE_H
+#define WSL_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "wsl_lora.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* h = x (+ residual, the sum rounded to bf16), written to h_out when it is not NULL;
+ * out = h * rsqrt(mean(h^2) + eps) * weight.   x, residual, h_out, out [rows, dim], weight [dim].
+ * Replaces RMSNorm (qwen3/model/model.py:296-314 attention_norm / ffn_norm / norm) and the
+ * residual add before it. dim % 8 == 0, dim <= 8192; 16-byte aligned rows. */
+int wsl_rmsnorm_fwd(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight,
+                    float eps, void* out, int64_t ldo, void* h_out, int64_t ldh, int64_t rows, int64_t dim,
+                    void* stream);
+
+/* One decode token per sequence. qkv [batch, ldqkv] holds q | k | v heads
+ * ([n_heads + 2 n_kv_heads] x head_dim). q and k are RMS-normed over head_dim
+ * (q_norm_w / k_norm_w [head_dim]), rotated by RoPE row `*pos` of `rope`
+ * ([*, 2 head_dim] fp32: cos then sin), q written to q_out [batch, n_heads, head_dim],
+ * k and v written into the caches at position *pos. Replaces
+ * qwen3/model/model.py:195-198 (q/k norm) and :73-90 (apply_rotary_emb) plus the cache
+ * write. head_dim in {64, 128, 256}. */
+int wsl_qk_norm_rope_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                         int64_t head_dim, const void* q_norm_w, const void* k_norm_w, float eps,
+                         const float* rope, const int64_t* pos, void* q_out, void* k_cache, void* v_cache,
+                         int64_t cache_len, void* stream);
+
+/* out [batch, n_heads * head_dim] = softmax(q . K^T * scale) . V over cache positions
+ * 0..*pos, query head h reading kv head h / (n_heads / n_kv_heads). Replaces the
+ * repeat_kv + scaled_dot_product_attention of qwen3/model/model.py:93-102,204-214 for one
+ * query token. n_heads / n_kv_heads in {1, 2, 4, 8}; head_dim in {64, 128}. */
+int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_cache, int64_t batch,
+                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t cache_len,
+                             const int64_t* pos, float scale, void* out, void* stream);
+
+/* out [rows, ffn] = silu(g) * u with g = gate_up[:, :ffn], u = gate_up[:, ffn:2 ffn].
+ * Replaces F.silu(w1(x)) * w3(x) (qwen3/model/model.py:250-251) given the two projections'
+ * outputs side by side. ffn % 8 == 0; 16-byte aligned rows. */
+int wsl_swiglu_fwd(const void* gate_up, int64_t ld, int64_t rows, int64_t ffn, void* out, int64_t ldo,
+                   void* stream);
+
+/* Thread-local description of the last failure of an entry point above ("" if none). */
+const char* wsl_decode_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WSL_DECODE_H */

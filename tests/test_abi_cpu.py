@@ -12,15 +12,19 @@ from weightshared_torchtitan_amd import _native as N
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "wsl_lora.h")
+HEADERS = sorted(os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include"))
+                 if f.endswith(".h"))
 
 needs_lib = pytest.mark.skipif(not os.path.exists(N.LIB_PATH),
                                reason="libwsl.so not built (run __graft_entry__.build())")
 
 
 def _header_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(wsl_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(wsl_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def _header_defines():
@@ -173,3 +177,23 @@ def test_ops_refuse_cpu_tensors():
     with pytest.raises((RuntimeError, NotImplementedError)):
         ops.factorized_embedding(torch.zeros(3, dtype=torch.int64), torch.zeros(10, 8, dtype=torch.bfloat16),
                                  torch.zeros(16, 8, dtype=torch.bfloat16))
+
+
+@needs_lib
+def test_decode_step_validation_codes():
+    lib = N.lib()
+    P2 = P
+    # rmsnorm: dim not a multiple of 8; misaligned pointer; empty batch
+    assert lib.wsl_rmsnorm_fwd(P2, 64, None, 0, P2, 1e-6, P2, 64, None, 0, 4, 60, None) == N.WSL_E_SHAPE
+    assert lib.wsl_rmsnorm_fwd(P2 + 2, 64, None, 0, P2, 1e-6, P2, 64, None, 0, 4, 64, None) == N.WSL_E_ALIGN
+    assert lib.wsl_rmsnorm_fwd(None, 64, None, 0, None, 1e-6, None, 64, None, 0, 0, 64, None) == N.WSL_OK
+    assert N.decode_last_error() == ""
+    # qk norm + rope: unsupported head_dim; ld too small
+    assert lib.wsl_qk_norm_rope_fwd(P2, 4096, 2, 16, 8, 96, P2, P2, 1e-6, P2, P2, P2, P2, P2, 64, None) == N.WSL_E_SHAPE
+    assert lib.wsl_qk_norm_rope_fwd(P2, 100, 2, 16, 8, 128, P2, P2, 1e-6, P2, P2, P2, P2, P2, 64, None) == N.WSL_E_SHAPE
+    assert N.decode_last_error() != ""
+    # attention: heads not a multiple of kv heads / unsupported grouping
+    assert lib.wsl_decode_attention_fwd(P2, P2, P2, 2, 12, 8, 128, 64, P2, 0.1, P2, None) == N.WSL_E_SHAPE
+    assert lib.wsl_decode_attention_fwd(P2, P2, P2, 2, 48, 3, 128, 64, P2, 0.1, P2, None) == N.WSL_E_SHAPE
+    # swiglu: ld below 2 * ffn
+    assert lib.wsl_swiglu_fwd(P2, 100, 4, 64, P2, 64, None) == N.WSL_E_SHAPE

@@ -1,0 +1,131 @@
+"""GPU parity of the decode-step kernels (include/wsl_decode.h) against plain PyTorch fp32
+references of the same ops, at the benchmark model's shapes and at small/edge shapes.
+
+Bar: max|y - y_ref| / max|y_ref| <= 1e-2 (bf16 output, fp32 arithmetic); bit-exact where
+the op is exact (the bf16 residual sum, cache positions the step must not touch)."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def rel(x, ref):
+    return ((x.float() - ref.float()).abs().max() / ref.float().abs().max()).item()
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def rms_ref(h, w, eps):
+    hf = h.float()
+    return hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+
+
+@pytest.mark.parametrize("rows,dim", [(8, 1024), (1, 2048), (3, 4096), (5, 8192), (16, 64)])
+def test_rmsnorm_and_add_rmsnorm(gpu, rows, dim):
+    from weightshared_torchtitan_amd import ops
+    _say(f"[rmsnorm] rows={rows} dim={dim}")
+    g = torch.Generator(device="cuda").manual_seed(rows * dim)
+    x = torch.randn(rows, dim, device=gpu, generator=g).bfloat16()
+    res = torch.randn(rows, dim, device=gpu, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(dim, device=gpu, generator=g)).bfloat16()
+    out = ops.rmsnorm_op(x, w, 1e-6)
+    assert rel(out, rms_ref(x, w, 1e-6)) <= TOL
+    out2, h = ops.add_rmsnorm_op(x, res, w, 1e-6)
+    h_ref = (x.float() + res.float()).bfloat16()
+    assert torch.equal(h, h_ref)  # the residual sum is one bf16 rounding either way
+    assert rel(out2, rms_ref(h_ref, w, 1e-6)) <= TOL
+
+
+def rope_ref(x, rc_row, hd):
+    cos, sin = rc_row[:hd], rc_row[hd:]
+    rot = torch.cat((-x[..., hd // 2:], x[..., :hd // 2]), dim=-1)
+    return x * cos + rot * sin
+
+
+@pytest.mark.parametrize("b,nh,nkv,hd,L,pos", [(8, 16, 8, 128, 1024, 517), (2, 4, 2, 64, 32, 0),
+                                             (3, 8, 8, 256, 16, 15)])
+def test_qk_norm_rope_writes_q_and_cache(gpu, b, nh, nkv, hd, L, pos):
+    from weightshared_torchtitan_amd import ops
+    from weightshared_torchtitan_amd.qwen3_shared import _rope_cache
+    _say(f"[qk_norm_rope] b={b} nh={nh} nkv={nkv} hd={hd} pos={pos}")
+    g = torch.Generator(device="cuda").manual_seed(hd + pos)
+    qkv = torch.randn(b, (nh + 2 * nkv) * hd, device=gpu, generator=g).bfloat16()
+    qw = (1 + 0.1 * torch.randn(hd, device=gpu, generator=g)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(hd, device=gpu, generator=g)).bfloat16()
+    rope = _rope_cache(hd, L, 1e6).to(gpu)
+    kc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+    vc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+    kc0, vc0 = kc.clone(), vc.clone()
+    p = torch.full((), pos, dtype=torch.int64, device=gpu)
+    q = ops.qk_norm_rope_op(qkv, qw, kw, 1e-6, rope, p, kc, vc, nh, nkv)
+    heads = qkv.view(b, nh + 2 * nkv, hd).float()
+    q_ref = rope_ref(rms_ref(heads[:, :nh], qw, 1e-6), rope[pos], hd)
+    k_ref = rope_ref(rms_ref(heads[:, nh:nh + nkv], kw, 1e-6), rope[pos], hd)
+    assert rel(q, q_ref) <= TOL
+    assert rel(kc[:, :, pos], k_ref) <= TOL
+    assert torch.equal(vc[:, :, pos], qkv.view(b, nh + 2 * nkv, hd)[:, nh + nkv:])
+    others = torch.arange(L, device=gpu) != pos
+    assert torch.equal(kc[:, :, others], kc0[:, :, others])
+    assert torch.equal(vc[:, :, others], vc0[:, :, others])
+
+
+def attn_ref(q, kc, vc, pos, scale):
+    b, nh, hd = q.shape
+    nkv = kc.shape[1]
+    rep = nh // nkv
+    k = kc[:, :, :pos + 1].float().repeat_interleave(rep, dim=1)   # [b, nh, t, hd]
+    v = vc[:, :, :pos + 1].float().repeat_interleave(rep, dim=1)
+    s = torch.einsum("bhd,bhtd->bht", q.float(), k) * scale
+    p = torch.softmax(s, dim=-1)
+    return torch.einsum("bht,bhtd->bhd", p, v).reshape(b, nh * hd)
+
+
+@pytest.mark.parametrize("b,nh,nkv,hd,L,pos", [(8, 16, 8, 128, 1024, 767), (8, 16, 8, 128, 1024, 0),
+                                             (2, 4, 2, 64, 64, 37), (1, 8, 1, 128, 300, 299),
+                                             (3, 4, 4, 64, 50, 31)])
+def test_decode_attention(gpu, b, nh, nkv, hd, L, pos):
+    from weightshared_torchtitan_amd import ops
+    _say(f"[decode_attention] b={b} nh={nh} nkv={nkv} hd={hd} L={L} pos={pos}")
+    g = torch.Generator(device="cuda").manual_seed(L + pos)
+    q = torch.randn(b, nh, hd, device=gpu, generator=g).bfloat16()
+    kc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+    vc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+    # positions past `pos` must not matter: fill them with huge values
+    if pos + 1 < L:
+        kc[:, :, pos + 1:] = 1e4
+        vc[:, :, pos + 1:] = -1e4
+    p = torch.full((), pos, dtype=torch.int64, device=gpu)
+    out = ops.decode_attention_op(q, kc, vc, p, hd ** -0.5)
+    ref = attn_ref(q, kc, vc, pos, hd ** -0.5)
+    assert rel(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("rows,ffn", [(8, 3072), (1, 6144), (5, 64)])
+def test_swiglu(gpu, rows, ffn):
+    from weightshared_torchtitan_amd import ops
+    _say(f"[swiglu] rows={rows} ffn={ffn}")
+    g = torch.Generator(device="cuda").manual_seed(ffn)
+    gu = torch.randn(rows, 2 * ffn, device=gpu, generator=g).bfloat16()
+    out = ops.swiglu_op(gu)
+    gf, uf = gu[:, :ffn].float(), gu[:, ffn:].float()
+    assert rel(out, torch.nn.functional.silu(gf) * uf) <= TOL
+
+
+def test_grouped_projection_equals_separate_calls(gpu):
+    """[W_q; W_k; W_v] with the block-diagonal B is the three LoRA linears."""
+    import weightshared_torchtitan_amd as wsl
+    _say("[grouped qkv] M=8 K=1024 r=32")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(8, 1024, device=gpu, generator=g).bfloat16()
+    Ws = [(torch.randn(n, 1024, device=gpu, generator=g) * 0.02).bfloat16() for n in (2048, 1024, 1024)]
+    As = [(torch.randn(32, 1024, device=gpu, generator=g) * 0.02).bfloat16() for _ in range(3)]
+    Bs = [(torch.randn(n, 32, device=gpu, generator=g) * 0.02).bfloat16() for n in (2048, 1024, 1024)]
+    sep = torch.cat([wsl.lora_linear(x, W, A, B, 2.0) for W, A, B in zip(Ws, As, Bs)], -1)
+    Bbd = torch.zeros(4096, 96, device=gpu, dtype=torch.bfloat16)
+    Bbd[:2048, :32], Bbd[2048:3072, 32:64], Bbd[3072:, 64:] = Bs
+    grp = wsl.lora_linear(x, torch.cat(Ws), torch.cat(As), Bbd, 2.0)
+    assert rel(grp, sep) <= 1e-2

@@ -27,13 +27,18 @@ WSL_DTYPE_BF16 = 0
 WSL_DTYPE_FP8_E4M3 = 1
 WSL_MAX_RANK = 256
 
-# Every symbol include/wsl_lora.h declares.
+# Every symbol include/wsl_lora.h and include/wsl_decode.h declare.
 EXPORTED = (
     "wsl_lora_linear_workspace_bytes",
     "wsl_lora_linear_fwd",
     "wsl_factorized_embedding_fwd",
     "wsl_last_error",
     "wsl_version",
+    "wsl_rmsnorm_fwd",
+    "wsl_qk_norm_rope_fwd",
+    "wsl_decode_attention_fwd",
+    "wsl_swiglu_fwd",
+    "wsl_decode_last_error",
 )
 
 _lib = None
@@ -67,6 +72,23 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, ctypes.c_size_t,          # workspace, bytes
         _c_vp,                           # stream
     ]
+    lib.wsl_decode_last_error.restype = ctypes.c_char_p
+    lib.wsl_decode_last_error.argtypes = []
+    lib.wsl_rmsnorm_fwd.restype = ctypes.c_int
+    lib.wsl_rmsnorm_fwd.argtypes = [
+        _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, ctypes.c_float,  # x, ldx, residual, ldr, weight, eps
+        _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]   # out, ldo, h_out, ldh, rows, dim, stream
+    lib.wsl_qk_norm_rope_fwd.restype = ctypes.c_int
+    lib.wsl_qk_norm_rope_fwd.argtypes = [
+        _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,        # qkv, ldqkv, batch, n_heads, n_kv, head_dim
+        _c_vp, _c_vp, ctypes.c_float, _c_vp, _c_vp,          # q_norm_w, k_norm_w, eps, rope, pos
+        _c_vp, _c_vp, _c_vp, _c_i64, _c_vp]                  # q_out, k_cache, v_cache, cache_len, stream
+    lib.wsl_decode_attention_fwd.restype = ctypes.c_int
+    lib.wsl_decode_attention_fwd.argtypes = [
+        _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # q, k, v, batch, nh, nkv, hd, cache_len
+        _c_vp, ctypes.c_float, _c_vp, _c_vp]                         # pos, scale, out, stream
+    lib.wsl_swiglu_fwd.restype = ctypes.c_int
+    lib.wsl_swiglu_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]
     lib.wsl_factorized_embedding_fwd.restype = ctypes.c_int
     lib.wsl_factorized_embedding_fwd.argtypes = [
         _c_vp, _c_i64,                   # ids, n_ids
@@ -98,11 +120,16 @@ def last_error() -> str:
     return lib().wsl_last_error().decode("utf-8", "replace")
 
 
-def check(rc: int, what: str) -> None:
-    """Maps a WSL_E_* code to the matching Python exception."""
+def decode_last_error() -> str:
+    return lib().wsl_decode_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int, what: str, decode: bool = False) -> None:
+    """Maps a WSL_E_* code to the matching Python exception (decode=True: the error text of
+    the decode-step entry points)."""
     if rc == WSL_OK:
         return
-    msg = f"{what}: {last_error()} (code {rc})"
+    msg = f"{what}: {decode_last_error() if decode else last_error()} (code {rc})"
     if rc in (WSL_E_INVALID_ARG, WSL_E_SHAPE, WSL_E_ALIGN):
         raise ValueError(msg)
     if rc == WSL_E_DTYPE:

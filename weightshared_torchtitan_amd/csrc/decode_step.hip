@@ -1,0 +1,422 @@
+// Decode-step kernels of the weight-shared Qwen3 harness for gfx950: the work between
+// the fused LoRA projections of one token step, each as one launch.
+//
+//   rmsnorm_kernel        h = x (+ residual, rounded to bf16); out = bf16(h * rsqrt(mean(h^2)
+//                         + eps) * w). One workgroup per row.
+//   qk_rope_kernel        per head of the step's q|k|v row: RMSNorm over head_dim (q, k),
+//                         rotary embedding at the step's position, q written out, k and v
+//                         written into the KV cache at that position. One wave per head.
+//   attention_kernel      GQA attention of one query token against positions 0..pos of the
+//                         cache: one workgroup per (sequence, kv head), 16-lane groups per
+//                         position, online softmax, groups combined through LDS.
+//   swiglu_kernel         out = bf16(silu(g) * u) from the gate|up projection output.
+//
+// Arithmetic is fp32 with one rounding to bf16 per output (the torch ops they replace
+// round after every op). Reference semantics: RMSNorm torchtitan/models/llama3/model/
+// model.py (nn.RMSNorm in Qwen3 blocks, torchtitan/experiments/qwen3/model/model.py:
+// 195-198, 296-314), RoPE :20-36,73-90, GQA attention :167-218, SwiGLU :250-251.
+#include "../../include/wsl_decode.h"
+#include "wsl_common.h"
+
+namespace wsl {
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t h) { return bf16_bits_to_f32(h); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// --------------------------------------------------------------------- RMSNorm
+constexpr int RN_T = 256;     // threads per row
+constexpr int RN_MAXC = 4;    // 16-byte chunks per thread: dim <= 256 * 8 * 4 = 8192
+
+__global__ void __launch_bounds__(RN_T) rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                      const uint16_t* __restrict__ res, int64_t ldr,
+                                                      const uint16_t* __restrict__ w, float eps,
+                                                      uint16_t* __restrict__ out, int64_t ldo,
+                                                      uint16_t* __restrict__ hout, int64_t ldh, int dim) {
+  __shared__ float part[RN_T / 64];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nch = dim >> 3;
+  float h[RN_MAXC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < RN_MAXC; ++c) {
+    const int ch = tid + c * RN_T;
+    if (ch < nch) {
+      const u32x4_t xv = ld_global_16(x + (int64_t)row * ldx + ch * 8);
+      u32x4_t rv = zero_u32x4();
+      if (res != nullptr) rv = ld_global_16(res + (int64_t)row * ldr + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = bf(xv[e >> 1] >> ((e & 1) * 16) & 0xffffu);
+        if (res != nullptr) v = bf(f32_to_bf16_bits(v + bf(rv[e >> 1] >> ((e & 1) * 16) & 0xffffu)));
+        h[c][e] = v;
+        ss += v * v;
+      }
+      if (hout != nullptr) {
+        u32x4_t hv;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) hv[q] = pack_bf16x2(h[c][2 * q], h[c][2 * q + 1]);
+        *reinterpret_cast<u32x4_t*>(hout + (int64_t)row * ldh + ch * 8) = hv;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < RN_T / 64; ++i) tot += part[i];
+  const float inv = rsqrtf(tot / (float)dim + eps);
+#pragma unroll
+  for (int c = 0; c < RN_MAXC; ++c) {
+    const int ch = tid + c * RN_T;
+    if (ch < nch) {
+      const u32x4_t wv = ld_global_16(w + ch * 8);
+      u32x4_t ov;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        ov[q] = pack_bf16x2(h[c][2 * q] * inv * bf(wv[q] & 0xffffu), h[c][2 * q + 1] * inv * bf(wv[q] >> 16));
+      *reinterpret_cast<u32x4_t*>(out + (int64_t)row * ldo + ch * 8) = ov;
+    }
+  }
+}
+
+// --------------------------------------------------------------------- q/k norm + RoPE + cache
+// Lane l of a head's wave holds elements l + 64c, c < C (head_dim = 64 C). The rotation
+// pairs element j with j + hd/2: the same lane's chunk c + C/2 when C >= 2, lane l ^ 32
+// when C == 1.
+template <int C>
+__global__ void __launch_bounds__(256) qk_rope_kernel(const uint16_t* __restrict__ qkv, int64_t ldq, int batch,
+                                                     int nh, int nkv, const uint16_t* __restrict__ qw,
+                                                     const uint16_t* __restrict__ kw, float eps,
+                                                     const float* __restrict__ rope, const int64_t* __restrict__ posp,
+                                                     uint16_t* __restrict__ qout, uint16_t* __restrict__ kc,
+                                                     uint16_t* __restrict__ vc, int cache_len) {
+  constexpr int HD = 64 * C;
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);  // (sequence, head) of this wave
+  const int heads = nh + nkv;
+  if (gw >= batch * heads) return;
+  const int b = gw / heads, hh = gw % heads;
+  const bool is_q = hh < nh;
+  const int64_t pos = *posp;
+  const uint16_t* src = qkv + (int64_t)b * ldq + (int64_t)hh * HD;
+  const uint16_t* nw = is_q ? qw : kw;
+  float v[C];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    v[c] = bf(src[lane + 64 * c]);
+    ss += v[c] * v[c];
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)HD + eps);
+  float n[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) n[c] = v[c] * inv * bf(nw[lane + 64 * c]);
+  // rope table row `pos`: cos in [0, HD), sin in [HD, 2 HD)
+  const float* rc = rope + pos * 2 * HD;
+  float o[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int j = lane + 64 * c;
+    float partner;
+    if constexpr (C == 1) {
+      partner = __shfl_xor(n[0], 32, 64);
+    } else {
+      partner = n[(c + C / 2) % C];
+    }
+    const float rot = (j < HD / 2) ? -partner : partner;  // rotate_half
+    o[c] = n[c] * rc[j] + rot * rc[HD + j];
+  }
+  if (is_q) {
+    uint16_t* dst = qout + ((int64_t)b * nh + hh) * HD;
+#pragma unroll
+    for (int c = 0; c < C; ++c) dst[lane + 64 * c] = f32_to_bf16_bits(o[c]);
+  } else {
+    const int kh = hh - nh;
+    const int64_t base = (((int64_t)b * nkv + kh) * cache_len + pos) * HD;
+    const uint16_t* vsrc = qkv + (int64_t)b * ldq + (int64_t)(nh + nkv + kh) * HD;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      kc[base + lane + 64 * c] = f32_to_bf16_bits(o[c]);
+      vc[base + lane + 64 * c] = vsrc[lane + 64 * c];
+    }
+  }
+}
+
+// --------------------------------------------------------------------- decode attention
+constexpr int AT_T = 512;              // 8 waves = 32 groups of 16 lanes
+constexpr int AT_G = AT_T / 16;
+constexpr int AT_U = 4;                // positions in flight per group
+
+// EPL (4 or 8) consecutive bf16 of a row as one 8- or 16-byte load.
+template <int EPL> struct Vec;
+template <> struct Vec<8> {
+  u32x4_t v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = ld_global_16(p); }
+  __device__ __forceinline__ float at(int e) const { return bf((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu); }
+};
+template <> struct Vec<4> {
+  uint2 v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint2*>(p); }
+  __device__ __forceinline__ float at(int e) const {
+    const uint32_t w = (e >> 1) ? v.y : v.x;
+    return bf((w >> ((e & 1) * 16)) & 0xffffu);
+  }
+};
+
+// EPL head_dim elements per lane (head_dim = 16 EPL), REP query heads per kv head.
+template <int EPL, int REP>
+__global__ void __launch_bounds__(AT_T) attention_kernel(const uint16_t* __restrict__ q,
+                                                        const uint16_t* __restrict__ kc,
+                                                        const uint16_t* __restrict__ vc, int nh, int nkv,
+                                                        int cache_len, const int64_t* __restrict__ posp,
+                                                        float scale, uint16_t* __restrict__ out) {
+  constexpr int HD = 16 * EPL;
+  extern __shared__ __attribute__((aligned(16))) float at_smem[];
+  float* s_m = at_smem;                       // [G][REP]
+  float* s_l = s_m + AT_G * REP;              // [G][REP]
+  float* s_acc = s_l + AT_G * REP;            // [G][REP][HD]
+  const int pair = blockIdx.x;                // b * nkv + kvh
+  const int b = pair / nkv, kvh = pair % nkv;
+  const int tid = threadIdx.x;
+  const int g = tid >> 4, l16 = tid & 15;
+  const int L = (int)(*posp) + 1;
+  // q slice of the REP heads sharing this kv head
+  float qv[REP][EPL];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    const uint16_t* qr = q + ((int64_t)b * nh + kvh * REP + h) * HD + l16 * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[h][e] = bf(qr[e]) * scale;
+  }
+  float m[REP], lsum[REP], acc[REP][EPL];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    m[h] = -INFINITY;
+    lsum[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[h][e] = 0.f;
+  }
+  const uint16_t* kbase = kc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  const uint16_t* vbase = vc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  for (int t0 = g; t0 < L; t0 += AT_G * AT_U) {
+    Vec<EPL> kv[AT_U], vv[AT_U];
+#pragma unroll
+    for (int u = 0; u < AT_U; ++u) {
+      const int t = min(t0 + u * AT_G, L - 1);
+      kv[u].load(kbase + (int64_t)t * HD);
+      vv[u].load(vbase + (int64_t)t * HD);
+    }
+#pragma unroll
+    for (int u = 0; u < AT_U; ++u) {
+      const int t = t0 + u * AT_G;
+      if (t >= L) break;
+#pragma unroll
+      for (int h = 0; h < REP; ++h) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) s += qv[h][e] * kv[u].at(e);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
+        const float mn = fmaxf(m[h], s);
+        const float corr = __expf(m[h] - mn);
+        const float p = __expf(s - mn);
+        lsum[h] = lsum[h] * corr + p;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[h][e] = acc[h][e] * corr + p * vv[u].at(e);
+        m[h] = mn;
+      }
+    }
+  }
+  // combine the groups
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    if (l16 == 0) {
+      s_m[g * REP + h] = m[h];
+      s_l[g * REP + h] = lsum[h];
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s_acc[(g * REP + h) * HD + l16 * EPL + e] = acc[h][e];
+  }
+  __syncthreads();
+  for (int q2 = tid; q2 < REP * HD; q2 += AT_T) {
+    const int h = q2 / HD, d = q2 % HD;
+    float mx = -INFINITY;
+    for (int gg = 0; gg < AT_G; ++gg) mx = fmaxf(mx, s_m[gg * REP + h]);
+    float num = 0.f, den = 0.f;
+    for (int gg = 0; gg < AT_G; ++gg) {
+      const float mg = s_m[gg * REP + h];
+      if (mg == -INFINITY) continue;  // a group that saw no position
+      const float f = __expf(mg - mx);
+      num += f * s_acc[(gg * REP + h) * HD + d];
+      den += f * s_l[gg * REP + h];
+    }
+    out[((int64_t)b * nh + kvh * REP + h) * HD + d] = f32_to_bf16_bits(num / den);
+  }
+}
+
+// --------------------------------------------------------------------- SwiGLU
+__global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t* __restrict__ gu, int64_t ld, int ffn,
+                                                    uint16_t* __restrict__ out, int64_t ldo) {
+  const int row = blockIdx.y;
+  const int ch = blockIdx.x * 256 + threadIdx.x;  // 8-element chunk
+  if (ch * 8 >= ffn) return;
+  const u32x4_t gv = ld_global_16(gu + (int64_t)row * ld + ch * 8);
+  const u32x4_t uv = ld_global_16(gu + (int64_t)row * ld + ffn + ch * 8);
+  u32x4_t ov;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float r[2];
+#pragma unroll
+    for (int hlf = 0; hlf < 2; ++hlf) {
+      const float gg = bf((gv[q] >> (16 * hlf)) & 0xffffu);
+      const float uu = bf((uv[q] >> (16 * hlf)) & 0xffffu);
+      r[hlf] = gg / (1.f + __expf(-gg)) * uu;
+    }
+    ov[q] = pack_bf16x2(r[0], r[1]);
+  }
+  *reinterpret_cast<u32x4_t*>(out + (int64_t)row * ldo + ch * 8) = ov;
+}
+
+bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int EPL, int R>
+hipError_t launch_attention_r(dim3 grid, size_t smem, hipStream_t st, const uint16_t* q, const uint16_t* kc,
+                              const uint16_t* vc, int nh, int nkv, int cache_len, const int64_t* pos, float scale,
+                              uint16_t* out) {
+  static bool ready = false;  // the combine buffer exceeds the default 64 KB for large REP
+  if (!ready) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<EPL, R>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    ready = true;
+  }
+  attention_kernel<EPL, R><<<grid, dim3(AT_T), smem, st>>>(q, kc, vc, nh, nkv, cache_len, pos, scale, out);
+  return hipGetLastError();
+}
+
+template <int EPL>
+hipError_t launch_attention(int rep, dim3 grid, size_t smem, hipStream_t st, const uint16_t* q,
+                            const uint16_t* kc, const uint16_t* vc, int nh, int nkv, int cache_len,
+                            const int64_t* pos, float scale, uint16_t* out) {
+  switch (rep) {
+#define WSL_AT(R) \
+  case R: return launch_attention_r<EPL, R>(grid, smem, st, q, kc, vc, nh, nkv, cache_len, pos, scale, out);
+    WSL_AT(1) WSL_AT(2) WSL_AT(4) WSL_AT(8)
+#undef WSL_AT
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+}  // namespace wsl
+
+using namespace wsl;
+
+namespace {
+thread_local char g_derr[256] = {0};
+int dfail(int code, const char* msg) {
+  snprintf(g_derr, sizeof(g_derr), "%s", msg);
+  return code;
+}
+}  // namespace
+
+extern "C" {
+
+const char* wsl_decode_last_error(void) { return g_derr; }
+
+int wsl_rmsnorm_fwd(const void* x, int64_t ldx, const void* residual, int64_t ldr, const void* weight,
+                    float eps, void* out, int64_t ldo, void* h_out, int64_t ldh, int64_t rows, int64_t dim,
+                    void* stream) {
+  g_derr[0] = 0;
+  if (rows < 0 || dim < 8 || dim % 8 != 0 || dim > RN_T * 8 * RN_MAXC)
+    return dfail(WSL_E_SHAPE, "rmsnorm: dim must be a multiple of 8 in [8, 8192], rows >= 0");
+  if (rows == 0) return WSL_OK;
+  if (x == nullptr || weight == nullptr || out == nullptr) return dfail(WSL_E_INVALID_ARG, "rmsnorm: null pointer");
+  if (ldx < dim || ldo < dim || (residual != nullptr && ldr < dim) || (h_out != nullptr && ldh < dim))
+    return dfail(WSL_E_SHAPE, "rmsnorm: leading dimension below dim");
+  if (!a16(x) || !a16(weight) || !a16(out) || (residual != nullptr && !a16(residual)) ||
+      (h_out != nullptr && !a16(h_out)) || ldx % 8 || ldo % 8 || (residual != nullptr && ldr % 8) ||
+      (h_out != nullptr && ldh % 8))
+    return dfail(WSL_E_ALIGN, "rmsnorm: pointers must be 16-byte aligned, leading dims multiples of 8");
+  rmsnorm_kernel<<<dim3((unsigned)rows), dim3(RN_T), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      (const uint16_t*)x, ldx, (const uint16_t*)residual, ldr, (const uint16_t*)weight, eps, (uint16_t*)out,
+      ldo, (uint16_t*)h_out, ldh, (int)dim);
+  return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "rmsnorm: launch failed");
+}
+
+int wsl_qk_norm_rope_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                         int64_t head_dim, const void* q_norm_w, const void* k_norm_w, float eps,
+                         const float* rope, const int64_t* pos, void* q_out, void* k_cache, void* v_cache,
+                         int64_t cache_len, void* stream) {
+  g_derr[0] = 0;
+  if (batch < 0 || n_heads < 1 || n_kv_heads < 1 || cache_len < 1)
+    return dfail(WSL_E_SHAPE, "qk_norm_rope: bad sizes");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return dfail(WSL_E_SHAPE, "qk_norm_rope: head_dim must be 64, 128 or 256");
+  if (ldqkv < (n_heads + 2 * n_kv_heads) * head_dim) return dfail(WSL_E_SHAPE, "qk_norm_rope: ldqkv too small");
+  if (batch == 0) return WSL_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !rope || !pos || !q_out || !k_cache || !v_cache)
+    return dfail(WSL_E_INVALID_ARG, "qk_norm_rope: null pointer");
+  const int64_t waves = batch * (n_heads + n_kv_heads);
+  dim3 grid((unsigned)((waves + 3) / 4));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define WSL_QK(CC)                                                                                             \
+  qk_rope_kernel<CC><<<grid, dim3(256), 0, st>>>((const uint16_t*)qkv, ldqkv, (int)batch, (int)n_heads,     \
+                                                 (int)n_kv_heads, (const uint16_t*)q_norm_w,                 \
+                                                 (const uint16_t*)k_norm_w, eps, rope, pos, (uint16_t*)q_out, \
+                                                 (uint16_t*)k_cache, (uint16_t*)v_cache, (int)cache_len)
+  if (head_dim == 64) WSL_QK(1);
+  else if (head_dim == 128) WSL_QK(2);
+  else WSL_QK(4);
+#undef WSL_QK
+  return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "qk_norm_rope: launch failed");
+}
+
+int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_cache, int64_t batch,
+                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t cache_len,
+                             const int64_t* pos, float scale, void* out, void* stream) {
+  g_derr[0] = 0;
+  if (batch < 0 || n_kv_heads < 1 || n_heads % n_kv_heads != 0 || cache_len < 1)
+    return dfail(WSL_E_SHAPE, "decode_attention: bad sizes");
+  const int64_t rep = n_heads / n_kv_heads;
+  if (rep != 1 && rep != 2 && rep != 4 && rep != 8)
+    return dfail(WSL_E_SHAPE, "decode_attention: n_heads / n_kv_heads must be 1, 2, 4 or 8");
+  if (head_dim != 64 && head_dim != 128) return dfail(WSL_E_SHAPE, "decode_attention: head_dim must be 64 or 128");
+  if (batch == 0) return WSL_OK;
+  if (!q || !k_cache || !v_cache || !pos || !out) return dfail(WSL_E_INVALID_ARG, "decode_attention: null pointer");
+  const size_t smem = (size_t)AT_G * rep * (2 + head_dim) * sizeof(float);
+  dim3 grid((unsigned)(batch * n_kv_heads));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = head_dim == 64
+                     ? launch_attention<4>((int)rep, grid, smem, st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                                           (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads,
+                                           (int)cache_len, pos, scale, (uint16_t*)out)
+                     : launch_attention<8>((int)rep, grid, smem, st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                                           (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads,
+                                           (int)cache_len, pos, scale, (uint16_t*)out);
+  return e == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "decode_attention: launch failed");
+}
+
+int wsl_swiglu_fwd(const void* gate_up, int64_t ld, int64_t rows, int64_t ffn, void* out, int64_t ldo,
+                   void* stream) {
+  g_derr[0] = 0;
+  if (rows < 0 || ffn < 8 || ffn % 8 != 0 || ld < 2 * ffn || ldo < ffn) return dfail(WSL_E_SHAPE, "swiglu: bad sizes");
+  if (rows == 0) return WSL_OK;
+  if (!gate_up || !out) return dfail(WSL_E_INVALID_ARG, "swiglu: null pointer");
+  if (!a16(gate_up) || !a16(out) || ld % 8 || ldo % 8) return dfail(WSL_E_ALIGN, "swiglu: 16-byte alignment required");
+  dim3 grid((unsigned)((ffn / 8 + 255) / 256), (unsigned)rows);
+  swiglu_kernel<<<grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>((const uint16_t*)gate_up, ld, (int)ffn,
+                                                                               (uint16_t*)out, ldo);
+  return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "swiglu: launch failed");
+}
+
+}  // extern "C"

@@ -195,3 +195,132 @@ def lora_linear(x: torch.Tensor, w: Optional[torch.Tensor], a: Optional[torch.Te
 
 def factorized_embedding(ids: torch.Tensor, emb: torch.Tensor, proj: torch.Tensor) -> torch.Tensor:
     return factorized_embedding_op(ids, emb, proj)
+
+
+# ------------------------------------------------------------------------------------------
+# Decode-step ops of the weight-shared Qwen3 harness (include/wsl_decode.h). GPU only.
+# ------------------------------------------------------------------------------------------
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _bf16_2d(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    t = t.reshape(-1, t.shape[-1])
+    if t.stride(-1) != 1 or t.stride(0) % 8 != 0 or t.data_ptr() % 16 != 0:
+        t = t.contiguous()
+    return t
+
+
+def _rmsnorm_launch(x, weight, eps, residual):
+    dev = _check_device(x, weight, residual)
+    dim = x.shape[-1]
+    x2 = _bf16_2d(x, "x")
+    r2 = _bf16_2d(residual, "residual") if residual is not None else None
+    w = weight.to(torch.bfloat16).contiguous()
+    out = torch.empty((x2.shape[0], dim), dtype=torch.bfloat16, device=dev)
+    h = torch.empty_like(out) if residual is not None else None
+    with torch.cuda.device(dev):
+        rc = _native.lib().wsl_rmsnorm_fwd(
+            x2.data_ptr(), x2.stride(0), _dev_ptr(r2), r2.stride(0) if r2 is not None else 0,
+            w.data_ptr(), float(eps), out.data_ptr(), out.stride(0),
+            _dev_ptr(h), h.stride(0) if h is not None else 0, x2.shape[0], dim, _stream(dev))
+    _native.check(rc, "wsl_rmsnorm_fwd", decode=True)
+    return out.view(x.shape), (h.view(x.shape) if h is not None else None)
+
+
+@torch.library.custom_op("wsl::rmsnorm", mutates_args=(), device_types="cuda")
+def rmsnorm_op(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm(x) * weight over the last dimension (bf16 in/out, fp32 arithmetic)."""
+    return _rmsnorm_launch(x, weight, eps, None)[0]
+
+
+@rmsnorm_op.register_fake
+def _rmsnorm_fake(x, weight, eps):
+    return x.new_empty(x.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wsl::add_rmsnorm", mutates_args=(), device_types="cuda")
+def add_rmsnorm_op(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                   eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(RMSNorm(h) * weight, h) with h = bf16(x + residual): the residual add of a block and
+    the next norm in one launch."""
+    return _rmsnorm_launch(x, weight, eps, residual)
+
+
+@add_rmsnorm_op.register_fake
+def _add_rmsnorm_fake(x, residual, weight, eps):
+    return x.new_empty(x.shape, dtype=torch.bfloat16), x.new_empty(x.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wsl::qk_norm_rope", mutates_args=("k_cache", "v_cache"), device_types="cuda")
+def qk_norm_rope_op(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, eps: float,
+                    rope: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    n_heads: int, n_kv_heads: int) -> torch.Tensor:
+    """q [b, n_heads, hd] after q-norm + RoPE; k (normed, rotated) and v written into the
+    caches [b, n_kv_heads, L, hd] at position `pos`."""
+    dev = _check_device(qkv, q_norm_w, k_norm_w, rope, pos, k_cache, v_cache)
+    b, _, L, hd = k_cache.shape
+    q2 = _bf16_2d(qkv, "qkv")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache and v_cache must be contiguous [b, n_kv_heads, L, head_dim]")
+    qw = q_norm_w.to(torch.bfloat16).contiguous()
+    kw = k_norm_w.to(torch.bfloat16).contiguous()
+    rope = rope.float().contiguous()
+    pos = pos.to(torch.int64).contiguous()
+    q = torch.empty((b, n_heads, hd), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        rc = _native.lib().wsl_qk_norm_rope_fwd(
+            q2.data_ptr(), q2.stride(0), b, n_heads, n_kv_heads, hd, qw.data_ptr(), kw.data_ptr(), float(eps),
+            rope.data_ptr(), pos.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), L, _stream(dev))
+    _native.check(rc, "wsl_qk_norm_rope_fwd", decode=True)
+    return q
+
+
+@qk_norm_rope_op.register_fake
+def _qk_norm_rope_fake(qkv, q_norm_w, k_norm_w, eps, rope, pos, k_cache, v_cache, n_heads, n_kv_heads):
+    return qkv.new_empty((k_cache.shape[0], n_heads, k_cache.shape[3]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wsl::decode_attention", mutates_args=(), device_types="cuda")
+def decode_attention_op(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                        scale: float) -> torch.Tensor:
+    """softmax(q . K^T * scale) . V over cache positions 0..pos; q [b, n_heads, hd],
+    caches [b, n_kv_heads, L, hd] -> [b, n_heads * hd]."""
+    dev = _check_device(q, k_cache, v_cache, pos)
+    b, nh, hd = q.shape
+    nkv, L = k_cache.shape[1], k_cache.shape[2]
+    q = q.contiguous()
+    pos = pos.to(torch.int64).contiguous()
+    out = torch.empty((b, nh * hd), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        rc = _native.lib().wsl_decode_attention_fwd(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), b, nh, nkv, hd, L, pos.data_ptr(),
+            float(scale), out.data_ptr(), _stream(dev))
+    _native.check(rc, "wsl_decode_attention_fwd", decode=True)
+    return out
+
+
+@decode_attention_op.register_fake
+def _decode_attention_fake(q, k_cache, v_cache, pos, scale):
+    return q.new_empty((q.shape[0], q.shape[1] * q.shape[2]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wsl::swiglu", mutates_args=(), device_types="cuda")
+def swiglu_op(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(g) * u for gate_up = [g | u] along the last dimension."""
+    dev = _check_device(gate_up)
+    ffn = gate_up.shape[-1] // 2
+    g2 = _bf16_2d(gate_up, "gate_up")
+    out = torch.empty((g2.shape[0], ffn), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        rc = _native.lib().wsl_swiglu_fwd(g2.data_ptr(), g2.stride(0), g2.shape[0], ffn, out.data_ptr(),
+                                          out.stride(0), _stream(dev))
+    _native.check(rc, "wsl_swiglu_fwd", decode=True)
+    return out.view(*gate_up.shape[:-1], ffn)
+
+
+@swiglu_op.register_fake
+def _swiglu_fake(gate_up):
+    return gate_up.new_empty((*gate_up.shape[:-1], gate_up.shape[-1] // 2), dtype=torch.bfloat16)

@@ -154,10 +154,11 @@ class FactorizedEmbedding(nn.Module):
 
 
 class KVCache:
-    """Per-layer K (stored transposed, [b, kv_heads, head_dim, L]) and V ([b, kv_heads, L, head_dim])."""
+    """Per-layer K and V, each [n_layers, b, kv_heads, max_len, head_dim] (one position's
+    head_dim vector contiguous, as the decode attention kernel streams them)."""
 
     def __init__(self, a: SharedQwen3Args, batch: int, max_len: int, device, dtype=torch.bfloat16):
-        self.k_t = torch.zeros(a.n_layers, batch, a.n_kv_heads, a.head_dim, max_len, device=device, dtype=dtype)
+        self.k = torch.zeros(a.n_layers, batch, a.n_kv_heads, max_len, a.head_dim, device=device, dtype=dtype)
         self.v = torch.zeros(a.n_layers, batch, a.n_kv_heads, max_len, a.head_dim, device=device, dtype=dtype)
         self.max_len = max_len
 
@@ -237,7 +238,7 @@ class SharedQwen3(nn.Module):
             xq = self._rope(blk.attention.q_norm(xq), rc)
             xk = self._rope(blk.attention.k_norm(xk), rc)
             if cache is not None:
-                cache.k_t[l, :, :, :, :s] = xk.permute(0, 2, 3, 1)
+                cache.k[l, :, :, :s] = xk.transpose(1, 2)
                 cache.v[l, :, :, :s] = xv.transpose(1, 2)
             kk = xk.repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
             vv = xv.repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
@@ -250,36 +251,84 @@ class SharedQwen3(nn.Module):
         return self.tok_embeddings.tied_logits(h)
 
     # ------------------------------------------------------------------ decode
+    def _decode_pack(self) -> dict:
+        """Concatenated operands for the decode step's fused q|k|v and gate|up projections.
+
+        [W_q; W_k; W_v] (per unique block) with per-layer [A_q; A_k; A_v] and the
+        block-diagonal [B_q, 0, 0; 0, B_k, 0; 0, 0, B_v] give exactly the three LoRA linears
+        (each output row meets only its own rank block; the zero blocks add exact zeros), in
+        one launch that streams all three weights; likewise [W_1; W_3] for gate|up. Rebuilt
+        when any parameter changes."""
+        key = tuple((p.data_ptr(), p._version) for p in self.parameters())
+        pk = getattr(self, "_pack_cache", None)
+        if pk is not None and pk["key"] == key:
+            return pk
+        a = self.args
+
+        def cat_w(blk, names):
+            return torch.cat([blk.base(n).weight for n in names], 0).contiguous()
+
+        def cat_lora(layer, names):
+            mods = [getattr(self.layer_loras[layer], n) for n in names]
+            scales = {m.scale for m in mods}
+            if len(scales) != 1:
+                return None
+            A = torch.cat([m.w_a.weight for m in mods], 0).contiguous()
+            rows = sum(m.w_b.weight.shape[0] for m in mods)
+            ranks = sum(m.w_b.weight.shape[1] for m in mods)
+            B = mods[0].w_b.weight.new_zeros(rows, ranks)
+            r0 = c0 = 0
+            for m in mods:
+                n, r = m.w_b.weight.shape
+                B[r0:r0 + n, c0:c0 + r] = m.w_b.weight
+                r0, c0 = r0 + n, c0 + r
+            return A, B, scales.pop()
+
+        with torch.no_grad():
+            pk = {"key": key,
+                  "w_qkv": [cat_w(blk, ("wq", "wk", "wv")) for blk in self.base_blocks],
+                  "w_gu": [cat_w(blk, ("w1", "w3")) for blk in self.base_blocks],
+                  "l_qkv": [cat_lora(l, ("wq", "wk", "wv")) for l in range(a.n_layers)],
+                  "l_gu": [cat_lora(l, ("w1", "w3")) for l in range(a.n_layers)]}
+        self._pack_cache = pk
+        return pk
+
+    def _proj_group(self, layer: int, group: str, names, x: torch.Tensor, pk: dict) -> torch.Tensor:
+        lo = pk["l_" + group][layer]
+        if lo is None:  # adapters with different scales: one call per projection
+            return torch.cat([self._proj(layer, n, x) for n in names], -1)
+        w = pk["w_" + group][self.args.block_of(layer)]
+        A, B, sc = lo
+        return ops.lora_linear(x, w, A, B, sc)
+
     def decode_step(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
         """One greedy step at position `pos` (0-d int64 device tensor) -> logits [b, vocab].
-        Shape-static and host-sync-free, so it can be captured in a HIP graph."""
+        Shape-static and host-sync-free, so it can be captured in a HIP graph. Per layer:
+        residual add + RMSNorm, fused q|k|v projection, q/k norm + RoPE + cache write,
+        decode attention, o projection, residual add + RMSNorm, fused gate|up projection,
+        SwiGLU, down projection (its residual add joins the next layer's norm)."""
         a = self.args
         b = token.shape[0]
-        L = cache.max_len
-        rep = a.n_heads // a.n_kv_heads
-        h = self.tok_embeddings(token.view(b, 1))  # [b, 1, dim]
-        rc = self.rope.index_select(0, pos.view(1)).view(1, 1, 1, 2 * a.head_dim)
-        masked = (torch.arange(L, device=token.device) > pos).view(1, 1, 1, L)
+        pk = self._decode_pack()
+        h = self.tok_embeddings(token.view(b)).view(b, a.dim)
         sm_scale = a.head_dim ** -0.5
+        pending = None
         for l in range(a.n_layers):
             blk = self.base_blocks[a.block_of(l)]
-            x = blk.attention_norm(h)
-            xq = self._proj(l, "wq", x).view(b, 1, a.n_heads, a.head_dim)
-            xk = self._proj(l, "wk", x).view(b, 1, a.n_kv_heads, a.head_dim)
-            xv = self._proj(l, "wv", x).view(b, 1, a.n_kv_heads, a.head_dim)
-            xq = self._rope(blk.attention.q_norm(xq), rc)
-            xk = self._rope(blk.attention.k_norm(xk), rc)
-            cache.k_t[l].index_copy_(3, pos.view(1), xk.view(b, a.n_kv_heads, a.head_dim, 1))
-            cache.v[l].index_copy_(2, pos.view(1), xv.view(b, a.n_kv_heads, 1, a.head_dim))
-            q = xq.view(b, a.n_kv_heads, rep, a.head_dim)
-            scores = torch.matmul(q, cache.k_t[l]).float() * sm_scale  # [b, kv, rep, L]
-            scores = scores.masked_fill(masked, float("-inf"))
-            probs = torch.softmax(scores, dim=-1).to(cache.v.dtype)
-            o = torch.matmul(probs, cache.v[l])  # [b, kv, rep, hd]
-            h = h + self._proj(l, "wo", o.reshape(b, 1, a.n_heads * a.head_dim))
-            h = self._ffn(l, h)
-        h = self.norm(h)
-        return self.tok_embeddings.tied_logits(h).view(b, -1)
+            if pending is None:
+                x = ops.rmsnorm_op(h, blk.attention_norm.weight, a.norm_eps)
+            else:
+                x, h = ops.add_rmsnorm_op(pending, h, blk.attention_norm.weight, a.norm_eps)
+            qkv = self._proj_group(l, "qkv", ("wq", "wk", "wv"), x, pk)
+            q = ops.qk_norm_rope_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight, a.norm_eps,
+                                    self.rope, pos, cache.k[l], cache.v[l], a.n_heads, a.n_kv_heads)
+            o = ops.decode_attention_op(q, cache.k[l], cache.v[l], pos, sm_scale)
+            o = self._proj(l, "wo", o)
+            x, h = ops.add_rmsnorm_op(o, h, blk.ffn_norm.weight, a.norm_eps)
+            gu = self._proj_group(l, "gu", ("w1", "w3"), x, pk)
+            pending = self._proj(l, "w2", ops.swiglu_op(gu))
+        x, _ = ops.add_rmsnorm_op(pending, h, self.norm.weight, a.norm_eps)
+        return self.tok_embeddings.tied_logits(x).view(b, -1)
 
     @torch.no_grad()
     def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True):
