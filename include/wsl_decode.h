@@ -61,6 +61,12 @@ int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_c
 int wsl_swiglu_fwd(const void* gate_up, int64_t ld, int64_t rows, int64_t ffn, void* out, int64_t ldo,
                    void* stream);
 
+/* out[row] = index of the largest x[row, 0..n) (bf16): the greedy token of a row of logits
+ * (scripts/generate/_generation.py:26-29 with top_k = 1 keeps only the argmax). Ties give
+ * the first index and NaN counts as largest, as torch.argmax. Rows that are 16-byte aligned
+ * with ldx % 8 == 0 are read 16 bytes at a time. */
+int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* stream);
+
 /* Thread-local description of the last failure of an entry point above ("" if none). */
 const char* wsl_decode_last_error(void);
 

@@ -129,3 +129,19 @@ def test_grouped_projection_equals_separate_calls(gpu):
     Bbd[:2048, :32], Bbd[2048:3072, 32:64], Bbd[3072:, 64:] = Bs
     grp = wsl.lora_linear(x, torch.cat(Ws), torch.cat(As), Bbd, 2.0)
     assert rel(grp, sep) <= 1e-2
+
+
+@pytest.mark.parametrize("rows,n", [(8, 151936), (3, 1000), (2, 13)])
+def test_argmax_rows_matches_torch(gpu, rows, n):
+    from weightshared_torchtitan_amd import ops
+    _say(f"[argmax] rows={rows} n={n}")
+    g = torch.Generator(device="cuda").manual_seed(n)
+    x = torch.randn(rows, n, device=gpu, generator=g).bfloat16()
+    x[0, n // 3] = 50.0          # unique maximum
+    if rows > 1:
+        x[1, 7 % n] = 60.0       # tie: the first index wins
+        x[1, n - 1] = 60.0
+    if rows > 2:
+        x[2, n // 2] = float("nan")
+    got = ops.argmax_rows_op(x)
+    assert torch.equal(got, torch.argmax(x.float(), dim=-1))

@@ -86,6 +86,10 @@ DECODE_CASES = [
     (33, 1000, 2048, 24, 2.0, True),     # 32-row groups with an N tail, partial rank group
     (64, 1000, 6144, 24, 2.0, True),     # six-way K split with tails
     (1, 2048, 6144, 128, 1.0, True),     # one token, long K, rank 128
+    (8, 151936, 256, 0, 2.0, True),      # tied output head: short K, 2 waves per row block
+    (3, 5000, 256, 16, 2.0, True),       # short K with rank rows
+    (20, 2000, 512, 24, 2.0, True),      # 4 waves per row block
+    (64, 1000, 256, 64, 2.0, True),      # short K at the largest M
 ]
 
 

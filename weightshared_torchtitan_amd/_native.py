@@ -38,6 +38,7 @@ EXPORTED = (
     "wsl_qk_norm_rope_fwd",
     "wsl_decode_attention_fwd",
     "wsl_swiglu_fwd",
+    "wsl_argmax_rows_fwd",
     "wsl_decode_last_error",
 )
 
@@ -89,6 +90,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, ctypes.c_float, _c_vp, _c_vp]                         # pos, scale, out, stream
     lib.wsl_swiglu_fwd.restype = ctypes.c_int
     lib.wsl_swiglu_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]
+    lib.wsl_argmax_rows_fwd.restype = ctypes.c_int
+    lib.wsl_argmax_rows_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]
     lib.wsl_factorized_embedding_fwd.restype = ctypes.c_int
     lib.wsl_factorized_embedding_fwd.argtypes = [
         _c_vp, _c_i64,                   # ids, n_ids

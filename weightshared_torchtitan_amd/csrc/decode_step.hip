@@ -10,6 +10,8 @@
 //                         cache: one workgroup per (sequence, kv head), 16-lane groups per
 //                         position, online softmax, groups combined through LDS.
 //   swiglu_kernel         out = bf16(silu(g) * u) from the gate|up projection output.
+//   argmax_kernel         greedy token: index of the largest logit of a row (first index on
+//                         ties, NaN counted as largest, as torch.argmax). One workgroup per row.
 //
 // Arithmetic is fp32 with one rounding to bf16 per output (the torch ops they replace
 // round after every op). Reference semantics: RMSNorm torchtitan/models/llama3/model/
@@ -286,6 +288,54 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t* __restrict_
   *reinterpret_cast<u32x4_t*>(out + (int64_t)row * ldo + ch * 8) = ov;
 }
 
+// --------------------------------------------------------------------- argmax
+constexpr int AM_T = 1024;
+
+// (v, i) beats (w, j): NaN above every number, then the larger value, then the smaller index.
+__device__ __forceinline__ bool am_better(float v, int64_t i, float w, int64_t j) {
+  const bool vn = v != v, wn = w != w;
+  if (vn != wn) return vn;
+  if (!vn && v != w) return v > w;
+  return i < j;
+}
+
+__global__ void __launch_bounds__(AM_T) argmax_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t n,
+                                                     int vec, int64_t* __restrict__ out) {
+  __shared__ float sv[AM_T / 64];
+  __shared__ int64_t si[AM_T / 64];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* xr = x + (int64_t)row * ldx;
+  float bv = -INFINITY;
+  int64_t bi = INT64_MAX;
+  const int64_t nch = vec ? (n >> 3) : 0;  // 16-byte chunks (aligned rows only), then a scalar tail
+  for (int64_t c = tid; c < nch; c += AM_T) {
+    const u32x4_t v = ld_global_16(xr + c * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = bf((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+      if (am_better(f, c * 8 + e, bv, bi)) { bv = f; bi = c * 8 + e; }
+    }
+  }
+  for (int64_t k = nch * 8 + tid; k < n; k += AM_T) {  // tail
+    const float f = bf(xr[k]);
+    if (am_better(f, k, bv, bi)) { bv = f; bi = k; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int64_t oi = __shfl_xor(bi, o, 64);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < AM_T / 64; ++w)
+      if (am_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    out[row] = bi;
+  }
+}
+
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <int EPL, int R>
@@ -404,6 +454,18 @@ int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_c
                                            (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads,
                                            (int)cache_len, pos, scale, (uint16_t*)out);
   return e == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "decode_attention: launch failed");
+}
+
+int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* stream) {
+  g_derr[0] = 0;
+  if (rows < 0 || n < 1 || ldx < n) return dfail(WSL_E_SHAPE, "argmax: bad sizes");
+  if (rows == 0) return WSL_OK;
+  if (!x || !out) return dfail(WSL_E_INVALID_ARG, "argmax: null pointer");
+  if (((uintptr_t)x & 1) || ((uintptr_t)out & 7)) return dfail(WSL_E_ALIGN, "argmax: misaligned pointer");
+  const int vec = (a16(x) && ldx % 8 == 0) ? 1 : 0;
+  argmax_kernel<<<dim3((unsigned)rows), dim3(AM_T), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      (const uint16_t*)x, ldx, n, vec, out);
+  return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "argmax: launch failed");
 }
 
 int wsl_swiglu_fwd(const void* gate_up, int64_t ld, int64_t rows, int64_t ffn, void* out, int64_t ldo,

@@ -12,8 +12,11 @@
 // A workgroup (8 waves) stages its slice of x into LDS with direct global->LDS loads
 // (no VGPRs, XOR-swizzled rows), and its B rows likewise, while the first PD K steps of
 // its W rows are already in flight into registers. Each lane streams 64 contiguous bytes
-// of a row per step (16 rows x 4 lane groups per wave, waves interleaved over K) and
-// v_mfma_f32_16x16x32_bf16 forms the dot products. Wave sums are reduced through LDS.
+// of a row per step (16 rows x 4 lane groups per wave) and v_mfma_f32_16x16x32_bf16
+// forms the dot products. The 8 waves form 8/KW row blocks of KW waves each; the KW
+// waves of a block interleave over K and their sums are reduced through LDS (KW = 8 for
+// K of 8 or more wave steps; short K gives each wave its own rows instead, so a launch
+// over a large N and small K, like the tied output head, keeps every wave streaming).
 // The up-projection T . B^T of the epilogue is r/32 more MFMAs per 16x16 output block.
 //
 // Cross-workgroup hand-offs (T to the W workgroups; the partial sums of a K split to
@@ -188,13 +191,13 @@ struct DecodeArgs {
   uint16_t* y; int64_t ldy;
   float s;
   int M, N, K, r, r32;
-  int gT, kst, kct;   // T groups (16 rows of A), K split and slice
+  int gT, kst, kct;   // T groups (16 * 8 / KW rows of A), K split and slice
   int gY, ksy, kcy;   // W groups (16*NR rows of W), K split and slice
   int flag_off;       // LDS byte offset of the broadcast word
   unsigned* cnt;      // counter prefix of the workspace
   uint64_t* tfin;     // T [M][r]: tag << 16 | bf16 bits
-  float* tpart;       // [gT][kst][M][16]
-  float* ypart;       // [gY][ksy][M][16*NR]
+  float* tpart;       // [gT][kst][M][T rows per group]
+  float* ypart;       // [gY][ksy][M][W rows per group]
   int spin;           // polls of the T counter before the local fallback
 };
 
@@ -223,7 +226,7 @@ __device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
 // Sums over one K slice of a group of 16*NR rows of `mat` against x (whose fill into
 // smem this wave has issued just before), reduced over the waves into sums[row][m]
 // (LDS, fp32, stride 16*MB). The x slice's LDS is reused for the reduction.
-template <int WDT, int NR, int MB>
+template <int WDT, int NR, int MB, int KW>
 __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
                                            int kbeg, int kc, int M, char* smem, float* sums) {
   using G = Geo<WDT>;
@@ -234,14 +237,16 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rb = wave / KW, kw = wave % KW;  // row block of this wave, its place along K
   const int l16 = lane & 15;
   const int grp = lane >> 4;
   const int nsteps = kc / G::WAVE_K;
-  const int my = nsteps > wave ? (nsteps - wave + NWV - 1) / NWV : 0;
+  const int my = nsteps > kw ? (nsteps - kw + KW - 1) / KW : 0;
+  const int rbase = row0 + rb * 16 * NR;
 
   int64_t rowoff[NR];
 #pragma unroll
-  for (int i = 0; i < NR; ++i) rowoff[i] = (int64_t)min(row0 + i * 16 + l16, nrows - 1) * ldm;
+  for (int i = 0; i < NR; ++i) rowoff[i] = (int64_t)min(rbase + i * 16 + l16, nrows - 1) * ldm;
   int xrow[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) xrow[mb] = min(mb * 16 + l16, M - 1);
@@ -249,7 +254,7 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
   u32x4_t wv[PD][NR][4];
 #pragma unroll
   for (int q = 0; q < PD; ++q)
-    if (q < my) load_step<WDT, NR>(wv[q], mat, rowoff, kbeg + (wave + q * NWV) * G::WAVE_K + grp * G::LANE_K);
+    if (q < my) load_step<WDT, NR>(wv[q], mat, rowoff, kbeg + (kw + q * KW) * G::WAVE_K + grp * G::LANE_K);
 
   f32x4_t acc[NR][MB];
 #pragma unroll
@@ -274,39 +279,41 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
     for (int q = 0; q < PD; ++q) {
       const int i = i0 + q;
       if (i < my) {
-        const int kl = (wave + i * NWV) * G::WAVE_K + grp * G::LANE_K;
+        const int kl = (kw + i * KW) * G::WAVE_K + grp * G::LANE_K;
         mma_step<WDT, NR, MB>(wv[q], smem, kc, xrow, kl, acc);
         if (i + PD < my)
-          load_step<WDT, NR>(wv[q], mat, rowoff, kbeg + (wave + (i + PD) * NWV) * G::WAVE_K + grp * G::LANE_K);
+          load_step<WDT, NR>(wv[q], mat, rowoff, kbeg + (kw + (i + PD) * KW) * G::WAVE_K + grp * G::LANE_K);
       }
     }
   }
 
-  // Cross-wave reduction (the x slice is dead: its LDS is reused).
+  // Cross-wave reduction within each row block (the x slice is dead: its LDS is reused).
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
-  if (wave > 0) {
+  if (kw > 0) {
+    const int slot = rb * (KW - 1) + kw - 1;
 #pragma unroll
     for (int i = 0; i < NR; ++i)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          red[((wave - 1) * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane] = acc[i][mb][e];
+          red[(slot * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane] = acc[i][mb][e];
   }
   __syncthreads();
-  if (wave == 0) {
+  if (kw == 0) {
 #pragma unroll
     for (int i = 0; i < NR; ++i)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         f32x4_t v = acc[i][mb];
-        for (int w2 = 0; w2 < NWV - 1; ++w2)
+        for (int w2 = 0; w2 < KW - 1; ++w2)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += red[(w2 * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane];
-        // D[row][m]: lane holds m = l16, rows grp*4 + e of block i
+          for (int e = 0; e < 4; ++e)
+            v[e] += red[((rb * (KW - 1) + w2) * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane];
+        // D[row][m]: lane holds m = l16, rows grp*4 + e of block i of row block rb
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sums[(i * 16 + grp * 4 + e) * MC + mb * 16 + l16] = v[e];
+        for (int e = 0; e < 4; ++e) sums[(rb * 16 * NR + i * 16 + grp * 4 + e) * MC + mb * 16 + l16] = v[e];
       }
   }
   __syncthreads();
@@ -390,10 +397,12 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
   __syncthreads();
 }
 
-template <int WDT, int NR, int MB>
+template <int WDT, int NR, int MB, int KW>
 __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  constexpr int ROWS = 16 * NR;
+  constexpr int RBK = NWV / KW;         // row blocks per workgroup
+  constexpr int ROWS = RBK * 16 * NR;   // W rows per workgroup
+  constexpr int TROWS = RBK * 16;       // A rows per T workgroup
   constexpr int MC = 16 * MB;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -406,17 +415,17 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
   const uint64_t tag = (ld_agent(launch) / kLaunchUnit + 1) & kTagMask;
 
   if (bid < nT) {
-    // ---------------- T workgroup: 16 rows of A over one K slice
+    // ---------------- T workgroup: TROWS rows of A over one K slice
     const int g = bid / p.kst, ks = bid % p.kst;
     const int kbeg = ks * p.kct;
-    constexpr int RED_T = (NWV - 1) * MB * 4 * 64 * 4;
+    constexpr int RED_T = (NWV - RBK) * MB * 4 * 64 * 4;
     float* sums = reinterpret_cast<float*>(smem + RED_T);
     fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
-    slice_sums<kBF16, 1, MB>(p.a, p.lda, p.r, g * 16, kbeg, p.kct, p.M, smem, sums);
-    if (split_reduce<16, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * 16, p.cnt + CNT_TG + g, ks,
-                             p.kst, p.M, flag)) {
-      for (int q = tid; q < p.M * 16; q += DT) {
-        const int m = q >> 4, rl = q & 15, j = g * 16 + rl;
+    slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums);
+    if (split_reduce<TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, p.cnt + CNT_TG + g, ks,
+                                p.kst, p.M, flag)) {
+      for (int q = tid; q < p.M * TROWS; q += DT) {
+        const int m = q / TROWS, rl = q % TROWS, j = g * TROWS + rl;
         if (j < p.r) st_agent(p.tfin + m * p.r + j, (tag << 16) | f32_to_bf16_bits(p.s * sums[rl * MC + m]));
       }
     }
@@ -426,7 +435,7 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
     const int g = yb / p.ksy, ks = yb % p.ksy;
     const int kbeg = ks * p.kcy;
     const int row0 = g * ROWS;
-    constexpr int RED = (NWV - 1) * NR * MB * 4 * 64 * 4;
+    constexpr int RED = (NWV - RBK) * NR * MB * 4 * 64 * 4;
     const int xs_bytes = p.M * p.kcy * 2;
     const int post = RED + ROWS * MC * 4 + MC * (p.r32 + 8) * 2;
     char* bl = smem + (xs_bytes > post ? xs_bytes : post);
@@ -434,14 +443,14 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
     uint16_t* tl = reinterpret_cast<uint16_t*>(smem + RED + ROWS * MC * 4);
     fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kcy, wave, lane);
     if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
-    slice_sums<WDT, NR, MB>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
+    slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
     if (split_reduce<ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, p.cnt + CNT_YG + g, ks,
                                p.ksy, p.M, flag)) {
       if (p.r > 0) gather_t<MC>(p, tl, tag, flag);
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
       const int l16 = lane & 15, grp = lane >> 4;
       const int tls = p.r32 + 8;
-      for (int blk = wave; blk < NR * MB; blk += NWV) {
+      for (int blk = wave; blk < (ROWS / 16) * MB; blk += NWV) {
         const int i = blk / MB, mb = blk % MB;
         f32x4_t d = {0.f, 0.f, 0.f, 0.f};
         for (int j0 = 0; j0 < p.r; j0 += 32) {
@@ -498,7 +507,7 @@ int fit_split(int64_t M, int64_t K, int wave_k) {
 }
 
 struct DecodePlan {
-  int mb, nr, rows, r32;
+  int mb, nr, kw, rows, trows, r32;
   int gT, kst, kct;
   int gY, ksy, kcy;
   size_t off_t, off_pt, off_py, total;
@@ -506,68 +515,92 @@ struct DecodePlan {
   bool ok;
 };
 
+size_t plan_smem(const DecodePlan& pl, int64_t M, size_t* flag_off) {
+  // LDS: max(x slice, reduction + sums + T) + B rows, then the broadcast word.
+  const size_t xs = (size_t)M * (pl.kcy > pl.kct ? pl.kcy : pl.kct) * 2;
+  const size_t red = (size_t)(NWV - NWV / pl.kw) * pl.nr * pl.mb * 4 * 64 * 4;
+  const size_t post = red + (size_t)pl.rows * 16 * pl.mb * 4 + (size_t)16 * pl.mb * (pl.r32 + 8) * 2;
+  *flag_off = (xs > post ? xs : post) + (size_t)pl.rows * pl.r32 * 2;
+  return *flag_off + 16;
+}
+
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
   DecodePlan pl{};
   pl.mb = (int)((M + 15) / 16);
   if (pl.mb < 1) pl.mb = 1;
   pl.nr = pl.mb >= 3 ? 2 : 1;
-  pl.rows = 16 * pl.nr;
   pl.r32 = (int)((r + 31) / 32 * 32);
   pl.ksy = fit_split(M, K, wave_k_of(wdt));
   pl.kcy = pl.ksy > 0 ? (int)(K / pl.ksy) : 0;
-  pl.gY = (int)((N + pl.rows - 1) / pl.rows);
   if (r > 0) {
-    pl.gT = (int)((r + 15) / 16);
     pl.kst = fit_split(M, K, wave_k_of(kBF16));
     pl.kct = pl.kst > 0 ? (int)(K / pl.kst) : 0;
   } else {
-    pl.gT = 0;
     pl.kst = 1;
     pl.kct = (int)K;
   }
-  pl.ok = pl.ksy > 0 && pl.kst > 0 && CNT_YG + pl.gY <= kCounterWords &&
+  // Waves per row block: all 8 along K when the slice has at least 8 wave steps, else
+  // the largest power of two not above the step count (more rows per workgroup), raised
+  // again while the B rows do not fit the LDS.
+  const int steps = pl.kcy > 0 ? pl.kcy / wave_k_of(wdt) : 8;
+  pl.kw = 8;
+  while (pl.kw > 1 && pl.kw > steps) pl.kw >>= 1;
+  for (;;) {
+    pl.rows = (NWV / pl.kw) * 16 * pl.nr;
+    pl.trows = (NWV / pl.kw) * 16;
+    if (pl.kw == 8 || plan_smem(pl, M, &pl.flag_off) <= (size_t)LDS_MAX) break;
+    pl.kw <<= 1;
+  }
+  pl.gY = (int)((N + pl.rows - 1) / pl.rows);
+  pl.gT = r > 0 ? (int)((r + pl.trows - 1) / pl.trows) : 0;
+  pl.ok = pl.ksy > 0 && pl.kst > 0 && CNT_YG + pl.gY <= kCounterWords && pl.gT <= CNT_YG - CNT_TG &&
           (uint64_t)pl.gT * pl.kst + (uint64_t)pl.gY * pl.ksy < kLaunchUnit;
   size_t off = kCounterBytes;
   pl.off_t = off;
   off += (size_t)M * r * 8;
   off = (off + 255) & ~(size_t)255;
   pl.off_pt = off;
-  if (pl.kst > 1) off += (size_t)pl.gT * pl.kst * M * 16 * 4;
+  if (pl.kst > 1) off += (size_t)pl.gT * pl.kst * M * pl.trows * 4;
   off = (off + 255) & ~(size_t)255;
   pl.off_py = off;
   if (pl.ksy > 1) off += (size_t)pl.gY * pl.ksy * M * pl.rows * 4;
   pl.total = off;
-  // LDS: max(x slice, reduction + sums + T) + B rows, then the broadcast word.
-  const size_t xs = (size_t)M * (pl.kcy > pl.kct ? pl.kcy : pl.kct) * 2;
-  const size_t red = (size_t)(NWV - 1) * pl.nr * pl.mb * 4 * 64 * 4;
-  const size_t post = red + (size_t)pl.rows * 16 * pl.mb * 4 + (size_t)16 * pl.mb * (pl.r32 + 8) * 2;
-  pl.flag_off = (xs > post ? xs : post) + (size_t)pl.rows * pl.r32 * 2;
-  pl.smem = pl.flag_off + 16;
+  pl.smem = plan_smem(pl, M, &pl.flag_off);
   if (pl.smem > (size_t)LDS_MAX) pl.ok = false;
   return pl;
 }
 
-template <int WDT, int NR, int MB>
+template <int WDT, int NR, int MB, int KW>
 hipError_t launch_one(const DecodeArgs& a, int grid, size_t smem, hipStream_t st) {
   static bool ready = false;  // the attribute is per kernel; setting it twice is harmless
   if (!ready) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<WDT, NR, MB>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<WDT, NR, MB, KW>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
     if (e != hipSuccess) return e;
     ready = true;
   }
-  decode_kernel<WDT, NR, MB><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a);
+  decode_kernel<WDT, NR, MB, KW><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a);
   return hipGetLastError();
 }
 
-template <int WDT>
-hipError_t dispatch(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
+template <int WDT, int KW>
+hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
   if (nr == 1) {
-    if (mb == 1) return launch_one<WDT, 1, 1>(a, grid, smem, st);
-    return launch_one<WDT, 1, 2>(a, grid, smem, st);
+    if (mb == 1) return launch_one<WDT, 1, 1, KW>(a, grid, smem, st);
+    return launch_one<WDT, 1, 2, KW>(a, grid, smem, st);
   }
-  if (mb == 3) return launch_one<WDT, 2, 3>(a, grid, smem, st);
-  return launch_one<WDT, 2, 4>(a, grid, smem, st);
+  if (mb == 3) return launch_one<WDT, 2, 3, KW>(a, grid, smem, st);
+  return launch_one<WDT, 2, 4, KW>(a, grid, smem, st);
+}
+
+template <int WDT>
+hipError_t dispatch(const DecodeArgs& a, int mb, int nr, int kw, int grid, size_t smem, hipStream_t st) {
+  switch (kw) {
+    case 1: return dispatch_kw<WDT, 1>(a, mb, nr, grid, smem, st);
+    case 2: return dispatch_kw<WDT, 2>(a, mb, nr, grid, smem, st);
+    case 4: return dispatch_kw<WDT, 4>(a, mb, nr, grid, smem, st);
+    default: return dispatch_kw<WDT, 8>(a, mb, nr, grid, smem, st);
+  }
 }
 
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
@@ -624,8 +657,8 @@ hipError_t launch_decode(const LoraArgs& p) {
   a.ypart = reinterpret_cast<float*>(ws + pl.off_py);
   a.spin = spin_limit();
   const int grid = pl.gT * pl.kst + pl.gY * pl.ksy;
-  return p.w_dtype == kFP8 ? dispatch<kFP8>(a, pl.mb, pl.nr, grid, pl.smem, p.stream)
-                           : dispatch<kBF16>(a, pl.mb, pl.nr, grid, pl.smem, p.stream);
+  return p.w_dtype == kFP8 ? dispatch<kFP8>(a, pl.mb, pl.nr, pl.kw, grid, pl.smem, p.stream)
+                           : dispatch<kBF16>(a, pl.mb, pl.nr, pl.kw, grid, pl.smem, p.stream);
 }
 
 }  // namespace wsl

@@ -324,3 +324,25 @@ def swiglu_op(gate_up: torch.Tensor) -> torch.Tensor:
 @swiglu_op.register_fake
 def _swiglu_fake(gate_up):
     return gate_up.new_empty((*gate_up.shape[:-1], gate_up.shape[-1] // 2), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("wsl::argmax_rows", mutates_args=(), device_types="cuda")
+def argmax_rows_op(x: torch.Tensor) -> torch.Tensor:
+    """int64 index of the largest element of each row (first on ties, NaN largest)."""
+    dev = _check_device(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16, got {x.dtype}")
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    out = torch.empty(x2.shape[0], dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        rc = _native.lib().wsl_argmax_rows_fwd(x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1],
+                                               out.data_ptr(), _stream(dev))
+    _native.check(rc, "wsl_argmax_rows_fwd", decode=True)
+    return out.view(x.shape[:-1])
+
+
+@argmax_rows_op.register_fake
+def _argmax_rows_fake(x):
+    return x.new_empty(x.shape[:-1], dtype=torch.int64)

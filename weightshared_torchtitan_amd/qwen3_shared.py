@@ -293,6 +293,16 @@ class SharedQwen3(nn.Module):
         self._pack_cache = pk
         return pk
 
+    def _rope32(self) -> torch.Tensor:
+        """The RoPE table in fp32 (the `rope` buffer follows the module's dtype, and cos/sin
+        in bf16 would lose precision), cached per device."""
+        dev = self.rope.device
+        t = getattr(self, "_rope32_cache", None)
+        if t is None or t.device != dev:
+            t = _rope_cache(self.args.head_dim, self.args.max_seq_len, self.args.rope_theta).to(dev)
+            self._rope32_cache = t
+        return t
+
     def _proj_group(self, layer: int, group: str, names, x: torch.Tensor, pk: dict) -> torch.Tensor:
         lo = pk["l_" + group][layer]
         if lo is None:  # adapters with different scales: one call per projection
@@ -310,6 +320,7 @@ class SharedQwen3(nn.Module):
         a = self.args
         b = token.shape[0]
         pk = self._decode_pack()
+        rope = self._rope32()
         h = self.tok_embeddings(token.view(b)).view(b, a.dim)
         sm_scale = a.head_dim ** -0.5
         pending = None
@@ -321,7 +332,7 @@ class SharedQwen3(nn.Module):
                 x, h = ops.add_rmsnorm_op(pending, h, blk.attention_norm.weight, a.norm_eps)
             qkv = self._proj_group(l, "qkv", ("wq", "wk", "wv"), x, pk)
             q = ops.qk_norm_rope_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight, a.norm_eps,
-                                    self.rope, pos, cache.k[l], cache.v[l], a.n_heads, a.n_kv_heads)
+                                    rope, pos, cache.k[l], cache.v[l], a.n_heads, a.n_kv_heads)
             o = ops.decode_attention_op(q, cache.k[l], cache.v[l], pos, sm_scale)
             o = self._proj(l, "wo", o)
             x, h = ops.add_rmsnorm_op(o, h, blk.ffn_norm.weight, a.norm_eps)
@@ -357,7 +368,7 @@ class SharedQwen3(nn.Module):
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 g_logits = self.decode_step(tok_buf, pos, cache)
-                g_next = g_logits.argmax(-1).view(b, 1)
+                g_next = ops.argmax_rows_op(g_logits).view(b, 1)
             # the warm-up wrote position s; the first replay rewrites it identically
             for i in range(1, n_new):
                 graph.replay()
@@ -367,7 +378,7 @@ class SharedQwen3(nn.Module):
         else:
             for i in range(1, n_new):
                 logits = self.decode_step(tok_buf, pos, cache)
-                nxt = logits.argmax(-1).view(b, 1)
+                nxt = ops.argmax_rows_op(logits).view(b, 1)
                 out[:, i] = nxt[:, 0]
                 tok_buf.copy_(nxt)
                 pos.add_(1)
