@@ -50,10 +50,16 @@ int wsl_qk_norm_rope_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t 
 /* out [batch, n_heads * head_dim] = softmax(q . K^T * scale) . V over cache positions
  * 0..*pos, query head h reading kv head h / (n_heads / n_kv_heads). Replaces the
  * repeat_kv + scaled_dot_product_attention of qwen3/model/model.py:93-102,204-214 for one
- * query token. n_heads / n_kv_heads in {1, 2, 4, 8}; head_dim in {64, 128}. */
+ * query token. The cache length is split into 64-position chunks whose partial softmax
+ * records go to `workspace` (wsl_decode_attention_workspace_bytes(...) bytes, 16-byte
+ * aligned, contents irrelevant) and are merged by a second launch.
+ * n_heads / n_kv_heads in {1, 2, 4, 8}; head_dim in {64, 128}. */
+size_t wsl_decode_attention_workspace_bytes(int64_t batch, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                             int64_t cache_len);
 int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_cache, int64_t batch,
                              int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t cache_len,
-                             const int64_t* pos, float scale, void* out, void* stream);
+                             const int64_t* pos, float scale, void* out, void* workspace, size_t workspace_bytes,
+                             void* stream);
 
 /* out [rows, ffn] = silu(g) * u with g = gate_up[:, :ffn], u = gate_up[:, ffn:2 ffn].
  * Replaces F.silu(w1(x)) * w3(x) (qwen3/model/model.py:250-251) given the two projections'

@@ -193,7 +193,11 @@ def test_decode_step_validation_codes():
     assert lib.wsl_qk_norm_rope_fwd(P2, 100, 2, 16, 8, 128, P2, P2, 1e-6, P2, P2, P2, P2, P2, 64, None) == N.WSL_E_SHAPE
     assert N.decode_last_error() != ""
     # attention: heads not a multiple of kv heads / unsupported grouping
-    assert lib.wsl_decode_attention_fwd(P2, P2, P2, 2, 12, 8, 128, 64, P2, 0.1, P2, None) == N.WSL_E_SHAPE
-    assert lib.wsl_decode_attention_fwd(P2, P2, P2, 2, 48, 3, 128, 64, P2, 0.1, P2, None) == N.WSL_E_SHAPE
+    assert lib.wsl_decode_attention_fwd(P2, P2, P2, 2, 12, 8, 128, 64, P2, 0.1, P2, P2, 1 << 20, None) == N.WSL_E_SHAPE
+    assert lib.wsl_decode_attention_fwd(P2, P2, P2, 2, 48, 3, 128, 64, P2, 0.1, P2, P2, 1 << 20, None) == N.WSL_E_SHAPE
+    need = lib.wsl_decode_attention_workspace_bytes(8, 16, 8, 128, 1024)
+    assert need == 8 * 16 * 16 * 130 * 4
+    assert lib.wsl_decode_attention_fwd(P2, P2, P2, 8, 16, 8, 128, 1024, P2, 0.1, P2, P2, need - 4, None) \
+        == N.WSL_E_WORKSPACE
     # swiglu: ld below 2 * ffn
     assert lib.wsl_swiglu_fwd(P2, 100, 4, 64, P2, 64, None) == N.WSL_E_SHAPE

@@ -6,9 +6,12 @@
 //   qk_rope_kernel        per head of the step's q|k|v row: RMSNorm over head_dim (q, k),
 //                         rotary embedding at the step's position, q written out, k and v
 //                         written into the KV cache at that position. One wave per head.
-//   attention_kernel      GQA attention of one query token against positions 0..pos of the
-//                         cache: one workgroup per (sequence, kv head), 16-lane groups per
-//                         position, online softmax, groups combined through LDS.
+//   attention_partial     GQA attention of one query token against positions 0..pos of the
+//   attention_combine     cache, split over the cache length: a workgroup takes 64 positions
+//                         of one (sequence, kv head), 16-lane groups per position with all
+//                         loads in flight at once, online softmax, groups combined through
+//                         LDS into a partial (max, sum, weighted V); a second launch merges
+//                         the partials of each (sequence, kv head).
 //   swiglu_kernel         out = bf16(silu(g) * u) from the gate|up projection output.
 //   argmax_kernel         greedy token: index of the largest logit of a row (first index on
 //                         ties, NaN counted as largest, as torch.argmax). One workgroup per row.
@@ -154,9 +157,10 @@ __global__ void __launch_bounds__(256) qk_rope_kernel(const uint16_t* __restrict
 }
 
 // --------------------------------------------------------------------- decode attention
-constexpr int AT_T = 512;              // 8 waves = 32 groups of 16 lanes
+constexpr int AT_T = 256;              // 4 waves = 16 groups of 16 lanes
 constexpr int AT_G = AT_T / 16;
-constexpr int AT_U = 4;                // positions in flight per group
+constexpr int AT_CH = 64;              // cache positions per workgroup
+constexpr int AT_U = AT_CH / AT_G;     // positions per group, all in flight
 
 // EPL (4 or 8) consecutive bf16 of a row as one 8- or 16-byte load.
 template <int EPL> struct Vec;
@@ -174,30 +178,39 @@ template <> struct Vec<4> {
   }
 };
 
-// EPL head_dim elements per lane (head_dim = 16 EPL), REP query heads per kv head.
+// Partial record of one (pair, chunk): per head the running max, the sum of exp and the
+// exp-weighted V sum, [REP][HD + 2] floats.
 template <int EPL, int REP>
-__global__ void __launch_bounds__(AT_T) attention_kernel(const uint16_t* __restrict__ q,
-                                                        const uint16_t* __restrict__ kc,
-                                                        const uint16_t* __restrict__ vc, int nh, int nkv,
-                                                        int cache_len, const int64_t* __restrict__ posp,
-                                                        float scale, uint16_t* __restrict__ out) {
+__global__ void __launch_bounds__(AT_T) attention_partial(const uint16_t* __restrict__ q,
+                                                         const uint16_t* __restrict__ kc,
+                                                         const uint16_t* __restrict__ vc, int nh, int nkv,
+                                                         int cache_len, int nchunk, const int64_t* __restrict__ posp,
+                                                         float scale, float* __restrict__ part) {
   constexpr int HD = 16 * EPL;
-  extern __shared__ __attribute__((aligned(16))) float at_smem[];
-  float* s_m = at_smem;                       // [G][REP]
-  float* s_l = s_m + AT_G * REP;              // [G][REP]
-  float* s_acc = s_l + AT_G * REP;            // [G][REP][HD]
-  const int pair = blockIdx.x;                // b * nkv + kvh
+  __shared__ float s_m[AT_G * REP], s_l[AT_G * REP];
+  __shared__ float s_acc[AT_G * REP * HD];
+  const int pair = blockIdx.x / nchunk, chunk = blockIdx.x % nchunk;
+  const int L = (int)(*posp) + 1;
+  const int t0 = chunk * AT_CH;
+  if (t0 >= L) return;  // the combine reads only the chunks below L
   const int b = pair / nkv, kvh = pair % nkv;
   const int tid = threadIdx.x;
   const int g = tid >> 4, l16 = tid & 15;
-  const int L = (int)(*posp) + 1;
-  // q slice of the REP heads sharing this kv head
   float qv[REP][EPL];
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
     const uint16_t* qr = q + ((int64_t)b * nh + kvh * REP + h) * HD + l16 * EPL;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) qv[h][e] = bf(qr[e]) * scale;
+  }
+  const uint16_t* kbase = kc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  const uint16_t* vbase = vc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  Vec<EPL> kv[AT_U], vv[AT_U];
+#pragma unroll
+  for (int u = 0; u < AT_U; ++u) {
+    const int t = min(t0 + g + u * AT_G, L - 1);
+    kv[u].load(kbase + (int64_t)t * HD);
+    vv[u].load(vbase + (int64_t)t * HD);
   }
   float m[REP], lsum[REP], acc[REP][EPL];
 #pragma unroll
@@ -207,38 +220,25 @@ __global__ void __launch_bounds__(AT_T) attention_kernel(const uint16_t* __restr
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[h][e] = 0.f;
   }
-  const uint16_t* kbase = kc + (int64_t)pair * cache_len * HD + l16 * EPL;
-  const uint16_t* vbase = vc + (int64_t)pair * cache_len * HD + l16 * EPL;
-  for (int t0 = g; t0 < L; t0 += AT_G * AT_U) {
-    Vec<EPL> kv[AT_U], vv[AT_U];
 #pragma unroll
-    for (int u = 0; u < AT_U; ++u) {
-      const int t = min(t0 + u * AT_G, L - 1);
-      kv[u].load(kbase + (int64_t)t * HD);
-      vv[u].load(vbase + (int64_t)t * HD);
-    }
+  for (int u = 0; u < AT_U; ++u) {
+    if (t0 + g + u * AT_G >= L) break;
 #pragma unroll
-    for (int u = 0; u < AT_U; ++u) {
-      const int t = t0 + u * AT_G;
-      if (t >= L) break;
+    for (int h = 0; h < REP; ++h) {
+      float sc = 0.f;
 #pragma unroll
-      for (int h = 0; h < REP; ++h) {
-        float s = 0.f;
+      for (int e = 0; e < EPL; ++e) sc += qv[h][e] * kv[u].at(e);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) s += qv[h][e] * kv[u].at(e);
+      for (int o = 8; o > 0; o >>= 1) sc += __shfl_xor(sc, o, 16);
+      const float mn = fmaxf(m[h], sc);
+      const float corr = __expf(m[h] - mn);
+      const float p = __expf(sc - mn);
+      lsum[h] = lsum[h] * corr + p;
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
-        const float mn = fmaxf(m[h], s);
-        const float corr = __expf(m[h] - mn);
-        const float p = __expf(s - mn);
-        lsum[h] = lsum[h] * corr + p;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[h][e] = acc[h][e] * corr + p * vv[u].at(e);
-        m[h] = mn;
-      }
+      for (int e = 0; e < EPL; ++e) acc[h][e] = acc[h][e] * corr + p * vv[u].at(e);
+      m[h] = mn;
     }
   }
-  // combine the groups
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
     if (l16 == 0) {
@@ -249,6 +249,7 @@ __global__ void __launch_bounds__(AT_T) attention_kernel(const uint16_t* __restr
     for (int e = 0; e < EPL; ++e) s_acc[(g * REP + h) * HD + l16 * EPL + e] = acc[h][e];
   }
   __syncthreads();
+  float* rec = part + (int64_t)blockIdx.x * REP * (HD + 2);
   for (int q2 = tid; q2 < REP * HD; q2 += AT_T) {
     const int h = q2 / HD, d = q2 % HD;
     float mx = -INFINITY;
@@ -261,8 +262,38 @@ __global__ void __launch_bounds__(AT_T) attention_kernel(const uint16_t* __restr
       num += f * s_acc[(gg * REP + h) * HD + d];
       den += f * s_l[gg * REP + h];
     }
-    out[((int64_t)b * nh + kvh * REP + h) * HD + d] = f32_to_bf16_bits(num / den);
+    rec[h * (HD + 2) + d] = num;
+    if (d == 0) {
+      rec[h * (HD + 2) + HD] = mx;
+      rec[h * (HD + 2) + HD + 1] = den;
+    }
   }
+}
+
+// One workgroup per (sequence, kv head), one thread per (head, element): merges the
+// partial records of the chunks below L.
+template <int HD, int REP>
+__global__ void __launch_bounds__(1024) attention_combine(const float* __restrict__ part, int nh, int nkv,
+                                                         int nchunk, const int64_t* __restrict__ posp,
+                                                         uint16_t* __restrict__ out) {
+  const int pair = blockIdx.x;
+  const int b = pair / nkv, kvh = pair % nkv;
+  const int tid = threadIdx.x;
+  if (tid >= REP * HD) return;
+  const int h = tid / HD, d = tid % HD;
+  const int L = (int)(*posp) + 1;
+  const int nc = min(nchunk, (L + AT_CH - 1) / AT_CH);
+  const float* rec = part + (int64_t)pair * nchunk * REP * (HD + 2) + h * (HD + 2);
+  float mx = -INFINITY;
+  for (int c = 0; c < nc; ++c) mx = fmaxf(mx, rec[(int64_t)c * REP * (HD + 2) + HD]);
+  float num = 0.f, den = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    const float* rc = rec + (int64_t)c * REP * (HD + 2);
+    const float f = __expf(rc[HD] - mx);
+    num += f * rc[d];
+    den += f * rc[HD + 1];
+  }
+  out[((int64_t)b * nh + kvh * REP + h) * HD + d] = f32_to_bf16_bits(num / den);
 }
 
 // --------------------------------------------------------------------- SwiGLU
@@ -339,27 +370,24 @@ __global__ void __launch_bounds__(AM_T) argmax_kernel(const uint16_t* __restrict
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <int EPL, int R>
-hipError_t launch_attention_r(dim3 grid, size_t smem, hipStream_t st, const uint16_t* q, const uint16_t* kc,
+hipError_t launch_attention_r(int pairs, int nchunk, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                               const uint16_t* vc, int nh, int nkv, int cache_len, const int64_t* pos, float scale,
-                              uint16_t* out) {
-  static bool ready = false;  // the combine buffer exceeds the default 64 KB for large REP
-  if (!ready) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<EPL, R>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    ready = true;
-  }
-  attention_kernel<EPL, R><<<grid, dim3(AT_T), smem, st>>>(q, kc, vc, nh, nkv, cache_len, pos, scale, out);
+                              float* part, uint16_t* out) {
+  attention_partial<EPL, R><<<dim3((unsigned)(pairs * nchunk)), dim3(AT_T), 0, st>>>(q, kc, vc, nh, nkv, cache_len,
+                                                                                   nchunk, pos, scale, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  attention_combine<16 * EPL, R><<<dim3((unsigned)pairs), dim3(1024), 0, st>>>(part, nh, nkv, nchunk, pos, out);
   return hipGetLastError();
 }
 
 template <int EPL>
-hipError_t launch_attention(int rep, dim3 grid, size_t smem, hipStream_t st, const uint16_t* q,
+hipError_t launch_attention(int rep, int pairs, int nchunk, hipStream_t st, const uint16_t* q,
                             const uint16_t* kc, const uint16_t* vc, int nh, int nkv, int cache_len,
-                            const int64_t* pos, float scale, uint16_t* out) {
+                            const int64_t* pos, float scale, float* part, uint16_t* out) {
   switch (rep) {
 #define WSL_AT(R) \
-  case R: return launch_attention_r<EPL, R>(grid, smem, st, q, kc, vc, nh, nkv, cache_len, pos, scale, out);
+  case R: return launch_attention_r<EPL, R>(pairs, nchunk, st, q, kc, vc, nh, nkv, cache_len, pos, scale, part, out);
     WSL_AT(1) WSL_AT(2) WSL_AT(4) WSL_AT(8)
 #undef WSL_AT
     default: return hipErrorInvalidValue;
@@ -431,9 +459,17 @@ int wsl_qk_norm_rope_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t 
   return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "qk_norm_rope: launch failed");
 }
 
+size_t wsl_decode_attention_workspace_bytes(int64_t batch, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                             int64_t cache_len) {
+  if (batch < 0 || n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || cache_len < 1) return 0;
+  const int64_t nchunk = (cache_len + AT_CH - 1) / AT_CH;
+  return (size_t)(batch * n_heads * nchunk * (head_dim + 2) * 4);
+}
+
 int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_cache, int64_t batch,
                              int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t cache_len,
-                             const int64_t* pos, float scale, void* out, void* stream) {
+                             const int64_t* pos, float scale, void* out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   g_derr[0] = 0;
   if (batch < 0 || n_kv_heads < 1 || n_heads % n_kv_heads != 0 || cache_len < 1)
     return dfail(WSL_E_SHAPE, "decode_attention: bad sizes");
@@ -443,16 +479,19 @@ int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_c
   if (head_dim != 64 && head_dim != 128) return dfail(WSL_E_SHAPE, "decode_attention: head_dim must be 64 or 128");
   if (batch == 0) return WSL_OK;
   if (!q || !k_cache || !v_cache || !pos || !out) return dfail(WSL_E_INVALID_ARG, "decode_attention: null pointer");
-  const size_t smem = (size_t)AT_G * rep * (2 + head_dim) * sizeof(float);
-  dim3 grid((unsigned)(batch * n_kv_heads));
+  const size_t need = wsl_decode_attention_workspace_bytes(batch, n_heads, n_kv_heads, head_dim, cache_len);
+  if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 15))
+    return dfail(WSL_E_WORKSPACE, "decode_attention: workspace missing, too small or misaligned");
+  const int pairs = (int)(batch * n_kv_heads);
+  const int nchunk = (int)((cache_len + AT_CH - 1) / AT_CH);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e = head_dim == 64
-                     ? launch_attention<4>((int)rep, grid, smem, st, (const uint16_t*)q, (const uint16_t*)k_cache,
-                                           (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads,
-                                           (int)cache_len, pos, scale, (uint16_t*)out)
-                     : launch_attention<8>((int)rep, grid, smem, st, (const uint16_t*)q, (const uint16_t*)k_cache,
-                                           (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads,
-                                           (int)cache_len, pos, scale, (uint16_t*)out);
+                     ? launch_attention<4>((int)rep, pairs, nchunk, st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                                           (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads, (int)cache_len,
+                                           pos, scale, (float*)workspace, (uint16_t*)out)
+                     : launch_attention<8>((int)rep, pairs, nchunk, st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                                           (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads, (int)cache_len,
+                                           pos, scale, (float*)workspace, (uint16_t*)out);
   return e == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "decode_attention: launch failed");
 }
 

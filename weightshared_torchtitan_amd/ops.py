@@ -294,10 +294,12 @@ def decode_attention_op(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     q = q.contiguous()
     pos = pos.to(torch.int64).contiguous()
     out = torch.empty((b, nh * hd), dtype=torch.bfloat16, device=dev)
+    nbytes = _native.lib().wsl_decode_attention_workspace_bytes(b, nh, nkv, hd, L)
+    part = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)  # partial softmax records
     with torch.cuda.device(dev):
         rc = _native.lib().wsl_decode_attention_fwd(
             q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), b, nh, nkv, hd, L, pos.data_ptr(),
-            float(scale), out.data_ptr(), _stream(dev))
+            float(scale), out.data_ptr(), part.data_ptr(), part.numel(), _stream(dev))
     _native.check(rc, "wsl_decode_attention_fwd", decode=True)
     return out
 
