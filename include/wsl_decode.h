@@ -61,6 +61,23 @@ int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_c
                              const int64_t* pos, float scale, void* out, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* One launch for the attention block of a decode step: wsl_qk_norm_rope_fwd's work (q and
+ * k RMS-normed and rotated, k and v written into the caches at *pos) fused with
+ * wsl_decode_attention_fwd's (out [batch, n_heads * head_dim]). Every 64-position chunk
+ * workgroup normalises its own query heads; the chunk holding *pos also produces the step's
+ * k and v. The chunks' partial softmax records are merged by the last one of each
+ * (sequence, kv head) to finish. `workspace` (wsl_decode_attention_step_workspace_bytes
+ * bytes, 256-byte aligned) starts with arrival counters: zero-fill it before its first use;
+ * every completed call leaves them zero. Calls that may run concurrently must not share
+ * a workspace. n_heads / n_kv_heads in {1, 2, 4}; head_dim in {64, 128}. */
+size_t wsl_decode_attention_step_workspace_bytes(int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                                                  int64_t head_dim, int64_t cache_len);
+int wsl_decode_attention_step_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t n_heads,
+                                  int64_t n_kv_heads, int64_t head_dim, const void* q_norm_w, const void* k_norm_w,
+                                  float eps, const float* rope, const int64_t* pos, void* k_cache, void* v_cache,
+                                  int64_t cache_len, float scale, void* out, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* out [rows, ffn] = silu(g) * u with g = gate_up[:, :ffn], u = gate_up[:, ffn:2 ffn].
  * Replaces F.silu(w1(x)) * w3(x) (qwen3/model/model.py:250-251) given the two projections'
  * outputs side by side. ffn % 8 == 0; 16-byte aligned rows. */

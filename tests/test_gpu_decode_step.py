@@ -145,3 +145,33 @@ def test_argmax_rows_matches_torch(gpu, rows, n):
         x[2, n // 2] = float("nan")
     got = ops.argmax_rows_op(x)
     assert torch.equal(got, torch.argmax(x.float(), dim=-1))
+
+
+@pytest.mark.parametrize("b,nh,nkv,hd,L,pos", [(8, 16, 8, 128, 1024, 767), (8, 16, 8, 128, 1024, 64),
+                                             (2, 4, 2, 64, 64, 0), (3, 8, 2, 128, 200, 130),
+                                             (2, 4, 4, 64, 80, 63)])
+def test_decode_attention_step_equals_unfused(gpu, b, nh, nkv, hd, L, pos):
+    """The fused step (norm + RoPE + cache write + split attention, merged by the last chunk
+    to arrive) against the fp32 reference, twice in a row (arrival counters reset), and its
+    cache writes equal to the unfused q/k-norm + RoPE kernel's."""
+    from weightshared_torchtitan_amd import ops
+    from weightshared_torchtitan_amd.qwen3_shared import _rope_cache
+    _say(f"[attention step] b={b} nh={nh} nkv={nkv} hd={hd} L={L} pos={pos}")
+    g = torch.Generator(device="cuda").manual_seed(3 * L + pos)
+    qkv = torch.randn(b, (nh + 2 * nkv) * hd, device=gpu, generator=g).bfloat16()
+    qw = (1 + 0.1 * torch.randn(hd, device=gpu, generator=g)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(hd, device=gpu, generator=g)).bfloat16()
+    rope = _rope_cache(hd, L, 1e6).to(gpu)
+    kc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+    vc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+    kc2, vc2 = kc.clone(), vc.clone()
+    p = torch.full((), pos, dtype=torch.int64, device=gpu)
+    scale = hd ** -0.5
+    q = ops.qk_norm_rope_op(qkv, qw, kw, 1e-6, rope, p, kc2, vc2, nh, nkv)
+    ref = attn_ref(q, kc2, vc2, pos, scale)
+    for _ in range(2):
+        out = ops.decode_attention_step_op(qkv, qw, kw, 1e-6, rope, p, kc, vc, nh, nkv, scale)
+        assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+        assert rel(out, ref) <= TOL
+    ws = ops.workspace(gpu, torch.cuda.current_stream(gpu).cuda_stream, 0, kind="attention")
+    assert int(ws[:256].count_nonzero()) == 0, "arrival counters not restored to zero"

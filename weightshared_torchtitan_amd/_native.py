@@ -38,6 +38,8 @@ EXPORTED = (
     "wsl_qk_norm_rope_fwd",
     "wsl_decode_attention_workspace_bytes",
     "wsl_decode_attention_fwd",
+    "wsl_decode_attention_step_workspace_bytes",
+    "wsl_decode_attention_step_fwd",
     "wsl_swiglu_fwd",
     "wsl_argmax_rows_fwd",
     "wsl_decode_last_error",
@@ -91,6 +93,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.wsl_decode_attention_fwd.argtypes = [
         _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # q, k, v, batch, nh, nkv, hd, cache_len
         _c_vp, ctypes.c_float, _c_vp, _c_vp, ctypes.c_size_t, _c_vp]  # pos, scale, out, workspace, bytes, stream
+    lib.wsl_decode_attention_step_workspace_bytes.restype = ctypes.c_size_t
+    lib.wsl_decode_attention_step_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]
+    lib.wsl_decode_attention_step_fwd.restype = ctypes.c_int
+    lib.wsl_decode_attention_step_fwd.argtypes = [
+        _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,        # qkv, ldqkv, batch, n_heads, n_kv, head_dim
+        _c_vp, _c_vp, ctypes.c_float, _c_vp, _c_vp,          # q_norm_w, k_norm_w, eps, rope, pos
+        _c_vp, _c_vp, _c_i64, ctypes.c_float, _c_vp,         # k_cache, v_cache, cache_len, scale, out
+        _c_vp, ctypes.c_size_t, _c_vp]                       # workspace, bytes, stream
     lib.wsl_swiglu_fwd.restype = ctypes.c_int
     lib.wsl_swiglu_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]
     lib.wsl_argmax_rows_fwd.restype = ctypes.c_int

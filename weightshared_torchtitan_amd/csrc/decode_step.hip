@@ -6,6 +6,13 @@
 //   qk_rope_kernel        per head of the step's q|k|v row: RMSNorm over head_dim (q, k),
 //                         rotary embedding at the step's position, q written out, k and v
 //                         written into the KV cache at that position. One wave per head.
+//   attention_step        the q/k norm + RoPE + cache write of one step fused with its
+//                         attention: every chunk workgroup normalises and rotates its own
+//                         query heads; the chunk holding `pos` also the step's k (and v),
+//                         writes them into the cache and uses them from LDS; the partial
+//                         records are merged by the last chunk workgroup of each (sequence,
+//                         kv head) to arrive (agent-scope atomics; arrival counters reset by
+//                         that workgroup), so the whole step is one launch.
 //   attention_partial     GQA attention of one query token against positions 0..pos of the
 //   attention_combine     cache, split over the cache length: a workgroup takes 64 positions
 //                         of one (sequence, kv head), 16-lane groups per position with all
@@ -167,11 +174,13 @@ template <int EPL> struct Vec;
 template <> struct Vec<8> {
   u32x4_t v;
   __device__ __forceinline__ void load(const uint16_t* p) { v = ld_global_16(p); }
+  __device__ __forceinline__ void load_lds(const uint16_t* p) { v = *reinterpret_cast<const u32x4_t*>(p); }
   __device__ __forceinline__ float at(int e) const { return bf((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu); }
 };
 template <> struct Vec<4> {
   uint2 v;
   __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint2*>(p); }
+  __device__ __forceinline__ void load_lds(const uint16_t* p) { v = *reinterpret_cast<const uint2*>(p); }
   __device__ __forceinline__ float at(int e) const {
     const uint32_t w = (e >> 1) ? v.y : v.x;
     return bf((w >> ((e & 1) * 16)) & 0xffffu);
@@ -369,6 +378,188 @@ __global__ void __launch_bounds__(AM_T) argmax_kernel(const uint16_t* __restrict
 
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ------------------------------------------------------------ fused step (norm + RoPE + attention)
+__device__ __forceinline__ void st_agent_f(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent_f(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int EPL, int REP>
+__global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restrict__ qkv, int64_t ldq, int nh, int nkv,
+                                                      const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+                                                      float eps, const float* __restrict__ rope,
+                                                      const int64_t* __restrict__ posp, uint16_t* __restrict__ kc,
+                                                      uint16_t* __restrict__ vc, int cache_len, int nchunk, float scale,
+                                                      unsigned* __restrict__ cnt, float* __restrict__ part,
+                                                      uint16_t* __restrict__ out) {
+  constexpr int HD = 16 * EPL;
+  constexpr int C = HD / 64;  // elements per lane when one wave holds one head
+  __shared__ float s_q[REP * HD];
+  __shared__ uint16_t s_knew[HD], s_vnew[HD];
+  __shared__ float s_m[AT_G * REP], s_l[AT_G * REP];
+  __shared__ float s_acc[AT_G * REP * HD];
+  __shared__ int s_last;
+  const int pair = blockIdx.x / nchunk, chunk = blockIdx.x % nchunk;
+  const int pos = (int)(*posp);
+  const int L = pos + 1;
+  const int t0 = chunk * AT_CH;
+  if (t0 >= L) return;  // no position here; the merge counts only the chunks below L
+  const int b = pair / nkv, kvh = pair % nkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = tid >> 4, l16 = tid & 15;
+  const bool owner = (pos / AT_CH) == chunk;
+  const float* rc = rope + (int64_t)pos * 2 * HD;
+  // q heads of this kv head (and, in the owner chunk, the step's k head): one wave each
+  const int nheads = REP + (owner ? 1 : 0);
+  for (int hh = wave; hh < nheads; hh += AT_T / 64) {
+    const bool is_q = hh < REP;
+    const int head = is_q ? kvh * REP + hh : nh + kvh;
+    const uint16_t* src = qkv + (int64_t)b * ldq + (int64_t)head * HD;
+    const uint16_t* nw = is_q ? qw : kw;
+    float v[C], ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      v[c] = bf(src[lane + 64 * c]);
+      ss += v[c] * v[c];
+    }
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss / (float)HD + eps);
+    float n[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) n[c] = v[c] * inv * bf(nw[lane + 64 * c]);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int j = lane + 64 * c;
+      float partner;
+      if constexpr (C == 1) partner = __shfl_xor(n[0], 32, 64);
+      else partner = n[(c + C / 2) % C];
+      const float rot = (j < HD / 2) ? -partner : partner;  // rotate_half
+      const float o = n[c] * rc[j] + rot * rc[HD + j];
+      if (is_q) {
+        s_q[hh * HD + j] = o * scale;
+      } else {
+        const int64_t at = ((int64_t)pair * cache_len + pos) * HD + j;
+        const uint16_t kb = f32_to_bf16_bits(o);
+        const uint16_t vb = qkv[(int64_t)b * ldq + (int64_t)(nh + nkv + kvh) * HD + j];
+        s_knew[j] = kb;
+        s_vnew[j] = vb;
+        kc[at] = kb;
+        vc[at] = vb;
+      }
+    }
+  }
+  __syncthreads();
+  float qv[REP][EPL];
+#pragma unroll
+  for (int h = 0; h < REP; ++h)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[h][e] = s_q[h * HD + l16 * EPL + e];
+  const uint16_t* kbase = kc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  const uint16_t* vbase = vc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  Vec<EPL> kv[AT_U], vv[AT_U];
+#pragma unroll
+  for (int u = 0; u < AT_U; ++u) {
+    const int t = min(t0 + g + u * AT_G, pos);
+    if (t == pos) {  // this step's k and v: from LDS (the cache write above may not be visible yet)
+      kv[u].load_lds(s_knew + l16 * EPL);
+      vv[u].load_lds(s_vnew + l16 * EPL);
+    } else {
+      kv[u].load(kbase + (int64_t)t * HD);
+      vv[u].load(vbase + (int64_t)t * HD);
+    }
+  }
+  float m[REP], lsum[REP], acc[REP][EPL];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    m[h] = -INFINITY;
+    lsum[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[h][e] = 0.f;
+  }
+#pragma unroll
+  for (int u = 0; u < AT_U; ++u) {
+    if (t0 + g + u * AT_G >= L) break;
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      float sc = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) sc += qv[h][e] * kv[u].at(e);
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) sc += __shfl_xor(sc, o, 16);
+      const float mn = fmaxf(m[h], sc);
+      const float corr = __expf(m[h] - mn);
+      const float p = __expf(sc - mn);
+      lsum[h] = lsum[h] * corr + p;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[h][e] = acc[h][e] * corr + p * vv[u].at(e);
+      m[h] = mn;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    if (l16 == 0) {
+      s_m[g * REP + h] = m[h];
+      s_l[g * REP + h] = lsum[h];
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s_acc[(g * REP + h) * HD + l16 * EPL + e] = acc[h][e];
+  }
+  __syncthreads();
+  // this chunk's record, published with agent-scope stores
+  float* rec = part + (int64_t)blockIdx.x * REP * (HD + 2);
+  for (int q2 = tid; q2 < REP * HD; q2 += AT_T) {
+    const int h = q2 / HD, d = q2 % HD;
+    float mx = -INFINITY;
+    for (int gg = 0; gg < AT_G; ++gg) mx = fmaxf(mx, s_m[gg * REP + h]);
+    float num = 0.f, den = 0.f;
+    for (int gg = 0; gg < AT_G; ++gg) {
+      const float mg = s_m[gg * REP + h];
+      if (mg == -INFINITY) continue;
+      const float f = __expf(mg - mx);
+      num += f * s_acc[(gg * REP + h) * HD + d];
+      den += f * s_l[gg * REP + h];
+    }
+    st_agent_f(rec + h * (HD + 2) + d, num);
+    if (d == 0) {
+      st_agent_f(rec + h * (HD + 2) + HD, mx);
+      st_agent_f(rec + h * (HD + 2) + HD + 1, den);
+    }
+  }
+  const int nc = (L + AT_CH - 1) / AT_CH;
+  if (nc > 1) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the record is out before the arrival
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned old = __hip_atomic_fetch_add(cnt + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == (unsigned)(nc - 1);
+      if (last) __hip_atomic_store(cnt + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+  }
+  // merge the records of every chunk of this pair (in chunk order)
+  const float* base = part + (int64_t)pair * nchunk * REP * (HD + 2);
+  for (int q2 = tid; q2 < REP * HD; q2 += AT_T) {
+    const int h = q2 / HD, d = q2 % HD;
+    float mx = -INFINITY;
+    for (int c = 0; c < nc; ++c) mx = fmaxf(mx, ld_agent_f(base + ((int64_t)c * REP + h) * (HD + 2) + HD));
+    float num = 0.f, den = 0.f;
+    for (int c = 0; c < nc; ++c) {
+      const float* r2 = base + ((int64_t)c * REP + h) * (HD + 2);
+      const float f = __expf(ld_agent_f(r2 + HD) - mx);
+      num += f * ld_agent_f(r2 + d);
+      den += f * ld_agent_f(r2 + HD + 1);
+    }
+    out[((int64_t)b * nh + kvh * REP + h) * HD + d] = f32_to_bf16_bits(num / den);
+  }
+}
+
 template <int EPL, int R>
 hipError_t launch_attention_r(int pairs, int nchunk, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                               const uint16_t* vc, int nh, int nkv, int cache_len, const int64_t* pos, float scale,
@@ -493,6 +684,53 @@ int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_c
                                            (const uint16_t*)v_cache, (int)n_heads, (int)n_kv_heads, (int)cache_len,
                                            pos, scale, (float*)workspace, (uint16_t*)out);
   return e == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "decode_attention: launch failed");
+}
+
+size_t wsl_decode_attention_step_workspace_bytes(int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                                                  int64_t head_dim, int64_t cache_len) {
+  if (batch < 0 || n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || cache_len < 1) return 0;
+  const int64_t nchunk = (cache_len + AT_CH - 1) / AT_CH;
+  const size_t counters = ((size_t)(batch * n_kv_heads) * 4 + 255) & ~(size_t)255;
+  return counters + (size_t)(batch * n_heads * nchunk * (head_dim + 2) * 4);
+}
+
+int wsl_decode_attention_step_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t n_heads,
+                                  int64_t n_kv_heads, int64_t head_dim, const void* q_norm_w, const void* k_norm_w,
+                                  float eps, const float* rope, const int64_t* pos, void* k_cache, void* v_cache,
+                                  int64_t cache_len, float scale, void* out, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  g_derr[0] = 0;
+  if (batch < 0 || n_kv_heads < 1 || n_heads % n_kv_heads != 0 || cache_len < 1)
+    return dfail(WSL_E_SHAPE, "decode_attention_step: bad sizes");
+  const int64_t rep = n_heads / n_kv_heads;
+  if (rep != 1 && rep != 2 && rep != 4)
+    return dfail(WSL_E_SHAPE, "decode_attention_step: n_heads / n_kv_heads must be 1, 2 or 4");
+  if (head_dim != 64 && head_dim != 128) return dfail(WSL_E_SHAPE, "decode_attention_step: head_dim must be 64 or 128");
+  if (ldqkv < (n_heads + 2 * n_kv_heads) * head_dim) return dfail(WSL_E_SHAPE, "decode_attention_step: ldqkv too small");
+  if (batch == 0) return WSL_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !rope || !pos || !k_cache || !v_cache || !out)
+    return dfail(WSL_E_INVALID_ARG, "decode_attention_step: null pointer");
+  const size_t need = wsl_decode_attention_step_workspace_bytes(batch, n_heads, n_kv_heads, head_dim, cache_len);
+  if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255))
+    return dfail(WSL_E_WORKSPACE, "decode_attention_step: workspace missing, too small or not 256-byte aligned");
+  const int pairs = (int)(batch * n_kv_heads);
+  const int nchunk = (int)((cache_len + AT_CH - 1) / AT_CH);
+  unsigned* cnt = reinterpret_cast<unsigned*>(workspace);
+  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + (((size_t)pairs * 4 + 255) & ~(size_t)255));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)(pairs * nchunk));
+#define WSL_AS(E, R)                                                                                           \
+  attention_step<E, R><<<grid, dim3(AT_T), 0, st>>>((const uint16_t*)qkv, ldqkv, (int)n_heads, (int)n_kv_heads, \
+                                                    (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, eps, rope, \
+                                                    pos, (uint16_t*)k_cache, (uint16_t*)v_cache, (int)cache_len,     \
+                                                    nchunk, scale, cnt, part, (uint16_t*)out)
+  if (head_dim == 64) {
+    if (rep == 1) WSL_AS(4, 1); else if (rep == 2) WSL_AS(4, 2); else WSL_AS(4, 4);
+  } else {
+    if (rep == 1) WSL_AS(8, 1); else if (rep == 2) WSL_AS(8, 2); else WSL_AS(8, 4);
+  }
+#undef WSL_AS
+  return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "decode_attention_step: launch failed");
 }
 
 int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* stream) {

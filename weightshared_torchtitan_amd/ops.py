@@ -52,15 +52,15 @@ _WS_MIN_BYTES = 16 << 20
 _workspaces: dict = {}
 
 
-def workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """The persistent scratch buffer of (device, stream).
+def workspace(dev: torch.device, stream: int, nbytes: int, kind: str = "lora") -> torch.Tensor:
+    """The persistent scratch buffer of (device, stream, kind).
 
-    libwsl requires its workspace to be zero-filled before first use (the leading
+    libwsl requires its workspaces to be zero-filled before first use (the leading
     counters of the decode kernels) and keeps those counters valid across calls, so one
-    zero-filled buffer per stream is reused by every call on that stream; it only grows
-    (a grown buffer starts zeroed again).
+    zero-filled buffer per stream and kind is reused by every call on that stream; it only
+    grows (a grown buffer starts zeroed again).
     """
-    key = (dev.index, stream)
+    key = (dev.index, stream, kind)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.zeros(max(2 * nbytes, _WS_MIN_BYTES), dtype=torch.uint8, device=dev)
@@ -132,7 +132,7 @@ def lora_linear_op(x: torch.Tensor, w: Optional[torch.Tensor], w_scale: Optional
                 M, N, K, r,
                 ws.data_ptr(), ws.numel(), stream)
         if rc != _native.WSL_OK:
-            _workspaces.pop((dev.index, stream), None)  # a failed launch may leave counters mid-update
+            _workspaces.pop((dev.index, stream, "lora"), None)  # a failed launch may leave counters mid-update
         _native.check(rc, "wsl_lora_linear_fwd")
     return y.reshape(*lead, N)
 
@@ -348,3 +348,41 @@ def argmax_rows_op(x: torch.Tensor) -> torch.Tensor:
 @argmax_rows_op.register_fake
 def _argmax_rows_fake(x):
     return x.new_empty(x.shape[:-1], dtype=torch.int64)
+
+
+@torch.library.custom_op("wsl::decode_attention_step", mutates_args=("k_cache", "v_cache"), device_types="cuda")
+def decode_attention_step_op(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, eps: float,
+                             rope: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             n_heads: int, n_kv_heads: int, scale: float) -> torch.Tensor:
+    """q/k norm + RoPE + cache write + attention of one decode step in one launch:
+    qkv [b, (n_heads + 2 n_kv_heads) hd] -> [b, n_heads * hd]; k, v written into the
+    caches [b, n_kv_heads, L, hd] at `pos`."""
+    dev = _check_device(qkv, q_norm_w, k_norm_w, rope, pos, k_cache, v_cache)
+    b, _, L, hd = k_cache.shape
+    q2 = _bf16_2d(qkv, "qkv")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache and v_cache must be contiguous [b, n_kv_heads, L, head_dim]")
+    qw = q_norm_w.to(torch.bfloat16).contiguous()
+    kw = k_norm_w.to(torch.bfloat16).contiguous()
+    rope = rope.float().contiguous()
+    pos = pos.to(torch.int64).contiguous()
+    out = torch.empty((b, n_heads * hd), dtype=torch.bfloat16, device=dev)
+    lib = _native.lib()
+    stream = _stream(dev)
+    ws = workspace(dev, stream, lib.wsl_decode_attention_step_workspace_bytes(b, n_heads, n_kv_heads, hd, L),
+                   kind="attention")
+    with torch.cuda.device(dev):
+        rc = lib.wsl_decode_attention_step_fwd(
+            q2.data_ptr(), q2.stride(0), b, n_heads, n_kv_heads, hd, qw.data_ptr(), kw.data_ptr(), float(eps),
+            rope.data_ptr(), pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), L, float(scale),
+            out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    if rc != _native.WSL_OK:
+        _workspaces.pop((dev.index, stream, "attention"), None)
+    _native.check(rc, "wsl_decode_attention_step_fwd", decode=True)
+    return out
+
+
+@decode_attention_step_op.register_fake
+def _decode_attention_step_fake(qkv, q_norm_w, k_norm_w, eps, rope, pos, k_cache, v_cache, n_heads, n_kv_heads,
+                                scale):
+    return qkv.new_empty((k_cache.shape[0], n_heads * k_cache.shape[3]), dtype=torch.bfloat16)

@@ -323,6 +323,7 @@ class SharedQwen3(nn.Module):
         rope = self._rope32()
         h = self.tok_embeddings(token.view(b)).view(b, a.dim)
         sm_scale = a.head_dim ** -0.5
+        fused_attn = a.n_heads // a.n_kv_heads in (1, 2, 4) and a.head_dim in (64, 128)
         pending = None
         for l in range(a.n_layers):
             blk = self.base_blocks[a.block_of(l)]
@@ -331,9 +332,14 @@ class SharedQwen3(nn.Module):
             else:
                 x, h = ops.add_rmsnorm_op(pending, h, blk.attention_norm.weight, a.norm_eps)
             qkv = self._proj_group(l, "qkv", ("wq", "wk", "wv"), x, pk)
-            q = ops.qk_norm_rope_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight, a.norm_eps,
-                                    rope, pos, cache.k[l], cache.v[l], a.n_heads, a.n_kv_heads)
-            o = ops.decode_attention_op(q, cache.k[l], cache.v[l], pos, sm_scale)
+            if fused_attn:
+                o = ops.decode_attention_step_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight,
+                                                 a.norm_eps, rope, pos, cache.k[l], cache.v[l], a.n_heads,
+                                                 a.n_kv_heads, sm_scale)
+            else:
+                q = ops.qk_norm_rope_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight, a.norm_eps,
+                                        rope, pos, cache.k[l], cache.v[l], a.n_heads, a.n_kv_heads)
+                o = ops.decode_attention_op(q, cache.k[l], cache.v[l], pos, sm_scale)
             o = self._proj(l, "wo", o)
             x, h = ops.add_rmsnorm_op(o, h, blk.ffn_norm.weight, a.norm_eps)
             gu = self._proj_group(l, "gu", ("w1", "w3"), x, pk)
