@@ -149,7 +149,7 @@ def test_argmax_rows_matches_torch(gpu, rows, n):
 
 @pytest.mark.parametrize("b,nh,nkv,hd,L,pos", [(8, 16, 8, 128, 1024, 767), (8, 16, 8, 128, 1024, 64),
                                              (2, 4, 2, 64, 64, 0), (3, 8, 2, 128, 200, 130),
-                                             (2, 4, 4, 64, 80, 63)])
+                                             (2, 4, 4, 64, 80, 63), (2, 8, 2, 128, 4096, 3000)])
 def test_decode_attention_step_equals_unfused(gpu, b, nh, nkv, hd, L, pos):
     """The fused step (norm + RoPE + cache write + split attention, merged by the last chunk
     to arrive) against the fp32 reference, twice in a row (arrival counters reset), and its

@@ -411,6 +411,17 @@ __global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restric
   const int g = tid >> 4, l16 = tid & 15;
   const bool owner = (pos / AT_CH) == chunk;
   const float* rc = rope + (int64_t)pos * 2 * HD;
+  // K/V of this group's positions, issued first so their latency overlaps the q work below.
+  // Position `pos` reads stale cache here; it is replaced from LDS after the barrier.
+  const uint16_t* kbase = kc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  const uint16_t* vbase = vc + (int64_t)pair * cache_len * HD + l16 * EPL;
+  Vec<EPL> kv[AT_U], vv[AT_U];
+#pragma unroll
+  for (int u = 0; u < AT_U; ++u) {
+    const int t = min(t0 + g + u * AT_G, pos);
+    kv[u].load(kbase + (int64_t)t * HD);
+    vv[u].load(vbase + (int64_t)t * HD);
+  }
   // q heads of this kv head (and, in the owner chunk, the step's k head): one wave each
   const int nheads = REP + (owner ? 1 : 0);
   for (int hh = wave; hh < nheads; hh += AT_T / 64) {
@@ -456,18 +467,11 @@ __global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restric
   for (int h = 0; h < REP; ++h)
 #pragma unroll
     for (int e = 0; e < EPL; ++e) qv[h][e] = s_q[h * HD + l16 * EPL + e];
-  const uint16_t* kbase = kc + (int64_t)pair * cache_len * HD + l16 * EPL;
-  const uint16_t* vbase = vc + (int64_t)pair * cache_len * HD + l16 * EPL;
-  Vec<EPL> kv[AT_U], vv[AT_U];
 #pragma unroll
   for (int u = 0; u < AT_U; ++u) {
-    const int t = min(t0 + g + u * AT_G, pos);
-    if (t == pos) {  // this step's k and v: from LDS (the cache write above may not be visible yet)
+    if (min(t0 + g + u * AT_G, pos) == pos) {  // this step's k and v, from LDS
       kv[u].load_lds(s_knew + l16 * EPL);
       vv[u].load_lds(s_vnew + l16 * EPL);
-    } else {
-      kv[u].load(kbase + (int64_t)t * HD);
-      vv[u].load(vbase + (int64_t)t * HD);
     }
   }
   float m[REP], lsum[REP], acc[REP][EPL];
@@ -543,20 +547,46 @@ __global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restric
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
   }
-  // merge the records of every chunk of this pair (in chunk order)
+  // merge the records of every chunk of this pair (in chunk order): all loads issued at
+  // once into LDS (the group buffers are free), then combined from there
   const float* base = part + (int64_t)pair * nchunk * REP * (HD + 2);
-  for (int q2 = tid; q2 < REP * HD; q2 += AT_T) {
-    const int h = q2 / HD, d = q2 % HD;
-    float mx = -INFINITY;
-    for (int c = 0; c < nc; ++c) mx = fmaxf(mx, ld_agent_f(base + ((int64_t)c * REP + h) * (HD + 2) + HD));
-    float num = 0.f, den = 0.f;
-    for (int c = 0; c < nc; ++c) {
-      const float* r2 = base + ((int64_t)c * REP + h) * (HD + 2);
-      const float f = __expf(ld_agent_f(r2 + HD) - mx);
-      num += f * ld_agent_f(r2 + d);
-      den += f * ld_agent_f(r2 + HD + 1);
+  constexpr int REC = REP * (HD + 2);
+  constexpr int PASS = (AT_G * REP * HD) / REC;  // records staged per pass (>= 15)
+  constexpr int NE = (REP * HD + AT_T - 1) / AT_T;
+  float* s_rec = s_acc;  // the group buffers are free
+  float rmx[NE], rnum[NE], rden[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    rmx[i] = -INFINITY;
+    rnum[i] = 0.f;
+    rden[i] = 0.f;
+  }
+  for (int c0 = 0; c0 < nc; c0 += PASS) {
+    const int cn = min(PASS, nc - c0);
+    __syncthreads();  // the previous pass is consumed
+    for (int q2 = tid; q2 < cn * REC; q2 += AT_T) s_rec[q2] = ld_agent_f(base + (int64_t)c0 * REC + q2);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int q2 = tid + i * AT_T;
+      if (q2 >= REP * HD) break;
+      const int h = q2 / HD, d = q2 % HD;
+      for (int c = 0; c < cn; ++c) {
+        const float* r2 = s_rec + c * REC + h * (HD + 2);
+        const float mn = fmaxf(rmx[i], r2[HD]);
+        const float fo = __expf(rmx[i] - mn), fc = __expf(r2[HD] - mn);
+        rnum[i] = rnum[i] * fo + r2[d] * fc;
+        rden[i] = rden[i] * fo + r2[HD + 1] * fc;
+        rmx[i] = mn;
+      }
     }
-    out[((int64_t)b * nh + kvh * REP + h) * HD + d] = f32_to_bf16_bits(num / den);
+  }
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int q2 = tid + i * AT_T;
+    if (q2 >= REP * HD) break;
+    const int h = q2 / HD, d = q2 % HD;
+    out[((int64_t)b * nh + kvh * REP + h) * HD + d] = f32_to_bf16_bits(rnum[i] / rden[i]);
   }
 }
 
