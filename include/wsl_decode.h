@@ -90,6 +90,32 @@ int wsl_swiglu_fwd(const void* gate_up, int64_t ld, int64_t rows, int64_t ffn, v
  * with ldx % 8 == 0 are read 16 bytes at a time. */
 int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* stream);
 
+/* The fused LoRA linear of wsl_lora_linear_fwd (bf16 w, decode-shaped 1 <= M <= 64) with
+ * the decode step's elementwise work folded into the same launch. `fuse` combines:
+ *   WSL_FUSE_RMSNORM   the projection input is bf16(x * rsqrt(mean(x^2) + eps) * norm_w),
+ *                      the block's pre-attention / pre-FFN RMSNorm
+ *                      (qwen3/model/model.py:296-314, torch.nn.RMSNorm); norm_w [K] bf16;
+ *   WSL_FUSE_SWIGLU    w and b hold the gate and up projections' rows interleaved in blocks
+ *                      of 8 (rows 16j..16j+7 = gate rows 8j..8j+7, rows 16j+8..16j+15 = up
+ *                      rows 8j..8j+7), a = [A_gate; A_up] with b's columns to match, and
+ *                      y [M, N/2] = bf16(silu(gate) * up) (qwen3/model/model.py:250-251);
+ *   WSL_FUSE_RESIDUAL  y = bf16(residual + bf16(projection)), the residual add h + attn(h)
+ *                      or h + ffn(h) (qwen3/model/model.py:313-314); residual [M, ldr] bf16
+ *                      may be y itself (each element is read before it is written).
+ * SWIGLU and RESIDUAL exclude each other. M == 0 is a no-op. Errors, workspace and streams are those of
+ * wsl_lora_linear_fwd (its workspace size query applies), reported by wsl_last_error().
+ * Shapes the fused form does not cover return WSL_E_SHAPE; wsl_lora_linear_fused_supported
+ * answers from the sizes alone (1 or 0, taking 16-byte aligned operands). */
+#define WSL_FUSE_RMSNORM 1
+#define WSL_FUSE_SWIGLU 2
+#define WSL_FUSE_RESIDUAL 4
+int wsl_lora_linear_fused_supported(int64_t M, int64_t N, int64_t K, int64_t r, int32_t fuse);
+int wsl_lora_linear_fused_fwd(const void* x, int64_t ldx, const void* norm_w, float eps, const void* w,
+                              int64_t ldw, const void* a, int64_t lda, const void* b, int64_t ldb, float scale,
+                              const void* residual, int64_t ldr, void* y, int64_t ldy, int64_t M, int64_t N,
+                              int64_t K, int64_t r, int32_t fuse, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* Thread-local description of the last failure of an entry point above ("" if none). */
 const char* wsl_decode_last_error(void);
 

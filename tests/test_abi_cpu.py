@@ -201,3 +201,56 @@ def test_decode_step_validation_codes():
         == N.WSL_E_WORKSPACE
     # swiglu: ld below 2 * ffn
     assert lib.wsl_swiglu_fwd(P2, 100, 4, 64, P2, 64, None) == N.WSL_E_SHAPE
+
+
+@needs_lib
+@pytest.mark.parametrize("M,Nn,K,r,fuse,ok", [
+    (8, 4096, 2048, 96, 1, 1),      # q|k|v of the bench model with the RMSNorm prologue
+    (8, 12288, 2048, 32, 3, 1),     # gate|up with RMSNorm + SwiGLU
+    (8, 2048, 6144, 16, 4, 1),      # down projection + residual
+    (8, 256, 2048, 0, 1, 1),        # the head's first factor
+    (8, 4096, 4096, 96, 1, 0),      # M * K / 8 chunks above what the prologue holds
+    (8, 1000, 2048, 32, 3, 0),      # SwiGLU needs N % 16 == 0
+    (8, 4096, 256, 16, 1, 0),       # short K: the fused kernels take 8 waves along K
+    (8, 2048, 2048, 16, 6, 0),      # SwiGLU and residual exclude each other
+    (65, 2048, 2048, 16, 4, 0),     # not decode-shaped
+    (8, 2048, 2048, 12, 4, 0),      # r % 8 != 0
+])
+def test_fused_supported_answers_from_sizes(M, Nn, K, r, fuse, ok):
+    assert N.lib().wsl_lora_linear_fused_supported(M, Nn, K, r, fuse) == ok
+    assert N.last_error() == ""
+
+
+def _fused(**kw):
+    a = dict(x=P, ldx=2048, nw=P, eps=1e-6, w=P, ldw=2048, a=P, lda=2048, b=P, ldb=16, scale=2.0,
+             res=None, ldr=0, y=P, ldy=4096, M=8, N=4096, K=2048, r=16, fuse=1, ws=P, ws_bytes=1 << 24)
+    a.update(kw)
+    return N.lib().wsl_lora_linear_fused_fwd(a["x"], a["ldx"], a["nw"], a["eps"], a["w"], a["ldw"], a["a"],
+                                             a["lda"], a["b"], a["ldb"], a["scale"], a["res"], a["ldr"], a["y"],
+                                             a["ldy"], a["M"], a["N"], a["K"], a["r"], a["fuse"], a["ws"],
+                                             a["ws_bytes"], None)
+
+
+@needs_lib
+@pytest.mark.parametrize("kw,code", [
+    (dict(fuse=0), N.WSL_E_INVALID_ARG),
+    (dict(fuse=8), N.WSL_E_INVALID_ARG),
+    (dict(fuse=6, N=2048, ldy=2048, res=P, ldr=2048), N.WSL_E_INVALID_ARG),
+    (dict(nw=None), N.WSL_E_INVALID_ARG),
+    (dict(fuse=4), N.WSL_E_INVALID_ARG),                    # residual missing
+    (dict(M=65), N.WSL_E_SHAPE),
+    (dict(fuse=3, N=1000, ldy=500), N.WSL_E_SHAPE),         # SwiGLU with N % 16 != 0
+    (dict(fuse=3, ldy=2047), N.WSL_E_SHAPE),                # y is [M, N / 2]
+    (dict(fuse=4, res=P, ldr=4000), N.WSL_E_SHAPE),
+    (dict(K=4096, ldx=4096, ldw=4096, lda=4096), N.WSL_E_SHAPE),  # prologue capacity
+    (dict(ws_bytes=1024), N.WSL_E_WORKSPACE),
+    (dict(ws=P + 16), N.WSL_E_ALIGN),
+])
+def test_fused_validation_codes(kw, code):
+    assert _fused(**kw) == code
+    assert N.last_error() != ""
+
+
+@needs_lib
+def test_fused_empty_batch_is_a_no_op():
+    assert _fused(M=0, x=None, y=None, ws=None, ws_bytes=0) == N.WSL_OK

@@ -175,3 +175,108 @@ def test_decode_attention_step_equals_unfused(gpu, b, nh, nkv, hd, L, pos):
         assert rel(out, ref) <= TOL
     ws = ops.workspace(gpu, torch.cuda.current_stream(gpu).cuda_stream, 0, kind="attention")
     assert int(ws[:256].count_nonzero()) == 0, "arrival counters not restored to zero"
+
+
+def _interleave8(g, u):
+    n = g.shape[0]
+    return torch.stack((g.reshape(n // 8, 8, -1), u.reshape(n // 8, 8, -1)), 1).reshape(2 * n, -1).contiguous()
+
+
+def _lora_ref(xb, W, A, B, s):
+    """fp32 arithmetic on the bf16 input; T rounded to bf16 as the kernels publish it."""
+    y = xb.float() @ W.float().t()
+    if A is not None:
+        t = (s * (xb.float() @ A.float().t())).bfloat16().float()
+        y = y + t @ B.float().t()
+    return y
+
+
+@pytest.mark.parametrize("M,N,K,r,fuse", [
+    (8, 4096, 2048, 96, 1),     # q|k|v of the benchmark model
+    (1, 256, 1024, 16, 1),
+    (16, 520, 1024, 32, 1),     # 16 * 1024 / 8: the prologue's full capacity
+    (5, 1000, 3072, 24, 1),
+    (2, 264, 1152, 8, 1),       # K / 8 = 144 chunks: 16-lane groups straddle wave boundaries
+    (8, 256, 2048, 0, 1),       # the head's first factor (no adapter)
+    (8, 12288, 2048, 32, 3),    # gate|up of the benchmark model
+    (1, 512, 1024, 16, 3),
+    (3, 2000, 1024, 24, 3),
+    (8, 2048, 2048, 16, 4),     # o projection + residual
+    (8, 2048, 6144, 16, 4),     # down projection + residual
+    (5, 1000, 1024, 24, 4),     # N % 16 != 0: a partial last row block
+    (64, 512, 1024, 8, 4),
+    (4, 512, 1024, 16, 5),      # RMSNorm + residual
+])
+def test_fused_decode_linear(gpu, M, N, K, r, fuse):
+    """The fused forms against the fp32 reference of the same composition, twice in a row
+    (the launch and arrival counters carry over), and against the separate kernels."""
+    from weightshared_torchtitan_amd import ops
+    import weightshared_torchtitan_amd as wsl
+    _say(f"[fused linear] M={M} N={N} K={K} r={r} fuse={fuse}")
+    g = torch.Generator(device="cuda").manual_seed(M * 7 + N + K + fuse)
+    x = torch.randn(M, K, device=gpu, generator=g).bfloat16()
+    nw = (1 + 0.1 * torch.randn(K, device=gpu, generator=g)).bfloat16() if fuse & 1 else None
+    W = (torch.randn(N, K, device=gpu, generator=g) * K ** -0.5).bfloat16()
+    A = (torch.randn(r, K, device=gpu, generator=g) * K ** -0.5).bfloat16() if r else None
+    B = (torch.randn(N, r, device=gpu, generator=g) * 0.3).bfloat16() if r else None
+    res = torch.randn(M, N, device=gpu, generator=g).bfloat16() if fuse & 4 else None
+    s = 2.0
+    xin = rms_ref(x, nw, 1e-6).bfloat16() if fuse & 1 else x
+    y = _lora_ref(xin, W, A, B, s)
+    if fuse & 2:
+        # the same weights read as interleaved gate/up rows
+        yv = y.view(M, N // 16, 2, 8)
+        gate, up = yv[:, :, 0].reshape(M, N // 2), yv[:, :, 1].reshape(M, N // 2)
+        ref = torch.nn.functional.silu(gate.bfloat16().float()) * up.bfloat16().float()
+    else:
+        ref = y
+    if fuse & 4:
+        ref = res.float() + y.bfloat16().float()
+    for _ in range(2):
+        out = ops.lora_linear_fused_op(x, nw, 1e-6, W, A, B, s, res, fuse)
+        assert out.shape == ref.shape
+        assert rel(out, ref) <= TOL
+    # the separate kernels of the same step
+    sep_in = ops.rmsnorm_op(x, nw, 1e-6) if fuse & 1 else x
+    sep = wsl.lora_linear(sep_in, W, A, B, s) if r else wsl.lora_linear(sep_in, W)
+    if fuse & 2:
+        sv = sep.view(M, N // 16, 2, 8)
+        gu = torch.cat([sv[:, :, 0].reshape(M, N // 2), sv[:, :, 1].reshape(M, N // 2)], 1)
+        sep = ops.swiglu_op(gu)
+    if fuse & 4:
+        sep = (res.float() + sep.float()).bfloat16()
+    assert rel(out, sep) <= TOL
+
+
+def test_fused_swiglu_matches_separate_projections(gpu):
+    """Interleaving gate/up rows (and B's rows, with A = [A1; A3] and B block-diagonal) is
+    the two LoRA linears followed by SwiGLU."""
+    from weightshared_torchtitan_amd import ops
+    import weightshared_torchtitan_amd as wsl
+    _say("[fused swiglu pack] M=8 F=3072 K=2048 r=16")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    M, F, K, r = 8, 3072, 2048, 16
+    x = torch.randn(M, K, device=gpu, generator=g).bfloat16()
+    nw = (1 + 0.1 * torch.randn(K, device=gpu, generator=g)).bfloat16()
+    W1, W3 = [(torch.randn(F, K, device=gpu, generator=g) * K ** -0.5).bfloat16() for _ in range(2)]
+    A1, A3 = [(torch.randn(r, K, device=gpu, generator=g) * K ** -0.5).bfloat16() for _ in range(2)]
+    B1, B3 = [(torch.randn(F, r, device=gpu, generator=g) * 0.3).bfloat16() for _ in range(2)]
+    z = torch.zeros_like(B1)
+    W = _interleave8(W1, W3)
+    B = _interleave8(torch.cat([B1, z], 1), torch.cat([z, B3], 1))
+    A = torch.cat([A1, A3], 0)
+    out = ops.lora_linear_fused_op(x, nw, 1e-6, W, A, B, 2.0, None, 3)
+    xn = ops.rmsnorm_op(x, nw, 1e-6)
+    gate, up = wsl.lora_linear(xn, W1, A1, B1, 2.0), wsl.lora_linear(xn, W3, A3, B3, 2.0)
+    ref = torch.nn.functional.silu(gate.float()) * up.float()
+    assert rel(out, ref) <= TOL
+
+
+def test_fused_unsupported_shape_raises(gpu):
+    from weightshared_torchtitan_amd import ops
+    x = torch.randn(8, 4096, device=gpu).bfloat16()
+    W = torch.randn(256, 4096, device=gpu).bfloat16()
+    nw = torch.ones(4096, device=gpu).bfloat16()
+    assert not ops.lora_linear_fused_supported(8, 256, 4096, 0, 1)
+    with pytest.raises(ValueError):
+        ops.lora_linear_fused_op(x, nw, 1e-6, W, None, None, 0.0, None, 1)

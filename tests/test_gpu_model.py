@@ -77,3 +77,55 @@ def test_decode_step_logits_match_oracle(gpu):
         got = m.decode_step(toks[:, 10:11].to(gpu), pos, cache)
     ref = Q.reference_forward(p, a, toks)[:, -1]
     assert rel(got, ref) <= LOGIT_TOL
+
+
+def fused_args():
+    """A configuration the fused decode-step launches cover (K >= 1024 on every projection)."""
+    from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3Args
+    return SharedQwen3Args(dim=1024, n_layers=4, n_unique_blocks=2, n_heads=8, n_kv_heads=4, head_dim=128,
+                           hidden_dim=2048, vocab_size=1000, embed_rank=64, lora_rank=16, max_seq_len=64)
+
+
+def test_fused_decode_step_matches_oracle_and_unfused(gpu):
+    from weightshared_torchtitan_amd.qwen3_shared import KVCache, SharedQwen3
+    a = fused_args()
+    m = SharedQwen3(a)
+    m.init_random(seed=4, std=0.03)
+    m = m.to(gpu).to(torch.bfloat16)
+    p = {k: v.detach().float().cpu() for k, v in m.named_parameters()}
+    g = torch.Generator().manual_seed(8)
+    toks = torch.randint(0, a.vocab_size, (2, 11), generator=g)
+    assert m._fusion_plan(2, m._decode_pack())["on"], "the fused launches should cover this configuration"
+    outs = {}
+    for fused in (True, False):
+        m.decode_fusion = fused
+        cache = KVCache(a, 2, 16, gpu)
+        with torch.no_grad():
+            m(toks[:, :10].to(gpu), cache)
+            pos = torch.full((), 10, dtype=torch.int64, device=gpu)
+            outs[fused] = m.decode_step(toks[:, 10:11].to(gpu), pos, cache)
+    ref = Q.reference_forward(p, a, toks)[:, -1]
+    assert rel(outs[True], ref) <= LOGIT_TOL
+    assert rel(outs[True], outs[False].float().cpu()) <= LOGIT_TOL
+
+
+def test_fused_decode_graph_greedy_matches_oracle(gpu):
+    from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3
+    a = fused_args()
+    m = SharedQwen3(a)
+    m.init_random(seed=5, std=0.03)
+    m = m.to(gpu).to(torch.bfloat16)
+    p = {k: v.detach().float().cpu() for k, v in m.named_parameters()}
+    g = torch.Generator().manual_seed(9)
+    prompt = torch.randint(0, a.vocab_size, (2, 7), generator=g)
+    n_new = 5
+    with torch.no_grad():
+        new, _ = m.generate(prompt.to(gpu), n_new, use_graph=True)
+    new = new.cpu()
+    toks = prompt
+    for i in range(n_new):
+        ref = Q.reference_forward(p, a, toks)[:, -1]
+        tol = LOGIT_TOL * ref.abs().max(dim=-1).values
+        chosen = ref.gather(1, new[:, i:i + 1])[:, 0]
+        assert bool((chosen >= ref.max(dim=-1).values - tol).all()), f"step {i}"
+        toks = torch.cat([toks, new[:, i:i + 1]], 1)

@@ -23,6 +23,10 @@ WSL_E_WORKSPACE = -5
 WSL_E_DEVICE = -6
 WSL_E_LAUNCH = -7
 
+WSL_FUSE_RMSNORM = 1
+WSL_FUSE_SWIGLU = 2
+WSL_FUSE_RESIDUAL = 4
+
 WSL_DTYPE_BF16 = 0
 WSL_DTYPE_FP8_E4M3 = 1
 WSL_MAX_RANK = 256
@@ -42,6 +46,8 @@ EXPORTED = (
     "wsl_decode_attention_step_fwd",
     "wsl_swiglu_fwd",
     "wsl_argmax_rows_fwd",
+    "wsl_lora_linear_fused_supported",
+    "wsl_lora_linear_fused_fwd",
     "wsl_decode_last_error",
 )
 
@@ -103,6 +109,15 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, ctypes.c_size_t, _c_vp]                       # workspace, bytes, stream
     lib.wsl_swiglu_fwd.restype = ctypes.c_int
     lib.wsl_swiglu_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]
+    lib.wsl_lora_linear_fused_supported.restype = ctypes.c_int
+    lib.wsl_lora_linear_fused_supported.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32]
+    lib.wsl_lora_linear_fused_fwd.restype = ctypes.c_int
+    lib.wsl_lora_linear_fused_fwd.argtypes = [
+        _c_vp, _c_i64, _c_vp, ctypes.c_float, _c_vp, _c_i64,  # x, ldx, norm_w, eps, w, ldw
+        _c_vp, _c_i64, _c_vp, _c_i64, ctypes.c_float,          # a, lda, b, ldb, scale
+        _c_vp, _c_i64, _c_vp, _c_i64,                          # residual, ldr, y, ldy
+        _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32,        # M, N, K, r, fuse
+        _c_vp, ctypes.c_size_t, _c_vp]                         # workspace, bytes, stream
     lib.wsl_argmax_rows_fwd.restype = ctypes.c_int
     lib.wsl_argmax_rows_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]
     lib.wsl_factorized_embedding_fwd.restype = ctypes.c_int

@@ -37,11 +37,23 @@
 // and are dispatched first); past the bound it computes T itself, so the launch always
 // drains.
 //
+// Optional fusions serve the decode step of the weight-shared Qwen3 harness (bf16 W):
+//   RMSNorm prologue   the projection input is bf16(x * rsqrt(mean(x^2) + eps) * w_norm);
+//                      the raw rows and w_norm are staged into LDS by direct loads issued
+//                      ahead of the W loads, and every workgroup normalises the M rows in
+//                      place while its W loads are in flight;
+//   SwiGLU epilogue    W holds the gate and up rows interleaved in blocks of 8, so the two
+//                      halves of a 16-row MFMA block are g and u of the same 8 outputs, and
+//                      y = silu(g) * u;
+//   residual epilogue  y = bf16(res + bf16(o)), the block's residual add on the rounded
+//                      projection output (y may be res itself).
+//
 // fp8 base rows are decoded to bf16 in registers (v_cvt_pk_f32_fp8). Reference
 // arithmetic: the decode loop runs the same projections at small M
 // (scripts/generate/_generation.py:35-80 calling
 // torchtitan/models/llama3/model/model.py:189-192,392-398).
 #include <cstdlib>
+#include <type_traits>
 
 #include "wsl_common.h"
 
@@ -87,6 +99,12 @@ __device__ __forceinline__ void plain_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// This wave's LDS writes complete (lgkmcnt(0)), then the plain barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  plain_barrier();
+}
+
 // x slice in LDS: rows 0..M-1, kc bf16 each, 16-byte chunk c of row m stored at chunk
 // c ^ (m & 15) (kc is a multiple of 128, so the XOR stays inside the row). The 16 lanes
 // that read one chunk index of 16 different rows hit 16 distinct bank groups.
@@ -95,7 +113,9 @@ __device__ __forceinline__ int xs_off(int row, int k, int kc) {
 }
 
 // Direct global->LDS fill of x[0..M)[kbeg .. kbeg+kc): the wave instruction j writes
-// LDS bytes [1024 j, 1024 j + 1024), lane i the 16 bytes at 1024 j + 16 i.
+// LDS bytes [1024 j, 1024 j + 1024), lane i the 16 bytes at 1024 j + 16 i. SWZ places the
+// chunks as xs_off does; without it the rows are stored as they are.
+template <bool SWZ = true>
 __device__ __forceinline__ void fill_x(char* xs, const uint16_t* __restrict__ x, int64_t ldx,
                                        int M, int kbeg, int kc, int wave, int lane) {
   const int cpr = kc >> 3;  // chunks per row
@@ -104,7 +124,7 @@ __device__ __forceinline__ void fill_x(char* xs, const uint16_t* __restrict__ x,
     const int p = j * 64 + lane;
     if (p < total) {
       const int row = p / cpr;
-      const int c = (p - row * cpr) ^ (row & 15);
+      const int c = SWZ ? ((p - row * cpr) ^ (row & 15)) : (p - row * cpr);
       const void* src = x + (int64_t)row * ldx + kbeg + c * 8;
       __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(xs + j * 1024), 16, 0, 0);
     }
@@ -185,6 +205,10 @@ __device__ __forceinline__ void mma_step(const u32x4_t (&wv)[NR][4], const char*
 
 struct DecodeArgs {
   const uint16_t* x; int64_t ldx;
+  // RMSNorm prologue: x := bf16(x * rsqrt(mean(x^2) + eps) * nw), nw staged at LDS nw_off
+  const uint16_t* nw; float eps; int nw_off;
+  // residual epilogue: y := bf16(res + bf16(y))
+  const uint16_t* res; int64_t ldr;
   const void* w; int64_t ldw; const float* w_scale;
   const uint16_t* a; int64_t lda;
   const uint16_t* b; int64_t ldb;
@@ -226,9 +250,14 @@ __device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
 // Sums over one K slice of a group of 16*NR rows of `mat` against x (whose fill into
 // smem this wave has issued just before), reduced over the waves into sums[row][m]
 // (LDS, fp32, stride 16*MB). The x slice's LDS is reused for the reduction.
-template <int WDT, int NR, int MB, int KW>
+struct NoPrologue {
+  __device__ __forceinline__ void operator()() const {}
+};
+
+template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue>
 __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
-                                           int kbeg, int kc, int M, char* smem, float* sums) {
+                                           int kbeg, int kc, int M, char* smem, float* sums,
+                                           const Pro& pro = Pro()) {
   using G = Geo<WDT>;
   constexpr int PD = NR == 1 ? 4 : 2;   // K steps in flight per wave
   constexpr int LPS = NR * 4;           // loads per step
@@ -263,7 +292,7 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
     for (int mb = 0; mb < MB; ++mb) acc[i][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // The x / B fills were issued before the W loads: wait until only the W loads are
-  // outstanding, then for every wave's fills.
+  // outstanding, then for every wave's fills (and LDS writes made before the call).
   const int npf = my < PD ? my : PD;
   if (npf == 0) wait_vm<0>();
   else if (npf == 1) wait_vm<LPS>();
@@ -272,7 +301,9 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
     if (npf == 3) wait_vm<3 * LPS>();
     else wait_vm<4 * LPS>();
   }
-  plain_barrier();
+  lds_barrier();
+  pro();  // the x slice computed from what the fills staged (W loads still in flight)
+  if constexpr (!std::is_same<Pro, NoPrologue>::value) plain_barrier();
 
   for (int i0 = 0; i0 < my; i0 += PD) {
 #pragma unroll
@@ -355,8 +386,25 @@ __device__ __forceinline__ bool split_reduce(float* sums, float* part, unsigned*
 // T[m][j] (bf16) into LDS tl[m][0..r32) (row stride r32 + 8 elements), zero for m >= M
 // or j >= r. Polls (bounded) until every element carries this launch's tag; past the
 // bound computes T itself from x and A.
-template <int MC>
-__device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint64_t tag, int* flag) {
+// Eight consecutive elements of the projection input x[m][k..k+8): x itself, or with the
+// RMSNorm prologue bf16(x * rsqrt(ss[m] / K + eps) * w_norm).
+template <bool NORM>
+__device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, int m, int k, float (&v)[8]) {
+  const u32x4_t xv = ld_global_16(p.x + (int64_t)m * p.ldx + k);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32((xv[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+  if constexpr (NORM) {
+    const u32x4_t wv = ld_global_16(p.nw + k);
+    const float inv = rsqrtf(ss[m] / (float)p.K + p.eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] * inv * bf16_bits_to_f32((wv[e >> 1] >> ((e & 1) * 16)) & 0xffffu)));
+  }
+}
+
+template <int MC, bool NORM = false>
+__device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint64_t tag, int* flag,
+                                         const float* ss = nullptr) {
   const int tid = threadIdx.x;
   const int tls = p.r32 + 8;
   for (int q = tid; q < MC * tls; q += DT) tl[q] = 0;
@@ -380,16 +428,14 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
   if (!ok) {
     for (int q = tid; q < n; q += DT) {
       const int m = q / p.r, j = q % p.r;
-      const uint16_t* xr = p.x + (int64_t)m * p.ldx;
       const uint16_t* ar = p.a + (int64_t)j * p.lda;
       float acc = 0.f;
       for (int k = 0; k < p.K; k += 8) {
-        const u32x4_t xv = ld_global_16(xr + k), av = ld_global_16(ar + k);
+        float xv[8];
+        load_x8<NORM>(p, ss, m, k, xv);
+        const u32x4_t av = ld_global_16(ar + k);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc += bf16_bits_to_f32(xv[e] & 0xffffu) * bf16_bits_to_f32(av[e] & 0xffffu);
-          acc += bf16_bits_to_f32(xv[e] >> 16) * bf16_bits_to_f32(av[e] >> 16);
-        }
+        for (int e = 0; e < 8; ++e) acc += xv[e] * bf16_bits_to_f32((av[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
       }
       tl[m * tls + j] = f32_to_bf16_bits(p.s * acc);
     }
@@ -397,8 +443,81 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
   __syncthreads();
 }
 
-template <int WDT, int NR, int MB, int KW>
+constexpr int NORM_CH = 4;  // 16-byte chunks of x per thread in the RMSNorm prologue
+constexpr int kFuseNorm = 1, kFuseAct = 2, kFuseRes = 4;
+constexpr int kNormLds = 64 * 4 + NORM_CH * DT / 16 * 4;  // row sums + slots
+
+// RMSNorm prologue, run by slice_sums once the direct fills have landed: the raw rows
+// x[0..M)[0..K) sit unswizzled in the x-slice region (chunk q of the M*K/8 at byte 16 q)
+// and w_norm at nws. Each thread takes up to NORM_CH chunks into registers; every 16
+// consecutive chunks (one 16-lane group, inside one row as K/8 is a multiple of 16) leave
+// their sum of squares in slot q/16, so row m owns the K/128 slots from m*K/128 on and its
+// sum is taken over them in a fixed order (plain LDS stores: an LDS atomic would make the
+// compiler wait for the W loads in flight). After a barrier every chunk is written back at
+// its swizzled place as bf16(x * rsqrt(sum / K + eps) * w_norm); threads m < M also leave
+// the row sum in ss[m] for the T fallback.
+struct NormPrologue {
+  const DecodeArgs* p;
+  char* xs;
+  float* ss;      // [64] row sums, then [NORM_CH * DT / 16] slots
+  const char* nws;
+
+  __device__ __forceinline__ float row_sum(const float* slots, int m, int spr) const {
+    float t = 0.f;
+    for (int k = 0; k < spr; ++k) t += slots[m * spr + k];
+    return t;
+  }
+
+  __device__ __forceinline__ void operator()() const {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int cpr = p->K >> 3;
+    const int spr = cpr >> 4;  // slots per row
+    const int total = p->M * cpr;
+    float* slots = ss + 64;
+    float h[NORM_CH][8];
+#pragma unroll
+    for (int j = 0; j < NORM_CH; ++j) {
+      const int q = tid + j * DT;
+      float part = 0.f;
+      if (q < total) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xs + q * 16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          h[j][e] = bf16_bits_to_f32((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+          part += h[j][e] * h[j][e];
+        }
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      if ((lane & 15) == 0 && q < total) slots[q >> 4] = part;
+    }
+    lds_barrier();  // every chunk is in registers and every slot written
+    if (tid < p->M) ss[tid] = row_sum(slots, tid, spr);
+#pragma unroll
+    for (int j = 0; j < NORM_CH; ++j) {
+      const int q = tid + j * DT;
+      if (q < total) {
+        const int m = q / cpr, c = q - m * cpr;
+        const float inv = rsqrtf(row_sum(slots, m, spr) / (float)p->K + p->eps);
+        const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(nws + c * 16);
+        u32x4_t ov;
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2)
+          ov[q2] = pack_bf16x2(h[j][2 * q2] * inv * bf16_bits_to_f32(wv[q2] & 0xffffu),
+                               h[j][2 * q2 + 1] * inv * bf16_bits_to_f32(wv[q2] >> 16));
+        *reinterpret_cast<u32x4_t*>(xs + xs_off(m, c * 8, p->K)) = ov;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // written before the caller's barrier
+  }
+};
+
+template <int WDT, int NR, int MB, int KW, int FUSE>
 __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
+  constexpr bool NORM = (FUSE & kFuseNorm) != 0;
+  constexpr bool ACT = (FUSE & kFuseAct) != 0;
+  constexpr bool RES = (FUSE & kFuseRes) != 0;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   constexpr int RBK = NWV / KW;         // row blocks per workgroup
   constexpr int ROWS = RBK * 16 * NR;   // W rows per workgroup
@@ -420,8 +539,16 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
     const int kbeg = ks * p.kct;
     constexpr int RED_T = (NWV - RBK) * MB * 4 * 64 * 4;
     float* sums = reinterpret_cast<float*>(smem + RED_T);
-    fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
-    slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums);
+    if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
+      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
+      fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
+      fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
+      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums,
+                                   NormPrologue{&p, smem, ss, smem + p.nw_off});
+    } else {
+      fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
+      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums);
+    }
     if (split_reduce<TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, p.cnt + CNT_TG + g, ks,
                                 p.kst, p.M, flag)) {
       for (int q = tid; q < p.M * TROWS; q += DT) {
@@ -441,12 +568,21 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
     char* bl = smem + (xs_bytes > post ? xs_bytes : post);
     float* sums = reinterpret_cast<float*>(smem + RED);
     uint16_t* tl = reinterpret_cast<uint16_t*>(smem + RED + ROWS * MC * 4);
-    fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kcy, wave, lane);
-    if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
-    slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
+    if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
+      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
+      fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
+      fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
+      if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
+      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums,
+                                  NormPrologue{&p, smem, ss, smem + p.nw_off});
+    } else {
+      fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kcy, wave, lane);
+      if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
+      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
+    }
     if (split_reduce<ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, p.cnt + CNT_YG + g, ks,
                                p.ksy, p.M, flag)) {
-      if (p.r > 0) gather_t<MC>(p, tl, tag, flag);
+      if (p.r > 0) gather_t<MC, NORM>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16));
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
       const int l16 = lane & 15, grp = lane >> 4;
       const int tls = p.r32 + 8;
@@ -461,7 +597,22 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
         // d: lane holds token m = mb*16 + l16, rows i*16 + grp*4 + e
         const int m = mb * 16 + l16;
         const int n0 = row0 + i * 16 + grp * 4;
-        if (m < p.M) {
+        if constexpr (ACT) {
+          // rows 0-7 of the block are gate rows, 8-15 the up rows of the same 8 outputs:
+          // lane l (groups 0, 1) pairs with lane l + 32 (groups 2, 3)
+          float o[4], u[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = sums[(i * 16 + grp * 4 + e) * MC + m] + d[e];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) u[e] = __shfl_xor(o[e], 32, 64);
+          const int f0 = (row0 + i * 16) / 2 + grp * 4;
+          if (m < p.M && grp < 2 && 2 * f0 < p.N) {
+            uint2 pk;
+            pk.x = pack_bf16x2(o[0] / (1.f + __expf(-o[0])) * u[0], o[1] / (1.f + __expf(-o[1])) * u[1]);
+            pk.y = pack_bf16x2(o[2] / (1.f + __expf(-o[2])) * u[2], o[3] / (1.f + __expf(-o[3])) * u[3]);
+            *reinterpret_cast<uint2*>(p.y + (int64_t)m * p.ldy + f0) = pk;
+          }
+        } else if (m < p.M) {
           float o[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -469,6 +620,20 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
             float v = sums[(i * 16 + grp * 4 + e) * MC + m];
             if (p.w_scale != nullptr && n < p.N) v *= p.w_scale[n];
             o[e] = v + d[e];
+          }
+          if constexpr (RES) {  // y = bf16(res + bf16(o)); res may be y itself (read first)
+            const uint16_t* rr = p.res + (int64_t)m * p.ldr;
+            if (n0 + 3 < p.N) {
+              const uint2 rv = *reinterpret_cast<const uint2*>(rr + n0);
+              o[0] = bf16_bits_to_f32(rv.x & 0xffffu) + bf16_round(o[0]);
+              o[1] = bf16_bits_to_f32(rv.x >> 16) + bf16_round(o[1]);
+              o[2] = bf16_bits_to_f32(rv.y & 0xffffu) + bf16_round(o[2]);
+              o[3] = bf16_bits_to_f32(rv.y >> 16) + bf16_round(o[3]);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (n0 + e < p.N) o[e] = bf16_bits_to_f32(rr[n0 + e]) + bf16_round(o[e]);
+            }
           }
           uint16_t* yr = p.y + (int64_t)m * p.ldy;
           if (n0 + 3 < p.N) {
@@ -521,7 +686,7 @@ size_t plan_smem(const DecodePlan& pl, int64_t M, size_t* flag_off) {
   const size_t red = (size_t)(NWV - NWV / pl.kw) * pl.nr * pl.mb * 4 * 64 * 4;
   const size_t post = red + (size_t)pl.rows * 16 * pl.mb * 4 + (size_t)16 * pl.mb * (pl.r32 + 8) * 2;
   *flag_off = (xs > post ? xs : post) + (size_t)pl.rows * pl.r32 * 2;
-  return *flag_off + 16;
+  return *flag_off + 16;  // the broadcast word (the RMSNorm prologue adds its own after it)
 }
 
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
@@ -570,17 +735,27 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
   return pl;
 }
 
-template <int WDT, int NR, int MB, int KW>
+template <int WDT, int NR, int MB, int KW, int FUSE = 0>
 hipError_t launch_one(const DecodeArgs& a, int grid, size_t smem, hipStream_t st) {
   static bool ready = false;  // the attribute is per kernel; setting it twice is harmless
   if (!ready) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<WDT, NR, MB, KW>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<WDT, NR, MB, KW, FUSE>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
     if (e != hipSuccess) return e;
     ready = true;
   }
-  decode_kernel<WDT, NR, MB, KW><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a);
+  decode_kernel<WDT, NR, MB, KW, FUSE><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a);
   return hipGetLastError();
+}
+
+template <int FUSE>
+hipError_t dispatch_fused(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
+  if (nr == 1) {
+    if (mb == 1) return launch_one<kBF16, 1, 1, 8, FUSE>(a, grid, smem, st);
+    return launch_one<kBF16, 1, 2, 8, FUSE>(a, grid, smem, st);
+  }
+  if (mb == 3) return launch_one<kBF16, 2, 3, 8, FUSE>(a, grid, smem, st);
+  return launch_one<kBF16, 2, 4, 8, FUSE>(a, grid, smem, st);
 }
 
 template <int WDT, int KW>
@@ -637,8 +812,8 @@ size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_
   return plan_decode(M, N, K, r, w_dtype).total;
 }
 
-hipError_t launch_decode(const LoraArgs& p) {
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
+namespace {
+DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl) {
   char* ws = reinterpret_cast<char*>(p.ws);
   DecodeArgs a{};
   a.x = reinterpret_cast<const uint16_t*>(p.x); a.ldx = p.ldx;
@@ -656,9 +831,53 @@ hipError_t launch_decode(const LoraArgs& p) {
   a.tpart = reinterpret_cast<float*>(ws + pl.off_pt);
   a.ypart = reinterpret_cast<float*>(ws + pl.off_py);
   a.spin = spin_limit();
+  return a;
+}
+}  // namespace
+
+hipError_t launch_decode(const LoraArgs& p) {
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
+  const DecodeArgs a = make_args(p, pl);
   const int grid = pl.gT * pl.kst + pl.gY * pl.ksy;
   return p.w_dtype == kFP8 ? dispatch<kFP8>(a, pl.mb, pl.nr, pl.kw, grid, pl.smem, p.stream)
                            : dispatch<kBF16>(a, pl.mb, pl.nr, pl.kw, grid, pl.smem, p.stream);
+}
+
+bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
+  if (f.fuse < 1 || f.fuse > 7 || ((f.fuse & kFuseAct) && (f.fuse & kFuseRes))) return false;
+  if (!decode_supported(p) || p.w_dtype != kBF16) return false;
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
+  if (pl.kw != 8) return false;
+  if (f.fuse & kFuseNorm) {
+    // whole rows in one slice, up to NORM_CH chunks per thread, w_norm staged after the plan's LDS
+    if (pl.ksy != 1 || (p.r > 0 && pl.kst != 1)) return false;
+    if (p.M * (p.K / 8) > (int64_t)NORM_CH * DT) return false;
+    if (f.nw == nullptr || !aligned16(f.nw)) return false;
+    if (pl.smem + (size_t)kNormLds + (size_t)p.K * 2 > (size_t)LDS_MAX) return false;
+  }
+  if ((f.fuse & kFuseAct) && p.N % 16 != 0) return false;
+  if (f.fuse & kFuseRes) {
+    if (f.res == nullptr || (reinterpret_cast<uintptr_t>(f.res) & 7u) != 0 || f.ldr % 4 != 0) return false;
+  }
+  return true;
+}
+
+hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
+  DecodeArgs a = make_args(p, pl);
+  a.nw = reinterpret_cast<const uint16_t*>(f.nw); a.eps = f.eps;
+  a.nw_off = (int)pl.flag_off + 16 + kNormLds;
+  a.res = reinterpret_cast<const uint16_t*>(f.res); a.ldr = f.ldr;
+  const size_t smem = pl.smem + ((f.fuse & kFuseNorm) ? (size_t)kNormLds + (size_t)p.K * 2 : 0);
+  const int grid = pl.gT * pl.kst + pl.gY * pl.ksy;
+  switch (f.fuse) {
+    case kFuseNorm: return dispatch_fused<kFuseNorm>(a, pl.mb, pl.nr, grid, smem, p.stream);
+    case kFuseNorm | kFuseAct: return dispatch_fused<kFuseNorm | kFuseAct>(a, pl.mb, pl.nr, grid, smem, p.stream);
+    case kFuseAct: return dispatch_fused<kFuseAct>(a, pl.mb, pl.nr, grid, smem, p.stream);
+    case kFuseRes: return dispatch_fused<kFuseRes>(a, pl.mb, pl.nr, grid, smem, p.stream);
+    case kFuseNorm | kFuseRes: return dispatch_fused<kFuseNorm | kFuseRes>(a, pl.mb, pl.nr, grid, smem, p.stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace wsl

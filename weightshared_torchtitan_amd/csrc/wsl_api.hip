@@ -7,6 +7,7 @@
 #include <cstring>
 #include <mutex>
 
+#include "../../include/wsl_decode.h"
 #include "../../include/wsl_lora.h"
 #include "wsl_common.h"
 
@@ -172,6 +173,64 @@ int wsl_lora_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, 
     case Path::kPrefill: e = wsl::launch_prefill(p); break;
     default: e = wsl::launch_generic(p); break;
   }
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
+int wsl_lora_linear_fused_supported(int64_t M, int64_t N, int64_t K, int64_t r, int32_t fuse) {
+  const bool sizes_ok = validate_sizes(M, N, K, r, WSL_DTYPE_BF16) == WSL_OK && M >= 1;
+  clear_err();  // a query leaves no error behind
+  if (!sizes_ok) return 0;
+  // the sizes alone: every operand taken as 16-byte aligned with tight leading dimensions
+  static char kAligned[16] __attribute__((aligned(16))) = {0};
+  wsl::LoraArgs p;
+  p.x = kAligned; p.ldx = K; p.w = kAligned; p.ldw = K; p.w_dtype = WSL_DTYPE_BF16; p.w_scale = nullptr;
+  p.a = kAligned; p.lda = K; p.b = kAligned; p.ldb = r; p.scale = 1.f;
+  p.y = kAligned; p.ldy = (fuse & WSL_FUSE_SWIGLU) ? N / 2 : N;
+  p.M = M; p.N = N; p.K = K; p.r = r; p.ws = nullptr; p.ws_bytes = 0; p.stream = nullptr;
+  p.gather = nullptr; p.gather_rows = 0;
+  if (p.ldy % 4 != 0 || (r > 0 && r % 8 != 0)) return 0;
+  const wsl::FusedArgs f{fuse, kAligned, 1e-6f, kAligned, N};
+  return wsl::decode_fused_supported(p, f) ? 1 : 0;
+}
+
+int wsl_lora_linear_fused_fwd(const void* x, int64_t ldx, const void* norm_w, float eps, const void* w,
+                              int64_t ldw, const void* a, int64_t lda, const void* b, int64_t ldb, float scale,
+                              const void* residual, int64_t ldr, void* y, int64_t ldy, int64_t M, int64_t N,
+                              int64_t K, int64_t r, int32_t fuse, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  clear_err();
+  int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
+  if (rc != WSL_OK) return rc;
+  if (fuse < 1 || fuse > 7 || ((fuse & WSL_FUSE_SWIGLU) && (fuse & WSL_FUSE_RESIDUAL)))
+    return fail(WSL_E_INVALID_ARG, "fuse must combine WSL_FUSE_* flags (SWIGLU and RESIDUAL exclude each other)");
+  if (M == 0) return WSL_OK;
+  if (M > wsl::kDecodeMaxM) return fail(WSL_E_SHAPE, "the fused form is decode-shaped: M <= 64");
+  if (x == nullptr || w == nullptr || y == nullptr) return fail(WSL_E_INVALID_ARG, "x, w and y must not be NULL");
+  if (r > 0 && (a == nullptr || b == nullptr)) return fail(WSL_E_INVALID_ARG, "r > 0 needs a and b");
+  if ((fuse & WSL_FUSE_RMSNORM) && norm_w == nullptr) return fail(WSL_E_INVALID_ARG, "norm_w must not be NULL");
+  if ((fuse & WSL_FUSE_RESIDUAL) && residual == nullptr)
+    return fail(WSL_E_INVALID_ARG, "residual must not be NULL");
+  if (ldx < K || ldw < K || (r > 0 && (lda < K || ldb < r))) return fail(WSL_E_SHAPE, "leading dimension too small");
+  if ((fuse & WSL_FUSE_SWIGLU) && N % 16 != 0) return fail(WSL_E_SHAPE, "SwiGLU needs N % 16 == 0 (interleaved rows)");
+  const int64_t ny = (fuse & WSL_FUSE_SWIGLU) ? N / 2 : N;
+  if (ldy < ny) return fail(WSL_E_SHAPE, "ldy too small");
+  if ((fuse & WSL_FUSE_RESIDUAL) && ldr < N) return fail(WSL_E_SHAPE, "ldr < N");
+  wsl::LoraArgs p;
+  p.x = x; p.ldx = ldx; p.w = w; p.ldw = ldw; p.w_dtype = WSL_DTYPE_BF16; p.w_scale = nullptr;
+  p.a = a; p.lda = lda; p.b = b; p.ldb = ldb; p.scale = scale; p.y = y; p.ldy = ldy;
+  p.M = M; p.N = N; p.K = K; p.r = r; p.ws = workspace; p.ws_bytes = workspace_bytes;
+  p.stream = reinterpret_cast<hipStream_t>(stream); p.gather = nullptr; p.gather_rows = 0;
+  const wsl::FusedArgs f{fuse, norm_w, eps, residual, ldr};
+  if (!wsl::decode_fused_supported(p, f))
+    return fail(WSL_E_SHAPE, "the fused form does not cover this shape or alignment (wsl_lora_linear_fused_supported)");
+  const size_t need = wsl::decode_workspace_bytes(M, N, K, r, WSL_DTYPE_BF16);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((uintptr_t)workspace & 255) return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
+  rc = check_device();
+  if (rc != WSL_OK) return rc;
+  const hipError_t e = wsl::launch_decode_fused(p, f);
   if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return WSL_OK;
 }

@@ -26,6 +26,9 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
+// fp32 rounded to the nearest bf16 value.
+__device__ __forceinline__ float bf16_round(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
 // Two fp32 -> packed bf16x2 (low half = a).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
@@ -98,6 +101,16 @@ bool prefill_supported(const LoraArgs& p);
 hipError_t launch_decode(const LoraArgs& p);
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool decode_supported(const LoraArgs& p);
+
+// Decode-step fusions of the decode kernel (bit 0: RMSNorm prologue on x, bit 1: SwiGLU
+// epilogue over interleaved gate/up rows, bit 2: residual-add epilogue).
+struct FusedArgs {
+  int fuse;
+  const void* nw; float eps;      // RMSNorm weight [K] and epsilon
+  const void* res; int64_t ldr;   // residual added to the output
+};
+bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f);
+hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f);
 
 hipError_t launch_generic(const LoraArgs& p);
 

@@ -386,3 +386,49 @@ def decode_attention_step_op(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w
 def _decode_attention_step_fake(qkv, q_norm_w, k_norm_w, eps, rope, pos, k_cache, v_cache, n_heads, n_kv_heads,
                                 scale):
     return qkv.new_empty((k_cache.shape[0], n_heads * k_cache.shape[3]), dtype=torch.bfloat16)
+
+
+def lora_linear_fused_supported(M: int, N: int, K: int, r: int, fuse: int) -> bool:
+    """Whether wsl::lora_linear_fused covers these sizes (16-byte aligned operands)."""
+    return bool(_native.lib().wsl_lora_linear_fused_supported(M, N, K, r, fuse))
+
+
+@torch.library.custom_op("wsl::lora_linear_fused", mutates_args=(), device_types="cuda")
+def lora_linear_fused_op(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: float, w: torch.Tensor,
+                         a: Optional[torch.Tensor], b: Optional[torch.Tensor], scale: float,
+                         residual: Optional[torch.Tensor], fuse: int) -> torch.Tensor:
+    """The decode-step fused LoRA linear (include/wsl_decode.h): bf16 W, 1 <= M <= 64, with
+    an RMSNorm prologue on x (norm_w), a SwiGLU epilogue over interleaved gate/up rows
+    (y [M, N/2]) and/or a residual-add epilogue (y = bf16(residual + bf16(y)))."""
+    dev = _check_device(x, norm_w, w, a, b, residual)
+    x2 = _bf16_2d(x, "x")
+    M, K = x2.shape
+    N = w.shape[0]
+    nw = norm_w.to(torch.bfloat16).contiguous() if norm_w is not None else None
+    res = _bf16_2d(residual, "residual") if residual is not None else None
+    w = _row_major(w, "w")
+    r = 0
+    if a is not None:
+        a, b = _row_major(a, "a"), _row_major(b, "b")
+        r = a.shape[0]
+    ny = N // 2 if fuse & _native.WSL_FUSE_SWIGLU else N
+    y = torch.empty((M, ny), dtype=torch.bfloat16, device=dev)
+    stream = _stream(dev)
+    ws = workspace(dev, stream, _native.workspace_bytes(M, N, K, r, _native.WSL_DTYPE_BF16))
+    with torch.cuda.device(dev):
+        rc = _native.lib().wsl_lora_linear_fused_fwd(
+            x2.data_ptr(), x2.stride(0), _dev_ptr(nw), float(eps), w.data_ptr(), w.stride(0),
+            _dev_ptr(a), a.stride(0) if a is not None else 0, _dev_ptr(b), b.stride(0) if b is not None else 0,
+            float(scale), _dev_ptr(res), res.stride(0) if res is not None else 0, y.data_ptr(), y.stride(0),
+            M, N, K, r, int(fuse), ws.data_ptr(), ws.numel(), stream)
+    if rc != _native.WSL_OK:
+        _workspaces.pop((dev.index, stream, "lora"), None)
+    _native.check(rc, "wsl_lora_linear_fused_fwd")
+    return y
+
+
+@lora_linear_fused_op.register_fake
+def _lora_linear_fused_fake(x, norm_w, eps, w, a, b, scale, residual, fuse):
+    M = x.reshape(-1, x.shape[-1]).shape[0]
+    ny = w.shape[0] // 2 if fuse & 2 else w.shape[0]
+    return x.new_empty((M, ny), dtype=torch.bfloat16)

@@ -284,14 +284,56 @@ class SharedQwen3(nn.Module):
                 r0, c0 = r0 + n, c0 + r
             return A, B, scales.pop()
 
+        def interleave8(g, u):
+            # rows 16j..16j+7 <- g rows 8j..8j+7, rows 16j+8..16j+15 <- u rows 8j..8j+7
+            n = g.shape[0]
+            return torch.stack((g.reshape(n // 8, 8, -1), u.reshape(n // 8, 8, -1)), 1).reshape(2 * n, -1)
+
+        def gu_interleaved(layer, blk):
+            w1, w3 = blk.base("w1").weight, blk.base("w3").weight
+            if w1.shape[0] % 8 != 0:
+                return None
+            lo = self.layer_loras[layer]
+            if lo.w1.scale != lo.w3.scale:
+                return None
+            b1, b3 = lo.w1.w_b.weight, lo.w3.w_b.weight
+            A = torch.cat([lo.w1.w_a.weight, lo.w3.w_a.weight], 0).contiguous()
+            B = interleave8(torch.cat([b1, torch.zeros_like(b3)], 1), torch.cat([torch.zeros_like(b1), b3], 1))
+            return A, B.contiguous(), lo.w1.scale
+
         with torch.no_grad():
             pk = {"key": key,
                   "w_qkv": [cat_w(blk, ("wq", "wk", "wv")) for blk in self.base_blocks],
                   "w_gu": [cat_w(blk, ("w1", "w3")) for blk in self.base_blocks],
                   "l_qkv": [cat_lora(l, ("wq", "wk", "wv")) for l in range(a.n_layers)],
                   "l_gu": [cat_lora(l, ("w1", "w3")) for l in range(a.n_layers)]}
+            if a.hidden_dim % 8 == 0:
+                pk["w_gu_il"] = [interleave8(blk.base("w1").weight, blk.base("w3").weight).contiguous()
+                                 for blk in self.base_blocks]
+                pk["l_gu_il"] = [gu_interleaved(l, self.base_blocks[a.block_of(l)]) for l in range(a.n_layers)]
         self._pack_cache = pk
         return pk
+
+    def _fusion_plan(self, b: int, pk: dict) -> dict:
+        """Which decode-step launches take the fused forms (include/wsl_decode.h) at batch b:
+        q|k|v with the RMSNorm prologue, o and down projections with the residual epilogue,
+        gate|up with RMSNorm + SwiGLU, the head's first factor with RMSNorm. A group whose
+        adapters differ in scale, or whose shape the fused kernel does not cover, keeps the
+        separate kernels."""
+        a = self.args
+        r = a.lora_rank
+        sup = ops.lora_linear_fused_supported
+        qkv_n = (a.n_heads + 2 * a.n_kv_heads) * a.head_dim
+        plan = {
+            "qkv": all(x is not None for x in pk["l_qkv"]) and sup(b, qkv_n, a.dim, 3 * r, 1),
+            "wo": sup(b, a.dim, a.n_heads * a.head_dim, r, 4),
+            "gu": "l_gu_il" in pk and all(x is not None for x in pk["l_gu_il"])
+                  and sup(b, 2 * a.hidden_dim, a.dim, 2 * r, 3),
+            "w2": sup(b, a.dim, a.hidden_dim, r, 4),
+            "head": sup(b, a.embed_rank, a.dim, 0, 1),
+        }
+        plan["on"] = self.decode_fusion and all(plan.values())
+        return plan
 
     def _rope32(self) -> torch.Tensor:
         """The RoPE table in fp32 (the `rope` buffer follows the module's dtype, and cos/sin
@@ -311,6 +353,31 @@ class SharedQwen3(nn.Module):
         A, B, sc = lo
         return ops.lora_linear(x, w, A, B, sc)
 
+    decode_fusion = True  # use the fused decode-step launches where _fusion_plan allows
+
+    def _decode_step_fused(self, h, pos, cache, pk, rope) -> torch.Tensor:
+        """The decode step in five launches per layer: q|k|v (RMSNorm prologue), the fused
+        attention step, o projection (+ residual), gate|up (RMSNorm prologue, SwiGLU
+        epilogue), down projection (+ residual)."""
+        a = self.args
+        b = h.shape[0]
+        sm_scale = a.head_dim ** -0.5
+        fl = ops.lora_linear_fused_op
+        for l in range(a.n_layers):
+            blk = self.base_blocks[a.block_of(l)]
+            lo = self.layer_loras[l]
+            A, B, sc = pk["l_qkv"][l]
+            qkv = fl(h, blk.attention_norm.weight, a.norm_eps, pk["w_qkv"][a.block_of(l)], A, B, sc, None, 1)
+            o = ops.decode_attention_step_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight,
+                                             a.norm_eps, rope, pos, cache.k[l], cache.v[l], a.n_heads,
+                                             a.n_kv_heads, sm_scale)
+            h = fl(o, None, 0.0, blk.base("wo").weight, lo.wo.w_a.weight, lo.wo.w_b.weight, lo.wo.scale, h, 4)
+            A, B, sc = pk["l_gu_il"][l]
+            act = fl(h, blk.ffn_norm.weight, a.norm_eps, pk["w_gu_il"][a.block_of(l)], A, B, sc, None, 3)
+            h = fl(act, None, 0.0, blk.base("w2").weight, lo.w2.w_a.weight, lo.w2.w_b.weight, lo.w2.scale, h, 4)
+        z = fl(h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(), None, None, 0.0, None, 1)
+        return ops.lora_linear(z, self.tok_embeddings.emb, None, None, 0.0).view(b, -1)
+
     def decode_step(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
         """One greedy step at position `pos` (0-d int64 device tensor) -> logits [b, vocab].
         Shape-static and host-sync-free, so it can be captured in a HIP graph. Per layer:
@@ -322,8 +389,10 @@ class SharedQwen3(nn.Module):
         pk = self._decode_pack()
         rope = self._rope32()
         h = self.tok_embeddings(token.view(b)).view(b, a.dim)
-        sm_scale = a.head_dim ** -0.5
         fused_attn = a.n_heads // a.n_kv_heads in (1, 2, 4) and a.head_dim in (64, 128)
+        if fused_attn and self._fusion_plan(b, pk)["on"]:
+            return self._decode_step_fused(h, pos, cache, pk, rope)
+        sm_scale = a.head_dim ** -0.5
         pending = None
         for l in range(a.n_layers):
             blk = self.base_blocks[a.block_of(l)]
