@@ -710,6 +710,12 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
   const int steps = pl.kcy > 0 ? pl.kcy / wave_k_of(wdt) : 8;
   pl.kw = 8;
   while (pl.kw > 1 && pl.kw > steps) pl.kw >>= 1;
+  // Short K over very many rows (the tied output head): every wave takes two 16-row
+  // blocks of its own, so a workgroup streams 256 rows and the grid stays a few per CU.
+  if (pl.kw <= 2 && pl.mb <= 2 && N >= 32768) {
+    pl.kw = 1;
+    pl.nr = 2;
+  }
   for (;;) {
     pl.rows = (NWV / pl.kw) * 16 * pl.nr;
     pl.trows = (NWV / pl.kw) * 16;
@@ -763,6 +769,10 @@ hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t sme
   if (nr == 1) {
     if (mb == 1) return launch_one<WDT, 1, 1, KW>(a, grid, smem, st);
     return launch_one<WDT, 1, 2, KW>(a, grid, smem, st);
+  }
+  if constexpr (KW == 1) {  // two row blocks per wave at one or two token blocks
+    if (mb == 1) return launch_one<WDT, 2, 1, KW>(a, grid, smem, st);
+    if (mb == 2) return launch_one<WDT, 2, 2, KW>(a, grid, smem, st);
   }
   if (mb == 3) return launch_one<WDT, 2, 3, KW>(a, grid, smem, st);
   return launch_one<WDT, 2, 4, KW>(a, grid, smem, st);
