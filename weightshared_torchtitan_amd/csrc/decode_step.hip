@@ -168,6 +168,7 @@ constexpr int AT_T = 256;              // 4 waves = 16 groups of 16 lanes
 constexpr int AT_G = AT_T / 16;
 constexpr int AT_CH = 64;              // cache positions per workgroup
 constexpr int AT_U = AT_CH / AT_G;     // positions per group, all in flight
+constexpr int AT_B = 8;                // record loads a thread keeps in flight in the merge
 
 // EPL (4 or 8) consecutive bf16 of a row as one 8- or 16-byte load.
 template <int EPL> struct Vec;
@@ -330,6 +331,7 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t* __restrict_
 
 // --------------------------------------------------------------------- argmax
 constexpr int AM_T = 1024;
+constexpr int AM_U = 8;     // 16-byte loads a thread keeps in flight
 
 // (v, i) beats (w, j): NaN above every number, then the larger value, then the smaller index.
 __device__ __forceinline__ bool am_better(float v, int64_t i, float w, int64_t j) {
@@ -349,7 +351,21 @@ __global__ void __launch_bounds__(AM_T) argmax_kernel(const uint16_t* __restrict
   float bv = -INFINITY;
   int64_t bi = INT64_MAX;
   const int64_t nch = vec ? (n >> 3) : 0;  // 16-byte chunks (aligned rows only), then a scalar tail
-  for (int64_t c = tid; c < nch; c += AM_T) {
+  int64_t c = tid;
+  for (; c + (AM_U - 1) * AM_T < nch; c += AM_U * AM_T) {  // AM_U loads in flight per thread
+    u32x4_t v[AM_U];
+#pragma unroll
+    for (int u = 0; u < AM_U; ++u) v[u] = ld_global_16(xr + (c + u * AM_T) * 8);
+#pragma unroll
+    for (int u = 0; u < AM_U; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = bf((v[u][e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+        const int64_t k = (c + u * AM_T) * 8 + e;
+        if (am_better(f, k, bv, bi)) { bv = f; bi = k; }
+      }
+  }
+  for (; c < nch; c += AM_T) {
     const u32x4_t v = ld_global_16(xr + c * 8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -564,7 +580,17 @@ __global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restric
   for (int c0 = 0; c0 < nc; c0 += PASS) {
     const int cn = min(PASS, nc - c0);
     __syncthreads();  // the previous pass is consumed
-    for (int q2 = tid; q2 < cn * REC; q2 += AT_T) s_rec[q2] = ld_agent_f(base + (int64_t)c0 * REC + q2);
+    // AT_B loads in flight per thread (clamped addresses: the loads are unconditional)
+    const int nrec = cn * REC;
+    for (int q0 = 0; q0 < nrec; q0 += AT_B * AT_T) {
+      float v[AT_B];
+#pragma unroll
+      for (int u = 0; u < AT_B; ++u)
+        v[u] = ld_agent_f(base + (int64_t)c0 * REC + min(q0 + u * AT_T + tid, nrec - 1));
+#pragma unroll
+      for (int u = 0; u < AT_B; ++u)
+        if (q0 + u * AT_T + tid < nrec) s_rec[q0 + u * AT_T + tid] = v[u];
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NE; ++i) {

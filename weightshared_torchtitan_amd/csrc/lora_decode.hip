@@ -75,6 +75,7 @@ constexpr uint64_t kLaunchUnit = 1ull << 20;  // C: what one launch adds to the 
 constexpr uint64_t kTagMask = (1ull << 48) - 1;
 
 constexpr int kDefaultSpin = 1 << 16;  // polls of the T counter before computing T locally
+constexpr int LB = 8;                   // workspace loads a thread keeps in flight
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -375,7 +376,14 @@ __device__ __forceinline__ bool split_reduce(float* sums, float* part, unsigned*
   if (*flag == 0) return false;
   for (int q = tid; q < n; q += DT) {
     float v = 0.f;
-    for (int s2 = 0; s2 < ksplit; ++s2) v += ld_agent(part + (int64_t)s2 * n + q);
+    for (int s0 = 0; s0 < ksplit; s0 += LB) {  // LB partials in flight (clamped), summed in split order
+      float pv[LB];
+#pragma unroll
+      for (int u = 0; u < LB; ++u) pv[u] = ld_agent(part + (int64_t)min(s0 + u, ksplit - 1) * n + q);
+#pragma unroll
+      for (int u = 0; u < LB; ++u)
+        if (s0 + u < ksplit) v += pv[u];
+    }
     const int m = q / ROWS, rl = q % ROWS;
     sums[rl * MC + m] = v;
   }
@@ -413,11 +421,19 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
   for (int it = 0;; ++it) {
     if (tid == 0) *flag = 0;
     __syncthreads();
-    for (int q = tid; q < n; q += DT) {
-      const uint64_t v = ld_agent(p.tfin + q);
-      if ((v >> 16) != tag) *flag = 1;
-      const int m = q / p.r, j = q % p.r;
-      tl[m * tls + j] = (uint16_t)(v & 0xffffu);
+    for (int q0 = 0; q0 < n; q0 += LB * DT) {  // LB loads in flight per thread (clamped)
+      uint64_t v[LB];
+#pragma unroll
+      for (int u = 0; u < LB; ++u) v[u] = ld_agent(p.tfin + min(q0 + u * DT + tid, n - 1));
+#pragma unroll
+      for (int u = 0; u < LB; ++u) {
+        const int q = q0 + u * DT + tid;
+        if (q < n) {
+          if ((v[u] >> 16) != tag) *flag = 1;
+          const int m = q / p.r, j = q % p.r;
+          tl[m * tls + j] = (uint16_t)(v[u] & 0xffffu);
+        }
+      }
     }
     __syncthreads();
     ok = *flag == 0;
