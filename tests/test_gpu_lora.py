@@ -57,6 +57,10 @@ PREFILL_CASES = [
     (384, 1024, 512, 0, 2.0, True),      # plain linear
     (400, 640, 320, 32, 2.0, False),     # delta only (LoRAModule.forward)
     (65, 1024, 1024, 32, 2.0, True),     # just above the decode cut-over
+    (8192, 3072, 64, 32, 2.0, True),     # 256 x 192 tiles (two full waves for N = 3072)
+    (8000, 2900, 128, 16, 2.0, True),    # 256 x 192 tiles with M and N tails
+    (8192, 3072, 64, 0, 2.0, True),      # 256 x 192, plain linear
+    (8192, 3072, 64, 128, 1.0, True),    # 256 x 192 consuming the pre-pass T
 ]
 
 
@@ -198,8 +202,10 @@ def test_properties_at_benchmark_shape(gpu):
     y1 = wsl.lora_linear(x, W, A, B, 2.0)
     y2 = wsl.lora_linear(x, W, A, B, 2.0)
     assert torch.equal(y1, y2), "not deterministic"
-    ys = wsl.lora_linear(x[1024:1536], W, A, B, 2.0)
-    assert torch.equal(ys, y1[1024:1536]), "rows not independent"
+    # A slice large enough to take the same tile configuration (configurations differ in
+    # how they split the rank down-projection's K sum, so only equal ones are bit-equal).
+    ys = wsl.lora_linear(x[1024:5120], W, A, B, 2.0)
+    assert torch.equal(ys, y1[1024:5120]), "rows not independent"
     y0 = wsl.lora_linear(x, W, A, torch.zeros_like(B), 2.0)
     yp = wsl.lora_linear(x, W, None, None, 0.0)
     assert torch.equal(y0, yp), "B = 0 must equal the plain linear"

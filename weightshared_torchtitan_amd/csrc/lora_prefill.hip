@@ -4,8 +4,10 @@
 //
 // Tiling. A workgroup of 8 waves (two per SIMD) owns a BM(m) x BN(n) output tile,
 // split over its waves as a WNW x WMW grid of wave tiles; a wave tile is a grid of
-// v_mfma_f32_32x32x16_bf16 blocks with fp32 accumulators. Two configurations:
+// v_mfma_f32_32x32x16_bf16 blocks with fp32 accumulators. Three configurations, chosen
+// by how evenly the tiles fill the 256 CUs:
 //   256 x 256, 128(n) x 64(m) per wave;
+//   256(m) x 192(n), 96 x 64 per wave (N = 3072: two full waves of tiles, not 1.5);
 //   128 x 256, 64 x 64 per wave — used when 256-row tiles would leave CUs idle.
 // (A 4-wave 256 x 256 tile with 128 x 128 per wave measured slower on these shapes:
 // one wave per SIMD leaves LDS latency exposed, and rank blocks overflow the AGPRs.)
@@ -526,6 +528,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
 using CfgBig = Cfg<256, 256, 2, 8>;   // 8 waves, 128(n) x 64(m) per wave
 using CfgTall = Cfg<128, 256, 4, 8>;  // 8 waves, 64 x 64 per wave
+using CfgMid = Cfg<256, 192, 2, 8>;   // 8 waves, 96(n) x 64(m) per wave
 
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
 hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
@@ -545,12 +548,16 @@ double wave_efficiency(int64_t tiles) {
   return (double)tiles / (double)(waves * 256);
 }
 
-// 128-row tiles trade register reuse for occupancy; used when they fill the chip better.
-bool use_tall(const LoraArgs& p) {
-  const int64_t tn = (p.N + 255) / 256;
-  const double big = wave_efficiency(((p.M + 255) / 256) * tn);
-  const double tall = wave_efficiency(((p.M + 127) / 128) * tn) * 0.85;
-  return tall > big;
+// Tile configuration by how well its tiles fill the CUs, discounted by its measured
+// in-loop efficiency relative to 256 x 256 (smaller wave tiles read more LDS per MFMA).
+enum class Tile { kBig, kMid, kTall };
+Tile choose_tile(const LoraArgs& p) {
+  const int64_t tm = (p.M + 255) / 256;
+  const double big = wave_efficiency(tm * ((p.N + 255) / 256));
+  const double mid = wave_efficiency(tm * ((p.N + 191) / 192)) * 0.95;
+  const double tall = wave_efficiency(((p.M + 127) / 128) * ((p.N + 255) / 256)) * 0.85;
+  if (mid > big && mid > tall) return Tile::kMid;
+  return tall > big ? Tile::kTall : Tile::kBig;
 }
 
 template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER = false>
@@ -560,8 +567,11 @@ hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
   if constexpr (RB == 2) {
     return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
   } else {
-    return use_tall(p) ? launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt)
-                       : launch_cfg<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    switch (choose_tile(p)) {
+      case Tile::kMid: return launch_cfg<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      case Tile::kTall: return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      default: return launch_cfg<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    }
   }
 }
 
