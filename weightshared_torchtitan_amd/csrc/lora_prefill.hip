@@ -38,6 +38,8 @@
 //
 // Reference arithmetic being fused: torchtitan/models/llama3/model/model.py:189-192
 // (LoRAModule.forward), :392-398 (base projection + broadcast_add with g = 1).
+#include <type_traits>
+
 #include "wsl_common.h"
 
 namespace wsl {
@@ -122,7 +124,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   constexpr int OS = C::BN * 2 + 16;          // LDS row stride of the staged output tile
   constexpr int LDS_BYTES = (2 * STAGE > C::BM * OS) ? 2 * STAGE : C::BM * OS;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-  static_assert(C::BM * ROWB + 16384 <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
+  static_assert(C::BM * ROWB <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
 
   const int tid = threadIdx.x;
@@ -170,7 +172,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     woff[i] = (uint32_t)((min(n0 + row, N - 1) - n0) * ldw * 2 + fill_chunk(lane, wave * C::NWI + i) * 16);
   }
   // rank-A slice: RB*32 rows = RB*4 fills, one per wave for waves < RB*4 (rows >= r read
-  // row r-1 and are zeroed before the MFMA)
+  // row r-1; their T ranks are zeroed when T is parked)
   constexpr int NAI = RB * 4;
   uint32_t aoff = 0;
   if constexpr (RB > 0) aoff = (uint32_t)(min(wave * 8 + (lane >> 3), r - 1) * lda * 2 + fill_chunk(lane, wave) * 16);
@@ -237,14 +239,18 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   };
 
-  // ---- T work split: TBLK (m block, rank block) pairs per m strip, shared by WNW waves ----
+  // ---- T work split: TBLK (m block, rank block) pairs per wave row (WNW waves) ----
+  // With at least WNW blocks every wave takes TPW of them. With fewer (the 128 x 256 tile),
+  // one group of TBLK waves per row takes one block each over every k step; successive
+  // rows use different groups, so the T waves fall on different SIMDs (wave w runs on
+  // SIMD w % 4) and each SIMD carries the same MFMA count.
   constexpr int TBLK = C::MJ * RB;
-  constexpr int TPW = (RB == 0) ? 0 : (TBLK >= C::WNW ? TBLK / C::WNW : 1);  // blocks per wave
-  constexpr int KSPLIT = (RB == 0 || TBLK >= C::WNW) ? 1 : C::WNW / TBLK;   // waves per block
+  constexpr bool ALL_T = RB > 0 && TBLK >= C::WNW;
+  constexpr int TPW = (RB == 0) ? 0 : (ALL_T ? TBLK / C::WNW : 1);  // blocks per T wave
+  constexpr int TG = (RB == 0 || ALL_T) ? 1 : C::WNW / TBLK;        // wave groups per row
   static_assert(RB == 0 || TBLK % C::WNW == 0 || C::WNW % TBLK == 0, "T split");
-  static_assert(KSPLIT <= 2, "T partial hand-off covers two phases");
-  const int t_first = (KSPLIT == 1) ? wn * TPW : wn % TBLK;  // first T block of this wave
-  const int t_phase = (KSPLIT == 1) ? 0 : wn / TBLK;          // k-step phase (KSPLIT > 1)
+  const int t_first = ALL_T ? wn * TPW : wn % TBLK;  // first T block of this wave
+  const bool t_wave = RB > 0 && (ALL_T || (wn / TBLK) == (wm % TG));
 
   f32x16_t acc[C::NI][C::MJ];
 #pragma unroll
@@ -259,24 +265,23 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   for (int q = 0; q < TPWX; ++q)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acct[q][v] = 0.f;
-  bool tlive[TPWX];  // rank rows of the T block exist (rows >= r multiply by zero)
   int tj[TPWX], trb[TPWX];
 #pragma unroll
   for (int q = 0; q < TPWX; ++q) {
     const int b = t_first + q;
     tj[q] = b % C::MJ;
     trb[q] = b / C::MJ;
-    tlive[q] = trb[q] * 32 + l32 < r;
   }
 
   // Fragments of one 16-wide k step: x rows (MFMA B operand), W rows and rank-A rows
-  // (A operand).
+  // (A operand). `do_t` (a compile-time bool) selects the rank-A part.
   struct Frags {
     u32x4_t x[C::MJ];
     u32x4_t w[C::NI];
     u32x4_t a[TPWX];
+    u32x4_t xt[ALL_T ? 1 : TPWX];  // x rows of the T block (read directly when not all waves do T)
   };
-  auto frag_load = [&](int stage, int kk, Frags& f) {
+  auto frag_load = [&](auto do_t, int stage, int kk, Frags& f) {
     const char* sx = lds + stage * STAGE;
     const char* sw = sx + C::XB;
     const char* sa = sw + C::WB;
@@ -287,17 +292,15 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
       for (int i = 0; i < C::NI; ++i) f.w[i] = lds_read16(sw, lds_off(wn * C::TN + i * 32 + l32, c));
     }
-    if constexpr (RB > 0) {
-      if (KSPLIT == 1 || t_phase == (kk % KSPLIT)) {
+    if constexpr (decltype(do_t)::value) {
 #pragma unroll
-        for (int q = 0; q < TPW; ++q) {
-          const u32x4_t av = lds_read16(sa, lds_off(trb[q] * 32 + l32, c));
-          f.a[q] = tlive[q] ? av : zero_u32x4();
-        }
+      for (int q = 0; q < TPW; ++q) {
+        f.a[q] = lds_read16(sa, lds_off(trb[q] * 32 + l32, c));
+        if constexpr (!ALL_T) f.xt[q] = lds_read16(sx, lds_off(wm * C::TM + tj[q] * 32 + l32, c));
       }
     }
   };
-  auto frag_mma = [&](const Frags& f, int kk) {
+  auto frag_mma = [&](auto do_t, const Frags& f) {
     if constexpr (HAS_W) {
 #pragma unroll
       for (int i = 0; i < C::NI; ++i)
@@ -305,15 +308,18 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         for (int j = 0; j < C::MJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f.w[i]), as_bf16x8(f.x[j]), acc[i][j], 0, 0, 0);
     }
-    if constexpr (RB > 0) {
-      if (KSPLIT == 1 || t_phase == (kk % KSPLIT)) {
+    if constexpr (decltype(do_t)::value) {
 #pragma unroll
-        for (int q = 0; q < TPW; ++q) {
-          u32x4_t xt = f.x[0];
+      for (int q = 0; q < TPW; ++q) {
+        u32x4_t xt;
+        if constexpr (ALL_T) {
+          xt = f.x[0];
 #pragma unroll
           for (int j = 1; j < C::MJ; ++j) xt = (tj[q] == j) ? f.x[j] : xt;  // whole-vector select
-          acct[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f.a[q]), as_bf16x8(xt), acct[q], 0, 0, 0);
+        } else {
+          xt = f.xt[q];
         }
+        acct[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f.a[q]), as_bf16x8(xt), acct[q], 0, 0, 0);
       }
     }
   };
@@ -321,9 +327,10 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   // Interleave the MFMAs of the current k step with the LDS reads of the next one, so
   // the reads are issued early and their latency hides behind the MFMAs (left to
   // itself the scheduler sinks each read next to its use).
-  auto interleave = [&]() {
-    constexpr int NMF = (HAS_W ? C::NI * C::MJ : 0) + TPW;
-    constexpr int NRD = C::MJ + (HAS_W ? C::NI : 0) + TPW;
+  auto interleave = [&](auto do_t) {
+    constexpr int TT = decltype(do_t)::value ? TPW : 0;
+    constexpr int NMF = (HAS_W ? C::NI * C::MJ : 0) + TT;
+    constexpr int NRD = C::MJ + (HAS_W ? C::NI : 0) + TT * (ALL_T ? 1 : 2);
     constexpr int PAIRS = NMF < NRD ? NMF : NRD;
 #pragma unroll
     for (int q = 0; q < PAIRS; ++q) {
@@ -341,7 +348,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   char* lora_b = lds + (nk & 1) * STAGE;
 
   constexpr bool RUN_K = HAS_W || RB > 0;
-  if constexpr (RUN_K) {
+  // The K loop, instantiated with and without this wave's T work (`do_t`), so the k steps
+  // carry no per-step branch and the MFMAs interleave with the next step's LDS reads.
+  auto run_k = [&](auto do_t) {
     issue(0, 0);
     load_w8(0);
     wait_vm0();
@@ -355,15 +364,15 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       if (nk == 1) issue_b(lora_b, 0);
     }
     Frags cur;
-    frag_load(0, 0, cur);
+    frag_load(do_t, 0, 0, cur);
     for (int kt = 0; kt < nk; ++kt) {
       const int buf = kt & 1;
 #pragma unroll
       for (int kk = 0; kk < KK - 1; ++kk) {
         Frags nxt;
-        frag_load(buf, kk + 1, nxt);
-        frag_mma(cur, kk);
-        interleave();
+        frag_load(do_t, buf, kk + 1, nxt);
+        frag_mma(do_t, cur);
+        interleave(do_t);
         cur = nxt;
       }
       if (kt + 1 < nk) {
@@ -380,12 +389,22 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       // One code path for the last k step of every tile keeps the accumulators in one
       // register class. After the last tile this read of the idle buffer is discarded.
       Frags nxt;
-      frag_load(buf ^ 1, 0, nxt);
-      frag_mma(cur, KK - 1);
-      interleave();
+      frag_load(do_t, buf ^ 1, 0, nxt);
+      frag_mma(do_t, cur);
+      interleave(do_t);
       cur = nxt;
     }
     __syncthreads();  // every wave is done with the ring before the LDS is reused
+  };
+  if constexpr (RUN_K) {
+    if constexpr (RB == 0) {
+      run_k(std::false_type{});
+    } else if constexpr (ALL_T) {
+      run_k(std::true_type{});
+    } else {
+      if (t_wave) run_k(std::true_type{});
+      else run_k(std::false_type{});
+    }
   } else if constexpr (LORA) {
     issue_b(lora_b, 0);
   }
@@ -410,33 +429,24 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   // ---- LoRA up-projection: acc[n][m] += sum_j B[n][j] * T[m][j] in 64-rank chunks ----
   if constexpr (LORA) {
     char* st = lora_t;                   // T chunk [BM m][64 ranks]
-    char* sp = lora_t + C::BM * ROWB;    // fp32 T partials of split k steps (16 KB)
     char* sb = lora_b;                   // B chunk [BN n][64 ranks]
     if constexpr (RB > 0) {
-      if constexpr (KSPLIT > 1) {
-        // phase-1 waves hand their partial sums to the phase-0 wave of the same block
-        float* part = reinterpret_cast<float*>(sp);
-        const int slot = (wm * TBLK + t_first) * 64 + lane;
-        if (t_phase == 1) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) part[slot * 16 + v] = acct[0][v];
-        }
-        __syncthreads();
-        if (t_phase == 0) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acct[0][v] += part[slot * 16 + v];
-        }
-      }
-      if (t_phase == 0) {
-        // park bf16(s * T): rows wm*TM + tj*32 + l32, ranks trb*32 + 8g + 4*lh + e
+      if (t_wave) {
+        // park bf16(s * T): rows wm*TM + tj*32 + l32, ranks trb*32 + 8g + 4*lh + e. Ranks
+        // >= r (A rows past r were filled with row r-1) are zeroed here: they meet finite
+        // stand-in columns of B in the up-projection.
 #pragma unroll
         for (int q = 0; q < TPW; ++q) {
           const int mrow = wm * C::TM + tj[q] * 32 + l32;
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
+            const int rk = trb[q] * 32 + g * 8 + lh * 4;
+            float t4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t4[e] = rk + e < r ? s * acct[q][g * 4 + e] : 0.f;
             uint2 v;
-            v.x = pack_bf16x2(s * acct[q][g * 4 + 0], s * acct[q][g * 4 + 1]);
-            v.y = pack_bf16x2(s * acct[q][g * 4 + 2], s * acct[q][g * 4 + 3]);
+            v.x = pack_bf16x2(t4[0], t4[1]);
+            v.y = pack_bf16x2(t4[2], t4[3]);
             *reinterpret_cast<uint2*>(st + lds_off(mrow, trb[q] * 4 + g) + lh * 8) = v;
           }
         }
