@@ -379,6 +379,17 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         wait_vm0();          // tile kt+1 has landed (the only fill in flight)
         store_w8(buf ^ 1);   // fp8 base: decoded tile kt+1 into its buffer
         ring_barrier();      // all fragments of tile kt are read; tile kt+1 visible
+      }
+      // One code path for the last k step of every tile keeps the accumulators in one
+      // register class (after the last tile its read of the idle buffer is discarded).
+      // The fill of tile kt+2 goes out after these MFMAs, so the MFMA pipes restart at
+      // once after the barrier.
+      Frags nxt;
+      frag_load(do_t, buf ^ 1, 0, nxt);
+      frag_mma(do_t, cur);
+      interleave(do_t);
+      cur = nxt;
+      if (kt + 1 < nk) {
         if (kt + 2 < nk) {
           issue(buf, (kt + 2) * BK);
           load_w8((kt + 2) * BK);
@@ -386,13 +397,6 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
           issue_b(lora_b, 0);  // kt + 2 == nk: buffer `buf` is lora_b
         }
       }
-      // One code path for the last k step of every tile keeps the accumulators in one
-      // register class. After the last tile this read of the idle buffer is discarded.
-      Frags nxt;
-      frag_load(do_t, buf ^ 1, 0, nxt);
-      frag_mma(do_t, cur);
-      interleave(do_t);
-      cur = nxt;
     }
     __syncthreads();  // every wave is done with the ring before the LDS is reused
   };
