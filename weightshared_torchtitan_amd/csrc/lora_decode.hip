@@ -79,6 +79,10 @@ constexpr int LB = 8;                   // workspace loads a thread keeps in fli
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Cache-policy bits of a direct LDS fill that must see data written in this launch by
+// other XCDs (sc1: agent-coherent, as the agent-scope atomic loads use).
+constexpr int kAgentCoherent = 16;
+
 // Elements of K one lane covers per step (64 bytes of the row) and per wave step.
 template <int WDT> struct Geo {
   static constexpr int LANE_K = (WDT == kFP8) ? 64 : 32;
@@ -116,7 +120,7 @@ __device__ __forceinline__ int xs_off(int row, int k, int kc) {
 // Direct global->LDS fill of x[0..M)[kbeg .. kbeg+kc): the wave instruction j writes
 // LDS bytes [1024 j, 1024 j + 1024), lane i the 16 bytes at 1024 j + 16 i. SWZ places the
 // chunks as xs_off does; without it the rows are stored as they are.
-template <bool SWZ = true>
+template <bool SWZ = true, int AUX = 0>
 __device__ __forceinline__ void fill_x(char* xs, const uint16_t* __restrict__ x, int64_t ldx,
                                        int M, int kbeg, int kc, int wave, int lane) {
   const int cpr = kc >> 3;  // chunks per row
@@ -127,7 +131,7 @@ __device__ __forceinline__ void fill_x(char* xs, const uint16_t* __restrict__ x,
       const int row = p / cpr;
       const int c = SWZ ? ((p - row * cpr) ^ (row & 15)) : (p - row * cpr);
       const void* src = x + (int64_t)row * ldx + kbeg + c * 8;
-      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(xs + j * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(xs + j * 1024), 16, 0, AUX);
     }
   }
 }
@@ -224,6 +228,11 @@ struct DecodeArgs {
   float* tpart;       // [gT][kst][M][T rows per group]
   float* ypart;       // [gY][ksy][M][W rows per group]
   int spin;           // polls of the T counter before the local fallback
+  // chained launches: a producer publishes (tag) per W group once its y rows are out;
+  // a consumer waits for all of them before it reads x (= the producer's y)
+  uint64_t* done;             // producer: [gY] done words
+  const uint64_t* wait_on;    // consumer: the producer's done words
+  int wait_n;                 // consumer: how many
 };
 
 __device__ __forceinline__ void st_agent(float* p, float v) {
@@ -255,10 +264,10 @@ struct NoPrologue {
   __device__ __forceinline__ void operator()() const {}
 };
 
-template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue>
+template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue, class Pre = NoPrologue>
 __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
                                            int kbeg, int kc, int M, char* smem, float* sums,
-                                           const Pro& pro = Pro()) {
+                                           const Pro& pro = Pro(), const Pre& pre = Pre()) {
   using G = Geo<WDT>;
   constexpr int PD = NR == 1 ? 4 : 2;   // K steps in flight per wave
   constexpr int LPS = NR * 4;           // loads per step
@@ -293,14 +302,21 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
     for (int mb = 0; mb < MB; ++mb) acc[i][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // The x / B fills were issued before the W loads: wait until only the W loads are
-  // outstanding, then for every wave's fills (and LDS writes made before the call).
-  const int npf = my < PD ? my : PD;
-  if (npf == 0) wait_vm<0>();
-  else if (npf == 1) wait_vm<LPS>();
-  else if (npf == 2) wait_vm<2 * LPS>();
-  else if constexpr (PD == 4) {
-    if (npf == 3) wait_vm<3 * LPS>();
-    else wait_vm<4 * LPS>();
+  // outstanding, then for every wave's fills (and LDS writes made before the call). A
+  // `pre` hook (a chained consumer) waits for its input and only then issues the x fill,
+  // after the W loads, so everything is waited for.
+  if constexpr (!std::is_same<Pre, NoPrologue>::value) {
+    pre();
+    wait_vm<0>();
+  } else {
+    const int npf = my < PD ? my : PD;
+    if (npf == 0) wait_vm<0>();
+    else if (npf == 1) wait_vm<LPS>();
+    else if (npf == 2) wait_vm<2 * LPS>();
+    else if constexpr (PD == 4) {
+      if (npf == 3) wait_vm<3 * LPS>();
+      else wait_vm<4 * LPS>();
+    }
   }
   lds_barrier();
   pro();  // the x slice computed from what the fills staged (W loads still in flight)
@@ -396,9 +412,16 @@ __device__ __forceinline__ bool split_reduce(float* sums, float* part, unsigned*
 // bound computes T itself from x and A.
 // Eight consecutive elements of the projection input x[m][k..k+8): x itself, or with the
 // RMSNorm prologue bf16(x * rsqrt(ss[m] / K + eps) * w_norm).
-template <bool NORM>
+template <bool NORM, bool COH = false>
 __device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, int m, int k, float (&v)[8]) {
-  const u32x4_t xv = ld_global_16(p.x + (int64_t)m * p.ldx + k);
+  u32x4_t xv;
+  if constexpr (COH) {  // x written earlier in this launch (a chained producer's y)
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p.x + (int64_t)m * p.ldx + k);
+    const uint64_t lo = ld_agent(q), hi = ld_agent(q + 1);
+    xv = u32x4_t{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+  } else {
+    xv = ld_global_16(p.x + (int64_t)m * p.ldx + k);
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32((xv[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
   if constexpr (NORM) {
@@ -410,7 +433,7 @@ __device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, in
   }
 }
 
-template <int MC, bool NORM = false>
+template <int MC, bool NORM = false, bool COH = false>
 __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint64_t tag, int* flag,
                                          const float* ss = nullptr) {
   const int tid = threadIdx.x;
@@ -448,7 +471,7 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
       float acc = 0.f;
       for (int k = 0; k < p.K; k += 8) {
         float xv[8];
-        load_x8<NORM>(p, ss, m, k, xv);
+        load_x8<NORM, COH>(p, ss, m, k, xv);
         const u32x4_t av = ld_global_16(ar + k);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += xv[e] * bf16_bits_to_f32((av[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
@@ -529,12 +552,53 @@ struct NormPrologue {
   }
 };
 
-template <int WDT, int NR, int MB, int KW, int FUSE>
-__global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
+constexpr int kRolePlain = 0, kRoleProducer = 1, kRoleConsumer = 2;
+
+// A chained consumer's input hook, run by slice_sums after the W loads are issued: wait
+// (bounded) until every W group of the producer has published this launch's tag, then
+// stage the raw x rows, read past the L2s (the producer wrote them in this launch, from
+// any XCD), and w_norm for the RMSNorm prologue. Past the bound it goes on (the launch
+// still drains; the result is then not defined).
+struct ConsumerPre {
+  const DecodeArgs* p;
+  char* xs;
+  char* nws;
+  uint64_t tag;
+  int* flag;
+
+  __device__ __forceinline__ void operator()() const {
+    const int tid = threadIdx.x;
+    for (int it = 0;; ++it) {
+      if (tid == 0) *flag = 0;
+      __syncthreads();
+      for (int q = tid; q < p->wait_n; q += DT)
+        if (ld_agent(p->wait_on + q) != tag) *flag = 1;
+      __syncthreads();
+      const bool ok = *flag == 0;
+      __syncthreads();  // every thread has read the flag before it is cleared again
+      if (ok || it >= p->spin) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    fill_x<false, kAgentCoherent>(xs, p->x, p->ldx, p->M, 0, p->K, wave, lane);
+    fill_x<false>(nws, p->nw, 0, 1, 0, p->K, wave, lane);
+  }
+};
+
+// The work of one workgroup of a decode launch: a T workgroup (bid < gT * kst) or a W
+// workgroup. ROLE adds the chained-launch hand-off: a producer (residual epilogue) writes
+// y with agent-scope stores and then publishes the tag for its W group; a consumer
+// (RMSNorm prologue) takes its x from the producer's y once every group is published.
+template <int WDT, int NR, int MB, int KW, int FUSE, int ROLE>
+__device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64_t tag, char* smem) {
   constexpr bool NORM = (FUSE & kFuseNorm) != 0;
   constexpr bool ACT = (FUSE & kFuseAct) != 0;
   constexpr bool RES = (FUSE & kFuseRes) != 0;
-  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  constexpr bool CONS = ROLE == kRoleConsumer;
+  constexpr bool PROD = ROLE == kRoleProducer;
+  static_assert(!CONS || NORM, "a chained consumer takes the RMSNorm prologue");
+  static_assert(!PROD || (RES && !ACT), "a chained producer is a residual-epilogue launch");
   constexpr int RBK = NWV / KW;         // row blocks per workgroup
   constexpr int ROWS = RBK * 16 * NR;   // W rows per workgroup
   constexpr int TROWS = RBK * 16;       // A rows per T workgroup
@@ -543,11 +607,7 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nT = p.gT * p.kst;
-  const int bid = blockIdx.x;
   int* flag = reinterpret_cast<int*>(smem + p.flag_off);
-  uint64_t* launch = reinterpret_cast<uint64_t*>(p.cnt + CNT_LAUNCH);
-  // This launch's tag (see the file comment); read before this workgroup's exit addition.
-  const uint64_t tag = (ld_agent(launch) / kLaunchUnit + 1) & kTagMask;
 
   if (bid < nT) {
     // ---------------- T workgroup: TROWS rows of A over one K slice
@@ -555,7 +615,12 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
     const int kbeg = ks * p.kct;
     constexpr int RED_T = (NWV - RBK) * MB * 4 * 64 * 4;
     float* sums = reinterpret_cast<float*>(smem + RED_T);
-    if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
+    if constexpr (CONS) {  // the x rows arrive from the producer during the A loads
+      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
+      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums,
+                                   NormPrologue{&p, smem, ss, smem + p.nw_off},
+                                   ConsumerPre{&p, smem, smem + p.nw_off, tag, flag});
+    } else if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
@@ -584,7 +649,13 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
     char* bl = smem + (xs_bytes > post ? xs_bytes : post);
     float* sums = reinterpret_cast<float*>(smem + RED);
     uint16_t* tl = reinterpret_cast<uint16_t*>(smem + RED + ROWS * MC * 4);
-    if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
+    if constexpr (CONS) {  // the x rows arrive from the producer during the W loads
+      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
+      if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
+      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums,
+                                  NormPrologue{&p, smem, ss, smem + p.nw_off},
+                                  ConsumerPre{&p, smem, smem + p.nw_off, tag, flag});
+    } else if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
@@ -598,7 +669,7 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
     }
     if (split_reduce<ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, p.cnt + CNT_YG + g, ks,
                                p.ksy, p.M, flag)) {
-      if (p.r > 0) gather_t<MC, NORM>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16));
+      if (p.r > 0) gather_t<MC, NORM, CONS>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16));
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
       const int l16 = lane & 15, grp = lane >> 4;
       const int tls = p.r32 + 8;
@@ -656,7 +727,10 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
             uint2 pk;
             pk.x = pack_bf16x2(o[0], o[1]);
             pk.y = pack_bf16x2(o[2], o[3]);
-            *reinterpret_cast<uint2*>(yr + n0) = pk;
+            if constexpr (PROD)  // read later in this launch by the consumer, from any XCD
+              st_agent(reinterpret_cast<uint64_t*>(yr + n0), ((uint64_t)pk.y << 32) | pk.x);
+            else
+              *reinterpret_cast<uint2*>(yr + n0) = pk;
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -664,15 +738,52 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
           }
         }
       }
+      if constexpr (PROD) {  // this group's y rows are out: publish the tag
+        wait_vm<0>();
+        __syncthreads();
+        if (tid == 0) st_agent(p.done + g, tag);
+      }
     }
   }
+}
 
-  // Exit: this workgroup's share of the launch's C (the tag was consumed above).
-  if (tid == 0) {
-    const uint64_t total = (uint64_t)(nT + p.gY * p.ksy);
-    const uint64_t share = kLaunchUnit / total + (bid == 0 ? kLaunchUnit % total : 0);
-    __hip_atomic_fetch_add(launch, share, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// This launch's tag (see the file comment), read before this workgroup's exit addition.
+__device__ __forceinline__ uint64_t launch_tag(const unsigned* cnt) {
+  return (ld_agent(reinterpret_cast<const uint64_t*>(cnt + CNT_LAUNCH)) / kLaunchUnit + 1) & kTagMask;
+}
+
+// Exit: this workgroup's share of the launch's C (the tag was consumed above).
+__device__ __forceinline__ void launch_exit(unsigned* cnt, int total_wgs) {
+  if (threadIdx.x == 0) {
+    const uint64_t total = (uint64_t)total_wgs;
+    const uint64_t share = kLaunchUnit / total + (blockIdx.x == 0 ? kLaunchUnit % total : 0);
+    __hip_atomic_fetch_add(reinterpret_cast<uint64_t*>(cnt + CNT_LAUNCH), share, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+template <int WDT, int NR, int MB, int KW, int FUSE>
+__global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const uint64_t tag = launch_tag(p.cnt);
+  decode_body<WDT, NR, MB, KW, FUSE, kRolePlain>(p, blockIdx.x, tag, smem);
+  launch_exit(p.cnt, p.gT * p.kst + p.gY * p.ksy);
+}
+
+// Two dependent decode launches in one grid: the producer (residual epilogue; its
+// workgroups first) and the consumer (RMSNorm prologue, x = the producer's y). The
+// consumer's workgroups issue their weight loads at once and wait for the producer's
+// groups only before they read x. Producers never wait on consumers, and workgroups are
+// dispatched in order, so every wait ends. One launch counter (the producer's) tags both.
+template <int NR, int MB, int FUSE_B>
+__global__ void __launch_bounds__(DT) chain_kernel(DecodeArgs a, DecodeArgs b) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const uint64_t tag = launch_tag(a.cnt);
+  const int na = a.gT * a.kst + a.gY * a.ksy;
+  const int bid = blockIdx.x;
+  if (bid < na) decode_body<kBF16, NR, MB, 8, kFuseRes, kRoleProducer>(a, bid, tag, smem);
+  else decode_body<kBF16, NR, MB, 8, FUSE_B, kRoleConsumer>(b, bid - na, tag, smem);
+  launch_exit(a.cnt, na + b.gT * b.kst + b.gY * b.ksy);
 }
 
 int wave_k_of(int wdt) { return wdt == kFP8 ? 256 : 128; }
@@ -839,8 +950,9 @@ size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_
 }
 
 namespace {
-DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl) {
-  char* ws = reinterpret_cast<char*>(p.ws);
+// cnt: the counter prefix; data: where the plan's workspace offsets (which start after a
+// kCounterBytes prefix) are based.
+DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl, char* cnt, char* data) {
   DecodeArgs a{};
   a.x = reinterpret_cast<const uint16_t*>(p.x); a.ldx = p.ldx;
   a.w = p.w; a.ldw = p.ldw; a.w_scale = p.w_scale;
@@ -852,12 +964,16 @@ DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl) {
   a.gT = pl.gT; a.kst = pl.kst; a.kct = pl.kct;
   a.gY = pl.gY; a.ksy = pl.ksy; a.kcy = pl.kcy;
   a.flag_off = (int)pl.flag_off;
-  a.cnt = reinterpret_cast<unsigned*>(ws);
-  a.tfin = reinterpret_cast<uint64_t*>(ws + pl.off_t);
-  a.tpart = reinterpret_cast<float*>(ws + pl.off_pt);
-  a.ypart = reinterpret_cast<float*>(ws + pl.off_py);
+  a.cnt = reinterpret_cast<unsigned*>(cnt);
+  a.tfin = reinterpret_cast<uint64_t*>(data + pl.off_t);
+  a.tpart = reinterpret_cast<float*>(data + pl.off_pt);
+  a.ypart = reinterpret_cast<float*>(data + pl.off_py);
   a.spin = spin_limit();
   return a;
+}
+DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl) {
+  char* ws = reinterpret_cast<char*>(p.ws);
+  return make_args(p, pl, ws, ws);
 }
 }  // namespace
 
@@ -886,6 +1002,87 @@ bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
     if (f.res == nullptr || (reinterpret_cast<uintptr_t>(f.res) & 7u) != 0 || f.ldr % 4 != 0) return false;
   }
   return true;
+}
+
+// ---------------------------------------------------------------------------- chains
+// Workspace of a chained launch: the counter prefix (kCounterBytes; the producer's counters
+// in its first half, the consumer's in the second), the producer's done words, then the
+// producer's and the consumer's plan data.
+namespace {
+constexpr size_t kChainHalf = kCounterBytes / 2;
+constexpr int kChainDoneMax = 4096;
+constexpr size_t kChainDoneBytes = kChainDoneMax * 8;
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+struct ChainLayout {
+  DecodePlan pa, pb;
+  size_t off_a, off_b, total;
+};
+ChainLayout chain_layout(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2) {
+  ChainLayout c;
+  c.pa = plan_decode(M, N, K, r, kBF16);
+  c.pb = plan_decode(M, N2, N, r2, kBF16);
+  c.off_a = kCounterBytes + kChainDoneBytes;  // plan offsets already skip kCounterBytes
+  c.off_b = align256(c.off_a + (c.pa.total - kCounterBytes));
+  c.total = c.off_b + (c.pb.total - kCounterBytes);
+  return c;
+}
+int half_words() { return (int)(kChainHalf / 4); }
+}  // namespace
+
+size_t decode_chain_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2) {
+  return chain_layout(M, N, K, r, N2, r2).total;
+}
+
+bool decode_chain_supported(const LoraArgs& pa, const FusedArgs& fa, const LoraArgs& pb, const FusedArgs& fb) {
+  if (fa.fuse != kFuseRes || (fb.fuse != kFuseNorm && fb.fuse != (kFuseNorm | kFuseAct))) return false;
+  if (pb.x != pa.y || pb.ldx != pa.ldy || pb.M != pa.M || pb.K != pa.N) return false;
+  if (!decode_fused_supported(pa, fa) || !decode_fused_supported(pb, fb)) return false;
+  if (pa.N % 16 != 0) return false;  // whole 4-element stores in the producer
+  const ChainLayout c = chain_layout(pa.M, pa.N, pa.K, pa.r, pb.N, pb.r);
+  if (c.pa.gY > kChainDoneMax) return false;
+  if (CNT_YG + c.pa.gY > half_words() || CNT_YG + c.pb.gY > half_words()) return false;
+  if (c.pa.mb != c.pb.mb || c.pa.nr != c.pb.nr) return false;
+  return true;
+}
+
+namespace {
+template <int FUSE_B>
+hipError_t launch_chain_fb(const DecodeArgs& a, const DecodeArgs& b, int mb, int nr, int grid, size_t smem,
+                           hipStream_t st) {
+  auto go = [&](auto kern) -> hipError_t {
+    static bool ready = false;
+    if (!ready) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
+      if (e != hipSuccess) return e;
+      ready = true;
+    }
+    kern<<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a, b);
+    return hipGetLastError();
+  };
+  if (nr == 1) return mb == 1 ? go(chain_kernel<1, 1, FUSE_B>) : go(chain_kernel<1, 2, FUSE_B>);
+  return mb == 3 ? go(chain_kernel<2, 3, FUSE_B>) : go(chain_kernel<2, 4, FUSE_B>);
+}
+}  // namespace
+
+hipError_t launch_decode_chain(const LoraArgs& pa, const FusedArgs& fa, const LoraArgs& pb, const FusedArgs& fb) {
+  const ChainLayout c = chain_layout(pa.M, pa.N, pa.K, pa.r, pb.N, pb.r);
+  char* ws = reinterpret_cast<char*>(pa.ws);
+  DecodeArgs a = make_args(pa, c.pa, ws, ws + c.off_a - kCounterBytes);
+  a.res = reinterpret_cast<const uint16_t*>(fa.res); a.ldr = fa.ldr;
+  a.done = reinterpret_cast<uint64_t*>(ws + kCounterBytes);
+  DecodeArgs b = make_args(pb, c.pb, ws + kChainHalf, ws + c.off_b - kCounterBytes);
+  b.nw = reinterpret_cast<const uint16_t*>(fb.nw); b.eps = fb.eps;
+  b.nw_off = (int)c.pb.flag_off + 16 + kNormLds;
+  b.wait_on = a.done;
+  b.wait_n = c.pa.gY;
+  const size_t smem_a = c.pa.smem;
+  const size_t smem_b = c.pb.smem + (size_t)kNormLds + (size_t)pb.K * 2;
+  const size_t smem = smem_a > smem_b ? smem_a : smem_b;
+  if (smem > (size_t)LDS_MAX) return hipErrorInvalidValue;
+  const int grid = c.pa.gT * c.pa.kst + c.pa.gY * c.pa.ksy + c.pb.gT * c.pb.kst + c.pb.gY * c.pb.ksy;
+  if (fb.fuse == kFuseNorm) return launch_chain_fb<kFuseNorm>(a, b, c.pa.mb, c.pa.nr, grid, smem, pa.stream);
+  return launch_chain_fb<kFuseNorm | kFuseAct>(a, b, c.pa.mb, c.pa.nr, grid, smem, pa.stream);
 }
 
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {

@@ -11,6 +11,8 @@ from __future__ import annotations
 
 from typing import Optional
 
+import ctypes
+
 import torch
 
 from . import _native
@@ -432,3 +434,62 @@ def _lora_linear_fused_fake(x, norm_w, eps, w, a, b, scale, residual, fuse):
     M = x.reshape(-1, x.shape[-1]).shape[0]
     ny = w.shape[0] // 2 if fuse & 2 else w.shape[0]
     return x.new_empty((M, ny), dtype=torch.bfloat16)
+
+
+def lora_linear_chain_supported(M: int, N: int, K: int, r: int, N2: int, r2: int, fuse2: int) -> bool:
+    """Whether wsl::lora_linear_chain covers these sizes (16-byte aligned operands)."""
+    return bool(_native.lib().wsl_lora_linear_chain_supported(M, N, K, r, N2, r2, fuse2))
+
+
+def chain_workspace_bytes(M: int, N: int, K: int, r: int, N2: int, r2: int) -> int:
+    out = ctypes.c_size_t()
+    _native.check(_native.lib().wsl_lora_linear_chain_workspace_bytes(M, N, K, r, N2, r2, ctypes.byref(out)),
+                  "wsl_lora_linear_chain_workspace_bytes")
+    return out.value
+
+
+@torch.library.custom_op("wsl::lora_linear_chain", mutates_args=(), device_types="cuda")
+def lora_linear_chain_op(x: torch.Tensor, w: torch.Tensor, a: Optional[torch.Tensor], b: Optional[torch.Tensor],
+                         scale: float, residual: torch.Tensor, norm_w: torch.Tensor, eps: float, w2: torch.Tensor,
+                         a2: Optional[torch.Tensor], b2: Optional[torch.Tensor], scale2: float,
+                         fuse2: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(y, y2) of two dependent decode projections in one launch (include/wsl_decode.h):
+    y = bf16(residual + bf16(lora(x))) and y2 = lora2(rmsnorm(y) * norm_w) [SwiGLU]."""
+    dev = _check_device(x, w, a, b, residual, norm_w, w2, a2, b2)
+    x2 = _bf16_2d(x, "x")
+    M, K = x2.shape
+    N, N2 = w.shape[0], w2.shape[0]
+    res = _bf16_2d(residual, "residual")
+    nw = norm_w.to(torch.bfloat16).contiguous()
+    w, w2 = _row_major(w, "w"), _row_major(w2, "w2")
+    r = r2 = 0
+    if a is not None:
+        a, b = _row_major(a, "a"), _row_major(b, "b")
+        r = a.shape[0]
+    if a2 is not None:
+        a2, b2 = _row_major(a2, "a2"), _row_major(b2, "b2")
+        r2 = a2.shape[0]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ny2 = N2 // 2 if fuse2 & _native.WSL_FUSE_SWIGLU else N2
+    y2 = torch.empty((M, ny2), dtype=torch.bfloat16, device=dev)
+    stream = _stream(dev)
+    ws = workspace(dev, stream, chain_workspace_bytes(M, N, K, r, N2, r2), kind="chain")
+    with torch.cuda.device(dev):
+        rc = _native.lib().wsl_lora_linear_chain_fwd(
+            x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0),
+            _dev_ptr(a), a.stride(0) if a is not None else 0, _dev_ptr(b), b.stride(0) if b is not None else 0,
+            float(scale), res.data_ptr(), res.stride(0), y.data_ptr(), y.stride(0), N, K, r,
+            nw.data_ptr(), float(eps), w2.data_ptr(), w2.stride(0),
+            _dev_ptr(a2), a2.stride(0) if a2 is not None else 0, _dev_ptr(b2), b2.stride(0) if b2 is not None else 0,
+            float(scale2), y2.data_ptr(), y2.stride(0), N2, r2, int(fuse2), M, ws.data_ptr(), ws.numel(), stream)
+    if rc != _native.WSL_OK:
+        _workspaces.pop((dev.index, stream, "chain"), None)
+    _native.check(rc, "wsl_lora_linear_chain_fwd")
+    return y, y2
+
+
+@lora_linear_chain_op.register_fake
+def _lora_linear_chain_fake(x, w, a, b, scale, residual, norm_w, eps, w2, a2, b2, scale2, fuse2):
+    M = x.reshape(-1, x.shape[-1]).shape[0]
+    ny2 = w2.shape[0] // 2 if fuse2 & 2 else w2.shape[0]
+    return (x.new_empty((M, w.shape[0]), dtype=torch.bfloat16), x.new_empty((M, ny2), dtype=torch.bfloat16))

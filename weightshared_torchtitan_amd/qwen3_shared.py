@@ -333,6 +333,12 @@ class SharedQwen3(nn.Module):
             "head": sup(b, a.embed_rank, a.dim, 0, 1),
         }
         plan["on"] = self.decode_fusion and all(plan.values())
+        csup = ops.lora_linear_chain_supported
+        hd = a.n_heads * a.head_dim
+        plan["chain"] = plan["on"] and self.decode_chain and all((
+            csup(b, a.dim, hd, r, 2 * a.hidden_dim, 2 * r, 3),
+            csup(b, a.dim, a.hidden_dim, r, qkv_n, 3 * r, 1),
+            csup(b, a.dim, a.hidden_dim, r, a.embed_rank, 0, 1)))
         return plan
 
     def _rope32(self) -> torch.Tensor:
@@ -354,28 +360,54 @@ class SharedQwen3(nn.Module):
         return ops.lora_linear(x, w, A, B, sc)
 
     decode_fusion = True  # use the fused decode-step launches where _fusion_plan allows
+    # Chain each residual launch with the normed launch after it (wsl_lora_linear_chain_fwd).
+    # Off by default: measured on MI355X, the in-launch cross-XCD hand-off (~2.5 us poll plus
+    # an agent-coherent x fill) costs as much as the launch boundary it removes.
+    decode_chain = False
 
-    def _decode_step_fused(self, h, pos, cache, pk, rope) -> torch.Tensor:
-        """The decode step in five launches per layer: q|k|v (RMSNorm prologue), the fused
-        attention step, o projection (+ residual), gate|up (RMSNorm prologue, SwiGLU
-        epilogue), down projection (+ residual)."""
+    def _decode_step_fused(self, h, pos, cache, pk, rope, chain: bool) -> torch.Tensor:
+        """The decode step in fused launches: q|k|v (RMSNorm prologue), the fused attention
+        step, o projection (+ residual), gate|up (RMSNorm prologue, SwiGLU epilogue), down
+        projection (+ residual). With `chain`, o + gate|up and down + the next block's q|k|v
+        (the last one: + the head's first factor) each run as one launch, so a layer is
+        three launches."""
         a = self.args
         b = h.shape[0]
         sm_scale = a.head_dim ** -0.5
         fl = ops.lora_linear_fused_op
+        ch = ops.lora_linear_chain_op
+        qkv = z = None
         for l in range(a.n_layers):
             blk = self.base_blocks[a.block_of(l)]
             lo = self.layer_loras[l]
-            A, B, sc = pk["l_qkv"][l]
-            qkv = fl(h, blk.attention_norm.weight, a.norm_eps, pk["w_qkv"][a.block_of(l)], A, B, sc, None, 1)
+            if qkv is None:
+                A, B, sc = pk["l_qkv"][l]
+                qkv = fl(h, blk.attention_norm.weight, a.norm_eps, pk["w_qkv"][a.block_of(l)], A, B, sc, None, 1)
             o = ops.decode_attention_step_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight,
                                              a.norm_eps, rope, pos, cache.k[l], cache.v[l], a.n_heads,
                                              a.n_kv_heads, sm_scale)
-            h = fl(o, None, 0.0, blk.base("wo").weight, lo.wo.w_a.weight, lo.wo.w_b.weight, lo.wo.scale, h, 4)
-            A, B, sc = pk["l_gu_il"][l]
-            act = fl(h, blk.ffn_norm.weight, a.norm_eps, pk["w_gu_il"][a.block_of(l)], A, B, sc, None, 3)
-            h = fl(act, None, 0.0, blk.base("w2").weight, lo.w2.w_a.weight, lo.w2.w_b.weight, lo.w2.scale, h, 4)
-        z = fl(h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(), None, None, 0.0, None, 1)
+            qkv = None
+            wo, Ao, Bo, so = blk.base("wo").weight, lo.wo.w_a.weight, lo.wo.w_b.weight, lo.wo.scale
+            Ag, Bg, sg = pk["l_gu_il"][l]
+            wgu = pk["w_gu_il"][a.block_of(l)]
+            if chain:
+                h, act = ch(o, wo, Ao, Bo, so, h, blk.ffn_norm.weight, a.norm_eps, wgu, Ag, Bg, sg, 3)
+            else:
+                h = fl(o, None, 0.0, wo, Ao, Bo, so, h, 4)
+                act = fl(h, blk.ffn_norm.weight, a.norm_eps, wgu, Ag, Bg, sg, None, 3)
+            w2, A2, B2, s2 = blk.base("w2").weight, lo.w2.w_a.weight, lo.w2.w_b.weight, lo.w2.scale
+            if chain and l + 1 < a.n_layers:
+                nb = self.base_blocks[a.block_of(l + 1)]
+                An, Bn, sn = pk["l_qkv"][l + 1]
+                h, qkv = ch(act, w2, A2, B2, s2, h, nb.attention_norm.weight, a.norm_eps,
+                            pk["w_qkv"][a.block_of(l + 1)], An, Bn, sn, 1)
+            elif chain:
+                h, z = ch(act, w2, A2, B2, s2, h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(),
+                          None, None, 0.0, 1)
+            else:
+                h = fl(act, None, 0.0, w2, A2, B2, s2, h, 4)
+        if z is None:
+            z = fl(h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(), None, None, 0.0, None, 1)
         return ops.lora_linear(z, self.tok_embeddings.emb, None, None, 0.0).view(b, -1)
 
     def decode_step(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
@@ -390,8 +422,10 @@ class SharedQwen3(nn.Module):
         rope = self._rope32()
         h = self.tok_embeddings(token.view(b)).view(b, a.dim)
         fused_attn = a.n_heads // a.n_kv_heads in (1, 2, 4) and a.head_dim in (64, 128)
-        if fused_attn and self._fusion_plan(b, pk)["on"]:
-            return self._decode_step_fused(h, pos, cache, pk, rope)
+        if fused_attn:
+            plan = self._fusion_plan(b, pk)
+            if plan["on"]:
+                return self._decode_step_fused(h, pos, cache, pk, rope, plan["chain"])
         sm_scale = a.head_dim ** -0.5
         pending = None
         for l in range(a.n_layers):
