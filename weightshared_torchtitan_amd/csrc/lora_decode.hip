@@ -440,30 +440,28 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
   const int tls = p.r32 + 8;
   for (int q = tid; q < MC * tls; q += DT) tl[q] = 0;
   const int n = p.M * p.r;
-  bool ok = false;
-  for (int it = 0;; ++it) {
-    if (tid == 0) *flag = 0;
-    __syncthreads();
-    for (int q0 = 0; q0 < n; q0 += LB * DT) {  // LB loads in flight per thread (clamped)
-      uint64_t v[LB];
+  if (tid == 0) *flag = 0;
+  __syncthreads();
+  // Each thread spins on its own elements (bounded; LB loads in flight per round), so an
+  // element is taken as soon as it is visible, without a workgroup round per poll.
+  for (int q0 = 0; q0 < n; q0 += LB * DT) {
+    uint64_t v[LB];
 #pragma unroll
-      for (int u = 0; u < LB; ++u) v[u] = ld_agent(p.tfin + min(q0 + u * DT + tid, n - 1));
+    for (int u = 0; u < LB; ++u) v[u] = ld_agent(p.tfin + min(q0 + u * DT + tid, n - 1));
 #pragma unroll
-      for (int u = 0; u < LB; ++u) {
-        const int q = q0 + u * DT + tid;
-        if (q < n) {
-          if ((v[u] >> 16) != tag) *flag = 1;
-          const int m = q / p.r, j = q % p.r;
-          tl[m * tls + j] = (uint16_t)(v[u] & 0xffffu);
-        }
+    for (int u = 0; u < LB; ++u) {
+      const int q = q0 + u * DT + tid;
+      if (q < n) {
+        for (int it = 0; (v[u] >> 16) != tag && it < p.spin; ++it) v[u] = ld_agent(p.tfin + q);
+        if ((v[u] >> 16) != tag) *flag = 1;
+        const int m = q / p.r, j = q % p.r;
+        tl[m * tls + j] = (uint16_t)(v[u] & 0xffffu);
       }
     }
-    __syncthreads();
-    ok = *flag == 0;
-    __syncthreads();  // every thread has read the flag before it is cleared again
-    if (ok || it >= p.spin) break;
-    __builtin_amdgcn_s_sleep(2);
   }
+  __syncthreads();
+  const bool ok = *flag == 0;
+  __syncthreads();  // every thread has read the flag before anyone reuses it
   if (!ok) {
     for (int q = tid; q < n; q += DT) {
       const int m = q / p.r, j = q % p.r;
@@ -555,7 +553,8 @@ struct NormPrologue {
 constexpr int kRolePlain = 0, kRoleProducer = 1, kRoleConsumer = 2;
 
 // A chained consumer's input hook, run by slice_sums after the W loads are issued: wait
-// (bounded) until every W group of the producer has published this launch's tag, then
+// (each thread on its own words, bounded) until every W group of the producer has
+// published this launch's tag, then
 // stage the raw x rows, read past the L2s (the producer wrote them in this launch, from
 // any XCD), and w_norm for the RMSNorm prologue. Past the bound it goes on (the launch
 // still drains; the result is then not defined).
@@ -568,17 +567,11 @@ struct ConsumerPre {
 
   __device__ __forceinline__ void operator()() const {
     const int tid = threadIdx.x;
-    for (int it = 0;; ++it) {
-      if (tid == 0) *flag = 0;
-      __syncthreads();
-      for (int q = tid; q < p->wait_n; q += DT)
-        if (ld_agent(p->wait_on + q) != tag) *flag = 1;
-      __syncthreads();
-      const bool ok = *flag == 0;
-      __syncthreads();  // every thread has read the flag before it is cleared again
-      if (ok || it >= p->spin) break;
-      __builtin_amdgcn_s_sleep(2);
+    for (int q = tid; q < p->wait_n; q += DT) {  // each thread spins on its own words (bounded)
+      uint64_t v = ld_agent(p->wait_on + q);
+      for (int it = 0; v != tag && it < p->spin; ++it) v = ld_agent(p->wait_on + q);
     }
+    __syncthreads();
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     fill_x<false, kAgentCoherent>(xs, p->x, p->ldx, p->M, 0, p->K, wave, lane);
