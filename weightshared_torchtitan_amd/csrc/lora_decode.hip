@@ -861,15 +861,19 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
   return pl;
 }
 
+// Lets KERN take the full LDS as dynamic shared memory; set once per kernel (a function-
+// local static: thread-safe, one per template instantiation).
+template <auto KERN>
+hipError_t allow_full_lds() {
+  static const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(KERN),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
+  return e;
+}
+
 template <int WDT, int NR, int MB, int KW, int FUSE = 0>
 hipError_t launch_one(const DecodeArgs& a, int grid, size_t smem, hipStream_t st) {
-  static bool ready = false;  // the attribute is per kernel; setting it twice is harmless
-  if (!ready) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<WDT, NR, MB, KW, FUSE>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
-    if (e != hipSuccess) return e;
-    ready = true;
-  }
+  const hipError_t e = allow_full_lds<decode_kernel<WDT, NR, MB, KW, FUSE>>();
+  if (e != hipSuccess) return e;
   decode_kernel<WDT, NR, MB, KW, FUSE><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a);
   return hipGetLastError();
 }
@@ -1039,22 +1043,23 @@ bool decode_chain_supported(const LoraArgs& pa, const FusedArgs& fa, const LoraA
 }
 
 namespace {
+template <int NR, int MB, int FUSE_B>
+hipError_t launch_chain_one(const DecodeArgs& a, const DecodeArgs& b, int grid, size_t smem, hipStream_t st) {
+  const hipError_t e = allow_full_lds<chain_kernel<NR, MB, FUSE_B>>();
+  if (e != hipSuccess) return e;
+  chain_kernel<NR, MB, FUSE_B><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a, b);
+  return hipGetLastError();
+}
+
 template <int FUSE_B>
 hipError_t launch_chain_fb(const DecodeArgs& a, const DecodeArgs& b, int mb, int nr, int grid, size_t smem,
                            hipStream_t st) {
-  auto go = [&](auto kern) -> hipError_t {
-    static bool ready = false;
-    if (!ready) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
-      if (e != hipSuccess) return e;
-      ready = true;
-    }
-    kern<<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a, b);
-    return hipGetLastError();
-  };
-  if (nr == 1) return mb == 1 ? go(chain_kernel<1, 1, FUSE_B>) : go(chain_kernel<1, 2, FUSE_B>);
-  return mb == 3 ? go(chain_kernel<2, 3, FUSE_B>) : go(chain_kernel<2, 4, FUSE_B>);
+  if (nr == 1) {
+    return mb == 1 ? launch_chain_one<1, 1, FUSE_B>(a, b, grid, smem, st)
+                   : launch_chain_one<1, 2, FUSE_B>(a, b, grid, smem, st);
+  }
+  return mb == 3 ? launch_chain_one<2, 3, FUSE_B>(a, b, grid, smem, st)
+                 : launch_chain_one<2, 4, FUSE_B>(a, b, grid, smem, st);
 }
 }  // namespace
 
