@@ -11,7 +11,7 @@ weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
 projections, and the CPU baseline (the reference's fp32 arithmetic on host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
-                      [--only c2|c3|c4|c5] [--copy-calibration]
+                      [--only c2|c3|c4|c5|emb] [--copy-calibration]
 
 --only runs one section and prints its JSON alone (for profiling one workload).
 --copy-calibration first runs a plain device copy of COPY_BYTES bytes (three launches),
@@ -198,6 +198,25 @@ def bench_c5(dev, steps, warmup):
     return out
 
 
+def bench_embedding(dev, steps, warmup):
+    """The factorized embedding at config 4's prefill: 8 x 512 token ids, E [151936, 256],
+    P [1024, 256] -> [4096, 1024] bf16 (wsl_factorized_embedding_fwd). Algorithmic bytes:
+    the gathered E rows, P, the ids and the output; FLOPs 2 * tokens * 256 * 1024."""
+    from weightshared_torchtitan_amd import factorized_embedding
+    g = torch.Generator(device=dev).manual_seed(11)
+    V, k, H, T = 151936, 256, 1024, 4096
+    emb = (torch.randn(V, k, device=dev, generator=g) * 0.02).bfloat16()
+    proj = (torch.randn(H, k, device=dev, generator=g) * 0.02).bfloat16()
+    ids = torch.randint(0, V, (T,), device=dev, generator=g)
+    L = 16
+    graph = graph_of(lambda: [factorized_embedding(ids, emb, proj) for _ in range(L)])
+    ms = time_replays(graph, steps, warmup) / L
+    nbytes = T * k * 2 + H * k * 2 + T * 8 + T * H * 2
+    return {"tokens": T, "us": round(ms * 1e3, 3), "Mtok/s": round(T / ms / 1e3, 1),
+            "GB/s": round(nbytes / ms / 1e6, 1), "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "TFLOP/s": round(2.0 * T * k * H / ms / 1e9, 1)}
+
+
 def bench_c4(dev):
     from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3, qwen3_0p6b_shared
     args = qwen3_0p6b_shared()
@@ -277,7 +296,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5"), default=None)
+    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5", "emb"), default=None)
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -296,7 +315,8 @@ def main():
     if args.only is not None and args.only != "c2":
         fn = {"c3": lambda: bench_c3(dev, args.steps, args.warmup),
               "c4": lambda: bench_c4(dev),
-              "c5": lambda: bench_c5(dev, args.steps, args.warmup)}[args.only]
+              "c5": lambda: bench_c5(dev, args.steps, args.warmup),
+              "emb": lambda: bench_embedding(dev, args.steps, args.warmup)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     flops, ms = bench_c2(dev, args.steps, args.warmup)
@@ -333,6 +353,7 @@ def main():
         extra["c3_qwen3_1.7b_decode"] = bench_c3(dev, args.steps, args.warmup)
         extra["c5_qwen3_8b_fp8_base"] = bench_c5(dev, args.steps, args.warmup)
         extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)
+        extra["factorized_embedding_c4_prefill"] = bench_embedding(dev, args.steps, args.warmup)
         res["extra"] = extra
     if not args.no_cpu and args.only is None:
         res["cpu_baseline"] = cpu_baseline()
