@@ -93,6 +93,18 @@ def test_workspace_includes_counter_prefix(M):
     assert big >= b
 
 
+@needs_lib
+def test_workspace_holds_split_prepass_partials():
+    # M = 4096, K = 4096, r = 128: 32 rank tiles, so the pre-pass splits K 8 ways and
+    # keeps 8 fp32 partial slices [M, r] beside T [M, r] bf16.
+    M, K, r = 4096, 4096, 128
+    need = N.workspace_bytes(M, 1024, K, r, N.WSL_DTYPE_BF16)
+    assert need >= _header_defines()["WSL_COUNTER_BYTES"] + M * r * 2 + 8 * M * r * 4
+    # one K tile cannot be split: T only
+    small = N.workspace_bytes(M, 1024, 64, r, N.WSL_DTYPE_BF16)
+    assert small < _header_defines()["WSL_COUNTER_BYTES"] + M * r * 2 + M * r * 4
+
+
 P = 0x100000  # a 256-aligned fake device address; never dereferenced
 
 

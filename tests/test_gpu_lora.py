@@ -61,6 +61,12 @@ PREFILL_CASES = [
     (8000, 2900, 128, 16, 2.0, True),    # 256 x 192 tiles with M and N tails
     (8192, 3072, 64, 0, 2.0, True),      # 256 x 192, plain linear
     (8192, 3072, 64, 128, 1.0, True),    # 256 x 192 consuming the pre-pass T
+    (1000, 1024, 2048, 128, 2.0, True),  # pre-pass split 8 ways over K, M tail
+    (700, 512, 1024, 256, 1.0, True),    # pre-pass split 4 ways, two rank tiles
+    (64 + 1, 640, 4096, 128, 2.0, False),  # delta only, pre-pass split 16 ways
+    (4096, 1024, 512, 0, 2.0, True),     # 128 x 128 tiles (256 of them), plain linear
+    (4096, 1000, 256, 128, 1.0, True),   # 128 x 128 tiles, pre-pass T, N tail
+    (2000, 1024, 512, 32, 2.0, False),   # 128 x 128 tiles, delta only, M tail
 ]
 
 
@@ -156,7 +162,7 @@ def test_golden_vectors_on_gpu(gpu):
 
 
 # ------------------------------------------------------------------ fp8 base
-@pytest.mark.parametrize("M,N,K", [(16, 1024, 4096), (512, 1024, 1024), (4, 512, 2048)])
+@pytest.mark.parametrize("M,N,K", [(16, 1024, 4096), (512, 1024, 1024), (4, 512, 2048), (4096, 1024, 4096)])
 def test_fp8_base_parity(gpu, M, N, K):
     from weightshared_torchtitan_amd import quantize_fp8_per_channel
     _say(f"[fp8] M={M} N={N} K={K} r=128 s=1")

@@ -4,11 +4,13 @@
 //
 // Tiling. A workgroup of 8 waves (two per SIMD) owns a BM(m) x BN(n) output tile,
 // split over its waves as a WNW x WMW grid of wave tiles; a wave tile is a grid of
-// v_mfma_f32_32x32x16_bf16 blocks with fp32 accumulators. Three configurations, chosen
+// v_mfma_f32_32x32x16_bf16 blocks with fp32 accumulators. Four configurations, chosen
 // by how evenly the tiles fill the 256 CUs:
 //   256 x 256, 128(n) x 64(m) per wave;
 //   256(m) x 192(n), 96 x 64 per wave (N = 3072: two full waves of tiles, not 1.5);
-//   128 x 256, 64 x 64 per wave — used when 256-row tiles would leave CUs idle.
+//   128 x 256, 64 x 64 per wave — used when 256-row tiles would leave CUs idle;
+//   128 x 128, 64 x 32 per wave (two workgroups fit on a CU) — for shapes that even
+//   128 x 256 tiles leave half-idle, and for the split-K rank pre-pass.
 // (A 4-wave 256 x 256 tile with 128 x 128 per wave measured slower on these shapes:
 // one wave per SIMD leaves LDS latency exposed, and rank blocks overflow the AGPRs.)
 // K is walked in 64-wide tiles through two LDS buffers filled by
@@ -27,7 +29,9 @@
 // is scaled by s, rounded to bf16 and parked in LDS, and the up-projection T . B^T
 // accumulates into the same accumulator registers as x . W^T; its B slice is filled
 // into the idle LDS buffer while the last K tile is multiplied. For r > 64 a pre-pass
-// writes T to the workspace and the kernel consumes it the same way.
+// writes T to the workspace and the kernel consumes it the same way; with N = r the
+// pre-pass has few tiles, so it splits K over a second grid dimension into fp32 partials
+// that a small kernel sums in split order (deterministic), scales and rounds.
 //
 // The MFMA "A" operand is the W tile (rows n) and "B" the x tile (rows m): each lane
 // ends with 4 consecutive n of one m per accumulator group; the tile is staged through
@@ -105,7 +109,10 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
+// SPLIT: split-K plain GEMM for the rank pre-pass. Workgroup row blockIdx.y takes the K
+// range [blockIdx.y * K, (blockIdx.y + 1) * K) of x and W and writes its fp32 partial
+// product to slice blockIdx.y of y (viewed as fp32 [gridDim.y][M][ldy]).
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false>
 __global__ void __launch_bounds__(C::NT, 1)
 prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const int64_t* __restrict__ gidx, int64_t grows,
@@ -126,6 +133,12 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert(C::BM * ROWB <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+  static_assert(!SPLIT || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "split-K is a plain bf16 GEMM");
+  if constexpr (SPLIT) {
+    const int64_t kofs = (int64_t)blockIdx.y * K;
+    x += kofs;
+    w = reinterpret_cast<const uint16_t*>(w) + kofs;
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -249,8 +262,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   constexpr int TPW = (RB == 0) ? 0 : (ALL_T ? TBLK / C::WNW : 1);  // blocks per T wave
   constexpr int TG = (RB == 0 || ALL_T) ? 1 : C::WNW / TBLK;        // wave groups per row
   static_assert(RB == 0 || TBLK % C::WNW == 0 || C::WNW % TBLK == 0, "T split");
-  const int t_first = ALL_T ? wn * TPW : wn % TBLK;  // first T block of this wave
-  const bool t_wave = RB > 0 && (ALL_T || (wn / TBLK) == (wm % TG));
+  constexpr int TBLKX = TBLK > 0 ? TBLK : 1;  // RB == 0: no T blocks (keeps % and / defined)
+  const int t_first = ALL_T ? wn * TPW : wn % TBLKX;  // first T block of this wave
+  const bool t_wave = RB > 0 && (ALL_T || (wn / TBLKX) == (wm % TG));
 
   f32x16_t acc[C::NI][C::MJ];
 #pragma unroll
@@ -491,6 +505,28 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
 
+  if constexpr (SPLIT) {
+    // fp32 partials straight from the accumulators: lane pairs (lh) cover 8 consecutive
+    // n of one row, the four groups g a whole 128-byte line, merged in L2.
+    float* yf = reinterpret_cast<float*>(y) + (int64_t)blockIdx.y * M * ldy;
+#pragma unroll
+    for (int j = 0; j < C::MJ; ++j) {
+      const int m = m0 + wm * C::TM + j * 32 + l32;
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * C::TN + i * 32 + g * 8 + lh * 4;  // N % 8 == 0: n < N covers n + 3
+          if (n < N)
+            *reinterpret_cast<f32x4_t*>(yf + (int64_t)m * ldy + n) =
+                f32x4_t{acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2], acc[i][j][g * 4 + 3]};
+        }
+      }
+    }
+    return;
+  }
+
   // ---- store. The accumulators hold 4 consecutive n of one m per lane and group, i.e.
   // 16-byte pieces of 32 different rows per wave instruction; written straight to y
   // they reach L2 as partial lines. The tile is staged through LDS (row stride OS) and
@@ -543,12 +579,13 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 using CfgBig = Cfg<256, 256, 2, 8>;   // 8 waves, 128(n) x 64(m) per wave
 using CfgTall = Cfg<128, 256, 4, 8>;  // 8 waves, 64 x 64 per wave
 using CfgMid = Cfg<256, 192, 2, 8>;   // 8 waves, 96(n) x 64(m) per wave
+using CfgSmall = Cfg<128, 128, 2, 8>;  // 8 waves, 64(n) x 32(m) per wave; also the rank pre-pass (N = r)
 
-template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
-hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false>
+hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1) {
   const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
   const int tiles_n = (int)((p.N + C::BN - 1) / C::BN);
-  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER><<<dim3(tiles_m * tiles_n), dim3(C::NT), 0, p.stream>>>(
+  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT><<<dim3(tiles_m * tiles_n, splits), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
@@ -564,12 +601,17 @@ double wave_efficiency(int64_t tiles) {
 
 // Tile configuration by how well its tiles fill the CUs, discounted by its measured
 // in-loop efficiency relative to 256 x 256 (smaller wave tiles read more LDS per MFMA).
-enum class Tile { kBig, kMid, kTall };
+// 128 x 128 on a full chip: 0.81 of 256 x 256 at M = N = 8192, K = 4096, 0.75 at
+// M = N = K = 4096; it wins where the larger tiles leave CUs idle (M = 4096, N = 1024:
+// 256 tiles against 128 of 128 x 256, 642 against 552 TFLOP/s).
+enum class Tile { kBig, kMid, kTall, kSmall };
 Tile choose_tile(const LoraArgs& p) {
   const int64_t tm = (p.M + 255) / 256;
   const double big = wave_efficiency(tm * ((p.N + 255) / 256));
   const double mid = wave_efficiency(tm * ((p.N + 191) / 192)) * 0.95;
   const double tall = wave_efficiency(((p.M + 127) / 128) * ((p.N + 255) / 256)) * 0.85;
+  const double small = wave_efficiency(((p.M + 127) / 128) * ((p.N + 127) / 128)) * 0.75;
+  if (small > big && small > mid && small > tall) return Tile::kSmall;
   if (mid > big && mid > tall) return Tile::kMid;
   return tall > big ? Tile::kTall : Tile::kBig;
 }
@@ -584,6 +626,7 @@ hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
     switch (choose_tile(p)) {
       case Tile::kMid: return launch_cfg<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
       case Tile::kTall: return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      case Tile::kSmall: return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
       default: return launch_cfg<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
     }
   }
@@ -598,6 +641,38 @@ hipError_t launch_rank(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
 }
 
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+// K splits of the rank pre-pass: enough 128 x 128 tiles to cover the 256 CUs, at least
+// kMinSplitTiles K tiles per split, and a divisor of the K tile count so every split has
+// the same length (the fp32 sums then do not depend on M).
+constexpr int kMaxSplits = 16;
+constexpr int kMinSplitTiles = 4;
+int rank_splits(int64_t M, int64_t K, int64_t r) {
+  const int64_t tiles = ((M + CfgSmall::BM - 1) / CfgSmall::BM) * ((r + CfgSmall::BN - 1) / CfgSmall::BN);
+  const int64_t nk = K / BK;
+  int64_t want = (256 + tiles - 1) / tiles;
+  if (want > kMaxSplits) want = kMaxSplits;
+  if (want > nk / kMinSplitTiles) want = nk / kMinSplitTiles;
+  for (int64_t s = want; s > 1; --s)
+    if (nk % s == 0) return (int)s;
+  return 1;
+}
+
+// T[m][k] = bf16(s * sum_q part[q][m][k]), q in order: 8 consecutive ranks per thread.
+__global__ void __launch_bounds__(256)
+rank_reduce_kernel(const float* __restrict__ part, int splits, int64_t slice, float s,
+                   uint16_t* __restrict__ t) {
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e >= slice) return;
+  f32x4_t lo = *reinterpret_cast<const f32x4_t*>(part + e);
+  f32x4_t hi = *reinterpret_cast<const f32x4_t*>(part + e + 4);
+  for (int q = 1; q < splits; ++q) {
+    lo += *reinterpret_cast<const f32x4_t*>(part + q * slice + e);
+    hi += *reinterpret_cast<const f32x4_t*>(part + q * slice + e + 4);
+  }
+  *reinterpret_cast<u32x4_t*>(t + e) = u32x4_t{pack_bf16x2(s * lo[0], s * lo[1]), pack_bf16x2(s * lo[2], s * lo[3]),
+                                               pack_bf16x2(s * hi[0], s * hi[1]), pack_bf16x2(s * hi[2], s * hi[3])};
+}
 
 }  // namespace
 
@@ -621,10 +696,14 @@ bool prefill_supported(const LoraArgs& p) {
   return true;
 }
 
+// Workspace of the rank pre-pass (r > RIN): T [M][r] bf16, then, when K is split, the
+// fp32 partials [splits][M][r] at the next 256-byte boundary.
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
-  (void)N; (void)K; (void)w_dtype;
+  (void)N; (void)w_dtype;
   if (r <= RIN) return 0;
-  return (size_t)(M * r * 2);
+  const size_t t_bytes = ((size_t)(M * r * 2) + 255) & ~(size_t)255;
+  const int splits = rank_splits(M, K, r);
+  return t_bytes + (splits > 1 ? (size_t)splits * M * r * 4 : 0);
 }
 
 hipError_t launch_prefill(const LoraArgs& p) {
@@ -638,13 +717,27 @@ hipError_t launch_prefill(const LoraArgs& p) {
   if (p.r > RIN) {
     // Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by this same kernel run
     // as a plain GEMM with A in the place of W (N = r) and s applied before rounding.
+    // With few row tiles (N = r is one or two tiles wide) K is split over grid rows into
+    // fp32 partials that a second kernel sums in split order, scales and rounds.
     ldt = p.r;
     uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
     LoraArgs q = p;
     q.w = p.a; q.ldw = p.lda; q.w_dtype = kBF16; q.w_scale = nullptr;
     q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0;
     q.N = p.r; q.y = t; q.ldy = ldt; q.yscale = p.scale;
-    const hipError_t e = launch_rank<kBF16, true>(q, nullptr, 0);
+    const int splits = rank_splits(p.M, p.K, p.r);
+    hipError_t e;
+    if (splits > 1) {
+      float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws) + (((size_t)(p.M * p.r * 2) + 255) & ~(size_t)255));
+      q.y = part; q.K = p.K / splits;
+      e = launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
+      if (e != hipSuccess) return e;
+      const int64_t slice = p.M * p.r;
+      rank_reduce_kernel<<<dim3((unsigned)((slice / 8 + 255) / 256)), dim3(256), 0, p.stream>>>(part, splits, slice, p.scale, t);
+      e = hipGetLastError();
+    } else {
+      e = launch_rank<kBF16, true>(q, nullptr, 0);
+    }
     if (e != hipSuccess) return e;
     tg = t;
   }
