@@ -100,6 +100,12 @@ DECODE_CASES = [
     (3, 5000, 256, 16, 2.0, True),       # short K with rank rows
     (20, 2000, 512, 24, 2.0, True),      # 4 waves per row block
     (64, 1000, 256, 64, 2.0, True),      # short K at the largest M
+    # rows per workgroup chosen by the plan's cost model (16, 32 or 64)
+    (64, 1024, 2048, 64, 2.0, True),     # 16 rows, four token blocks
+    (48, 1024, 2048, 64, 2.0, True),     # 16 rows, three token blocks
+    (40, 6144, 2048, 32, 2.0, True),     # 64 rows, three token blocks
+    (32, 12288, 1024, 16, 2.0, True),    # 64 rows, two token blocks
+    (20, 4096, 1024, 16, 2.0, True),     # 32 rows, two token blocks
 ]
 
 

@@ -269,7 +269,7 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
                                            int kbeg, int kc, int M, char* smem, float* sums,
                                            const Pro& pro = Pro(), const Pre& pre = Pre()) {
   using G = Geo<WDT>;
-  constexpr int PD = NR == 1 ? 4 : 2;   // K steps in flight per wave
+  constexpr int PD = NR == 1 ? 4 : (NR == 2 ? 2 : 1);  // K steps in flight per wave (NR*4*PD = 16 loads)
   constexpr int LPS = NR * 4;           // loads per step
   constexpr int MC = 16 * MB;
   constexpr int PER_LANE = NR * MB * 4;
@@ -809,7 +809,19 @@ size_t plan_smem(const DecodePlan& pl, int64_t M, size_t* flag_off) {
   return *flag_off + 16;  // the broadcast word (the RMSNorm prologue adds its own after it)
 }
 
-DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
+// Modelled time of a plan with `nr` row blocks per wave (KW = 8, so 16*nr rows per W
+// workgroup), in us: one workgroup per CU (the x slice holds most of the LDS), so the
+// grid runs in ceil(workgroups / 256) waves, each costing a fixed latency plus the
+// workgroup's bytes (W rows and x slice) at the rate one CU streams them. Constants from
+// M = 32 and 64 sweeps over N, K in {1024, 2048, 6144}: 4 us and 40 GB/s per CU.
+double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
+  const int64_t rows = 16 * nr;
+  const int64_t wgs = (int64_t)pl.gT * pl.kst + (N + rows - 1) / rows * pl.ksy;
+  const double waves = (double)((wgs + 255) / 256);
+  return waves * (4.0 + (double)((rows + M) * pl.kcy * 2) / 40e3);
+}
+
+DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, bool pick_nr = true) {
   DecodePlan pl{};
   pl.mb = (int)((M + 15) / 16);
   if (pl.mb < 1) pl.mb = 1;
@@ -842,8 +854,28 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt) {
     if (pl.kw == 8 || plan_smem(pl, M, &pl.flag_off) <= (size_t)LDS_MAX) break;
     pl.kw <<= 1;
   }
-  pl.gY = (int)((N + pl.rows - 1) / pl.rows);
   pl.gT = r > 0 ? (int)((r + pl.trows - 1) / pl.trows) : 0;
+  // Two or more token blocks, whole wave steps along K: rows per workgroup (16, 32 or
+  // 64) by the modelled time, among the choices whose LDS fits.
+  if (pick_nr && pl.mb >= 2 && pl.kw == 8 && pl.ksy > 0 && pl.kst > 0) {
+    double best = plan_cost(pl, M, N, pl.nr);
+    const int legacy = pl.nr;
+    for (int nr : {1, 2, 4}) {
+      if (nr == legacy) continue;
+      DecodePlan c = pl;
+      c.nr = nr;
+      c.rows = 16 * nr;
+      size_t fo;
+      if (plan_smem(c, M, &fo) > (size_t)LDS_MAX) continue;
+      const double cost = plan_cost(pl, M, N, nr);
+      if (cost < best) {
+        best = cost;
+        pl.nr = nr;
+      }
+    }
+    pl.rows = 16 * pl.nr;
+  }
+  pl.gY = (int)((N + pl.rows - 1) / pl.rows);
   pl.ok = pl.ksy > 0 && pl.kst > 0 && CNT_YG + pl.gY <= kCounterWords && pl.gT <= CNT_YG - CNT_TG &&
           (uint64_t)pl.gT * pl.kst + (uint64_t)pl.gY * pl.ksy < kLaunchUnit;
   size_t off = kCounterBytes;
@@ -880,26 +912,46 @@ hipError_t launch_one(const DecodeArgs& a, int grid, size_t smem, hipStream_t st
 
 template <int FUSE>
 hipError_t dispatch_fused(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
-  if (nr == 1) {
-    if (mb == 1) return launch_one<kBF16, 1, 1, 8, FUSE>(a, grid, smem, st);
-    return launch_one<kBF16, 1, 2, 8, FUSE>(a, grid, smem, st);
-  }
-  if (mb == 3) return launch_one<kBF16, 2, 3, 8, FUSE>(a, grid, smem, st);
-  return launch_one<kBF16, 2, 4, 8, FUSE>(a, grid, smem, st);
+  if (nr == 1 && mb == 1) return launch_one<kBF16, 1, 1, 8, FUSE>(a, grid, smem, st);
+  if (nr == 1 && mb == 2) return launch_one<kBF16, 1, 2, 8, FUSE>(a, grid, smem, st);
+  if (nr == 2 && mb == 3) return launch_one<kBF16, 2, 3, 8, FUSE>(a, grid, smem, st);
+  if (nr == 2 && mb == 4) return launch_one<kBF16, 2, 4, 8, FUSE>(a, grid, smem, st);
+  return hipErrorInvalidValue;  // the fused plans use the fixed rows-per-group rule only
 }
 
+// Every (rows per group, token blocks) pair a plan can produce maps to its own kernel; any
+// other pair is an error, never a kernel sized for a different plan.
 template <int WDT, int KW>
 hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
   if (nr == 1) {
     if (mb == 1) return launch_one<WDT, 1, 1, KW>(a, grid, smem, st);
-    return launch_one<WDT, 1, 2, KW>(a, grid, smem, st);
+    if (mb == 2) return launch_one<WDT, 1, 2, KW>(a, grid, smem, st);
+    if constexpr (KW == 8) {  // rows per workgroup chosen by plan_cost
+      if (mb == 3) return launch_one<WDT, 1, 3, KW>(a, grid, smem, st);
+      if (mb == 4) return launch_one<WDT, 1, 4, KW>(a, grid, smem, st);
+    }
+    return hipErrorInvalidValue;
   }
-  if constexpr (KW == 1) {  // two row blocks per wave at one or two token blocks
-    if (mb == 1) return launch_one<WDT, 2, 1, KW>(a, grid, smem, st);
-    if (mb == 2) return launch_one<WDT, 2, 2, KW>(a, grid, smem, st);
+  if (nr == 2) {
+    if constexpr (KW == 1) {  // two row blocks per wave at one or two token blocks
+      if (mb == 1) return launch_one<WDT, 2, 1, KW>(a, grid, smem, st);
+      if (mb == 2) return launch_one<WDT, 2, 2, KW>(a, grid, smem, st);
+    }
+    if constexpr (KW == 8) {
+      if (mb == 2) return launch_one<WDT, 2, 2, KW>(a, grid, smem, st);
+    }
+    if (mb == 3) return launch_one<WDT, 2, 3, KW>(a, grid, smem, st);
+    if (mb == 4) return launch_one<WDT, 2, 4, KW>(a, grid, smem, st);
+    return hipErrorInvalidValue;
   }
-  if (mb == 3) return launch_one<WDT, 2, 3, KW>(a, grid, smem, st);
-  return launch_one<WDT, 2, 4, KW>(a, grid, smem, st);
+  if constexpr (KW == 8) {
+    if (nr == 4) {
+      if (mb == 2) return launch_one<WDT, 4, 2, KW>(a, grid, smem, st);
+      if (mb == 3) return launch_one<WDT, 4, 3, KW>(a, grid, smem, st);
+      if (mb == 4) return launch_one<WDT, 4, 4, KW>(a, grid, smem, st);
+    }
+  }
+  return hipErrorInvalidValue;
 }
 
 template <int WDT>
@@ -942,8 +994,11 @@ bool decode_supported(const LoraArgs& p) {
   return plan_decode(p.M, p.N, p.K, p.r, p.w_dtype).ok;
 }
 
+// Covers both the plain launch's plan and the fused launches' (fixed rows per group).
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
-  return plan_decode(M, N, K, r, w_dtype).total;
+  const size_t a = plan_decode(M, N, K, r, w_dtype).total;
+  const size_t b = plan_decode(M, N, K, r, w_dtype, false).total;
+  return a > b ? a : b;
 }
 
 namespace {
@@ -985,8 +1040,8 @@ hipError_t launch_decode(const LoraArgs& p) {
 bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
   if (f.fuse < 1 || f.fuse > 7 || ((f.fuse & kFuseAct) && (f.fuse & kFuseRes))) return false;
   if (!decode_supported(p) || p.w_dtype != kBF16) return false;
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
-  if (pl.kw != 8) return false;
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, false);
+  if (!pl.ok || pl.kw != 8) return false;
   if (f.fuse & kFuseNorm) {
     // whole rows in one slice, up to NORM_CH chunks per thread, w_norm staged after the plan's LDS
     if (pl.ksy != 1 || (p.r > 0 && pl.kst != 1)) return false;
@@ -1016,8 +1071,8 @@ struct ChainLayout {
 };
 ChainLayout chain_layout(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2) {
   ChainLayout c;
-  c.pa = plan_decode(M, N, K, r, kBF16);
-  c.pb = plan_decode(M, N2, N, r2, kBF16);
+  c.pa = plan_decode(M, N, K, r, kBF16, false);
+  c.pb = plan_decode(M, N2, N, r2, kBF16, false);
   c.off_a = kCounterBytes + kChainDoneBytes;  // plan offsets already skip kCounterBytes
   c.off_b = align256(c.off_a + (c.pa.total - kCounterBytes));
   c.total = c.off_b + (c.pb.total - kCounterBytes);
@@ -1054,12 +1109,11 @@ hipError_t launch_chain_one(const DecodeArgs& a, const DecodeArgs& b, int grid, 
 template <int FUSE_B>
 hipError_t launch_chain_fb(const DecodeArgs& a, const DecodeArgs& b, int mb, int nr, int grid, size_t smem,
                            hipStream_t st) {
-  if (nr == 1) {
-    return mb == 1 ? launch_chain_one<1, 1, FUSE_B>(a, b, grid, smem, st)
-                   : launch_chain_one<1, 2, FUSE_B>(a, b, grid, smem, st);
-  }
-  return mb == 3 ? launch_chain_one<2, 3, FUSE_B>(a, b, grid, smem, st)
-                 : launch_chain_one<2, 4, FUSE_B>(a, b, grid, smem, st);
+  if (nr == 1 && mb == 1) return launch_chain_one<1, 1, FUSE_B>(a, b, grid, smem, st);
+  if (nr == 1 && mb == 2) return launch_chain_one<1, 2, FUSE_B>(a, b, grid, smem, st);
+  if (nr == 2 && mb == 3) return launch_chain_one<2, 3, FUSE_B>(a, b, grid, smem, st);
+  if (nr == 2 && mb == 4) return launch_chain_one<2, 4, FUSE_B>(a, b, grid, smem, st);
+  return hipErrorInvalidValue;  // chained plans use the fixed rows-per-group rule only
 }
 }  // namespace
 
@@ -1084,7 +1138,7 @@ hipError_t launch_decode_chain(const LoraArgs& pa, const FusedArgs& fa, const Lo
 }
 
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, false);
   DecodeArgs a = make_args(p, pl);
   a.nw = reinterpret_cast<const uint16_t*>(f.nw); a.eps = f.eps;
   a.nw_off = (int)pl.flag_off + 16 + kNormLds;
