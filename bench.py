@@ -11,9 +11,14 @@ weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
 projections, and the CPU baseline (the reference's fp32 arithmetic on host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
-                      [--only c2|c3|c4|c5|emb] [--copy-calibration]
+                      [--only c2|c3|c4|c5|emb|vendor|shape] [--shape M,N,K,r] [--vendor]
+                      [--copy-calibration]
 
 --only runs one section and prints its JSON alone (for profiling one workload).
+--only vendor times the same shapes through torch.matmul (hipBLASLt): the plain GEMM and
+the unfused three-call LoRA linear, beside the fused op.
+--only shape runs five eager launches of one M,N,K,r shape (the fused op, or with
+--vendor torch.matmul's plain GEMM), for rocprofv3 counter runs of a single kernel.
 --copy-calibration first runs a plain device copy of COPY_BYTES bytes (three launches),
 the reference point against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are
 scaled to HBM bytes.
@@ -110,6 +115,82 @@ class ProjectionStack:
     def bytes(self):
         wb = 1 if self.fp8 else 2
         return self.layers * sum(lora_bytes(self.M, N, K, self.r, wb, self.fp8) for _, N, K in self.shapes)
+
+
+class VendorStack(ProjectionStack):
+    """The same inputs run through torch.matmul (hipBLASLt on this image): the plain
+    base GEMM x . W^T, and the unfused LoRA linear x . W^T + s (x . A^T) . B^T (three
+    library calls, the reference's arithmetic)."""
+
+    def run_plain(self):
+        for l in range(self.layers):
+            c = l % self.copies
+            for p, (_, N, K) in enumerate(self.shapes):
+                torch.matmul(self.x[K], self.W[c][p].t())
+
+    def run_lora(self):
+        for l in range(self.layers):
+            c = l % self.copies
+            for p, (_, N, K) in enumerate(self.shapes):
+                x = self.x[K]
+                torch.addmm(torch.matmul(x, self.W[c][p].t()), torch.matmul(x, self.A[l][p].t()),
+                            self.B[l][p].t(), alpha=self.scale)
+
+
+def bench_vendor(dev, steps, warmup):
+    """Vendor-library comparison on the headline shapes, in one process: the fused op
+    against torch.matmul's plain GEMM and the unfused three-call LoRA linear, each
+    captured as a HIP graph of the same launches. Prefill: configs 2 (0.6B, 28 layers)
+    and the 1.7B shapes (4 layers), M = 8192, r = 32, TFLOP/s of the LoRA linear's FLOPs
+    (the plain GEMM's own FLOPs for the plain line). Decode: config 3 (1.7B, r = 64,
+    28 layers, 6 rotating weight copies), GB/s of the LoRA linear's bytes."""
+    out = {}
+    for name, shapes, layers in (("c2_qwen3_0.6b_prefill", QWEN3_0P6B, 28), ("qwen3_1.7b_prefill", QWEN3_1P7B, 4)):
+        st = VendorStack(shapes, M=8192, r=32, layers=layers, dev=dev, seed=2)
+        plain_flops = layers * sum(2.0 * 8192 * N * K for _, N, K in shapes)
+        row = {}
+        for label, fn, fl in (("wsl_fused", st.run, st.flops()), ("torch_plain_gemm", st.run_plain, plain_flops),
+                              ("torch_unfused_lora", st.run_lora, st.flops())):
+            g = graph_of(fn)
+            ms = time_replays(g, steps, warmup)
+            row[label] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1)}
+            del g
+        out[name] = row
+        del st
+        torch.cuda.empty_cache()
+    dec = {}
+    for M in (1, 8, 32, 64):
+        st = VendorStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
+        row = {}
+        for label, fn in (("wsl_fused", st.run), ("torch_plain_gemm", st.run_plain), ("torch_unfused_lora", st.run_lora)):
+            g = graph_of(fn)
+            ms = time_replays(g, steps, warmup)
+            row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1)}
+            del g
+        dec[f"M={M}"] = row
+        del st
+        torch.cuda.empty_cache()
+    out["c3_qwen3_1.7b_decode_cold"] = dec
+    return out
+
+
+def run_shape(dev, shape, vendor):
+    """Five eager launches of one shape (for rocprofv3 runs of a single kernel):
+    wsl.lora_linear, or with `vendor` torch.matmul's plain GEMM."""
+    M, N, K, r = shape
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    W = (torch.randn(N, K, device=dev, generator=g) * 0.02).bfloat16()
+    A = (torch.randn(r, K, device=dev, generator=g) * 0.02).bfloat16() if r else None
+    B = (torch.randn(N, r, device=dev, generator=g) * 0.02).bfloat16() if r else None
+    from weightshared_torchtitan_amd import lora_linear
+    for _ in range(5):
+        if vendor:
+            torch.matmul(x, W.t())
+        else:
+            lora_linear(x, W, A, B, 2.0)
+    torch.cuda.synchronize()
+    return {"M": M, "N": N, "K": K, "r": r, "launches": 5, "vendor": bool(vendor)}
 
 
 def graph_of(fn):
@@ -296,7 +377,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5", "emb"), default=None)
+    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5", "emb", "vendor", "shape"), default=None)
+    ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
+    ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -316,7 +399,9 @@ def main():
         fn = {"c3": lambda: bench_c3(dev, args.steps, args.warmup),
               "c4": lambda: bench_c4(dev),
               "c5": lambda: bench_c5(dev, args.steps, args.warmup),
-              "emb": lambda: bench_embedding(dev, args.steps, args.warmup)}[args.only]
+              "emb": lambda: bench_embedding(dev, args.steps, args.warmup),
+              "vendor": lambda: bench_vendor(dev, args.steps, args.warmup),
+              "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     flops, ms = bench_c2(dev, args.steps, args.warmup)

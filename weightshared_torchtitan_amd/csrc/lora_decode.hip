@@ -22,20 +22,21 @@
 // Cross-workgroup hand-offs (T to the W workgroups; the partial sums of a K split to
 // the last of its workgroups) go through the workspace with agent-scope atomic loads
 // and stores, which are coherent across the XCDs' L2s without the whole-L2 write-back
-// and invalidate that a device-scope fence costs on this part; where data precedes a
-// counter, an s_waitcnt vmcnt(0) orders it ahead of the increment.
+// and invalidate that a device-scope fence costs on this part.
 //
-// T needs no counter: each element is published as one 64-bit word (launch tag << 16 |
-// bf16 bits), so a reader knows an element is this launch's by its tag. The tag is the
-// launch ordinal + 1, read from a 64-bit launch counter in the workspace prefix: every
-// workgroup adds C / total at exit (workgroup 0 also adds C % total), so each launch
-// adds exactly C; a workgroup reads the counter when it starts, before its own
-// addition, so floor(count / C) is the ordinal of the running launch for every one of
-// its workgroups. The per-group counters of a K split are reset by their last arriver.
-// Every launch therefore leaves the prefix in a valid state without a final barrier.
-// A W workgroup waits for T with a bounded poll (T workgroups never wait on anything
-// and are dispatched first); past the bound it computes T itself, so the launch always
-// drains.
+// Neither needs a counter: each element is published as one 64-bit word that carries
+// the launch's tag (T: bf16 bits under a 48-bit tag with bit 63 set; a partial sum: fp32
+// bits under a 31-bit tag, bit 63 clear), so a reader knows an element is this launch's
+// by its tag. The tag is the launch ordinal + 1, read from a 64-bit launch counter in
+// the workspace prefix: every workgroup adds C / total at exit (workgroup 0 also adds
+// C % total), so each launch adds exactly C; a workgroup reads the counter when it
+// starts, before its own addition, so floor(count / C) is the ordinal of the running
+// launch for every one of its workgroups. Every launch therefore leaves the prefix in a
+// valid state without a final barrier. The reader of a K split is its last workgroup.
+// Readers wait with a bounded poll on workgroups dispatched before them that never wait
+// themselves (T workgroups come first; workgroups are dispatched in index order); past
+// the bound a reader computes the missing values itself from x and the weights, so the
+// launch always drains.
 //
 // Optional fusions serve the decode step of the weight-shared Qwen3 harness (bf16 W):
 //   RMSNorm prologue   the projection input is bf16(x * rsqrt(mean(x^2) + eps) * w_norm);
@@ -66,11 +67,8 @@ constexpr int64_t LDS_MAX = 160 * 1024;     // gfx950 LDS per workgroup
 constexpr int64_t BL_MAX = 32 * 256 * 2;    // B rows of one group: 32 rows x r32 <= 256
 constexpr int64_t XS_MAX = LDS_MAX - BL_MAX - 1024;
 
-// Words of the workspace prefix: a 64-bit launch counter, then 32-bit arrival counters.
-constexpr int CNT_LAUNCH = 0;  // 64-bit, words 0-1
-constexpr int CNT_TG = 16;     // [16] arrivals per T group (K split)
-constexpr int CNT_YG = 64;     // [..] arrivals per W group (K split)
-constexpr int kCounterWords = (int)(kCounterBytes / 4);
+// Words of the workspace prefix: a 64-bit launch counter (words 0-1); the rest stays zero.
+constexpr int CNT_LAUNCH = 0;
 constexpr uint64_t kLaunchUnit = 1ull << 20;  // C: what one launch adds to the counter
 constexpr uint64_t kTagMask = (1ull << 48) - 1;
 
@@ -224,9 +222,9 @@ struct DecodeArgs {
   int gY, ksy, kcy;   // W groups (16*NR rows of W), K split and slice
   int flag_off;       // LDS byte offset of the broadcast word
   unsigned* cnt;      // counter prefix of the workspace
-  uint64_t* tfin;     // T [M][r]: tag << 16 | bf16 bits
-  float* tpart;       // [gT][kst][M][T rows per group]
-  float* ypart;       // [gY][ksy][M][W rows per group]
+  uint64_t* tfin;     // T [M][r]: ttag << 16 | bf16 bits
+  uint64_t* tpart;    // [gT][kst][T rows per group][M]: ptag << 32 | fp32 partial sum
+  uint64_t* ypart;    // [gY][ksy][W rows per group][M]: likewise
   int spin;           // polls of the T counter before the local fallback
   // chained launches: a producer publishes (tag) per W group once its y rows are out;
   // a consumer waits for all of them before it reads x (= the producer's y)
@@ -243,9 +241,6 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 }
 __device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
   return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned add_agent(unsigned* p, unsigned v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_agent(unsigned* p, unsigned v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -336,6 +331,10 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
   }
 
   // Cross-wave reduction within each row block (the x slice is dead: its LDS is reused).
+  // The first wave of a row block writes its sums in place (D[row][m]: lane holds
+  // m = l16, rows grp*4 + e of block i); the others park theirs in `red` in register
+  // order, and then every thread finishes a share of the elements, adding the waves in
+  // order (a single summing wave was the launch's longest step at 64 rows x 64 tokens).
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
   if (kw > 0) {
@@ -347,65 +346,110 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           red[(slot * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane] = acc[i][mb][e];
-  }
-  __syncthreads();
-  if (kw == 0) {
+  } else {
 #pragma unroll
     for (int i = 0; i < NR; ++i)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        f32x4_t v = acc[i][mb];
-        for (int w2 = 0; w2 < KW - 1; ++w2)
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            v[e] += red[((rb * (KW - 1) + w2) * PER_LANE + (i * MB + mb) * 4 + e) * 64 + lane];
-        // D[row][m]: lane holds m = l16, rows grp*4 + e of block i of row block rb
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sums[(rb * 16 * NR + i * 16 + grp * 4 + e) * MC + mb * 16 + l16] = v[e];
-      }
+        for (int e = 0; e < 4; ++e) sums[(rb * 16 * NR + i * 16 + grp * 4 + e) * MC + mb * 16 + l16] = acc[i][mb][e];
   }
   __syncthreads();
+  if constexpr (KW > 1) {
+    constexpr int EPB = PER_LANE * 64;  // register-order elements of one row block
+    for (int gidx = tid; gidx < (NWV / KW) * EPB; gidx += DT) {
+      const int rbg = gidx / EPB, el = gidx % EPB;
+      const int k = el / 64, ln = el % 64;  // k = (i * MB + mb) * 4 + e
+      const int e = k % 4, mb = (k / 4) % MB, i = k / (4 * MB);
+      float* dst = sums + (rbg * 16 * NR + i * 16 + (ln >> 4) * 4 + e) * MC + mb * 16 + (ln & 15);
+      float v = *dst;
+      for (int w2 = 0; w2 < KW - 1; ++w2) v += red[(rbg * (KW - 1) + w2) * EPB + el];
+      *dst = v;
+    }
+    __syncthreads();
+  }
 }
 
-// The K split of a group: publish this workgroup's partial sums; the last arriver sums
-// all partials in split order (so the result does not depend on arrival order) into
-// `sums` and returns true. With one split, returns true at once.
-template <int ROWS, int MC>
-__device__ __forceinline__ bool split_reduce(float* sums, float* part, unsigned* cnt, int ks, int ksplit,
-                                             int M, int* flag) {
+// One partial sum recomputed from global memory: row `row` of `mat` (bf16 or fp8) against
+// x[m] over [kbeg, kbeg + kc). The reducer's fallback past its poll bound.
+template <int WDT>
+__device__ float direct_partial(const void* __restrict__ mat, int64_t ldm, int row, const uint16_t* __restrict__ x,
+                                int64_t ldx, int m, int kbeg, int kc) {
+  float acc = 0.f;
+  for (int k = kbeg; k < kbeg + kc; ++k) {
+    float wv;
+    if constexpr (WDT == kFP8)
+      wv = __builtin_amdgcn_cvt_pk_f32_fp8((int)reinterpret_cast<const uint8_t*>(mat)[(int64_t)row * ldm + k], false)[0];
+    else
+      wv = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(mat)[(int64_t)row * ldm + k]);
+    acc += wv * bf16_bits_to_f32(x[(int64_t)m * ldx + k]);
+  }
+  return acc;
+}
+
+// The K split of a group. Element q = (row rl, token m), tokens fastest (consecutive
+// threads read consecutive LDS words). Every split but the last publishes its partial
+// sums as 64-bit words ptag << 32 | fp32 bits (bit 63 clear: never a T word) and is done
+// (no wait, no counter). The last split, dispatched after all the others (workgroups are
+// dispatched in index order, and the others never wait), polls their words (LB elements
+// in flight per thread, one split at a time), sums them in split order with its own last
+// (so the result does not depend on timing) and returns true. Past the poll bound it recomputes
+// a missing partial from W and x. With one split, returns true at once.
+template <int WDT, int ROWS, int MC>
+__device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks, int ksplit, int M, uint32_t ptag,
+                                             int spin, const void* mat, int64_t ldm, int nrows, int row0,
+                                             const uint16_t* x, int64_t ldx, int kc) {
   if (ksplit == 1) return true;
   const int tid = threadIdx.x;
   const int n = M * ROWS;
-  for (int q = tid; q < n; q += DT) {
-    const int m = q / ROWS, rl = q % ROWS;
-    st_agent(part + (int64_t)ks * n + q, sums[rl * MC + m]);
-  }
-  wait_vm<0>();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned old = add_agent(cnt, 1u);
-    const bool last = old == (unsigned)(ksplit - 1);
-    if (last) st_agent(cnt, 0u);  // every other split has arrived: reset for the next launch
-    *flag = last ? 1 : 0;
-  }
-  __syncthreads();
-  if (*flag == 0) return false;
-  for (int q = tid; q < n; q += DT) {
-    float v = 0.f;
-    for (int s0 = 0; s0 < ksplit; s0 += LB) {  // LB partials in flight (clamped), summed in split order
-      float pv[LB];
-#pragma unroll
-      for (int u = 0; u < LB; ++u) pv[u] = ld_agent(part + (int64_t)min(s0 + u, ksplit - 1) * n + q);
-#pragma unroll
-      for (int u = 0; u < LB; ++u)
-        if (s0 + u < ksplit) v += pv[u];
+  const uint64_t hi = (uint64_t)ptag << 32;
+  if (ks < ksplit - 1) {
+    for (int q = tid; q < n; q += DT) {
+      const int rl = q / M, m = q % M;
+      st_agent(part + (int64_t)ks * n + q, hi | __float_as_uint(sums[rl * MC + m]));
     }
-    const int m = q / ROWS, rl = q % ROWS;
-    sums[rl * MC + m] = v;
+    return false;
+  }
+  for (int q0 = 0; q0 < n; q0 += LB * DT) {
+    float v[LB];
+#pragma unroll
+    for (int u = 0; u < LB; ++u) v[u] = 0.f;
+    for (int sp = 0; sp < ksplit - 1; ++sp) {
+      uint64_t* ps = part + (int64_t)sp * n;
+      uint64_t w[LB];
+#pragma unroll
+      for (int u = 0; u < LB; ++u) w[u] = ld_agent(ps + min(q0 + u * DT + tid, n - 1));
+#pragma unroll
+      for (int u = 0; u < LB; ++u) {
+        const int q = q0 + u * DT + tid;
+        if (q < n) {
+          for (int it = 0; (w[u] >> 32) != ptag && it < spin; ++it) w[u] = ld_agent(ps + q);
+          const int rl = q / M, m = q % M;
+          v[u] += (w[u] >> 32) == ptag
+                      ? __uint_as_float((uint32_t)w[u])
+                      : direct_partial<WDT>(mat, ldm, min(row0 + rl, nrows - 1), x, ldx, m, sp * kc, kc);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      const int q = q0 + u * DT + tid;
+      if (q < n) {
+        const int rl = q / M, m = q % M;
+        sums[rl * MC + m] = v[u] + sums[rl * MC + m];
+      }
+    }
   }
   __syncthreads();
   return true;
 }
+
+// Tags of the two kinds of hand-off word. A T word's upper 48 bits are 1 << 47 | the low
+// 47 bits of the launch tag; a partial-sum word's upper 32 bits are the launch tag folded
+// into [1, 2^31 - 1], so bit 63 tells the kinds apart (workspaces are shared by launches
+// of different shapes, whose regions overlap) and a zero word matches neither.
+__device__ __forceinline__ uint64_t ttag_of(uint64_t tag) { return (1ull << 47) | (tag & ((1ull << 47) - 1)); }
+__device__ __forceinline__ uint32_t ptag_of(uint64_t tag) { return (uint32_t)((tag - 1) % 0x7fffffffull) + 1u; }
 
 // T[m][j] (bf16) into LDS tl[m][0..r32) (row stride r32 + 8 elements), zero for m >= M
 // or j >= r. Polls (bounded) until every element carries this launch's tag; past the
@@ -438,6 +482,7 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
                                          const float* ss = nullptr) {
   const int tid = threadIdx.x;
   const int tls = p.r32 + 8;
+  const uint64_t ttag = ttag_of(tag);
   for (int q = tid; q < MC * tls; q += DT) tl[q] = 0;
   const int n = p.M * p.r;
   if (tid == 0) *flag = 0;
@@ -452,8 +497,8 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
     for (int u = 0; u < LB; ++u) {
       const int q = q0 + u * DT + tid;
       if (q < n) {
-        for (int it = 0; (v[u] >> 16) != tag && it < p.spin; ++it) v[u] = ld_agent(p.tfin + q);
-        if ((v[u] >> 16) != tag) *flag = 1;
+        for (int it = 0; (v[u] >> 16) != ttag && it < p.spin; ++it) v[u] = ld_agent(p.tfin + q);
+        if ((v[u] >> 16) != ttag) *flag = 1;
         const int m = q / p.r, j = q % p.r;
         tl[m * tls + j] = (uint16_t)(v[u] & 0xffffu);
       }
@@ -623,11 +668,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
       slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums);
     }
-    if (split_reduce<TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, p.cnt + CNT_TG + g, ks,
-                                p.kst, p.M, flag)) {
+    if (split_reduce<kBF16, TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, ks, p.kst, p.M,
+                                       ptag_of(tag), p.spin, p.a, p.lda, p.r, g * TROWS, p.x, p.ldx,
+                                       p.kct)) {
       for (int q = tid; q < p.M * TROWS; q += DT) {
         const int m = q / TROWS, rl = q % TROWS, j = g * TROWS + rl;
-        if (j < p.r) st_agent(p.tfin + m * p.r + j, (tag << 16) | f32_to_bf16_bits(p.s * sums[rl * MC + m]));
+        if (j < p.r) st_agent(p.tfin + m * p.r + j, (ttag_of(tag) << 16) | f32_to_bf16_bits(p.s * sums[rl * MC + m]));
       }
     }
   } else {
@@ -660,8 +706,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
       slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
     }
-    if (split_reduce<ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, p.cnt + CNT_YG + g, ks,
-                               p.ksy, p.M, flag)) {
+    if (split_reduce<WDT, ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, ks, p.ksy, p.M,
+                                    ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy)) {
       if (p.r > 0) gather_t<MC, NORM, CONS>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16));
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
       const int l16 = lane & 15, grp = lane >> 4;
@@ -876,17 +922,17 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, bool
     pl.rows = 16 * pl.nr;
   }
   pl.gY = (int)((N + pl.rows - 1) / pl.rows);
-  pl.ok = pl.ksy > 0 && pl.kst > 0 && CNT_YG + pl.gY <= kCounterWords && pl.gT <= CNT_YG - CNT_TG &&
+  pl.ok = pl.ksy > 0 && pl.kst > 0 &&
           (uint64_t)pl.gT * pl.kst + (uint64_t)pl.gY * pl.ksy < kLaunchUnit;
   size_t off = kCounterBytes;
   pl.off_t = off;
   off += (size_t)M * r * 8;
   off = (off + 255) & ~(size_t)255;
   pl.off_pt = off;
-  if (pl.kst > 1) off += (size_t)pl.gT * pl.kst * M * pl.trows * 4;
+  if (pl.kst > 1) off += (size_t)pl.gT * pl.kst * M * pl.trows * 8;
   off = (off + 255) & ~(size_t)255;
   pl.off_py = off;
-  if (pl.ksy > 1) off += (size_t)pl.gY * pl.ksy * M * pl.rows * 4;
+  if (pl.ksy > 1) off += (size_t)pl.gY * pl.ksy * M * pl.rows * 8;
   pl.total = off;
   pl.smem = plan_smem(pl, M, &pl.flag_off);
   if (pl.smem > (size_t)LDS_MAX) pl.ok = false;
@@ -1018,8 +1064,8 @@ DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl, char* cnt, char* d
   a.flag_off = (int)pl.flag_off;
   a.cnt = reinterpret_cast<unsigned*>(cnt);
   a.tfin = reinterpret_cast<uint64_t*>(data + pl.off_t);
-  a.tpart = reinterpret_cast<float*>(data + pl.off_pt);
-  a.ypart = reinterpret_cast<float*>(data + pl.off_py);
+  a.tpart = reinterpret_cast<uint64_t*>(data + pl.off_pt);
+  a.ypart = reinterpret_cast<uint64_t*>(data + pl.off_py);
   a.spin = spin_limit();
   return a;
 }
@@ -1078,7 +1124,6 @@ ChainLayout chain_layout(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2,
   c.total = c.off_b + (c.pb.total - kCounterBytes);
   return c;
 }
-int half_words() { return (int)(kChainHalf / 4); }
 }  // namespace
 
 size_t decode_chain_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2) {
@@ -1092,7 +1137,6 @@ bool decode_chain_supported(const LoraArgs& pa, const FusedArgs& fa, const LoraA
   if (pa.N % 16 != 0) return false;  // whole 4-element stores in the producer
   const ChainLayout c = chain_layout(pa.M, pa.N, pa.K, pa.r, pb.N, pb.r);
   if (c.pa.gY > kChainDoneMax) return false;
-  if (CNT_YG + c.pa.gY > half_words() || CNT_YG + c.pb.gY > half_words()) return false;
   if (c.pa.mb != c.pb.mb || c.pa.nr != c.pb.nr) return false;
   return true;
 }
