@@ -47,11 +47,11 @@ extern "C" {
  * function: touches no device.
  *
  * Workspace contract: the workspace must be zero-filled before its first use. It
- * starts with WSL_COUNTER_BYTES of launch and arrival counters that every completed
- * call leaves valid for the next one, so a workspace is allocated and zeroed once and
- * then reused; do not modify it between calls. Calls that may run concurrently
- * (different streams) must not share a workspace. The rest of the workspace is scratch
- * whose contents do not matter.
+ * starts with WSL_COUNTER_BYTES holding a launch counter (the rest of the prefix stays
+ * zero) that every completed call leaves valid for the next one, so a workspace is
+ * allocated and zeroed once and then reused; do not modify it between calls. Calls that
+ * may run concurrently (different streams) must not share a workspace. The rest of the
+ * workspace holds scratch data and launch-tagged hand-off words.
  */
 #define WSL_COUNTER_BYTES 65536
 int wsl_lora_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r,

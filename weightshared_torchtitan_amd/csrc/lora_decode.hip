@@ -629,7 +629,7 @@ struct ConsumerPre {
 // y with agent-scope stores and then publishes the tag for its W group; a consumer
 // (RMSNorm prologue) takes its x from the producer's y once every group is published.
 template <int WDT, int NR, int MB, int KW, int FUSE, int ROLE>
-__device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64_t tag, char* smem) {
+__device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64_t cnt_raw, char* smem) {
   constexpr bool NORM = (FUSE & kFuseNorm) != 0;
   constexpr bool ACT = (FUSE & kFuseAct) != 0;
   constexpr bool RES = (FUSE & kFuseRes) != 0;
@@ -646,6 +646,14 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nT = p.gT * p.kst;
   int* flag = reinterpret_cast<int*>(smem + p.flag_off);
+  // The launch counter was loaded at entry. The tag is formed where it is first needed,
+  // behind an empty asm: formed at entry, its wait for the load (a memory round trip)
+  // held back every workgroup's first W and x loads.
+  const auto late_tag = [cnt_raw]() {
+    uint64_t c = cnt_raw;
+    asm volatile("" : "+v"(c));
+    return (c / kLaunchUnit + 1) & kTagMask;
+  };
 
   if (bid < nT) {
     // ---------------- T workgroup: TROWS rows of A over one K slice
@@ -657,7 +665,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums,
                                    NormPrologue{&p, smem, ss, smem + p.nw_off},
-                                   ConsumerPre{&p, smem, smem + p.nw_off, tag, flag});
+                                   ConsumerPre{&p, smem, smem + p.nw_off, late_tag(), flag});
     } else if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
@@ -668,6 +676,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
       slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums);
     }
+    const uint64_t tag = late_tag();
     if (split_reduce<kBF16, TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, ks, p.kst, p.M,
                                        ptag_of(tag), p.spin, p.a, p.lda, p.r, g * TROWS, p.x, p.ldx,
                                        p.kct)) {
@@ -693,7 +702,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
       slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums,
                                   NormPrologue{&p, smem, ss, smem + p.nw_off},
-                                  ConsumerPre{&p, smem, smem + p.nw_off, tag, flag});
+                                  ConsumerPre{&p, smem, smem + p.nw_off, late_tag(), flag});
     } else if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
@@ -706,6 +715,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
       slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
     }
+    const uint64_t tag = late_tag();
     if (split_reduce<WDT, ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, ks, p.ksy, p.M,
                                     ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy)) {
       if (p.r > 0) gather_t<MC, NORM, CONS>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16));
@@ -786,9 +796,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
   }
 }
 
-// This launch's tag (see the file comment), read before this workgroup's exit addition.
-__device__ __forceinline__ uint64_t launch_tag(const unsigned* cnt) {
-  return (ld_agent(reinterpret_cast<const uint64_t*>(cnt + CNT_LAUNCH)) / kLaunchUnit + 1) & kTagMask;
+// The launch counter, read before this workgroup's exit addition; the body forms the
+// launch's tag from it (see the file comment).
+__device__ __forceinline__ uint64_t launch_count(const unsigned* cnt) {
+  return ld_agent(reinterpret_cast<const uint64_t*>(cnt + CNT_LAUNCH));
 }
 
 // Exit: this workgroup's share of the launch's C (the tag was consumed above).
@@ -804,8 +815,7 @@ __device__ __forceinline__ void launch_exit(unsigned* cnt, int total_wgs) {
 template <int WDT, int NR, int MB, int KW, int FUSE>
 __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  const uint64_t tag = launch_tag(p.cnt);
-  decode_body<WDT, NR, MB, KW, FUSE, kRolePlain>(p, blockIdx.x, tag, smem);
+  decode_body<WDT, NR, MB, KW, FUSE, kRolePlain>(p, blockIdx.x, launch_count(p.cnt), smem);
   launch_exit(p.cnt, p.gT * p.kst + p.gY * p.ksy);
 }
 
@@ -817,11 +827,11 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
 template <int NR, int MB, int FUSE_B>
 __global__ void __launch_bounds__(DT) chain_kernel(DecodeArgs a, DecodeArgs b) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  const uint64_t tag = launch_tag(a.cnt);
+  const uint64_t cnt_raw = launch_count(a.cnt);
   const int na = a.gT * a.kst + a.gY * a.ksy;
   const int bid = blockIdx.x;
-  if (bid < na) decode_body<kBF16, NR, MB, 8, kFuseRes, kRoleProducer>(a, bid, tag, smem);
-  else decode_body<kBF16, NR, MB, 8, FUSE_B, kRoleConsumer>(b, bid - na, tag, smem);
+  if (bid < na) decode_body<kBF16, NR, MB, 8, kFuseRes, kRoleProducer>(a, bid, cnt_raw, smem);
+  else decode_body<kBF16, NR, MB, 8, FUSE_B, kRoleConsumer>(b, bid - na, cnt_raw, smem);
   launch_exit(a.cnt, na + b.gT * b.kst + b.gY * b.ksy);
 }
 
