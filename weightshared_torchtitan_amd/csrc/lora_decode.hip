@@ -877,7 +877,11 @@ double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
   return waves * (4.0 + (double)((rows + M) * pl.kcy * 2) / 40e3);
 }
 
-DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, bool pick_nr = true) {
+// Which rows-per-group choices a plan may take: every one (plain launches), those the
+// fused kernels are built for (one token block), or none (chained launches: fixed rule).
+enum class Pick { kAll, kFused, kFixed };
+
+DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick pick = Pick::kAll) {
   DecodePlan pl{};
   pl.mb = (int)((M + 15) / 16);
   if (pl.mb < 1) pl.mb = 1;
@@ -911,9 +915,11 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, bool
     pl.kw <<= 1;
   }
   pl.gT = r > 0 ? (int)((r + pl.trows - 1) / pl.trows) : 0;
-  // Two or more token blocks, whole wave steps along K: rows per workgroup (16, 32 or
-  // 64) by the modelled time, among the choices whose LDS fits.
-  if (pick_nr && pl.mb >= 2 && pl.kw == 8 && pl.ksy > 0 && pl.kst > 0) {
+  // Whole wave steps along K: rows per workgroup (16, 32 or 64) by the modelled time,
+  // among the choices whose LDS fits. (At M = 1 and 8, 6144 x 2048 went 13.0 -> 11.3 us;
+  // fp8 at M = 16, 12288 x 4096 went 40.7 -> 20.6 us: one wave of workgroups, not three.)
+  const bool can_pick = pick == Pick::kAll || (pick == Pick::kFused && pl.mb == 1);
+  if (can_pick && pl.kw == 8 && pl.ksy > 0 && pl.kst > 0) {
     double best = plan_cost(pl, M, N, pl.nr);
     const int legacy = pl.nr;
     for (int nr : {1, 2, 4}) {
@@ -969,10 +975,12 @@ hipError_t launch_one(const DecodeArgs& a, int grid, size_t smem, hipStream_t st
 template <int FUSE>
 hipError_t dispatch_fused(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
   if (nr == 1 && mb == 1) return launch_one<kBF16, 1, 1, 8, FUSE>(a, grid, smem, st);
+  if (nr == 2 && mb == 1) return launch_one<kBF16, 2, 1, 8, FUSE>(a, grid, smem, st);
+  if (nr == 4 && mb == 1) return launch_one<kBF16, 4, 1, 8, FUSE>(a, grid, smem, st);
   if (nr == 1 && mb == 2) return launch_one<kBF16, 1, 2, 8, FUSE>(a, grid, smem, st);
   if (nr == 2 && mb == 3) return launch_one<kBF16, 2, 3, 8, FUSE>(a, grid, smem, st);
   if (nr == 2 && mb == 4) return launch_one<kBF16, 2, 4, 8, FUSE>(a, grid, smem, st);
-  return hipErrorInvalidValue;  // the fused plans use the fixed rows-per-group rule only
+  return hipErrorInvalidValue;  // Pick::kFused plans produce only these pairs
 }
 
 // Every (rows per group, token blocks) pair a plan can produce maps to its own kernel; any
@@ -994,6 +1002,7 @@ hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t sme
       if (mb == 2) return launch_one<WDT, 2, 2, KW>(a, grid, smem, st);
     }
     if constexpr (KW == 8) {
+      if (mb == 1) return launch_one<WDT, 2, 1, KW>(a, grid, smem, st);
       if (mb == 2) return launch_one<WDT, 2, 2, KW>(a, grid, smem, st);
     }
     if (mb == 3) return launch_one<WDT, 2, 3, KW>(a, grid, smem, st);
@@ -1002,6 +1011,7 @@ hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t sme
   }
   if constexpr (KW == 8) {
     if (nr == 4) {
+      if (mb == 1) return launch_one<WDT, 4, 1, KW>(a, grid, smem, st);
       if (mb == 2) return launch_one<WDT, 4, 2, KW>(a, grid, smem, st);
       if (mb == 3) return launch_one<WDT, 4, 3, KW>(a, grid, smem, st);
       if (mb == 4) return launch_one<WDT, 4, 4, KW>(a, grid, smem, st);
@@ -1050,11 +1060,13 @@ bool decode_supported(const LoraArgs& p) {
   return plan_decode(p.M, p.N, p.K, p.r, p.w_dtype).ok;
 }
 
-// Covers both the plain launch's plan and the fused launches' (fixed rows per group).
+// Covers the plain, fused and chained launches' plans of the problem.
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
   const size_t a = plan_decode(M, N, K, r, w_dtype).total;
-  const size_t b = plan_decode(M, N, K, r, w_dtype, false).total;
-  return a > b ? a : b;
+  const size_t b = plan_decode(M, N, K, r, w_dtype, Pick::kFused).total;
+  const size_t c = plan_decode(M, N, K, r, w_dtype, Pick::kFixed).total;
+  const size_t ab = a > b ? a : b;
+  return ab > c ? ab : c;
 }
 
 namespace {
@@ -1096,7 +1108,7 @@ hipError_t launch_decode(const LoraArgs& p) {
 bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
   if (f.fuse < 1 || f.fuse > 7 || ((f.fuse & kFuseAct) && (f.fuse & kFuseRes))) return false;
   if (!decode_supported(p) || p.w_dtype != kBF16) return false;
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, false);
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kFused);
   if (!pl.ok || pl.kw != 8) return false;
   if (f.fuse & kFuseNorm) {
     // whole rows in one slice, up to NORM_CH chunks per thread, w_norm staged after the plan's LDS
@@ -1127,8 +1139,8 @@ struct ChainLayout {
 };
 ChainLayout chain_layout(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2) {
   ChainLayout c;
-  c.pa = plan_decode(M, N, K, r, kBF16, false);
-  c.pb = plan_decode(M, N2, N, r2, kBF16, false);
+  c.pa = plan_decode(M, N, K, r, kBF16, Pick::kFixed);
+  c.pb = plan_decode(M, N2, N, r2, kBF16, Pick::kFixed);
   c.off_a = kCounterBytes + kChainDoneBytes;  // plan offsets already skip kCounterBytes
   c.off_b = align256(c.off_a + (c.pa.total - kCounterBytes));
   c.total = c.off_b + (c.pb.total - kCounterBytes);
@@ -1192,7 +1204,7 @@ hipError_t launch_decode_chain(const LoraArgs& pa, const FusedArgs& fa, const Lo
 }
 
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, false);
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kFused);
   DecodeArgs a = make_args(p, pl);
   a.nw = reinterpret_cast<const uint16_t*>(f.nw); a.eps = f.eps;
   a.nw_off = (int)pl.flag_off + 16 + kNormLds;
