@@ -67,9 +67,10 @@ int wsl_decode_attention_fwd(const void* q, const void* k_cache, const void* v_c
  * workgroup normalises its own query heads; the chunk holding *pos also produces the step's
  * k and v. The chunks' partial softmax records are merged by the last one of each
  * (sequence, kv head) to finish. `workspace` (wsl_decode_attention_step_workspace_bytes
- * bytes, 256-byte aligned) starts with arrival counters: zero-fill it before its first use;
- * every completed call leaves them zero. Calls that may run concurrently must not share
- * a workspace. n_heads / n_kv_heads in {1, 2, 4}; head_dim in {64, 128}. */
+ * bytes, 256-byte aligned) starts with a fixed 64 KB region of arrival counters: zero-fill
+ * it before its first use; every completed call, of any shape, leaves them zero. Calls
+ * that may run concurrently must not share a workspace. n_heads / n_kv_heads in {1, 2, 4};
+ * head_dim in {64, 128}; batch * n_kv_heads <= 16384. */
 size_t wsl_decode_attention_step_workspace_bytes(int64_t batch, int64_t n_heads, int64_t n_kv_heads,
                                                   int64_t head_dim, int64_t cache_len);
 int wsl_decode_attention_step_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t n_heads,

@@ -174,8 +174,35 @@ def test_decode_attention_step_equals_unfused(gpu, b, nh, nkv, hd, L, pos):
         assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
         assert rel(out, ref) <= TOL
     ws = ops.workspace(gpu, torch.cuda.current_stream(gpu).cuda_stream, 0, kind="attention")
-    assert int(ws[:256].count_nonzero()) == 0, "arrival counters not restored to zero"
+    assert int(ws[:65536].count_nonzero()) == 0, "arrival counters not restored to zero"
 
+
+
+def test_decode_attention_step_workspace_shared_across_shapes(gpu):
+    """One attention workspace serves calls of different shapes in turn: a call with few
+    (sequence, kv head) pairs leaves records where a later call with more pairs might put
+    counters, so the counters live in a fixed region of their own."""
+    from weightshared_torchtitan_amd import ops
+    from weightshared_torchtitan_amd.qwen3_shared import _rope_cache
+    for (b, nh, nkv, hd, L, pos) in [(2, 4, 2, 64, 64, 0), (3, 8, 2, 128, 200, 130), (1, 4, 1, 64, 300, 299),
+                                     (16, 16, 8, 64, 256, 200), (2, 4, 2, 64, 64, 10)]:
+        _say(f"[attention step shared ws] b={b} nh={nh} nkv={nkv} hd={hd} L={L} pos={pos}")
+        g = torch.Generator(device="cuda").manual_seed(7 * L + pos + b)
+        qkv = torch.randn(b, (nh + 2 * nkv) * hd, device=gpu, generator=g).bfloat16()
+        qw = (1 + 0.1 * torch.randn(hd, device=gpu, generator=g)).bfloat16()
+        kw = (1 + 0.1 * torch.randn(hd, device=gpu, generator=g)).bfloat16()
+        rope = _rope_cache(hd, L, 1e6).to(gpu)
+        kc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+        vc = torch.randn(b, nkv, L, hd, device=gpu, generator=g).bfloat16()
+        kc2, vc2 = kc.clone(), vc.clone()
+        p = torch.full((), pos, dtype=torch.int64, device=gpu)
+        scale = hd ** -0.5
+        q = ops.qk_norm_rope_op(qkv, qw, kw, 1e-6, rope, p, kc2, vc2, nh, nkv)
+        ref = attn_ref(q, kc2, vc2, pos, scale)
+        out = ops.decode_attention_step_op(qkv, qw, kw, 1e-6, rope, p, kc, vc, nh, nkv, scale)
+        assert rel(out, ref) <= TOL
+    ws = ops.workspace(gpu, torch.cuda.current_stream(gpu).cuda_stream, 0, kind="attention")
+    assert int(ws[:65536].count_nonzero()) == 0, "arrival counters not restored to zero"
 
 def _interleave8(g, u):
     n = g.shape[0]

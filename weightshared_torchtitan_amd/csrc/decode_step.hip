@@ -169,6 +169,14 @@ constexpr int AT_G = AT_T / 16;
 constexpr int AT_CH = 64;              // cache positions per workgroup
 constexpr int AT_U = AT_CH / AT_G;     // positions per group, all in flight
 constexpr int AT_B = 8;                // record loads a thread keeps in flight in the merge
+// Arrival counters: a fixed 64 KB region at the start of the workspace, which nothing
+// else writes (the records follow it), so counters stay zero between calls of any shape.
+// A pair's counter is on its own 128-byte line up to 512 pairs, packed closer beyond.
+constexpr size_t AT_CREGION = 65536;
+constexpr int64_t AT_MAX_PAIRS = (int64_t)(AT_CREGION / 4);
+int at_cstride(int64_t pairs) {
+  return pairs <= 512 ? 32 : (int)(AT_MAX_PAIRS / pairs);
+}
 
 // EPL (4 or 8) consecutive bf16 of a row as one 8- or 16-byte load.
 template <int EPL> struct Vec;
@@ -408,7 +416,7 @@ __global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restric
                                                       float eps, const float* __restrict__ rope,
                                                       const int64_t* __restrict__ posp, uint16_t* __restrict__ kc,
                                                       uint16_t* __restrict__ vc, int cache_len, int nchunk, float scale,
-                                                      unsigned* __restrict__ cnt, float* __restrict__ part,
+                                                      unsigned* __restrict__ cnt, int cstride, float* __restrict__ part,
                                                       uint16_t* __restrict__ out) {
   constexpr int HD = 16 * EPL;
   constexpr int C = HD / 64;  // elements per lane when one wave holds one head
@@ -552,9 +560,10 @@ __global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restric
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the record is out before the arrival
     __syncthreads();
     if (tid == 0) {
-      const unsigned old = __hip_atomic_fetch_add(cnt + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unsigned* pc = cnt + pair * cstride;
+      const unsigned old = __hip_atomic_fetch_add(pc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const bool last = old == (unsigned)(nc - 1);
-      if (last) __hip_atomic_store(cnt + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) __hip_atomic_store(pc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = last ? 1 : 0;
     }
     __syncthreads();
@@ -746,8 +755,7 @@ size_t wsl_decode_attention_step_workspace_bytes(int64_t batch, int64_t n_heads,
                                                   int64_t head_dim, int64_t cache_len) {
   if (batch < 0 || n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || cache_len < 1) return 0;
   const int64_t nchunk = (cache_len + AT_CH - 1) / AT_CH;
-  const size_t counters = ((size_t)(batch * n_kv_heads) * 4 + 255) & ~(size_t)255;
-  return counters + (size_t)(batch * n_heads * nchunk * (head_dim + 2) * 4);
+  return AT_CREGION + (size_t)(batch * n_heads * nchunk * (head_dim + 2) * 4);
 }
 
 int wsl_decode_attention_step_fwd(const void* qkv, int64_t ldqkv, int64_t batch, int64_t n_heads,
@@ -764,6 +772,8 @@ int wsl_decode_attention_step_fwd(const void* qkv, int64_t ldqkv, int64_t batch,
   if (head_dim != 64 && head_dim != 128) return dfail(WSL_E_SHAPE, "decode_attention_step: head_dim must be 64 or 128");
   if (ldqkv < (n_heads + 2 * n_kv_heads) * head_dim) return dfail(WSL_E_SHAPE, "decode_attention_step: ldqkv too small");
   if (batch == 0) return WSL_OK;
+  if (batch * n_kv_heads > AT_MAX_PAIRS)
+    return dfail(WSL_E_SHAPE, "decode_attention_step: batch * n_kv_heads above 16384");
   if (!qkv || !q_norm_w || !k_norm_w || !rope || !pos || !k_cache || !v_cache || !out)
     return dfail(WSL_E_INVALID_ARG, "decode_attention_step: null pointer");
   const size_t need = wsl_decode_attention_step_workspace_bytes(batch, n_heads, n_kv_heads, head_dim, cache_len);
@@ -772,14 +782,15 @@ int wsl_decode_attention_step_fwd(const void* qkv, int64_t ldqkv, int64_t batch,
   const int pairs = (int)(batch * n_kv_heads);
   const int nchunk = (int)((cache_len + AT_CH - 1) / AT_CH);
   unsigned* cnt = reinterpret_cast<unsigned*>(workspace);
-  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + (((size_t)pairs * 4 + 255) & ~(size_t)255));
+  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + AT_CREGION);
+  const int cstride = at_cstride(pairs);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   dim3 grid((unsigned)(pairs * nchunk));
 #define WSL_AS(E, R)                                                                                           \
   attention_step<E, R><<<grid, dim3(AT_T), 0, st>>>((const uint16_t*)qkv, ldqkv, (int)n_heads, (int)n_kv_heads, \
                                                     (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, eps, rope, \
                                                     pos, (uint16_t*)k_cache, (uint16_t*)v_cache, (int)cache_len,     \
-                                                    nchunk, scale, cnt, part, (uint16_t*)out)
+                                                    nchunk, scale, cnt, cstride, part, (uint16_t*)out)
   if (head_dim == 64) {
     if (rep == 1) WSL_AS(4, 1); else if (rep == 2) WSL_AS(4, 2); else WSL_AS(4, 4);
   } else {
