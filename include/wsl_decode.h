@@ -88,8 +88,14 @@ int wsl_swiglu_fwd(const void* gate_up, int64_t ld, int64_t rows, int64_t ffn, v
 /* out[row] = index of the largest x[row, 0..n) (bf16): the greedy token of a row of logits
  * (scripts/generate/_generation.py:26-29 with top_k = 1 keeps only the argmax). Ties give
  * the first index and NaN counts as largest, as torch.argmax. Rows that are 16-byte aligned
- * with ldx % 8 == 0 are read 16 bytes at a time. */
-int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* stream);
+ * with ldx % 8 == 0 are read 16 bytes at a time.
+ * With a workspace (wsl_argmax_rows_workspace_bytes bytes, 256-byte aligned, zero-filled
+ * before its first use; every completed call leaves it zero; n < 2^32) each row is split
+ * over up to 64 workgroups merged by a 64-bit atomic max; with workspace == NULL one
+ * workgroup reads each row. */
+size_t wsl_argmax_rows_workspace_bytes(int64_t rows, int64_t n);
+int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* The fused LoRA linear of wsl_lora_linear_fwd (bf16 w, decode-shaped 1 <= M <= 64) with
  * the decode step's elementwise work folded into the same launch. `fuse` combines:

@@ -213,6 +213,13 @@ def test_decode_step_validation_codes():
         == N.WSL_E_WORKSPACE
     # swiglu: ld below 2 * ffn
     assert lib.wsl_swiglu_fwd(P2, 100, 4, 64, P2, 64, None) == N.WSL_E_SHAPE
+    # argmax: a 256-byte key/counter block per row; short or misaligned workspace; bad sizes
+    assert lib.wsl_argmax_rows_workspace_bytes(8, 151936) == 8 * 256
+    assert lib.wsl_argmax_rows_workspace_bytes(0, 10) == 0
+    assert lib.wsl_argmax_rows_fwd(P2, 151936, 8, 151936, P2, P2, 8 * 256 - 1, None) == N.WSL_E_WORKSPACE
+    assert lib.wsl_argmax_rows_fwd(P2, 151936, 8, 151936, P2, P2 + 16, 8 * 256, None) == N.WSL_E_WORKSPACE
+    assert lib.wsl_argmax_rows_fwd(P2, 100, 8, 151936, P2, P2, 8 * 256, None) == N.WSL_E_SHAPE
+    assert lib.wsl_argmax_rows_fwd(P2, 16, 0, 16, P2, None, 0, None) == N.WSL_OK
 
 
 @needs_lib

@@ -131,7 +131,7 @@ def test_grouped_projection_equals_separate_calls(gpu):
     assert rel(grp, sep) <= 1e-2
 
 
-@pytest.mark.parametrize("rows,n", [(8, 151936), (3, 1000), (2, 13)])
+@pytest.mark.parametrize("rows,n", [(8, 151936), (3, 1000), (2, 13), (16, 151936), (3, 4097), (5, 40000)])
 def test_argmax_rows_matches_torch(gpu, rows, n):
     from weightshared_torchtitan_amd import ops
     _say(f"[argmax] rows={rows} n={n}")
@@ -145,6 +145,31 @@ def test_argmax_rows_matches_torch(gpu, rows, n):
         x[2, n // 2] = float("nan")
     got = ops.argmax_rows_op(x)
     assert torch.equal(got, torch.argmax(x.float(), dim=-1))
+    again = ops.argmax_rows_op(x)  # the split path's keys and counters were reset
+    assert torch.equal(again, got)
+
+
+def test_argmax_rows_edge_cases_and_paths(gpu):
+    """Signed zeros tie (the first wins), several NaNs (the first wins), an all -inf row, and
+    the one-workgroup-per-row path (no workspace) against the split path."""
+    import ctypes
+    from weightshared_torchtitan_amd import _native, ops
+    n = 151936
+    x = torch.full((4, n), -1.0, device=gpu, dtype=torch.bfloat16)
+    x[0, 70000] = -0.0
+    x[0, 90000] = 0.0
+    x[1, 100] = float("nan")
+    x[1, 50] = float("nan")
+    x[1, 7] = float("inf")
+    x[2, :] = float("-inf")
+    x[3, 151935] = 3.0
+    want = torch.argmax(x.float(), dim=-1)
+    assert torch.equal(ops.argmax_rows_op(x), want)
+    out = torch.empty(4, dtype=torch.int64, device=gpu)
+    rc = _native.lib().wsl_argmax_rows_fwd(x.data_ptr(), x.stride(0), 4, n, out.data_ptr(), None, 0,
+                                           torch.cuda.current_stream(gpu).cuda_stream)
+    assert rc == 0
+    assert torch.equal(out, want)
 
 
 @pytest.mark.parametrize("b,nh,nkv,hd,L,pos", [(8, 16, 8, 128, 1024, 767), (8, 16, 8, 128, 1024, 64),

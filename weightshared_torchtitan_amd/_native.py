@@ -46,6 +46,7 @@ EXPORTED = (
     "wsl_decode_attention_step_fwd",
     "wsl_swiglu_fwd",
     "wsl_argmax_rows_fwd",
+    "wsl_argmax_rows_workspace_bytes",
     "wsl_lora_linear_fused_supported",
     "wsl_lora_linear_fused_fwd",
     "wsl_lora_linear_chain_supported",
@@ -135,7 +136,9 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_i64, _c_i64, ctypes.c_int32, _c_i64,                      # N2, r2, fuse2, M
         _c_vp, ctypes.c_size_t, _c_vp]                               # workspace, bytes, stream
     lib.wsl_argmax_rows_fwd.restype = ctypes.c_int
-    lib.wsl_argmax_rows_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]
+    lib.wsl_argmax_rows_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, ctypes.c_size_t, _c_vp]
+    lib.wsl_argmax_rows_workspace_bytes.restype = ctypes.c_size_t
+    lib.wsl_argmax_rows_workspace_bytes.argtypes = [_c_i64, _c_i64]
     lib.wsl_factorized_embedding_fwd.restype = ctypes.c_int
     lib.wsl_factorized_embedding_fwd.argtypes = [
         _c_vp, _c_i64,                   # ids, n_ids

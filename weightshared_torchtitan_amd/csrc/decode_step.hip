@@ -400,6 +400,80 @@ __global__ void __launch_bounds__(AM_T) argmax_kernel(const uint16_t* __restrict
   }
 }
 
+// Split argmax: a row's chunks are reduced by separate workgroups and merged with a 64-bit
+// atomic max on a key that orders (value, then the lower index) as am_better does: the
+// value's order-preserving bits (NaN above everything, -0 folded into +0) over the
+// complemented index. The last chunk of a row (arrival counter) writes the index and
+// returns the key and the counter to zero. Workspace: per row, the key and the counter on
+// lines of their own (AMS_ROW bytes).
+constexpr int AMS_T = 256;
+constexpr int64_t AMS_CHUNK = 4096;  // elements per workgroup (at least)
+constexpr int AMS_MAXS = 64;         // chunks per row (at most)
+constexpr size_t AMS_ROW = 256;
+
+__device__ __forceinline__ uint64_t am_key(float v, int64_t i) {
+  uint32_t o;
+  if (v != v) {
+    o = 0xffffffffu;
+  } else {
+    const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+    o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+}
+
+__global__ void __launch_bounds__(AMS_T) argmax_split_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t n,
+                                                            int vec, int nsplit, int64_t chunk,
+                                                            char* __restrict__ ws, int64_t* __restrict__ out) {
+  __shared__ float sv[AMS_T / 64];
+  __shared__ int64_t si[AMS_T / 64];
+  const int row = blockIdx.x / nsplit, sp = blockIdx.x % nsplit;
+  const int tid = threadIdx.x;
+  const uint16_t* xr = x + (int64_t)row * ldx;
+  const int64_t k0 = sp * chunk, k1 = min(n, k0 + chunk);
+  float bv = -INFINITY;
+  int64_t bi = INT64_MAX;
+  int64_t k = k0;
+  if (vec) {  // chunk is a multiple of 8 and the rows are 16-byte aligned
+    const int64_t c1 = k0 / 8 + (k1 - k0) / 8;
+    for (int64_t c = k0 / 8 + tid; c < c1; c += AMS_T) {
+      const u32x4_t v = ld_global_16(xr + c * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = bf((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+        if (am_better(f, c * 8 + e, bv, bi)) { bv = f; bi = c * 8 + e; }
+      }
+    }
+    k = c1 * 8;
+  }
+  for (int64_t kk = k + tid; kk < k1; kk += AMS_T) {  // tail (or the whole chunk without vec)
+    const float f = bf(xr[kk]);
+    if (am_better(f, kk, bv, bi)) { bv = f; bi = kk; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int64_t oi = __shfl_xor(bi, o, 64);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < AMS_T / 64; ++w)
+      if (am_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    uint64_t* key = reinterpret_cast<uint64_t*>(ws + (size_t)row * AMS_ROW);
+    unsigned* cnt = reinterpret_cast<unsigned*>(ws + (size_t)row * AMS_ROW + 128);
+    if (bi != INT64_MAX) __hip_atomic_fetch_max(key, am_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (unsigned)(nsplit - 1)) {  // every chunk's key is in
+      const uint64_t kv = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      out[row] = (int64_t)(0xffffffffu - (uint32_t)kv);
+      __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ------------------------------------------------------------ fused step (norm + RoPE + attention)
@@ -800,15 +874,34 @@ int wsl_decode_attention_step_fwd(const void* qkv, int64_t ldqkv, int64_t batch,
   return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "decode_attention_step: launch failed");
 }
 
-int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* stream) {
+size_t wsl_argmax_rows_workspace_bytes(int64_t rows, int64_t n) {
+  if (rows < 0 || n < 1) return 0;
+  return (size_t)rows * AMS_ROW;
+}
+
+int wsl_argmax_rows_fwd(const void* x, int64_t ldx, int64_t rows, int64_t n, int64_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
   g_derr[0] = 0;
   if (rows < 0 || n < 1 || ldx < n) return dfail(WSL_E_SHAPE, "argmax: bad sizes");
   if (rows == 0) return WSL_OK;
   if (!x || !out) return dfail(WSL_E_INVALID_ARG, "argmax: null pointer");
   if (((uintptr_t)x & 1) || ((uintptr_t)out & 7)) return dfail(WSL_E_ALIGN, "argmax: misaligned pointer");
   const int vec = (a16(x) && ldx % 8 == 0) ? 1 : 0;
-  argmax_kernel<<<dim3((unsigned)rows), dim3(AM_T), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      (const uint16_t*)x, ldx, n, vec, out);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (workspace == nullptr) {  // one workgroup per row
+    argmax_kernel<<<dim3((unsigned)rows), dim3(AM_T), 0, st>>>((const uint16_t*)x, ldx, n, vec, out);
+  } else {
+    if (workspace_bytes < wsl_argmax_rows_workspace_bytes(rows, n) || ((uintptr_t)workspace & 255))
+      return dfail(WSL_E_WORKSPACE, "argmax: workspace too small or not 256-byte aligned");
+    if (n > (int64_t)0xffffffffLL) return dfail(WSL_E_SHAPE, "argmax: n above 2^32 - 1 with a workspace");
+    int64_t chunk = (n + AMS_MAXS - 1) / AMS_MAXS;
+    if (chunk < AMS_CHUNK) chunk = AMS_CHUNK;
+    chunk = (chunk + 7) / 8 * 8;
+    const int nsplit = (int)((n + chunk - 1) / chunk);
+    if (rows * nsplit > (int64_t)INT32_MAX) return dfail(WSL_E_SHAPE, "argmax: too many rows");
+    argmax_split_kernel<<<dim3((unsigned)(rows * nsplit)), dim3(AMS_T), 0, st>>>(
+        (const uint16_t*)x, ldx, n, vec, nsplit, chunk, (char*)workspace, out);
+  }
   return hipGetLastError() == hipSuccess ? WSL_OK : dfail(WSL_E_LAUNCH, "argmax: launch failed");
 }
 

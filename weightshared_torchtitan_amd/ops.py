@@ -340,9 +340,14 @@ def argmax_rows_op(x: torch.Tensor) -> torch.Tensor:
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     out = torch.empty(x2.shape[0], dtype=torch.int64, device=dev)
+    lib = _native.lib()
+    stream = _stream(dev)
+    ws = workspace(dev, stream, lib.wsl_argmax_rows_workspace_bytes(x2.shape[0], x2.shape[1]), kind="argmax")
     with torch.cuda.device(dev):
-        rc = _native.lib().wsl_argmax_rows_fwd(x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1],
-                                               out.data_ptr(), _stream(dev))
+        rc = lib.wsl_argmax_rows_fwd(x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1], out.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), stream)
+    if rc != 0:
+        _workspaces.pop((dev.index, stream, "argmax"), None)  # a failed launch may leave keys set
     _native.check(rc, "wsl_argmax_rows_fwd", decode=True)
     return out.view(x.shape[:-1])
 
