@@ -918,11 +918,13 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
   const int steps = pl.kcy > 0 ? pl.kcy / wave_k_of(wdt) : 8;
   pl.kw = 8;
   while (pl.kw > 1 && pl.kw > steps) pl.kw >>= 1;
-  // Short K over very many rows (the tied output head): every wave takes two 16-row
-  // blocks of its own, so a workgroup streams 256 rows and the grid stays a few per CU.
+  // Short K over very many rows (the tied output head): every wave takes 16-row blocks of
+  // its own (three at one token block: 384 rows per workgroup, 396 workgroups for 151936
+  // rows, within one wave of two per CU; two blocks gave 594, 1.16 waves), so the grid
+  // stays a few per CU.
   if (pl.kw <= 2 && pl.mb <= 2 && N >= 32768) {
     pl.kw = 1;
-    pl.nr = 2;
+    pl.nr = pl.mb == 1 ? 3 : 2;
   }
   for (;;) {
     pl.rows = (NWV / pl.kw) * 16 * pl.nr;
@@ -1003,6 +1005,9 @@ hipError_t dispatch_fused(const DecodeArgs& a, int mb, int nr, int grid, size_t 
 // other pair is an error, never a kernel sized for a different plan.
 template <int WDT, int KW>
 hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t smem, hipStream_t st) {
+  if constexpr (KW == 1) {  // the tied head at one token block
+    if (nr == 3 && mb == 1) return launch_one<WDT, 3, 1, KW>(a, grid, smem, st);
+  }
   if (nr == 1) {
     if (mb == 1) return launch_one<WDT, 1, 1, KW>(a, grid, smem, st);
     if (mb == 2) return launch_one<WDT, 1, 2, KW>(a, grid, smem, st);
