@@ -202,7 +202,7 @@ def graph_of(fn):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the warm-up stream: its workspaces exist already
         fn()
     torch.cuda.synchronize()
     return g

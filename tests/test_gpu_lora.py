@@ -323,7 +323,7 @@ def test_decode_in_graph_replays_match_eager(gpu, M, N, K, r):
         wsl.lora_linear(x, W, A, B, 2.0)
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         out = wsl.lora_linear(x, W, A, B, 2.0)
     for _ in range(3):
         out.zero_()
@@ -331,6 +331,31 @@ def test_decode_in_graph_replays_match_eager(gpu, M, N, K, r):
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
         wsl.lora_linear(x, W, A, B, 2.0)  # eager work on the default stream between replays
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_workspace_growth_refused_during_capture(gpu):
+    """A workspace that would have to grow inside a graph capture raises instead of being
+    allocated (and zero-filled) by the graph; after an eager call on the capture stream the
+    same capture succeeds."""
+    import weightshared_torchtitan_amd as wsl
+    x, W, A, B = (t.to(gpu) for t in _inputs(4, 512, 1024, 16, seed=41))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="during graph capture"):
+        with torch.cuda.graph(g, stream=s):
+            wsl.lora_linear(x, W, A, B, 2.0)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        eager = wsl.lora_linear(x, W, A, B, 2.0)
+    torch.cuda.current_stream().wait_stream(s)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=s):
+        out = wsl.lora_linear(x, W, A, B, 2.0)
+    g2.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
 
 
 @pytest.mark.parametrize("M,N,K,r", [(1, 2048, 2048, 64), (40, 1000, 6144, 24)])

@@ -65,6 +65,12 @@ def workspace(dev: torch.device, stream: int, nbytes: int, kind: str = "lora") -
     key = (dev.index, stream, kind)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            # allocated inside a capture, the buffer would come from the graph's private
+            # pool and its zero-fill would replay with the graph
+            raise RuntimeError(
+                f"libwsl: the {kind!r} workspace would have to grow to {nbytes} bytes during graph "
+                "capture; run the op once eagerly with the same shapes before capturing")
         buf = torch.zeros(max(2 * nbytes, _WS_MIN_BYTES), dtype=torch.uint8, device=dev)
         _workspaces[key] = buf
     return buf

@@ -472,10 +472,11 @@ class SharedQwen3(nn.Module):
             stream = torch.cuda.Stream()
             stream.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(stream):
-                _ = self.decode_step(tok_buf, pos, cache)
+                _ = ops.argmax_rows_op(self.decode_step(tok_buf, pos, cache))
             torch.cuda.current_stream().wait_stream(stream)
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
+            # captured on the warm-up stream: the ops' per-stream workspaces already exist
+            with torch.cuda.graph(graph, stream=stream):
                 g_logits = self.decode_step(tok_buf, pos, cache)
                 g_next = ops.argmax_rows_op(g_logits).view(b, 1)
             # the warm-up wrote position s; the first replay rewrites it identically
