@@ -565,6 +565,23 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   __syncthreads();
   constexpr int CPR = C::BN / 8;  // 16-byte chunks per tile row
   const bool a16 = ((reinterpret_cast<uintptr_t>(y) & 15u) == 0) && ((ldy & 7) == 0);
+  if (a16 && m0 + C::BM <= M && n0 + C::BN <= N) {
+    // whole tile in range: every LDS read first, then the stores, with no per-chunk tests
+    constexpr int IT = C::BM * CPR / NT;
+    static_assert(C::BM * CPR % NT == 0, "store split");
+    u32x4_t v[IT];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int q = i * NT + tid;
+      v[i] = *reinterpret_cast<const u32x4_t*>(ot + (q / CPR) * OS + (q % CPR) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int q = i * NT + tid;
+      *reinterpret_cast<u32x4_t*>(y + (int64_t)(m0 + q / CPR) * ldy + n0 + (q % CPR) * 8) = v[i];
+    }
+    return;
+  }
 #pragma unroll 4
   for (int q = tid; q < C::BM * CPR; q += NT) {
     const int row = q / CPR, c = q % CPR;

@@ -15,11 +15,15 @@ typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
 enum : int { kBF16 = 0, kFP8 = 1 };
 
 // Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept NaN with its quiet bit set. Lowers to
+// gfx950's v_cvt_pk_bf16_f32, which matches the integer rounding u + 0x7fff + ((u >> 16) & 1)
+// (and (u >> 16) | 0x40 for NaN) on all 2^32 inputs; the branch of the integer form for NaN
+// costs exec-mask juggling per element in the epilogues.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
@@ -31,7 +35,7 @@ __device__ __forceinline__ float bf16_round(float f) { return bf16_bits_to_f32(f
 
 // Two fp32 -> packed bf16x2 (low half = a).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 // Four OCP e4m3fn bytes (packed in one dword, byte 0 first) -> 4 bf16 in two dwords.
