@@ -202,3 +202,43 @@ def tied_logits(h, P, E):
     <tied_logits(h)[t, v]> = <h[t], factorized_embedding([v])> (tests/test_oracle.py).
     """
     return (np.asarray(h, np.float64) @ np.asarray(P, np.float64)) @ np.asarray(E, np.float64).T
+
+
+# ----------------------------------------------------------------------------------------
+# Backward of the LoRA linear
+# ----------------------------------------------------------------------------------------
+def lora_linear_backward(x, W, A, B, scale, gy, w_scale=None):
+    """Gradients of y = x . (W * w_scale[:, None])^T + scale * (x . A^T) . B^T w.r.t. x, W,
+    A and B, given dL/dy = gy. Returns (dx, dW, dA, dB); dW is None when W is None and
+    dA, dB are None without a LoRA term. For an fp8 W, dW is the gradient w.r.t. the
+    dequantised weight W * w_scale[:, None].
+
+    The reference has no backward of its own: torch autograd differentiates
+    LoRAModule.forward (torchtitan/models/llama3/model/model.py:189-192, two bias-free
+    nn.Linear and a multiply) and the base nn.Linear (:257-273) composed by broadcast_add
+    with g = 1 (:392-398); the trainer runs it at torchtitan/train.py:456. With
+    T = x . A^T and U = gy . B:
+        dx = gy . W + scale * U . A,   dW = gy^T . x,
+        dA = scale * U^T . x,          dB = scale * gy^T . T.
+    Pinned by: torch.autograd of the same expression in float64, and central finite
+    differences of a scalar loss on tiny shapes (tests/test_oracle.py).
+    """
+    x = np.asarray(x, np.float64)
+    gy = np.asarray(gy, np.float64)
+    dx = np.zeros_like(x)
+    dW = dA = dB = None
+    if W is not None:
+        Wd = np.asarray(W, np.float64)
+        if w_scale is not None:
+            Wd = Wd * np.asarray(w_scale, np.float64)[:, None]
+        dx = dx + gy @ Wd
+        dW = gy.T @ x
+    if A is not None and A.shape[0] > 0:
+        A = np.asarray(A, np.float64)
+        B = np.asarray(B, np.float64)
+        U = gy @ B
+        T = x @ A.T
+        dx = dx + float(scale) * (U @ A)
+        dA = float(scale) * (U.T @ x)
+        dB = float(scale) * (gy.T @ T)
+    return dx, dW, dA, dB

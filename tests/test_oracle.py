@@ -192,3 +192,57 @@ def test_oracle_matches_reference_style_torch_cpu_path(case):
     t = lambda a: torch.from_numpy(np.asarray(a, np.float32))
     y_ref = reference_lora_linear(t(x), t(W), t(A), t(B), 2.0).numpy()
     assert O.max_rel_err(y_ref, O.lora_linear(x, W, A, B, 2.0)) < 1e-5
+
+
+# ---------------------------------------------------------------- backward
+def test_backward_matches_torch_autograd_float64(case):
+    x, W, A, B = case
+    gy = np.random.default_rng(7).standard_normal((x.shape[0], W.shape[0]))
+    ws = np.random.default_rng(8).uniform(0.5, 2.0, W.shape[0])
+    for w_scale in (None, ws):
+        tx, tW, tA, tB = (torch.tensor(v, dtype=torch.float64, requires_grad=True) for v in (x, W, A, B))
+        Wd = tW * torch.tensor(w_scale)[:, None] if w_scale is not None else tW
+        y = tx @ Wd.T + 2.0 * (tx @ tA.T) @ tB.T
+        y.backward(torch.tensor(gy))
+        dx, dW, dA, dB = O.lora_linear_backward(x, W, A, B, 2.0, gy, w_scale=w_scale)
+        np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(dA, tA.grad.numpy(), rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(dB, tB.grad.numpy(), rtol=1e-12, atol=1e-12)
+        gW = tW.grad.numpy() if w_scale is None else tW.grad.numpy() / w_scale[:, None]
+        np.testing.assert_allclose(dW, gW, rtol=1e-10, atol=1e-12)
+
+
+def test_backward_matches_central_differences():
+    # brute force on a tiny case: L = <gy, y>, every input element perturbed in turn
+    rng = np.random.default_rng(11)
+    M, N, K, r = 3, 4, 5, 2
+    x, W, A, B = (rng.standard_normal(s) for s in ((M, K), (N, K), (r, K), (N, r)))
+    gy = rng.standard_normal((M, N))
+    s, h = 1.7, 1e-6
+
+    def loss(x_, W_, A_, B_):
+        return float((O.lora_linear(x_, W_, A_, B_, s) * gy).sum())
+
+    grads = O.lora_linear_backward(x, W, A, B, s, gy)
+    args = [x, W, A, B]
+    for which, g in enumerate(grads):
+        num = np.zeros_like(args[which])
+        for idx in np.ndindex(*args[which].shape):
+            hi = [a.copy() for a in args]
+            lo = [a.copy() for a in args]
+            hi[which][idx] += h
+            lo[which][idx] -= h
+            num[idx] = (loss(*hi) - loss(*lo)) / (2 * h)
+        np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-8)
+
+
+def test_backward_dx_is_forward_with_transposed_weights(case):
+    # dx = gy . W + s (gy . B) . A is the forward of the same op with W^T, B^T, A^T: the
+    # identity the GPU backward uses to run dx on the forward kernel
+    x, W, A, B = case
+    gy = O.bf16_round(np.random.default_rng(9).standard_normal((x.shape[0], W.shape[0])))
+    dx = O.lora_linear_backward(x, W, A, B, 2.0, gy)[0]
+    np.testing.assert_allclose(O.lora_linear(gy, W.T, B.T, A.T, 2.0), dx, rtol=1e-12, atol=1e-13)
+    # a dropped LoRA term or a flipped sign on it is caught
+    assert O.max_rel_err(O.lora_linear(gy, W.T), dx) > 1e-3
+    assert O.max_rel_err(O.lora_linear(gy, W.T, B.T, A.T, -2.0), dx) > 1e-3

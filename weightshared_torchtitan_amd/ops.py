@@ -151,6 +151,62 @@ def _lora_linear_fake(x, w, w_scale, a, b, scale):
     return x.new_empty((*x.shape[:-1], N), dtype=torch.bfloat16)
 
 
+def _lora_linear_setup(ctx, inputs, output):
+    x, w, w_scale, a, b, scale = inputs
+    ctx.save_for_backward(x, w, w_scale, a, b)
+    ctx.scale = scale
+
+
+def _lora_linear_backward(ctx, gy):
+    """Backward of ``wsl::lora_linear``. With T = x . a^T and U = gy . b:
+
+        dx = gy . W + scale * U . a     one launch of the fused kernel, as the forward of
+                                        the same op on (gy, W^T, b^T, a^T): the fused
+                                        kernel's K is the forward's N
+        dW = gy^T . x                   plain GEMMs (reductions over the tokens M)
+        da = scale * U^T . x
+        db = scale * gy^T . T
+
+    The reference has no backward of its own: torch autograd differentiates
+    LoRAModule.forward (torchtitan/models/llama3/model/model.py:189-192) and the base
+    nn.Linear (:257-273) composed by broadcast_add with g = 1 (:392-398); the trainer runs
+    it at torchtitan/train.py:456. An fp8 ``w`` gets no gradient (it is not a trainable
+    dtype); its dx uses the dequantised weight. ``w_scale`` gets no gradient.
+    """
+    x, w, w_scale, a, b = ctx.saved_tensors
+    s = float(ctx.scale)
+    need_x, need_w, _, need_a, need_b, _ = ctx.needs_input_grad
+    K = x.shape[-1]
+    gy2 = _row_major(gy.reshape(-1, gy.shape[-1]).to(torch.bfloat16), "grad_y")
+    x2 = x.reshape(-1, K)
+    has_lora = a is not None and a.shape[0] > 0
+    dx = dw = da = db = None
+    if need_x:
+        wt = None
+        if w is not None:
+            wd = w if w.dtype != _FP8 else (w.float() * w_scale[:, None]).to(torch.bfloat16)
+            wt = wd.t().contiguous()
+        if has_lora:
+            dx = lora_linear_op(gy2, wt, None, b.t().contiguous(), a.t().contiguous(), s)
+        elif wt is not None:
+            dx = lora_linear_op(gy2, wt, None, None, None, s)
+        else:
+            dx = torch.zeros_like(x2)
+        dx = dx.reshape(x.shape)
+    if need_w and w is not None and w.dtype == torch.bfloat16:
+        dw = torch.mm(gy2.t(), x2)
+    if has_lora and need_a:
+        u = torch.mm(gy2, b)
+        da = torch.mm(u.t(), x2).mul_(s)
+    if has_lora and need_b:
+        t = torch.mm(x2, a.t().contiguous())
+        db = torch.mm(gy2.t(), t).mul_(s)
+    return dx, dw, None, da, db, None
+
+
+lora_linear_op.register_autograd(_lora_linear_backward, setup_context=_lora_linear_setup)
+
+
 @torch.library.custom_op("wsl::factorized_embedding", mutates_args=(), device_types="cuda")
 def factorized_embedding_op(ids: torch.Tensor, emb: torch.Tensor, proj: torch.Tensor) -> torch.Tensor:
     """out[..., :] = emb[ids[...], :] . proj^T   (emb [V,k], proj [H,k], bf16)."""
