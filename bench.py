@@ -279,6 +279,66 @@ def bench_c5(dev, steps, warmup):
     return out
 
 
+def lora_backward_flops(M, N, K, r):
+    """dx = gy.W + s(gy.B).A, dW = gy^T.x, dA = s(gy.B)^T.x, dB = s gy^T.(x.A^T): U = gy.B
+    and T = x.A^T counted once each."""
+    return 2.0 * M * (2 * N * K + 2 * r * (N + K) + r * N + r * K)
+
+
+def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
+    """Backward of the config-2 projections (Qwen3-0.6B, M = 8192, r = 32) over `layers`
+    layers that share one base W set, every tensor requiring grad (the weight-shared
+    trainer's case; each layer has its own inputs, the three projections of a layer that
+    read one activation share it, as q/k/v and gate/up do). Timed eagerly with HIP events around loss.backward() only; the
+    forward runs untimed before each step. Two paths on the same inputs: the fused op
+    (dx on the fused kernel, weight gradients on hipBLASLt) and torch autograd of the
+    reference's unfused arithmetic x.W^T + s (x.A^T).B^T."""
+    from weightshared_torchtitan_amd import lora_linear
+    g = torch.Generator(device=dev).manual_seed(12)
+    Ws = [(torch.randn(N, K, device=dev, generator=g) * 0.02).bfloat16().requires_grad_(True)
+          for _, N, K in QWEN3_0P6B]
+    xs = [{K: torch.randn(M, K, device=dev, generator=g).bfloat16().requires_grad_(True)
+           for K in sorted({K for _, _, K in QWEN3_0P6B})} for _ in range(layers)]
+    lor = [[((torch.randn(r, K, device=dev, generator=g) * 0.02).bfloat16().requires_grad_(True),
+             (torch.randn(N, r, device=dev, generator=g) * 0.02).bfloat16().requires_grad_(True))
+            for _, N, K in QWEN3_0P6B] for _ in range(layers)]
+    gys = [torch.randn(M, N, device=dev, generator=g).bfloat16() for _, N, _ in QWEN3_0P6B]
+
+    def fused():
+        return [lora_linear(xs[l][K], Ws[i], *lor[l][i], 2.0)
+                for l in range(layers) for i, (_, _, K) in enumerate(QWEN3_0P6B)]
+
+    def unfused():
+        return [xs[l][K] @ Ws[i].t() + 2.0 * (xs[l][K] @ lor[l][i][0].t()) @ lor[l][i][1].t()
+                for l in range(layers) for i, (_, _, K) in enumerate(QWEN3_0P6B)]
+
+    def timed(fwd):
+        total = 0.0
+        for it in range(warmup + steps):
+            for t in [v for d in xs for v in d.values()] + Ws + [p for pr in lor for ab in pr for p in ab]:
+                t.grad = None
+            ys = fwd()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            torch.autograd.backward(ys, [gys[i % 7] for i in range(len(ys))])
+            e1.record()
+            e1.synchronize()
+            if it >= warmup:
+                total += e0.elapsed_time(e1)
+        return total / steps
+
+    fl = layers * sum(lora_backward_flops(M, N, K, r) for _, N, K in QWEN3_0P6B)
+    out = {"layers": layers, "M": M, "r": r}
+    for name, fwd in (("wsl_fused", fused), ("torch_unfused_autograd", unfused)):
+        ms = timed(fwd)
+        out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
+                     "frac_mfma": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+    del Ws, xs, lor, gys
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_embedding(dev, steps, warmup):
     """The factorized embedding at config 4's prefill: 8 x 512 token ids, E [151936, 256],
     P [1024, 256] -> [4096, 1024] bf16 (wsl_factorized_embedding_fwd). Algorithmic bytes:
@@ -377,7 +437,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5", "emb", "vendor", "shape"), default=None)
+    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5", "emb", "vendor", "backward", "shape"), default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -401,6 +461,7 @@ def main():
               "c5": lambda: bench_c5(dev, args.steps, args.warmup),
               "emb": lambda: bench_embedding(dev, args.steps, args.warmup),
               "vendor": lambda: bench_vendor(dev, args.steps, args.warmup),
+              "backward": lambda: bench_backward(dev, min(args.steps, 10), min(args.warmup, 3)),
               "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
@@ -439,6 +500,7 @@ def main():
         extra["c5_qwen3_8b_fp8_base"] = bench_c5(dev, args.steps, args.warmup)
         extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)
         extra["factorized_embedding_c4_prefill"] = bench_embedding(dev, args.steps, args.warmup)
+        extra["c2_backward"] = bench_backward(dev, min(args.steps, 10), min(args.warmup, 3))
         res["extra"] = extra
     if not args.no_cpu and args.only is None:
         res["cpu_baseline"] = cpu_baseline()

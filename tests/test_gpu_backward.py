@@ -118,3 +118,29 @@ def test_lora_linear_module_trains(gpu):
         for p in params:  # a descent step of 2 % of each parameter's norm (bf16 resolves it)
             p -= 0.02 * p.float().norm() * p.grad / p.grad.float().norm()
     assert loss_fn().item() < loss.item()
+
+
+def test_shared_weight_transpose_follows_updates(gpu):
+    # dx of layers sharing one W reuses W^T; an in-place update of W must be seen by the
+    # next backward
+    import weightshared_torchtitan_amd as wsl
+    M, N, K, r = 256, 512, 384, 16
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    A = (torch.randn(r, K, generator=g) * 0.02).bfloat16()
+    B = (torch.randn(N, r, generator=g) * 0.02).bfloat16()
+    gy = torch.randn(M, N, generator=g).bfloat16()
+    tW = W.to(gpu).requires_grad_(True)
+    for step in range(3):
+        _say(f"[shared W] step {step}")
+        tx = x.to(gpu).requires_grad_(True)
+        ys = [wsl.lora_linear(tx, tW, A.to(gpu), B.to(gpu), 2.0) for _ in range(2)]  # two layers
+        torch.autograd.backward(ys, [gy.to(gpu)] * 2)
+        torch.cuda.synchronize()
+        Wn = _np(tW)
+        dx = 2 * O.lora_linear_backward(_np(x), Wn, _np(A), _np(B), 2.0, _np(gy))[0]
+        assert O.max_rel_err(_np(tx.grad), dx) <= BF16_TOL
+        with torch.no_grad():
+            tW.mul_(-1.5).add_(0.01)  # an optimizer-like in-place update
+        tW.grad = None

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 from typing import Optional
 
+import collections
 import ctypes
 
 import torch
@@ -151,6 +152,26 @@ def _lora_linear_fake(x, w, w_scale, a, b, scale):
     return x.new_empty((*x.shape[:-1], N), dtype=torch.bfloat16)
 
 
+# W^T of a bf16 base weight, reused by the backward of every layer that shares W (the
+# weight-shared model runs one W in up to 7 layers). An entry holds W itself, so its memory
+# cannot be reused while cached; a changed W (an optimizer step bumps _version) misses.
+_WT_CACHE: "collections.OrderedDict" = collections.OrderedDict()
+_WT_CACHE_MAX = 16
+
+
+def _transposed(w: torch.Tensor) -> torch.Tensor:
+    key = (w.data_ptr(), tuple(w.shape), tuple(w.stride()), w.dtype, w.device)
+    hit = _WT_CACHE.get(key)
+    if hit is not None and hit[1] == w._version:
+        _WT_CACHE.move_to_end(key)
+        return hit[2]
+    wt = w.t().contiguous()
+    _WT_CACHE[key] = (w.detach(), w._version, wt)
+    while len(_WT_CACHE) > _WT_CACHE_MAX:
+        _WT_CACHE.popitem(last=False)
+    return wt
+
+
 def _lora_linear_setup(ctx, inputs, output):
     x, w, w_scale, a, b, scale = inputs
     ctx.save_for_backward(x, w, w_scale, a, b)
@@ -183,9 +204,10 @@ def _lora_linear_backward(ctx, gy):
     dx = dw = da = db = None
     if need_x:
         wt = None
-        if w is not None:
-            wd = w if w.dtype != _FP8 else (w.float() * w_scale[:, None]).to(torch.bfloat16)
-            wt = wd.t().contiguous()
+        if w is not None and w.dtype == _FP8:
+            wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous()
+        elif w is not None:
+            wt = _transposed(w)
         if has_lora:
             dx = lora_linear_op(gy2, wt, None, b.t().contiguous(), a.t().contiguous(), s)
         elif wt is not None:
@@ -195,12 +217,12 @@ def _lora_linear_backward(ctx, gy):
         dx = dx.reshape(x.shape)
     if need_w and w is not None and w.dtype == torch.bfloat16:
         dw = torch.mm(gy2.t(), x2)
-    if has_lora and need_a:
-        u = torch.mm(gy2, b)
-        da = torch.mm(u.t(), x2).mul_(s)
-    if has_lora and need_b:
-        t = torch.mm(x2, a.t().contiguous())
-        db = torch.mm(gy2.t(), t).mul_(s)
+    if has_lora and (need_a or need_b):
+        zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)  # beta = 0: s rides on alpha
+        if need_a:
+            da = torch.addmm(zero, torch.mm(gy2, b).t(), x2, beta=0, alpha=s)
+        if need_b:
+            db = torch.addmm(zero, gy2.t(), torch.mm(x2, a.t().contiguous()), beta=0, alpha=s)
     return dx, dw, None, da, db, None
 
 
