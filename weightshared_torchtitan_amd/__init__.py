@@ -4,6 +4,7 @@ Public surface:
   ops.lora_linear / torch.ops.wsl.lora_linear           fused y = x.W^T + s (x.A^T).B^T
   ops.factorized_embedding / torch.ops.wsl.factorized_embedding
   lora.LoRAModule, lora.LoRALinear, lora.broadcast_add, lora.quantize_fp8_per_channel
+  converter.WslLoRAConverter                           the "wsl_lora" model converter
 """
 from . import ops  # noqa: F401  (registers torch.ops.wsl.*)
 from .lora import LoRALinear, LoRAModule, broadcast_add, quantize_fp8_per_channel  # noqa: F401
