@@ -11,8 +11,9 @@
 //   128 x 256, 64 x 64 per wave — used when 256-row tiles would leave CUs idle;
 //   128 x 128, 64 x 32 per wave (two workgroups fit on a CU) — for shapes that even
 //   128 x 256 tiles leave half-idle, and for the split-K rank pre-pass.
-// (A 4-wave 256 x 256 tile with 128 x 128 per wave measured slower on these shapes:
-// one wave per SIMD leaves LDS latency exposed, and rank blocks overflow the AGPRs.)
+// (4-wave tiles, one wave per SIMD, measured slower: 128 x 256 with 128 x 64 per wave ran
+// 3-8 % behind the 8-wave 64 x 64 tiling, since one wave per SIMD leaves LDS latency
+// exposed; 128 x 128 per wave does not fit its rank blocks beside 256 accumulators.)
 // K is walked in 64-wide tiles through two LDS buffers filled by
 // global_load_lds_dwordx4 (global memory -> LDS without passing through VGPRs; lane i
 // of a wave instruction lands at the wave-uniform LDS base + 16*i, so the XOR swizzle of
@@ -644,8 +645,8 @@ Tile choose_tile(const LoraArgs& p) {
 
 template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER = false>
 hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
-  // Two in-kernel rank blocks do not fit beside the 128 x 128 accumulators of the
-  // 4-wave tile; those ranks use the 8-wave configuration.
+  // Ranks 33-64 (two rank blocks) use 128 x 256, whose 64 x 64 wave tile leaves registers
+  // for the second block's T accumulators beside the base accumulators.
   if constexpr (RB == 2) {
     return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
   } else {
