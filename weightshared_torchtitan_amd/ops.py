@@ -172,6 +172,11 @@ def _transposed(w: torch.Tensor) -> torch.Tensor:
     return wt
 
 
+def clear_transpose_cache() -> None:
+    """Drops the cached W^T copies (and the references they hold to their weights)."""
+    _WT_CACHE.clear()
+
+
 def _lora_linear_setup(ctx, inputs, output):
     x, w, w_scale, a, b, scale = inputs
     ctx.save_for_backward(x, w, w_scale, a, b)
