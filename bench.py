@@ -3,8 +3,10 @@
 Headline (the JSON line's `value`): BASELINE config 2 — Qwen3-0.6B-shaped prefill
 projections in bf16, M = 8192 tokens, 7 projections x 28 layers per step, one shared
 base weight set, per-layer rank-32 LoRA (scale 2). A step is one pass over the 196
-projections, captured once as a HIP graph and replayed. value = algorithmic TFLOP/s,
-FLOPs = sum over launches of 2*M*(N*K + r*(K+N)).
+projections, captured once as a HIP graph and replayed, one launch per projection. The
+same inputs with the projections that read one activation (q|k|v, gate|up) as grouped
+launches (4 per layer) are reported beside it. value = algorithmic TFLOP/s, FLOPs = sum
+over projections of 2*M*(N*K + r*(K+N)).
 
 Also reported (same JSON line, key "extra"): config 3 decode GB/s (cold and warm
 weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
@@ -108,6 +110,32 @@ class ProjectionStack:
             c = l % self.copies
             for p, (_, N, K) in enumerate(self.shapes):
                 lora_linear(self.x[K], self.W[c][p], self.A[l][p], self.B[l][p], self.scale, w_scale=self.S[c][p])
+
+    # Projections that read the same activation, run as one grouped launch each
+    # (wsl_lora_linear_grouped_fwd): q|k|v and gate|up. Indices into `shapes`.
+    GROUPS = ((0, 1, 2), (3,), (4, 5), (6,))
+
+    def stack_groups(self):
+        """Stacked operands of the grouped run, built once from the same tensors: per
+        weight copy [W_q; W_k; W_v] and [W_1; W_3], per layer the A and B factors likewise."""
+        cat = lambda ts: torch.cat(ts, 0).contiguous() if len(ts) > 1 else ts[0]
+        self.gW = [[cat([self.W[c][p] for p in grp]) for grp in self.GROUPS] for c in range(self.copies)]
+        self.gS = [[cat([self.S[c][p] for p in grp]) if self.fp8 else None for grp in self.GROUPS]
+                   for c in range(self.copies)]
+        self.gA = [[cat([self.A[l][p] for p in grp]) if self.r else None for grp in self.GROUPS]
+                   for l in range(self.layers)]
+        self.gB = [[cat([self.B[l][p] for p in grp]) if self.r else None for grp in self.GROUPS]
+                   for l in range(self.layers)]
+        self.gN = [[self.shapes[p][1] for p in grp] for grp in self.GROUPS]
+        self.gK = [self.shapes[grp[0]][2] for grp in self.GROUPS]
+
+    def run_grouped(self):
+        from weightshared_torchtitan_amd import ops
+        for l in range(self.layers):
+            c = l % self.copies
+            for q in range(len(self.GROUPS)):
+                ops.lora_linear_grouped_op(self.x[self.gK[q]], self.gW[c][q], self.gS[c][q], self.gA[l][q],
+                                           self.gB[l][q], self.scale, self.gN[q])
 
     def flops(self):
         return self.layers * sum(lora_flops(self.M, N, K, self.r) for _, N, K in self.shapes)
@@ -226,21 +254,41 @@ def time_replays(graph, steps, warmup):
 
 
 # ------------------------------------------------------------------------------ configs
-def bench_c2(dev, steps, warmup):
+def bench_c2(dev, steps, warmup, grouped=True):
+    """Config 2, two ways on the same inputs: one launch per projection (7 per layer, 196
+    per step; the headline) and, with `grouped`, q|k|v and gate|up as grouped launches (4 per
+    layer, 112 per step). Back to back, the launch after a grouped one runs slower (it
+    follows a 64-96 MB output write), so the two come out alike here."""
     st = ProjectionStack(QWEN3_0P6B, M=8192, r=32, layers=28, dev=dev, seed=2)
     g = graph_of(st.run)
     ms = time_replays(g, steps, warmup)
     del g
-    return st.flops(), ms
+    ms_grouped = None
+    if grouped:
+        st.stack_groups()
+        g = graph_of(st.run_grouped)
+        ms_grouped = time_replays(g, steps, warmup)
+        del g
+    del st
+    torch.cuda.empty_cache()
+    return lora_flops_c2(), ms, ms_grouped
+
+
+def lora_flops_c2():
+    return 28 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_0P6B)
 
 
 def bench_c2_1p7b(dev, steps, warmup):
     st = ProjectionStack(QWEN3_1P7B, M=8192, r=32, layers=4, dev=dev, seed=21)
     g = graph_of(st.run)
     ms = time_replays(g, steps, warmup)
+    del g
+    st.stack_groups()
+    g = graph_of(st.run_grouped)
+    ms_grouped = time_replays(g, steps, warmup)
     del g, st
     torch.cuda.empty_cache()
-    return ms
+    return ms, ms_grouped
 
 
 def bench_c3(dev, steps, warmup):
@@ -290,9 +338,10 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
     layers that share one base W set, every tensor requiring grad (the weight-shared
     trainer's case; each layer has its own inputs, the three projections of a layer that
     read one activation share it, as q/k/v and gate/up do). Timed eagerly with HIP events around loss.backward() only; the
-    forward runs untimed before each step. Two paths on the same inputs: the fused op
-    (dx on the fused kernel, weight gradients on hipBLASLt) and torch autograd of the
-    reference's unfused arithmetic x.W^T + s (x.A^T).B^T."""
+    forward runs untimed before each step. Three paths on the same inputs: the fused op
+    (dx on the fused kernel, weight gradients on hipBLASLt), the grouped op for q|k|v and
+    gate|up (stacked parameters), and torch autograd of the reference's unfused arithmetic
+    x.W^T + s (x.A^T).B^T."""
     from weightshared_torchtitan_amd import lora_linear
     g = torch.Generator(device=dev).manual_seed(12)
     Ws = [(torch.randn(N, K, device=dev, generator=g) * 0.02).bfloat16().requires_grad_(True)
@@ -312,16 +361,35 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
         return [xs[l][K] @ Ws[i].t() + 2.0 * (xs[l][K] @ lor[l][i][0].t()) @ lor[l][i][1].t()
                 for l in range(layers) for i, (_, _, K) in enumerate(QWEN3_0P6B)]
 
-    def timed(fwd):
+    # grouped: q|k|v and gate|up as one op each, on stacked leaves holding the same values
+    # (a trainer that keeps the stacked tensors as its parameters)
+    groups = ProjectionStack.GROUPS
+    leaf = lambda ts: torch.cat([t.detach() for t in ts], 0).requires_grad_(True)
+    gWs = [leaf([Ws[i] for i in grp]) for grp in groups]
+    glor = [[(leaf([lor[l][i][0] for i in grp]), leaf([lor[l][i][1] for i in grp])) for grp in groups]
+            for l in range(layers)]
+    gN = [[QWEN3_0P6B[i][1] for i in grp] for grp in groups]
+    gK = [QWEN3_0P6B[grp[0]][2] for grp in groups]
+    ggys = [torch.cat([gys[i] for i in grp], 1) for grp in groups]
+
+    def grouped():
+        from weightshared_torchtitan_amd import ops
+        return [ops.lora_linear_grouped_op(xs[l][gK[q]], gWs[q], None, glor[l][q][0], glor[l][q][1], 2.0, gN[q])
+                for l in range(layers) for q in range(len(groups))]
+
+    params = ([v for d in xs for v in d.values()] + Ws + [p for pr in lor for ab in pr for p in ab] + gWs
+              + [p for pr in glor for ab in pr for p in ab])
+
+    def timed(fwd, grads):
         total = 0.0
         for it in range(warmup + steps):
-            for t in [v for d in xs for v in d.values()] + Ws + [p for pr in lor for ab in pr for p in ab]:
+            for t in params:
                 t.grad = None
             ys = fwd()
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            torch.autograd.backward(ys, [gys[i % 7] for i in range(len(ys))])
+            torch.autograd.backward(ys, [grads[i % len(grads)] for i in range(len(ys))])
             e1.record()
             e1.synchronize()
             if it >= warmup:
@@ -330,11 +398,12 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
 
     fl = layers * sum(lora_backward_flops(M, N, K, r) for _, N, K in QWEN3_0P6B)
     out = {"layers": layers, "M": M, "r": r}
-    for name, fwd in (("wsl_fused", fused), ("torch_unfused_autograd", unfused)):
-        ms = timed(fwd)
+    for name, fwd, grads in (("wsl_fused", fused, gys), ("wsl_grouped_qkv_gateup", grouped, ggys),
+                             ("torch_unfused_autograd", unfused, gys)):
+        ms = timed(fwd, grads)
         out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
                      "frac_mfma": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
-    del Ws, xs, lor, gys
+    del Ws, xs, lor, gys, gWs, glor, ggys, params
     torch.cuda.empty_cache()
     return out
 
@@ -465,7 +534,7 @@ def main():
               "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
-    flops, ms = bench_c2(dev, args.steps, args.warmup)
+    flops, ms, ms_grouped = bench_c2(dev, args.steps, args.warmup, grouped=args.only is None)
     tflops = flops / ms / 1e9
     launches = 7 * 28
     res = {
@@ -490,17 +559,23 @@ def main():
                      "avg_launch_us": round(ms * 1e3 / launches, 3)},
     }
     extra = {}
+    if ms_grouped is not None:
+        extra["c2_grouped_qkv_gateup"] = {"TFLOP/s": round(flops / ms_grouped / 1e9, 1),
+                                          "frac_mfma": round(flops / ms_grouped / 1e9 / BF16_PEAK_TFLOPS, 4),
+                                          "ms_per_step": round(ms_grouped, 4), "launches": 4 * 28}
     if not args.no_extra and args.only is None:
-        ms17 = bench_c2_1p7b(dev, args.steps, args.warmup)
+        ms17, ms17s = bench_c2_1p7b(dev, args.steps, args.warmup)
         f17 = 4 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_1P7B)
         extra["c2_qwen3_1.7b_prefill"] = {"TFLOP/s": round(f17 / ms17 / 1e9, 1),
                                           "frac_mfma": round(f17 / ms17 / 1e9 / BF16_PEAK_TFLOPS, 4),
-                                          "ms_per_4_layers": round(ms17, 4)}
+                                          "ms_per_4_layers": round(ms17, 4),
+                                          "grouped_qkv_gateup_TFLOP/s": round(f17 / ms17s / 1e9, 1)}
         extra["c3_qwen3_1.7b_decode"] = bench_c3(dev, args.steps, args.warmup)
         extra["c5_qwen3_8b_fp8_base"] = bench_c5(dev, args.steps, args.warmup)
         extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)
         extra["factorized_embedding_c4_prefill"] = bench_embedding(dev, args.steps, args.warmup)
         extra["c2_backward"] = bench_backward(dev, min(args.steps, 10), min(args.warmup, 3))
+    if extra:
         res["extra"] = extra
     if not args.no_cpu and args.only is None:
         res["cpu_baseline"] = cpu_baseline()

@@ -90,6 +90,40 @@ int wsl_lora_linear_fwd(const void* x, int64_t ldx,
                         void* stream);
 
 /*
+ * Grouped fused LoRA linear: up to WSL_MAX_GROUPS projections that read the same x, in
+ * one call. Group g covers output columns [n_g, n_g + group_n[g]) with
+ * n_g = group_n[0] + ... + group_n[g-1], and
+ *
+ *   y[:, n_g : n_g + group_n[g]] = x . W_g^T (* diag(w_scale_g)) + scale * (x . A_g^T) . B_g^T
+ *
+ * which is exactly wsl_lora_linear_fwd on each group's column range. Operands are the
+ * groups' tensors stacked: w [N,K] (W_g rows stacked, N = sum of group_n), w_scale [N],
+ * b [N,r] (B_g rows stacked), y [N columns], and a [n_groups*r, K] (A_g is rows
+ * g*r .. g*r+r-1). Every group has rank r. group_n is a host array.
+ *
+ * Replaces the projections of one reference block that read the same activation: q, k
+ * and v (torchtitan/models/llama3/model/model.py:376-398, each base + broadcast_add of
+ * its LoRA delta; Qwen3 wq/wk/wv, torchtitan/experiments/qwen3/model/model.py:184) and
+ * gate/up (qwen3/model/model.py:250-251). On the prefill path with group boundaries that
+ * whole output tiles respect (multiples of 128; of 256 for ranks 33-64) the groups run as
+ * one launch, each output tile taking its group's rank block; otherwise the groups run
+ * as consecutive launches on `stream`. Results are those of the per-group calls.
+ */
+#define WSL_MAX_GROUPS 4
+int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int32_t n_groups,
+                                            const int64_t* group_n, int32_t w_dtype, size_t* bytes);
+int wsl_lora_linear_grouped_fwd(const void* x, int64_t ldx,
+                                const void* w, int64_t ldw, int32_t w_dtype, const float* w_scale,
+                                const void* a, int64_t lda,
+                                const void* b, int64_t ldb,
+                                float scale,
+                                void* y, int64_t ldy,
+                                int64_t M, int64_t K, int64_t r,
+                                int32_t n_groups, const int64_t* group_n,
+                                void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/*
  * Factorized embedding:  out[t, :] = E[ids[t], :] . P^T      (k -> hidden)
  *
  * Replaces the reference's token embedding nn.Embedding(vocab, dim)

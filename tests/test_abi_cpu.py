@@ -312,3 +312,52 @@ def test_chain_validation_codes():
     sz = ctypes.c_size_t()
     assert lib.wsl_lora_linear_chain_workspace_bytes(8, 1024, 2048, 32, 6144, 64, ctypes.byref(sz)) == N.WSL_OK
     assert sz.value >= _header_defines()["WSL_COUNTER_BYTES"]
+
+
+def _grouped(group_n=(64, 64), **kw):
+    a = dict(x=P, ldx=64, w=P, ldw=64, w_dtype=0, w_scale=None, a=P, lda=64, b=P, ldb=8,
+             scale=2.0, y=P, ldy=128, M=4, K=64, r=8, ws=P, ws_bytes=1 << 24, stream=None)
+    a.update(kw)
+    gn = N.group_array(group_n) if group_n is not None else None
+    ng = kw.get("n_groups", len(group_n) if group_n is not None else 2)
+    return N.lib().wsl_lora_linear_grouped_fwd(a["x"], a["ldx"], a["w"], a["ldw"], a["w_dtype"], a["w_scale"],
+                                               a["a"], a["lda"], a["b"], a["ldb"], a["scale"], a["y"], a["ldy"],
+                                               a["M"], a["K"], a["r"], ng, gn, a["ws"], a["ws_bytes"],
+                                               a["stream"])
+
+
+@needs_lib
+@pytest.mark.parametrize("group_n,kw,code", [
+    ((64, 64), dict(n_groups=0), N.WSL_E_SHAPE),
+    ((64,) * 5, {}, N.WSL_E_SHAPE),                   # more than WSL_MAX_GROUPS
+    ((64, 0), {}, N.WSL_E_SHAPE),                     # empty group
+    (None, dict(n_groups=2), N.WSL_E_INVALID_ARG),    # group_n NULL
+    ((64, 64), dict(ldy=127), N.WSL_E_SHAPE),         # ldy < sum of widths
+    ((64, 64), dict(x=None), N.WSL_E_INVALID_ARG),
+    ((64, 64), dict(a=None), N.WSL_E_INVALID_ARG),
+    ((64, 64), dict(w_dtype=1), N.WSL_E_INVALID_ARG),  # fp8 without w_scale
+    ((64, 64), dict(lda=63), N.WSL_E_SHAPE),
+    ((64, 64), dict(x=P + 1), N.WSL_E_ALIGN),
+    ((64, 64), dict(ws=None), N.WSL_E_WORKSPACE),
+    ((64, 64), dict(ws_bytes=16), N.WSL_E_WORKSPACE),
+])
+def test_grouped_validation_codes(group_n, kw, code):
+    assert _grouped(group_n, **kw) == code
+    assert N.last_error() != ""
+
+
+@needs_lib
+def test_grouped_empty_batch_is_a_no_op():
+    assert _grouped((64, 64), M=0, x=None, y=None, ws=None, ws_bytes=0) == N.WSL_OK
+
+
+@needs_lib
+def test_grouped_workspace_covers_pre_pass_and_per_group_calls():
+    # rank 128 over 3 groups: one pre-pass over 384 ranks (T [M, 384] plus split partials)
+    M, K, r, gn = 4096, 4096, 128, (2048, 1024, 1024)
+    need = N.grouped_workspace_bytes(M, K, r, gn, N.WSL_DTYPE_BF16)
+    assert need >= _header_defines()["WSL_COUNTER_BYTES"] + M * 3 * r * 2
+    for n in gn:  # the per-group fallback reuses the same workspace
+        assert need >= N.workspace_bytes(M, n, K, r, N.WSL_DTYPE_BF16)
+    # decode-shaped M: per-group calls
+    assert N.grouped_workspace_bytes(8, 2048, 64, gn, 0) >= N.workspace_bytes(8, 2048, 2048, 64, 0)

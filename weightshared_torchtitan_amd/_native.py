@@ -35,6 +35,8 @@ WSL_MAX_RANK = 256
 EXPORTED = (
     "wsl_lora_linear_workspace_bytes",
     "wsl_lora_linear_fwd",
+    "wsl_lora_linear_grouped_workspace_bytes",
+    "wsl_lora_linear_grouped_fwd",
     "wsl_factorized_embedding_fwd",
     "wsl_last_error",
     "wsl_version",
@@ -83,6 +85,23 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_float,                  # scale
         _c_vp, _c_i64,                   # y, ldy
         _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
+        _c_vp, ctypes.c_size_t,          # workspace, bytes
+        _c_vp,                           # stream
+    ]
+    lib.wsl_lora_linear_grouped_workspace_bytes.restype = ctypes.c_int
+    lib.wsl_lora_linear_grouped_workspace_bytes.argtypes = [
+        _c_i64, _c_i64, _c_i64, ctypes.c_int32, ctypes.POINTER(_c_i64), ctypes.c_int32,
+        ctypes.POINTER(ctypes.c_size_t)]
+    lib.wsl_lora_linear_grouped_fwd.restype = ctypes.c_int
+    lib.wsl_lora_linear_grouped_fwd.argtypes = [
+        _c_vp, _c_i64,                   # x, ldx
+        _c_vp, _c_i64, ctypes.c_int32, _c_vp,  # w, ldw, w_dtype, w_scale
+        _c_vp, _c_i64,                   # a, lda
+        _c_vp, _c_i64,                   # b, ldb
+        ctypes.c_float,                  # scale
+        _c_vp, _c_i64,                   # y, ldy
+        _c_i64, _c_i64, _c_i64,          # M, K, r
+        ctypes.c_int32, ctypes.POINTER(_c_i64),  # n_groups, group_n
         _c_vp, ctypes.c_size_t,          # workspace, bytes
         _c_vp,                           # stream
     ]
@@ -191,4 +210,20 @@ def workspace_bytes(M: int, N: int, K: int, r: int, w_dtype: int) -> int:
     out = ctypes.c_size_t(0)
     check(lib().wsl_lora_linear_workspace_bytes(M, N, K, r, w_dtype, ctypes.byref(out)),
           "wsl_lora_linear_workspace_bytes")
+    return int(out.value)
+
+
+WSL_MAX_GROUPS = 4
+
+
+def group_array(group_n) -> "ctypes.Array":
+    """The host array of group widths a grouped call takes."""
+    return (_c_i64 * len(group_n))(*[int(n) for n in group_n])
+
+
+def grouped_workspace_bytes(M: int, K: int, r: int, group_n, w_dtype: int) -> int:
+    out = ctypes.c_size_t(0)
+    check(lib().wsl_lora_linear_grouped_workspace_bytes(M, K, r, len(group_n), group_array(group_n), w_dtype,
+                                                        ctypes.byref(out)),
+          "wsl_lora_linear_grouped_workspace_bytes")
     return int(out.value)

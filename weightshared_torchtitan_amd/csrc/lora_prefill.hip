@@ -43,6 +43,7 @@
 //
 // Reference arithmetic being fused: torchtitan/models/llama3/model/model.py:189-192
 // (LoRAModule.forward), :392-398 (base projection + broadcast_add with g = 1).
+#include <climits>
 #include <type_traits>
 
 #include "wsl_common.h"
@@ -131,7 +132,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const uint16_t* __restrict__ tg, int64_t ldt,
                const uint16_t* __restrict__ bm, int64_t ldb, float s, float yscale,
                uint16_t* __restrict__ y, int64_t ldy,
-               int M, int N, int K, int r, int tiles_m, int tiles_n) {
+               int M, int N, int K, int r, int tiles_m, int tiles_n,
+               int ge0, int ge1, int ge2, int64_t a_gstride, int t_gstride) {
   constexpr bool W8 = HAS_W && WDT == kFP8;
   constexpr bool WDIRECT = HAS_W && WDT == kBF16;
   constexpr bool LORA = RB > 0 || EXT_T;
@@ -170,6 +172,15 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   const int tn = (t % group_size) / gm;
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
+  // Grouped launch: output columns [ge_{g-1}, ge_g) are projection g, whose LoRA down
+  // factor is rank block g of a (rows g*r..g*r+r-1) and whose T is column block g of the
+  // pre-pass output. Group ends are multiples of BN, so a tile lies in one group; B rows
+  // and W rows are indexed by the output column as in a single projection.
+  {
+    const int grp = (n0 >= ge0) + (n0 >= ge1) + (n0 >= ge2);
+    a += grp * a_gstride;
+    tg += grp * t_gstride;
+  }
 
   // ---- sources of this wave's direct fills: uniform tile base + 32-bit lane offset ----
   const char* xbase = reinterpret_cast<const char*>(GATHER ? x : x + (int64_t)m0 * ldx);
@@ -608,6 +619,17 @@ using CfgTall = Cfg<128, 256, 4, 8>;  // 8 waves, 64 x 64 per wave
 using CfgMid = Cfg<256, 192, 2, 8>;   // 8 waves, 96(n) x 64(m) per wave
 using CfgSmall = Cfg<128, 128, 2, 8>;  // 8 waves, 64(n) x 32(m) per wave; also the rank pre-pass (N = r)
 
+// End column of group g of a grouped launch (INT_MAX past the last group: no tile
+// starts there).
+int group_end(const LoraArgs& p, int g) { return g + 1 < p.groups ? (int)p.gend[g] : INT_MAX; }
+
+// Whether tiles BN wide keep every group of a grouped launch within whole tiles.
+bool groups_fit(const LoraArgs& p, int bn) {
+  for (int g = 0; g + 1 < p.groups; ++g)
+    if (p.gend[g] % bn != 0) return false;
+  return true;
+}
+
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false>
 hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1) {
   const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
@@ -616,7 +638,9 @@ hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int sp
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
-      reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n);
+      reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n,
+      group_end(p, 0), group_end(p, 1), group_end(p, 2), p.groups > 1 ? p.r * p.lda : 0,
+      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0);
   return hipGetLastError();
 }
 
@@ -632,12 +656,15 @@ double wave_efficiency(int64_t tiles) {
 // M = N = K = 4096; it wins where the larger tiles leave CUs idle (M = 4096, N = 1024:
 // 256 tiles against 128 of 128 x 256, 642 against 552 TFLOP/s).
 enum class Tile { kBig, kMid, kTall, kSmall };
+// A grouped launch only considers configurations whose tile width divides every group
+// boundary (one of 256 and 128 always does: prefill_groups_supported checks it).
 Tile choose_tile(const LoraArgs& p) {
   const int64_t tm = (p.M + 255) / 256;
-  const double big = wave_efficiency(tm * ((p.N + 255) / 256));
-  const double mid = wave_efficiency(tm * ((p.N + 191) / 192)) * 0.95;
-  const double tall = wave_efficiency(((p.M + 127) / 128) * ((p.N + 255) / 256)) * 0.85;
-  const double small = wave_efficiency(((p.M + 127) / 128) * ((p.N + 127) / 128)) * 0.75;
+  const bool f256 = groups_fit(p, 256), f192 = groups_fit(p, 192), f128 = groups_fit(p, 128);
+  const double big = f256 ? wave_efficiency(tm * ((p.N + 255) / 256)) : -1.0;
+  const double mid = f192 ? wave_efficiency(tm * ((p.N + 191) / 192)) * 0.95 : -1.0;
+  const double tall = f256 ? wave_efficiency(((p.M + 127) / 128) * ((p.N + 255) / 256)) * 0.85 : -1.0;
+  const double small = f128 ? wave_efficiency(((p.M + 127) / 128) * ((p.N + 127) / 128)) * 0.75 : -1.0;
   if (small > big && small > mid && small > tall) return Tile::kSmall;
   if (mid > big && mid > tall) return Tile::kMid;
   return tall > big ? Tile::kTall : Tile::kBig;
@@ -648,7 +675,7 @@ hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
   // Ranks 33-64 (two rank blocks) use 128 x 256, whose 64 x 64 wave tile leaves registers
   // for the second block's T accumulators beside the base accumulators.
   if constexpr (RB == 2) {
-    return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);  // groups fit 256 (checked)
   } else {
     switch (choose_tile(p)) {
       case Tile::kMid: return launch_cfg<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
@@ -703,6 +730,15 @@ rank_reduce_kernel(const float* __restrict__ part, int splits, int64_t slice, fl
 
 }  // namespace
 
+// A grouped launch needs the prefill path and group ends that whole tiles of one of the
+// configurations its rank takes respect (ranks 33-64 run only on 256-wide tiles).
+bool prefill_groups_supported(const LoraArgs& p) {
+  if (p.groups < 1 || p.groups > kMaxGroups) return false;
+  if (p.groups == 1) return true;
+  if (p.r > 32 && p.r <= RIN) return groups_fit(p, 256);
+  return groups_fit(p, 256) || groups_fit(p, 192) || groups_fit(p, 128);
+}
+
 bool prefill_supported(const LoraArgs& p) {
   if (p.K % BK != 0) return false;
   if (p.M > (int64_t)1 << 30 || p.N > (int64_t)1 << 30 || p.K > (int64_t)1 << 30) return false;
@@ -745,21 +781,23 @@ hipError_t launch_prefill(const LoraArgs& p) {
     // Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by this same kernel run
     // as a plain GEMM with A in the place of W (N = r) and s applied before rounding.
     // With few row tiles (N = r is one or two tiles wide) K is split over grid rows into
-    // fp32 partials that a second kernel sums in split order, scales and rounds.
-    ldt = p.r;
+    // fp32 partials that a second kernel sums in split order, scales and rounds. A grouped
+    // launch runs one pre-pass over all groups' A blocks (N = groups * r).
+    const int64_t rt = p.r * p.groups;
+    ldt = rt;
     uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
     LoraArgs q = p;
     q.w = p.a; q.ldw = p.lda; q.w_dtype = kBF16; q.w_scale = nullptr;
-    q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0;
-    q.N = p.r; q.y = t; q.ldy = ldt; q.yscale = p.scale;
-    const int splits = rank_splits(p.M, p.K, p.r);
+    q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0; q.groups = 1;
+    q.N = rt; q.y = t; q.ldy = ldt; q.yscale = p.scale;
+    const int splits = rank_splits(p.M, p.K, rt);
     hipError_t e;
     if (splits > 1) {
-      float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws) + (((size_t)(p.M * p.r * 2) + 255) & ~(size_t)255));
+      float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws) + (((size_t)(p.M * rt * 2) + 255) & ~(size_t)255));
       q.y = part; q.K = p.K / splits;
       e = launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
       if (e != hipSuccess) return e;
-      const int64_t slice = p.M * p.r;
+      const int64_t slice = p.M * rt;
       rank_reduce_kernel<<<dim3((unsigned)((slice / 8 + 255) / 256)), dim3(256), 0, p.stream>>>(part, splits, slice, p.scale, t);
       e = hipGetLastError();
     } else {

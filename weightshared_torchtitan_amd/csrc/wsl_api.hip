@@ -99,6 +99,95 @@ int validate_sizes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t w_dtype) 
   return WSL_OK;
 }
 
+
+// Argument checks shared by the single and grouped entry points (sizes, pointers,
+// leading dimensions, element alignment). Touches no device.
+int validate_call(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+                  const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
+                  const void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t r) {
+  int rc = validate_sizes(M, N, K, r, w_dtype);
+  if (rc != WSL_OK) return rc;
+  if (M > 0 && x == nullptr) return fail(WSL_E_INVALID_ARG, "x must not be NULL");
+  if (M > 0 && y == nullptr) return fail(WSL_E_INVALID_ARG, "y must not be NULL");
+  if (w == nullptr && r == 0) return fail(WSL_E_INVALID_ARG, "w is NULL and r == 0: nothing to compute");
+  if (r > 0 && (a == nullptr || b == nullptr)) return fail(WSL_E_INVALID_ARG, "r > 0 needs a and b");
+  if (w != nullptr && w_dtype == WSL_DTYPE_FP8_E4M3 && w_scale == nullptr)
+    return fail(WSL_E_INVALID_ARG, "fp8 w needs w_scale");
+  if (w_dtype == WSL_DTYPE_BF16 && w_scale != nullptr)
+    return fail(WSL_E_INVALID_ARG, "w_scale is only valid with an fp8 w");
+  if (ldx < K) return fail(WSL_E_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
+  if (w != nullptr && ldw < K) return fail(WSL_E_SHAPE, "ldw (%lld) < K (%lld)", (long long)ldw, (long long)K);
+  if (r > 0 && lda < K) return fail(WSL_E_SHAPE, "lda (%lld) < K (%lld)", (long long)lda, (long long)K);
+  if (r > 0 && ldb < r) return fail(WSL_E_SHAPE, "ldb (%lld) < r (%lld)", (long long)ldb, (long long)r);
+  if (ldy < N) return fail(WSL_E_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
+  if (((uintptr_t)x & 1) || ((uintptr_t)y & 1) || ((uintptr_t)a & 1) || ((uintptr_t)b & 1) ||
+      ((uintptr_t)w_scale & 3) || (w_dtype == WSL_DTYPE_BF16 && ((uintptr_t)w & 1)))
+    return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
+  return WSL_OK;
+}
+
+// Group widths of a grouped call: 1..WSL_MAX_GROUPS groups, each at least one column;
+// *N receives their sum.
+int validate_groups(int32_t n_groups, const int64_t* group_n, int64_t* N) {
+  if (n_groups < 1 || n_groups > WSL_MAX_GROUPS)
+    return fail(WSL_E_SHAPE, "n_groups must be in [1, %d] (got %d)", WSL_MAX_GROUPS, (int)n_groups);
+  if (group_n == nullptr) return fail(WSL_E_INVALID_ARG, "group_n must not be NULL");
+  int64_t n = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    if (group_n[g] < 1) return fail(WSL_E_SHAPE, "group %d has width %lld (must be >= 1)", g, (long long)group_n[g]);
+    if (group_n[g] > ((int64_t)1 << 31)) return fail(WSL_E_SHAPE, "group widths must be below 2^31");
+    n += group_n[g];
+  }
+  *N = n;
+  return WSL_OK;
+}
+
+wsl::LoraArgs make_args(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+                        const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
+                        float scale, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t r,
+                        void* stream) {
+  wsl::LoraArgs p;
+  p.x = x; p.ldx = ldx;
+  p.w = w; p.ldw = ldw; p.w_dtype = w_dtype; p.w_scale = w_scale;
+  p.a = a; p.lda = lda; p.b = b; p.ldb = ldb;
+  p.scale = scale;
+  p.y = y; p.ldy = ldy;
+  p.M = M; p.N = N; p.K = K; p.r = r;
+  p.ws = nullptr; p.ws_bytes = 0;
+  p.stream = reinterpret_cast<hipStream_t>(stream);
+  p.gather = nullptr; p.gather_rows = 0;
+  return p;
+}
+
+// Path choice, workspace and device checks, and the launch of one validated call (a
+// grouped call with p.groups > 1 only reaches here on the prefill path).
+int run_call(wsl::LoraArgs p, void* workspace, size_t workspace_bytes) {
+  const Path path = choose_path(p);
+  if (path == Path::kNone) return WSL_OK;
+  size_t need = workspace_for(p);
+  if (p.groups > 1) need = prefill_ws(p.M, p.N, p.K, p.r * p.groups, p.w_dtype);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((uintptr_t)workspace & 255)
+    return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
+  const int rc = check_device();
+  if (rc != WSL_OK) return rc;
+  p.ws = workspace;
+  p.ws_bytes = workspace_bytes;
+  if (path != Path::kDecode) {
+    p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes;
+    p.ws_bytes = workspace_bytes - wsl::kCounterBytes;
+  }
+  hipError_t e;
+  switch (path) {
+    case Path::kDecode: e = wsl::launch_decode(p); break;
+    case Path::kPrefill: e = wsl::launch_prefill(p); break;
+    default: e = wsl::launch_generic(p); break;
+  }
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -123,57 +212,67 @@ int wsl_lora_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, 
                         int64_t K, int64_t r, void* workspace, size_t workspace_bytes,
                         void* stream) {
   clear_err();
-  int rc = validate_sizes(M, N, K, r, w_dtype);
+  const int rc = validate_call(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, y, ldy, M, N, K, r);
   if (rc != WSL_OK) return rc;
-  if (M > 0 && x == nullptr) return fail(WSL_E_INVALID_ARG, "x must not be NULL");
-  if (M > 0 && y == nullptr) return fail(WSL_E_INVALID_ARG, "y must not be NULL");
-  if (w == nullptr && r == 0) return fail(WSL_E_INVALID_ARG, "w is NULL and r == 0: nothing to compute");
-  if (r > 0 && (a == nullptr || b == nullptr)) return fail(WSL_E_INVALID_ARG, "r > 0 needs a and b");
-  if (w != nullptr && w_dtype == WSL_DTYPE_FP8_E4M3 && w_scale == nullptr)
-    return fail(WSL_E_INVALID_ARG, "fp8 w needs w_scale");
-  if (w_dtype == WSL_DTYPE_BF16 && w_scale != nullptr)
-    return fail(WSL_E_INVALID_ARG, "w_scale is only valid with an fp8 w");
-  if (ldx < K) return fail(WSL_E_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
-  if (w != nullptr && ldw < K) return fail(WSL_E_SHAPE, "ldw (%lld) < K (%lld)", (long long)ldw, (long long)K);
-  if (r > 0 && lda < K) return fail(WSL_E_SHAPE, "lda (%lld) < K (%lld)", (long long)lda, (long long)K);
-  if (r > 0 && ldb < r) return fail(WSL_E_SHAPE, "ldb (%lld) < r (%lld)", (long long)ldb, (long long)r);
-  if (ldy < N) return fail(WSL_E_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
-  if (((uintptr_t)x & 1) || ((uintptr_t)y & 1) || ((uintptr_t)a & 1) || ((uintptr_t)b & 1) ||
-      ((uintptr_t)w_scale & 3) || (w_dtype == WSL_DTYPE_BF16 && ((uintptr_t)w & 1)))
-    return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
+  return run_call(make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r, stream),
+                  workspace, workspace_bytes);
+}
 
-  wsl::LoraArgs p;
-  p.x = x; p.ldx = ldx;
-  p.w = w; p.ldw = ldw; p.w_dtype = w_dtype; p.w_scale = w_scale;
-  p.a = a; p.lda = lda; p.b = b; p.ldb = ldb;
-  p.scale = scale;
-  p.y = y; p.ldy = ldy;
-  p.M = M; p.N = N; p.K = K; p.r = r;
-  p.ws = workspace; p.ws_bytes = workspace_bytes;
-  p.stream = reinterpret_cast<hipStream_t>(stream);
-  p.gather = nullptr; p.gather_rows = 0;
-
-  Path path = choose_path(p);
-  if (path == Path::kNone) return WSL_OK;
-  const size_t need = workspace_for(p);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
-  if ((uintptr_t)workspace & 255)
-    return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
-  rc = check_device();
+int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int32_t n_groups,
+                                            const int64_t* group_n, int32_t w_dtype, size_t* bytes) {
+  clear_err();
+  if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
+  int64_t N = 0;
+  int rc = validate_groups(n_groups, group_n, &N);
   if (rc != WSL_OK) return rc;
+  rc = validate_sizes(M, N, K, r, w_dtype);
+  if (rc != WSL_OK) return rc;
+  size_t b = prefill_ws(M, N, K, r * n_groups, w_dtype);
+  for (int g = 0; g < n_groups; ++g) {
+    const size_t s1 = workspace_upper_bound(M, group_n[g], K, r, w_dtype);
+    if (s1 > b) b = s1;
+  }
+  *bytes = b;
+  return WSL_OK;
+}
 
-  hipError_t e;
-  if (path != Path::kDecode) {
-    p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes;
-    p.ws_bytes = workspace_bytes - wsl::kCounterBytes;
+int wsl_lora_linear_grouped_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+                                const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
+                                float scale, void* y, int64_t ldy, int64_t M, int64_t K, int64_t r,
+                                int32_t n_groups, const int64_t* group_n, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  clear_err();
+  int64_t N = 0;
+  int rc = validate_groups(n_groups, group_n, &N);
+  if (rc != WSL_OK) return rc;
+  rc = validate_call(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, y, ldy, M, N, K, r);
+  if (rc != WSL_OK) return rc;
+  wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r, stream);
+  p.groups = n_groups;
+  int64_t end = 0;
+  for (int g = 0; g < n_groups; ++g) p.gend[g] = (end += group_n[g]);
+  if (n_groups == 1 || r == 0) {
+    p.groups = 1;
+    return run_call(p, workspace, workspace_bytes);
   }
-  switch (path) {
-    case Path::kDecode: e = wsl::launch_decode(p); break;
-    case Path::kPrefill: e = wsl::launch_prefill(p); break;
-    default: e = wsl::launch_generic(p); break;
+  if (choose_path(p) == Path::kPrefill && wsl::prefill_groups_supported(p)) return run_call(p, workspace, workspace_bytes);
+  // Decode-shaped, unaligned or tile-incompatible groups: one launch per group, in order,
+  // on the same stream (the workspace is reused stream-ordered).
+  const int64_t wbytes = (w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;
+  int64_t n0 = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    wsl::LoraArgs q = p;
+    q.groups = 1;
+    q.N = group_n[g];
+    if (w != nullptr) q.w = reinterpret_cast<const char*>(w) + n0 * ldw * wbytes;
+    if (w_scale != nullptr) q.w_scale = w_scale + n0;
+    q.a = reinterpret_cast<const uint16_t*>(a) + (int64_t)g * r * lda;
+    q.b = reinterpret_cast<const uint16_t*>(b) + n0 * ldb;
+    q.y = reinterpret_cast<uint16_t*>(y) + n0;
+    rc = run_call(q, workspace, workspace_bytes);
+    if (rc != WSL_OK) return rc;
+    n0 += group_n[g];
   }
-  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return WSL_OK;
 }
 

@@ -79,6 +79,8 @@ __device__ __forceinline__ u32x4_t zero_u32x4() {
 // Host-side launch helpers shared by the translation units of libwsl.
 namespace wsl {
 
+constexpr int kMaxGroups = 4;  // projections in one grouped launch (WSL_MAX_GROUPS)
+
 struct LoraArgs {
   const void* x; int64_t ldx;
   const void* w; int64_t ldw; int w_dtype; const float* w_scale;
@@ -95,12 +97,18 @@ struct LoraArgs {
   // Factor applied to the fp32 result before the bf16 rounding of y (prefill path; the
   // rank pre-pass uses it to store bf16(s * x . A^T)).
   float yscale = 1.f;
+  // Grouped launch (prefill path): `groups` projections side by side in N. Group g holds
+  // output columns [gend[g-1], gend[g]) (gend[groups-1] = N) and uses rows g*r..g*r+r-1
+  // of a; w, w_scale, b and y are indexed by the output column as usual.
+  int groups = 1;
+  int64_t gend[kMaxGroups] = {0, 0, 0, 0};
 };
 
 // Each launcher returns hipSuccess or the launch error.
 hipError_t launch_prefill(const LoraArgs& p);
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool prefill_supported(const LoraArgs& p);
+bool prefill_groups_supported(const LoraArgs& p);
 
 hipError_t launch_decode(const LoraArgs& p);
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);

@@ -234,6 +234,167 @@ def _lora_linear_backward(ctx, gy):
 lora_linear_op.register_autograd(_lora_linear_backward, setup_context=_lora_linear_setup)
 
 
+@torch.library.custom_op("wsl::lora_linear_grouped", mutates_args=(), device_types="cuda")
+def lora_linear_grouped_op(x: torch.Tensor, w: torch.Tensor, w_scale: Optional[torch.Tensor],
+                           a: Optional[torch.Tensor], b: Optional[torch.Tensor], scale: float,
+                           group_n: list[int]) -> torch.Tensor:
+    """Projections that read the same x, side by side in N (wsl_lora_linear_grouped_fwd).
+
+    w [N, K] and b [N, r] stack the groups' rows (N = sum(group_n)); a [G*r, K] stacks
+    their A factors (group g uses rows g*r..g*r+r-1). Output column block g is
+    ``x . w_g^T (* w_scale_g) + scale * (x . a_g^T) . b_g^T``, the result of
+    ``lora_linear_op`` on that group alone.
+    """
+    dev = _check_device(x, w, w_scale, a, b)
+    K = x.shape[-1]
+    G = len(group_n)
+    if not 1 <= G <= _native.WSL_MAX_GROUPS or any(int(n) < 1 for n in group_n):
+        raise ValueError(f"group_n must hold 1..{_native.WSL_MAX_GROUPS} positive widths, got {group_n}")
+    N = sum(int(n) for n in group_n)
+    lead = x.shape[:-1]
+    x2 = _row_major(x.reshape(-1, K), "x")
+    M = x2.shape[0]
+    if x2.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16, got {x2.dtype}")
+    w = _row_major(w, "w")
+    if w.shape != (N, K):
+        raise ValueError(f"w is {tuple(w.shape)}, expected ({N}, {K}) for groups {group_n}")
+    w_dtype = _native.WSL_DTYPE_BF16
+    if w.dtype == _FP8:
+        w_dtype = _native.WSL_DTYPE_FP8_E4M3
+        if w_scale is None or w_scale.dtype != torch.float32 or w_scale.shape != (N,):
+            raise ValueError(f"an fp8 w needs w_scale fp32 [{N}]")
+        w_scale = w_scale.contiguous()
+    elif w.dtype != torch.bfloat16:
+        raise TypeError(f"w must be bfloat16 or float8_e4m3fn, got {w.dtype}")
+    elif w_scale is not None:
+        raise ValueError("w_scale is only valid with an fp8 w")
+    r = 0
+    if a is not None or b is not None:
+        if a is None or b is None:
+            raise ValueError("a and b must be given together")
+        a = _row_major(a, "a")
+        b = _row_major(b, "b")
+        r = b.shape[1]
+        if a.shape != (G * r, K) or b.shape[0] != N:
+            raise ValueError(f"LoRA shapes a {tuple(a.shape)}, b {tuple(b.shape)} do not match "
+                             f"{G} groups of rank {r}, K={K}, N={N}")
+        if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+            raise TypeError("a and b must be bfloat16")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    if M > 0:
+        gn = _native.group_array(group_n)
+        ws_bytes = _native.grouped_workspace_bytes(M, K, r, group_n, w_dtype)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws = workspace(dev, stream, ws_bytes)
+        with torch.cuda.device(dev):
+            rc = _native.lib().wsl_lora_linear_grouped_fwd(
+                x2.data_ptr(), x2.stride(0),
+                w.data_ptr(), w.stride(0), w_dtype, _dev_ptr(w_scale),
+                _dev_ptr(a), a.stride(0) if a is not None else 0,
+                _dev_ptr(b), b.stride(0) if b is not None else 0,
+                float(scale),
+                y.data_ptr(), y.stride(0),
+                M, K, r, G, gn,
+                ws.data_ptr(), ws.numel(), stream)
+        if rc != _native.WSL_OK:
+            _workspaces.pop((dev.index, stream, "lora"), None)
+        _native.check(rc, "wsl_lora_linear_grouped_fwd")
+    return y.reshape(*lead, N)
+
+
+@lora_linear_grouped_op.register_fake
+def _lora_linear_grouped_fake(x, w, w_scale, a, b, scale, group_n):
+    return x.new_empty((*x.shape[:-1], sum(int(n) for n in group_n)), dtype=torch.bfloat16)
+
+
+def _block_diag_rows(b: torch.Tensor, group_n, r: int) -> torch.Tensor:
+    """[N, G*r] with group g's rows of b in column block g and zeros elsewhere."""
+    out = b.new_zeros(b.shape[0], len(group_n) * r)
+    n0 = 0
+    for g, n in enumerate(group_n):
+        out[n0:n0 + n, g * r:(g + 1) * r] = b[n0:n0 + n]
+        n0 += n
+    return out
+
+
+def _lora_linear_grouped_setup(ctx, inputs, output):
+    x, w, w_scale, a, b, scale, group_n = inputs
+    ctx.save_for_backward(x, w, w_scale, a, b)
+    ctx.scale = scale
+    ctx.group_n = [int(n) for n in group_n]
+
+
+def _lora_linear_grouped_backward(ctx, gy):
+    """Backward of ``wsl::lora_linear_grouped``: the per-group backward of
+    ``wsl::lora_linear`` summed over the groups for dx. With Bd the block-diagonal
+    [N, G*r] form of b (group g's rows in column block g):
+
+        dx = gy . W + scale * (gy . Bd) . a      one launch of the fused kernel, rank G*r
+        dW = gy^T . x                            one GEMM over all groups
+        da = scale * (gy . Bd)^T . x             one GEMM over all groups
+        db_g = scale * gy_g^T . (x . a_g^T)      per group (x . a^T computed once)
+
+    The reference differentiates each projection separately (torch autograd over
+    torchtitan/models/llama3/model/model.py:189-192,392-398) and sums the three dx of
+    q, k and v where x fans out; this is the same sum.
+    """
+    x, w, w_scale, a, b = ctx.saved_tensors
+    s = float(ctx.scale)
+    gn = ctx.group_n
+    need_x, need_w, _, need_a, need_b, _, _ = ctx.needs_input_grad
+    K = x.shape[-1]
+    gy2 = _row_major(gy.reshape(-1, gy.shape[-1]).to(torch.bfloat16), "grad_y")
+    x2 = x.reshape(-1, K)
+    has_lora = a is not None and b is not None and b.shape[1] > 0
+    r = b.shape[1] if has_lora else 0
+    bd = _block_diag_rows(b, gn, r) if has_lora else None
+    dx = dw = da = db = None
+    if need_x:
+        if w.dtype == _FP8:
+            wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous()
+        else:
+            wt = _transposed(w)
+        if has_lora:
+            dx = lora_linear_op(gy2, wt, None, bd.t().contiguous(), a.t().contiguous(), s)
+        else:
+            dx = lora_linear_op(gy2, wt, None, None, None, s)
+        dx = dx.reshape(x.shape)
+    if need_w and w.dtype == torch.bfloat16:
+        dw = torch.mm(gy2.t(), x2)
+    if has_lora and (need_a or need_b):
+        zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)
+        if need_a:
+            da = torch.addmm(zero, torch.mm(gy2, bd).t(), x2, beta=0, alpha=s)
+        if need_b:
+            t = torch.mm(x2, a.t().contiguous())
+            db = torch.empty_like(b)
+            n0 = 0
+            for g, n in enumerate(gn):
+                torch.addmm(zero, gy2[:, n0:n0 + n].t(), t[:, g * r:(g + 1) * r], beta=0, alpha=s, out=db[n0:n0 + n])
+                n0 += n
+    return dx, dw, None, da, db, None, None
+
+
+lora_linear_grouped_op.register_autograd(_lora_linear_grouped_backward, setup_context=_lora_linear_grouped_setup)
+
+
+def lora_linear_grouped(x: torch.Tensor, ws, as_=None, bs=None, scale: float = 2.0) -> list:
+    """Several LoRA linears over the same x in one call: ``ws`` lists the base weights
+    [N_g, K], ``as_`` / ``bs`` the LoRA factors [r, K] / [N_g, r] (all of rank r), one scale.
+    Returns the per-group outputs as views of one [..., sum N_g] tensor. The operands are
+    stacked with torch.cat (differentiable), so callers that reuse them should stack once
+    and call ``lora_linear_grouped_op`` directly."""
+    group_n = [int(w_.shape[0]) for w_ in ws]
+    w = torch.cat(list(ws), 0) if len(ws) > 1 else ws[0]
+    a = b = None
+    if as_ is not None:
+        a = torch.cat(list(as_), 0)
+        b = torch.cat(list(bs), 0)
+    y = lora_linear_grouped_op(x, w, None, a, b, float(scale), group_n)
+    return list(torch.split(y, group_n, dim=-1))
+
+
 @torch.library.custom_op("wsl::factorized_embedding", mutates_args=(), device_types="cuda")
 def factorized_embedding_op(ids: torch.Tensor, emb: torch.Tensor, proj: torch.Tensor) -> torch.Tensor:
     """out[..., :] = emb[ids[...], :] . proj^T   (emb [V,k], proj [H,k], bf16)."""
