@@ -292,12 +292,16 @@ def bench_c2_1p7b(dev, steps, warmup):
 
 
 def bench_c3(dev, steps, warmup):
+    """Config 3 per M: one launch per projection with cold weights (6 rotating copies) and
+    warm (one copy), and cold with q|k|v and gate|up as grouped launches (4 per layer)."""
     out = {}
     for M in (1, 8, 32, 64):
         row = {}
-        for label, copies in (("cold", 6), ("warm", 1)):
+        for label, copies, grouped in (("cold", 6, False), ("warm", 1, False), ("cold_grouped", 6, True)):
             st = ProjectionStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=copies)
-            g = graph_of(st.run)
+            if grouped:
+                st.stack_groups()
+            g = graph_of(st.run_grouped if grouped else st.run)
             ms = time_replays(g, steps, warmup)
             row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
                           "frac_hbm": round(st.bytes() / ms / 1e6 / HBM_PEAK_GBS, 4)}

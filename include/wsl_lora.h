@@ -104,10 +104,12 @@ int wsl_lora_linear_fwd(const void* x, int64_t ldx,
  * Replaces the projections of one reference block that read the same activation: q, k
  * and v (torchtitan/models/llama3/model/model.py:376-398, each base + broadcast_add of
  * its LoRA delta; Qwen3 wq/wk/wv, torchtitan/experiments/qwen3/model/model.py:184) and
- * gate/up (qwen3/model/model.py:250-251). On the prefill path with group boundaries that
- * whole output tiles respect (multiples of 128; of 256 for ranks 33-64) the groups run as
- * one launch, each output tile taking its group's rank block; otherwise the groups run
- * as consecutive launches on `stream`. Results are those of the per-group calls.
+ * gate/up (qwen3/model/model.py:250-251). The groups run as one launch where every group
+ * boundary falls on the launch's work grid: on the prefill path, whole output tiles
+ * (multiples of 128; of 256 for ranks 33-64), each tile taking its group's rank block; on
+ * the decode path (M <= 64), whole row groups of W (multiples of 64 suffice), the T
+ * work covering all groups' A rows. Otherwise the groups run as consecutive launches on
+ * `stream`. Results are those of the per-group calls.
  */
 #define WSL_MAX_GROUPS 4
 int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int32_t n_groups,

@@ -40,7 +40,11 @@ CASES = [
     (8192, 128, 32, (3072, 3072), 2.0),         # gate|up: 256 x 192 or 256 x 256 tiles
     (4096, 256, 16, (384, 640), 2.0),           # boundary at 384: 128-wide tiles only
     (300, 192, 24, (128, 128, 256, 128), 2.0),  # four groups, odd rank
-    (8, 512, 32, (1024, 512, 512), 2.0),        # decode-shaped M: one launch per group
+    (8, 512, 32, (1024, 512, 512), 2.0),        # decode-shaped M: one launch, T over 3 rank blocks
+    (1, 2048, 64, (2048, 1024, 1024), 2.0),     # config-3 q|k|v at M = 1
+    (32, 1024, 64, (1024, 512, 512), 2.0),      # M = 32: two token blocks
+    (64, 512, 32, (1536, 1536), 2.0),           # M = 64, gate|up
+    (3, 256, 16, (96, 160), 2.0),               # decode, boundary off the row groups: per group
     (500, 256, 16, (200, 120), 2.0),            # boundary off every tile grid: per group
     (260, 200, 16, (256, 128), 2.0),            # K % 64 != 0: generic path per group
     (512, 256, 0, (512, 256), 2.0),             # no LoRA: plain stacked linear
@@ -145,3 +149,41 @@ def test_grouped_backward(gpu, M, K, r, group_n):
         err = O.max_rel_err(got.float().cpu().numpy(), ref)
         _say(f"   {name} max_rel_err {err:.2e}")
         assert err <= BF16_TOL, (name, err)
+
+
+def test_grouped_decode_t_wait_fallback(gpu, monkeypatch):
+    """With the T poll bound at zero every W workgroup computes its group's T columns
+    itself from x and the stacked A (the fallback reads rows g*r.. of a): same bits as
+    the published path."""
+    from weightshared_torchtitan_amd import ops
+    M, K, r, group_n = 8, 1024, 32, (1024, 512, 512)
+    _say(f"[grouped decode fallback] M={M} K={K} r={r} groups={group_n}")
+    x, Ws, As, Bs = _inputs(M, K, r, group_n, seed=13)
+    args = [t.to(gpu) for t in (x, torch.cat(Ws).bfloat16(), torch.cat(As), torch.cat(Bs))]
+    y0 = ops.lora_linear_grouped_op(args[0], args[1], None, args[2], args[3], 2.0, list(group_n))
+    torch.cuda.synchronize()
+    monkeypatch.setenv("WSL_DECODE_SPIN_LIMIT", "0")
+    y1 = ops.lora_linear_grouped_op(args[0], args[1], None, args[2], args[3], 2.0, list(group_n))
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+
+
+def test_grouped_decode_fp8_base(gpu):
+    from weightshared_torchtitan_amd import lora, ops
+    M, K, r, group_n = 16, 1024, 128, (1024, 256, 256)
+    _say(f"[grouped decode fp8] M={M} K={K} r={r} groups={group_n}")
+    x, Ws, As, Bs = _inputs(M, K, r, group_n, seed=17)
+    wq, sc = lora.quantize_fp8_per_channel(torch.cat(Ws, 0))
+    d = lambda t: t.to(gpu)
+    y = ops.lora_linear_grouped_op(d(x), d(wq), d(sc), d(torch.cat(As)), d(torch.cat(Bs)), 1.0, list(group_n)).cpu()
+    import weightshared_torchtitan_amd as wsl
+    n0 = 0
+    for g, n in enumerate(group_n):
+        yg = wsl.lora_linear(d(x), d(wq[n0:n0 + n].contiguous()), d(As[g]), d(Bs[g]), 1.0,
+                             w_scale=d(sc[n0:n0 + n].contiguous())).cpu()
+        assert torch.equal(y[:, n0:n0 + n], yg), g
+        ref = O.lora_linear(x.float().numpy(), Ws[g].float().numpy(), As[g].float().numpy(), Bs[g].float().numpy(), 1.0)
+        err = O.max_rel_err(y[:, n0:n0 + n].float().numpy(), ref)
+        _say(f"   group {g} max_rel_err {err:.2e}")
+        assert err <= FP8_TOL, (g, err)
+        n0 += n

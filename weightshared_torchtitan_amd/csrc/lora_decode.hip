@@ -53,6 +53,7 @@
 // arithmetic: the decode loop runs the same projections at small M
 // (scripts/generate/_generation.py:35-80 calling
 // torchtitan/models/llama3/model/model.py:189-192,392-398).
+#include <climits>
 #include <cstdlib>
 #include <type_traits>
 
@@ -222,11 +223,15 @@ struct DecodeArgs {
   uint16_t* y; int64_t ldy;
   float s;
   int M, N, K, r, r32;
+  // Grouped launch: T holds rt = groups * r rank columns (A stacked by group); W rows from
+  // ge_{g-1} to ge_g belong to group g, whose T columns start at g * r. rt = r and every
+  // ge = INT_MAX for a single projection.
+  int rt, ge0, ge1, ge2;
   int gT, kst, kct;   // T groups (16 * 8 / KW rows of A), K split and slice
   int gY, ksy, kcy;   // W groups (16*NR rows of W), K split and slice
   int flag_off;       // LDS byte offset of the broadcast word
   unsigned* cnt;      // counter prefix of the workspace
-  uint64_t* tfin;     // T [M][r]: ttag << 16 | bf16 bits
+  uint64_t* tfin;     // T [M][rt]: ttag << 16 | bf16 bits
   uint64_t* tpart;    // [gT][kst][T rows per group][M]: ptag << 32 | fp32 partial sum
   uint64_t* ypart;    // [gY][ksy][W rows per group][M]: likewise
   int spin;           // polls of the T counter before the local fallback
@@ -494,7 +499,7 @@ __device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, in
 
 template <int MC, bool NORM = false, bool COH = false>
 __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint64_t tag, int* flag,
-                                         const float* ss = nullptr) {
+                                         const float* ss = nullptr, int goff = 0) {
   const int tid = threadIdx.x;
   const int tls = p.r32 + 8;
   const uint64_t ttag = ttag_of(tag);
@@ -507,14 +512,18 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
   for (int q0 = 0; q0 < n; q0 += LB * DT) {
     uint64_t v[LB];
 #pragma unroll
-    for (int u = 0; u < LB; ++u) v[u] = ld_agent(p.tfin + min(q0 + u * DT + tid, n - 1));
+    for (int u = 0; u < LB; ++u) {
+      const int q = min(q0 + u * DT + tid, n - 1);
+      v[u] = ld_agent(p.tfin + (q / p.r) * p.rt + goff + q % p.r);
+    }
 #pragma unroll
     for (int u = 0; u < LB; ++u) {
       const int q = q0 + u * DT + tid;
       if (q < n) {
-        for (int it = 0; (v[u] >> 16) != ttag && it < p.spin; ++it) v[u] = ld_agent(p.tfin + q);
-        if ((v[u] >> 16) != ttag) *flag = 1;
         const int m = q / p.r, j = q % p.r;
+        const uint64_t* src = p.tfin + m * p.rt + goff + j;
+        for (int it = 0; (v[u] >> 16) != ttag && it < p.spin; ++it) v[u] = ld_agent(src);
+        if ((v[u] >> 16) != ttag) *flag = 1;
         tl[m * tls + j] = (uint16_t)(v[u] & 0xffffu);
       }
     }
@@ -525,7 +534,7 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
   if (!ok) {
     for (int q = tid; q < n; q += DT) {
       const int m = q / p.r, j = q % p.r;
-      const uint16_t* ar = p.a + (int64_t)j * p.lda;
+      const uint16_t* ar = p.a + (int64_t)(goff + j) * p.lda;
       float acc = 0.f;
       for (int k = 0; k < p.K; k += 8) {
         float xv[8];
@@ -678,26 +687,26 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     float* sums = reinterpret_cast<float*>(smem + RED_T);
     if constexpr (CONS) {  // the x rows arrive from the producer during the A loads
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
-      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums,
+      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums,
                                    NormPrologue{&p, smem, ss, smem + p.nw_off},
                                    ConsumerPre{&p, smem, smem + p.nw_off, late_tag(), flag});
     } else if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
-      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums,
+      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums,
                                    NormPrologue{&p, smem, ss, smem + p.nw_off});
     } else {
       fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
-      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.r, g * TROWS, kbeg, p.kct, p.M, smem, sums);
+      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums);
     }
     const uint64_t tag = late_tag();
     if (split_reduce<kBF16, TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, ks, p.kst, p.M,
-                                       ptag_of(tag), p.spin, p.a, p.lda, p.r, g * TROWS, p.x, p.ldx,
+                                       ptag_of(tag), p.spin, p.a, p.lda, p.rt, g * TROWS, p.x, p.ldx,
                                        p.kct)) {
       for (int q = tid; q < p.M * TROWS; q += DT) {
         const int m = q / TROWS, rl = q % TROWS, j = g * TROWS + rl;
-        if (j < p.r) st_agent(p.tfin + m * p.r + j, (ttag_of(tag) << 16) | f32_to_bf16_bits(p.s * sums[rl * MC + m]));
+        if (j < p.rt) st_agent(p.tfin + m * p.rt + j, (ttag_of(tag) << 16) | f32_to_bf16_bits(p.s * sums[rl * MC + m]));
       }
     }
   } else {
@@ -733,7 +742,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     const uint64_t tag = late_tag();
     if (split_reduce<WDT, ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, ks, p.ksy, p.M,
                                     ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy)) {
-      if (p.r > 0) gather_t<MC, NORM, CONS>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16));
+      if (p.r > 0) {
+        const int goff = ((row0 >= p.ge0) + (row0 >= p.ge1) + (row0 >= p.ge2)) * p.r;
+        gather_t<MC, NORM, CONS>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
+      }
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
       const int l16 = lane & 15, grp = lane >> 4;
       const int tls = p.r32 + 8;
@@ -897,7 +909,10 @@ double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
 // fused kernels are built for (one token block), or none (chained launches: fixed rule).
 enum class Pick { kAll, kFused, kFixed };
 
-DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick pick = Pick::kAll) {
+// rt: rank rows of the T work (groups * r for a grouped launch; r when negative).
+DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick pick = Pick::kAll,
+                       int64_t rt = -1) {
+  if (rt < 0) rt = r;
   DecodePlan pl{};
   pl.mb = (int)((M + 15) / 16);
   if (pl.mb < 1) pl.mb = 1;
@@ -932,7 +947,7 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
     if (pl.kw == 8 || plan_smem(pl, M, &pl.flag_off) <= (size_t)LDS_MAX) break;
     pl.kw <<= 1;
   }
-  pl.gT = r > 0 ? (int)((r + pl.trows - 1) / pl.trows) : 0;
+  pl.gT = r > 0 ? (int)((rt + pl.trows - 1) / pl.trows) : 0;
   // Whole wave steps along K: rows per workgroup (16, 32 or 64) by the modelled time,
   // among the choices whose LDS fits. (At M = 1 and 8, 6144 x 2048 went 13.0 -> 11.3 us;
   // fp8 at M = 16, 12288 x 4096 went 40.7 -> 20.6 us: one wave of workgroups, not three.)
@@ -960,7 +975,7 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
           (uint64_t)pl.gT * pl.kst + (uint64_t)pl.gY * pl.ksy < kLaunchUnit;
   size_t off = kCounterBytes;
   pl.off_t = off;
-  off += (size_t)M * r * 8;
+  off += (size_t)M * rt * 8;
   off = (off + 255) & ~(size_t)255;
   pl.off_pt = off;
   if (pl.kst > 1) off += (size_t)pl.gT * pl.kst * M * pl.trows * 8;
@@ -1102,6 +1117,10 @@ DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl, char* cnt, char* d
   a.y = reinterpret_cast<uint16_t*>(p.y); a.ldy = p.ldy;
   a.s = p.scale;
   a.M = (int)p.M; a.N = (int)p.N; a.K = (int)p.K; a.r = (int)p.r; a.r32 = pl.r32;
+  a.rt = (int)(p.r * p.groups);
+  a.ge0 = p.groups > 1 ? (int)p.gend[0] : INT_MAX;
+  a.ge1 = p.groups > 2 ? (int)p.gend[1] : INT_MAX;
+  a.ge2 = p.groups > 3 ? (int)p.gend[2] : INT_MAX;
   a.gT = pl.gT; a.kst = pl.kst; a.kct = pl.kct;
   a.gY = pl.gY; a.ksy = pl.ksy; a.kcy = pl.kcy;
   a.flag_off = (int)pl.flag_off;
@@ -1118,8 +1137,25 @@ DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl) {
 }
 }  // namespace
 
+// A grouped launch on the decode path: every group boundary on a W workgroup boundary
+// (whole row groups of the plan), so each workgroup's rows take one group's T columns.
+bool decode_groups_supported(const LoraArgs& p) {
+  if (p.groups < 1 || p.groups > kMaxGroups) return false;
+  if (p.groups == 1) return true;
+  if (p.r == 0) return false;
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kAll, p.r * p.groups);
+  if (!pl.ok) return false;
+  for (int g = 0; g + 1 < p.groups; ++g)
+    if (p.gend[g] % pl.rows != 0) return false;
+  return true;
+}
+
+size_t decode_grouped_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int groups, int w_dtype) {
+  return plan_decode(M, N, K, r, w_dtype, Pick::kAll, r * groups).total;
+}
+
 hipError_t launch_decode(const LoraArgs& p) {
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype);
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kAll, p.r * p.groups);
   const DecodeArgs a = make_args(p, pl);
   const int grid = pl.gT * pl.kst + pl.gY * pl.ksy;
   return p.w_dtype == kFP8 ? dispatch<kFP8>(a, pl.mb, pl.nr, pl.kw, grid, pl.smem, p.stream)

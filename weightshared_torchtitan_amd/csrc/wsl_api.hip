@@ -165,7 +165,9 @@ int run_call(wsl::LoraArgs p, void* workspace, size_t workspace_bytes) {
   const Path path = choose_path(p);
   if (path == Path::kNone) return WSL_OK;
   size_t need = workspace_for(p);
-  if (p.groups > 1) need = prefill_ws(p.M, p.N, p.K, p.r * p.groups, p.w_dtype);
+  if (p.groups > 1)
+    need = path == Path::kDecode ? wsl::decode_grouped_workspace_bytes(p.M, p.N, p.K, p.r, p.groups, p.w_dtype)
+                                 : prefill_ws(p.M, p.N, p.K, p.r * p.groups, p.w_dtype);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
   if ((uintptr_t)workspace & 255)
@@ -228,6 +230,10 @@ int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int
   rc = validate_sizes(M, N, K, r, w_dtype);
   if (rc != WSL_OK) return rc;
   size_t b = prefill_ws(M, N, K, r * n_groups, w_dtype);
+  if (M >= 1 && M <= wsl::kDecodeMaxM) {
+    const size_t d = wsl::decode_grouped_workspace_bytes(M, N, K, r, n_groups, w_dtype);
+    if (d > b) b = d;
+  }
   for (int g = 0; g < n_groups; ++g) {
     const size_t s1 = workspace_upper_bound(M, group_n[g], K, r, w_dtype);
     if (s1 > b) b = s1;
@@ -255,9 +261,12 @@ int wsl_lora_linear_grouped_fwd(const void* x, int64_t ldx, const void* w, int64
     p.groups = 1;
     return run_call(p, workspace, workspace_bytes);
   }
-  if (choose_path(p) == Path::kPrefill && wsl::prefill_groups_supported(p)) return run_call(p, workspace, workspace_bytes);
-  // Decode-shaped, unaligned or tile-incompatible groups: one launch per group, in order,
-  // on the same stream (the workspace is reused stream-ordered).
+  const Path path = choose_path(p);
+  if ((path == Path::kPrefill && wsl::prefill_groups_supported(p)) ||
+      (path == Path::kDecode && wsl::decode_groups_supported(p)))
+    return run_call(p, workspace, workspace_bytes);
+  // Unaligned operands or group ends off the launch's tile / row-group grid: one launch
+  // per group, in order, on the same stream (the workspace is reused stream-ordered).
   const int64_t wbytes = (w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;
   int64_t n0 = 0;
   for (int g = 0; g < n_groups; ++g) {
