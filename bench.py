@@ -118,7 +118,12 @@ class ProjectionStack:
     def stack_groups(self):
         """Stacked operands of the grouped run, built once from the same tensors: per
         weight copy [W_q; W_k; W_v] and [W_1; W_3], per layer the A and B factors likewise."""
-        cat = lambda ts: torch.cat(ts, 0).contiguous() if len(ts) > 1 else ts[0]
+        def cat(ts):
+            if len(ts) == 1:
+                return ts[0]
+            if ts[0].dtype == torch.float8_e4m3fn:  # stacked as bytes
+                return torch.cat([t.view(torch.uint8) for t in ts], 0).view(torch.float8_e4m3fn)
+            return torch.cat(ts, 0).contiguous()
         self.gW = [[cat([self.W[c][p] for p in grp]) for grp in self.GROUPS] for c in range(self.copies)]
         self.gS = [[cat([self.S[c][p] for p in grp]) if self.fp8 else None for grp in self.GROUPS]
                    for c in range(self.copies)]
@@ -319,13 +324,21 @@ def bench_c5(dev, steps, warmup):
                              copies=copies, fp8=True, scale=1.0)
         g = graph_of(st.run)
         ms = time_replays(g, steps, warmup)
+        del g
+        st.stack_groups()
+        g = graph_of(st.run_grouped)
+        ms_g = time_replays(g, steps, warmup)
         base = st.layers * sum(2.0 * M * N * K for _, N, K in st.shapes)
         lora = st.flops() - base
         t_min = base / (FP8_PEAK_TFLOPS * 1e12) + lora / (BF16_PEAK_TFLOPS * 1e12)
         out[f"M={M}"] = {"ms": round(ms, 4), "TFLOP/s": round(st.flops() / ms / 1e9, 1),
                          "GB/s": round(st.bytes() / ms / 1e6, 1),
                          "frac_mixed_mfma_roofline": round(t_min * 1e3 / ms, 4),
-                         "frac_hbm": round(st.bytes() / ms / 1e6 / HBM_PEAK_GBS, 4)}
+                         "frac_hbm": round(st.bytes() / ms / 1e6 / HBM_PEAK_GBS, 4),
+                         "grouped_qkv_gateup": {"ms": round(ms_g, 4), "TFLOP/s": round(st.flops() / ms_g / 1e9, 1),
+                                                "GB/s": round(st.bytes() / ms_g / 1e6, 1),
+                                                "frac_mixed_mfma_roofline": round(t_min * 1e3 / ms_g, 4),
+                                                "frac_hbm": round(st.bytes() / ms_g / 1e6 / HBM_PEAK_GBS, 4)}}
         del g, st
         torch.cuda.empty_cache()
     return out

@@ -134,3 +134,20 @@ def test_fused_decode_graph_greedy_matches_oracle(gpu):
         chosen = ref.gather(1, new[:, i:i + 1])[:, 0]
         assert bool((chosen >= ref.max(dim=-1).values - tol).all()), f"step {i}"
         toks = torch.cat([toks, new[:, i:i + 1]], 1)
+
+
+@pytest.mark.parametrize("seq", [12, 40, 100])
+def test_grouped_prefill_matches_per_projection(gpu, seq):
+    """Inference prefill with q|k|v and gate|up as grouped launches gives the same logits,
+    bit for bit, as one launch per projection (each group's block is the single op's)."""
+    a, m, p = build(gpu, seed=2)
+    g = torch.Generator().manual_seed(100 + seq)
+    toks = torch.randint(0, a.vocab_size, (2, seq), generator=g).to(gpu)
+    with torch.no_grad():
+        m.prefill_grouped = True
+        grouped = m(toks)
+        m.prefill_grouped = False
+        single = m(toks)
+    assert torch.equal(grouped, single)
+    ref = Q.reference_forward(p, a, toks.cpu())
+    assert rel(grouped, ref) <= LOGIT_TOL

@@ -212,12 +212,33 @@ class SharedQwen3(nn.Module):
         sin = rc[..., hd:].to(x.dtype)
         return x * cos + _rotate_half(x) * sin
 
-    def _ffn(self, layer: int, h: torch.Tensor) -> torch.Tensor:
+    def _ffn(self, layer: int, h: torch.Tensor, pk: Optional[dict] = None) -> torch.Tensor:
         blk = self.base_blocks[self.args.block_of(layer)]
         x = blk.ffn_norm(h)
-        g = self._proj(layer, "w1", x)
-        u = self._proj(layer, "w3", x)
+        gu = self._grouped(layer, "gu", x, pk)
+        if gu is not None:
+            g, u = gu
+        else:
+            g = self._proj(layer, "w1", x)
+            u = self._proj(layer, "w3", x)
         return h + self._proj(layer, "w2", F.silu(g) * u)
+
+    # With prefill_grouped, inference prefill runs q|k|v and gate|up as grouped launches (one
+    # each, on the stacked operands cached with the decode pack); with autograd on, always
+    # one launch per projection so the gradients reach the module parameters. Off by
+    # default: at the config-4 prompt (M = 4096) the per-projection launches fill the CUs
+    # with better-suited tiles (128 x 256 and 128 x 128 against one wave of 256 x 256), and
+    # the forward measured 21.9 ms against 22.2 ms grouped on MI355X.
+    prefill_grouped = False
+
+    def _grouped(self, layer: int, group: str, x: torch.Tensor, pk: Optional[dict]):
+        """The group's projections of x in one grouped launch, as a list of views, or None
+        when this call takes the per-projection path."""
+        if pk is None or pk["g_" + group][layer] is None:
+            return None
+        A, B, sc, widths = pk["g_" + group][layer]
+        y = ops.lora_linear_grouped_op(x, pk["w_" + group][self.args.block_of(layer)], None, A, B, sc, widths)
+        return list(y.split(widths, -1))
 
     # ------------------------------------------------------------------ prefill
     def forward(self, tokens: torch.Tensor, cache: Optional[KVCache] = None) -> torch.Tensor:
@@ -225,6 +246,7 @@ class SharedQwen3(nn.Module):
         Fills `cache` (positions 0..s-1) when given."""
         a = self.args
         b, s = tokens.shape
+        pk = self._decode_pack() if (self.prefill_grouped and not torch.is_grad_enabled()) else None
         h = self.tok_embeddings(tokens)
         rc = self.rope[:s].view(1, s, 1, 2 * a.head_dim)
         rep = a.n_heads // a.n_kv_heads
@@ -232,9 +254,12 @@ class SharedQwen3(nn.Module):
         for l in range(a.n_layers):
             blk = self.base_blocks[a.block_of(l)]
             x = blk.attention_norm(h)
-            xq = self._proj(l, "wq", x).view(b, s, a.n_heads, a.head_dim)
-            xk = self._proj(l, "wk", x).view(b, s, a.n_kv_heads, a.head_dim)
-            xv = self._proj(l, "wv", x).view(b, s, a.n_kv_heads, a.head_dim)
+            qkv = self._grouped(l, "qkv", x, pk)
+            if qkv is None:
+                qkv = [self._proj(l, n, x) for n in ("wq", "wk", "wv")]
+            xq = qkv[0].view(b, s, a.n_heads, a.head_dim)
+            xk = qkv[1].view(b, s, a.n_kv_heads, a.head_dim)
+            xv = qkv[2].view(b, s, a.n_kv_heads, a.head_dim)
             xq = self._rope(blk.attention.q_norm(xq), rc)
             xk = self._rope(blk.attention.k_norm(xk), rc)
             if cache is not None:
@@ -246,7 +271,7 @@ class SharedQwen3(nn.Module):
                 o = F.scaled_dot_product_attention(xq.transpose(1, 2).contiguous(), kk, vv, is_causal=True)
             o = o.transpose(1, 2).reshape(b, s, a.n_heads * a.head_dim)
             h = h + self._proj(l, "wo", o)
-            h = self._ffn(l, h)
+            h = self._ffn(l, h, pk)
         h = self.norm(h)
         return self.tok_embeddings.tied_logits(h)
 
@@ -284,6 +309,15 @@ class SharedQwen3(nn.Module):
                 r0, c0 = r0 + n, c0 + r
             return A, B, scales.pop()
 
+        def stack_lora(layer, names):
+            # [A_1; A_2; ...] and [B_1; B_2; ...] for wsl::lora_linear_grouped (one rank, one scale)
+            mods = [getattr(self.layer_loras[layer], n) for n in names]
+            if len({m.scale for m in mods}) != 1 or len({m.w_a.weight.shape[0] for m in mods}) != 1:
+                return None
+            A = torch.cat([m.w_a.weight for m in mods], 0).contiguous()
+            B = torch.cat([m.w_b.weight for m in mods], 0).contiguous()
+            return A, B, mods[0].scale, [m.w_b.weight.shape[0] for m in mods]
+
         def interleave8(g, u):
             # rows 16j..16j+7 <- g rows 8j..8j+7, rows 16j+8..16j+15 <- u rows 8j..8j+7
             n = g.shape[0]
@@ -306,7 +340,9 @@ class SharedQwen3(nn.Module):
                   "w_qkv": [cat_w(blk, ("wq", "wk", "wv")) for blk in self.base_blocks],
                   "w_gu": [cat_w(blk, ("w1", "w3")) for blk in self.base_blocks],
                   "l_qkv": [cat_lora(l, ("wq", "wk", "wv")) for l in range(a.n_layers)],
-                  "l_gu": [cat_lora(l, ("w1", "w3")) for l in range(a.n_layers)]}
+                  "l_gu": [cat_lora(l, ("w1", "w3")) for l in range(a.n_layers)],
+                  "g_qkv": [stack_lora(l, ("wq", "wk", "wv")) for l in range(a.n_layers)],
+                  "g_gu": [stack_lora(l, ("w1", "w3")) for l in range(a.n_layers)]}
             if a.hidden_dim % 8 == 0:
                 pk["w_gu_il"] = [interleave8(blk.base("w1").weight, blk.base("w3").weight).contiguous()
                                  for blk in self.base_blocks]
