@@ -3,17 +3,19 @@
 Headline (the JSON line's `value`): BASELINE config 2 — Qwen3-0.6B-shaped prefill
 projections in bf16, M = 8192 tokens, 7 projections x 28 layers per step, one shared
 base weight set, per-layer rank-32 LoRA (scale 2). A step is one pass over the 196
-projections, captured once as a HIP graph and replayed, one launch per projection. The
-same inputs with the projections that read one activation (q|k|v, gate|up) as grouped
-launches (4 per layer) are reported beside it. value = algorithmic TFLOP/s, FLOPs = sum
-over projections of 2*M*(N*K + r*(K+N)).
+projections, captured once as a HIP graph and replayed. The projections that read one
+activation (q|k|v, gate|up) run as one grouped launch each (wsl_lora_linear_grouped_fwd;
+each group's output is bit-identical to its own launch), so a layer is 4 launches; the same
+inputs with one launch per projection (7 per layer) are reported beside it. value =
+algorithmic TFLOP/s, FLOPs = sum over projections of 2*M*(N*K + r*(K+N)).
 
 Also reported (same JSON line, key "extra"): config 3 decode GB/s (cold and warm
 weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
 projections, and the CPU baseline (the reference's fp32 arithmetic on host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
-                      [--only c2|c3|c4|c5|emb|vendor|shape] [--shape M,N,K,r] [--vendor]
+                      [--only c2|c2single|c3|c4|c5|emb|vendor|backward|shape] [--shape M,N,K,r]
+                      [--vendor]
                       [--copy-calibration]
 
 --only runs one section and prints its JSON alone (for profiling one workload).
@@ -259,24 +261,25 @@ def time_replays(graph, steps, warmup):
 
 
 # ------------------------------------------------------------------------------ configs
-def bench_c2(dev, steps, warmup, grouped=True):
-    """Config 2, two ways on the same inputs: one launch per projection (7 per layer, 196
-    per step; the headline) and, with `grouped`, q|k|v and gate|up as grouped launches (4 per
-    layer, 112 per step). Back to back, the launch after a grouped one runs slower (it
-    follows a 64-96 MB output write), so the two come out alike here."""
+def bench_c2(dev, steps, warmup, grouped=True, single=True):
+    """Config 2 on the same inputs, two ways: q|k|v and gate|up (the projections that read
+    one activation) as grouped launches, 4 per layer, 112 per step (the headline), and one
+    launch per projection, 7 per layer, 196 per step. Returns (FLOPs, ms grouped, ms single);
+    a way not run gives None."""
     st = ProjectionStack(QWEN3_0P6B, M=8192, r=32, layers=28, dev=dev, seed=2)
-    g = graph_of(st.run)
-    ms = time_replays(g, steps, warmup)
-    del g
-    ms_grouped = None
+    ms_grouped = ms_single = None
     if grouped:
         st.stack_groups()
         g = graph_of(st.run_grouped)
         ms_grouped = time_replays(g, steps, warmup)
         del g
+    if single:
+        g = graph_of(st.run)
+        ms_single = time_replays(g, steps, warmup)
+        del g
     del st
     torch.cuda.empty_cache()
-    return lora_flops_c2(), ms, ms_grouped
+    return lora_flops_c2(), ms_grouped, ms_single
 
 
 def lora_flops_c2():
@@ -523,7 +526,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=("c2", "c3", "c4", "c5", "emb", "vendor", "backward", "shape"), default=None)
+    ap.add_argument("--only", choices=("c2", "c2single", "c3", "c4", "c5", "emb", "vendor", "backward", "shape"),
+                    default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -541,7 +545,7 @@ def main():
     torch.cuda.synchronize()
     if args.copy_calibration:
         copy_calibration(dev)
-    if args.only is not None and args.only != "c2":
+    if args.only is not None and args.only not in ("c2", "c2single"):
         fn = {"c3": lambda: bench_c3(dev, args.steps, args.warmup),
               "c4": lambda: bench_c4(dev),
               "c5": lambda: bench_c5(dev, args.steps, args.warmup),
@@ -551,9 +555,15 @@ def main():
               "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
-    flops, ms, ms_grouped = bench_c2(dev, args.steps, args.warmup, grouped=args.only is None)
+    flops, ms, ms_single = bench_c2(dev, args.steps, args.warmup, grouped=args.only != "c2single",
+                                    single=args.only in (None, "c2single"))
+    if args.only == "c2single":
+        print(json.dumps({"c2single": {"TFLOP/s": round(flops / ms_single / 1e9, 2), "ms_per_step": round(ms_single, 4),
+                                       "launches": 7 * 28, "avg_launch_us": round(ms_single * 1e3 / 196, 3)}}),
+              flush=True)
+        return
     tflops = flops / ms / 1e9
-    launches = 7 * 28
+    launches = 4 * 28
     res = {
         "metric": METRIC,
         "value": round(tflops, 2),
@@ -568,18 +578,20 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (x ~ N(0,1); W, A, B ~ N(0, 0.02^2); seeded)",
         "config": {"workload": "config 2: Qwen3-0.6B prefill projections, M=8192, 7 proj x 28 layers, "
-                               "one shared base W set, per-layer rank-32 LoRA, scale 2",
-                   "M": 8192, "hidden": 1024, "rank": 32, "layers": 28, "projections": 7},
+                               "one shared base W set, per-layer rank-32 LoRA, scale 2; the projections that "
+                               "read one activation (q|k|v, gate|up) run as one grouped launch each",
+                   "M": 8192, "hidden": 1024, "rank": 32, "layers": 28, "projections": 7,
+                   "launches_per_layer": 4},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": measured_traffic(),
-                     "kernel": "prefill_kernel (196 launches per step, one per projection)",
+                     "kernel": "prefill_kernel (112 launches per step: q|k|v, o, gate|up, down per layer)",
                      "avg_launch_us": round(ms * 1e3 / launches, 3)},
     }
     extra = {}
-    if ms_grouped is not None:
-        extra["c2_grouped_qkv_gateup"] = {"TFLOP/s": round(flops / ms_grouped / 1e9, 1),
-                                          "frac_mfma": round(flops / ms_grouped / 1e9 / BF16_PEAK_TFLOPS, 4),
-                                          "ms_per_step": round(ms_grouped, 4), "launches": 4 * 28}
+    if ms_single is not None:
+        extra["c2_one_launch_per_projection"] = {"TFLOP/s": round(flops / ms_single / 1e9, 1),
+                                                 "frac_mfma": round(flops / ms_single / 1e9 / BF16_PEAK_TFLOPS, 4),
+                                                 "ms_per_step": round(ms_single, 4), "launches": 7 * 28}
     if not args.no_extra and args.only is None:
         ms17, ms17s = bench_c2_1p7b(dev, args.steps, args.warmup)
         f17 = 4 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_1P7B)
