@@ -189,6 +189,23 @@ def test_ops_refuse_cpu_tensors():
     with pytest.raises((RuntimeError, NotImplementedError)):
         ops.factorized_embedding(torch.zeros(3, dtype=torch.int64), torch.zeros(10, 8, dtype=torch.bfloat16),
                                  torch.zeros(16, 8, dtype=torch.bfloat16))
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        ops.lora_linear_grouped(x, [w, w], [torch.zeros(8, 64, dtype=torch.bfloat16)] * 2,
+                                [torch.zeros(32, 8, dtype=torch.bfloat16)] * 2, 2.0)
+
+
+def test_grouped_op_fake_kernel_shapes():
+    # the meta implementation gives [..., sum of widths] bf16, as the device op does
+    import torch
+
+    from weightshared_torchtitan_amd import ops
+    with torch.device("meta"):
+        x = torch.empty(3, 5, 64, dtype=torch.bfloat16)
+        w = torch.empty(96, 64, dtype=torch.bfloat16)
+        a = torch.empty(3 * 8, 64, dtype=torch.bfloat16)
+        b = torch.empty(96, 8, dtype=torch.bfloat16)
+        y = ops.lora_linear_grouped_op(x, w, None, a, b, 2.0, [64, 16, 16])
+    assert y.shape == (3, 5, 96) and y.dtype == torch.bfloat16 and y.device.type == "meta"
 
 
 @needs_lib

@@ -1,6 +1,8 @@
-"""torch custom ops over libwsl: ``wsl::lora_linear`` and ``wsl::factorized_embedding``.
+"""torch custom ops over libwsl: ``wsl::lora_linear``, ``wsl::lora_linear_grouped`` (the
+projections that read one activation in one call), ``wsl::factorized_embedding`` and the
+decode-step ops of the weight-shared Qwen3 harness.
 
-Both ops have a HIP (device type "cuda" on ROCm) implementation only. Called with CPU
+Every op has a HIP (device type "cuda" on ROCm) implementation only. Called with CPU
 tensors they raise; there is no CPU or eager-PyTorch fallback. Each op has a fake
 (meta) implementation so models can be built on the meta device and traced by
 torch.compile, matching how the reference builds its model
@@ -333,7 +335,7 @@ def _lora_linear_grouped_backward(ctx, gy):
         dx = gy . W + scale * (gy . Bd) . a      one launch of the fused kernel, rank G*r
         dW = gy^T . x                            one GEMM over all groups
         da = scale * (gy . Bd)^T . x             one GEMM over all groups
-        db_g = scale * gy_g^T . (x . a_g^T)      per group (x . a^T computed once)
+        db_g = scale * gy_g^T . (x . a_g^T)      the diagonal blocks of one [N, G*r] GEMM
 
     The reference differentiates each projection separately (torch autograd over
     torchtitan/models/llama3/model/model.py:189-192,392-398) and sums the three dx of
@@ -367,11 +369,14 @@ def _lora_linear_grouped_backward(ctx, gy):
         if need_a:
             da = torch.addmm(zero, torch.mm(gy2, bd).t(), x2, beta=0, alpha=s)
         if need_b:
+            # one product over all groups (gy read once), then each group's diagonal block:
+            # the off-diagonal blocks are a few GFLOP, cheaper than G strided skinny GEMMs
             t = torch.mm(x2, a.t().contiguous())
+            full = torch.addmm(zero, gy2.t(), t, beta=0, alpha=s)
             db = torch.empty_like(b)
             n0 = 0
             for g, n in enumerate(gn):
-                torch.addmm(zero, gy2[:, n0:n0 + n].t(), t[:, g * r:(g + 1) * r], beta=0, alpha=s, out=db[n0:n0 + n])
+                db[n0:n0 + n] = full[n0:n0 + n, g * r:(g + 1) * r]
                 n0 += n
     return dx, dw, None, da, db, None, None
 
