@@ -118,7 +118,8 @@ def test_grouped_in_graph_replays_match_eager(gpu):
 @pytest.mark.parametrize("M,K,r,group_n", [
     (1000, 256, 32, (512, 256, 256)),   # one launch, in-kernel rank
     (600, 256, 96, (256, 256)),         # one launch, pre-pass rank; dx at rank 192
-    (8, 256, 16, (256, 128, 128)),      # decode-shaped: per-group launches
+    (8, 256, 16, (256, 128, 128)),      # decode-shaped: one grouped launch
+    (300, 128, 128, (128, 128, 128)),   # G*r = 384 > WSL_MAX_RANK: dx per group, summed
 ])
 def test_grouped_backward(gpu, M, K, r, group_n):
     """Gradients of the grouped op against the float64 oracle of the per-projection

@@ -357,8 +357,17 @@ def _lora_linear_grouped_backward(ctx, gy):
             wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous()
         else:
             wt = _transposed(w)
-        if has_lora:
+        if has_lora and len(gn) * r <= _native.WSL_MAX_RANK:
             dx = lora_linear_op(gy2, wt, None, bd.t().contiguous(), a.t().contiguous(), s)
+        elif has_lora:  # G*r above the kernels' rank limit: one dx launch per group, summed
+            dx = None
+            n0 = 0
+            for g, n in enumerate(gn):
+                ag = a[g * r:(g + 1) * r]
+                d = lora_linear_op(gy2[:, n0:n0 + n], wt[:, n0:n0 + n], None, b[n0:n0 + n].t().contiguous(),
+                                   ag.t().contiguous(), s)
+                dx = d if dx is None else dx + d
+                n0 += n
         else:
             dx = lora_linear_op(gy2, wt, None, None, None, s)
         dx = dx.reshape(x.shape)
