@@ -163,6 +163,13 @@ class VendorStack(ProjectionStack):
             for p, (_, N, K) in enumerate(self.shapes):
                 torch.matmul(self.x[K], self.W[c][p].t())
 
+    def run_plain_grouped(self):
+        """The plain GEMM on the stacked q|k|v and gate|up weights (stack_groups first)."""
+        for l in range(self.layers):
+            c = l % self.copies
+            for q in range(len(self.GROUPS)):
+                torch.matmul(self.x[self.gK[q]], self.gW[c][q].t())
+
     def run_lora(self):
         for l in range(self.layers):
             c = l % self.copies
@@ -178,13 +185,18 @@ def bench_vendor(dev, steps, warmup):
     captured as a HIP graph of the same launches. Prefill: configs 2 (0.6B, 28 layers)
     and the 1.7B shapes (4 layers), M = 8192, r = 32, TFLOP/s of the LoRA linear's FLOPs
     (the plain GEMM's own FLOPs for the plain line). Decode: config 3 (1.7B, r = 64,
-    28 layers, 6 rotating weight copies), GB/s of the LoRA linear's bytes."""
+    28 layers, 6 rotating weight copies), GB/s of the LoRA linear's bytes. Each also with
+    q|k|v and gate|up grouped: the fused op's grouped launches, and the plain GEMM on the
+    stacked weights."""
     out = {}
     for name, shapes, layers in (("c2_qwen3_0.6b_prefill", QWEN3_0P6B, 28), ("qwen3_1.7b_prefill", QWEN3_1P7B, 4)):
         st = VendorStack(shapes, M=8192, r=32, layers=layers, dev=dev, seed=2)
+        st.stack_groups()
         plain_flops = layers * sum(2.0 * 8192 * N * K for _, N, K in shapes)
         row = {}
-        for label, fn, fl in (("wsl_fused", st.run, st.flops()), ("torch_plain_gemm", st.run_plain, plain_flops),
+        for label, fn, fl in (("wsl_fused", st.run, st.flops()), ("wsl_fused_grouped", st.run_grouped, st.flops()),
+                              ("torch_plain_gemm", st.run_plain, plain_flops),
+                              ("torch_plain_gemm_grouped", st.run_plain_grouped, plain_flops),
                               ("torch_unfused_lora", st.run_lora, st.flops())):
             g = graph_of(fn)
             ms = time_replays(g, steps, warmup)
@@ -196,8 +208,11 @@ def bench_vendor(dev, steps, warmup):
     dec = {}
     for M in (1, 8, 32, 64):
         st = VendorStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
+        st.stack_groups()
         row = {}
-        for label, fn in (("wsl_fused", st.run), ("torch_plain_gemm", st.run_plain), ("torch_unfused_lora", st.run_lora)):
+        for label, fn in (("wsl_fused", st.run), ("wsl_fused_grouped", st.run_grouped),
+                          ("torch_plain_gemm", st.run_plain), ("torch_plain_gemm_grouped", st.run_plain_grouped),
+                          ("torch_unfused_lora", st.run_lora)):
             g = graph_of(fn)
             ms = time_replays(g, steps, warmup)
             row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1)}
