@@ -56,7 +56,7 @@ constexpr int BK = 64;    // K per LDS buffer
 constexpr int ROWB = 128; // bytes per LDS row (BK bf16)
 constexpr int KK = 4;     // MFMA k steps per K tile
 constexpr int N_XCD = 8;
-constexpr int GROUP_M = 8;
+constexpr int GROUP_M = 4;  // row tiles per XCD group (4 against 8 and 16: +0.9 % at config 2 grouped)
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
