@@ -14,7 +14,8 @@ weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
 projections, and the CPU baseline (the reference's fp32 arithmetic on host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
-                      [--only c2|c2single|c3|c4|c5|emb|vendor|backward|shape] [--shape M,N,K,r]
+                      [--only c1|c2|c2single|c2_1p7b|c3|c4|c5|emb|vendor|backward|shape]
+                      [--shape M,N,K,r]
                       [--vendor]
                       [--copy-calibration]
 
@@ -314,6 +315,17 @@ def bench_c2_1p7b(dev, steps, warmup):
     return ms, ms_grouped
 
 
+def c2_1p7b_extra(dev, steps, warmup):
+    """The Qwen3-1.7B prefill shapes (the north star's >= 70 % target): 4 layers of the 7
+    projections, M = 8192, r = 32, one launch per projection and grouped."""
+    ms17, ms17g = bench_c2_1p7b(dev, steps, warmup)
+    f17 = 4 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_1P7B)
+    return {"TFLOP/s": round(f17 / ms17 / 1e9, 1), "frac_mfma": round(f17 / ms17 / 1e9 / BF16_PEAK_TFLOPS, 4),
+            "ms_per_4_layers": round(ms17, 4), "grouped_qkv_gateup_TFLOP/s": round(f17 / ms17g / 1e9, 1),
+            "grouped_frac_mfma": round(f17 / ms17g / 1e9 / BF16_PEAK_TFLOPS, 4),
+            "grouped_ms_per_4_layers": round(ms17g, 4)}
+
+
 def bench_c3(dev, steps, warmup):
     """Config 3 per M: one launch per projection with cold weights (6 rotating copies) and
     warm (one copy), and cold with q|k|v and gate|up as grouped launches (4 per layer)."""
@@ -462,6 +474,28 @@ def bench_embedding(dev, steps, warmup):
             "TFLOP/s": round(2.0 * T * k * H / ms / 1e9, 1)}
 
 
+def c4_step_bytes(a, batch, prompt, n_new):
+    """Algorithmic HBM bytes of one config-4 decode step, averaged over the steps: the KV
+    cache read at every position up to the step's (K and V, kv heads x head_dim bf16 per
+    sequence per layer), each unique block's base weights once, every layer's LoRA factors,
+    the embedding table E and P (the tied head reads all of E), and, as a second figure,
+    with every layer's base weights counted (no reuse across the 7 layers of a block)."""
+    sh = a.proj_shapes()
+    base = sum(o * i for o, i in sh.values()) * 2  # one block, bf16
+    lora = sum(a.lora_rank * (o + i) for o, i in sh.values()) * 2 * a.n_layers
+    emb = a.vocab_size * a.embed_rank * 2 + a.dim * a.embed_rank * 2
+    kv_pos = 2 * a.n_kv_heads * a.head_dim * 2 * batch * a.n_layers  # bytes per cached position
+    steps = n_new - 1
+    mean_len = sum(prompt + i + 1 for i in range(steps)) / steps  # positions 0..pos read at pos
+    kv = kv_pos * mean_len
+    act = batch * a.dim * 2 * 4 * a.n_layers  # activations in and out of the launches (small)
+    unique = kv + base * a.n_unique_blocks + lora + emb + act
+    every = kv + base * a.n_layers + lora + emb + act
+    return {"unique": unique, "every_layer": every,
+            "terms": {"kv_cache": kv, "base_unique": base * a.n_unique_blocks, "lora": lora, "embedding": emb,
+                      "activations": act}}
+
+
 def bench_c4(dev):
     from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3, qwen3_0p6b_shared
     args = qwen3_0p6b_shared()
@@ -475,20 +509,88 @@ def bench_c4(dev):
     torch.cuda.synchronize()
     toks, t = model.generate(prompt, 256)
     n_new = 256
+    steps = n_new - 1  # the first new token comes from the prefill
+    step_ms = t["decode_ms"] / steps
+    by = c4_step_bytes(args, batch=8, prompt=512, n_new=n_new)
     res = {"batch": 8, "prompt": 512, "new_tokens": n_new,
            "decode_tok_s": round(8 * n_new / (t["decode_ms"] / 1e3), 1),
            "prefill_ms": round(t["prefill_ms"], 2), "decode_ms": round(t["decode_ms"], 2),
-           "reference_formula_tok_s": round(8 * (512 + n_new) / ((t["prefill_ms"] + t["decode_ms"]) / 1e3), 1)}
+           "ms_per_step": round(step_ms, 4),
+           "reference_formula_tok_s": round(8 * (512 + n_new) / ((t["prefill_ms"] + t["decode_ms"]) / 1e3), 1),
+           "roofline": {"bound": "hbm", "bytes_per_step": round(by["unique"]),
+                        "achieved_GB/s": round(by["unique"] / step_ms / 1e6, 1),
+                        "frac": round(by["unique"] / step_ms / 1e6 / HBM_PEAK_GBS, 4),
+                        "bytes_per_step_every_layer_weights": round(by["every_layer"]),
+                        "frac_every_layer_weights": round(by["every_layer"] / step_ms / 1e6 / HBM_PEAK_GBS, 4),
+                        "terms_MB": {k: round(v / 1e6, 2) for k, v in by["terms"].items()}}}
     del model
     torch.cuda.empty_cache()
     return res
 
 
+def cpu_threads():
+    """Every CPU this process may run on (its affinity set, the box's CPU share), bounded by
+    OMP_NUM_THREADS when the environment sets it."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def bench_c1(dev, steps, warmup):
+    """Config 1 exactly: one LoRA linear, x [2048,1024] ~ N(0,1), W [1024,1024], A [16,1024],
+    B [1024,16] ~ N(0, 0.02^2), alpha 32 / rank 16 = scale 2, all from one seed.
+    CPU: the reference's fp32 arithmetic (F.linear(x,W) + F.linear(F.linear(x,A),B)*s,
+    torchtitan/models/llama3/model/model.py:189-192,392-398) on every available host core,
+    torch.utils.benchmark median. GPU: the fused op on the same values in bf16, HIP-event
+    mean over a graph of 64 launches."""
+    import torch.utils.benchmark as tb
+    from oracle.qwen3_ref import reference_lora_linear
+    from weightshared_torchtitan_amd import lora_linear
+    M, N, K, r = 2048, 1024, 1024, 16
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, K, generator=g)
+    W = torch.randn(N, K, generator=g) * 0.02
+    A = torch.randn(r, K, generator=g) * 0.02
+    B = torch.randn(N, r, generator=g) * 0.02
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    t = tb.Timer("f(x, W, A, B, 2.0)", globals={"f": reference_lora_linear, "x": x, "W": W, "A": A, "B": B},
+                 num_threads=threads)
+    cpu_s = t.blocked_autorange(min_run_time=2.0).median
+    fl = lora_flops(M, N, K, r)
+    xd, Wd, Ad, Bd = (v.to(dev).bfloat16() for v in (x, W, A, B))
+    L = 64
+    graph = graph_of(lambda: [lora_linear(xd, Wd, Ad, Bd, 2.0) for _ in range(L)])
+    gpu_ms = time_replays(graph, steps, warmup) / L
+    del graph
+    return {"shape": "x [2048,1024], W [1024,1024], A [16,1024], B [1024,16], scale 2",
+            "cpu_fp32": {"us": round(cpu_s * 1e6, 1), "TFLOP/s": round(fl / cpu_s / 1e12, 4), "threads": threads,
+                         "cpu_model": cpu_model(), "kind": "reference arithmetic (F.linear x3 + mul + add)"},
+            "mi355x_bf16": {"us": round(gpu_ms * 1e3, 3), "TFLOP/s": round(fl / gpu_ms / 1e9, 1),
+                            "GB/s": round(lora_bytes(M, N, K, r) / gpu_ms / 1e6, 1)}}
+
+
 def cpu_baseline(seconds=10.0):
     """The reference's fp32 CPU arithmetic (F.linear(x,W) + F.linear(F.linear(x,A),B)*s),
-    timed on host cores over a bounded sample of the config-2 projections."""
+    timed on every available host core over a bounded sample of the config-2 projections."""
     from oracle.qwen3_ref import reference_lora_linear
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     M = 8192
@@ -509,6 +611,7 @@ def cpu_baseline(seconds=10.0):
         if el >= seconds and n >= 7:
             break
     return {"value": round(flops / el / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
             "sample": f"{n} config-2 projections (M=8192, hidden 1024, r=32) in fp32, {el:.1f} s"}
 
 
@@ -541,8 +644,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=("c2", "c2single", "c3", "c4", "c5", "emb", "vendor", "backward", "shape"),
-                    default=None)
+    ap.add_argument("--only", choices=("c1", "c2", "c2single", "c2_1p7b", "c3", "c4", "c5", "emb", "vendor",
+                                       "backward", "shape"), default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -561,7 +664,9 @@ def main():
     if args.copy_calibration:
         copy_calibration(dev)
     if args.only is not None and args.only not in ("c2", "c2single"):
-        fn = {"c3": lambda: bench_c3(dev, args.steps, args.warmup),
+        fn = {"c1": lambda: bench_c1(dev, args.steps, args.warmup),
+              "c2_1p7b": lambda: c2_1p7b_extra(dev, args.steps, args.warmup),
+              "c3": lambda: bench_c3(dev, args.steps, args.warmup),
               "c4": lambda: bench_c4(dev),
               "c5": lambda: bench_c5(dev, args.steps, args.warmup),
               "emb": lambda: bench_embedding(dev, args.steps, args.warmup),
@@ -608,12 +713,8 @@ def main():
                                                  "frac_mfma": round(flops / ms_single / 1e9 / BF16_PEAK_TFLOPS, 4),
                                                  "ms_per_step": round(ms_single, 4), "launches": 7 * 28}
     if not args.no_extra and args.only is None:
-        ms17, ms17s = bench_c2_1p7b(dev, args.steps, args.warmup)
-        f17 = 4 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_1P7B)
-        extra["c2_qwen3_1.7b_prefill"] = {"TFLOP/s": round(f17 / ms17 / 1e9, 1),
-                                          "frac_mfma": round(f17 / ms17 / 1e9 / BF16_PEAK_TFLOPS, 4),
-                                          "ms_per_4_layers": round(ms17, 4),
-                                          "grouped_qkv_gateup_TFLOP/s": round(f17 / ms17s / 1e9, 1)}
+        extra["c1_exact"] = bench_c1(dev, args.steps, args.warmup)
+        extra["c2_qwen3_1.7b_prefill"] = c2_1p7b_extra(dev, args.steps, args.warmup)
         extra["c3_qwen3_1.7b_decode"] = bench_c3(dev, args.steps, args.warmup)
         extra["c5_qwen3_8b_fp8_base"] = bench_c5(dev, args.steps, args.warmup)
         extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)

@@ -123,31 +123,6 @@ int wsl_lora_linear_fused_fwd(const void* x, int64_t ldx, const void* norm_w, fl
                               int64_t K, int64_t r, int32_t fuse, void* workspace, size_t workspace_bytes,
                               void* stream);
 
-/* Two dependent fused decode projections in one launch:
- *   y  = bf16(residual + bf16(x . W^T + scale . (x . A^T) . B^T))        (WSL_FUSE_RESIDUAL)
- *   y2 = lora(bf16(rmsnorm(y) . norm_w); w2, a2, b2, scale2)            (fuse2 = WSL_FUSE_RMSNORM,
- *                                                                        optionally | WSL_FUSE_SWIGLU)
- * i.e. the o projection + residual followed by the pre-FFN norm + gate|up (+ SwiGLU), or
- * the down projection + residual followed by the next block's pre-attention norm + q|k|v
- * (qwen3/model/model.py:296-314). The second projection's workgroups load their weights
- * at once and wait inside the launch (bounded) for the first one's y. The result equals
- * the two wsl_lora_linear_fused_fwd calls. y may be residual itself; y2 must not alias
- * y. M <= 64, bf16 operands; shapes the form does not cover return WSL_E_SHAPE. The
- * workspace (size from wsl_lora_linear_chain_workspace_bytes) is zero-filled before its
- * first use and then persistent, as for wsl_lora_linear_fwd. Errors are reported by
- * wsl_last_error(). wsl_lora_linear_chain_supported answers from the sizes alone (1 or
- * 0, taking 16-byte aligned operands). */
-int wsl_lora_linear_chain_supported(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2,
-                                    int32_t fuse2);
-int wsl_lora_linear_chain_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2,
-                                          size_t* bytes);
-int wsl_lora_linear_chain_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* a, int64_t lda,
-                              const void* b, int64_t ldb, float scale, const void* residual, int64_t ldr, void* y,
-                              int64_t ldy, int64_t N, int64_t K, int64_t r, const void* norm_w, float eps,
-                              const void* w2, int64_t ldw2, const void* a2, int64_t lda2, const void* b2,
-                              int64_t ldb2, float scale2, void* y2, int64_t ldy2, int64_t N2, int64_t r2,
-                              int32_t fuse2, int64_t M, void* workspace, size_t workspace_bytes, void* stream);
-
 /* Thread-local description of the last failure of an entry point above ("" if none). */
 const char* wsl_decode_last_error(void);
 

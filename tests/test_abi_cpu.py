@@ -292,45 +292,6 @@ def test_fused_empty_batch_is_a_no_op():
     assert _fused(M=0, x=None, y=None, ws=None, ws_bytes=0) == N.WSL_OK
 
 
-@needs_lib
-@pytest.mark.parametrize("args,ok", [
-    ((8, 1024, 2048, 32, 6144, 64, 3), 1),   # o + residual -> norm + gate|up + SwiGLU
-    ((8, 1024, 3072, 32, 4096, 96, 1), 1),   # down + residual -> norm + q|k|v
-    ((33, 1024, 2048, 32, 2048, 32, 1), 0),  # consumer's norm prologue holds M * K / 8 <= 2048 chunks
-    ((8, 1024, 2048, 32, 6144, 64, 2), 0),   # the consumer takes the norm prologue
-    ((8, 1000, 2048, 32, 2048, 32, 1), 0),   # producer rows in whole 16-row groups
-])
-def test_chain_supported_answers_from_sizes(args, ok):
-    assert N.lib().wsl_lora_linear_chain_supported(*args) == ok
-    assert N.last_error() == ""
-
-
-@needs_lib
-def test_chain_validation_codes():
-    lib = N.lib()
-    ok = dict(x=P, ldx=2048, w=P, ldw=2048, a=P, lda=2048, b=P, ldb=32, scale=2.0, res=P, ldr=1024, y=P,
-              ldy=1024, N=1024, K=2048, r=32, nw=P, eps=1e-6, w2=P, ldw2=1024, a2=P, lda2=1024, b2=P, ldb2=64,
-              scale2=2.0, y2=P, ldy2=3072, N2=6144, r2=64, fuse2=3, M=8, ws=P, wsb=1 << 24)
-
-    def call(**kw):
-        a = dict(ok)
-        a.update(kw)
-        return lib.wsl_lora_linear_chain_fwd(*[a[k] for k in ok], None)
-
-    assert call(fuse2=2) == N.WSL_E_INVALID_ARG
-    assert call(res=None) == N.WSL_E_INVALID_ARG
-    assert call(nw=None) == N.WSL_E_INVALID_ARG
-    assert call(M=65) == N.WSL_E_SHAPE
-    assert call(ldy2=3000) == N.WSL_E_SHAPE
-    assert call(M=33) == N.WSL_E_SHAPE           # beyond the prologue's capacity
-    assert call(wsb=1024) == N.WSL_E_WORKSPACE
-    assert call(ws=P + 64) == N.WSL_E_ALIGN
-    assert call(M=0, x=None, y=None, y2=None, ws=None, wsb=0) == N.WSL_OK
-    sz = ctypes.c_size_t()
-    assert lib.wsl_lora_linear_chain_workspace_bytes(8, 1024, 2048, 32, 6144, 64, ctypes.byref(sz)) == N.WSL_OK
-    assert sz.value >= _header_defines()["WSL_COUNTER_BYTES"]
-
-
 def _grouped(group_n=(64, 64), **kw):
     a = dict(x=P, ldx=64, w=P, ldw=64, w_dtype=0, w_scale=None, a=P, lda=64, b=P, ldb=8,
              scale=2.0, y=P, ldy=128, M=4, K=64, r=8, ws=P, ws_bytes=1 << 24, stream=None)

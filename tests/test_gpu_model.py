@@ -95,23 +95,20 @@ def test_fused_decode_step_matches_oracle_and_unfused(gpu):
     p = {k: v.detach().float().cpu() for k, v in m.named_parameters()}
     g = torch.Generator().manual_seed(8)
     toks = torch.randint(0, a.vocab_size, (2, 11), generator=g)
-    m.decode_chain = True
     plan = m._fusion_plan(2, m._decode_pack())
-    assert plan["on"] and plan["chain"], "the fused and chained launches should cover this configuration"
+    assert plan["on"], "the fused launches should cover this configuration"
     outs = {}
-    for mode in ("chain", "fused", "separate"):
+    for mode in ("fused", "separate"):
         m.decode_fusion = mode != "separate"
-        m.decode_chain = mode == "chain"
         cache = KVCache(a, 2, 16, gpu)
         with torch.no_grad():
             m(toks[:, :10].to(gpu), cache)
             pos = torch.full((), 10, dtype=torch.int64, device=gpu)
             outs[mode] = m.decode_step(toks[:, 10:11].to(gpu), pos, cache)
-    m.decode_fusion, m.decode_chain = True, False
+    m.decode_fusion = True
     ref = Q.reference_forward(p, a, toks)[:, -1]
-    assert rel(outs["chain"], ref) <= LOGIT_TOL
-    assert torch.equal(outs["chain"], outs["fused"])  # the chain changes the hand-off, not the arithmetic
-    assert rel(outs["chain"], outs["separate"].float().cpu()) <= LOGIT_TOL
+    assert rel(outs["fused"], ref) <= LOGIT_TOL
+    assert rel(outs["fused"], outs["separate"].float().cpu()) <= LOGIT_TOL
 
 
 def test_fused_decode_graph_greedy_matches_oracle(gpu):

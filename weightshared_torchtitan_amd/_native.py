@@ -51,9 +51,6 @@ EXPORTED = (
     "wsl_argmax_rows_workspace_bytes",
     "wsl_lora_linear_fused_supported",
     "wsl_lora_linear_fused_fwd",
-    "wsl_lora_linear_chain_supported",
-    "wsl_lora_linear_chain_workspace_bytes",
-    "wsl_lora_linear_chain_fwd",
     "wsl_decode_last_error",
 )
 
@@ -141,19 +138,6 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, _c_i64, _c_vp, _c_i64,                          # residual, ldr, y, ldy
         _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32,        # M, N, K, r, fuse
         _c_vp, ctypes.c_size_t, _c_vp]                         # workspace, bytes, stream
-    lib.wsl_lora_linear_chain_supported.restype = ctypes.c_int
-    lib.wsl_lora_linear_chain_supported.argtypes = [_c_i64] * 6 + [ctypes.c_int32]
-    lib.wsl_lora_linear_chain_workspace_bytes.restype = ctypes.c_int
-    lib.wsl_lora_linear_chain_workspace_bytes.argtypes = [_c_i64] * 6 + [ctypes.POINTER(ctypes.c_size_t)]
-    lib.wsl_lora_linear_chain_fwd.restype = ctypes.c_int
-    lib.wsl_lora_linear_chain_fwd.argtypes = [
-        _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,  # x, ldx, w, ldw, a, lda, b, ldb
-        ctypes.c_float, _c_vp, _c_i64, _c_vp, _c_i64,                # scale, residual, ldr, y, ldy
-        _c_i64, _c_i64, _c_i64,                                      # N, K, r
-        _c_vp, ctypes.c_float, _c_vp, _c_i64, _c_vp, _c_i64,         # norm_w, eps, w2, ldw2, a2, lda2
-        _c_vp, _c_i64, ctypes.c_float, _c_vp, _c_i64,                # b2, ldb2, scale2, y2, ldy2
-        _c_i64, _c_i64, ctypes.c_int32, _c_i64,                      # N2, r2, fuse2, M
-        _c_vp, ctypes.c_size_t, _c_vp]                               # workspace, bytes, stream
     lib.wsl_argmax_rows_fwd.restype = ctypes.c_int
     lib.wsl_argmax_rows_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, ctypes.c_size_t, _c_vp]
     lib.wsl_argmax_rows_workspace_bytes.restype = ctypes.c_size_t

@@ -53,14 +53,27 @@ def _compile(hipcc: str, src: str, verbose: bool) -> str:
     return obj
 
 
-def build_library(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compiles every csrc/*.hip and links libwsl.so. Always rebuilds."""
+def _stale(src: str) -> bool:
+    """Whether src's object is missing or older than src or any header it may include."""
+    obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
+    if not os.path.exists(obj):
+        return True
+    deps = [src] + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")] + \
+           [os.path.join(INCLUDE_DIR, f) for f in os.listdir(INCLUDE_DIR) if f.endswith(".h")]
+    return max(os.path.getmtime(d) for d in deps) > os.path.getmtime(obj)
+
+
+def build_library(verbose: bool = False, jobs: int | None = None, incremental: bool = False) -> str:
+    """Compiles every csrc/*.hip and links libwsl.so. Rebuilds everything unless
+    `incremental`, which recompiles only sources whose object is out of date."""
     hipcc = _hipcc()
     os.makedirs(BUILD_DIR, exist_ok=True)
     srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    todo = [s for s in srcs if _stale(s)] if incremental else srcs
+    jobs = jobs or min(max(len(todo), 1), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(hipcc, s, verbose), srcs))
+        list(ex.map(lambda s: _compile(hipcc, s, verbose), todo))
+    objs = [os.path.join(BUILD_DIR, os.path.basename(s)[:-4] + ".o") for s in srcs]
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
@@ -73,5 +86,5 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> str:
 
 
 if __name__ == "__main__":
-    path = build_library(verbose="-v" in sys.argv)
+    path = build_library(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv)
     print(path)

@@ -118,6 +118,14 @@ __global__ void __launch_bounds__(256) qk_rope_kernel(const uint16_t* __restrict
   const int b = gw / heads, hh = gw % heads;
   const bool is_q = hh < nh;
   const int64_t pos = *posp;
+  if (pos < 0 || pos >= cache_len) {  // no rope row or cache slot: NaN q, nothing written
+    if (is_q) {
+      uint16_t* dst = qout + ((int64_t)b * nh + hh) * HD;
+#pragma unroll
+      for (int c = 0; c < C; ++c) dst[lane + 64 * c] = 0x7fc0;
+    }
+    return;
+  }
   const uint16_t* src = qkv + (int64_t)b * ldq + (int64_t)hh * HD;
   const uint16_t* nw = is_q ? qw : kw;
   float v[C];
@@ -208,7 +216,9 @@ __global__ void __launch_bounds__(AT_T) attention_partial(const uint16_t* __rest
   __shared__ float s_m[AT_G * REP], s_l[AT_G * REP];
   __shared__ float s_acc[AT_G * REP * HD];
   const int pair = blockIdx.x / nchunk, chunk = blockIdx.x % nchunk;
-  const int L = (int)(*posp) + 1;
+  const int64_t pos = *posp;
+  if (pos < 0 || pos >= cache_len) return;  // the combine writes NaN
+  const int L = (int)pos + 1;
   const int t0 = chunk * AT_CH;
   if (t0 >= L) return;  // the combine reads only the chunks below L
   const int b = pair / nkv, kvh = pair % nkv;
@@ -292,14 +302,19 @@ __global__ void __launch_bounds__(AT_T) attention_partial(const uint16_t* __rest
 // partial records of the chunks below L.
 template <int HD, int REP>
 __global__ void __launch_bounds__(1024) attention_combine(const float* __restrict__ part, int nh, int nkv,
-                                                         int nchunk, const int64_t* __restrict__ posp,
+                                                         int cache_len, int nchunk, const int64_t* __restrict__ posp,
                                                          uint16_t* __restrict__ out) {
   const int pair = blockIdx.x;
   const int b = pair / nkv, kvh = pair % nkv;
   const int tid = threadIdx.x;
   if (tid >= REP * HD) return;
   const int h = tid / HD, d = tid % HD;
-  const int L = (int)(*posp) + 1;
+  const int64_t pos = *posp;
+  if (pos < 0 || pos >= cache_len) {  // past the cache: no records were written
+    out[((int64_t)b * nh + kvh * REP + h) * HD + d] = 0x7fc0;
+    return;
+  }
+  const int L = (int)pos + 1;
   const int nc = min(nchunk, (L + AT_CH - 1) / AT_CH);
   const float* rec = part + (int64_t)pair * nchunk * REP * (HD + 2) + h * (HD + 2);
   float mx = -INFINITY;
@@ -500,12 +515,18 @@ __global__ void __launch_bounds__(AT_T) attention_step(const uint16_t* __restric
   __shared__ float s_acc[AT_G * REP * HD];
   __shared__ int s_last;
   const int pair = blockIdx.x / nchunk, chunk = blockIdx.x % nchunk;
-  const int pos = (int)(*posp);
+  const int b = pair / nkv, kvh = pair % nkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t pos64 = *posp;
+  if (pos64 < 0 || pos64 >= cache_len) {  // no rope row or cache slot: NaN out, nothing written
+    if (chunk == 0)
+      for (int q2 = tid; q2 < REP * HD; q2 += AT_T) out[((int64_t)b * nh + kvh * REP) * HD + q2] = 0x7fc0;
+    return;
+  }
+  const int pos = (int)pos64;
   const int L = pos + 1;
   const int t0 = chunk * AT_CH;
   if (t0 >= L) return;  // no position here; the merge counts only the chunks below L
-  const int b = pair / nkv, kvh = pair % nkv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = tid >> 4, l16 = tid & 15;
   const bool owner = (pos / AT_CH) == chunk;
   const float* rc = rope + (int64_t)pos * 2 * HD;
@@ -707,7 +728,8 @@ hipError_t launch_attention_r(int pairs, int nchunk, hipStream_t st, const uint1
                                                                                    nchunk, pos, scale, part);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  attention_combine<16 * EPL, R><<<dim3((unsigned)pairs), dim3(1024), 0, st>>>(part, nh, nkv, nchunk, pos, out);
+  attention_combine<16 * EPL, R><<<dim3((unsigned)pairs), dim3(1024), 0, st>>>(part, nh, nkv, cache_len, nchunk,
+                                                                               pos, out);
   return hipGetLastError();
 }
 

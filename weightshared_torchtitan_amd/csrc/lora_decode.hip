@@ -235,11 +235,6 @@ struct DecodeArgs {
   uint64_t* tpart;    // [gT][kst][T rows per group][M]: ptag << 32 | fp32 partial sum
   uint64_t* ypart;    // [gY][ksy][W rows per group][M]: likewise
   int spin;           // polls of the T counter before the local fallback
-  // chained launches: a producer publishes (tag) per W group once its y rows are out;
-  // a consumer waits for all of them before it reads x (= the producer's y)
-  uint64_t* done;             // producer: [gY] done words
-  const uint64_t* wait_on;    // consumer: the producer's done words
-  int wait_n;                 // consumer: how many
 };
 
 __device__ __forceinline__ void st_agent(float* p, float v) {
@@ -268,10 +263,10 @@ struct NoPrologue {
   __device__ __forceinline__ void operator()() const {}
 };
 
-template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue, class Pre = NoPrologue>
+template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue>
 __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
                                            int kbeg, int kc, int M, char* smem, float* sums,
-                                           const Pro& pro = Pro(), const Pre& pre = Pre()) {
+                                           const Pro& pro = Pro()) {
   using G = Geo<WDT>;
   constexpr int PD = NR == 1 ? 4 : (NR == 2 ? 2 : 1);  // K steps in flight per wave (NR*4*PD = 16 loads)
   constexpr int LPS = NR * 4;           // loads per step
@@ -306,13 +301,8 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
     for (int mb = 0; mb < MB; ++mb) acc[i][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // The x / B fills were issued before the W loads: wait until only the W loads are
-  // outstanding, then for every wave's fills (and LDS writes made before the call). A
-  // `pre` hook (a chained consumer) waits for its input and only then issues the x fill,
-  // after the W loads, so everything is waited for.
-  if constexpr (!std::is_same<Pre, NoPrologue>::value) {
-    pre();
-    wait_vm<0>();
-  } else {
+  // outstanding, then for every wave's fills (and LDS writes made before the call).
+  {
     const int npf = my < PD ? my : PD;
     if (npf == 0) wait_vm<0>();
     else if (npf == 1) wait_vm<LPS>();
@@ -434,9 +424,12 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
         if (q < n) {
           for (int it = 0; (w[u] >> 32) != ptag && it < spin; ++it) w[u] = ld_agent(ps + q);
           const int rl = q / M, m = q % M;
-          v[u] += (w[u] >> 32) == ptag
-                      ? __uint_as_float((uint32_t)w[u])
+          const bool got = (w[u] >> 32) == ptag;
+          v[u] += got ? __uint_as_float((uint32_t)w[u])
                       : direct_partial<WDT>(mat, ldm, min(row0 + rl, nrows - 1), x, ldx, m, sp * kc, kc);
+          // a consumed word is cleared (a zero word matches no tag), so partial words
+          // never outlive their launch and the 31-bit tag cannot wrap onto a stale one
+          if (got) st_agent(ps + q, 0ull);
         }
       }
     }
@@ -476,16 +469,9 @@ __device__ __forceinline__ uint32_t ptag_of(uint64_t tag) { return (uint32_t)((t
 // bound computes T itself from x and A.
 // Eight consecutive elements of the projection input x[m][k..k+8): x itself, or with the
 // RMSNorm prologue bf16(x * rsqrt(ss[m] / K + eps) * w_norm).
-template <bool NORM, bool COH = false>
+template <bool NORM>
 __device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, int m, int k, float (&v)[8]) {
-  u32x4_t xv;
-  if constexpr (COH) {  // x written earlier in this launch (a chained producer's y)
-    const uint64_t* q = reinterpret_cast<const uint64_t*>(p.x + (int64_t)m * p.ldx + k);
-    const uint64_t lo = ld_agent(q), hi = ld_agent(q + 1);
-    xv = u32x4_t{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-  } else {
-    xv = ld_global_16(p.x + (int64_t)m * p.ldx + k);
-  }
+  const u32x4_t xv = ld_global_16(p.x + (int64_t)m * p.ldx + k);
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32((xv[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
   if constexpr (NORM) {
@@ -497,7 +483,7 @@ __device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, in
   }
 }
 
-template <int MC, bool NORM = false, bool COH = false>
+template <int MC, bool NORM = false>
 __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint64_t tag, int* flag,
                                          const float* ss = nullptr, int goff = 0) {
   const int tid = threadIdx.x;
@@ -538,7 +524,7 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
       float acc = 0.f;
       for (int k = 0; k < p.K; k += 8) {
         float xv[8];
-        load_x8<NORM, COH>(p, ss, m, k, xv);
+        load_x8<NORM>(p, ss, m, k, xv);
         const u32x4_t av = ld_global_16(ar + k);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += xv[e] * bf16_bits_to_f32((av[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
@@ -619,48 +605,13 @@ struct NormPrologue {
   }
 };
 
-constexpr int kRolePlain = 0, kRoleProducer = 1, kRoleConsumer = 2;
-
-// A chained consumer's input hook, run by slice_sums after the W loads are issued: wait
-// (each thread on its own words, bounded) until every W group of the producer has
-// published this launch's tag, then
-// stage the raw x rows, read past the L2s (the producer wrote them in this launch, from
-// any XCD), and w_norm for the RMSNorm prologue. Past the bound it goes on (the launch
-// still drains; the result is then not defined).
-struct ConsumerPre {
-  const DecodeArgs* p;
-  char* xs;
-  char* nws;
-  uint64_t tag;
-  int* flag;
-
-  __device__ __forceinline__ void operator()() const {
-    const int tid = threadIdx.x;
-    for (int q = tid; q < p->wait_n; q += DT) {  // each thread spins on its own words (bounded)
-      uint64_t v = ld_agent(p->wait_on + q);
-      for (int it = 0; v != tag && it < p->spin; ++it) v = ld_agent(p->wait_on + q);
-    }
-    __syncthreads();
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    fill_x<false, kAgentCoherent>(xs, p->x, p->ldx, p->M, 0, p->K, wave, lane);
-    fill_x<false>(nws, p->nw, 0, 1, 0, p->K, wave, lane);
-  }
-};
-
 // The work of one workgroup of a decode launch: a T workgroup (bid < gT * kst) or a W
-// workgroup. ROLE adds the chained-launch hand-off: a producer (residual epilogue) writes
-// y with agent-scope stores and then publishes the tag for its W group; a consumer
-// (RMSNorm prologue) takes its x from the producer's y once every group is published.
-template <int WDT, int NR, int MB, int KW, int FUSE, int ROLE>
+// workgroup.
+template <int WDT, int NR, int MB, int KW, int FUSE>
 __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64_t cnt_raw, char* smem) {
   constexpr bool NORM = (FUSE & kFuseNorm) != 0;
   constexpr bool ACT = (FUSE & kFuseAct) != 0;
   constexpr bool RES = (FUSE & kFuseRes) != 0;
-  constexpr bool CONS = ROLE == kRoleConsumer;
-  constexpr bool PROD = ROLE == kRoleProducer;
-  static_assert(!CONS || NORM, "a chained consumer takes the RMSNorm prologue");
-  static_assert(!PROD || (RES && !ACT), "a chained producer is a residual-epilogue launch");
   constexpr int RBK = NWV / KW;         // row blocks per workgroup
   constexpr int ROWS = RBK * 16 * NR;   // W rows per workgroup
   constexpr int TROWS = RBK * 16;       // A rows per T workgroup
@@ -685,12 +636,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     const int kbeg = ks * p.kct;
     constexpr int RED_T = (NWV - RBK) * MB * 4 * 64 * 4;
     float* sums = reinterpret_cast<float*>(smem + RED_T);
-    if constexpr (CONS) {  // the x rows arrive from the producer during the A loads
-      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
-      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums,
-                                   NormPrologue{&p, smem, ss, smem + p.nw_off},
-                                   ConsumerPre{&p, smem, smem + p.nw_off, late_tag(), flag});
-    } else if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
+    if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
@@ -721,13 +667,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     char* bl = smem + (xs_bytes > post ? xs_bytes : post);
     float* sums = reinterpret_cast<float*>(smem + RED);
     uint16_t* tl = reinterpret_cast<uint16_t*>(smem + RED + ROWS * MC * 4);
-    if constexpr (CONS) {  // the x rows arrive from the producer during the W loads
-      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
-      if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
-      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums,
-                                  NormPrologue{&p, smem, ss, smem + p.nw_off},
-                                  ConsumerPre{&p, smem, smem + p.nw_off, late_tag(), flag});
-    } else if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
+    if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
@@ -744,7 +684,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
                                     ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy)) {
       if (p.r > 0) {
         const int goff = ((row0 >= p.ge0) + (row0 >= p.ge1) + (row0 >= p.ge2)) * p.r;
-        gather_t<MC, NORM, CONS>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
+        gather_t<MC, NORM>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
       }
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
       const int l16 = lane & 15, grp = lane >> 4;
@@ -803,21 +743,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
             uint2 pk;
             pk.x = pack_bf16x2(o[0], o[1]);
             pk.y = pack_bf16x2(o[2], o[3]);
-            if constexpr (PROD)  // read later in this launch by the consumer, from any XCD
-              st_agent(reinterpret_cast<uint64_t*>(yr + n0), ((uint64_t)pk.y << 32) | pk.x);
-            else
-              *reinterpret_cast<uint2*>(yr + n0) = pk;
+            *reinterpret_cast<uint2*>(yr + n0) = pk;
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               if (n0 + e < p.N) yr[n0 + e] = f32_to_bf16_bits(o[e]);
           }
         }
-      }
-      if constexpr (PROD) {  // this group's y rows are out: publish the tag
-        wait_vm<0>();
-        __syncthreads();
-        if (tid == 0) st_agent(p.done + g, tag);
       }
     }
   }
@@ -843,24 +775,8 @@ __device__ __forceinline__ void launch_exit(unsigned* cnt, int total_wgs) {
 template <int WDT, int NR, int MB, int KW, int FUSE>
 __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  decode_body<WDT, NR, MB, KW, FUSE, kRolePlain>(p, blockIdx.x, launch_count(p.cnt), smem);
+  decode_body<WDT, NR, MB, KW, FUSE>(p, blockIdx.x, launch_count(p.cnt), smem);
   launch_exit(p.cnt, p.gT * p.kst + p.gY * p.ksy);
-}
-
-// Two dependent decode launches in one grid: the producer (residual epilogue; its
-// workgroups first) and the consumer (RMSNorm prologue, x = the producer's y). The
-// consumer's workgroups issue their weight loads at once and wait for the producer's
-// groups only before they read x. Producers never wait on consumers, and workgroups are
-// dispatched in order, so every wait ends. One launch counter (the producer's) tags both.
-template <int NR, int MB, int FUSE_B>
-__global__ void __launch_bounds__(DT) chain_kernel(DecodeArgs a, DecodeArgs b) {
-  extern __shared__ __attribute__((aligned(1024))) char smem[];
-  const uint64_t cnt_raw = launch_count(a.cnt);
-  const int na = a.gT * a.kst + a.gY * a.ksy;
-  const int bid = blockIdx.x;
-  if (bid < na) decode_body<kBF16, NR, MB, 8, kFuseRes, kRoleProducer>(a, bid, cnt_raw, smem);
-  else decode_body<kBF16, NR, MB, 8, FUSE_B, kRoleConsumer>(b, bid - na, cnt_raw, smem);
-  launch_exit(a.cnt, na + b.gT * b.kst + b.gY * b.ksy);
 }
 
 int wave_k_of(int wdt) { return wdt == kFP8 ? 256 : 128; }
@@ -905,9 +821,9 @@ double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
   return waves * (4.0 + (double)((rows + M) * pl.kcy * 2) / 40e3);
 }
 
-// Which rows-per-group choices a plan may take: every one (plain launches), those the
-// fused kernels are built for (one token block), or none (chained launches: fixed rule).
-enum class Pick { kAll, kFused, kFixed };
+// Which rows-per-group choices a plan may take: every one (plain launches) or those the
+// fused kernels are built for (one token block).
+enum class Pick { kAll, kFused };
 
 // rt: rank rows of the T work (groups * r for a grouped launch; r when negative).
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick pick = Pick::kAll,
@@ -1096,13 +1012,11 @@ bool decode_supported(const LoraArgs& p) {
   return plan_decode(p.M, p.N, p.K, p.r, p.w_dtype).ok;
 }
 
-// Covers the plain, fused and chained launches' plans of the problem.
+// Covers the plain and fused launches' plans of the problem.
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
   const size_t a = plan_decode(M, N, K, r, w_dtype).total;
   const size_t b = plan_decode(M, N, K, r, w_dtype, Pick::kFused).total;
-  const size_t c = plan_decode(M, N, K, r, w_dtype, Pick::kFixed).total;
-  const size_t ab = a > b ? a : b;
-  return ab > c ? ab : c;
+  return a > b ? a : b;
 }
 
 namespace {
@@ -1179,85 +1093,6 @@ bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
     if (f.res == nullptr || (reinterpret_cast<uintptr_t>(f.res) & 7u) != 0 || f.ldr % 4 != 0) return false;
   }
   return true;
-}
-
-// ---------------------------------------------------------------------------- chains
-// Workspace of a chained launch: the counter prefix (kCounterBytes; the producer's counters
-// in its first half, the consumer's in the second), the producer's done words, then the
-// producer's and the consumer's plan data.
-namespace {
-constexpr size_t kChainHalf = kCounterBytes / 2;
-constexpr int kChainDoneMax = 4096;
-constexpr size_t kChainDoneBytes = kChainDoneMax * 8;
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-struct ChainLayout {
-  DecodePlan pa, pb;
-  size_t off_a, off_b, total;
-};
-ChainLayout chain_layout(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2) {
-  ChainLayout c;
-  c.pa = plan_decode(M, N, K, r, kBF16, Pick::kFixed);
-  c.pb = plan_decode(M, N2, N, r2, kBF16, Pick::kFixed);
-  c.off_a = kCounterBytes + kChainDoneBytes;  // plan offsets already skip kCounterBytes
-  c.off_b = align256(c.off_a + (c.pa.total - kCounterBytes));
-  c.total = c.off_b + (c.pb.total - kCounterBytes);
-  return c;
-}
-}  // namespace
-
-size_t decode_chain_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2) {
-  return chain_layout(M, N, K, r, N2, r2).total;
-}
-
-bool decode_chain_supported(const LoraArgs& pa, const FusedArgs& fa, const LoraArgs& pb, const FusedArgs& fb) {
-  if (fa.fuse != kFuseRes || (fb.fuse != kFuseNorm && fb.fuse != (kFuseNorm | kFuseAct))) return false;
-  if (pb.x != pa.y || pb.ldx != pa.ldy || pb.M != pa.M || pb.K != pa.N) return false;
-  if (!decode_fused_supported(pa, fa) || !decode_fused_supported(pb, fb)) return false;
-  if (pa.N % 16 != 0) return false;  // whole 4-element stores in the producer
-  const ChainLayout c = chain_layout(pa.M, pa.N, pa.K, pa.r, pb.N, pb.r);
-  if (c.pa.gY > kChainDoneMax) return false;
-  if (c.pa.mb != c.pb.mb || c.pa.nr != c.pb.nr) return false;
-  return true;
-}
-
-namespace {
-template <int NR, int MB, int FUSE_B>
-hipError_t launch_chain_one(const DecodeArgs& a, const DecodeArgs& b, int grid, size_t smem, hipStream_t st) {
-  const hipError_t e = allow_full_lds<chain_kernel<NR, MB, FUSE_B>>();
-  if (e != hipSuccess) return e;
-  chain_kernel<NR, MB, FUSE_B><<<dim3((unsigned)grid), dim3(DT), smem, st>>>(a, b);
-  return hipGetLastError();
-}
-
-template <int FUSE_B>
-hipError_t launch_chain_fb(const DecodeArgs& a, const DecodeArgs& b, int mb, int nr, int grid, size_t smem,
-                           hipStream_t st) {
-  if (nr == 1 && mb == 1) return launch_chain_one<1, 1, FUSE_B>(a, b, grid, smem, st);
-  if (nr == 1 && mb == 2) return launch_chain_one<1, 2, FUSE_B>(a, b, grid, smem, st);
-  if (nr == 2 && mb == 3) return launch_chain_one<2, 3, FUSE_B>(a, b, grid, smem, st);
-  if (nr == 2 && mb == 4) return launch_chain_one<2, 4, FUSE_B>(a, b, grid, smem, st);
-  return hipErrorInvalidValue;  // chained plans use the fixed rows-per-group rule only
-}
-}  // namespace
-
-hipError_t launch_decode_chain(const LoraArgs& pa, const FusedArgs& fa, const LoraArgs& pb, const FusedArgs& fb) {
-  const ChainLayout c = chain_layout(pa.M, pa.N, pa.K, pa.r, pb.N, pb.r);
-  char* ws = reinterpret_cast<char*>(pa.ws);
-  DecodeArgs a = make_args(pa, c.pa, ws, ws + c.off_a - kCounterBytes);
-  a.res = reinterpret_cast<const uint16_t*>(fa.res); a.ldr = fa.ldr;
-  a.done = reinterpret_cast<uint64_t*>(ws + kCounterBytes);
-  DecodeArgs b = make_args(pb, c.pb, ws + kChainHalf, ws + c.off_b - kCounterBytes);
-  b.nw = reinterpret_cast<const uint16_t*>(fb.nw); b.eps = fb.eps;
-  b.nw_off = (int)c.pb.flag_off + 16 + kNormLds;
-  b.wait_on = a.done;
-  b.wait_n = c.pa.gY;
-  const size_t smem_a = c.pa.smem;
-  const size_t smem_b = c.pb.smem + (size_t)kNormLds + (size_t)pb.K * 2;
-  const size_t smem = smem_a > smem_b ? smem_a : smem_b;
-  if (smem > (size_t)LDS_MAX) return hipErrorInvalidValue;
-  const int grid = c.pa.gT * c.pa.kst + c.pa.gY * c.pa.ksy + c.pb.gT * c.pb.kst + c.pb.gY * c.pb.ksy;
-  if (fb.fuse == kFuseNorm) return launch_chain_fb<kFuseNorm>(a, b, c.pa.mb, c.pa.nr, grid, smem, pa.stream);
-  return launch_chain_fb<kFuseNorm | kFuseAct>(a, b, c.pa.mb, c.pa.nr, grid, smem, pa.stream);
 }
 
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {

@@ -56,34 +56,40 @@ Path choose_path(const wsl::LoraArgs& p) {
   return Path::kGeneric;
 }
 
-// Workspace layout: kCounterBytes of arrival counters (decode path), then the path's
-// scratch. The prefill and generic paths place their scratch after the prefix, so the
-// counters stay zero whichever path a call takes.
-size_t generic_ws(int64_t M, int64_t r) { return wsl::kCounterBytes + (size_t)(M * r * 2); }
-size_t prefill_ws(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
-  return wsl::kCounterBytes + wsl::prefill_workspace_bytes(M, N, K, r, w_dtype);
+// Workspace layout: kCounterBytes holding the decode path's launch counter, then two halves
+// of equal size H (half_of): the decode path's launch-tagged hand-off words live in
+// [kCounterBytes, kCounterBytes + H), the prefill and generic paths' plain scratch (bf16 T,
+// fp32 split partials) in [kCounterBytes + H, kCounterBytes + 2H). Whatever shapes share a
+// workspace, a value left by a prefill or generic call never sits where a decode launch
+// looks for a tagged word, so it can never be taken for one.
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+size_t half_of(size_t bytes) {
+  return bytes <= wsl::kCounterBytes ? 0 : ((bytes - wsl::kCounterBytes) / 2) & ~(size_t)255;
 }
+// Bytes of a workspace whose halves each hold `data` bytes.
+size_t layout_bytes(size_t data) { return wsl::kCounterBytes + 2 * align256(data); }
 
-size_t workspace_for(const wsl::LoraArgs& p) {
-  switch (choose_path(p)) {
-    case Path::kDecode: return wsl::decode_workspace_bytes(p.M, p.N, p.K, p.r, p.w_dtype);
-    case Path::kPrefill: return prefill_ws(p.M, p.N, p.K, p.r, p.w_dtype);
-    case Path::kGeneric: return generic_ws(p.M, p.r);
-    default: return 0;
-  }
+size_t decode_data(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype, int groups = 1) {
+  const size_t t = groups > 1 ? wsl::decode_grouped_workspace_bytes(M, N, K, r, groups, w_dtype)
+                              : wsl::decode_workspace_bytes(M, N, K, r, w_dtype);
+  return t - wsl::kCounterBytes;  // plan offsets start after the counter prefix
+}
+size_t generic_data(int64_t M, int64_t r) { return (size_t)(M * r * 2); }
+size_t prefill_data(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
+  return wsl::prefill_workspace_bytes(M, N, K, r, w_dtype);
 }
 
 // Upper bound over the paths a problem of this size can take (the path also depends on
 // pointer alignment, which the size query does not see).
 size_t workspace_upper_bound(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
-  size_t b = generic_ws(M, r);
-  size_t pf = prefill_ws(M, N, K, r, w_dtype);
+  size_t b = generic_data(M, r);
+  const size_t pf = prefill_data(M, N, K, r, w_dtype);
   if (pf > b) b = pf;
   if (M >= 1 && M <= wsl::kDecodeMaxM) {
-    size_t d = wsl::decode_workspace_bytes(M, N, K, r, w_dtype);
+    const size_t d = decode_data(M, N, K, r, w_dtype);
     if (d > b) b = d;
   }
-  return b;
+  return layout_bytes(b);
 }
 
 int validate_sizes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t w_dtype) {
@@ -164,21 +170,25 @@ wsl::LoraArgs make_args(const void* x, int64_t ldx, const void* w, int64_t ldw, 
 int run_call(wsl::LoraArgs p, void* workspace, size_t workspace_bytes) {
   const Path path = choose_path(p);
   if (path == Path::kNone) return WSL_OK;
-  size_t need = workspace_for(p);
-  if (p.groups > 1)
-    need = path == Path::kDecode ? wsl::decode_grouped_workspace_bytes(p.M, p.N, p.K, p.r, p.groups, p.w_dtype)
-                                 : prefill_ws(p.M, p.N, p.K, p.r * p.groups, p.w_dtype);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  size_t need;
+  switch (path) {
+    case Path::kDecode: need = decode_data(p.M, p.N, p.K, p.r, p.w_dtype, p.groups); break;
+    case Path::kPrefill: need = prefill_data(p.M, p.N, p.K, p.r * p.groups, p.w_dtype); break;
+    default: need = generic_data(p.M, p.r); break;
+  }
+  const size_t half = half_of(workspace_bytes);
+  if (workspace == nullptr || workspace_bytes < layout_bytes(need))
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", layout_bytes(need), workspace_bytes);
   if ((uintptr_t)workspace & 255)
     return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
   const int rc = check_device();
   if (rc != WSL_OK) return rc;
-  p.ws = workspace;
-  p.ws_bytes = workspace_bytes;
-  if (path != Path::kDecode) {
-    p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes;
-    p.ws_bytes = workspace_bytes - wsl::kCounterBytes;
+  if (path == Path::kDecode) {  // plan offsets include the counter prefix
+    p.ws = workspace;
+    p.ws_bytes = wsl::kCounterBytes + half;
+  } else {
+    p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes + half;
+    p.ws_bytes = half;
   }
   hipError_t e;
   switch (path) {
@@ -229,9 +239,9 @@ int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int
   if (rc != WSL_OK) return rc;
   rc = validate_sizes(M, N, K, r, w_dtype);
   if (rc != WSL_OK) return rc;
-  size_t b = prefill_ws(M, N, K, r * n_groups, w_dtype);
+  size_t b = layout_bytes(prefill_data(M, N, K, r * n_groups, w_dtype));
   if (M >= 1 && M <= wsl::kDecodeMaxM) {
-    const size_t d = wsl::decode_grouped_workspace_bytes(M, N, K, r, n_groups, w_dtype);
+    const size_t d = layout_bytes(decode_data(M, N, K, r, w_dtype, n_groups));
     if (d > b) b = d;
   }
   for (int g = 0; g < n_groups; ++g) {
@@ -332,97 +342,14 @@ int wsl_lora_linear_fused_fwd(const void* x, int64_t ldx, const void* norm_w, fl
   const wsl::FusedArgs f{fuse, norm_w, eps, residual, ldr};
   if (!wsl::decode_fused_supported(p, f))
     return fail(WSL_E_SHAPE, "the fused form does not cover this shape or alignment (wsl_lora_linear_fused_supported)");
-  const size_t need = wsl::decode_workspace_bytes(M, N, K, r, WSL_DTYPE_BF16);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  const size_t need = decode_data(M, N, K, r, WSL_DTYPE_BF16);
+  if (workspace == nullptr || workspace_bytes < layout_bytes(need))
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", layout_bytes(need), workspace_bytes);
   if ((uintptr_t)workspace & 255) return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
   rc = check_device();
   if (rc != WSL_OK) return rc;
+  p.ws_bytes = wsl::kCounterBytes + half_of(workspace_bytes);
   const hipError_t e = wsl::launch_decode_fused(p, f);
-  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
-  return WSL_OK;
-}
-
-int wsl_lora_linear_chain_supported(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2,
-                                    int32_t fuse2) {
-  const bool sizes_ok = validate_sizes(M, N, K, r, WSL_DTYPE_BF16) == WSL_OK &&
-                        validate_sizes(M, N2, N, r2, WSL_DTYPE_BF16) == WSL_OK && M >= 1;
-  clear_err();  // a query leaves no error behind
-  if (!sizes_ok || (fuse2 != WSL_FUSE_RMSNORM && fuse2 != (WSL_FUSE_RMSNORM | WSL_FUSE_SWIGLU))) return 0;
-  if ((r > 0 && r % 8 != 0) || (r2 > 0 && r2 % 8 != 0)) return 0;
-  // the sizes alone: 16-byte aligned operands with tight leading dimensions
-  static char kAligned[16] __attribute__((aligned(16))) = {0};
-  static char kY[16] __attribute__((aligned(16))) = {0};
-  wsl::LoraArgs pa;
-  pa.x = kAligned; pa.ldx = K; pa.w = kAligned; pa.ldw = K; pa.w_dtype = WSL_DTYPE_BF16; pa.w_scale = nullptr;
-  pa.a = kAligned; pa.lda = K; pa.b = kAligned; pa.ldb = r; pa.scale = 1.f; pa.y = kY; pa.ldy = N;
-  pa.M = M; pa.N = N; pa.K = K; pa.r = r; pa.ws = nullptr; pa.ws_bytes = 0; pa.stream = nullptr;
-  pa.gather = nullptr; pa.gather_rows = 0;
-  wsl::LoraArgs pb = pa;
-  pb.x = kY; pb.ldx = N; pb.w = kAligned; pb.ldw = N; pb.a = kAligned; pb.lda = N; pb.b = kAligned; pb.ldb = r2;
-  pb.y = kAligned; pb.ldy = (fuse2 & WSL_FUSE_SWIGLU) ? N2 / 2 : N2; pb.N = N2; pb.K = N; pb.r = r2;
-  if (pa.ldy % 4 != 0 || pb.ldy % 4 != 0) return 0;
-  const wsl::FusedArgs fa{WSL_FUSE_RESIDUAL, nullptr, 0.f, kAligned, N};
-  const wsl::FusedArgs fb{fuse2, kAligned, 1e-6f, nullptr, 0};
-  return wsl::decode_chain_supported(pa, fa, pb, fb) ? 1 : 0;
-}
-
-int wsl_lora_linear_chain_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2,
-                                          size_t* bytes) {
-  clear_err();
-  if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
-  int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
-  if (rc != WSL_OK) return rc;
-  rc = validate_sizes(M, N2, N, r2, WSL_DTYPE_BF16);
-  if (rc != WSL_OK) return rc;
-  *bytes = wsl::decode_chain_workspace_bytes(M, N, K, r, N2, r2);
-  return WSL_OK;
-}
-
-int wsl_lora_linear_chain_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* a, int64_t lda,
-                              const void* b, int64_t ldb, float scale, const void* residual, int64_t ldr, void* y,
-                              int64_t ldy, int64_t N, int64_t K, int64_t r, const void* norm_w, float eps,
-                              const void* w2, int64_t ldw2, const void* a2, int64_t lda2, const void* b2,
-                              int64_t ldb2, float scale2, void* y2, int64_t ldy2, int64_t N2, int64_t r2,
-                              int32_t fuse2, int64_t M, void* workspace, size_t workspace_bytes, void* stream) {
-  clear_err();
-  int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
-  if (rc != WSL_OK) return rc;
-  rc = validate_sizes(M, N2, N, r2, WSL_DTYPE_BF16);
-  if (rc != WSL_OK) return rc;
-  if (fuse2 != WSL_FUSE_RMSNORM && fuse2 != (WSL_FUSE_RMSNORM | WSL_FUSE_SWIGLU))
-    return fail(WSL_E_INVALID_ARG, "fuse2 must be WSL_FUSE_RMSNORM, optionally with WSL_FUSE_SWIGLU");
-  if (M == 0) return WSL_OK;
-  if (M > wsl::kDecodeMaxM) return fail(WSL_E_SHAPE, "chained launches are decode-shaped: M <= 64");
-  if (x == nullptr || w == nullptr || y == nullptr || residual == nullptr || norm_w == nullptr ||
-      w2 == nullptr || y2 == nullptr)
-    return fail(WSL_E_INVALID_ARG, "x, w, residual, y, norm_w, w2 and y2 must not be NULL");
-  if ((r > 0 && (a == nullptr || b == nullptr)) || (r2 > 0 && (a2 == nullptr || b2 == nullptr)))
-    return fail(WSL_E_INVALID_ARG, "a rank > 0 needs its a and b");
-  if (ldx < K || ldw < K || ldr < N || ldy < N || ldw2 < N || (r > 0 && (lda < K || ldb < r)) ||
-      (r2 > 0 && (lda2 < N || ldb2 < r2)))
-    return fail(WSL_E_SHAPE, "leading dimension too small");
-  const int64_t ny2 = (fuse2 & WSL_FUSE_SWIGLU) ? N2 / 2 : N2;
-  if (ldy2 < ny2) return fail(WSL_E_SHAPE, "ldy2 too small");
-  wsl::LoraArgs pa;
-  pa.x = x; pa.ldx = ldx; pa.w = w; pa.ldw = ldw; pa.w_dtype = WSL_DTYPE_BF16; pa.w_scale = nullptr;
-  pa.a = a; pa.lda = lda; pa.b = b; pa.ldb = ldb; pa.scale = scale; pa.y = y; pa.ldy = ldy;
-  pa.M = M; pa.N = N; pa.K = K; pa.r = r; pa.ws = workspace; pa.ws_bytes = workspace_bytes;
-  pa.stream = reinterpret_cast<hipStream_t>(stream); pa.gather = nullptr; pa.gather_rows = 0;
-  wsl::LoraArgs pb = pa;
-  pb.x = y; pb.ldx = ldy; pb.w = w2; pb.ldw = ldw2; pb.a = a2; pb.lda = lda2; pb.b = b2; pb.ldb = ldb2;
-  pb.scale = scale2; pb.y = y2; pb.ldy = ldy2; pb.N = N2; pb.K = N; pb.r = r2;
-  const wsl::FusedArgs fa{WSL_FUSE_RESIDUAL, nullptr, 0.f, residual, ldr};
-  const wsl::FusedArgs fb{fuse2, norm_w, eps, nullptr, 0};
-  if (!wsl::decode_chain_supported(pa, fa, pb, fb))
-    return fail(WSL_E_SHAPE, "the chained form does not cover these shapes or alignments");
-  const size_t need = wsl::decode_chain_workspace_bytes(M, N, K, r, N2, r2);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
-  if ((uintptr_t)workspace & 255) return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
-  rc = check_device();
-  if (rc != WSL_OK) return rc;
-  const hipError_t e = wsl::launch_decode_chain(pa, fa, pb, fb);
   if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return WSL_OK;
 }

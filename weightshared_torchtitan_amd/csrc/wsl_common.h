@@ -125,11 +125,6 @@ struct FusedArgs {
 };
 bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f);
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f);
-// Two dependent fused decode launches in one grid: a producer with the residual epilogue
-// and a consumer (RMSNorm prologue, optionally SwiGLU) whose x is the producer's y.
-bool decode_chain_supported(const LoraArgs& pa, const FusedArgs& fa, const LoraArgs& pb, const FusedArgs& fb);
-size_t decode_chain_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int64_t N2, int64_t r2);
-hipError_t launch_decode_chain(const LoraArgs& pa, const FusedArgs& fa, const LoraArgs& pb, const FusedArgs& fb);
 
 hipError_t launch_generic(const LoraArgs& p);
 

@@ -15,6 +15,7 @@ from typing import Optional
 
 import collections
 import ctypes
+import os
 
 import torch
 
@@ -55,6 +56,17 @@ def _check_device(*ts: Optional[torch.Tensor]) -> torch.device:
 
 _WS_MIN_BYTES = 16 << 20
 _workspaces: dict = {}
+# Workspaces that were replaced (grown, or dropped after a failed launch). A HIP graph
+# captured while one of them was current keeps its raw address and writes to it on every
+# replay, so none of them is ever returned to the caching allocator: they stay referenced
+# here until the process ends.
+_retired: list = []
+
+
+def _retire(key) -> None:
+    buf = _workspaces.pop(key, None)
+    if buf is not None:
+        _retired.append(buf)
 
 
 def workspace(dev: torch.device, stream: int, nbytes: int, kind: str = "lora") -> torch.Tensor:
@@ -63,17 +75,19 @@ def workspace(dev: torch.device, stream: int, nbytes: int, kind: str = "lora") -
     libwsl requires its workspaces to be zero-filled before first use (the leading
     counters of the decode kernels) and keeps those counters valid across calls, so one
     zero-filled buffer per stream and kind is reused by every call on that stream; it only
-    grows (a grown buffer starts zeroed again).
+    grows (a grown buffer starts zeroed again). A replaced buffer is kept alive for the
+    life of the process (graphs captured earlier still address it).
     """
     key = (dev.index, stream, kind)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
+        if dev.type == "cuda" and torch.cuda.is_current_stream_capturing():
             # allocated inside a capture, the buffer would come from the graph's private
             # pool and its zero-fill would replay with the graph
             raise RuntimeError(
                 f"libwsl: the {kind!r} workspace would have to grow to {nbytes} bytes during graph "
                 "capture; run the op once eagerly with the same shapes before capturing")
+        _retire(key)
         buf = torch.zeros(max(2 * nbytes, _WS_MIN_BYTES), dtype=torch.uint8, device=dev)
         _workspaces[key] = buf
     return buf
@@ -143,7 +157,7 @@ def lora_linear_op(x: torch.Tensor, w: Optional[torch.Tensor], w_scale: Optional
                 M, N, K, r,
                 ws.data_ptr(), ws.numel(), stream)
         if rc != _native.WSL_OK:
-            _workspaces.pop((dev.index, stream, "lora"), None)  # a failed launch may leave counters mid-update
+            _retire((dev.index, stream, "lora"))  # a failed launch may leave counters mid-update
         _native.check(rc, "wsl_lora_linear_fwd")
     return y.reshape(*lead, N)
 
@@ -300,7 +314,7 @@ def lora_linear_grouped_op(x: torch.Tensor, w: torch.Tensor, w_scale: Optional[t
                 M, K, r, G, gn,
                 ws.data_ptr(), ws.numel(), stream)
         if rc != _native.WSL_OK:
-            _workspaces.pop((dev.index, stream, "lora"), None)
+            _retire((dev.index, stream, "lora"))
         _native.check(rc, "wsl_lora_linear_grouped_fwd")
     return y.reshape(*lead, N)
 
@@ -440,26 +454,78 @@ def _factorized_embedding_fake(ids, emb, proj):
     return emb.new_empty((*ids.shape, proj.shape[0]), dtype=torch.bfloat16)
 
 
+# ------------------------------------------------------------------------------------------
+# Autocast rules. The reference trains under torch.autocast(device, dtype=bf16) on the
+# single-device / DDP path (torchtitan/distributed/utils.py:219-239), where nn.Linear casts
+# its floating inputs to the autocast dtype. The wsl ops compute in bf16 only, so inside an
+# autocast region their activation and weight operands are cast to bf16, whatever the region's
+# dtype; an fp8 base weight keeps its storage type and its fp32 per-channel scale stays fp32.
+# The rules sit on the ops themselves (dispatch key AutocastCUDA, which ROCm's autocast uses),
+# so torch.ops.wsl.* called directly, a compiled graph or the Python wrappers all get them.
+# ------------------------------------------------------------------------------------------
+def autocast_operand(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """bf16 for a floating operand of another type; fp8, bf16 and non-floating tensors and
+    None pass unchanged."""
+    if t is None or not t.is_floating_point() or t.dtype in (torch.bfloat16, _FP8):
+        return t
+    return t.to(torch.bfloat16)
+
+
+_AUTOCAST_KEYS = (torch._C.DispatchKeySet(torch._C.DispatchKey.AutocastCUDA)
+                  | torch._C.DispatchKeySet(torch._C.DispatchKey.AutocastCPU))
+_autocast_lib = torch.library.Library("wsl", "IMPL")
+
+
+def _autocast_lora_linear(_ks, x, w, w_scale, a, b, scale):
+    with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYS):
+        return lora_linear_op(autocast_operand(x), autocast_operand(w), w_scale, autocast_operand(a),
+                              autocast_operand(b), scale)
+
+
+def _autocast_lora_linear_grouped(_ks, x, w, w_scale, a, b, scale, group_n):
+    with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYS):
+        return lora_linear_grouped_op(autocast_operand(x), autocast_operand(w), w_scale, autocast_operand(a),
+                                      autocast_operand(b), scale, group_n)
+
+
+def _autocast_factorized_embedding(_ks, ids, emb, proj):
+    with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYS):
+        return factorized_embedding_op(ids, autocast_operand(emb), autocast_operand(proj))
+
+
+_autocast_lib.impl("lora_linear", _autocast_lora_linear, "AutocastCUDA", with_keyset=True)
+_autocast_lib.impl("lora_linear_grouped", _autocast_lora_linear_grouped, "AutocastCUDA", with_keyset=True)
+_autocast_lib.impl("factorized_embedding", _autocast_factorized_embedding, "AutocastCUDA", with_keyset=True)
+
+
 def lora_linear(x: torch.Tensor, w: Optional[torch.Tensor], a: Optional[torch.Tensor] = None,
                 b: Optional[torch.Tensor] = None, scale: float = 2.0,
                 w_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Fused LoRA linear ``x . w^T + scale * (x . a^T) . b^T``.
-
-    Under ``torch.autocast("cuda", dtype=torch.bfloat16)`` floating inputs are cast to
-    bf16 (an fp8 ``w`` and its fp32 ``w_scale`` are left as they are), mirroring the
-    reference's AMP path (torchtitan/distributed/utils.py:219-239).
-    """
-    if torch.is_autocast_enabled("cuda"):
-        def cast(t):
-            return t.to(torch.bfloat16) if (t is not None and t.is_floating_point()
-                                             and t.dtype not in (torch.bfloat16, _FP8)) else t
-        x, a, b = cast(x), cast(a), cast(b)
-        if w is not None and w.dtype != _FP8:
-            w = cast(w)
+    """Fused LoRA linear ``x . w^T + scale * (x . a^T) . b^T`` (``torch.ops.wsl.lora_linear``;
+    under autocast its operands are cast by the op's autocast rule above)."""
     return lora_linear_op(x, w, w_scale, a, b, float(scale))
 
 
+# When set (or with WSL_CHECK_EMBEDDING_IDS=1 in the environment), factorized_embedding raises
+# IndexError for an id outside [0, vocab), as the reference's nn.Embedding does. Off by default:
+# the check reads the ids' range back to the host (a synchronisation, and impossible inside a
+# graph capture). Unchecked, the kernel turns an out-of-range id into a zero row and never
+# reads outside the table.
+CHECK_EMBEDDING_IDS = os.environ.get("WSL_CHECK_EMBEDDING_IDS", "") not in ("", "0")
+
+
+def check_embedding_ids(ids: torch.Tensor, vocab: int) -> None:
+    """Raises IndexError unless every id is in [0, vocab) (one host read of the ids' range)."""
+    if ids.numel() == 0:
+        return
+    lo, hi = int(ids.min()), int(ids.max())
+    if lo < 0 or hi >= vocab:
+        raise IndexError(f"token id out of range: ids span [{lo}, {hi}] but the vocabulary has {vocab} rows")
+
+
 def factorized_embedding(ids: torch.Tensor, emb: torch.Tensor, proj: torch.Tensor) -> torch.Tensor:
+    if CHECK_EMBEDDING_IDS and not torch.cuda.is_current_stream_capturing():
+        check_embedding_ids(ids, emb.shape[0])
     return factorized_embedding_op(ids, emb, proj)
 
 
@@ -477,6 +543,15 @@ def _bf16_2d(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.stride(-1) != 1 or t.stride(0) % 8 != 0 or t.data_ptr() % 16 != 0:
         t = t.contiguous()
     return t
+
+
+def _check_rope(rope: torch.Tensor, cache_len: int, head_dim: int) -> None:
+    """The RoPE table must cover every cache position: [>= cache_len, 2 * head_dim] (cos
+    then sin). The kernels index row `pos` of it for any pos < cache_len; a position at or
+    past cache_len gives NaN outputs and writes nothing."""
+    if rope.dim() != 2 or rope.shape[1] != 2 * head_dim or rope.shape[0] < cache_len:
+        raise ValueError(f"rope must be [>= {cache_len}, {2 * head_dim}] (cos | sin) to cover the cache; "
+                         f"got {tuple(rope.shape)}")
 
 
 def _rmsnorm_launch(x, weight, eps, residual):
@@ -531,6 +606,7 @@ def qk_norm_rope_op(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.T
     q2 = _bf16_2d(qkv, "qkv")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("k_cache and v_cache must be contiguous [b, n_kv_heads, L, head_dim]")
+    _check_rope(rope, L, hd)
     qw = q_norm_w.to(torch.bfloat16).contiguous()
     kw = k_norm_w.to(torch.bfloat16).contiguous()
     rope = rope.float().contiguous()
@@ -611,7 +687,7 @@ def argmax_rows_op(x: torch.Tensor) -> torch.Tensor:
         rc = lib.wsl_argmax_rows_fwd(x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1], out.data_ptr(),
                                      ws.data_ptr(), ws.numel(), stream)
     if rc != 0:
-        _workspaces.pop((dev.index, stream, "argmax"), None)  # a failed launch may leave keys set
+        _retire((dev.index, stream, "argmax"))  # a failed launch may leave keys set
     _native.check(rc, "wsl_argmax_rows_fwd", decode=True)
     return out.view(x.shape[:-1])
 
@@ -633,6 +709,7 @@ def decode_attention_step_op(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w
     q2 = _bf16_2d(qkv, "qkv")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("k_cache and v_cache must be contiguous [b, n_kv_heads, L, head_dim]")
+    _check_rope(rope, L, hd)
     qw = q_norm_w.to(torch.bfloat16).contiguous()
     kw = k_norm_w.to(torch.bfloat16).contiguous()
     rope = rope.float().contiguous()
@@ -648,7 +725,7 @@ def decode_attention_step_op(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w
             rope.data_ptr(), pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), L, float(scale),
             out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
     if rc != _native.WSL_OK:
-        _workspaces.pop((dev.index, stream, "attention"), None)
+        _retire((dev.index, stream, "attention"))
     _native.check(rc, "wsl_decode_attention_step_fwd", decode=True)
     return out
 
@@ -693,7 +770,7 @@ def lora_linear_fused_op(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: f
             float(scale), _dev_ptr(res), res.stride(0) if res is not None else 0, y.data_ptr(), y.stride(0),
             M, N, K, r, int(fuse), ws.data_ptr(), ws.numel(), stream)
     if rc != _native.WSL_OK:
-        _workspaces.pop((dev.index, stream, "lora"), None)
+        _retire((dev.index, stream, "lora"))
     _native.check(rc, "wsl_lora_linear_fused_fwd")
     return y
 
@@ -703,62 +780,3 @@ def _lora_linear_fused_fake(x, norm_w, eps, w, a, b, scale, residual, fuse):
     M = x.reshape(-1, x.shape[-1]).shape[0]
     ny = w.shape[0] // 2 if fuse & 2 else w.shape[0]
     return x.new_empty((M, ny), dtype=torch.bfloat16)
-
-
-def lora_linear_chain_supported(M: int, N: int, K: int, r: int, N2: int, r2: int, fuse2: int) -> bool:
-    """Whether wsl::lora_linear_chain covers these sizes (16-byte aligned operands)."""
-    return bool(_native.lib().wsl_lora_linear_chain_supported(M, N, K, r, N2, r2, fuse2))
-
-
-def chain_workspace_bytes(M: int, N: int, K: int, r: int, N2: int, r2: int) -> int:
-    out = ctypes.c_size_t()
-    _native.check(_native.lib().wsl_lora_linear_chain_workspace_bytes(M, N, K, r, N2, r2, ctypes.byref(out)),
-                  "wsl_lora_linear_chain_workspace_bytes")
-    return out.value
-
-
-@torch.library.custom_op("wsl::lora_linear_chain", mutates_args=(), device_types="cuda")
-def lora_linear_chain_op(x: torch.Tensor, w: torch.Tensor, a: Optional[torch.Tensor], b: Optional[torch.Tensor],
-                         scale: float, residual: torch.Tensor, norm_w: torch.Tensor, eps: float, w2: torch.Tensor,
-                         a2: Optional[torch.Tensor], b2: Optional[torch.Tensor], scale2: float,
-                         fuse2: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """(y, y2) of two dependent decode projections in one launch (include/wsl_decode.h):
-    y = bf16(residual + bf16(lora(x))) and y2 = lora2(rmsnorm(y) * norm_w) [SwiGLU]."""
-    dev = _check_device(x, w, a, b, residual, norm_w, w2, a2, b2)
-    x2 = _bf16_2d(x, "x")
-    M, K = x2.shape
-    N, N2 = w.shape[0], w2.shape[0]
-    res = _bf16_2d(residual, "residual")
-    nw = norm_w.to(torch.bfloat16).contiguous()
-    w, w2 = _row_major(w, "w"), _row_major(w2, "w2")
-    r = r2 = 0
-    if a is not None:
-        a, b = _row_major(a, "a"), _row_major(b, "b")
-        r = a.shape[0]
-    if a2 is not None:
-        a2, b2 = _row_major(a2, "a2"), _row_major(b2, "b2")
-        r2 = a2.shape[0]
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    ny2 = N2 // 2 if fuse2 & _native.WSL_FUSE_SWIGLU else N2
-    y2 = torch.empty((M, ny2), dtype=torch.bfloat16, device=dev)
-    stream = _stream(dev)
-    ws = workspace(dev, stream, chain_workspace_bytes(M, N, K, r, N2, r2), kind="chain")
-    with torch.cuda.device(dev):
-        rc = _native.lib().wsl_lora_linear_chain_fwd(
-            x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0),
-            _dev_ptr(a), a.stride(0) if a is not None else 0, _dev_ptr(b), b.stride(0) if b is not None else 0,
-            float(scale), res.data_ptr(), res.stride(0), y.data_ptr(), y.stride(0), N, K, r,
-            nw.data_ptr(), float(eps), w2.data_ptr(), w2.stride(0),
-            _dev_ptr(a2), a2.stride(0) if a2 is not None else 0, _dev_ptr(b2), b2.stride(0) if b2 is not None else 0,
-            float(scale2), y2.data_ptr(), y2.stride(0), N2, r2, int(fuse2), M, ws.data_ptr(), ws.numel(), stream)
-    if rc != _native.WSL_OK:
-        _workspaces.pop((dev.index, stream, "chain"), None)
-    _native.check(rc, "wsl_lora_linear_chain_fwd")
-    return y, y2
-
-
-@lora_linear_chain_op.register_fake
-def _lora_linear_chain_fake(x, w, a, b, scale, residual, norm_w, eps, w2, a2, b2, scale2, fuse2):
-    M = x.reshape(-1, x.shape[-1]).shape[0]
-    ny2 = w2.shape[0] // 2 if fuse2 & 2 else w2.shape[0]
-    return (x.new_empty((M, w.shape[0]), dtype=torch.bfloat16), x.new_empty((M, ny2), dtype=torch.bfloat16))

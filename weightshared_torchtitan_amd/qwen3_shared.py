@@ -246,6 +246,8 @@ class SharedQwen3(nn.Module):
         Fills `cache` (positions 0..s-1) when given."""
         a = self.args
         b, s = tokens.shape
+        if s > a.max_seq_len:
+            raise IndexError(f"sequence of {s} tokens exceeds max_seq_len {a.max_seq_len} (the RoPE table)")
         pk = self._decode_pack() if (self.prefill_grouped and not torch.is_grad_enabled()) else None
         h = self.tok_embeddings(tokens)
         rc = self.rope[:s].view(1, s, 1, 2 * a.head_dim)
@@ -369,12 +371,6 @@ class SharedQwen3(nn.Module):
             "head": sup(b, a.embed_rank, a.dim, 0, 1),
         }
         plan["on"] = self.decode_fusion and all(plan.values())
-        csup = ops.lora_linear_chain_supported
-        hd = a.n_heads * a.head_dim
-        plan["chain"] = plan["on"] and self.decode_chain and all((
-            csup(b, a.dim, hd, r, 2 * a.hidden_dim, 2 * r, 3),
-            csup(b, a.dim, a.hidden_dim, r, qkv_n, 3 * r, 1),
-            csup(b, a.dim, a.hidden_dim, r, a.embed_rank, 0, 1)))
         return plan
 
     def _rope32(self) -> torch.Tensor:
@@ -396,54 +392,30 @@ class SharedQwen3(nn.Module):
         return ops.lora_linear(x, w, A, B, sc)
 
     decode_fusion = True  # use the fused decode-step launches where _fusion_plan allows
-    # Chain each residual launch with the normed launch after it (wsl_lora_linear_chain_fwd).
-    # Off by default: measured on MI355X, the in-launch cross-XCD hand-off (~2.5 us poll plus
-    # an agent-coherent x fill) costs as much as the launch boundary it removes.
-    decode_chain = False
 
-    def _decode_step_fused(self, h, pos, cache, pk, rope, chain: bool) -> torch.Tensor:
+    def _decode_step_fused(self, h, pos, cache, pk, rope) -> torch.Tensor:
         """The decode step in fused launches: q|k|v (RMSNorm prologue), the fused attention
         step, o projection (+ residual), gate|up (RMSNorm prologue, SwiGLU epilogue), down
-        projection (+ residual). With `chain`, o + gate|up and down + the next block's q|k|v
-        (the last one: + the head's first factor) each run as one launch, so a layer is
-        three launches."""
+        projection (+ residual); then the head's first factor with the final RMSNorm."""
         a = self.args
         b = h.shape[0]
         sm_scale = a.head_dim ** -0.5
         fl = ops.lora_linear_fused_op
-        ch = ops.lora_linear_chain_op
-        qkv = z = None
         for l in range(a.n_layers):
             blk = self.base_blocks[a.block_of(l)]
             lo = self.layer_loras[l]
-            if qkv is None:
-                A, B, sc = pk["l_qkv"][l]
-                qkv = fl(h, blk.attention_norm.weight, a.norm_eps, pk["w_qkv"][a.block_of(l)], A, B, sc, None, 1)
+            A, B, sc = pk["l_qkv"][l]
+            qkv = fl(h, blk.attention_norm.weight, a.norm_eps, pk["w_qkv"][a.block_of(l)], A, B, sc, None, 1)
             o = ops.decode_attention_step_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight,
                                              a.norm_eps, rope, pos, cache.k[l], cache.v[l], a.n_heads,
                                              a.n_kv_heads, sm_scale)
-            qkv = None
             wo, Ao, Bo, so = blk.base("wo").weight, lo.wo.w_a.weight, lo.wo.w_b.weight, lo.wo.scale
             Ag, Bg, sg = pk["l_gu_il"][l]
-            wgu = pk["w_gu_il"][a.block_of(l)]
-            if chain:
-                h, act = ch(o, wo, Ao, Bo, so, h, blk.ffn_norm.weight, a.norm_eps, wgu, Ag, Bg, sg, 3)
-            else:
-                h = fl(o, None, 0.0, wo, Ao, Bo, so, h, 4)
-                act = fl(h, blk.ffn_norm.weight, a.norm_eps, wgu, Ag, Bg, sg, None, 3)
+            h = fl(o, None, 0.0, wo, Ao, Bo, so, h, 4)
+            act = fl(h, blk.ffn_norm.weight, a.norm_eps, pk["w_gu_il"][a.block_of(l)], Ag, Bg, sg, None, 3)
             w2, A2, B2, s2 = blk.base("w2").weight, lo.w2.w_a.weight, lo.w2.w_b.weight, lo.w2.scale
-            if chain and l + 1 < a.n_layers:
-                nb = self.base_blocks[a.block_of(l + 1)]
-                An, Bn, sn = pk["l_qkv"][l + 1]
-                h, qkv = ch(act, w2, A2, B2, s2, h, nb.attention_norm.weight, a.norm_eps,
-                            pk["w_qkv"][a.block_of(l + 1)], An, Bn, sn, 1)
-            elif chain:
-                h, z = ch(act, w2, A2, B2, s2, h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(),
-                          None, None, 0.0, 1)
-            else:
-                h = fl(act, None, 0.0, w2, A2, B2, s2, h, 4)
-        if z is None:
-            z = fl(h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(), None, None, 0.0, None, 1)
+            h = fl(act, None, 0.0, w2, A2, B2, s2, h, 4)
+        z = fl(h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(), None, None, 0.0, None, 1)
         return ops.lora_linear(z, self.tok_embeddings.emb, None, None, 0.0).view(b, -1)
 
     def decode_step(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
@@ -461,7 +433,7 @@ class SharedQwen3(nn.Module):
         if fused_attn:
             plan = self._fusion_plan(b, pk)
             if plan["on"]:
-                return self._decode_step_fused(h, pos, cache, pk, rope, plan["chain"])
+                return self._decode_step_fused(h, pos, cache, pk, rope)
         sm_scale = a.head_dim ** -0.5
         pending = None
         for l in range(a.n_layers):
@@ -487,11 +459,22 @@ class SharedQwen3(nn.Module):
         return self.tok_embeddings.tied_logits(x).view(b, -1)
 
     @torch.no_grad()
-    def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True):
-        """Greedy decoding with a KV cache. Returns (new tokens [b, n_new], timings dict)."""
+    def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True, return_logits: bool = False):
+        """Greedy decoding with a KV cache. Returns (new tokens [b, n_new], timings dict); with
+        `return_logits` the dict also holds "logits" [b, n_new, vocab], the logits each new
+        token was chosen from (copied out of the step's buffer after every step).
+
+        Positions 0..s + n_new - 2 are embedded (the last new token is not fed back), so
+        s + n_new - 1 may not exceed max_seq_len, the length of the RoPE table; the
+        reference's rope cache lookup raises an IndexError in that case too."""
         b, s = prompt.shape
+        if n_new < 1:
+            raise ValueError("n_new must be >= 1")
+        if s + n_new - 1 > self.args.max_seq_len:
+            raise IndexError(f"prompt {s} + {n_new} new tokens needs {s + n_new - 1} positions; "
+                             f"max_seq_len is {self.args.max_seq_len}")
         dev = prompt.device
-        cache = KVCache(self.args, b, s + n_new, dev)
+        cache = KVCache(self.args, b, s + n_new - 1, dev)  # positions 0 .. s + n_new - 2
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t2 = torch.cuda.Event(enable_timing=True)
@@ -501,6 +484,10 @@ class SharedQwen3(nn.Module):
         t1.record()
         out = torch.empty(b, n_new, dtype=torch.int64, device=dev)
         out[:, 0] = tok[:, 0]
+        logits_out = None
+        if return_logits:
+            logits_out = torch.empty(b, n_new, logits.shape[-1], dtype=logits.dtype, device=dev)
+            logits_out[:, 0] = logits
         pos = torch.full((), s, dtype=torch.int64, device=dev)
         tok_buf = tok.clone()
         if use_graph and n_new > 1:
@@ -519,6 +506,8 @@ class SharedQwen3(nn.Module):
             for i in range(1, n_new):
                 graph.replay()
                 out[:, i] = g_next[:, 0]
+                if logits_out is not None:
+                    logits_out[:, i] = g_logits
                 tok_buf.copy_(g_next)
                 pos.add_(1)
         else:
@@ -526,8 +515,13 @@ class SharedQwen3(nn.Module):
                 logits = self.decode_step(tok_buf, pos, cache)
                 nxt = ops.argmax_rows_op(logits).view(b, 1)
                 out[:, i] = nxt[:, 0]
+                if logits_out is not None:
+                    logits_out[:, i] = logits
                 tok_buf.copy_(nxt)
                 pos.add_(1)
         t2.record()
         t2.synchronize()
-        return out, {"prefill_ms": t0.elapsed_time(t1), "decode_ms": t1.elapsed_time(t2)}
+        res = {"prefill_ms": t0.elapsed_time(t1), "decode_ms": t1.elapsed_time(t2)}
+        if logits_out is not None:
+            res["logits"] = logits_out
+        return out, res
