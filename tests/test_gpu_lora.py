@@ -188,6 +188,31 @@ def test_fp8_base_parity(gpu, M, N, K):
     assert err_dq <= BF16_TOL
 
 
+@pytest.mark.parametrize("M", [16, 4096])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (12288, 4096), (4096, 12288)])  # q/o, gate/up, down at 8B
+def test_fp8_base_parity_c5_shapes(gpu, M, N, K):
+    """Config 5's fp8 projections at their full size (rank 128, scale 1). The kernel runs on
+    all M rows; the float64 oracle checks every row at M = 16 and every 16th row at
+    M = 4096 (rows are independent, so the sample is exact for the rows it covers)."""
+    from weightshared_torchtitan_amd import quantize_fp8_per_channel
+    _say(f"[fp8 c5] M={M} N={N} K={K} r=128 s=1")
+    g = torch.Generator().manual_seed(N + K + M)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    Wf = torch.randn(N, K, generator=g) * 0.02
+    A = (torch.randn(128, K, generator=g) * 0.02).bfloat16()
+    B = (torch.randn(N, 128, generator=g) * 0.02).bfloat16()
+    q, sc = quantize_fp8_per_channel(Wf)
+    y = _run(gpu, x, q, A, B, 1.0, w_scale=sc).float().numpy()
+    rows = np.arange(0, M, 1 if M <= 64 else 16)
+    ref = O.lora_linear(_np(x)[rows], Wf.numpy(), _np(A), _np(B), 1.0)
+    err = O.max_rel_err(y[rows], ref)
+    wdq = O.dequantize_fp8(q.view(torch.uint8).numpy(), sc.numpy())
+    err_dq = O.max_rel_err(y[rows], O.lora_linear(_np(x)[rows], wdq, _np(A), _np(B), 1.0))
+    _say(f"  vs fp32 W: {err:.3e}   vs dequantised W: {err_dq:.3e}")
+    assert err <= FP8_TOL
+    assert err_dq <= BF16_TOL
+
+
 def test_fp8_decode_table_on_gpu(gpu):
     """Every finite e4m3fn code through the kernel's decoder: x = e_k one-hot rows."""
     _say("[fp8 table] K=256 one-hot")

@@ -424,12 +424,9 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
         if (q < n) {
           for (int it = 0; (w[u] >> 32) != ptag && it < spin; ++it) w[u] = ld_agent(ps + q);
           const int rl = q / M, m = q % M;
-          const bool got = (w[u] >> 32) == ptag;
-          v[u] += got ? __uint_as_float((uint32_t)w[u])
+          v[u] += (w[u] >> 32) == ptag
+                      ? __uint_as_float((uint32_t)w[u])
                       : direct_partial<WDT>(mat, ldm, min(row0 + rl, nrows - 1), x, ldx, m, sp * kc, kc);
-          // a consumed word is cleared (a zero word matches no tag), so partial words
-          // never outlive their launch and the 31-bit tag cannot wrap onto a stale one
-          if (got) st_agent(ps + q, 0ull);
         }
       }
     }
