@@ -90,6 +90,30 @@ int wsl_lora_linear_fwd(const void* x, int64_t ldx,
                         void* stream);
 
 /*
+ * wsl_lora_linear_fwd without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It has no counterpart in the reference. Same arguments, results and errors as
+ * wsl_lora_linear_fwd (the same kernels run); the scratch memory lives in a static device
+ * array of WSL_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. A problem whose
+ * scratch need exceeds it returns WSL_E_WORKSPACE before touching a device. Nothing here
+ * allocates or frees memory.
+ *   - The first call on a device sets the array up (its address, a zero fill on `stream`
+ *     and a synchronisation of `stream`); that call may not be under graph capture
+ *     (WSL_E_INVALID_ARG). Later calls may be captured.
+ *   - Every call on a GPU shares that GPU's array: calls that may overlap on one GPU (on
+ *     different streams without ordering between them) race and must not be issued.
+ */
+#define WSL_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)
+int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx,
+                                const void* w, int64_t ldw, int32_t w_dtype, const float* w_scale,
+                                const void* a, int64_t lda,
+                                const void* b, int64_t ldb,
+                                float scale,
+                                void* y, int64_t ldy,
+                                int64_t M, int64_t N, int64_t K, int64_t r,
+                                void* stream);
+
+/*
  * Grouped fused LoRA linear: up to WSL_MAX_GROUPS projections that read the same x, in
  * one call. Group g covers output columns [n_g, n_g + group_n[g]) with
  * n_g = group_n[0] + ... + group_n[g-1], and

@@ -339,3 +339,39 @@ def test_grouped_workspace_covers_pre_pass_and_per_group_calls():
         assert need >= N.workspace_bytes(M, n, K, r, N.WSL_DTYPE_BF16)
     # decode-shaped M: per-group calls
     assert N.grouped_workspace_bytes(8, 2048, 64, gn, 0) >= N.workspace_bytes(8, 2048, 2048, 64, 0)
+
+
+def _noalloc(**kw):
+    a = dict(x=P, ldx=64, w=P, ldw=64, w_dtype=0, w_scale=None, a=P, lda=64, b=P, ldb=8,
+             scale=2.0, y=P, ldy=64, M=4, N=64, K=64, r=8, stream=None)
+    a.update(kw)
+    return N.lib().wsl_lora_linear_fwd_noalloc(a["x"], a["ldx"], a["w"], a["ldw"], a["w_dtype"], a["w_scale"],
+                                               a["a"], a["lda"], a["b"], a["ldb"], a["scale"], a["y"], a["ldy"],
+                                               a["M"], a["N"], a["K"], a["r"], a["stream"])
+
+
+@needs_lib
+@pytest.mark.parametrize("kw,code", [
+    (dict(x=None), N.WSL_E_INVALID_ARG),
+    (dict(w=None, r=0), N.WSL_E_INVALID_ARG),
+    (dict(ldx=63), N.WSL_E_SHAPE),
+    (dict(w_dtype=5), N.WSL_E_DTYPE),
+    (dict(y=P + 1), N.WSL_E_ALIGN),
+    # prefill rank pre-pass whose T alone is 32 MB: twice that (the workspace halves) and the
+    # counter prefix exceed the static scratch, refused before any device is touched
+    (dict(M=65536, N=1024, K=64, r=256, ldx=64, ldw=64, lda=64, ldb=256, ldy=1024), N.WSL_E_WORKSPACE),
+])
+def test_noalloc_validation_codes(kw, code):
+    assert _noalloc(**kw) == code
+    assert N.last_error() != ""
+
+
+@needs_lib
+def test_noalloc_empty_batch_is_a_no_op():
+    assert _noalloc(M=0, x=None, y=None) == N.WSL_OK
+
+
+def test_noalloc_scratch_size_matches_header():
+    assert N.WSL_NOALLOC_SCRATCH_BYTES == 64 * 1024 * 1024
+    text = open(HEADER).read()
+    assert "#define WSL_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)" in text

@@ -30,11 +30,13 @@ WSL_FUSE_RESIDUAL = 4
 WSL_DTYPE_BF16 = 0
 WSL_DTYPE_FP8_E4M3 = 1
 WSL_MAX_RANK = 256
+WSL_NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024
 
 # Every symbol include/wsl_lora.h and include/wsl_decode.h declare.
 EXPORTED = (
     "wsl_lora_linear_workspace_bytes",
     "wsl_lora_linear_fwd",
+    "wsl_lora_linear_fwd_noalloc",
     "wsl_lora_linear_grouped_workspace_bytes",
     "wsl_lora_linear_grouped_fwd",
     "wsl_factorized_embedding_fwd",
@@ -83,6 +85,17 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, _c_i64,                   # y, ldy
         _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
         _c_vp, ctypes.c_size_t,          # workspace, bytes
+        _c_vp,                           # stream
+    ]
+    lib.wsl_lora_linear_fwd_noalloc.restype = ctypes.c_int
+    lib.wsl_lora_linear_fwd_noalloc.argtypes = [
+        _c_vp, _c_i64,                   # x, ldx
+        _c_vp, _c_i64, ctypes.c_int32, _c_vp,  # w, ldw, w_dtype, w_scale
+        _c_vp, _c_i64,                   # a, lda
+        _c_vp, _c_i64,                   # b, ldb
+        ctypes.c_float,                  # scale
+        _c_vp, _c_i64,                   # y, ldy
+        _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
         _c_vp,                           # stream
     ]
     lib.wsl_lora_linear_grouped_workspace_bytes.restype = ctypes.c_int

@@ -47,6 +47,55 @@ int check_device() {
   return WSL_OK;
 }
 
+// ---- scratch of the no-allocation entry point (wsl_lora_linear_fwd_noalloc) ----
+// One array per GPU, held for the life of the process. In host code `scratch` is only a
+// stand-in for the device symbol: its device address comes from hipGetSymbolAddress, once
+// per device with that device current, and only that address is ever passed to kernels.
+static __device__ __align__(256) unsigned char scratch[WSL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+__global__ void __launch_bounds__(256) zero_fill_kernel(uint4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The current device's scratch address, set up on the first call on that device: the
+// symbol's address, then the whole array zero-filled by a kernel on `stream` (the decode
+// path's launch counter must start at zero; stale words elsewhere are then zero, which no
+// launch tag matches) and the stream synchronised, so later calls on any stream see it.
+// That first call must not be under graph capture: a captured fill would replay, and
+// resetting the launch counter on every replay would repeat launch tags.
+int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(WSL_E_DEVICE, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(WSL_E_DEVICE, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cap);
+    if (e != hipSuccess) return fail(WSL_E_LAUNCH, "hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(WSL_E_INVALID_ARG, "the first wsl_lora_linear_fwd_noalloc call on a device sets up its scratch "
+                                     "and may not be captured; call it once outside graph capture first");
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(WSL_E_DEVICE, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    zero_fill_kernel<<<dim3(1024), dim3(256), 0, stream>>>(reinterpret_cast<uint4*>(ptr),
+                                                           (size_t)WSL_NOALLOC_SCRATCH_BYTES / 16);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return fail(WSL_E_LAUNCH, "scratch zero-fill failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return WSL_OK;
+}
+
 enum class Path { kNone, kPrefill, kDecode, kGeneric };
 
 Path choose_path(const wsl::LoraArgs& p) {
@@ -228,6 +277,35 @@ int wsl_lora_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, 
   if (rc != WSL_OK) return rc;
   return run_call(make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r, stream),
                   workspace, workspace_bytes);
+}
+
+int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+                                const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
+                                float scale, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t r,
+                                void* stream) {
+  clear_err();
+  int rc = validate_call(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, y, ldy, M, N, K, r);
+  if (rc != WSL_OK) return rc;
+  const wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r,
+                                    stream);
+  if (choose_path(p) == Path::kNone) return WSL_OK;
+  // the exact need of the path this call takes (sizes and alignment are known here)
+  size_t need;
+  switch (choose_path(p)) {
+    case Path::kDecode: need = layout_bytes(decode_data(M, N, K, r, w_dtype)); break;
+    case Path::kPrefill: need = layout_bytes(prefill_data(M, N, K, r, w_dtype)); break;
+    default: need = layout_bytes(generic_data(M, r)); break;
+  }
+  if (need > (size_t)WSL_NOALLOC_SCRATCH_BYTES)
+    return fail(WSL_E_WORKSPACE, "this problem needs %zu bytes of scratch; the no-allocation entry point holds %zu "
+                                 "(use wsl_lora_linear_fwd with a workspace)", need,
+                (size_t)WSL_NOALLOC_SCRATCH_BYTES);
+  rc = check_device();
+  if (rc != WSL_OK) return rc;
+  void* ws = nullptr;
+  rc = noalloc_scratch(reinterpret_cast<hipStream_t>(stream), &ws);
+  if (rc != WSL_OK) return rc;
+  return run_call(p, ws, (size_t)WSL_NOALLOC_SCRATCH_BYTES);
 }
 
 int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int32_t n_groups,
