@@ -123,6 +123,22 @@ int wsl_lora_linear_fused_fwd(const void* x, int64_t ldx, const void* norm_w, fl
                               int64_t K, int64_t r, int32_t fuse, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* The tied output head fused with greedy sampling: out[m] = argmax_n bf16(x[m] . w[n]) for
+ * x [M, K] and w [N, K] bf16 (the factorized head's second factor: x = h . P, w = E), in one
+ * launch that streams w once and writes no logits. Replaces the head matmul and the
+ * argmax of scripts/generate/_generation.py:19-32 (top_k = 1 keeps only the argmax) over
+ * the tied output (torchtitan/experiments/qwen3/infra/parallelize.py:123-125); the result is
+ * torch.argmax of the bf16 logits the unfused head stores (ties give the first index, NaN
+ * counts as largest). out [M] int64. 1 <= M <= 64, N < 2^32, and a short K (two wave steps
+ * of 128, e.g. the rank-256 factor); wsl_tied_head_argmax_supported answers from the sizes
+ * alone (16-byte aligned operands). The workspace (wsl_tied_head_argmax_workspace_bytes(M)
+ * bytes, 256-byte aligned) is zero-filled before its first use; every completed call
+ * leaves it valid for the next. Errors are reported by wsl_last_error(). */
+size_t wsl_tied_head_argmax_workspace_bytes(int64_t M);
+int wsl_tied_head_argmax_supported(int64_t M, int64_t N, int64_t K);
+int wsl_tied_head_argmax_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t N, int64_t K, int64_t M,
+                             int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Thread-local description of the last failure of an entry point above ("" if none). */
 const char* wsl_decode_last_error(void);
 

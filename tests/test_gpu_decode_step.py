@@ -332,3 +332,84 @@ def test_fused_unsupported_shape_raises(gpu):
     assert not ops.lora_linear_fused_supported(8, 256, 4096, 0, 1)
     with pytest.raises(ValueError):
         ops.lora_linear_fused_op(x, nw, 1e-6, W, None, None, 0.0, None, 1)
+
+
+# ------------------------------------------------------------------ tied head + greedy argmax
+@pytest.mark.parametrize("M", [1, 8, 16, 17, 33, 64])
+def test_tied_head_argmax_equals_argmax_of_logits(gpu, M):
+    """The fused head (no logits written) gives torch.argmax of the bf16 logits the unfused
+    head stores, bit for bit, at the config-4 head shape (vocab 151936, rank 256), over the
+    plans M takes (one, two, three and four token blocks); twice in a row (the keys and the
+    counter return to zero)."""
+    from weightshared_torchtitan_amd import ops
+    _say(f"[head argmax] M={M}")
+    g = torch.Generator(device="cuda").manual_seed(100 + M)
+    V, k = 151936, 256
+    E = (torch.randn(V, k, device=gpu, generator=g) * 0.02).bfloat16()
+    z = torch.randn(M, k, device=gpu, generator=g).bfloat16()
+    assert ops.tied_head_argmax_supported(M, V, k)
+    logits = ops.lora_linear(z, E, None, None, 0.0)  # the unfused head (same kernel sums)
+    want = torch.argmax(logits, dim=-1)
+    for _ in range(2):
+        got = ops.tied_head_argmax_op(z, E)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+    # against the fp32 logits: the chosen logit is within one bf16 rounding of the maximum
+    ref = z.float() @ E.float().t()
+    chosen = ref.gather(1, got[:, None])[:, 0]
+    assert bool((chosen >= ref.max(-1).values - 2 ** -7 * ref.abs().max(-1).values).all())
+
+
+def test_tied_head_argmax_ties_and_nan(gpu):
+    """Ties give the first index and NaN counts as largest (the first NaN wins), as
+    torch.argmax; placed in different workgroups' rows so the cross-workgroup merge decides."""
+    from weightshared_torchtitan_amd import ops
+    _say("[head argmax] ties and NaN")
+    V, k, M = 151936, 256, 3
+    g = torch.Generator(device="cuda").manual_seed(7)
+    E = (torch.randn(V, k, device=gpu, generator=g) * 0.01).bfloat16()
+    z = torch.ones(M, k, device=gpu).bfloat16()
+    z[1] = -z[1]
+    win = torch.full((k,), 0.5, device=gpu).bfloat16()
+    for idx in (90001, 4242, 150000):      # row 0: equal maxima at three rows -> 4242
+        E[idx] = win
+    for idx in (120000, 777):              # row 1 (z negated): the same rows lose; its own tie
+        E[idx] = -win
+    nanrow = E[5].clone()
+    nanrow[3] = float("nan")
+    E[60000] = nanrow                      # every row of z meets a NaN at 60000 and at 140000
+    E[140000] = nanrow
+    got = ops.tied_head_argmax_op(z, E)
+    torch.cuda.synchronize()
+    want = torch.argmax(ops.lora_linear(z, E, None, None, 0.0), dim=-1)
+    assert torch.equal(got, want)
+    assert got.tolist() == [60000, 60000, 60000]
+    E[60000] = E[6]
+    E[140000] = E[7]
+    got = ops.tied_head_argmax_op(z, E)
+    torch.cuda.synchronize()
+    assert got[0].item() == 4242 and got[1].item() == 777
+    assert torch.equal(got, torch.argmax(ops.lora_linear(z, E, None, None, 0.0), dim=-1))
+
+
+def test_tied_head_argmax_in_graph_replays(gpu):
+    from weightshared_torchtitan_amd import ops
+    _say("[head argmax] graph replays")
+    V, k, M = 151936, 256, 8
+    g = torch.Generator(device="cuda").manual_seed(9)
+    E = (torch.randn(V, k, device=gpu, generator=g) * 0.02).bfloat16()
+    z = torch.randn(M, k, device=gpu, generator=g).bfloat16()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.tied_head_argmax_op(z, E)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = ops.tied_head_argmax_op(z, E)
+    for i in range(4):
+        z.copy_(torch.randn(M, k, device=gpu, generator=g).bfloat16())
+        graph.replay()
+        torch.cuda.synchronize()
+        want = torch.argmax(ops.lora_linear(z, E, None, None, 0.0), dim=-1)
+        assert torch.equal(out, want), f"replay {i}"

@@ -133,6 +133,29 @@ def test_fused_decode_graph_greedy_matches_oracle(gpu):
         toks = torch.cat([toks, new[:, i:i + 1]], 1)
 
 
+def test_greedy_tokens_with_and_without_the_fused_head(gpu):
+    """generate() with the head fused into the argmax (no logits written) picks the same tokens
+    as with the unfused head + separate argmax, step for step (the fused config covers it)."""
+    from weightshared_torchtitan_amd.qwen3_shared import SharedQwen3
+    from weightshared_torchtitan_amd import ops
+    a = fused_args()
+    a.embed_rank = 256
+    a.vocab_size = 40000
+    m = SharedQwen3(a)
+    m.init_random(seed=11, std=0.03)
+    m = m.to(gpu).to(torch.bfloat16)
+    assert ops.tied_head_argmax_supported(2, a.vocab_size, a.embed_rank)
+    g = torch.Generator().manual_seed(12)
+    prompt = torch.randint(0, a.vocab_size, (2, 9), generator=g).to(gpu)
+    with torch.no_grad():
+        m.head_argmax_fusion = True
+        fused, _ = m.generate(prompt, 6, use_graph=True)
+        m.head_argmax_fusion = False
+        plain, _ = m.generate(prompt, 6, use_graph=True)
+        m.head_argmax_fusion = True
+    assert torch.equal(fused, plain)
+
+
 @pytest.mark.parametrize("seq", [12, 40, 100])
 def test_grouped_prefill_matches_per_projection(gpu, seq):
     """Inference prefill with q|k|v and gate|up as grouped launches gives the same logits,

@@ -54,6 +54,9 @@ EXPORTED = (
     "wsl_lora_linear_fused_supported",
     "wsl_lora_linear_fused_fwd",
     "wsl_decode_last_error",
+    "wsl_tied_head_argmax_workspace_bytes",
+    "wsl_tied_head_argmax_supported",
+    "wsl_tied_head_argmax_fwd",
 )
 
 _lib = None
@@ -151,6 +154,14 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, _c_i64, _c_vp, _c_i64,                          # residual, ldr, y, ldy
         _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32,        # M, N, K, r, fuse
         _c_vp, ctypes.c_size_t, _c_vp]                         # workspace, bytes, stream
+    lib.wsl_tied_head_argmax_workspace_bytes.restype = ctypes.c_size_t
+    lib.wsl_tied_head_argmax_workspace_bytes.argtypes = [_c_i64]
+    lib.wsl_tied_head_argmax_supported.restype = ctypes.c_int
+    lib.wsl_tied_head_argmax_supported.argtypes = [_c_i64, _c_i64, _c_i64]
+    lib.wsl_tied_head_argmax_fwd.restype = ctypes.c_int
+    lib.wsl_tied_head_argmax_fwd.argtypes = [
+        _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,  # x, ldx, w, ldw, N, K, M
+        _c_vp, _c_vp, ctypes.c_size_t, _c_vp]                  # out, workspace, bytes, stream
     lib.wsl_argmax_rows_fwd.restype = ctypes.c_int
     lib.wsl_argmax_rows_fwd.argtypes = [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, ctypes.c_size_t, _c_vp]
     lib.wsl_argmax_rows_workspace_bytes.restype = ctypes.c_size_t

@@ -426,17 +426,6 @@ constexpr int64_t AMS_CHUNK = 4096;  // elements per workgroup (at least)
 constexpr int AMS_MAXS = 64;         // chunks per row (at most)
 constexpr size_t AMS_ROW = 256;
 
-__device__ __forceinline__ uint64_t am_key(float v, int64_t i) {
-  uint32_t o;
-  if (v != v) {
-    o = 0xffffffffu;
-  } else {
-    const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
-    o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  }
-  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-}
-
 __global__ void __launch_bounds__(AMS_T) argmax_split_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t n,
                                                             int vec, int nsplit, int64_t chunk,
                                                             char* __restrict__ ws, int64_t* __restrict__ out) {
@@ -482,7 +471,7 @@ __global__ void __launch_bounds__(AMS_T) argmax_split_kernel(const uint16_t* __r
     const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (old == (unsigned)(nsplit - 1)) {  // every chunk's key is in
       const uint64_t kv = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      out[row] = (int64_t)(0xffffffffu - (uint32_t)kv);
+      out[row] = am_index(kv);
       __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

@@ -235,6 +235,9 @@ struct DecodeArgs {
   uint64_t* tpart;    // [gT][kst][T rows per group][M]: ptag << 32 | fp32 partial sum
   uint64_t* ypart;    // [gY][ksy][W rows per group][M]: likewise
   int spin;           // polls of the T counter before the local fallback
+  // greedy-token epilogue (kFuseArgmax): per token m the key am_keys[m * kAmStride] (64-bit
+  // atomic max), one arrival counter, the winning index to am_out[m]; LDS scratch at am_red
+  uint64_t* am_keys; unsigned* am_cnt; int64_t* am_out; int am_red; int am_total;
 };
 
 __device__ __forceinline__ void st_agent(float* p, float v) {
@@ -533,7 +536,8 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
 }
 
 constexpr int NORM_CH = 4;  // 16-byte chunks of x per thread in the RMSNorm prologue
-constexpr int kFuseNorm = 1, kFuseAct = 2, kFuseRes = 4;
+constexpr int kFuseNorm = 1, kFuseAct = 2, kFuseRes = 4, kFuseArgmax = 8;
+constexpr int kAmStride = 32;  // uint64 words between two tokens' keys (256 bytes)
 constexpr int kNormLds = 64 * 4 + NORM_CH * DT / 16 * 4;  // row sums + slots
 
 // RMSNorm prologue, run by slice_sums once the direct fills have landed: the raw rows
@@ -601,6 +605,57 @@ struct NormPrologue {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // written before the caller's barrier
   }
 };
+
+// Greedy-token epilogue of a W workgroup: no output is written. Each token's logits over
+// this workgroup's rows are rounded to bf16 (the values the unfused head would store), and
+// the best (value, lowest index) key per token goes into a 64-bit atomic max. The last
+// workgroup to arrive writes each token's index and returns the keys and the counter to
+// zero, so every completed launch leaves them zero.
+template <int ROWS, int MC>
+__device__ __forceinline__ void argmax_epilogue(const DecodeArgs& p, const float* sums, int row0, char* smem) {
+  constexpr int RG = DT / MC;  // row groups
+  const int tid = threadIdx.x;
+  const int tok = tid % MC, rg = tid / MC;
+  uint64_t* red = reinterpret_cast<uint64_t*>(smem + p.am_red);
+  int* last = reinterpret_cast<int*>(red + DT);  // dynamic LDS: the kernel takes the full LDS as dynamic
+  uint64_t best = 0;
+  if (tok < p.M) {
+    for (int rl = rg; rl < ROWS; rl += RG) {
+      const int n = row0 + rl;
+      if (n < p.N) {
+        float v = sums[rl * MC + tok];
+        if (p.w_scale != nullptr) v *= p.w_scale[n];
+        const uint64_t k = am_key(bf16_round(v), n);
+        best = k > best ? k : best;
+      }
+    }
+  }
+  red[rg * MC + tok] = best;
+  __syncthreads();
+  if (tid < p.M) {
+    uint64_t b = 0;
+    for (int q = 0; q < RG; ++q) {
+      const uint64_t v = red[q * MC + tid];
+      b = v > b ? v : b;
+    }
+    if (b != 0) __hip_atomic_fetch_max(p.am_keys + (size_t)tid * kAmStride, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  wait_vm<0>();     // every maximum of this workgroup is performed
+  __syncthreads();  // ... before its arrival
+  if (tid == 0) {
+    const unsigned old = __hip_atomic_fetch_add(p.am_cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    *last = old == (unsigned)(p.am_total - 1);
+  }
+  __syncthreads();
+  if (!*last) return;
+  if (tid < p.M) {
+    uint64_t* key = p.am_keys + (size_t)tid * kAmStride;
+    const uint64_t kv = __hip_atomic_load(key, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    p.am_out[tid] = am_index(kv);
+    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (tid == 0) __hip_atomic_store(p.am_cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The work of one workgroup of a decode launch: a T workgroup (bid < gT * kst) or a W
 // workgroup.
@@ -679,6 +734,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     const uint64_t tag = late_tag();
     if (split_reduce<WDT, ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, ks, p.ksy, p.M,
                                     ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy)) {
+      if constexpr ((FUSE & kFuseArgmax) != 0) {  // the head's greedy token: no logits written
+        argmax_epilogue<ROWS, MC>(p, sums, row0, smem);
+        return;
+      }
       if (p.r > 0) {
         const int goff = ((row0 >= p.ge0) + (row0 >= p.ge1) + (row0 >= p.ge2)) * p.r;
         gather_t<MC, NORM>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
@@ -1090,6 +1149,41 @@ bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
     if (f.res == nullptr || (reinterpret_cast<uintptr_t>(f.res) & 7u) != 0 || f.ldr % 4 != 0) return false;
   }
   return true;
+}
+
+// The greedy-token head (kFuseArgmax): a bf16 table, no adapter, one K slice, and one of the
+// plans a short-K head over many rows takes (K of two wave steps: one or two token blocks
+// with every wave on its own rows, three or four with two waves along K).
+namespace {
+bool argmax_plan_ok(const DecodePlan& pl) {
+  if (!pl.ok || pl.ksy != 1 || pl.gT != 0) return false;
+  if (pl.kw == 1) return (pl.nr == 3 && pl.mb == 1) || (pl.nr == 2 && pl.mb == 2);
+  if (pl.kw == 2) return pl.nr == 2 && (pl.mb == 3 || pl.mb == 4);
+  return false;
+}
+}  // namespace
+
+bool decode_argmax_supported(const LoraArgs& p) {
+  if (p.r != 0 || p.w_dtype != kBF16 || !decode_supported(p)) return false;
+  return argmax_plan_ok(plan_decode(p.M, p.N, p.K, 0, kBF16, Pick::kFused));
+}
+
+hipError_t launch_decode_argmax(const LoraArgs& p, void* keys, int64_t* out) {
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, 0, kBF16, Pick::kFused);
+  if (!argmax_plan_ok(pl)) return hipErrorInvalidValue;
+  DecodeArgs a = make_args(p, pl);
+  a.am_keys = reinterpret_cast<uint64_t*>(keys);
+  a.am_cnt = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(keys) + 128);
+  a.am_out = out;
+  a.am_red = (int)((pl.flag_off + 16 + 7) & ~(size_t)7);
+  a.am_total = pl.gY;
+  const size_t smem = (size_t)a.am_red + (size_t)DT * 8 + 16;
+  if (smem > (size_t)LDS_MAX) return hipErrorInvalidValue;
+  const int grid = pl.gY;
+  if (pl.kw == 1 && pl.nr == 3) return launch_one<kBF16, 3, 1, 1, kFuseArgmax>(a, grid, smem, p.stream);
+  if (pl.kw == 1) return launch_one<kBF16, 2, 2, 1, kFuseArgmax>(a, grid, smem, p.stream);
+  if (pl.mb == 3) return launch_one<kBF16, 2, 3, 2, kFuseArgmax>(a, grid, smem, p.stream);
+  return launch_one<kBF16, 2, 4, 2, kFuseArgmax>(a, grid, smem, p.stream);
 }
 
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {

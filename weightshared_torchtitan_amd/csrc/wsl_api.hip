@@ -432,6 +432,50 @@ int wsl_lora_linear_fused_fwd(const void* x, int64_t ldx, const void* norm_w, fl
   return WSL_OK;
 }
 
+size_t wsl_tied_head_argmax_workspace_bytes(int64_t M) {
+  return wsl::kCounterBytes + (size_t)(M > 1 ? M : 1) * 256;
+}
+
+int wsl_tied_head_argmax_supported(int64_t M, int64_t N, int64_t K) {
+  const bool sizes_ok = validate_sizes(M, N, K, 0, WSL_DTYPE_BF16) == WSL_OK && M >= 1;
+  clear_err();  // a query leaves no error behind
+  if (!sizes_ok) return 0;
+  static char kAligned[16] __attribute__((aligned(16))) = {0};
+  wsl::LoraArgs p = make_args(kAligned, K, kAligned, K, WSL_DTYPE_BF16, nullptr, nullptr, 0, nullptr, 0, 0.f,
+                              kAligned, N + (4 - N % 4) % 4, M, N, K, 0, nullptr);
+  return wsl::decode_argmax_supported(p) ? 1 : 0;
+}
+
+int wsl_tied_head_argmax_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t N, int64_t K,
+                             int64_t M, int64_t* out, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_err();
+  int rc = validate_sizes(M, N, K, 0, WSL_DTYPE_BF16);
+  if (rc != WSL_OK) return rc;
+  if (M == 0) return WSL_OK;
+  if (M > wsl::kDecodeMaxM) return fail(WSL_E_SHAPE, "the fused head is decode-shaped: M <= 64");
+  if (N > ((int64_t)1 << 32) - 1) return fail(WSL_E_SHAPE, "N must be below 2^32 (indices live in 32 bits)");
+  if (x == nullptr || w == nullptr || out == nullptr) return fail(WSL_E_INVALID_ARG, "x, w and out must not be NULL");
+  if (ldx < K || ldw < K) return fail(WSL_E_SHAPE, "leading dimension too small");
+  if (((uintptr_t)x & 1) || ((uintptr_t)w & 1) || ((uintptr_t)out & 7))
+    return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
+  // y is not written; the plan check takes out (8-byte aligned) as a stand-in of a y row
+  wsl::LoraArgs p = make_args(x, ldx, w, ldw, WSL_DTYPE_BF16, nullptr, nullptr, 0, nullptr, 0, 0.f, out,
+                              N + (4 - N % 4) % 4, M, N, K, 0, stream);
+  if (!wsl::decode_argmax_supported(p))
+    return fail(WSL_E_SHAPE, "the fused head does not cover this shape or alignment (wsl_tied_head_argmax_supported)");
+  if (workspace == nullptr || workspace_bytes < wsl_tied_head_argmax_workspace_bytes(M))
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", wsl_tied_head_argmax_workspace_bytes(M),
+                workspace_bytes);
+  if ((uintptr_t)workspace & 255) return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
+  rc = check_device();
+  if (rc != WSL_OK) return rc;
+  p.ws = workspace;
+  p.ws_bytes = wsl::kCounterBytes;
+  const hipError_t e = wsl::launch_decode_argmax(p, reinterpret_cast<char*>(workspace) + wsl::kCounterBytes, out);
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
 int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids, const void* emb, int64_t lde,
                                  int64_t vocab, int64_t k, const void* proj, int64_t ldp,
                                  int64_t hidden, void* out, int64_t ldo, void* stream) {

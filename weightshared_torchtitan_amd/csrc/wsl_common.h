@@ -61,6 +61,24 @@ __device__ __forceinline__ u32x4_t fp8x8_to_bf16x8(uint32_t q0, uint32_t q1) {
                  fp8x2_to_bf16x2<false>(q1), fp8x2_to_bf16x2<true>(q1)};
 }
 
+// Greedy-token key of (value, index): the value's order-preserving bits (NaN above
+// everything, -0 folded into +0) over the complemented index, so the larger key is the
+// larger value and, among equal values, the lower index (torch.argmax's order). Every key
+// of a real value is above zero, so a zero word is "no candidate yet".
+__device__ __forceinline__ uint64_t am_key(float v, int64_t i) {
+  uint32_t o;
+  if (v != v) {
+    o = 0xffffffffu;
+  } else {
+    const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+    o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+}
+
+// The index a key holds.
+__device__ __forceinline__ int64_t am_index(uint64_t k) { return (int64_t)(0xffffffffu - (uint32_t)k); }
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
@@ -125,6 +143,11 @@ struct FusedArgs {
 };
 bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f);
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f);
+// The tied output head fused with the greedy argmax: out[m] = argmax_n bf16(x[m] . W[n]),
+// no logits written. `keys` holds one 256-byte slot per token (64-bit key; the slot of
+// token 0 also holds the arrival counter at byte 128), zero before a launch and after it.
+bool decode_argmax_supported(const LoraArgs& p);
+hipError_t launch_decode_argmax(const LoraArgs& p, void* keys, int64_t* out);
 
 hipError_t launch_generic(const LoraArgs& p);
 

@@ -736,6 +736,42 @@ def _decode_attention_step_fake(qkv, q_norm_w, k_norm_w, eps, rope, pos, k_cache
     return qkv.new_empty((k_cache.shape[0], n_heads * k_cache.shape[3]), dtype=torch.bfloat16)
 
 
+def tied_head_argmax_supported(M: int, N: int, K: int) -> bool:
+    """Whether wsl::tied_head_argmax covers these sizes (16-byte aligned operands)."""
+    return bool(_native.lib().wsl_tied_head_argmax_supported(M, N, K))
+
+
+@torch.library.custom_op("wsl::tied_head_argmax", mutates_args=(), device_types="cuda")
+def tied_head_argmax_op(z: torch.Tensor, emb: torch.Tensor) -> torch.Tensor:
+    """Greedy token of the tied head: argmax over n of bf16(z[m] . emb[n]) for every row of z
+    [M, k] (M <= 64), without writing the [M, vocab] logits (include/wsl_decode.h)."""
+    dev = _check_device(z, emb)
+    z2 = _bf16_2d(z, "z")
+    if emb.dtype != torch.bfloat16:
+        raise TypeError(f"emb must be bfloat16, got {emb.dtype}")
+    emb = _row_major(emb, "emb")
+    M, K = z2.shape
+    V = emb.shape[0]
+    if emb.shape[1] != K:
+        raise ValueError(f"emb {tuple(emb.shape)} does not match z's width {K}")
+    out = torch.empty(M, dtype=torch.int64, device=dev)
+    lib = _native.lib()
+    stream = _stream(dev)
+    ws = workspace(dev, stream, lib.wsl_tied_head_argmax_workspace_bytes(M), kind="head_argmax")
+    with torch.cuda.device(dev):
+        rc = lib.wsl_tied_head_argmax_fwd(z2.data_ptr(), z2.stride(0), emb.data_ptr(), emb.stride(0), V, K, M,
+                                          out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    if rc != _native.WSL_OK:
+        _retire((dev.index, stream, "head_argmax"))  # a failed launch may leave keys set
+    _native.check(rc, "wsl_tied_head_argmax_fwd")
+    return out
+
+
+@tied_head_argmax_op.register_fake
+def _tied_head_argmax_fake(z, emb):
+    return z.new_empty((z.reshape(-1, z.shape[-1]).shape[0],), dtype=torch.int64)
+
+
 def lora_linear_fused_supported(M: int, N: int, K: int, r: int, fuse: int) -> bool:
     """Whether wsl::lora_linear_fused covers these sizes (16-byte aligned operands)."""
     return bool(_native.lib().wsl_lora_linear_fused_supported(M, N, K, r, fuse))

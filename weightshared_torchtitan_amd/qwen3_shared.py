@@ -394,9 +394,10 @@ class SharedQwen3(nn.Module):
     decode_fusion = True  # use the fused decode-step launches where _fusion_plan allows
 
     def _decode_step_fused(self, h, pos, cache, pk, rope) -> torch.Tensor:
-        """The decode step in fused launches: q|k|v (RMSNorm prologue), the fused attention
-        step, o projection (+ residual), gate|up (RMSNorm prologue, SwiGLU epilogue), down
-        projection (+ residual); then the head's first factor with the final RMSNorm."""
+        """The decode step in fused launches up to the head input z = rmsnorm(h) . P [b, k]:
+        q|k|v (RMSNorm prologue), the fused attention step, o projection (+ residual),
+        gate|up (RMSNorm prologue, SwiGLU epilogue), down projection (+ residual); then the
+        head's first factor with the final RMSNorm."""
         a = self.args
         b = h.shape[0]
         sm_scale = a.head_dim ** -0.5
@@ -415,15 +416,15 @@ class SharedQwen3(nn.Module):
             act = fl(h, blk.ffn_norm.weight, a.norm_eps, pk["w_gu_il"][a.block_of(l)], Ag, Bg, sg, None, 3)
             w2, A2, B2, s2 = blk.base("w2").weight, lo.w2.w_a.weight, lo.w2.w_b.weight, lo.w2.scale
             h = fl(act, None, 0.0, w2, A2, B2, s2, h, 4)
-        z = fl(h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(), None, None, 0.0, None, 1)
-        return ops.lora_linear(z, self.tok_embeddings.emb, None, None, 0.0).view(b, -1)
+        return fl(h, self.norm.weight, a.norm_eps, self.tok_embeddings.proj_t(), None, None, 0.0, None, 1)
 
-    def decode_step(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
-        """One greedy step at position `pos` (0-d int64 device tensor) -> logits [b, vocab].
-        Shape-static and host-sync-free, so it can be captured in a HIP graph. Per layer:
-        residual add + RMSNorm, fused q|k|v projection, q/k norm + RoPE + cache write,
-        decode attention, o projection, residual add + RMSNorm, fused gate|up projection,
-        SwiGLU, down projection (its residual add joins the next layer's norm)."""
+    def _decode_z(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        """One decode step at position `pos` (0-d int64 device tensor) up to the head input
+        z = rmsnorm(h) . P [b, k]. Shape-static and host-sync-free, so it can be captured in
+        a HIP graph. Per layer: residual add + RMSNorm, fused q|k|v projection, q/k norm +
+        RoPE + cache write, decode attention, o projection, residual add + RMSNorm, fused
+        gate|up projection, SwiGLU, down projection (its residual add joins the next layer's
+        norm)."""
         a = self.args
         b = token.shape[0]
         pk = self._decode_pack()
@@ -456,7 +457,27 @@ class SharedQwen3(nn.Module):
             gu = self._proj_group(l, "gu", ("w1", "w3"), x, pk)
             pending = self._proj(l, "w2", ops.swiglu_op(gu))
         x, _ = ops.add_rmsnorm_op(pending, h, self.norm.weight, a.norm_eps)
-        return self.tok_embeddings.tied_logits(x).view(b, -1)
+        return ops.lora_linear(x, self.tok_embeddings.proj_t(), None, None, 0.0)
+
+    def decode_step(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        """One step at position `pos` -> logits [b, vocab] (the tied head (h . P) . E^T)."""
+        z = self._decode_z(token, pos, cache)
+        return ops.lora_linear(z, self.tok_embeddings.emb, None, None, 0.0).view(token.shape[0], -1)
+
+    # Greedy steps take the head fused with the argmax (wsl_tied_head_argmax_fwd: E streamed
+    # once, no logits written) where it covers the shape; off, the logits are written and a
+    # separate argmax reads them.
+    head_argmax_fusion = True
+
+    def decode_next(self, token: torch.Tensor, pos: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        """One greedy step at position `pos` -> the next tokens [b] (int64): the argmax of
+        the step's bf16 logits (first index on ties, NaN largest, as torch.argmax; the
+        reference's top_k = 1 sampling, scripts/generate/_generation.py:19-32)."""
+        z = self._decode_z(token, pos, cache)
+        emb = self.tok_embeddings.emb
+        if self.head_argmax_fusion and ops.tied_head_argmax_supported(z.shape[0], emb.shape[0], emb.shape[1]):
+            return ops.tied_head_argmax_op(z, emb)
+        return ops.argmax_rows_op(ops.lora_linear(z, emb, None, None, 0.0))
 
     @torch.no_grad()
     def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True, return_logits: bool = False):
@@ -492,16 +513,21 @@ class SharedQwen3(nn.Module):
         tok_buf = tok.clone()
         if use_graph and n_new > 1:
             # warm up outside the graph (kernel selection, allocator), then capture one step
+            def step():
+                if logits_out is None:
+                    return None, self.decode_next(tok_buf, pos, cache).view(b, 1)
+                lg = self.decode_step(tok_buf, pos, cache)
+                return lg, ops.argmax_rows_op(lg).view(b, 1)
+
             stream = torch.cuda.Stream()
             stream.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(stream):
-                _ = ops.argmax_rows_op(self.decode_step(tok_buf, pos, cache))
+                step()
             torch.cuda.current_stream().wait_stream(stream)
             graph = torch.cuda.CUDAGraph()
             # captured on the warm-up stream: the ops' per-stream workspaces already exist
             with torch.cuda.graph(graph, stream=stream):
-                g_logits = self.decode_step(tok_buf, pos, cache)
-                g_next = ops.argmax_rows_op(g_logits).view(b, 1)
+                g_logits, g_next = step()
             # the warm-up wrote position s; the first replay rewrites it identically
             for i in range(1, n_new):
                 graph.replay()
@@ -512,11 +538,13 @@ class SharedQwen3(nn.Module):
                 pos.add_(1)
         else:
             for i in range(1, n_new):
-                logits = self.decode_step(tok_buf, pos, cache)
-                nxt = ops.argmax_rows_op(logits).view(b, 1)
-                out[:, i] = nxt[:, 0]
-                if logits_out is not None:
+                if logits_out is None:
+                    nxt = self.decode_next(tok_buf, pos, cache).view(b, 1)
+                else:
+                    logits = self.decode_step(tok_buf, pos, cache)
+                    nxt = ops.argmax_rows_op(logits).view(b, 1)
                     logits_out[:, i] = logits
+                out[:, i] = nxt[:, 0]
                 tok_buf.copy_(nxt)
                 pos.add_(1)
         t2.record()
