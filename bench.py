@@ -346,6 +346,45 @@ def bench_c3(dev, steps, warmup):
     return out
 
 
+def bench_c5_paths(dev, steps, warmup):
+    """Config 5 at M = 4096 on each fp8 prefill path, same inputs: the fp8 matrix cores with
+    two activation terms (the default), with one term (the opt-in WSL_DTYPE_FP8_E4M3_ACT8),
+    and W decoded onto the bf16 matrix cores (WSL_FP8_PREFILL=weight_only)."""
+    from weightshared_torchtitan_amd import ops
+    st = ProjectionStack(QWEN3_8B, M=4096, r=128, layers=1, dev=dev, seed=5, copies=1, fp8=True, scale=1.0)
+    st.stack_groups()
+    base = st.layers * sum(2.0 * 4096 * N * K for _, N, K in st.shapes)
+    lora = st.flops() - base
+    t_min = base / (FP8_PEAK_TFLOPS * 1e12) + lora / (BF16_PEAK_TFLOPS * 1e12)
+    out = {}
+    saved = (ops.FP8_ACTIVATIONS, os.environ.get("WSL_FP8_PREFILL"))
+    try:
+        for name, act8, env in (("fp8_mfma_two_term", False, None), ("fp8_mfma_one_term", True, None),
+                                ("weight_only_bf16_mfma", False, "weight_only")):
+            ops.FP8_ACTIVATIONS = act8
+            if env is None:
+                os.environ.pop("WSL_FP8_PREFILL", None)
+            else:
+                os.environ["WSL_FP8_PREFILL"] = env
+            row = {}
+            for label, fn in (("per_projection", st.run), ("grouped_qkv_gateup", st.run_grouped)):
+                g = graph_of(fn)
+                ms = time_replays(g, steps, warmup)
+                del g
+                row[label] = {"ms": round(ms, 4), "TFLOP/s": round(st.flops() / ms / 1e9, 1),
+                              "frac_mixed_mfma_roofline": round(t_min * 1e3 / ms, 4)}
+            out[name] = row
+    finally:
+        ops.FP8_ACTIVATIONS = saved[0]
+        if saved[1] is None:
+            os.environ.pop("WSL_FP8_PREFILL", None)
+        else:
+            os.environ["WSL_FP8_PREFILL"] = saved[1]
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_c5(dev, steps, warmup):
     out = {}
     for M in (16, 4096):
@@ -644,8 +683,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=("c1", "c2", "c2single", "c2_1p7b", "c3", "c4", "c5", "emb", "vendor",
-                                       "backward", "shape"), default=None)
+    ap.add_argument("--only", choices=("c1", "c2", "c2single", "c2_1p7b", "c3", "c4", "c5", "c5paths", "emb",
+                                       "vendor", "backward", "shape"), default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -669,6 +708,7 @@ def main():
               "c3": lambda: bench_c3(dev, args.steps, args.warmup),
               "c4": lambda: bench_c4(dev),
               "c5": lambda: bench_c5(dev, args.steps, args.warmup),
+              "c5paths": lambda: bench_c5_paths(dev, args.steps, args.warmup),
               "emb": lambda: bench_embedding(dev, args.steps, args.warmup),
               "vendor": lambda: bench_vendor(dev, args.steps, args.warmup),
               "backward": lambda: bench_backward(dev, min(args.steps, 10), min(args.warmup, 3)),
@@ -717,6 +757,7 @@ def main():
         extra["c2_qwen3_1.7b_prefill"] = c2_1p7b_extra(dev, args.steps, args.warmup)
         extra["c3_qwen3_1.7b_decode"] = bench_c3(dev, args.steps, args.warmup)
         extra["c5_qwen3_8b_fp8_base"] = bench_c5(dev, args.steps, args.warmup)
+        extra["c5_qwen3_8b_fp8_base"]["M=4096_paths"] = bench_c5_paths(dev, args.steps, args.warmup)
         extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)
         extra["factorized_embedding_c4_prefill"] = bench_embedding(dev, args.steps, args.warmup)
         extra["c2_backward"] = bench_backward(dev, min(args.steps, 10), min(args.warmup, 3))

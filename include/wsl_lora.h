@@ -35,9 +35,19 @@ extern "C" {
 #define WSL_E_DEVICE (-6)      /* no HIP device, or device is not gfx950          */
 #define WSL_E_LAUNCH (-7)      /* a kernel launch failed                          */
 
-/* Storage type of the base weight W. */
+/* Storage type of the base weight W.
+ *   WSL_DTYPE_FP8_E4M3       fp8 W with per-output-channel fp32 scales; the activations keep
+ *                            bf16 precision: on prefill shapes (M > 64) the product runs on
+ *                            the fp8 matrix cores with each activation split into two e4m3
+ *                            terms under a per-token power-of-two scale (x = 2^e (hi + lo/16),
+ *                            exact to 2^-8), on decode shapes W is decoded to bf16.
+ *   WSL_DTYPE_FP8_E4M3_ACT8  the same weight, with the prefill product on one e4m3 term per
+ *                            activation: half the matrix-core work, plus e4m3 rounding of x
+ *                            (about 3.7e-2 against an fp32-W reference at config-5 shapes,
+ *                            against 2.4-2.6e-2 for WSL_DTYPE_FP8_E4M3). Decode shapes as above. */
 #define WSL_DTYPE_BF16 0
 #define WSL_DTYPE_FP8_E4M3 1
+#define WSL_DTYPE_FP8_E4M3_ACT8 2
 
 /* Largest LoRA rank the kernels accept. */
 #define WSL_MAX_RANK 256

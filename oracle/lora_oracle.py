@@ -176,6 +176,56 @@ def dequantize_fp8(q, s):
     return fp8_e4m3_decode(q) * np.asarray(s, np.float64)[:, None]
 
 
+FP8_LO_SHIFT = 4  # the low activation term carries the residual times 2^4
+
+
+def fp8_token_exponent(x):
+    """Per-row power-of-two scale exponent of the fp8 activations: the smallest integer e
+    with max|x[m]| * 2^-e <= 448 (0 for an all-zero row), clamped to [-126, 127].
+
+    The build's own fp8-activation scheme (the reference's fp8 is torchao's dynamic
+    training recipe, torchtitan/components/quantization/float8.py:26-218, absent here).
+    With f = max|x[m]| = mf * 2^ef, mf in [1, 2): e = ef - 8 + (mf > 1.75), since
+    448 = 1.75 * 2^8. Pinned by: brute-force search for the smallest such e on random and
+    edge-case rows (tests/test_fp8_activation_cpu.py).
+    """
+    x = np.asarray(x, np.float64)
+    amax = np.abs(x).max(axis=-1)
+    m, ex = np.frexp(amax)          # amax = m * 2^ex, m in [0.5, 1)
+    e = (ex - 1) - 8 + (2.0 * m > 1.75)
+    e = np.where(amax > 0, e, 0)
+    return np.clip(e, -126, 127).astype(np.int64)
+
+
+def fp8_split_activations(x, terms=2):
+    """Activations x [M, K] (bf16 values) as `terms` e4m3 codes per element and a per-row
+    exponent e: x[m, k] ~= 2^e[m] * (dec(c[0, m, k]) + 2^-4 dec(c[1, m, k])).
+
+    c[0] = e4m3(x * 2^-e) rounded to nearest even; c[1] = e4m3((x * 2^-e - dec(c[0])) * 2^4),
+    the rounding residual one e4m3 step further down. Every step but the two roundings is
+    exact (power-of-two scaling; the residual of a bf16 value against its e4m3 rounding is
+    an fp32 value). With two terms a bf16 value is carried to within 2^-8 of itself, so the
+    fp8 MFMA sees bf16-quality activations.
+    Pinned by: a per-element pure-Python restatement on a tiny case, exact reconstruction
+    of bf16 values, and the error bounds of tests/test_fp8_activation_cpu.py.
+    """
+    x = np.asarray(x, np.float64)
+    e = fp8_token_exponent(x)
+    xs = x * np.exp2(-e.astype(np.float64))[:, None]
+    hi = fp8_e4m3_encode(xs)
+    codes = [hi]
+    if terms >= 2:
+        res = (xs - fp8_e4m3_decode(hi)) * 2.0 ** FP8_LO_SHIFT
+        codes.append(fp8_e4m3_encode(res))
+    return np.stack(codes), e
+
+
+def fp8_activations_value(codes, e):
+    """The activations the fp8 MFMA path multiplies: 2^e * sum_t 2^(-4 t) dec(codes[t])."""
+    v = sum(fp8_e4m3_decode(codes[t]) * 2.0 ** (-FP8_LO_SHIFT * t) for t in range(codes.shape[0]))
+    return v * np.exp2(np.asarray(e, np.float64))[:, None]
+
+
 # ----------------------------------------------------------------------------------------
 # factorized embedding + tied output
 # ----------------------------------------------------------------------------------------

@@ -29,6 +29,7 @@ WSL_FUSE_RESIDUAL = 4
 
 WSL_DTYPE_BF16 = 0
 WSL_DTYPE_FP8_E4M3 = 1
+WSL_DTYPE_FP8_E4M3_ACT8 = 2
 WSL_MAX_RANK = 256
 WSL_NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024
 

@@ -44,6 +44,8 @@
 // Reference arithmetic being fused: torchtitan/models/llama3/model/model.py:189-192
 // (LoRAModule.forward), :392-398 (base projection + broadcast_add with g = 1).
 #include <climits>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "wsl_common.h"
@@ -763,14 +765,57 @@ bool prefill_supported(const LoraArgs& p) {
   return true;
 }
 
-// Workspace of the rank pre-pass (r > RIN): T [M][r] bf16, then, when K is split, the
-// fp32 partials [splits][M][r] at the next 256-byte boundary.
+// Bytes of the rank pre-pass region for M rows of rank rt: T [M][rt] bf16, then, when K is
+// split, the fp32 partials [splits][M][rt] at the next 256-byte boundary.
+size_t rank_prepass_bytes(int64_t M, int64_t K, int64_t rt) {
+  const size_t t_bytes = ((size_t)(M * rt * 2) + 255) & ~(size_t)255;
+  const int splits = rank_splits(M, K, rt);
+  return t_bytes + (splits > 1 ? (size_t)splits * M * rt * 4 : 0);
+}
+
+namespace {
+// Which path an fp8 W takes on prefill shapes: the fp8 matrix cores (activation terms per
+// p.fp8_terms) unless WSL_FP8_PREFILL=weight_only asks for W decoded onto the bf16 matrix
+// cores (kept for side-by-side measurement).
+bool fp8_matrix_cores(const LoraArgs& p) {
+  const char* e = std::getenv("WSL_FP8_PREFILL");  // read per call: a benchmark can switch it
+  const bool weight_only = e != nullptr && std::strcmp(e, "weight_only") == 0;
+  return !weight_only && p.fp8_terms > 0 && prefill_fp8_supported(p);
+}
+}  // namespace
+
+// Workspace of the prefill path: the rank pre-pass region (r > RIN, or any rank on the fp8
+// matrix-core path, which takes T from the pre-pass), then for an fp8 W the activation codes
+// of the fp8 matrix-core path.
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
-  (void)N; (void)w_dtype;
-  if (r <= RIN) return 0;
-  const size_t t_bytes = ((size_t)(M * r * 2) + 255) & ~(size_t)255;
-  const int splits = rank_splits(M, K, r);
-  return t_bytes + (splits > 1 ? (size_t)splits * M * r * 4 : 0);
+  (void)N;
+  if (w_dtype == kFP8)
+    return (r > 0 ? rank_prepass_bytes(M, K, r) : 0) + prefill_fp8_workspace_bytes(M, K, 2);
+  return r > RIN ? rank_prepass_bytes(M, K, r) : 0;
+}
+
+// Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by the prefill kernel run as a
+// plain GEMM with A in the place of W (N = r) and s applied before rounding. With few row
+// tiles (N = r is one or two tiles wide) K is split over grid rows into fp32 partials that
+// a second kernel sums in split order, scales and rounds. A grouped launch runs one pre-pass
+// over all groups' A blocks (N = groups * r).
+hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
+  const int64_t rt = p.r * p.groups;
+  LoraArgs q = p;
+  q.w = p.a; q.ldw = p.lda; q.w_dtype = kBF16; q.w_scale = nullptr;
+  q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0; q.groups = 1;
+  q.N = rt; q.y = t; q.ldy = rt; q.yscale = p.scale;
+  const int splits = rank_splits(p.M, p.K, rt);
+  if (splits > 1) {
+    float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(t) + (((size_t)(p.M * rt * 2) + 255) & ~(size_t)255));
+    q.y = part; q.K = p.K / splits;
+    hipError_t e = launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
+    if (e != hipSuccess) return e;
+    const int64_t slice = p.M * rt;
+    rank_reduce_kernel<<<dim3((unsigned)((slice / 8 + 255) / 256)), dim3(256), 0, p.stream>>>(part, splits, slice, p.scale, t);
+    return hipGetLastError();
+  }
+  return launch_rank<kBF16, true>(q, nullptr, 0);
 }
 
 hipError_t launch_prefill(const LoraArgs& p) {
@@ -779,36 +824,23 @@ hipError_t launch_prefill(const LoraArgs& p) {
     return launch_variant<kBF16, true, 0, false, true>(p, nullptr, 0);
   }
   const bool has_w = p.w != nullptr;
+  const int64_t rt = p.r * p.groups;
+  uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
+  if (has_w && p.w_dtype == kFP8 && fp8_matrix_cores(p)) {
+    if (p.r > 0) {
+      const hipError_t e = rank_prepass(p, t);
+      if (e != hipSuccess) return e;
+    }
+    char* codes = reinterpret_cast<char*>(p.ws) + (p.r > 0 ? rank_prepass_bytes(p.M, p.K, rt) : 0);
+    return launch_prefill_fp8(p, p.r > 0 ? t : nullptr, rt, codes, p.fp8_terms);
+  }
   const uint16_t* tg = nullptr;
   int64_t ldt = 0;
   if (p.r > RIN) {
-    // Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by this same kernel run
-    // as a plain GEMM with A in the place of W (N = r) and s applied before rounding.
-    // With few row tiles (N = r is one or two tiles wide) K is split over grid rows into
-    // fp32 partials that a second kernel sums in split order, scales and rounds. A grouped
-    // launch runs one pre-pass over all groups' A blocks (N = groups * r).
-    const int64_t rt = p.r * p.groups;
-    ldt = rt;
-    uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
-    LoraArgs q = p;
-    q.w = p.a; q.ldw = p.lda; q.w_dtype = kBF16; q.w_scale = nullptr;
-    q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0; q.groups = 1;
-    q.N = rt; q.y = t; q.ldy = ldt; q.yscale = p.scale;
-    const int splits = rank_splits(p.M, p.K, rt);
-    hipError_t e;
-    if (splits > 1) {
-      float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws) + (((size_t)(p.M * rt * 2) + 255) & ~(size_t)255));
-      q.y = part; q.K = p.K / splits;
-      e = launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
-      if (e != hipSuccess) return e;
-      const int64_t slice = p.M * rt;
-      rank_reduce_kernel<<<dim3((unsigned)((slice / 8 + 255) / 256)), dim3(256), 0, p.stream>>>(part, splits, slice, p.scale, t);
-      e = hipGetLastError();
-    } else {
-      e = launch_rank<kBF16, true>(q, nullptr, 0);
-    }
+    const hipError_t e = rank_prepass(p, t);
     if (e != hipSuccess) return e;
     tg = t;
+    ldt = rt;
   }
   if (has_w && p.w_dtype == kFP8) return launch_rank<kFP8, true>(p, tg, ldt);
   if (has_w) return launch_rank<kBF16, true>(p, tg, ldt);

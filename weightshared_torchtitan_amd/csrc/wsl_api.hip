@@ -141,6 +141,17 @@ size_t workspace_upper_bound(int64_t M, int64_t N, int64_t K, int64_t r, int w_d
   return layout_bytes(b);
 }
 
+// The storage type the kernels see and the fp8 activation terms of a public w_dtype code:
+// WSL_DTYPE_FP8_E4M3_ACT8 is an fp8 W whose prefill product takes one activation term.
+int32_t kernel_dtype(int32_t w_dtype, int* terms) {
+  *terms = 2;
+  if (w_dtype == WSL_DTYPE_FP8_E4M3_ACT8) {
+    *terms = 1;
+    return WSL_DTYPE_FP8_E4M3;
+  }
+  return w_dtype;
+}
+
 int validate_sizes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t w_dtype) {
   if (M < 0) return fail(WSL_E_SHAPE, "M must be >= 0 (got %lld)", (long long)M);
   if (N < 1) return fail(WSL_E_SHAPE, "N must be >= 1 (got %lld)", (long long)N);
@@ -257,9 +268,11 @@ int wsl_version(void) { return 100; }
 
 const char* wsl_last_error(void) { return g_err; }
 
-int wsl_lora_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t w_dtype,
+int wsl_lora_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t w_dtype_in,
                                     size_t* bytes) {
   clear_err();
+  int terms;
+  const int32_t w_dtype = kernel_dtype(w_dtype_in, &terms);
   if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
   int rc = validate_sizes(M, N, K, r, w_dtype);
   if (rc != WSL_OK) return rc;
@@ -267,27 +280,33 @@ int wsl_lora_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, 
   return WSL_OK;
 }
 
-int wsl_lora_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+int wsl_lora_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype_in,
                         const float* w_scale, const void* a, int64_t lda, const void* b,
                         int64_t ldb, float scale, void* y, int64_t ldy, int64_t M, int64_t N,
                         int64_t K, int64_t r, void* workspace, size_t workspace_bytes,
                         void* stream) {
   clear_err();
+  int terms;
+  const int32_t w_dtype = kernel_dtype(w_dtype_in, &terms);
   const int rc = validate_call(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, y, ldy, M, N, K, r);
   if (rc != WSL_OK) return rc;
-  return run_call(make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r, stream),
-                  workspace, workspace_bytes);
+  wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r, stream);
+  p.fp8_terms = terms;
+  return run_call(p, workspace, workspace_bytes);
 }
 
-int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype_in,
                                 const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
                                 float scale, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t r,
                                 void* stream) {
   clear_err();
+  int terms;
+  const int32_t w_dtype = kernel_dtype(w_dtype_in, &terms);
   int rc = validate_call(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, y, ldy, M, N, K, r);
   if (rc != WSL_OK) return rc;
-  const wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r,
-                                    stream);
+  wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r,
+                              stream);
+  p.fp8_terms = terms;
   if (choose_path(p) == Path::kNone) return WSL_OK;
   // the exact need of the path this call takes (sizes and alignment are known here)
   size_t need;
@@ -309,8 +328,10 @@ int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx, const void* w, int64
 }
 
 int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int32_t n_groups,
-                                            const int64_t* group_n, int32_t w_dtype, size_t* bytes) {
+                                            const int64_t* group_n, int32_t w_dtype_in, size_t* bytes) {
   clear_err();
+  int terms;
+  const int32_t w_dtype = kernel_dtype(w_dtype_in, &terms);
   if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
   int64_t N = 0;
   int rc = validate_groups(n_groups, group_n, &N);
@@ -330,18 +351,21 @@ int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int
   return WSL_OK;
 }
 
-int wsl_lora_linear_grouped_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype,
+int wsl_lora_linear_grouped_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype_in,
                                 const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
                                 float scale, void* y, int64_t ldy, int64_t M, int64_t K, int64_t r,
                                 int32_t n_groups, const int64_t* group_n, void* workspace,
                                 size_t workspace_bytes, void* stream) {
   clear_err();
+  int terms;
+  const int32_t w_dtype = kernel_dtype(w_dtype_in, &terms);
   int64_t N = 0;
   int rc = validate_groups(n_groups, group_n, &N);
   if (rc != WSL_OK) return rc;
   rc = validate_call(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, y, ldy, M, N, K, r);
   if (rc != WSL_OK) return rc;
   wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r, stream);
+  p.fp8_terms = terms;
   p.groups = n_groups;
   int64_t end = 0;
   for (int g = 0; g < n_groups; ++g) p.gend[g] = (end += group_n[g]);

@@ -120,6 +120,9 @@ struct LoraArgs {
   // of a; w, w_scale, b and y are indexed by the output column as usual.
   int groups = 1;
   int64_t gend[kMaxGroups] = {0, 0, 0, 0};
+  // fp8 W on prefill shapes: activation terms of the fp8 matrix-core path (2: bf16-quality
+  // activations, 1: one e4m3 term); 0 decodes W to bf16 on the bf16 matrix cores instead.
+  int fp8_terms = 2;
 };
 
 // Each launcher returns hipSuccess or the launch error.
@@ -127,6 +130,12 @@ hipError_t launch_prefill(const LoraArgs& p);
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool prefill_supported(const LoraArgs& p);
 bool prefill_groups_supported(const LoraArgs& p);
+
+// fp8 matrix-core prefill path (csrc/lora_prefill_fp8.hip): T from the rank pre-pass, the
+// activation codes and per-token scales in `scratch` (prefill_fp8_workspace_bytes).
+bool prefill_fp8_supported(const LoraArgs& p);
+size_t prefill_fp8_workspace_bytes(int64_t M, int64_t K, int terms);
+hipError_t launch_prefill_fp8(const LoraArgs& p, const uint16_t* tg, int64_t ldt, void* scratch, int terms);
 
 hipError_t launch_decode(const LoraArgs& p);
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);

@@ -23,6 +23,17 @@ from . import _native
 
 _FP8 = torch.float8_e4m3fn
 
+# fp8 base weights: on prefill shapes the product runs on the fp8 matrix cores with bf16-quality
+# activations (two e4m3 terms per element). When set (or with WSL_FP8_ACTIVATIONS=1), one
+# e4m3 term per activation instead (WSL_DTYPE_FP8_E4M3_ACT8): half the matrix-core work, and
+# an error of about 3.7e-2 against the fp32-weight reference at config-5 shapes, above the
+# 3e-2 bar the default keeps (2.4-2.6e-2).
+FP8_ACTIVATIONS = os.environ.get("WSL_FP8_ACTIVATIONS", "") not in ("", "0")
+
+
+def _fp8_code() -> int:
+    return _native.WSL_DTYPE_FP8_E4M3_ACT8 if FP8_ACTIVATIONS else _native.WSL_DTYPE_FP8_E4M3
+
 
 def _dev_ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
@@ -120,7 +131,7 @@ def lora_linear_op(x: torch.Tensor, w: Optional[torch.Tensor], w_scale: Optional
         if w.shape[1] != K:
             raise ValueError(f"w is {tuple(w.shape)} but x has K={K}")
         if w.dtype == _FP8:
-            w_dtype = _native.WSL_DTYPE_FP8_E4M3
+            w_dtype = _fp8_code()
             if w_scale is None:
                 raise ValueError("an fp8 w needs w_scale [N] fp32")
             if w_scale.dtype != torch.float32 or w_scale.shape != (N,):
@@ -277,7 +288,7 @@ def lora_linear_grouped_op(x: torch.Tensor, w: torch.Tensor, w_scale: Optional[t
         raise ValueError(f"w is {tuple(w.shape)}, expected ({N}, {K}) for groups {group_n}")
     w_dtype = _native.WSL_DTYPE_BF16
     if w.dtype == _FP8:
-        w_dtype = _native.WSL_DTYPE_FP8_E4M3
+        w_dtype = _fp8_code()
         if w_scale is None or w_scale.dtype != torch.float32 or w_scale.shape != (N,):
             raise ValueError(f"an fp8 w needs w_scale fp32 [{N}]")
         w_scale = w_scale.contiguous()
