@@ -160,6 +160,37 @@ int wsl_lora_linear_grouped_fwd(const void* x, int64_t ldx,
                                 void* stream);
 
 /*
+ * Shared-base LoRA linears: one base weight W [base_n, K] serving n_groups projections, each
+ * with its own LoRA factors, and optionally shared across head groups:
+ *
+ *   y[:, j N : (j + 1) N] = broadcast_add(x . W^T (* w_scale), scale * (x . A_j^T) . B_j^T, g)
+ *
+ * with broadcast_add as the reference's (torchtitan/models/llama3/model/model.py:111-145):
+ * output column c of a group reads base column (c / (hpg D')) D' + c % D', D' = base_n / g,
+ * hpg = N / base_n. Replaces the reference's attention compositions
+ *   head_sharing: xq = broadcast_add(wq_base(x), wq_offset(x), g = grouping)  (model.py:255-273,
+ *                 396-398; base_n = grouping * head_dim < N), and
+ *   qkv_sharing:  one base module for q, k and v, val = base(x) added to each projection's
+ *                 offset (model.py:239-253, 381-398; n_groups = 3, base_n = N),
+ * in one launch that never materialises the expanded base: every kernel reads W rows through
+ * the column map. a [n_groups * r, K] (A_j = rows j r .. j r + r - 1), b [n_groups * N, r],
+ * y [M, n_groups * N] columns, w_scale [base_n] (fp8 W). N % base_n == 0, base_n % g == 0,
+ * 1 <= n_groups <= WSL_MAX_GROUPS. Workspace from wsl_lora_linear_bcast_workspace_bytes.
+ */
+int wsl_lora_linear_bcast_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t n_groups,
+                                          int32_t w_dtype, size_t* bytes);
+int wsl_lora_linear_bcast_fwd(const void* x, int64_t ldx,
+                              const void* w, int64_t ldw, int32_t w_dtype, const float* w_scale,
+                              const void* a, int64_t lda,
+                              const void* b, int64_t ldb,
+                              float scale,
+                              void* y, int64_t ldy,
+                              int64_t M, int64_t N, int64_t K, int64_t r,
+                              int64_t base_n, int64_t g, int32_t n_groups,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/*
  * Factorized embedding:  out[t, :] = E[ids[t], :] . P^T      (k -> hidden)
  *
  * Replaces the reference's token embedding nn.Embedding(vocab, dim)

@@ -35,3 +35,55 @@ class RefAttentionProjections(nn.Module):
         q = broadcast_add(self.wq_base(x), self.wq_offset(x), g=1)
         k = broadcast_add(self.wk_base(x), self.wk_offset(x), g=self.g)
         return self.wo(q), k
+
+
+class RefSharedAttention(nn.Module):
+    """The projection part of the reference's Attention with its sharing switches: base widths
+    as its constructor sets them (torchtitan/models/llama3/model/model.py:218-273: one base per
+    qkv_sharing group named str(group), GQA off under qkv_sharing; g = grouping templates under
+    head_sharing; k/v bases g / n_rep templates wide) and the composition of its forward
+    (:376-398: every projection is broadcast_add(base, offset, g=self.grouping)). Returns
+    (xq, xk, xv)."""
+
+    def __init__(self, dim=512, n_heads=16, n_kv_heads=8, rank=8, head_sharing=False, grouping=1,
+                 qkv_sharing=None):
+        super().__init__()
+        self.n_heads, self.n_kv_heads = n_heads, n_kv_heads
+        self.qkv_sharing, self.head_sharing = qkv_sharing, head_sharing
+        self.grouping = grouping if grouping else 1
+        self.two_step = False
+        self.head_dim = dim // n_heads
+        self.n_rep = n_heads // n_kv_heads
+        if qkv_sharing:
+            self.n_kv_heads, self.n_rep = n_heads, 1
+            base_dim = self.head_dim * self.grouping if head_sharing else self.head_dim * n_heads
+            for grp in qkv_sharing:
+                setattr(self, str(grp), nn.Linear(dim, base_dim, bias=False))
+        else:
+            dim_mult = self.grouping if head_sharing else n_heads
+            kv_dim_mult = dim_mult // self.n_rep
+            self.wq_base = nn.Linear(dim, self.head_dim * dim_mult, bias=False)
+            self.wk_base = nn.Linear(dim, self.head_dim * kv_dim_mult, bias=False)
+            self.wv_base = nn.Linear(dim, self.head_dim * kv_dim_mult, bias=False)
+        self.wq_offset = RefLoRA(dim, n_heads * self.head_dim, rank)
+        self.wk_offset = RefLoRA(dim, self.n_kv_heads * self.head_dim, rank)
+        self.wv_offset = RefLoRA(dim, self.n_kv_heads * self.head_dim, rank)
+
+    def forward(self, x):
+        wq_offset, wk_offset, wv_offset = self.wq_offset(x), self.wk_offset(x), self.wv_offset(x)
+        if self.qkv_sharing:
+            for grp in self.qkv_sharing:
+                val = getattr(self, str(grp))(x)
+                for wgt in grp:
+                    if wgt == "q":
+                        q_base = val
+                    elif wgt == "k":
+                        k_base = val
+                    elif wgt == "v":
+                        v_base = val
+        else:
+            q_base, k_base, v_base = self.wq_base(x), self.wk_base(x), self.wv_base(x)
+        xq = broadcast_add(q_base, wq_offset, g=self.grouping)
+        xk = broadcast_add(k_base, wk_offset, g=self.grouping)
+        xv = broadcast_add(v_base, wv_offset, g=self.grouping)
+        return xq, xk, xv

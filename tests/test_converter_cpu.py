@@ -28,12 +28,13 @@ def test_convert_keeps_parameters_and_state_dict_keys():
     assert list(m.state_dict().keys()) == keys
     for n, p in m.named_parameters():
         assert p is params[n], n
-    assert sorted(conv.fused) == ["0.wq_offset", "1.wq_offset"]
-    assert sorted(conv.converted) == ["0.wk_offset", "1.wk_offset"]
+    # q (equal widths) and k (a base of g templates broadcast over the offset) both fold
+    assert sorted(conv.fused) == ["0.wk_offset", "0.wq_offset", "1.wk_offset", "1.wq_offset"]
+    assert conv.converted == []
     for i, blk in enumerate(m):
         assert isinstance(blk.wq_base, C.FusedBase) and blk.wq_base.weight is params[f"{i}.wq_base.weight"]
         assert isinstance(blk.wq_offset, LoRAModule) and blk.wq_offset.scale == 2.0
-        assert type(blk.wk_offset) is LoRAModule and isinstance(blk.wk_base, torch.nn.Linear)
+        assert isinstance(blk.wk_base, C.FusedBase) and blk.wk_base.weight is params[f"{i}.wk_base.weight"]
         assert type(blk.wo) is torch.nn.Linear
 
 
@@ -48,3 +49,35 @@ def test_convert_is_idempotent_and_keeps_unpaired_scale():
     conv2.convert(m)
     assert conv2.fused == [] and conv2.converted == []
     assert [type(x) for x in m.modules()] == before
+
+
+def test_shared_attention_modes_fold_and_keep_keys():
+    """Every sharing switch of the reference's attention folds into fused bases; parameters and
+    state-dict keys are kept; the module's broadcast_add is wrapped once, keeping its original."""
+    import tests._ref_style as R
+    orig = getattr(R.broadcast_add, "_wsl_original", R.broadcast_add)  # an earlier test may have wrapped it
+    for kw, n_fused, n_shared in ((dict(), 3, 0), (dict(head_sharing=True, grouping=2), 3, 0),
+                                  (dict(qkv_sharing=[["q", "k", "v"]]), 3, 1),
+                                  (dict(qkv_sharing=[["q", "k"], ["v"]], head_sharing=True, grouping=4), 3, 2)):
+        m = R.RefSharedAttention(**kw)
+        keys = list(m.state_dict().keys())
+        params = {n: p for n, p in m.named_parameters()}
+        conv = C.WslLoRAConverter()
+        conv.convert(m)
+        assert list(m.state_dict().keys()) == keys, kw
+        for n, p in m.named_parameters():
+            assert p is params[n], (kw, n)
+        assert len(conv.fused) == n_fused and len(conv.shared) == n_shared, (kw, conv.fused, conv.shared)
+        assert getattr(R.broadcast_add, "_wsl_original", None) is orig
+    R.broadcast_add = orig  # leave the stand-in module as found
+
+
+def test_folding_broadcast_add_keeps_original_semantics():
+    """Calls without placeholders go to the original broadcast_add unchanged."""
+    import numpy as np
+    from weightshared_torchtitan_amd.lora import broadcast_add as ref_ba
+    fn = C.folding_broadcast_add(ref_ba)
+    g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "broadcast_add.npz"))
+    for name in g["names"]:
+        out = fn(torch.from_numpy(g[f"{name}_base"]), torch.from_numpy(g[f"{name}_delta"]), g=int(g[f"{name}_g"]))
+        np.testing.assert_array_equal(out.numpy(), g[f"{name}_out"])

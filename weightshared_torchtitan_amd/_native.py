@@ -40,6 +40,8 @@ EXPORTED = (
     "wsl_lora_linear_fwd_noalloc",
     "wsl_lora_linear_grouped_workspace_bytes",
     "wsl_lora_linear_grouped_fwd",
+    "wsl_lora_linear_bcast_workspace_bytes",
+    "wsl_lora_linear_bcast_fwd",
     "wsl_factorized_embedding_fwd",
     "wsl_last_error",
     "wsl_version",
@@ -116,6 +118,22 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, _c_i64,                   # y, ldy
         _c_i64, _c_i64, _c_i64,          # M, K, r
         ctypes.c_int32, ctypes.POINTER(_c_i64),  # n_groups, group_n
+        _c_vp, ctypes.c_size_t,          # workspace, bytes
+        _c_vp,                           # stream
+    ]
+    lib.wsl_lora_linear_bcast_workspace_bytes.restype = ctypes.c_int
+    lib.wsl_lora_linear_bcast_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32,
+                                                          ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]
+    lib.wsl_lora_linear_bcast_fwd.restype = ctypes.c_int
+    lib.wsl_lora_linear_bcast_fwd.argtypes = [
+        _c_vp, _c_i64,                   # x, ldx
+        _c_vp, _c_i64, ctypes.c_int32, _c_vp,  # w, ldw, w_dtype, w_scale
+        _c_vp, _c_i64,                   # a, lda
+        _c_vp, _c_i64,                   # b, ldb
+        ctypes.c_float,                  # scale
+        _c_vp, _c_i64,                   # y, ldy
+        _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
+        _c_i64, _c_i64, ctypes.c_int32,  # base_n, g, n_groups
         _c_vp, ctypes.c_size_t,          # workspace, bytes
         _c_vp,                           # stream
     ]
@@ -228,6 +246,13 @@ WSL_MAX_GROUPS = 4
 def group_array(group_n) -> "ctypes.Array":
     """The host array of group widths a grouped call takes."""
     return (_c_i64 * len(group_n))(*[int(n) for n in group_n])
+
+
+def bcast_workspace_bytes(M: int, N: int, K: int, r: int, n_groups: int, w_dtype: int) -> int:
+    out = ctypes.c_size_t(0)
+    check(lib().wsl_lora_linear_bcast_workspace_bytes(M, N, K, r, n_groups, w_dtype, ctypes.byref(out)),
+          "wsl_lora_linear_bcast_workspace_bytes")
+    return int(out.value)
 
 
 def grouped_workspace_bytes(M: int, K: int, r: int, group_n, w_dtype: int) -> int:

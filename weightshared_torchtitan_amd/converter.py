@@ -5,28 +5,38 @@ constructed with ``(job_config, parallel_dims)``, ``convert(model)`` rewrites th
 place, ``post_optimizer_hook(model)`` runs after each optimizer step; converters are
 registered by name (:36-50) and applied by the trainer (torchtitan/train.py:160-161).
 
-The reference's attention holds each LoRA projection as a pair (model.py:246-273,
-302-324) and adds the two outputs in its forward (:392-398):
+The reference's attention holds each LoRA projection as a base ``nn.Linear`` and a
+``LoRAModule`` offset and composes them in its forward (model.py:239-330, 376-398):
 
-    xq = broadcast_add(self.wq_base(x), self.wq_offset(x), g)
+    default        xq = broadcast_add(self.wq_base(x), self.wq_offset(x), g)        (base as wide as q)
+    head_sharing   the same call, wq_base holding g templates of width D' < q's width
+    qkv_sharing    val = getattr(self, str(group))(x); q_base = k_base = v_base = val;
+                   xq = broadcast_add(q_base, self.wq_offset(x), g), likewise k and v
 
-``WslLoRAConverter.convert`` rewrites every such pair whose widths match (g = 1, where
-broadcast_add is a plain add) so the parent's forward runs one fused launch:
+``WslLoRAConverter.convert`` folds each composition into one launch of the shared-base
+fused op (``wsl::lora_linear_bcast``: x . W^T broadcast over the head templates plus the
+offset's s (x . A^T) . B^T, never materialising the expanded base or the delta):
 
-- ``<p>_base`` becomes a ``FusedBase`` whose forward is the fused
-  ``x . W^T + s (x . A^T) . B^T``;
-- ``<p>_offset`` becomes a wsl ``LoRAModule`` in folded mode, whose forward returns a
-  broadcast zero (no memory of its own), so the parent's add is the identity on the fused
-  output.
+- a ``<p>_base`` / ``<p>_offset`` pair (default and head sharing) becomes a ``FusedBase`` and
+  a folded offset;
+- a shared q/k/v base module becomes a ``FusedSharedBase`` and the group's offsets folded
+  offsets.
 
-Any other LoRA module (an unpaired one, or one whose base is expanded over head groups)
-becomes a wsl ``LoRAModule``: the delta in one launch instead of two GEMMs and a multiply.
-Every Parameter object is kept, so the optimizer's state and the state-dict keys
+The fused modules and folded offsets return zero-stride placeholders that record their
+input. The converter swaps the ``broadcast_add`` that the attention's module calls for a
+wrapper: given a fused base's placeholder and a folded offset's, it runs the one launch
+(with the ``g`` of the call) and returns the projection (its column block for a shared base;
+the other projections of the group reuse the same launch); any other call keeps the
+original semantics, and a fused base used alone is computed as the plain base. So the
+parent's forward is unchanged and pays no extra pass over its outputs. Offsets of the
+``two_step`` variant and unpaired LoRA modules become wsl ``LoRAModule``s (the delta in one
+launch). Every Parameter object is kept, so optimizer state and state-dict keys
 (``<p>_base.weight``, ``<p>_offset.w_a.weight``, ``<p>_offset.w_b.weight``) do not change.
 """
 from __future__ import annotations
 
-from typing import Dict, List, Union
+import sys
+from typing import Dict, List, Optional, Union
 
 import torch
 import torch.nn as nn
@@ -34,32 +44,124 @@ import torch.nn as nn
 from . import ops
 from .lora import LoRAModule
 
+_PENDING = "_wsl_pending"  # on a fused base's placeholder: its _Pending record
+_FOLDED = "_wsl_folded"    # on a folded offset's placeholder: its block in the fused output
+
+
+class _Pending:
+    """A fused base's call: its input and the fused outputs computed from it, by g."""
+
+    def __init__(self, x: torch.Tensor, owner: nn.Module):
+        self.x = x
+        self.owner = owner
+        self.out: Dict[int, torch.Tensor] = {}
+
+
+_ZEROS: Dict[torch.device, torch.Tensor] = {}
+
+
+def _placeholder(x: torch.Tensor, width: int, attr: str, value) -> torch.Tensor:
+    """A zero-stride view of one cached zero per device (no device work), tagged."""
+    z = _ZEROS.get(x.device)
+    if z is None:
+        z = _ZEROS[x.device] = torch.zeros((), dtype=torch.bfloat16, device=x.device)
+    t = z.expand(*x.shape[:-1], width)
+    setattr(t, attr, value)
+    return t
+
+
+def folding_broadcast_add(original):
+    """``broadcast_add`` for converted modules. Given a fused base's placeholder and a folded
+    offset's, the fused launch of the base's input runs once per ``g`` and the offset's
+    column block of it is returned; a fused base's placeholder with any other delta is first
+    computed as the plain base x . W^T; every other call is ``original(base, delta, dim=dim,
+    g=g)``."""
+    def broadcast_add(base, delta, *, dim=-1, g=1):
+        pend = getattr(base, _PENDING, None)
+        slot = getattr(delta, _FOLDED, None)
+        if pend is not None and slot is not None and (dim == -1 or dim == base.dim() - 1):
+            out = pend.out.get(int(g))
+            if out is None:
+                out = pend.owner.fused(pend.x, int(g))
+                pend.out[int(g)] = out
+            block, width = slot
+            return out if out.shape[-1] == width else out.narrow(-1, block * width, width)
+        if pend is not None:
+            base = pend.owner.plain(pend.x)
+        if slot is not None:
+            raise RuntimeError("a folded LoRA offset's placeholder met a base that is not its fused base")
+        return original(base, delta, dim=dim, g=g)
+
+    broadcast_add._wsl_original = original
+    return broadcast_add
+
 
 class FusedBase(nn.Module):
     """The base half of a fused pair: ``weight`` is the original base Parameter; the LoRA
     factors are read from the paired offset module (held outside the module tree so its
-    parameters keep their one state-dict key)."""
+    parameters keep their one state-dict key). Its forward is a placeholder; the projection
+    is computed where the module's broadcast_add meets it with the folded offset's."""
 
     def __init__(self, base: nn.Linear, lora: LoRAModule):
         super().__init__()
         self.weight = base.weight
         self.in_features = base.in_features
         self.out_features = base.out_features
-        object.__setattr__(self, "_lora", lora)
+        object.__setattr__(self, "_loras", [lora])
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        lora = self._lora
-        return ops.lora_linear(x, self.weight, lora.w_a.weight, lora.w_b.weight, lora.scale)
+        return _placeholder(x, self.out_features, _PENDING, _Pending(x, self))
+
+    def plain(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.lora_linear(x, self.weight, None, None, 0.0)
+
+    def _stacked(self):
+        """[A_0; A_1; ...] and [B_0; B_1; ...] of the offsets. With autograd on they are
+        stacked on every call (the stack is differentiable); without, once per parameter
+        version."""
+        ls = self._loras
+        if len(ls) == 1:
+            return ls[0].w_a.weight, ls[0].w_b.weight
+        if torch.is_grad_enabled():
+            return torch.cat([m.w_a.weight for m in ls], 0), torch.cat([m.w_b.weight for m in ls], 0)
+        key = tuple((p.data_ptr(), p._version) for m in ls for p in (m.w_a.weight, m.w_b.weight))
+        cache = getattr(self, "_stack_cache", None)
+        if cache is None or cache[0] != key:
+            cache = (key, torch.cat([m.w_a.weight for m in ls], 0), torch.cat([m.w_b.weight for m in ls], 0))
+            object.__setattr__(self, "_stack_cache", cache)
+        return cache[1], cache[2]
+
+    def fused(self, x: torch.Tensor, g: int) -> torch.Tensor:
+        """broadcast_add(x . W^T, each offset's delta, g), the offsets side by side."""
+        ls = self._loras
+        lora = ls[0]
+        if len(ls) == 1 and lora.out_dim == self.out_features:
+            return ops.lora_linear(x, self.weight, lora.w_a.weight, lora.w_b.weight, lora.scale)
+        a, b = self._stacked()
+        return ops.lora_linear_bcast_op(x, self.weight, None, a, b, float(lora.scale), g, len(ls))
 
     def extra_repr(self) -> str:
-        return f"in_features={self.in_features}, out_features={self.out_features}, fused LoRA rank={self._lora.rank}"
+        return (f"in_features={self.in_features}, out_features={self.out_features}, fused LoRA "
+                f"rank={self._loras[0].rank}, projections={len(self._loras)}")
+
+
+class FusedSharedBase(FusedBase):
+    """A base shared by several projections (the reference's qkv_sharing): one launch gives
+    every projection of the group, side by side, each broadcast_add(base, its offset, g)."""
+
+    def __init__(self, base: nn.Linear, loras: List[LoRAModule]):
+        super().__init__(base, loras[0])
+        object.__setattr__(self, "_loras", list(loras))
 
 
 class _FoldedLoRA(LoRAModule):
-    """A wsl LoRAModule whose delta is already inside its paired ``FusedBase`` output."""
+    """A wsl LoRAModule whose delta is computed inside its fused base's launch: its forward is
+    a placeholder for the converted module's ``broadcast_add`` (see the module docstring)."""
+
+    _block = 0
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return x.new_zeros((), dtype=torch.bfloat16).expand(*x.shape[:-1], self.out_dim)
+        return _placeholder(x, self.out_dim, _FOLDED, (self._block, self.out_dim))
 
 
 def _is_lora(m: nn.Module) -> bool:
@@ -74,24 +176,75 @@ def _as_wsl(m: nn.Module, cls=LoRAModule) -> LoRAModule:
                w_b_override=m.w_b, scale=scale)
 
 
+def _folded(m: nn.Module, block: int) -> _FoldedLoRA:
+    f = _as_wsl(m, _FoldedLoRA)
+    f._block = block
+    return f
+
+
+def _is_base(m) -> bool:
+    return isinstance(m, nn.Linear) and type(m) is nn.Linear and m.bias is None
+
+
 class WslLoRAConverter:
     """``model.converters = ["wsl_lora"]``: fused LoRA linears (see the module docstring)."""
 
     def __init__(self, job_config=None, parallel_dims=None):
-        self.fused: List[str] = []
-        self.converted: List[str] = []
+        self.fused: List[str] = []       # offsets folded into a fused base
+        self.converted: List[str] = []   # other LoRA modules moved to wsl LoRAModule
+        self.shared: List[str] = []      # shared q/k/v bases folded with their offsets
+        self._patched_modules: List[str] = []
+
+    def _patch(self, parent: nn.Module) -> bool:
+        """Swap the broadcast_add the parent's module calls for the folding one. False when
+        the module has none (then nothing is folded: the placeholders would be added)."""
+        mod = sys.modules.get(type(parent).__module__)
+        fn = getattr(mod, "broadcast_add", None) if mod is not None else None
+        if fn is None:
+            return False
+        if getattr(fn, "_wsl_original", None) is None:
+            mod.broadcast_add = folding_broadcast_add(fn)
+            self._patched_modules.append(mod.__name__)
+        return True
+
+    def _fold_shared(self, pname: str, parent: nn.Module) -> None:
+        groups = getattr(parent, "qkv_sharing", None)
+        if not groups or getattr(parent, "two_step", False):
+            return
+        for grp in groups:
+            base = getattr(parent, str(grp), None)
+            offs = [getattr(parent, f"w{letter}_offset", None) for letter in grp]
+            if not _is_base(base) or not all(o is not None and _is_lora(o) for o in offs):
+                continue
+            widths = {o.w_b.out_features for o in offs}
+            ranks = {o.rank for o in offs}
+            scales = {(o.scale if isinstance(o, LoRAModule) else o.alpha / o.rank) for o in offs}
+            if len(widths) != 1 or len(ranks) != 1 or len(scales) != 1 or len(offs) > ops._native.WSL_MAX_GROUPS:
+                continue
+            if widths.pop() % base.out_features != 0 or base.in_features != offs[0].w_a.in_features:
+                continue
+            if not self._patch(parent):
+                continue
+            folded = []
+            for j, letter in enumerate(grp):
+                f = _folded(offs[j], j)
+                setattr(parent, f"w{letter}_offset", f)
+                folded.append(f)
+                self.fused.append(f"{pname}.w{letter}_offset" if pname else f"w{letter}_offset")
+            setattr(parent, str(grp), FusedSharedBase(base, folded))
+            self.shared.append(f"{pname}.{grp}" if pname else str(grp))
 
     def convert(self, model: nn.Module) -> None:
         for pname, parent in list(model.named_modules()):
+            self._fold_shared(pname, parent)
             for name, child in list(parent.named_children()):
                 path = f"{pname}.{name}" if pname else name
                 if not name.endswith("_offset") or not _is_lora(child) or isinstance(child, _FoldedLoRA):
                     continue
                 base = getattr(parent, name[: -len("_offset")] + "_base", None)
-                if (isinstance(base, nn.Linear) and base.bias is None
-                        and base.out_features == child.w_b.out_features
-                        and base.in_features == child.w_a.in_features):
-                    lora = _as_wsl(child, _FoldedLoRA)
+                if (_is_base(base) and base.in_features == child.w_a.in_features
+                        and child.w_b.out_features % base.out_features == 0 and self._patch(parent)):
+                    lora = _folded(child, 0)
                     setattr(parent, name, lora)
                     setattr(parent, name[: -len("_offset")] + "_base", FusedBase(base, lora))
                     self.fused.append(path)

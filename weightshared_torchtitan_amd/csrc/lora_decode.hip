@@ -235,6 +235,7 @@ struct DecodeArgs {
   uint64_t* tpart;    // [gT][kst][T rows per group][M]: ptag << 32 | fp32 partial sum
   uint64_t* ypart;    // [gY][ksy][W rows per group][M]: likewise
   int spin;           // polls of the T counter before the local fallback
+  RowMap wmap;        // W and w_scale rows by output row (shared-base forms)
   // greedy-token epilogue (kFuseArgmax): per token m the key am_keys[m * kAmStride] (64-bit
   // atomic max), one arrival counter, the winning index to am_out[m]; LDS scratch at am_red
   uint64_t* am_keys; unsigned* am_cnt; int64_t* am_out; int am_red; int am_total;
@@ -269,7 +270,7 @@ struct NoPrologue {
 template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue>
 __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
                                            int kbeg, int kc, int M, char* smem, float* sums,
-                                           const Pro& pro = Pro()) {
+                                           const Pro& pro = Pro(), RowMap rmap = RowMap{}) {
   using G = Geo<WDT>;
   constexpr int PD = NR == 1 ? 4 : (NR == 2 ? 2 : 1);  // K steps in flight per wave (NR*4*PD = 16 loads)
   constexpr int LPS = NR * 4;           // loads per step
@@ -287,7 +288,7 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
 
   int64_t rowoff[NR];
 #pragma unroll
-  for (int i = 0; i < NR; ++i) rowoff[i] = (int64_t)min(rbase + i * 16 + l16, nrows - 1) * ldm;
+  for (int i = 0; i < NR; ++i) rowoff[i] = (int64_t)map_row(min(rbase + i * 16 + l16, nrows - 1), rmap) * ldm;
   int xrow[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) xrow[mb] = min(mb * 16 + l16, M - 1);
@@ -400,7 +401,7 @@ __device__ float direct_partial(const void* __restrict__ mat, int64_t ldm, int r
 template <int WDT, int ROWS, int MC>
 __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks, int ksplit, int M, uint32_t ptag,
                                              int spin, const void* mat, int64_t ldm, int nrows, int row0,
-                                             const uint16_t* x, int64_t ldx, int kc) {
+                                             const uint16_t* x, int64_t ldx, int kc, RowMap rmap = RowMap{}) {
   if (ksplit == 1) return true;
   const int tid = threadIdx.x;
   const int n = M * ROWS;
@@ -429,7 +430,8 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
           const int rl = q / M, m = q % M;
           v[u] += (w[u] >> 32) == ptag
                       ? __uint_as_float((uint32_t)w[u])
-                      : direct_partial<WDT>(mat, ldm, min(row0 + rl, nrows - 1), x, ldx, m, sp * kc, kc);
+                      : direct_partial<WDT>(mat, ldm, map_row(min(row0 + rl, nrows - 1), rmap), x, ldx, m, sp * kc,
+                                            kc);
         }
       }
     }
@@ -624,7 +626,7 @@ __device__ __forceinline__ void argmax_epilogue(const DecodeArgs& p, const float
       const int n = row0 + rl;
       if (n < p.N) {
         float v = sums[rl * MC + tok];
-        if (p.w_scale != nullptr) v *= p.w_scale[n];
+        if (p.w_scale != nullptr) v *= p.w_scale[map_row(n, p.wmap)];
         const uint64_t k = am_key(bf16_round(v), n);
         best = k > best ? k : best;
       }
@@ -725,15 +727,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
       if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
       slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums,
-                                  NormPrologue{&p, smem, ss, smem + p.nw_off});
+                                  NormPrologue{&p, smem, ss, smem + p.nw_off}, p.wmap);
     } else {
       fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kcy, wave, lane);
       if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
-      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums);
+      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums, NoPrologue{}, p.wmap);
     }
     const uint64_t tag = late_tag();
     if (split_reduce<WDT, ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, ks, p.ksy, p.M,
-                                    ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy)) {
+                                    ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy, p.wmap)) {
       if constexpr ((FUSE & kFuseArgmax) != 0) {  // the head's greedy token: no logits written
         argmax_epilogue<ROWS, MC>(p, sums, row0, smem);
         return;
@@ -777,7 +779,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
           for (int e = 0; e < 4; ++e) {
             const int n = n0 + e;
             float v = sums[(i * 16 + grp * 4 + e) * MC + m];
-            if (p.w_scale != nullptr && n < p.N) v *= p.w_scale[n];
+            if (p.w_scale != nullptr && n < p.N) v *= p.w_scale[map_row(n, p.wmap)];
             o[e] = v + d[e];
           }
           if constexpr (RES) {  // y = bf16(res + bf16(o)); res may be y itself (read first)
@@ -1099,6 +1101,7 @@ DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl, char* cnt, char* d
   a.tpart = reinterpret_cast<uint64_t*>(data + pl.off_pt);
   a.ypart = reinterpret_cast<uint64_t*>(data + pl.off_py);
   a.spin = spin_limit();
+  a.wmap = p.wmap;
   return a;
 }
 DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl) {

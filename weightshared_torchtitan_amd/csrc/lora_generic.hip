@@ -39,7 +39,7 @@ __global__ void __launch_bounds__(GT* GT) generic_main_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const int64_t* __restrict__ gidx, int64_t grows, const void* __restrict__ w, int64_t ldw,
     int w_dtype, const float* __restrict__ w_scale, const uint16_t* __restrict__ t,
     const uint16_t* __restrict__ b, int64_t ldb, uint16_t* __restrict__ y, int64_t ldy,
-    int64_t M, int64_t N, int64_t K, int64_t r) {
+    int64_t M, int64_t N, int64_t K, int64_t r, RowMap wmap) {
   __shared__ float xs[GT][GT + 1];
   __shared__ float ws[GT][GT + 1];
   const int tx = threadIdx.x % GT, ty = threadIdx.x / GT;
@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(GT* GT) generic_main_kernel(
         }
       }
       xs[ty][tx] = xv;
-      ws[ty][tx] = (n0 + ty < N && kx < K) ? load_w(w, w_dtype, (n0 + ty) * ldw + kx) : 0.f;
+      ws[ty][tx] = (n0 + ty < N && kx < K) ? load_w(w, w_dtype, (int64_t)map_row((int)(n0 + ty), wmap) * ldw + kx) : 0.f;
       __syncthreads();
 #pragma unroll
       for (int kk = 0; kk < GT; ++kk) acc += xs[ty][kk] * ws[tx][kk];
@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(GT* GT) generic_main_kernel(
     }
   }
   if (m >= M || n >= N) return;
-  if (w_scale != nullptr) acc *= w_scale[n];
+  if (w_scale != nullptr) acc *= w_scale[map_row((int)n, wmap)];
   if (r > 0) {
     const uint16_t* tr = t + m * r;
     const uint16_t* br = b + n * ldb;
@@ -96,7 +96,7 @@ hipError_t launch_generic(const LoraArgs& p) {
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw,
       p.w_dtype, p.w_scale, t,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, reinterpret_cast<uint16_t*>(p.y), p.ldy,
-      p.M, p.N, p.K, p.r);
+      p.M, p.N, p.K, p.r, p.wmap);
   return hipGetLastError();
 }
 

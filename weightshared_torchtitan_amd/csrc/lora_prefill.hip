@@ -135,7 +135,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const uint16_t* __restrict__ bm, int64_t ldb, float s, float yscale,
                uint16_t* __restrict__ y, int64_t ldy,
                int M, int N, int K, int r, int tiles_m, int tiles_n,
-               int ge0, int ge1, int ge2, int64_t a_gstride, int t_gstride) {
+               int ge0, int ge1, int ge2, int64_t a_gstride, int t_gstride, RowMap wmap) {
   constexpr bool W8 = HAS_W && WDT == kFP8;
   constexpr bool WDIRECT = HAS_W && WDT == kBF16;
   constexpr bool LORA = RB > 0 || EXT_T;
@@ -200,12 +200,15 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       xoff[i] = (uint32_t)((gr - m0) * ldx * 2 + fill_chunk(lane, wave * C::NXI + i) * 16);
     }
   }
-  const char* wbase = reinterpret_cast<const char*>(w) + (WDIRECT ? (int64_t)n0 * ldw * 2 : 0);
+  // W rows by output column (mapped for the shared-base forms, whose W is small enough for
+  // 32-bit offsets from its start)
+  const int wrow0 = wmap.P == 0 ? n0 : 0;
+  const char* wbase = reinterpret_cast<const char*>(w) + (WDIRECT ? (int64_t)wrow0 * ldw * 2 : 0);
   uint32_t woff[C::NWI];
 #pragma unroll
   for (int i = 0; i < C::NWI; ++i) {
     const int row = (wave * C::NWI + i) * 8 + (lane >> 3);
-    woff[i] = (uint32_t)((min(n0 + row, N - 1) - n0) * ldw * 2 + fill_chunk(lane, wave * C::NWI + i) * 16);
+    woff[i] = (uint32_t)((map_row(min(n0 + row, N - 1), wmap) - wrow0) * ldw * 2 + fill_chunk(lane, wave * C::NWI + i) * 16);
   }
   // rank-A slice: RB*32 rows = RB*4 fills, one per wave for waves < RB*4 (rows >= r read
   // row r-1; their T ranks are zeroed when T is parked)
@@ -219,7 +222,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
     for (int i = 0; i < W8C; ++i) {
       const int id = i * NT + tid;
-      w8row[i] = reinterpret_cast<const uint8_t*>(w) + (int64_t)min(n0 + (id >> 2), N - 1) * ldw + (id & 3) * 16;
+      w8row[i] = reinterpret_cast<const uint8_t*>(w) + (int64_t)map_row(min(n0 + (id >> 2), N - 1), wmap) * ldw + (id & 3) * 16;
     }
   }
 
@@ -459,7 +462,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int n = n0 + wn * C::TN + i * 32 + g * 8 + lh * 4 + e;
-          const float sc = w_scale[min(n, N - 1)];
+          const float sc = w_scale[map_row(min(n, N - 1), wmap)];
 #pragma unroll
           for (int j = 0; j < C::MJ; ++j) acc[i][j][g * 4 + e] *= sc;
         }
@@ -646,7 +649,7 @@ hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int sp
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
       reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n,
       group_end(p, 0), group_end(p, 1), group_end(p, 2), p.groups > 1 ? p.r * p.lda : 0,
-      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0);
+      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0, p.wmap);
   return hipGetLastError();
 }
 
@@ -751,6 +754,7 @@ bool prefill_supported(const LoraArgs& p) {
   // 32-bit lane offsets of the direct fills cover a 256-row tile of x and W
   if (p.ldx > ((int64_t)1 << 22) || p.ldw > ((int64_t)1 << 22) || p.lda > ((int64_t)1 << 22)) return false;
   if (!aligned16(p.x) || p.ldx % 8 != 0) return false;
+  if (p.wmap.P != 0 && p.wrows * p.ldw * 2 >= ((int64_t)1 << 32)) return false;
   if (p.w != nullptr) {
     if (!aligned16(p.w)) return false;
     if (p.w_dtype == kBF16 && p.ldw % 8 != 0) return false;
@@ -804,6 +808,7 @@ hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
   LoraArgs q = p;
   q.w = p.a; q.ldw = p.lda; q.w_dtype = kBF16; q.w_scale = nullptr;
   q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0; q.groups = 1;
+  q.wmap = RowMap{}; q.wrows = rt;
   q.N = rt; q.y = t; q.ldy = rt; q.yscale = p.scale;
   const int splits = rank_splits(p.M, p.K, rt);
   if (splits > 1) {

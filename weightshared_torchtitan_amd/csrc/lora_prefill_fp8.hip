@@ -243,7 +243,7 @@ fp8_gemm_kernel(const uint8_t* __restrict__ xq, int64_t term_stride, const float
                 const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ w_scale,
                 const uint16_t* __restrict__ tg, int64_t ldt, const uint16_t* __restrict__ bm, int64_t ldb,
                 uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int r, int tiles_m, int tiles_n,
-                int ge0, int ge1, int ge2, int t_gstride) {
+                int ge0, int ge1, int ge2, int t_gstride, RowMap wmap) {
   constexpr int STAGE = F8_TILE * (1 + TERMS);  // W tile, then the x tiles
   constexpr int OS = F8_BN * 2 + 16;            // row stride of the staged output tile
   constexpr int LDS_BYTES = (F8_S * STAGE > F8_BM * OS) ? F8_S * STAGE : F8_BM * OS;
@@ -276,15 +276,16 @@ fp8_gemm_kernel(const uint8_t* __restrict__ xq, int64_t term_stride, const float
   // Direct-fill sources: tile base (wave-uniform) + 32-bit lane offset. Fill g of a tile
   // writes its rows 16 g .. 16 g + 15; wave v issues fills 2 v and 2 v + 1.
   const int fc = f8_fill_chunk(lane);
+  const int wrow0 = wmap.P == 0 ? n0 : 0;  // mapped W rows are offsets from W's start
   uint32_t xoff[2], woff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int row = (wave * 2 + i) * 16 + (lane >> 2);
     xoff[i] = (uint32_t)((int64_t)(min(m0 + row, M - 1) - m0) * K + fc * 16);
-    woff[i] = (uint32_t)((int64_t)(min(n0 + row, N - 1) - n0) * ldw + fc * 16);
+    woff[i] = (uint32_t)((int64_t)(map_row(min(n0 + row, N - 1), wmap) - wrow0) * ldw + fc * 16);
   }
   const char* xbase = reinterpret_cast<const char*>(xq) + (int64_t)m0 * K;
-  const char* wbase = reinterpret_cast<const char*>(w) + (int64_t)n0 * ldw;
+  const char* wbase = reinterpret_cast<const char*>(w) + (int64_t)wrow0 * ldw;
   auto issue = [&](int stage, int k0) {
     char* sw = lds + stage * STAGE;
 #pragma unroll
@@ -350,7 +351,7 @@ fp8_gemm_kernel(const uint8_t* __restrict__ xq, int64_t term_stride, const float
       for (int g = 0; g < 4; ++g)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float sc = w_scale[min(n0 + wn * F8_TN + i * 32 + g * 8 + lh * 4 + e, N - 1)];
+          const float sc = w_scale[map_row(min(n0 + wn * F8_TN + i * 32 + g * 8 + lh * 4 + e, N - 1), wmap)];
 #pragma unroll
           for (int j = 0; j < F8_MJ; ++j) acc[i][j][g * 4 + e] *= sc * sm[j];
         }
@@ -457,6 +458,7 @@ bool prefill_fp8_supported(const LoraArgs& p) {
   if (p.r > 0 && ((reinterpret_cast<uintptr_t>(p.b) & 15u) != 0 || p.ldb % 8 != 0)) return false;
   if ((reinterpret_cast<uintptr_t>(p.w) & 15u) != 0 || p.ldw % 16 != 0) return false;
   if (p.ldw * (int64_t)F8_BN >= ((int64_t)1 << 32) || p.K * (int64_t)F8_BM >= ((int64_t)1 << 32)) return false;
+  if (p.wmap.P != 0 && p.wrows * p.ldw >= ((int64_t)1 << 32)) return false;
   if ((reinterpret_cast<uintptr_t>(p.x) & 15u) != 0 || p.ldx % 8 != 0) return false;
   if ((reinterpret_cast<uintptr_t>(p.y) & 7u) != 0 || p.ldy % 4 != 0) return false;
   for (int g = 0; g + 1 < p.groups; ++g)
@@ -488,20 +490,20 @@ hipError_t launch_prefill_fp8(const LoraArgs& p, const uint16_t* tg, int64_t ldt
     if (lora)
       fp8_gemm_kernel<2, true><<<grid, block, 0, p.stream>>>(xq, term_stride, sx, w8, p.ldw, p.w_scale, tg, ldt, b,
                                                             p.ldb, y, p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r,
-                                                            tiles_m, tiles_n, g0, g1, g2, tgs);
+                                                            tiles_m, tiles_n, g0, g1, g2, tgs, p.wmap);
     else
       fp8_gemm_kernel<2, false><<<grid, block, 0, p.stream>>>(xq, term_stride, sx, w8, p.ldw, p.w_scale, tg, ldt, b,
                                                              p.ldb, y, p.ldy, (int)p.M, (int)p.N, (int)p.K, 0,
-                                                             tiles_m, tiles_n, g0, g1, g2, 0);
+                                                             tiles_m, tiles_n, g0, g1, g2, 0, p.wmap);
   } else {
     if (lora)
       fp8_gemm_kernel<1, true><<<grid, block, 0, p.stream>>>(xq, term_stride, sx, w8, p.ldw, p.w_scale, tg, ldt, b,
                                                             p.ldb, y, p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r,
-                                                            tiles_m, tiles_n, g0, g1, g2, tgs);
+                                                            tiles_m, tiles_n, g0, g1, g2, tgs, p.wmap);
     else
       fp8_gemm_kernel<1, false><<<grid, block, 0, p.stream>>>(xq, term_stride, sx, w8, p.ldw, p.w_scale, tg, ldt, b,
                                                              p.ldb, y, p.ldy, (int)p.M, (int)p.N, (int)p.K, 0,
-                                                             tiles_m, tiles_n, g0, g1, g2, 0);
+                                                             tiles_m, tiles_n, g0, g1, g2, 0, p.wmap);
   }
   return hipGetLastError();
 }

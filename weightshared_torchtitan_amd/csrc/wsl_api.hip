@@ -260,6 +260,43 @@ int run_call(wsl::LoraArgs p, void* workspace, size_t workspace_bytes) {
   return WSL_OK;
 }
 
+// A grouped call after validation: one launch when the path's grid respects the group
+// ends, else one launch per group in order on the same stream (the workspace is reused
+// stream-ordered). With `shared_base` every group reads the same W (and w_scale) rows
+// through p.wmap; otherwise group g's W rows follow the previous groups'.
+int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shared_base, void* workspace,
+                size_t workspace_bytes) {
+  p.groups = n_groups;
+  int64_t end = 0;
+  for (int g = 0; g < n_groups; ++g) p.gend[g] = (end += group_n[g]);
+  if (n_groups == 1 || p.r == 0) {
+    p.groups = 1;
+    return run_call(p, workspace, workspace_bytes);
+  }
+  const Path path = choose_path(p);
+  if ((path == Path::kPrefill && wsl::prefill_groups_supported(p)) ||
+      (path == Path::kDecode && wsl::decode_groups_supported(p)))
+    return run_call(p, workspace, workspace_bytes);
+  const int64_t wbytes = (p.w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;
+  int64_t n0 = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    wsl::LoraArgs q = p;
+    q.groups = 1;
+    q.N = group_n[g];
+    if (!shared_base) {
+      if (p.w != nullptr) q.w = reinterpret_cast<const char*>(p.w) + n0 * p.ldw * wbytes;
+      if (p.w_scale != nullptr) q.w_scale = p.w_scale + n0;
+    }
+    q.a = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)g * p.r * p.lda;
+    q.b = reinterpret_cast<const uint16_t*>(p.b) + n0 * p.ldb;
+    q.y = reinterpret_cast<uint16_t*>(p.y) + n0;
+    const int rc = run_call(q, workspace, workspace_bytes);
+    if (rc != WSL_OK) return rc;
+    n0 += group_n[g];
+  }
+  return WSL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -366,35 +403,49 @@ int wsl_lora_linear_grouped_fwd(const void* x, int64_t ldx, const void* w, int64
   if (rc != WSL_OK) return rc;
   wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, N, K, r, stream);
   p.fp8_terms = terms;
-  p.groups = n_groups;
-  int64_t end = 0;
-  for (int g = 0; g < n_groups; ++g) p.gend[g] = (end += group_n[g]);
-  if (n_groups == 1 || r == 0) {
-    p.groups = 1;
-    return run_call(p, workspace, workspace_bytes);
+  return run_grouped(p, n_groups, group_n, false, workspace, workspace_bytes);
+}
+
+int wsl_lora_linear_bcast_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int32_t n_groups,
+                                          int32_t w_dtype, size_t* bytes) {
+  if (n_groups < 1 || n_groups > WSL_MAX_GROUPS) {
+    clear_err();
+    return fail(WSL_E_SHAPE, "n_groups must be in [1, %d] (got %d)", WSL_MAX_GROUPS, (int)n_groups);
   }
-  const Path path = choose_path(p);
-  if ((path == Path::kPrefill && wsl::prefill_groups_supported(p)) ||
-      (path == Path::kDecode && wsl::decode_groups_supported(p)))
-    return run_call(p, workspace, workspace_bytes);
-  // Unaligned operands or group ends off the launch's tile / row-group grid: one launch
-  // per group, in order, on the same stream (the workspace is reused stream-ordered).
-  const int64_t wbytes = (w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;
-  int64_t n0 = 0;
-  for (int g = 0; g < n_groups; ++g) {
-    wsl::LoraArgs q = p;
-    q.groups = 1;
-    q.N = group_n[g];
-    if (w != nullptr) q.w = reinterpret_cast<const char*>(w) + n0 * ldw * wbytes;
-    if (w_scale != nullptr) q.w_scale = w_scale + n0;
-    q.a = reinterpret_cast<const uint16_t*>(a) + (int64_t)g * r * lda;
-    q.b = reinterpret_cast<const uint16_t*>(b) + n0 * ldb;
-    q.y = reinterpret_cast<uint16_t*>(y) + n0;
-    rc = run_call(q, workspace, workspace_bytes);
-    if (rc != WSL_OK) return rc;
-    n0 += group_n[g];
-  }
-  return WSL_OK;
+  int64_t gn[WSL_MAX_GROUPS];
+  for (int g = 0; g < n_groups; ++g) gn[g] = N;
+  return wsl_lora_linear_grouped_workspace_bytes(M, K, r, n_groups, gn, w_dtype, bytes);
+}
+
+int wsl_lora_linear_bcast_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t w_dtype_in,
+                              const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
+                              float scale, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t r,
+                              int64_t base_n, int64_t g, int32_t n_groups, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  clear_err();
+  int terms;
+  const int32_t w_dtype = kernel_dtype(w_dtype_in, &terms);
+  if (n_groups < 1 || n_groups > WSL_MAX_GROUPS)
+    return fail(WSL_E_SHAPE, "n_groups must be in [1, %d] (got %d)", WSL_MAX_GROUPS, (int)n_groups);
+  if (w == nullptr) return fail(WSL_E_INVALID_ARG, "the shared-base form needs w");
+  if (base_n < 1 || g < 1 || N < 1 || N % base_n != 0 || base_n % g != 0)
+    return fail(WSL_E_SHAPE, "need N %% base_n == 0 and base_n %% g == 0 (N %lld, base_n %lld, g %lld)", (long long)N,
+                (long long)base_n, (long long)g);
+  const int64_t Nt = N * n_groups;
+  int rc = validate_call(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, y, ldy, M, Nt, K, r);
+  if (rc != WSL_OK) return rc;
+  wsl::LoraArgs p = make_args(x, ldx, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, y, ldy, M, Nt, K, r, stream);
+  p.fp8_terms = terms;
+  // column c of a group reads base row (c / (hpg D')) D' + c % D': the reference's
+  // broadcast_add index map (D' = base_n / g templates' width, hpg = N / base_n heads each)
+  const int64_t dw = base_n / g, hpg = N / base_n;
+  p.wmap.P = (int)N;
+  p.wmap.S = (int)(hpg * dw);
+  p.wmap.D = (int)dw;
+  p.wrows = base_n;
+  int64_t gn[WSL_MAX_GROUPS];
+  for (int q = 0; q < n_groups; ++q) gn[q] = N;
+  return run_grouped(p, n_groups, gn, true, workspace, workspace_bytes);
 }
 
 int wsl_lora_linear_fused_supported(int64_t M, int64_t N, int64_t K, int64_t r, int32_t fuse) {

@@ -97,6 +97,19 @@ __device__ __forceinline__ u32x4_t zero_u32x4() {
 // Host-side launch helpers shared by the translation units of libwsl.
 namespace wsl {
 
+// Base-row map of the shared-base forms (the reference's broadcast_add with g > 1, and one
+// base weight serving several projections): output column c takes row
+// ((c mod P) / S) * D + (c mod P) mod D of W and of w_scale. P == 0 is the identity.
+// Every kernel maps the rows it reads once per tile or wave (never inside the K loop).
+struct RowMap {
+  int P = 0, S = 1, D = 1;
+};
+__host__ __device__ __forceinline__ int map_row(int c, const RowMap& m) {
+  if (m.P == 0) return c;
+  const int c2 = c % m.P;
+  return (c2 / m.S) * m.D + c2 % m.D;
+}
+
 constexpr int kMaxGroups = 4;  // projections in one grouped launch (WSL_MAX_GROUPS)
 
 struct LoraArgs {
@@ -123,6 +136,9 @@ struct LoraArgs {
   // fp8 W on prefill shapes: activation terms of the fp8 matrix-core path (2: bf16-quality
   // activations, 1: one e4m3 term); 0 decodes W to bf16 on the bf16 matrix cores instead.
   int fp8_terms = 2;
+  // Shared-base forms: W (and w_scale) rows by output column, and W's row count.
+  RowMap wmap;
+  int64_t wrows = 0;
 };
 
 // Each launcher returns hipSuccess or the launch error.

@@ -335,6 +335,136 @@ def _lora_linear_grouped_fake(x, w, w_scale, a, b, scale, group_n):
     return x.new_empty((*x.shape[:-1], sum(int(n) for n in group_n)), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op("wsl::lora_linear_bcast", mutates_args=(), device_types="cuda")
+def lora_linear_bcast_op(x: torch.Tensor, w: torch.Tensor, w_scale: Optional[torch.Tensor],
+                         a: Optional[torch.Tensor], b: Optional[torch.Tensor], scale: float, g: int,
+                         n_groups: int) -> torch.Tensor:
+    """Shared-base LoRA linears in one launch (wsl_lora_linear_bcast_fwd): w [base_n, K] serves
+    n_groups projections of width N = b.shape[0] / n_groups (N = w.shape[0] without LoRA), and
+    output block j is the reference's broadcast_add(x . w^T, scale * (x . a_j^T) . b_j^T, g),
+    a = [a_0; a_1; ...] [n_groups * r, K], b = [b_0; b_1; ...] [n_groups * N, r]."""
+    dev = _check_device(x, w, w_scale, a, b)
+    K = x.shape[-1]
+    G = int(n_groups)
+    if not 1 <= G <= _native.WSL_MAX_GROUPS:
+        raise ValueError(f"n_groups must be in [1, {_native.WSL_MAX_GROUPS}], got {G}")
+    lead = x.shape[:-1]
+    x2 = _row_major(x.reshape(-1, K), "x")
+    M = x2.shape[0]
+    if x2.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16, got {x2.dtype}")
+    w = _row_major(w, "w")
+    base_n = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"w is {tuple(w.shape)} but x has K={K}")
+    w_dtype = _native.WSL_DTYPE_BF16
+    if w.dtype == _FP8:
+        w_dtype = _fp8_code()
+        if w_scale is None or w_scale.dtype != torch.float32 or w_scale.shape != (base_n,):
+            raise ValueError(f"an fp8 w needs w_scale fp32 [{base_n}]")
+        w_scale = w_scale.contiguous()
+    elif w.dtype != torch.bfloat16:
+        raise TypeError(f"w must be bfloat16 or float8_e4m3fn, got {w.dtype}")
+    elif w_scale is not None:
+        raise ValueError("w_scale is only valid with an fp8 w")
+    r = 0
+    N = base_n
+    if a is not None or b is not None:
+        if a is None or b is None:
+            raise ValueError("a and b must be given together")
+        a = _row_major(a, "a")
+        b = _row_major(b, "b")
+        r = b.shape[1]
+        if b.shape[0] % G != 0 or a.shape != (G * r, K):
+            raise ValueError(f"LoRA shapes a {tuple(a.shape)}, b {tuple(b.shape)} do not match {G} groups, K={K}")
+        N = b.shape[0] // G
+        if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+            raise TypeError("a and b must be bfloat16")
+    if N % base_n != 0 or base_n % int(g) != 0:
+        raise ValueError(f"broadcast needs N % base_n == 0 and base_n % g == 0 (N {N}, base_n {base_n}, g {g})")
+    y = torch.empty((M, G * N), dtype=torch.bfloat16, device=dev)
+    if M > 0:
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws = workspace(dev, stream, _native.bcast_workspace_bytes(M, N, K, r, G, w_dtype))
+        with torch.cuda.device(dev):
+            rc = _native.lib().wsl_lora_linear_bcast_fwd(
+                x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), w_dtype, _dev_ptr(w_scale),
+                _dev_ptr(a), a.stride(0) if a is not None else 0, _dev_ptr(b), b.stride(0) if b is not None else 0,
+                float(scale), y.data_ptr(), y.stride(0), M, N, K, r, base_n, int(g), G,
+                ws.data_ptr(), ws.numel(), stream)
+        if rc != _native.WSL_OK:
+            _retire((dev.index, stream, "lora"))
+        _native.check(rc, "wsl_lora_linear_bcast_fwd")
+    return y.reshape(*lead, G * N)
+
+
+@lora_linear_bcast_op.register_fake
+def _lora_linear_bcast_fake(x, w, w_scale, a, b, scale, g, n_groups):
+    N = b.shape[0] // int(n_groups) if b is not None else w.shape[0]
+    return x.new_empty((*x.shape[:-1], int(n_groups) * N), dtype=torch.bfloat16)
+
+
+def _lora_linear_bcast_setup(ctx, inputs, output):
+    x, w, w_scale, a, b, scale, g, n_groups = inputs
+    ctx.save_for_backward(x, w, w_scale, a, b)
+    ctx.scale = scale
+    ctx.g = int(g)
+    ctx.G = int(n_groups)
+
+
+def _lora_linear_bcast_backward(ctx, gy):
+    """Backward of ``wsl::lora_linear_bcast``. Every output column c of group j reads base row
+    base(c) = (c / (hpg D)) D + c % D, so W's gradient gathers them: with gy_b [M, base_n]
+    the sum of gy over the groups and the heads of each template,
+
+        dx = gy_b . W + scale * (gy . Bd) . a       two launches of the fused kernel
+        dW = gy_b^T . x
+        da = scale * (gy . Bd)^T . x,   db_j = scale * gy_j^T . (x . a_j^T)
+
+    (Bd: b block-diagonal over the groups). The reference differentiates broadcast_add's
+    expand and the separate projections (torchtitan/models/llama3/model/model.py:111-145,
+    381-398); these are the same sums."""
+    x, w, w_scale, a, b, scale = *ctx.saved_tensors, ctx.scale
+    s = float(scale)
+    G, g = ctx.G, ctx.g
+    need_x, need_w, _, need_a, need_b, _, _, _ = ctx.needs_input_grad
+    K = x.shape[-1]
+    base_n = w.shape[0]
+    gy2 = _row_major(gy.reshape(-1, gy.shape[-1]).to(torch.bfloat16), "grad_y")
+    M = gy2.shape[0]
+    N = gy2.shape[1] // G
+    D = base_n // g
+    hpg = N // base_n
+    x2 = x.reshape(-1, K)
+    gyb = gy2.float().view(M, G, g, hpg, D).sum(dim=(1, 3)).reshape(M, base_n).to(torch.bfloat16)
+    has_lora = a is not None and b is not None and b.shape[1] > 0
+    r = b.shape[1] if has_lora else 0
+    bd = _block_diag_rows(b, [N] * G, r) if has_lora else None
+    dx = dw = da = db = None
+    if need_x:
+        wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous() if w.dtype == _FP8 else _transposed(w)
+        dx = lora_linear_op(gyb, wt, None, None, None, 0.0)
+        if has_lora:
+            dx = dx + lora_linear_op(gy2, None, None, bd.t().contiguous(), a.t().contiguous(), s)
+        dx = dx.reshape(x.shape)
+    if need_w and w.dtype == torch.bfloat16:
+        dw = torch.mm(gyb.t(), x2)
+    if has_lora and (need_a or need_b):
+        zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)
+        if need_a:
+            da = torch.addmm(zero, torch.mm(gy2, bd).t(), x2, beta=0, alpha=s)
+        if need_b:
+            t = torch.mm(x2, a.t().contiguous())
+            full = torch.addmm(zero, gy2.t(), t, beta=0, alpha=s)
+            db = torch.empty_like(b)
+            for j in range(G):
+                db[j * N:(j + 1) * N] = full[j * N:(j + 1) * N, j * r:(j + 1) * r]
+    return dx, dw, None, da, db, None, None, None
+
+
+lora_linear_bcast_op.register_autograd(_lora_linear_bcast_backward, setup_context=_lora_linear_bcast_setup)
+
+
 def _block_diag_rows(b: torch.Tensor, group_n, r: int) -> torch.Tensor:
     """[N, G*r] with group g's rows of b in column block g and zeros elsewhere."""
     out = b.new_zeros(b.shape[0], len(group_n) * r)
@@ -504,7 +634,14 @@ def _autocast_factorized_embedding(_ks, ids, emb, proj):
         return factorized_embedding_op(ids, autocast_operand(emb), autocast_operand(proj))
 
 
+def _autocast_lora_linear_bcast(_ks, x, w, w_scale, a, b, scale, g, n_groups):
+    with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYS):
+        return lora_linear_bcast_op(autocast_operand(x), autocast_operand(w), w_scale, autocast_operand(a),
+                                    autocast_operand(b), scale, g, n_groups)
+
+
 _autocast_lib.impl("lora_linear", _autocast_lora_linear, "AutocastCUDA", with_keyset=True)
+_autocast_lib.impl("lora_linear_bcast", _autocast_lora_linear_bcast, "AutocastCUDA", with_keyset=True)
 _autocast_lib.impl("lora_linear_grouped", _autocast_lora_linear_grouped, "AutocastCUDA", with_keyset=True)
 _autocast_lib.impl("factorized_embedding", _autocast_factorized_embedding, "AutocastCUDA", with_keyset=True)
 
