@@ -425,9 +425,11 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
     trainer's case; each layer has its own inputs, the three projections of a layer that
     read one activation share it, as q/k/v and gate/up do). Timed eagerly with HIP events around loss.backward() only; the
     forward runs untimed before each step. Three paths on the same inputs: the fused op
-    (dx on the fused kernel, weight gradients on hipBLASLt), the grouped op for q|k|v and
-    gate|up (stacked parameters), and torch autograd of the reference's unfused arithmetic
-    x.W^T + s (x.A^T).B^T."""
+    (dx on the fused kernel, weight gradients by wsl_lora_linear_bwd_weights), the grouped
+    op for q|k|v and gate|up (stacked parameters), and torch autograd of the reference's
+    unfused arithmetic x.W^T + s (x.A^T).B^T. "weight_grads" times dW, dA and dB alone per
+    projection shape: the HIP entry point against the same three products on torch GEMMs
+    (hipBLASLt)."""
     from weightshared_torchtitan_amd import lora_linear
     g = torch.Generator(device=dev).manual_seed(12)
     Ws = [(torch.randn(N, K, device=dev, generator=g) * 0.02).bfloat16().requires_grad_(True)
@@ -489,6 +491,46 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
         ms = timed(fwd, grads)
         out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
                      "frac_mfma": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+    from weightshared_torchtitan_amd import ops
+
+    def wg_ms(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    wg = {}
+    tot_hip = tot_torch = 0.0
+    for i, (name, N, K) in enumerate(QWEN3_0P6B):
+        x2, gy2 = xs[0][K].detach(), gys[i]
+        a, b = lor[0][i][0].detach(), lor[0][i][1].detach()
+        hip = wg_ms(lambda: ops.lora_linear_weight_grads_op(x2, gy2, a, b, 2.0, True, True, True))
+        tch = wg_ms(lambda: ops._weight_grads_torch(x2, gy2, a, b, 2.0, True, True, True))
+        fl = 2.0 * M * (N * K + r * (N + K)) + 2.0 * M * r * (N + K)  # dW, dA, dB + the T, U pre-passes
+        wg[name] = {"N": N, "K": K, "hip_ms": round(hip, 4), "torch_ms": round(tch, 4),
+                    "hip_TFLOP/s": round(fl / hip / 1e9, 1), "torch_TFLOP/s": round(fl / tch / 1e9, 1)}
+        tot_hip += hip
+        tot_torch += tch
+    # config 2's own projection shape (N = K = 4096)
+    x2 = torch.randn(M, 4096, device=dev, generator=g).bfloat16()
+    gy2 = torch.randn(M, 4096, device=dev, generator=g).bfloat16()
+    a = (torch.randn(r, 4096, device=dev, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(4096, r, device=dev, generator=g) * 0.02).bfloat16()
+    hip = wg_ms(lambda: ops.lora_linear_weight_grads_op(x2, gy2, a, b, 2.0, True, True, True))
+    tch = wg_ms(lambda: ops._weight_grads_torch(x2, gy2, a, b, 2.0, True, True, True))
+    fl = 2.0 * M * (4096 * 4096 + r * 8192) + 2.0 * M * r * 8192
+    out["weight_grads"] = {"per_projection": wg, "layer_hip_ms": round(tot_hip, 4),
+                           "layer_torch_ms": round(tot_torch, 4),
+                           "c2_N4096_K4096": {"hip_ms": round(hip, 4), "torch_ms": round(tch, 4),
+                                              "hip_TFLOP/s": round(fl / hip / 1e9, 1),
+                                              "torch_TFLOP/s": round(fl / tch / 1e9, 1)}}
+    del x2, gy2, a, b
     del Ws, xs, lor, gys, gWs, glor, ggys, params
     torch.cuda.empty_cache()
     return out

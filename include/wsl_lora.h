@@ -191,6 +191,37 @@ int wsl_lora_linear_bcast_fwd(const void* x, int64_t ldx,
                               void* stream);
 
 /*
+ * Weight gradients of y = x . W^T + scale * (x . a^T) . b^T, given gy = dL/dy:
+ *
+ *   dw = gy^T . x                  [N, K]   (row stride lddw)
+ *   da = scale * (gy . b)^T . x    [r, K]   (row stride ldda)
+ *   db = scale * gy^T . (x . a^T)  [N, r]   (row stride lddb)
+ *
+ * (scale * gy . b and scale * x . a^T are rounded to bf16 once, as the forward's rank
+ * pre-pass rounds its T.) Replaces what torch autograd computes for the reference's
+ * LoRAModule.forward (torchtitan/models/llama3/model/model.py:189-192) and the base
+ * nn.Linear (:257-273) composed by broadcast_add (:392-398), as run by the trainer's
+ * loss.backward() (torchtitan/train.py:456); the reference has no kernel of its own.
+ * All tensors bf16 [rows, ld]; x [M, K], gy [M, N], a [r, K], b [N, r]. Any of dw, da, db
+ * may be NULL (not computed); da and db need r > 0. Deterministic: split reductions are
+ * summed in a fixed order. The layouts taken (wsl_lora_linear_bwd_weights_supported): K and
+ * N multiples of 64, r a multiple of 8, x, gy, a, b 16-byte aligned with leading dimensions
+ * multiples of 8; anything else returns WSL_E_SHAPE. Workspace (256-byte aligned) from
+ * wsl_lora_linear_bwd_weights_workspace_bytes; it may be the forward's workspace (the
+ * decode path's counter prefix is left as it is).
+ */
+int wsl_lora_linear_bwd_weights_supported(const void* x, int64_t ldx, const void* gy, int64_t ldg,
+                                          const void* a, int64_t lda, const void* b, int64_t ldb,
+                                          int64_t M, int64_t N, int64_t K, int64_t r);
+int wsl_lora_linear_bwd_weights_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, size_t* bytes);
+int wsl_lora_linear_bwd_weights(const void* x, int64_t ldx, const void* gy, int64_t ldg,
+                                const void* a, int64_t lda, const void* b, int64_t ldb,
+                                float scale, int64_t M, int64_t N, int64_t K, int64_t r,
+                                void* dw, int64_t lddw, void* da, int64_t ldda, void* db, int64_t lddb,
+                                void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/*
  * Factorized embedding:  out[t, :] = E[ids[t], :] . P^T      (k -> hidden)
  *
  * Replaces the reference's token embedding nn.Embedding(vocab, dim)

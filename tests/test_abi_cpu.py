@@ -208,6 +208,24 @@ def test_grouped_op_fake_kernel_shapes():
     assert y.shape == (3, 5, 96) and y.dtype == torch.bfloat16 and y.device.type == "meta"
 
 
+def test_weight_grads_op_fake_kernel_shapes():
+    # the meta implementation gives dW [N, K], dA [r, K], dB [N, r] bf16 and an empty tensor
+    # for each gradient not asked for, as the device op does
+    import torch
+
+    from weightshared_torchtitan_amd import ops
+    with torch.device("meta"):
+        x = torch.empty(40, 64, dtype=torch.bfloat16)
+        gy = torch.empty(40, 128, dtype=torch.bfloat16)
+        a = torch.empty(8, 64, dtype=torch.bfloat16)
+        b = torch.empty(128, 8, dtype=torch.bfloat16)
+        dw, da, db = ops.lora_linear_weight_grads_op(x, gy, a, b, 2.0, True, True, True)
+        none = ops.lora_linear_weight_grads_op(x, gy, a, b, 2.0, True, False, False)
+    assert (dw.shape, da.shape, db.shape) == ((128, 64), (8, 64), (128, 8))
+    assert all(t.dtype == torch.bfloat16 and t.device.type == "meta" for t in (dw, da, db))
+    assert none[0].shape == (128, 64) and none[1].numel() == 0 and none[2].numel() == 0
+
+
 @needs_lib
 def test_decode_step_validation_codes():
     lib = N.lib()
@@ -375,3 +393,56 @@ def test_noalloc_scratch_size_matches_header():
     assert N.WSL_NOALLOC_SCRATCH_BYTES == 64 * 1024 * 1024
     text = open(HEADER).read()
     assert "#define WSL_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)" in text
+
+
+def _bwd_weights(**kw):
+    a = dict(x=P, ldx=64, gy=P, ldg=128, a=P, lda=64, b=P, ldb=8, scale=2.0, M=4, N=128, K=64, r=8,
+             dw=P, lddw=64, da=P, ldda=64, db=P, lddb=8, ws=None, ws_bytes=0, stream=None)
+    a.update(kw)
+    return N.lib().wsl_lora_linear_bwd_weights(a["x"], a["ldx"], a["gy"], a["ldg"], a["a"], a["lda"], a["b"],
+                                               a["ldb"], a["scale"], a["M"], a["N"], a["K"], a["r"], a["dw"],
+                                               a["lddw"], a["da"], a["ldda"], a["db"], a["lddb"], a["ws"],
+                                               a["ws_bytes"], a["stream"])
+
+
+@needs_lib
+@pytest.mark.parametrize("kw,code", [
+    (dict(x=None), N.WSL_E_INVALID_ARG),
+    (dict(a=None), N.WSL_E_INVALID_ARG),
+    (dict(r=0), N.WSL_E_INVALID_ARG),            # da, db asked for without a rank
+    (dict(ldx=63), N.WSL_E_SHAPE),
+    (dict(ldg=127), N.WSL_E_SHAPE),
+    (dict(lddb=7), N.WSL_E_SHAPE),
+    (dict(dw=P + 1), N.WSL_E_ALIGN),
+    (dict(K=72, ldx=72, lda=72, lddw=72, ldda=72), N.WSL_E_SHAPE),  # K off the 64 grid: not taken
+    (dict(x=P + 2), N.WSL_E_SHAPE),              # x not 16-byte aligned: not taken
+    (dict(), N.WSL_E_WORKSPACE),                 # no workspace
+])
+def test_bwd_weights_validation_codes(kw, code):
+    """Every refusal happens on the host, before any device is touched."""
+    assert _bwd_weights(**kw) == code
+    assert N.last_error() != ""
+
+
+@needs_lib
+def test_bwd_weights_nothing_to_do_is_a_no_op():
+    assert _bwd_weights(M=0, x=None, gy=None) == N.WSL_OK
+    assert _bwd_weights(dw=None, da=None, db=None) == N.WSL_OK
+
+
+@needs_lib
+@pytest.mark.parametrize("K,r,x,ok", [(64, 8, P, 1), (72, 8, P, 0), (64, 12, P, 0), (64, 8, P + 8, 0), (64, 0, P, 1)])
+def test_bwd_weights_supported_answers_from_layout(K, r, x, ok):
+    L = N.lib()
+    assert L.wsl_lora_linear_bwd_weights_supported(x, K, P, 128, P, K, P, max(r, 8), 256, 128, K, r) == ok
+    assert N.last_error() == ""
+
+
+@needs_lib
+def test_bwd_weights_workspace_holds_transposes_and_partials():
+    """The weight-gradient workspace holds at least the token-contiguous copies of x, gy
+    and T, U ((K + r + N + r) x M bf16) beside the counter prefix and its halves."""
+    M, Nn, K, r = 8192, 1024, 1024, 32
+    got = N.bwd_weights_workspace_bytes(M, Nn, K, r)
+    assert got >= 65536 + 2 * (K + r + Nn + r) * M * 2
+    assert N.bwd_weights_workspace_bytes(0, Nn, K, r) >= 65536

@@ -42,6 +42,9 @@ EXPORTED = (
     "wsl_lora_linear_grouped_fwd",
     "wsl_lora_linear_bcast_workspace_bytes",
     "wsl_lora_linear_bcast_fwd",
+    "wsl_lora_linear_bwd_weights_supported",
+    "wsl_lora_linear_bwd_weights_workspace_bytes",
+    "wsl_lora_linear_bwd_weights",
     "wsl_factorized_embedding_fwd",
     "wsl_last_error",
     "wsl_version",
@@ -134,6 +137,23 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, _c_i64,                   # y, ldy
         _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
         _c_i64, _c_i64, ctypes.c_int32,  # base_n, g, n_groups
+        _c_vp, ctypes.c_size_t,          # workspace, bytes
+        _c_vp,                           # stream
+    ]
+    lib.wsl_lora_linear_bwd_weights_supported.restype = ctypes.c_int
+    lib.wsl_lora_linear_bwd_weights_supported.argtypes = [
+        _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,  # x, ldx, gy, ldg, a, lda, b, ldb
+        _c_i64, _c_i64, _c_i64, _c_i64]                              # M, N, K, r
+    lib.wsl_lora_linear_bwd_weights_workspace_bytes.restype = ctypes.c_int
+    lib.wsl_lora_linear_bwd_weights_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64,
+                                                                ctypes.POINTER(ctypes.c_size_t)]
+    lib.wsl_lora_linear_bwd_weights.restype = ctypes.c_int
+    lib.wsl_lora_linear_bwd_weights.argtypes = [
+        _c_vp, _c_i64, _c_vp, _c_i64,    # x, ldx, gy, ldg
+        _c_vp, _c_i64, _c_vp, _c_i64,    # a, lda, b, ldb
+        ctypes.c_float,                  # scale
+        _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
+        _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,  # dw, lddw, da, ldda, db, lddb
         _c_vp, ctypes.c_size_t,          # workspace, bytes
         _c_vp,                           # stream
     ]
@@ -260,4 +280,11 @@ def grouped_workspace_bytes(M: int, K: int, r: int, group_n, w_dtype: int) -> in
     check(lib().wsl_lora_linear_grouped_workspace_bytes(M, K, r, len(group_n), group_array(group_n), w_dtype,
                                                         ctypes.byref(out)),
           "wsl_lora_linear_grouped_workspace_bytes")
+    return int(out.value)
+
+
+def bwd_weights_workspace_bytes(M: int, N: int, K: int, r: int) -> int:
+    out = ctypes.c_size_t(0)
+    check(lib().wsl_lora_linear_bwd_weights_workspace_bytes(M, N, K, r, ctypes.byref(out)),
+          "wsl_lora_linear_bwd_weights_workspace_bytes")
     return int(out.value)

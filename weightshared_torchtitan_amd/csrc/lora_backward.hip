@@ -1,0 +1,295 @@
+// Weight gradients of the fused LoRA linear (y = x . W^T + s (x . A^T) . B^T) on gfx950:
+//
+//   dW = gy^T . x            [N, K]
+//   dA = s (gy . B)^T . x    [r, K]
+//   dB = s gy^T . (x . A^T)  [N, r]
+//
+// dW reduces over the M tokens of two operands that store tokens as rows. The tile kernel
+// of the forward reduces along a contiguous K, so x and gy are transposed once into
+// token-contiguous rows (tokens zero-padded to Mp): xt [K, Mp], gt [N, Mp], and
+// dW = gt . xt^T is that kernel's product. An output too small to fill the 256 CUs splits
+// the token reduction into equal parts (fp32 partials) that a reduce kernel sums in split
+// order (deterministic), rounding once to bf16.
+//
+// With dW at hand, dA and dB follow from it by associativity, as products over K or N
+// instead of over the tokens:
+//
+//   dB = s (gy^T . x) . A^T = s dW . A^T        dA = s B^T . (gy^T . x) = s B^T . dW
+//
+// 2 N K r multiply-adds each instead of 2 M r (N + K) for the rank projections T = x . A^T,
+// U = gy . B and their products: both read the bf16 dW (dA through its transpose) and
+// nothing of size M. Without dW (a frozen base) they take the token route instead:
+// T = bf16(s x . A^T) and U = bf16(s gy . B) from the forward's rank pre-pass, transposed
+// beside x and gy (xt = [x^T ; T^T], gt = [gy^T ; U^T]), dB = gt[0,N) . xt[K,K+r)^T,
+// dA = gt[N,N+r) . xt[0,K)^T.
+//
+// The reference has no backward of its own: torch autograd differentiates LoRAModule.forward
+// (torchtitan/models/llama3/model/model.py:189-192) and the base nn.Linear (:257-273)
+// composed by broadcast_add (:392-398); the trainer runs it at torchtitan/train.py:456.
+#include "wsl_common.h"
+
+namespace wsl {
+
+namespace {
+
+constexpr int TT = 64;       // transpose tile: 64 rows x 64 columns
+constexpr int TS = TT + 2;   // its LDS row stride in bf16 (odd word count: spread banks)
+
+// dst[c][i] = src[i][c] for i < R and 0 for R <= i < Rp (tokens padded to the split grid),
+// c < C. 16-byte global accesses both ways (C % 8 == 0, Rp % 8 == 0, 16-byte aligned rows).
+__global__ void __launch_bounds__(256) transpose_pad_kernel(const uint16_t* __restrict__ src, int64_t lds_,
+                                                           int64_t R, int64_t C, uint16_t* __restrict__ dst,
+                                                           int64_t ldd, int64_t Rp) {
+  __shared__ uint32_t tile[TT * TS / 2];
+  const uint16_t* t16 = reinterpret_cast<const uint16_t*>(tile);
+  const int64_t r0 = (int64_t)blockIdx.y * TT, c0 = (int64_t)blockIdx.x * TT;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + 256 * i, row = idx >> 3, ch = idx & 7;
+    const int64_t r = r0 + row, c = c0 + ch * 8;
+    u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+    if (r < R && c < C) v = *reinterpret_cast<const u32x4_t*>(src + r * lds_ + c);
+    uint32_t* d = tile + (row * TS + ch * 8) / 2;  // TS even, ch * 8 even: word aligned
+    d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + 256 * i, q = idx & 7, c = idx >> 3;  // 8 lanes: one 128-byte output row piece
+    if (c0 + c >= C || r0 + q * 8 >= Rp) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)t16[(q * 8 + 2 * j) * TS + c] | ((uint32_t)t16[(q * 8 + 2 * j + 1) * TS + c] << 16);
+    *reinterpret_cast<u32x4_t*>(dst + (c0 + c) * ldd + r0 + q * 8) = u32x4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// Four bf16 of row-major `d` (8-byte pieces when `vec`).
+__device__ __forceinline__ void store4(uint16_t* d, f32x4_t v, bool vec) {
+  if (vec) {
+    *reinterpret_cast<uint2*>(d) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  } else {
+    d[0] = f32_to_bf16_bits(v[0]); d[1] = f32_to_bf16_bits(v[1]);
+    d[2] = f32_to_bf16_bits(v[2]); d[3] = f32_to_bf16_bits(v[3]);
+  }
+}
+
+// dst = bf16(scale * sum over the splits of part[s]) for an fp32 [splits][rows][cols] partial
+// product, splits in order; four consecutive columns per thread (cols % 4 == 0).
+__global__ void __launch_bounds__(256) split_sum_kernel(const float* __restrict__ part, int splits, int64_t rows,
+                                                       int64_t cols, float scale, uint16_t* __restrict__ dst,
+                                                       int64_t ldd, int vec) {
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  const int64_t slice = rows * cols;
+  if (e >= slice) return;
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + e);
+  for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4_t*>(part + (int64_t)s * slice + e);
+  store4(dst + (e / cols) * ldd + e % cols, v * scale, vec != 0);
+}
+
+// dW = bf16(sum over the splits of part[s]) ([splits][N][K] fp32, splits in order) to the
+// caller's dw (row stride lddw, 8-byte pieces when `vec`), to the contiguous copy dwc
+// [N][K] when given, and transposed to dwt [K][N] when given. 64 x 64 tiles (N % 64 ==
+// K % 64 == 0); the transpose goes through LDS as in transpose_pad_kernel.
+__global__ void __launch_bounds__(256) dw_reduce_kernel(const float* __restrict__ part, int splits, int64_t N,
+                                                       int64_t K, uint16_t* __restrict__ dw, int64_t lddw, int vec,
+                                                       uint16_t* __restrict__ dwc, uint16_t* __restrict__ dwt) {
+  __shared__ uint32_t tile[TT * TS / 2];
+  const uint16_t* t16 = reinterpret_cast<const uint16_t*>(tile);
+  const int64_t n0 = (int64_t)blockIdx.y * TT, k0 = (int64_t)blockIdx.x * TT;
+  const int tid = threadIdx.x;
+  const int64_t slice = N * K;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = tid / 16 + 16 * i, col = (tid % 16) * 4;
+    const int64_t e = (n0 + row) * K + k0 + col;
+    f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + e);
+    for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4_t*>(part + (int64_t)s * slice + e);
+    store4(dw + (n0 + row) * lddw + k0 + col, v, vec != 0);
+    const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
+    if (dwc != nullptr) *reinterpret_cast<uint2*>(dwc + e) = uint2{lo, hi};
+    uint32_t* d = tile + (row * TS + col) / 2;
+    d[0] = lo; d[1] = hi;
+  }
+  if (dwt == nullptr) return;  // uniform over the workgroup
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + 256 * i, q = idx & 7, c = idx >> 3;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)t16[(q * 8 + 2 * j) * TS + c] | ((uint32_t)t16[(q * 8 + 2 * j + 1) * TS + c] << 16);
+    *reinterpret_cast<u32x4_t*>(dwt + (k0 + c) * N + n0 + q * 8) = u32x4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
+hipError_t transpose_pad(const void* src, int64_t lds_, int64_t R, int64_t C, uint16_t* dst, int64_t ldd,
+                         int64_t Rp, hipStream_t st) {
+  if (C == 0 || Rp == 0) return hipSuccess;
+  const dim3 grid((unsigned)((C + TT - 1) / TT), (unsigned)((Rp + TT - 1) / TT));
+  transpose_pad_kernel<<<grid, dim3(256), 0, st>>>(reinterpret_cast<const uint16_t*>(src), lds_, R, C, dst, ldd, Rp);
+  return hipGetLastError();
+}
+
+size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+// Workspace plan. It depends on the sizes only, so the workspace query needs no flags: the
+// union of both routes' buffers.
+struct Plan {
+  int sw;          // token splits of the dW product
+  int sb, sa;      // token route: token splits of the dB and dA products
+  int sdb, sda;    // dW route: splits of dB = s dW . A^T (over K) and dA = s B^T . dW (over N)
+  int64_t Mp;      // tokens padded to 64 x the largest token split count
+  size_t off_t, off_u, off_bt, off_xt, off_gt, off_dwc, off_dwt, off_part, total;
+};
+
+Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t r) {
+  Plan L{};
+  const int64_t nk = (M + 63) / 64;
+  L.sw = product_splits(N, K, nk, false);
+  L.sb = r > 0 ? product_splits(N, r, nk, false) : 1;
+  L.sa = r > 0 ? product_splits(r, K, nk, false) : 1;
+  L.sdb = r > 0 ? product_splits(N, r, K / 64, true) : 1;
+  L.sda = r > 0 ? product_splits(r, K, N / 64, true) : 1;
+  int smax = L.sw > L.sb ? L.sw : L.sb;
+  if (L.sa > smax) smax = L.sa;
+  const int64_t grid = 64 * (int64_t)smax;
+  L.Mp = (M + grid - 1) / grid * grid;
+  size_t off = 0;
+  L.off_t = off;   off = a256(off + (r > 0 ? rank_prepass_bytes(M, K, r) : 0));
+  L.off_u = off;   off = a256(off + (r > 0 ? rank_prepass_bytes(M, N, r) : 0));
+  L.off_bt = off;  off = a256(off + (size_t)r * N * 2);
+  L.off_xt = off;  off = a256(off + (size_t)(K + r) * L.Mp * 2);
+  L.off_gt = off;  off = a256(off + (size_t)(N + r) * L.Mp * 2);
+  L.off_dwc = off; off = a256(off + (r > 0 ? (size_t)N * K * 2 : 0));
+  L.off_dwt = off; off = a256(off + (r > 0 ? (size_t)N * K * 2 : 0));
+  L.off_part = off;
+  size_t part = (size_t)L.sw * N * K;  // worst case: any product may go through partials
+  const size_t cand[4] = {(size_t)L.sb * N * r, (size_t)L.sa * r * K, (size_t)L.sdb * N * r, (size_t)L.sda * r * K};
+  for (size_t c : cand) part = c > part ? c : part;
+  L.total = a256(off + part * 4);
+  return L;
+}
+
+}  // namespace
+
+// Shapes and layouts the weight-gradient path takes: K and N on the 64-element tile grid
+// (the reductions of the dA and dB products and of the token route's pre-passes), ranks in
+// multiples of 8, 16-byte aligned rows, and token counts whose padded transposes keep the
+// tile kernel's 32-bit lane offsets.
+bool weight_grads_supported(const LoraArgs& p, const void* gy, int64_t ldg) {
+  if (p.M < 1 || p.K % 64 != 0 || p.N % 64 != 0 || p.r % 8 != 0) return false;
+  if (p.M > ((int64_t)1 << 22) - 2048 || p.N > ((int64_t)1 << 22) || p.K > ((int64_t)1 << 22)) return false;
+  if (!al16(p.x) || p.ldx % 8 != 0 || !al16(gy) || ldg % 8 != 0) return false;
+  if (p.ldx > ((int64_t)1 << 22) || ldg > ((int64_t)1 << 22)) return false;
+  if (p.r > 0 && (!al16(p.a) || p.lda % 8 != 0 || !al16(p.b) || p.ldb % 8 != 0 || p.lda > ((int64_t)1 << 22)))
+    return false;
+  return true;
+}
+
+size_t weight_grads_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, bool need_w, bool need_ab) {
+  (void)need_w;
+  return make_plan(M, N, K, need_ab ? r : 0).total;
+}
+
+hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, void* dw, int64_t lddw, void* da,
+                               int64_t ldda, void* db, int64_t lddb) {
+  const int64_t M = p.M, N = p.N, K = p.K;
+  const int64_t r = (da != nullptr || db != nullptr) ? p.r : 0;
+  if (r == 0) da = db = nullptr;
+  if (dw == nullptr && r == 0) return hipSuccess;
+  const Plan L = make_plan(M, N, K, r);
+  char* ws = reinterpret_cast<char*>(p.ws);
+  uint16_t* T = reinterpret_cast<uint16_t*>(ws + L.off_t);
+  uint16_t* U = reinterpret_cast<uint16_t*>(ws + L.off_u);
+  uint16_t* Bt = reinterpret_cast<uint16_t*>(ws + L.off_bt);
+  uint16_t* xt = reinterpret_cast<uint16_t*>(ws + L.off_xt);
+  uint16_t* gt = reinterpret_cast<uint16_t*>(ws + L.off_gt);
+  uint16_t* dwc = reinterpret_cast<uint16_t*>(ws + L.off_dwc);
+  uint16_t* dwt = reinterpret_cast<uint16_t*>(ws + L.off_dwt);
+  float* part = reinterpret_cast<float*>(ws + L.off_part);
+  const hipStream_t st = p.stream;
+  hipError_t e = hipSuccess;
+
+  // y' = scale * x' . W'^T [rows, cols] over a reduction of `red` (x', W' rows `red` long,
+  // row strides ldx', ldw'): straight to bf16 when unsplit and the destination takes the
+  // tile store's 8-byte pieces, else through fp32 partials and split_sum_kernel
+  auto product = [&](const void* xa, int64_t ldxa, int64_t rows, const void* wb, int64_t ldwb, int64_t cols,
+                     int64_t red, int splits, float scale, void* dst, int64_t ldd) -> hipError_t {
+    LoraArgs q = p;
+    q.x = xa; q.ldx = ldxa; q.w = wb; q.ldw = ldwb; q.M = rows; q.N = cols; q.yscale = scale;
+    const bool vec = (reinterpret_cast<uintptr_t>(dst) & 7u) == 0 && ldd % 4 == 0;
+    if (splits == 1 && vec) {
+      q.K = red; q.y = dst; q.ldy = ldd;
+      return launch_product(q, nullptr, 1);
+    }
+    q.K = red / splits;
+    hipError_t err = launch_product(q, part, splits);
+    if (err != hipSuccess) return err;
+    const int64_t n4 = rows * cols / 4;
+    split_sum_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st>>>(
+        part, splits, rows, cols, scale, reinterpret_cast<uint16_t*>(dst), ldd, vec ? 1 : 0);
+    return hipGetLastError();
+  };
+
+  if (dw != nullptr) {
+    // ---- dW route: dW over the tokens, then dB = s dW . A^T and dA = s B^T . dW ----
+    e = transpose_pad(p.x, p.ldx, M, K, xt, L.Mp, L.Mp, st);
+    if (e == hipSuccess) e = transpose_pad(gy, ldg, M, N, gt, L.Mp, L.Mp, st);
+    if (e != hipSuccess) return e;
+    const bool direct = L.sw == 1 && al16(dw) && lddw % 8 == 0;
+    const uint16_t* dws = reinterpret_cast<const uint16_t*>(dw);  // bf16 dW rows for dB
+    int64_t ldws = lddw;
+    if (direct) {
+      e = product(gt, L.Mp, N, xt, L.Mp, K, L.Mp, 1, 1.f, dw, lddw);
+      if (e == hipSuccess && da != nullptr) e = transpose_pad(dw, lddw, N, K, dwt, N, N, st);
+    } else {
+      LoraArgs q = p;
+      q.x = gt; q.ldx = L.Mp; q.w = xt; q.ldw = L.Mp; q.M = N; q.N = K; q.K = L.Mp / L.sw;
+      e = launch_product(q, part, L.sw);
+      if (e == hipSuccess) {
+        const bool vec = (reinterpret_cast<uintptr_t>(dw) & 7u) == 0 && lddw % 4 == 0;
+        dw_reduce_kernel<<<dim3((unsigned)(K / TT), (unsigned)(N / TT)), dim3(256), 0, st>>>(
+            part, L.sw, N, K, reinterpret_cast<uint16_t*>(dw), lddw, vec ? 1 : 0, db != nullptr ? dwc : nullptr,
+            da != nullptr ? dwt : nullptr);
+        e = hipGetLastError();
+      }
+      dws = dwc;
+      ldws = K;
+    }
+    if (e == hipSuccess && db != nullptr) e = product(dws, ldws, N, p.a, p.lda, r, K, L.sdb, p.scale, db, lddb);
+    if (e == hipSuccess && da != nullptr) {
+      e = transpose_pad(p.b, p.ldb, N, r, Bt, N, N, st);
+      if (e == hipSuccess) e = product(Bt, N, r, dwt, N, K, N, L.sda, p.scale, da, ldda);
+    }
+    return e;
+  }
+
+  // ---- token route (no dW): T, U by the rank pre-pass, products over the tokens ----
+  if (db != nullptr) {  // T = bf16(s x . A^T)
+    LoraArgs q = p;
+    q.groups = 1;
+    e = rank_prepass(q, T);
+    if (e == hipSuccess) e = transpose_pad(T, r, M, r, xt + K * L.Mp, L.Mp, L.Mp, st);
+    if (e == hipSuccess) e = transpose_pad(gy, ldg, M, N, gt, L.Mp, L.Mp, st);
+    if (e == hipSuccess) e = product(gt, L.Mp, N, xt + K * L.Mp, L.Mp, r, L.Mp, L.sb, 1.f, db, lddb);
+    if (e != hipSuccess) return e;
+  }
+  if (da != nullptr) {  // U = bf16(s gy . B), with B^T [r, N] in the place of A
+    e = transpose_pad(p.b, p.ldb, N, r, Bt, N, N, st);
+    if (e != hipSuccess) return e;
+    LoraArgs q = p;
+    q.x = gy; q.ldx = ldg; q.K = N; q.a = Bt; q.lda = N; q.groups = 1;
+    e = rank_prepass(q, U);
+    if (e == hipSuccess) e = transpose_pad(U, r, M, r, gt + N * L.Mp, L.Mp, L.Mp, st);
+    if (e == hipSuccess) e = transpose_pad(p.x, p.ldx, M, K, xt, L.Mp, L.Mp, st);
+    if (e == hipSuccess) e = product(gt + N * L.Mp, L.Mp, r, xt, L.Mp, K, L.Mp, L.sa, 1.f, da, ldda);
+  }
+  return e;
+}
+
+}  // namespace wsl

@@ -823,6 +823,42 @@ hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
   return launch_rank<kBF16, true>(q, nullptr, 0);
 }
 
+// Plain bf16 products over a long contiguous K (the weight gradients, csrc/lora_backward.hip):
+// y' = yscale * x' . W'^T, x' [M, K], W' [N, K]. The split count (a power of two, each part
+// at least kMinSplitTiles K tiles, dividing the nk K tiles when `divides`): 1 when a tile
+// configuration fills the CUs on its own, else K cut into equal parts over 128 x 128 tiles,
+// fp32 partials. Scored by the fraction of the 256 CUs kept busy, 128 x 128 tiles at 0.78 of
+// the larger tiles' loop rate and split partials at 0.95 for their fp32 round trip.
+constexpr int kMaxProductSplits = 32;
+int product_splits(int64_t M, int64_t N, int64_t nk, bool divides) {
+  const int64_t tb = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t ts = ((M + 127) / 128) * ((N + 127) / 128);
+  double best = wave_efficiency(tb);
+  if (0.78 * wave_efficiency(ts) > best) best = 0.78 * wave_efficiency(ts);
+  int pick = 1;
+  for (int s = 2; s <= kMaxProductSplits && s <= nk / kMinSplitTiles; s *= 2) {
+    if (divides && nk % s != 0) break;
+    const double sc = 0.78 * 0.95 * wave_efficiency(ts * s);
+    if (sc > best + 1e-9) {
+      best = sc;
+      pick = s;
+    }
+  }
+  return pick;
+}
+
+// part == nullptr (splits 1): bf16 y' (p.y, p.ldy) over the whole K by the tile choice of
+// the forward, p.yscale applied; else unscaled fp32 partials [splits][M][N] into `part`, p.K
+// being one part's length (the reduce applies the scale).
+hipError_t launch_product(const LoraArgs& p, float* part, int splits) {
+  LoraArgs q = p;
+  q.w_dtype = kBF16; q.w_scale = nullptr; q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0;
+  q.groups = 1; q.gather = nullptr; q.gather_rows = 0; q.wmap = RowMap{}; q.wrows = q.N;
+  if (part == nullptr) return launch_rank<kBF16, true>(q, nullptr, 0);
+  q.y = part; q.ldy = q.N;
+  return launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
+}
+
 hipError_t launch_prefill(const LoraArgs& p) {
   if (p.gather != nullptr) {
     // factorized embedding: gathered x rows, bf16 base, no LoRA term

@@ -448,6 +448,65 @@ int wsl_lora_linear_bcast_fwd(const void* x, int64_t ldx, const void* w, int64_t
   return run_grouped(p, n_groups, gn, true, workspace, workspace_bytes);
 }
 
+int wsl_lora_linear_bwd_weights_supported(const void* x, int64_t ldx, const void* gy, int64_t ldg, const void* a,
+                                          int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                                          int64_t r) {
+  const bool sizes_ok = validate_sizes(M, N, K, r, WSL_DTYPE_BF16) == WSL_OK && M >= 1;
+  clear_err();  // a query leaves no error behind
+  if (!sizes_ok) return 0;
+  wsl::LoraArgs p = make_args(x, ldx, nullptr, 0, WSL_DTYPE_BF16, nullptr, a, lda, b, ldb, 1.f, nullptr, 0, M, N, K,
+                              r, nullptr);
+  return wsl::weight_grads_supported(p, gy, ldg) ? 1 : 0;
+}
+
+int wsl_lora_linear_bwd_weights_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, size_t* bytes) {
+  clear_err();
+  if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
+  const int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
+  if (rc != WSL_OK) return rc;
+  *bytes = layout_bytes(M > 0 ? wsl::weight_grads_workspace_bytes(M, N, K, r, true, true) : 0);
+  return WSL_OK;
+}
+
+int wsl_lora_linear_bwd_weights(const void* x, int64_t ldx, const void* gy, int64_t ldg, const void* a, int64_t lda,
+                                const void* b, int64_t ldb, float scale, int64_t M, int64_t N, int64_t K, int64_t r,
+                                void* dw, int64_t lddw, void* da, int64_t ldda, void* db, int64_t lddb,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  clear_err();
+  int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
+  if (rc != WSL_OK) return rc;
+  if (r == 0 && (da != nullptr || db != nullptr)) return fail(WSL_E_INVALID_ARG, "da and db need r > 0");
+  if (M == 0 || (dw == nullptr && da == nullptr && db == nullptr)) return WSL_OK;
+  if (x == nullptr || gy == nullptr) return fail(WSL_E_INVALID_ARG, "x and gy must not be NULL");
+  if (r > 0 && (a == nullptr || b == nullptr)) return fail(WSL_E_INVALID_ARG, "r > 0 needs a and b");
+  if (ldx < K) return fail(WSL_E_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
+  if (ldg < N) return fail(WSL_E_SHAPE, "ldg (%lld) < N (%lld)", (long long)ldg, (long long)N);
+  if (r > 0 && lda < K) return fail(WSL_E_SHAPE, "lda (%lld) < K (%lld)", (long long)lda, (long long)K);
+  if (r > 0 && ldb < r) return fail(WSL_E_SHAPE, "ldb (%lld) < r (%lld)", (long long)ldb, (long long)r);
+  if (dw != nullptr && lddw < K) return fail(WSL_E_SHAPE, "lddw (%lld) < K (%lld)", (long long)lddw, (long long)K);
+  if (da != nullptr && ldda < K) return fail(WSL_E_SHAPE, "ldda (%lld) < K (%lld)", (long long)ldda, (long long)K);
+  if (db != nullptr && lddb < r) return fail(WSL_E_SHAPE, "lddb (%lld) < r (%lld)", (long long)lddb, (long long)r);
+  if (((uintptr_t)dw & 1) || ((uintptr_t)da & 1) || ((uintptr_t)db & 1))
+    return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
+  wsl::LoraArgs p = make_args(x, ldx, nullptr, 0, WSL_DTYPE_BF16, nullptr, a, lda, b, ldb, scale, nullptr, 0, M, N, K,
+                              r, stream);
+  if (!wsl::weight_grads_supported(p, gy, ldg))
+    return fail(WSL_E_SHAPE, "layout not taken by the weight-gradient path (K, N multiples of 64, r of 8, "
+                             "16-byte aligned operands, leading dimensions multiples of 8)");
+  const size_t need = wsl::weight_grads_workspace_bytes(M, N, K, r, true, true);
+  if (workspace == nullptr || workspace_bytes < layout_bytes(need))
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", layout_bytes(need), workspace_bytes);
+  if ((uintptr_t)workspace & 255) return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
+  rc = check_device();
+  if (rc != WSL_OK) return rc;
+  const size_t half = half_of(workspace_bytes);
+  p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes + half;
+  p.ws_bytes = half;
+  const hipError_t e = wsl::launch_weight_grads(p, gy, ldg, dw, lddw, da, ldda, db, lddb);
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
 int wsl_lora_linear_fused_supported(int64_t M, int64_t N, int64_t K, int64_t r, int32_t fuse) {
   const bool sizes_ok = validate_sizes(M, N, K, r, WSL_DTYPE_BF16) == WSL_OK && M >= 1;
   clear_err();  // a query leaves no error behind

@@ -146,6 +146,17 @@ hipError_t launch_prefill(const LoraArgs& p);
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool prefill_supported(const LoraArgs& p);
 bool prefill_groups_supported(const LoraArgs& p);
+// Plain bf16 products over a long contiguous K (csrc/lora_prefill.hip) and the rank
+// pre-pass T = bf16(s x . A^T), for the weight gradients (csrc/lora_backward.hip).
+int product_splits(int64_t M, int64_t N, int64_t nk, bool divides);
+hipError_t launch_product(const LoraArgs& p, float* part, int splits);
+size_t rank_prepass_bytes(int64_t M, int64_t K, int64_t rt);
+hipError_t rank_prepass(const LoraArgs& p, uint16_t* t);
+// Weight gradients dW = gy^T x, dA = s (gy B)^T x, dB = s gy^T (x A^T) (csrc/lora_backward.hip).
+bool weight_grads_supported(const LoraArgs& p, const void* gy, int64_t ldg);
+size_t weight_grads_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, bool need_w, bool need_ab);
+hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, void* dw, int64_t lddw, void* da,
+                               int64_t ldda, void* db, int64_t lddb);
 
 // fp8 matrix-core prefill path (csrc/lora_prefill_fp8.hip): T from the rank pre-pass, the
 // activation codes and per-token scales in `scratch` (prefill_fp8_workspace_bytes).

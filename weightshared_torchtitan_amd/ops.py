@@ -204,6 +204,92 @@ def clear_transpose_cache() -> None:
     _WT_CACHE.clear()
 
 
+def _weight_grads_torch(x2, gy2, a, b, s, need_w, need_a, need_b):
+    """The same gradients by torch GEMMs on the device, for layouts the HIP path does not
+    take (K or N off the 64 grid, r not a multiple of 8, unaligned operands)."""
+    dw = torch.mm(gy2.t(), x2) if need_w else None
+    da = db = None
+    zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)  # beta = 0: s rides on alpha
+    if need_a:
+        da = torch.addmm(zero, torch.mm(gy2, b).t(), x2, beta=0, alpha=s)
+    if need_b:
+        db = torch.addmm(zero, gy2.t(), torch.mm(x2, a.t().contiguous()), beta=0, alpha=s)
+    return dw, da, db
+
+
+@torch.library.custom_op("wsl::lora_linear_weight_grads", mutates_args=(), device_types="cuda")
+def lora_linear_weight_grads_op(x: torch.Tensor, gy: torch.Tensor, a: Optional[torch.Tensor],
+                                b: Optional[torch.Tensor], scale: float, need_w: bool, need_a: bool,
+                                need_b: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """dw = gy^T . x [N, K], da = scale (gy . b)^T . x [r, K], db = scale gy^T . (x . a^T)
+    [N, r], each only when asked for (else an empty tensor), bf16 from bf16 x [M, K],
+    gy [M, N], a [r, K], b [N, r] (wsl_lora_linear_bwd_weights: one transpose of x and gy
+    to token-contiguous rows, then the fused kernel's tile loop on each product)."""
+    dev = _check_device(x, gy, a, b)
+    x2 = _row_major(x.reshape(-1, x.shape[-1]), "x")
+    gy2 = _row_major(gy.reshape(-1, gy.shape[-1]), "grad_y")
+    M, K = x2.shape
+    N = gy2.shape[1]
+    if gy2.shape[0] != M:
+        raise ValueError(f"x has {M} rows but grad_y has {gy2.shape[0]}")
+    if x2.dtype != torch.bfloat16 or gy2.dtype != torch.bfloat16:
+        raise TypeError("x and grad_y must be bfloat16")
+    r = 0
+    if need_a or need_b:
+        if a is None or b is None:
+            raise ValueError("da and db need a and b")
+        a = _row_major(a, "a")
+        b = _row_major(b, "b")
+        r = a.shape[0]
+        if a.shape[1] != K or b.shape != (N, r):
+            raise ValueError(f"LoRA shapes a {tuple(a.shape)}, b {tuple(b.shape)} do not match K={K}, N={N}")
+        if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+            raise TypeError("a and b must be bfloat16")
+    empty = lambda: x2.new_empty(0)  # a fresh one per unused output: returns may not alias
+    if M == 0:
+        return (x2.new_zeros(N, K) if need_w else empty(), x2.new_zeros(r, K) if need_a else empty(),
+                x2.new_zeros(N, r) if need_b else empty())
+    L = _native.lib()
+    supported = L.wsl_lora_linear_bwd_weights_supported(
+        x2.data_ptr(), x2.stride(0), gy2.data_ptr(), gy2.stride(0), _dev_ptr(a), a.stride(0) if r else 0,
+        _dev_ptr(b), b.stride(0) if r else 0, M, N, K, r)
+    if not supported:
+        dw, da, db = _weight_grads_torch(x2, gy2, a, b, float(scale), need_w, need_a, need_b)
+        return dw if need_w else empty(), da if need_a else empty(), db if need_b else empty()
+    dw = torch.empty((N, K), dtype=torch.bfloat16, device=dev) if need_w else None
+    da = torch.empty((r, K), dtype=torch.bfloat16, device=dev) if need_a else None
+    db = torch.empty((N, r), dtype=torch.bfloat16, device=dev) if need_b else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = workspace(dev, stream, _native.bwd_weights_workspace_bytes(M, N, K, r))
+    with torch.cuda.device(dev):
+        rc = L.wsl_lora_linear_bwd_weights(
+            x2.data_ptr(), x2.stride(0), gy2.data_ptr(), gy2.stride(0),
+            _dev_ptr(a), a.stride(0) if r else 0, _dev_ptr(b), b.stride(0) if r else 0,
+            float(scale), M, N, K, r,
+            _dev_ptr(dw), K, _dev_ptr(da), K, _dev_ptr(db), r,
+            ws.data_ptr(), ws.numel(), stream)
+    _native.check(rc, "wsl_lora_linear_bwd_weights")
+    return dw if need_w else empty(), da if need_a else empty(), db if need_b else empty()
+
+
+@lora_linear_weight_grads_op.register_fake
+def _lora_linear_weight_grads_fake(x, gy, a, b, scale, need_w, need_a, need_b):
+    K, N = x.shape[-1], gy.shape[-1]
+    r = a.shape[0] if a is not None else 0
+    empty = lambda: x.new_empty(0, dtype=torch.bfloat16)
+    return (x.new_empty((N, K), dtype=torch.bfloat16) if need_w else empty(),
+            x.new_empty((r, K), dtype=torch.bfloat16) if need_a else empty(),
+            x.new_empty((N, r), dtype=torch.bfloat16) if need_b else empty())
+
+
+def weight_grads(x2, gy2, a, b, s, need_w, need_a, need_b):
+    """(dw, da, db) with None for the ones not asked for (see lora_linear_weight_grads_op)."""
+    if not (need_w or need_a or need_b):
+        return None, None, None
+    dw, da, db = lora_linear_weight_grads_op(x2, gy2, a, b, float(s), bool(need_w), bool(need_a), bool(need_b))
+    return dw if need_w else None, da if need_a else None, db if need_b else None
+
+
 def _lora_linear_setup(ctx, inputs, output):
     x, w, w_scale, a, b, scale = inputs
     ctx.save_for_backward(x, w, w_scale, a, b)
@@ -216,9 +302,9 @@ def _lora_linear_backward(ctx, gy):
         dx = gy . W + scale * U . a     one launch of the fused kernel, as the forward of
                                         the same op on (gy, W^T, b^T, a^T): the fused
                                         kernel's K is the forward's N
-        dW = gy^T . x                   plain GEMMs (reductions over the tokens M)
-        da = scale * U^T . x
-        db = scale * gy^T . T
+        dW = gy^T . x                   one wsl::lora_linear_weight_grads call: reductions
+        da = scale * U^T . x            over the tokens M on the same tile kernel, after
+        db = scale * gy^T . T           one transpose of x and gy
 
     The reference has no backward of its own: torch autograd differentiates
     LoRAModule.forward (torchtitan/models/llama3/model/model.py:189-192) and the base
@@ -247,14 +333,8 @@ def _lora_linear_backward(ctx, gy):
         else:
             dx = torch.zeros_like(x2)
         dx = dx.reshape(x.shape)
-    if need_w and w is not None and w.dtype == torch.bfloat16:
-        dw = torch.mm(gy2.t(), x2)
-    if has_lora and (need_a or need_b):
-        zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)  # beta = 0: s rides on alpha
-        if need_a:
-            da = torch.addmm(zero, torch.mm(gy2, b).t(), x2, beta=0, alpha=s)
-        if need_b:
-            db = torch.addmm(zero, gy2.t(), torch.mm(x2, a.t().contiguous()), beta=0, alpha=s)
+    dw, da, db = weight_grads(x2, gy2, a, b, s, need_w and w is not None and w.dtype == torch.bfloat16,
+                              has_lora and need_a, has_lora and need_b)
     return dx, dw, None, da, db, None
 
 
@@ -447,18 +527,24 @@ def _lora_linear_bcast_backward(ctx, gy):
         if has_lora:
             dx = dx + lora_linear_op(gy2, None, None, bd.t().contiguous(), a.t().contiguous(), s)
         dx = dx.reshape(x.shape)
-    if need_w and w.dtype == torch.bfloat16:
-        dw = torch.mm(gyb.t(), x2)
+    dw, _, _ = weight_grads(x2, gyb, None, None, s, need_w and w.dtype == torch.bfloat16, False, False)
     if has_lora and (need_a or need_b):
-        zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)
-        if need_a:
-            da = torch.addmm(zero, torch.mm(gy2, bd).t(), x2, beta=0, alpha=s)
-        if need_b:
-            t = torch.mm(x2, a.t().contiguous())
-            full = torch.addmm(zero, gy2.t(), t, beta=0, alpha=s)
-            db = torch.empty_like(b)
+        if G * r <= _native.WSL_MAX_RANK:
+            _, da, full = weight_grads(x2, gy2, a, bd, s, False, need_a, need_b)
+            if full is not None:
+                db = torch.empty_like(b)
+                for j in range(G):
+                    db[j * N:(j + 1) * N] = full[j * N:(j + 1) * N, j * r:(j + 1) * r]
+        else:  # G*r above the rank limit: per group
+            da = torch.empty_like(a) if need_a else None
+            db = torch.empty_like(b) if need_b else None
             for j in range(G):
-                db[j * N:(j + 1) * N] = full[j * N:(j + 1) * N, j * r:(j + 1) * r]
+                _, daj, dbj = weight_grads(x2, gy2[:, j * N:(j + 1) * N], a[j * r:(j + 1) * r],
+                                           b[j * N:(j + 1) * N], s, False, need_a, need_b)
+                if need_a:
+                    da[j * r:(j + 1) * r] = daj
+                if need_b:
+                    db[j * N:(j + 1) * N] = dbj
     return dx, dw, None, da, db, None, None, None
 
 
@@ -526,22 +612,30 @@ def _lora_linear_grouped_backward(ctx, gy):
         else:
             dx = lora_linear_op(gy2, wt, None, None, None, s)
         dx = dx.reshape(x.shape)
-    if need_w and w.dtype == torch.bfloat16:
-        dw = torch.mm(gy2.t(), x2)
-    if has_lora and (need_a or need_b):
-        zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)
-        if need_a:
-            da = torch.addmm(zero, torch.mm(gy2, bd).t(), x2, beta=0, alpha=s)
-        if need_b:
-            # one product over all groups (gy read once), then each group's diagonal block:
-            # the off-diagonal blocks are a few GFLOP, cheaper than G strided skinny GEMMs
-            t = torch.mm(x2, a.t().contiguous())
-            full = torch.addmm(zero, gy2.t(), t, beta=0, alpha=s)
-            db = torch.empty_like(b)
-            n0 = 0
-            for g, n in enumerate(gn):
-                db[n0:n0 + n] = full[n0:n0 + n, g * r:(g + 1) * r]
-                n0 += n
+    # one weight-gradient call over all groups (x and gy read once): da from Bd, db as the
+    # diagonal blocks of the [N, G*r] product (the off-diagonal blocks are a few GFLOP,
+    # cheaper than G strided skinny products)
+    lora_ab = has_lora and len(gn) * r <= _native.WSL_MAX_RANK
+    dw, da, full = weight_grads(x2, gy2, a, bd, s, need_w and w.dtype == torch.bfloat16,
+                                lora_ab and need_a, lora_ab and need_b)
+    if has_lora and not lora_ab and (need_a or need_b):  # G*r above the rank limit: per group
+        da = torch.empty_like(a) if need_a else None
+        db = torch.empty_like(b) if need_b else None
+        n0 = 0
+        for g, n in enumerate(gn):
+            _, dag, dbg = weight_grads(x2, gy2[:, n0:n0 + n], a[g * r:(g + 1) * r], b[n0:n0 + n], s, False,
+                                       need_a, need_b)
+            if need_a:
+                da[g * r:(g + 1) * r] = dag
+            if need_b:
+                db[n0:n0 + n] = dbg
+            n0 += n
+    elif full is not None:
+        db = torch.empty_like(b)
+        n0 = 0
+        for g, n in enumerate(gn):
+            db[n0:n0 + n] = full[n0:n0 + n, g * r:(g + 1) * r]
+            n0 += n
     return dx, dw, None, da, db, None, None
 
 
