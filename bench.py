@@ -14,7 +14,7 @@ weights), config 4 weight-shared Qwen3 greedy decode tokens/s, config 5 fp8-base
 projections, and the CPU baseline (the reference's fp32 arithmetic on host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
-                      [--only c1|c2|c2single|c2_1p7b|c3|c4|c5|emb|vendor|backward|shape]
+                      [--only c1|c2|c2single|c2_1p7b|c3|c4|c5|c5paths|emb|vendor|backward|medium|shape]
                       [--shape M,N,K,r]
                       [--vendor]
                       [--copy-calibration]
@@ -343,6 +343,41 @@ def bench_c3(dev, steps, warmup):
             del g, st
             torch.cuda.empty_cache()
         out[f"M={M}"] = row
+    return out
+
+
+def bench_medium(dev, steps, warmup):
+    """Medium M (between the decode path's 64 and a few hundred tokens) at the Qwen3-1.7B
+    projection shapes, r = 64, cold weights (6 rotating copies), 28 layers per graph, grouped
+    q|k|v and gate|up: the prefill path's split-K form (the default for 64 < M <= 256) beside
+    its unsplit tiles (WSL_PREFILL_MEDIUM=off), and M = 64 on the decode path for reference."""
+    out = {}
+    saved = os.environ.get("WSL_PREFILL_MEDIUM")
+    try:
+        for M in (64, 65, 96, 128, 192, 256):
+            row = {}
+            for label, env in (("split", None), ("unsplit", "off")):
+                if M == 64 and env is not None:
+                    continue
+                if env is None:
+                    os.environ.pop("WSL_PREFILL_MEDIUM", None)
+                else:
+                    os.environ["WSL_PREFILL_MEDIUM"] = env
+                st = ProjectionStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
+                st.stack_groups()
+                g = graph_of(st.run_grouped)
+                ms = time_replays(g, steps, warmup)
+                row["decode" if M == 64 else label] = {
+                    "ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
+                    "TFLOP/s": round(st.flops() / ms / 1e9, 1)}
+                del g, st
+                torch.cuda.empty_cache()
+            out[f"M={M}"] = row
+    finally:
+        if saved is None:
+            os.environ.pop("WSL_PREFILL_MEDIUM", None)
+        else:
+            os.environ["WSL_PREFILL_MEDIUM"] = saved
     return out
 
 
@@ -726,7 +761,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=("c1", "c2", "c2single", "c2_1p7b", "c3", "c4", "c5", "c5paths", "emb",
-                                       "vendor", "backward", "shape"), default=None)
+                                       "vendor", "backward", "medium", "shape"), default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -753,6 +788,7 @@ def main():
               "c5paths": lambda: bench_c5_paths(dev, args.steps, args.warmup),
               "emb": lambda: bench_embedding(dev, args.steps, args.warmup),
               "vendor": lambda: bench_vendor(dev, args.steps, args.warmup),
+              "medium": lambda: bench_medium(dev, min(args.steps, 10), min(args.warmup, 3)),
               "backward": lambda: bench_backward(dev, min(args.steps, 10), min(args.warmup, 3)),
               "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)

@@ -76,6 +76,21 @@ __device__ __forceinline__ void store4(uint16_t* d, f32x4_t v, bool vec) {
   }
 }
 
+// sum over q of p[q * slice .. + 4) in split order, four loads in flight at a time (16-byte
+// aligned p, slice % 4 == 0).
+__device__ __forceinline__ f32x4_t sum_splits(const float* p, int64_t slice, int splits) {
+  const f32x4_t* pv = reinterpret_cast<const f32x4_t*>(p);
+  const int64_t sv = slice / 4;
+  f32x4_t a = pv[0];
+  int q = 1;
+  for (; q + 4 <= splits; q += 4) {
+    const f32x4_t a0 = pv[q * sv], a1 = pv[(q + 1) * sv], a2 = pv[(q + 2) * sv], a3 = pv[(q + 3) * sv];
+    a += a0; a += a1; a += a2; a += a3;
+  }
+  for (; q < splits; ++q) a += pv[q * sv];
+  return a;
+}
+
 // dst = bf16(scale * sum over the splits of part[s]) for an fp32 [splits][rows][cols] partial
 // product, splits in order; four consecutive columns per thread (cols % 4 == 0).
 __global__ void __launch_bounds__(256) split_sum_kernel(const float* __restrict__ part, int splits, int64_t rows,
@@ -84,9 +99,7 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float* __restrict_
   const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   const int64_t slice = rows * cols;
   if (e >= slice) return;
-  f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + e);
-  for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4_t*>(part + (int64_t)s * slice + e);
-  store4(dst + (e / cols) * ldd + e % cols, v * scale, vec != 0);
+  store4(dst + (e / cols) * ldd + e % cols, sum_splits(part + e, slice, splits) * scale, vec != 0);
 }
 
 // dW = bf16(sum over the splits of part[s]) ([splits][N][K] fp32, splits in order) to the
@@ -105,8 +118,7 @@ __global__ void __launch_bounds__(256) dw_reduce_kernel(const float* __restrict_
   for (int i = 0; i < 4; ++i) {
     const int row = tid / 16 + 16 * i, col = (tid % 16) * 4;
     const int64_t e = (n0 + row) * K + k0 + col;
-    f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + e);
-    for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4_t*>(part + (int64_t)s * slice + e);
+    const f32x4_t v = sum_splits(part + e, slice, splits);
     store4(dw + (n0 + row) * lddw + k0 + col, v, vec != 0);
     const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
     if (dwc != nullptr) *reinterpret_cast<uint2*>(dwc + e) = uint2{lo, hi};

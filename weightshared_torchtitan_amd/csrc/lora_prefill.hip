@@ -788,13 +788,157 @@ bool fp8_matrix_cores(const LoraArgs& p) {
 }
 }  // namespace
 
-// Workspace of the prefill path: the rank pre-pass region (r > RIN, or any rank on the fp8
-// matrix-core path, which takes T from the pre-pass), then for an fp8 W the activation codes
-// of the fp8 matrix-core path.
+// ---- Medium M: split-K over few row tiles ----
+// Just past the decode path (M <= 64) the tile grid has one or two rows of tiles, and each
+// workgroup's K loop is a chain of dependent fills with little MFMA work to hide them (at
+// M = 65, 2048 x 6144 ran 94 us, W streamed at 0.27 TB/s). Such shapes split K: the base
+// product runs as the split-K plain GEMM over 128 x 128 tiles (fp32 partials
+// [splits][M][N]), T comes from the rank pre-pass, and a combine kernel sums the partials in
+// split order, adds T . B^T and rounds once. The split count depends on M and K, halved
+// while the partials exceed their budget; a grouped call whose groups would take another
+// count alone goes group by group, so grouped outputs stay those of the single calls.
+constexpr int kMediumMaxM = 160;  // measured: the split form wins at M = 65-128, loses at 192-256
+constexpr int kMediumMaxSplits = 16;
+constexpr size_t kMediumPartBytes = (size_t)24 << 20;  // with T, within the no-allocation scratch
+
+int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool has_w, bool gather) {
+  if (!has_w || gather || w_dtype != kBF16 || M > kMediumMaxM || M < 1) return 0;
+  if (rt > 256) return 0;  // the combine kernel stages 32 rows of T (all rt ranks) in LDS
+  const char* env = std::getenv("WSL_PREFILL_MEDIUM");  // "off": the unsplit tiles, for side-by-side timing
+  if (env != nullptr && std::strcmp(env, "off") == 0) return 0;
+  const int64_t nk = K / BK;
+  if (nk < 8) return 0;
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  if (tiles >= 192) return 0;  // enough workgroups without a split
+  int s = 1;
+  while (s * 2 <= kMediumMaxSplits && nk % (s * 2) == 0 && nk / (s * 2) >= 2) s *= 2;
+  while (s > 1 && (size_t)s * M * N * 4 > kMediumPartBytes) s /= 2;
+  return s > 1 ? s : 0;
+}
+
+namespace {
+// y[m][n] = bf16(sum_s part[s][m][n] + sum_j T[m][goff(n) + j] B[n][j]): the partials in split
+// order, then the LoRA up-projection over the bf16 T of the rank pre-pass (s applied there).
+// A workgroup owns 32 rows x 32 columns: it stages their T rows (all rt ranks) and B rows in
+// LDS, and each thread takes 4 consecutive columns of one row (coalesced partials, 8-byte
+// stores); lanes of one row read the same T words and lanes of one column quad the same B
+// words, so the LDS reads broadcast.
+constexpr int MC_ROWS = 32, MC_COLS = 32;
+__global__ void __launch_bounds__(256)
+medium_combine_kernel(const float* __restrict__ part, int splits, int M, int N, const uint16_t* __restrict__ t,
+                      int ldt, const uint16_t* __restrict__ b, int64_t ldb, int r, int ge0, int ge1, int ge2,
+                      uint16_t* __restrict__ y, int64_t ldy) {
+  // LDS rows padded by one word: the 8 rows (T) or column quads (B) a wave reads at once
+  // then fall on different banks instead of one
+  extern __shared__ __attribute__((aligned(16))) uint32_t mc_lds[];
+  const int tsw = ldt / 2 + 1, bsw = r / 2 + 1;  // row strides in 32-bit words
+  uint32_t* tl = mc_lds;                   // [MC_ROWS][tsw]
+  uint32_t* bl = mc_lds + MC_ROWS * tsw;   // [MC_COLS][bsw]
+  const int m0 = blockIdx.y * MC_ROWS, n0 = blockIdx.x * MC_COLS;
+  const int tid = threadIdx.x;
+  if (r > 0) {  // 16-byte global chunks: ldt and r are multiples of 8
+    const int tc = ldt / 8, bc = r / 8;
+    for (int q = tid; q < MC_ROWS * tc; q += 256) {
+      const int row = q / tc, c = q % tc;
+      const int m = min(m0 + row, M - 1);
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(t + (int64_t)m * ldt + c * 8);
+      uint32_t* d = tl + row * tsw + c * 4;
+      d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+    }
+    for (int q = tid; q < MC_COLS * bc; q += 256) {
+      const int row = q / bc, c = q % bc;
+      const int n = min(n0 + row, N - 1);
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(b + (int64_t)n * ldb + c * 8);
+      uint32_t* d = bl + row * bsw + c * 4;
+      d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+    }
+    __syncthreads();
+  }
+  const int rl = tid / 8, cq = tid % 8;  // row, column quad
+  const int m = m0 + rl, nb = n0 + cq * 4;
+  if (m >= M || nb >= N) return;
+  const int64_t slice = (int64_t)M * N;
+  const int64_t e = (int64_t)m * N + nb;
+  const int nn = N - nb < 4 ? N - nb : 4;
+  float v[4];
+  if (nn == 4 && (N & 3) == 0) {
+    // split order kept; four loads in flight at a time rather than one round trip per split
+    const f32x4_t* pv = reinterpret_cast<const f32x4_t*>(part + e);
+    const int64_t sv = slice / 4;
+    f32x4_t a = pv[0];
+    int q = 1;
+    for (; q + 4 <= splits; q += 4) {
+      const f32x4_t a0 = pv[q * sv], a1 = pv[(q + 1) * sv], a2 = pv[(q + 2) * sv], a3 = pv[(q + 3) * sv];
+      a += a0; a += a1; a += a2; a += a3;
+    }
+    for (; q < splits; ++q) a += pv[q * sv];
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+  } else {
+    for (int c = 0; c < 4; ++c) {
+      v[c] = 0.f;
+      if (c < nn)
+        for (int q = 0; q < splits; ++q) v[c] += part[q * slice + e + c];
+    }
+  }
+  if (r > 0) {
+    const uint32_t* trow = tl + rl * tsw;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int n = nb + c;
+      const int goff = ((n >= ge0) + (n >= ge1) + (n >= ge2)) * r;
+      const uint32_t* tw = trow + goff / 2;
+      const uint32_t* bw = bl + (cq * 4 + c) * bsw;
+      float d = 0.f;
+      for (int j = 0; j < r / 2; ++j) {
+        const uint32_t tv = tw[j], bv = bw[j];
+        d += bf16_bits_to_f32(tv & 0xffffu) * bf16_bits_to_f32(bv & 0xffffu);
+        d += bf16_bits_to_f32(tv >> 16) * bf16_bits_to_f32(bv >> 16);
+      }
+      v[c] += d;
+    }
+  }
+  uint16_t* dst = y + (int64_t)m * ldy + nb;
+  if (nn == 4) {
+    *reinterpret_cast<uint2*>(dst) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  } else {
+    for (int c = 0; c < nn; ++c) dst[c] = f32_to_bf16_bits(v[c]);
+  }
+}
+
+hipError_t launch_medium(const LoraArgs& p, int splits) {
+  const int64_t rt = p.r * p.groups;
+  uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
+  const size_t t_bytes = p.r > 0 ? rank_prepass_bytes(p.M, p.K, rt) : 0;
+  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(p.ws) + ((t_bytes + 255) & ~(size_t)255));
+  if (p.r > 0) {
+    const hipError_t e = rank_prepass(p, t);
+    if (e != hipSuccess) return e;
+  }
+  LoraArgs q = p;
+  q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0; q.groups = 1; q.yscale = 1.f;
+  q.y = part; q.ldy = p.N; q.K = p.K / splits;
+  hipError_t e = launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)((p.N + MC_COLS - 1) / MC_COLS), (unsigned)((p.M + MC_ROWS - 1) / MC_ROWS));
+  const size_t lds = p.r > 0 ? (size_t)(MC_ROWS * (rt / 2 + 1) + MC_COLS * (p.r / 2 + 1)) * 4 : 0;  // < 34 KB
+  medium_combine_kernel<<<grid, dim3(256), lds, p.stream>>>(
+      part, splits, (int)p.M, (int)p.N, t, (int)rt, reinterpret_cast<const uint16_t*>(p.b), p.ldb, (int)p.r,
+      group_end(p, 0), group_end(p, 1), group_end(p, 2), reinterpret_cast<uint16_t*>(p.y), p.ldy);
+  return hipGetLastError();
+}
+}  // namespace
+
+// Workspace of the prefill path: the rank pre-pass region (r > RIN, any rank on the fp8
+// matrix-core path or on the medium-M split path, which take T from the pre-pass), then for
+// an fp8 W the activation codes of the fp8 matrix-core path, or the medium path's partials.
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
-  (void)N;
   if (w_dtype == kFP8)
     return (r > 0 ? rank_prepass_bytes(M, K, r) : 0) + prefill_fp8_workspace_bytes(M, K, 2);
+  const int ms = medium_splits(M, N, K, r, w_dtype, true, false);
+  if (ms > 0) {
+    const size_t t_bytes = r > 0 ? ((rank_prepass_bytes(M, K, r) + 255) & ~(size_t)255) : 0;
+    return t_bytes + (size_t)ms * M * N * 4;
+  }
   return r > RIN ? rank_prepass_bytes(M, K, r) : 0;
 }
 
@@ -874,6 +1018,10 @@ hipError_t launch_prefill(const LoraArgs& p) {
     }
     char* codes = reinterpret_cast<char*>(p.ws) + (p.r > 0 ? rank_prepass_bytes(p.M, p.K, rt) : 0);
     return launch_prefill_fp8(p, p.r > 0 ? t : nullptr, rt, codes, p.fp8_terms);
+  }
+  if (has_w && p.w_dtype == kBF16) {
+    const int ms = medium_splits(p.M, p.N, p.K, rt, p.w_dtype, true, false);
+    if (ms > 0) return launch_medium(p, ms);
   }
   const uint16_t* tg = nullptr;
   int64_t ldt = 0;

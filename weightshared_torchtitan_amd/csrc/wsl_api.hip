@@ -274,7 +274,17 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
     return run_call(p, workspace, workspace_bytes);
   }
   const Path path = choose_path(p);
-  if ((path == Path::kPrefill && wsl::prefill_groups_supported(p)) ||
+  // The prefill path's medium-M split form must be taken (with the same split count) by the
+  // grouped launch exactly when each group alone takes it, so the groups' outputs stay those
+  // of the single calls bit for bit; otherwise the groups go one by one.
+  bool medium_agrees = true;
+  if (path == Path::kPrefill) {
+    const int ms = wsl::medium_splits(p.M, p.N, p.K, p.r * n_groups, p.w_dtype, p.w != nullptr, false);
+    for (int g = 0; g < n_groups; ++g)
+      medium_agrees =
+          medium_agrees && wsl::medium_splits(p.M, group_n[g], p.K, p.r, p.w_dtype, p.w != nullptr, false) == ms;
+  }
+  if ((path == Path::kPrefill && medium_agrees && wsl::prefill_groups_supported(p)) ||
       (path == Path::kDecode && wsl::decode_groups_supported(p)))
     return run_call(p, workspace, workspace_bytes);
   const int64_t wbytes = (p.w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;

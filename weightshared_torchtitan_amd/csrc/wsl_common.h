@@ -146,6 +146,8 @@ hipError_t launch_prefill(const LoraArgs& p);
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool prefill_supported(const LoraArgs& p);
 bool prefill_groups_supported(const LoraArgs& p);
+// K splits of the medium-M split form of the prefill path (0: not taken); rt = r * groups.
+int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool has_w, bool gather);
 // Plain bf16 products over a long contiguous K (csrc/lora_prefill.hip) and the rank
 // pre-pass T = bf16(s x . A^T), for the weight gradients (csrc/lora_backward.hip).
 int product_splits(int64_t M, int64_t N, int64_t nk, bool divides);
