@@ -439,10 +439,12 @@ def test_bwd_weights_supported_answers_from_layout(K, r, x, ok):
 
 
 @needs_lib
-def test_bwd_weights_workspace_holds_transposes_and_partials():
-    """The weight-gradient workspace holds at least the token-contiguous copies of x, gy
-    and T, U ((K + r + N + r) x M bf16) beside the counter prefix and its halves."""
+def test_bwd_weights_workspace_holds_dw_copies_and_partials():
+    """The weight-gradient workspace holds, in each half beside the counter prefix, the bf16 dW
+    copy and dW^T of the dW route and the fp32 split partials (4 splits of 1024 x 1024 at
+    M = 8192), and nothing the size of x or gy (the operands are read where they lie)."""
     M, Nn, K, r = 8192, 1024, 1024, 32
     got = N.bwd_weights_workspace_bytes(M, Nn, K, r)
-    assert got >= 65536 + 2 * (K + r + Nn + r) * M * 2
+    assert got >= 65536 + 2 * (2 * Nn * K * 2 + 4 * Nn * K * 4)
+    assert got < 65536 + 2 * (K + Nn) * M * 2
     assert N.bwd_weights_workspace_bytes(0, Nn, K, r) >= 65536

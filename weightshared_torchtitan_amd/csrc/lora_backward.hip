@@ -4,12 +4,11 @@
 //   dA = s (gy . B)^T . x    [r, K]
 //   dB = s gy^T . (x . A^T)  [N, r]
 //
-// dW reduces over the M tokens of two operands that store tokens as rows. The tile kernel
-// of the forward reduces along a contiguous K, so x and gy are transposed once into
-// token-contiguous rows (tokens zero-padded to Mp): xt [K, Mp], gt [N, Mp], and
-// dW = gt . xt^T is that kernel's product. An output too small to fill the 256 CUs splits
-// the token reduction into equal parts (fp32 partials) that a reduce kernel sums in split
-// order (deterministic), rounding once to bf16.
+// dW reduces over the M tokens of two operands that store tokens as rows. The fused kernel's
+// tile loop takes them in that form (TN: the tiles go into LDS as they lie and each MFMA
+// fragment is read with gfx950's transposing LDS reads), so neither operand is copied. An
+// output too small to fill the 256 CUs splits the token reduction into equal parts (fp32
+// partials) that a reduce kernel sums in split order (deterministic), rounding once to bf16.
 //
 // With dW at hand, dA and dB follow from it by associativity, as products over K or N
 // instead of over the tokens:
@@ -19,9 +18,8 @@
 // 2 N K r multiply-adds each instead of 2 M r (N + K) for the rank projections T = x . A^T,
 // U = gy . B and their products: both read the bf16 dW (dA through its transpose) and
 // nothing of size M. Without dW (a frozen base) they take the token route instead:
-// T = bf16(s x . A^T) and U = bf16(s gy . B) from the forward's rank pre-pass, transposed
-// beside x and gy (xt = [x^T ; T^T], gt = [gy^T ; U^T]), dB = gt[0,N) . xt[K,K+r)^T,
-// dA = gt[N,N+r) . xt[0,K)^T.
+// T = bf16(s x . A^T) and U = bf16(s gy . B) from the forward's rank pre-pass, then
+// dB = gy^T . T and dA = U^T . x as token-major products.
 //
 // The reference has no backward of its own: torch autograd differentiates LoRAModule.forward
 // (torchtitan/models/llama3/model/model.py:189-192) and the base nn.Linear (:257-273)
@@ -155,8 +153,7 @@ struct Plan {
   int sw;          // token splits of the dW product
   int sb, sa;      // token route: token splits of the dB and dA products
   int sdb, sda;    // dW route: splits of dB = s dW . A^T (over K) and dA = s B^T . dW (over N)
-  int64_t Mp;      // tokens padded to 64 x the largest token split count
-  size_t off_t, off_u, off_bt, off_xt, off_gt, off_dwc, off_dwt, off_part, total;
+  size_t off_t, off_u, off_bt, off_dwc, off_dwt, off_part, total;
 };
 
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t r) {
@@ -167,16 +164,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t r) {
   L.sa = r > 0 ? product_splits(r, K, nk, false) : 1;
   L.sdb = r > 0 ? product_splits(N, r, K / 64, true) : 1;
   L.sda = r > 0 ? product_splits(r, K, N / 64, true) : 1;
-  int smax = L.sw > L.sb ? L.sw : L.sb;
-  if (L.sa > smax) smax = L.sa;
-  const int64_t grid = 64 * (int64_t)smax;
-  L.Mp = (M + grid - 1) / grid * grid;
   size_t off = 0;
   L.off_t = off;   off = a256(off + (r > 0 ? rank_prepass_bytes(M, K, r) : 0));
   L.off_u = off;   off = a256(off + (r > 0 ? rank_prepass_bytes(M, N, r) : 0));
   L.off_bt = off;  off = a256(off + (size_t)r * N * 2);
-  L.off_xt = off;  off = a256(off + (size_t)(K + r) * L.Mp * 2);
-  L.off_gt = off;  off = a256(off + (size_t)(N + r) * L.Mp * 2);
   L.off_dwc = off; off = a256(off + (r > 0 ? (size_t)N * K * 2 : 0));
   L.off_dwt = off; off = a256(off + (r > 0 ? (size_t)N * K * 2 : 0));
   L.off_part = off;
@@ -191,8 +182,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t r) {
 
 // Shapes and layouts the weight-gradient path takes: K and N on the 64-element tile grid
 // (the reductions of the dA and dB products and of the token route's pre-passes), ranks in
-// multiples of 8, 16-byte aligned rows, and token counts whose padded transposes keep the
-// tile kernel's 32-bit lane offsets.
+// multiples of 8, 16-byte aligned rows, and sizes within the tile kernel's int range.
 bool weight_grads_supported(const LoraArgs& p, const void* gy, int64_t ldg) {
   if (p.M < 1 || p.K % 64 != 0 || p.N % 64 != 0 || p.r % 8 != 0) return false;
   if (p.M > ((int64_t)1 << 22) - 2048 || p.N > ((int64_t)1 << 22) || p.K > ((int64_t)1 << 22)) return false;
@@ -219,55 +209,76 @@ hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, v
   uint16_t* T = reinterpret_cast<uint16_t*>(ws + L.off_t);
   uint16_t* U = reinterpret_cast<uint16_t*>(ws + L.off_u);
   uint16_t* Bt = reinterpret_cast<uint16_t*>(ws + L.off_bt);
-  uint16_t* xt = reinterpret_cast<uint16_t*>(ws + L.off_xt);
-  uint16_t* gt = reinterpret_cast<uint16_t*>(ws + L.off_gt);
   uint16_t* dwc = reinterpret_cast<uint16_t*>(ws + L.off_dwc);
   uint16_t* dwt = reinterpret_cast<uint16_t*>(ws + L.off_dwt);
   float* part = reinterpret_cast<float*>(ws + L.off_part);
   const hipStream_t st = p.stream;
+  const int64_t nkt = (M + 63) / 64;  // 64-token K tiles
   hipError_t e = hipSuccess;
 
-  // y' = scale * x' . W'^T [rows, cols] over a reduction of `red` (x', W' rows `red` long,
-  // row strides ldx', ldw'): straight to bf16 when unsplit and the destination takes the
-  // tile store's 8-byte pieces, else through fp32 partials and split_sum_kernel
-  auto product = [&](const void* xa, int64_t ldxa, int64_t rows, const void* wb, int64_t ldwb, int64_t cols,
-                     int64_t red, int splits, float scale, void* dst, int64_t ldd) -> hipError_t {
-    LoraArgs q = p;
-    q.x = xa; q.ldx = ldxa; q.w = wb; q.ldw = ldwb; q.M = rows; q.N = cols; q.yscale = scale;
-    const bool vec = (reinterpret_cast<uintptr_t>(dst) & 7u) == 0 && ldd % 4 == 0;
-    if (splits == 1 && vec) {
-      q.K = red; q.y = dst; q.ldy = ldd;
-      return launch_product(q, nullptr, 1);
-    }
-    q.K = red / splits;
-    hipError_t err = launch_product(q, part, splits);
-    if (err != hipSuccess) return err;
+  auto vec_ok = [](const void* dst, int64_t ldd) { return (reinterpret_cast<uintptr_t>(dst) & 7u) == 0 && ldd % 4 == 0; };
+  // dst = bf16(scale * sum_s part[s]) [rows, cols] from the partial products
+  auto reduce = [&](int splits, int64_t rows, int64_t cols, float scale, void* dst, int64_t ldd, bool vec) {
     const int64_t n4 = rows * cols / 4;
     split_sum_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st>>>(
         part, splits, rows, cols, scale, reinterpret_cast<uint16_t*>(dst), ldd, vec ? 1 : 0);
     return hipGetLastError();
   };
+  // y' = scale * x' . W'^T, x' and W' rows `red` long: straight to bf16 when unsplit and the
+  // destination takes the tile store's 8-byte pieces, else through fp32 partials
+  auto product = [&](const void* xa, int64_t ldxa, int64_t rows, const void* wb, int64_t ldwb, int64_t cols,
+                     int64_t red, int splits, float scale, void* dst, int64_t ldd) -> hipError_t {
+    LoraArgs q = p;
+    q.x = xa; q.ldx = ldxa; q.w = wb; q.ldw = ldwb; q.M = rows; q.N = cols; q.yscale = scale;
+    const bool vec = vec_ok(dst, ldd);
+    if (splits == 1 && vec) {
+      q.K = red; q.y = dst; q.ldy = ldd;
+      return launch_product(q, nullptr, 1);
+    }
+    q.K = red / splits;
+    const hipError_t err = launch_product(q, part, splits);
+    return err != hipSuccess ? err : reduce(splits, rows, cols, scale, dst, ldd, vec);
+  };
+  // Token splits as launched: equal whole 64-token tiles, none starting past the tokens.
+  auto tn_splits = [&](int splits, int64_t* per) {
+    const int64_t kt = (nkt + splits - 1) / splits;
+    *per = kt * 64;
+    return (int)((nkt + kt - 1) / kt);
+  };
+  // the same over the tokens with token-major operands: x'[m][t] = xa[t * ldxa + m],
+  // W'[n][t] = wb[t * ldwb + n]
+  auto product_tn = [&](const void* xa, int64_t ldxa, int64_t rows, const void* wb, int64_t ldwb, int64_t cols,
+                        int splits, float scale, void* dst, int64_t ldd) -> hipError_t {
+    LoraArgs q = p;
+    q.x = xa; q.ldx = ldxa; q.w = wb; q.ldw = ldwb; q.M = rows; q.N = cols; q.yscale = scale;
+    const int s = tn_splits(splits, &q.K);
+    const bool vec = vec_ok(dst, ldd);
+    if (s == 1 && vec) {
+      q.y = dst; q.ldy = ldd;
+      return launch_product_tn(q, M, nullptr, 1);
+    }
+    const hipError_t err = launch_product_tn(q, M, part, s);
+    return err != hipSuccess ? err : reduce(s, rows, cols, scale, dst, ldd, vec);
+  };
 
   if (dw != nullptr) {
     // ---- dW route: dW over the tokens, then dB = s dW . A^T and dA = s B^T . dW ----
-    e = transpose_pad(p.x, p.ldx, M, K, xt, L.Mp, L.Mp, st);
-    if (e == hipSuccess) e = transpose_pad(gy, ldg, M, N, gt, L.Mp, L.Mp, st);
-    if (e != hipSuccess) return e;
-    const bool direct = L.sw == 1 && al16(dw) && lddw % 8 == 0;
+    int64_t per = 0;
+    const int sw = tn_splits(L.sw, &per);
+    const bool direct = sw == 1 && al16(dw) && lddw % 8 == 0;
     const uint16_t* dws = reinterpret_cast<const uint16_t*>(dw);  // bf16 dW rows for dB
     int64_t ldws = lddw;
     if (direct) {
-      e = product(gt, L.Mp, N, xt, L.Mp, K, L.Mp, 1, 1.f, dw, lddw);
+      e = product_tn(gy, ldg, N, p.x, p.ldx, K, 1, 1.f, dw, lddw);
       if (e == hipSuccess && da != nullptr) e = transpose_pad(dw, lddw, N, K, dwt, N, N, st);
     } else {
       LoraArgs q = p;
-      q.x = gt; q.ldx = L.Mp; q.w = xt; q.ldw = L.Mp; q.M = N; q.N = K; q.K = L.Mp / L.sw;
-      e = launch_product(q, part, L.sw);
+      q.x = gy; q.ldx = ldg; q.w = p.x; q.ldw = p.ldx; q.M = N; q.N = K; q.K = per;
+      e = launch_product_tn(q, M, part, sw);
       if (e == hipSuccess) {
-        const bool vec = (reinterpret_cast<uintptr_t>(dw) & 7u) == 0 && lddw % 4 == 0;
         dw_reduce_kernel<<<dim3((unsigned)(K / TT), (unsigned)(N / TT)), dim3(256), 0, st>>>(
-            part, L.sw, N, K, reinterpret_cast<uint16_t*>(dw), lddw, vec ? 1 : 0, db != nullptr ? dwc : nullptr,
-            da != nullptr ? dwt : nullptr);
+            part, sw, N, K, reinterpret_cast<uint16_t*>(dw), lddw, vec_ok(dw, lddw) ? 1 : 0,
+            db != nullptr ? dwc : nullptr, da != nullptr ? dwt : nullptr);
         e = hipGetLastError();
       }
       dws = dwc;
@@ -281,25 +292,21 @@ hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, v
     return e;
   }
 
-  // ---- token route (no dW): T, U by the rank pre-pass, products over the tokens ----
-  if (db != nullptr) {  // T = bf16(s x . A^T)
+  // ---- token route (no dW): T, U by the rank pre-pass, token-major products ----
+  if (db != nullptr) {  // dB = gy^T . T, T = bf16(s x . A^T)
     LoraArgs q = p;
     q.groups = 1;
     e = rank_prepass(q, T);
-    if (e == hipSuccess) e = transpose_pad(T, r, M, r, xt + K * L.Mp, L.Mp, L.Mp, st);
-    if (e == hipSuccess) e = transpose_pad(gy, ldg, M, N, gt, L.Mp, L.Mp, st);
-    if (e == hipSuccess) e = product(gt, L.Mp, N, xt + K * L.Mp, L.Mp, r, L.Mp, L.sb, 1.f, db, lddb);
+    if (e == hipSuccess) e = product_tn(gy, ldg, N, T, r, r, L.sb, 1.f, db, lddb);
     if (e != hipSuccess) return e;
   }
-  if (da != nullptr) {  // U = bf16(s gy . B), with B^T [r, N] in the place of A
+  if (da != nullptr) {  // dA = U^T . x, U = bf16(s gy . B) with B^T [r, N] in the place of A
     e = transpose_pad(p.b, p.ldb, N, r, Bt, N, N, st);
     if (e != hipSuccess) return e;
     LoraArgs q = p;
     q.x = gy; q.ldx = ldg; q.K = N; q.a = Bt; q.lda = N; q.groups = 1;
     e = rank_prepass(q, U);
-    if (e == hipSuccess) e = transpose_pad(U, r, M, r, gt + N * L.Mp, L.Mp, L.Mp, st);
-    if (e == hipSuccess) e = transpose_pad(p.x, p.ldx, M, K, xt, L.Mp, L.Mp, st);
-    if (e == hipSuccess) e = product(gt + N * L.Mp, L.Mp, r, xt, L.Mp, K, L.Mp, L.sa, 1.f, da, ldda);
+    if (e == hipSuccess) e = product_tn(U, r, r, p.x, p.ldx, K, L.sa, 1.f, da, ldda);
   }
   return e;
 }

@@ -86,6 +86,21 @@ __device__ __forceinline__ int lds_off(int row, int c) { return row * ROWB + ((c
 // i%8 of row R = grp*8 + i/8, which holds global chunk (i%8) ^ ((R >> 1) & 7).
 __device__ __forceinline__ int fill_chunk(int lane, int grp) { return (lane & 7) ^ (((grp & 1) << 2) | (lane >> 4)); }
 
+// gfx950 transposing LDS read (ds_read_b64_tr_b16). Within each 16-lane group, lane i gets
+// for e = 0..3 element (i % 4) of the 8 bytes addressed by lane 4e + i / 4 of its group (read
+// off the hardware with an in-bounds probe). So if lane j of a group addresses row
+// kb + j / 4 at column f0 + 4 (j % 4) of a row-major 16-bit matrix, lane i receives rows
+// kb .. kb + 3 of column f0 + i: four k values of one row of the transposed matrix.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr8(const char* base, int off) {
+  const v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)(base + off));
+  uint2 r;
+  r.x = (uint32_t)(uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16);
+  r.y = (uint32_t)(uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16);
+  return r;
+}
+
 __device__ __forceinline__ u32x4_t lds_read16(const char* base, int off) {
   return *reinterpret_cast<const u32x4_t*>(base + off);
 }
@@ -125,7 +140,15 @@ __device__ __forceinline__ void ring_barrier() {
 // SPLIT: split-K plain GEMM for the rank pre-pass. Workgroup row blockIdx.y takes the K
 // range [blockIdx.y * K, (blockIdx.y + 1) * K) of x and W and writes its fp32 partial
 // product to slice blockIdx.y of y (viewed as fp32 [gridDim.y][M][ldy]).
-template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false>
+//
+// TN: plain GEMM over operands stored with the reduction as rows ("token-major"): x'[m][k] is
+// x[k * ldx + m] and W'[n][k] is w[k * ldw + n], as the weight gradients' dY and x are (a
+// reduction over the tokens). The tiles go into LDS as they lie, [64 k][BM or BN columns]
+// (direct fills, 16-byte chunk c of row k at chunk c ^ 4 (k & 3)), and each MFMA fragment is
+// two transposing LDS reads (lds_read_tr8). K rows from `grows` (the token count, from this
+// split's start) on are read clamped and zeroed in the x' tile after they land. M and N are
+// multiples of 8.
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false>
 __global__ void __launch_bounds__(C::NT, 1)
 prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const int64_t* __restrict__ gidx, int64_t grows,
@@ -148,10 +171,18 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   static_assert(C::BM * ROWB <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   static_assert(!SPLIT || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "split-K is a plain bf16 GEMM");
+  static_assert(!TN || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "token-major operands: plain bf16 GEMM");
+  int64_t tok_rem = grows;  // TN: K rows from this workgroup's first one to the end (>= 1)
   if constexpr (SPLIT) {
     const int64_t kofs = (int64_t)blockIdx.y * K;
-    x += kofs;
-    w = reinterpret_cast<const uint16_t*>(w) + kofs;
+    if constexpr (TN) {
+      x += kofs * ldx;
+      w = reinterpret_cast<const uint16_t*>(w) + kofs * ldw;
+      tok_rem = grows - kofs;
+    } else {
+      x += kofs;
+      w = reinterpret_cast<const uint16_t*>(w) + kofs;
+    }
   }
 
   const int tid = threadIdx.x;
@@ -226,10 +257,31 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
 
+  // TN fills: wave fill q covers LDS bytes [1024 q, 1024 q + 1024) of a [64][cols] tile, lane i
+  // the 16 bytes at 1024 q + 16 i: row (1024 q + 16 i) / (2 cols), physical chunk s, which
+  // holds column chunk s ^ 4 (row & 3) (clamped to the last full chunk: dropped rows of y)
+  auto tn_fill = [&](char* tile, int cols, int q, const uint16_t* src, int64_t ld, int col0, int ncols, int k0) {
+    const int cpr = cols / 8;  // 16-byte chunks per row
+    const int row = (q * 1024 + lane * 16) / (cols * 2);
+    const int sc = lane % cpr;
+    const int c = sc ^ ((row & 3) << 2);
+    const int f = min(col0 + c * 8, ncols - 8);
+    const int64_t t = min((int64_t)(k0 + row), tok_rem - 1);
+    direct_fill(tile, q, src + t * ld + f);
+  };
   auto issue = [&](int stage, int k0) {
     char* sx = lds + stage * STAGE;
     char* sw = sx + C::XB;
     char* sa = sw + C::WB;
+    if constexpr (TN) {
+      constexpr int QX = 64 * C::BM * 2 / 1024 / C::NW, QW = 64 * C::BN * 2 / 1024 / C::NW;
+#pragma unroll
+      for (int i = 0; i < QX; ++i) tn_fill(sx, C::BM, wave * QX + i, x, ldx, m0, M, k0);
+#pragma unroll
+      for (int i = 0; i < QW; ++i)
+        tn_fill(sw, C::BN, wave * QW + i, reinterpret_cast<const uint16_t*>(w), ldw, n0, N, k0);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < C::NXI; ++i) {
       if constexpr (GATHER) direct_fill(sx, wave * C::NXI + i, xg[i] + k0);
@@ -261,6 +313,19 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     if constexpr (W8) {
 #pragma unroll
       for (int i = 0; i < W8C; ++i) w8stage[i] = ld_global_16(w8row[i] + k0);
+    }
+  };
+  // TN: K rows past the token count (clamped reads) are zeroed in the x' tile once it has
+  // landed, so they add nothing whatever the W' tile holds there
+  auto tn_zero = [&](int stage, int k0) {
+    if constexpr (TN) {
+      const int64_t valid = tok_rem - k0;
+      if (valid < 64) {
+        char* sx = lds + stage * STAGE;
+        const int v0 = valid > 0 ? (int)valid : 0;
+        constexpr int CPR = C::BM / 8;
+        for (int q = v0 * CPR + tid; q < 64 * CPR; q += NT) lds_write16(sx, q * 16, zero_u32x4());
+      }
     }
   };
   auto store_w8 = [&](int stage) {
@@ -321,10 +386,27 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     u32x4_t a[TPWX];
     u32x4_t xt[ALL_T ? 1 : TPWX];  // x rows of the T block (read directly when not all waves do T)
   };
+  // TN fragment: 32 columns from fbase, k = 16 kk + 8 (lane / 32) + 0..7 of a [64][cols]
+  // tile: two transposing reads, rows kb .. kb + 3 and kb + 4 .. kb + 7
+  auto tn_frag = [&](const char* tile, int cols, int fbase, int kk) {
+    const int g = lane >> 4, i16 = lane & 15;
+    const int row = kk * 16 + 8 * (g >> 1) + (i16 >> 2);
+    const int f = fbase + 16 * (g & 1) + 4 * (i16 & 3);
+    const int off = row * cols * 2 + (((f >> 3) ^ ((row & 3) << 2)) << 4) + (f & 7) * 2;
+    const uint2 lo = lds_read_tr8(tile, off), hi = lds_read_tr8(tile, off + 4 * cols * 2);
+    return u32x4_t{lo.x, lo.y, hi.x, hi.y};
+  };
   auto frag_load = [&](auto do_t, int stage, int kk, Frags& f) {
     const char* sx = lds + stage * STAGE;
     const char* sw = sx + C::XB;
     const char* sa = sw + C::WB;
+    if constexpr (TN) {
+#pragma unroll
+      for (int j = 0; j < C::MJ; ++j) f.x[j] = tn_frag(sx, C::BM, wm * C::TM + j * 32, kk);
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i) f.w[i] = tn_frag(sw, C::BN, wn * C::TN + i * 32, kk);
+      return;
+    }
     const int c = kk * 2 + lh;
 #pragma unroll
     for (int j = 0; j < C::MJ; ++j) f.x[j] = lds_read16(sx, lds_off(wm * C::TM + j * 32 + l32, c));
@@ -370,7 +452,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   auto interleave = [&](auto do_t) {
     constexpr int TT = decltype(do_t)::value ? TPW : 0;
     constexpr int NMF = (HAS_W ? C::NI * C::MJ : 0) + TT;
-    constexpr int NRD = C::MJ + (HAS_W ? C::NI : 0) + TT * (ALL_T ? 1 : 2);
+    constexpr int NRD = (C::MJ + (HAS_W ? C::NI : 0)) * (TN ? 2 : 1) + TT * (ALL_T ? 1 : 2);
     constexpr int PAIRS = NMF < NRD ? NMF : NRD;
 #pragma unroll
     for (int q = 0; q < PAIRS; ++q) {
@@ -395,6 +477,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     load_w8(0);
     wait_vm0();
     store_w8(0);
+    tn_zero(0, 0);
     ring_barrier();
     if (nk > 1) {
       issue(1, BK);
@@ -418,6 +501,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       if (kt + 1 < nk) {
         wait_vm0();          // tile kt+1 has landed (the only fill in flight)
         store_w8(buf ^ 1);   // fp8 base: decoded tile kt+1 into its buffer
+        tn_zero(buf ^ 1, (kt + 1) * BK);
         ring_barrier();      // all fragments of tile kt are read; tile kt+1 visible
       }
       // One code path for the last k step of every tile keeps the accumulators in one
@@ -639,11 +723,11 @@ bool groups_fit(const LoraArgs& p, int bn) {
   return true;
 }
 
-template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false>
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false>
 hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1) {
   const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
   const int tiles_n = (int)((p.N + C::BN - 1) / C::BN);
-  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT><<<dim3(tiles_m * tiles_n, splits), dim3(C::NT), 0, p.stream>>>(
+  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN><<<dim3(tiles_m * tiles_n, splits), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
@@ -1001,6 +1085,24 @@ hipError_t launch_product(const LoraArgs& p, float* part, int splits) {
   if (part == nullptr) return launch_rank<kBF16, true>(q, nullptr, 0);
   q.y = part; q.ldy = q.N;
   return launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
+}
+
+// Token-major products (the weight gradients): x' from p.x [tokens][M] (row stride ldx),
+// W' from p.w [tokens][N] (ldw), bf16, M and N multiples of 8, 16-byte aligned rows;
+// `tokens` rows in all, p.K per split (a multiple of BK; every split starts below `tokens`).
+// part == nullptr (splits 1): bf16 y' (p.y, p.ldy, p.yscale) over 256 x 256 tiles when they
+// fill the CUs, else 128 x 128; otherwise unscaled fp32 partials [splits][M][N] over 128 x 128.
+hipError_t launch_product_tn(const LoraArgs& p, int64_t tokens, float* part, int splits) {
+  LoraArgs q = p;
+  q.w_dtype = kBF16; q.w_scale = nullptr; q.a = nullptr; q.lda = 0; q.b = nullptr; q.ldb = 0; q.r = 0;
+  q.groups = 1; q.gather = nullptr; q.gather_rows = tokens; q.wmap = RowMap{}; q.wrows = q.N;
+  if (part == nullptr) {
+    const int64_t tb = ((q.M + 255) / 256) * ((q.N + 255) / 256);
+    if (tb >= 192) return launch_cfg<CfgBig, kBF16, true, 0, false, false, false, true>(q, nullptr, 0);
+    return launch_cfg<CfgSmall, kBF16, true, 0, false, false, false, true>(q, nullptr, 0);
+  }
+  q.y = part; q.ldy = q.N;
+  return launch_cfg<CfgSmall, kBF16, true, 0, false, false, true, true>(q, nullptr, 0, splits);
 }
 
 hipError_t launch_prefill(const LoraArgs& p) {

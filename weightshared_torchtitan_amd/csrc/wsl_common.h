@@ -152,6 +152,7 @@ int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool
 // pre-pass T = bf16(s x . A^T), for the weight gradients (csrc/lora_backward.hip).
 int product_splits(int64_t M, int64_t N, int64_t nk, bool divides);
 hipError_t launch_product(const LoraArgs& p, float* part, int splits);
+hipError_t launch_product_tn(const LoraArgs& p, int64_t tokens, float* part, int splits);
 size_t rank_prepass_bytes(int64_t M, int64_t K, int64_t rt);
 hipError_t rank_prepass(const LoraArgs& p, uint16_t* t);
 // Weight gradients dW = gy^T x, dA = s (gy B)^T x, dB = s gy^T (x A^T) (csrc/lora_backward.hip).

@@ -223,8 +223,8 @@ def lora_linear_weight_grads_op(x: torch.Tensor, gy: torch.Tensor, a: Optional[t
                                 need_b: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """dw = gy^T . x [N, K], da = scale (gy . b)^T . x [r, K], db = scale gy^T . (x . a^T)
     [N, r], each only when asked for (else an empty tensor), bf16 from bf16 x [M, K],
-    gy [M, N], a [r, K], b [N, r] (wsl_lora_linear_bwd_weights: one transpose of x and gy
-    to token-contiguous rows, then the fused kernel's tile loop on each product)."""
+    gy [M, N], a [r, K], b [N, r] (wsl_lora_linear_bwd_weights: dW over the tokens on the
+    fused kernel's tile loop, reading x and gy as they lie; da and db from dW)."""
     dev = _check_device(x, gy, a, b)
     x2 = _row_major(x.reshape(-1, x.shape[-1]), "x")
     gy2 = _row_major(gy.reshape(-1, gy.shape[-1]), "grad_y")
@@ -302,9 +302,9 @@ def _lora_linear_backward(ctx, gy):
         dx = gy . W + scale * U . a     one launch of the fused kernel, as the forward of
                                         the same op on (gy, W^T, b^T, a^T): the fused
                                         kernel's K is the forward's N
-        dW = gy^T . x                   one wsl::lora_linear_weight_grads call: reductions
-        da = scale * U^T . x            over the tokens M on the same tile kernel, after
-        db = scale * gy^T . T           one transpose of x and gy
+        dW = gy^T . x                   one wsl::lora_linear_weight_grads call: dW over the
+        da = scale * U^T . x            tokens on the fused kernel's tile loop (operands
+        db = scale * gy^T . T           read as they lie), da and db from dW
 
     The reference has no backward of its own: torch autograd differentiates
     LoRAModule.forward (torchtitan/models/llama3/model/model.py:189-192) and the base
