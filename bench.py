@@ -839,6 +839,7 @@ def main():
         extra["c4_weightshared_qwen3_0.6b_decode"] = bench_c4(dev)
         extra["factorized_embedding_c4_prefill"] = bench_embedding(dev, args.steps, args.warmup)
         extra["c2_backward"] = bench_backward(dev, min(args.steps, 10), min(args.warmup, 3))
+        extra["medium_m_qwen3_1.7b"] = bench_medium(dev, min(args.steps, 10), min(args.warmup, 3))
     if extra:
         res["extra"] = extra
     if not args.no_cpu and args.only is None:
