@@ -33,8 +33,8 @@ namespace {
 constexpr int TT = 64;       // transpose tile: 64 rows x 64 columns
 constexpr int TS = TT + 2;   // its LDS row stride in bf16 (odd word count: spread banks)
 
-// dst[c][i] = src[i][c] for i < R and 0 for R <= i < Rp (tokens padded to the split grid),
-// c < C. 16-byte global accesses both ways (C % 8 == 0, Rp % 8 == 0, 16-byte aligned rows).
+// dst[c][i] = src[i][c] for i < R and 0 for R <= i < Rp, c < C (B^T and dW^T here, Rp = R).
+// 16-byte global accesses both ways (C % 8 == 0, Rp % 8 == 0, 16-byte aligned rows).
 __global__ void __launch_bounds__(256) transpose_pad_kernel(const uint16_t* __restrict__ src, int64_t lds_,
                                                            int64_t R, int64_t C, uint16_t* __restrict__ dst,
                                                            int64_t ldd, int64_t Rp) {
