@@ -54,6 +54,7 @@
 // (scripts/generate/_generation.py:35-80 calling
 // torchtitan/models/llama3/model/model.py:189-192,392-398).
 #include <climits>
+#include <cstring>
 #include <cstdlib>
 #include <type_traits>
 
@@ -229,6 +230,7 @@ struct DecodeArgs {
   int rt, ge0, ge1, ge2;
   int gT, kst, kct;   // T groups (16 * 8 / KW rows of A), K split and slice
   int gY, ksy, kcy;   // W groups (16*NR rows of W), K split and slice
+  int kpt, kpy;       // passes over a T / W slice (x refilled between them)
   int flag_off;       // LDS byte offset of the broadcast word
   unsigned* cnt;      // counter prefix of the workspace
   uint64_t* tfin;     // T [M][rt]: ttag << 16 | bf16 bits
@@ -267,10 +269,21 @@ struct NoPrologue {
   __device__ __forceinline__ void operator()() const {}
 };
 
+// Passes over a workgroup's K slice: the slice is walked in `kp` equal parts, and x (rows
+// 0..M-1 of `x`) is refilled into the LDS between them, so a slice whose x rows do not fit
+// the LDS at once needs no K split across workgroups (and no split hand-off). kp = 1: the
+// x slice was filled whole before the call.
+struct XPasses {
+  const uint16_t* x = nullptr;
+  int64_t ldx = 0;
+  int kp = 1;
+};
+
 template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue>
 __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
                                            int kbeg, int kc, int M, char* smem, float* sums,
-                                           const Pro& pro = Pro(), RowMap rmap = RowMap{}) {
+                                           const Pro& pro = Pro(), RowMap rmap = RowMap{},
+                                           XPasses xp = XPasses{}) {
   using G = Geo<WDT>;
   constexpr int PD = NR == 1 ? 4 : (NR == 2 ? 2 : 1);  // K steps in flight per wave (NR*4*PD = 16 loads)
   constexpr int LPS = NR * 4;           // loads per step
@@ -285,6 +298,10 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
   const int nsteps = kc / G::WAVE_K;
   const int my = nsteps > kw ? (nsteps - kw + KW - 1) / KW : 0;
   const int rbase = row0 + rb * 16 * NR;
+  // Passes: each holds kcp columns, kcp / WAVE_K a multiple of KW (the plan's condition), so
+  // every wave takes spw steps of each pass and meets the pass barriers with the others.
+  const int kcp = kc / xp.kp;
+  const int spw = my / xp.kp;
 
   int64_t rowoff[NR];
 #pragma unroll
@@ -320,15 +337,27 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
   pro();  // the x slice computed from what the fills staged (W loads still in flight)
   if constexpr (!std::is_same<Pro, NoPrologue>::value) plain_barrier();
 
+  int ip = 0, pass = 0;  // step within the pass, pass
   for (int i0 = 0; i0 < my; i0 += PD) {
 #pragma unroll
     for (int q = 0; q < PD; ++q) {
       const int i = i0 + q;
       if (i < my) {
-        const int kl = (kw + i * KW) * G::WAVE_K + grp * G::LANE_K;
-        mma_step<WDT, NR, MB>(wv[q], smem, kc, xrow, kl, acc);
+        const int kl = (kw + ip * KW) * G::WAVE_K + grp * G::LANE_K;
+        mma_step<WDT, NR, MB>(wv[q], smem, kcp, xrow, kl, acc);
         if (i + PD < my)
           load_step<WDT, NR>(wv[q], mat, rowoff, kbeg + (kw + (i + PD) * KW) * G::WAVE_K + grp * G::LANE_K);
+        if (++ip == spw && i + 1 < my) {
+          // Pass boundary: every wave is done with this pass's x columns; refill them with
+          // the next pass's. The fill is younger than the W steps already in flight, so its
+          // wait also lands those, which the next MFMAs need first anyway.
+          ip = 0;
+          ++pass;
+          lds_barrier();
+          fill_x(smem, xp.x, xp.ldx, M, kbeg + pass * kcp, kcp, wave, lane);
+          wait_vm<0>();
+          lds_barrier();
+        }
       }
     }
   }
@@ -413,25 +442,38 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
     }
     return false;
   }
+  // The words of SC splits are requested together (one memory round trip for up to SC
+  // splits, where one split at a time cost a round trip each: M = 64, K = 6144 has six
+  // splits); they are still added in split order.
+  constexpr int SC = 4;
   for (int q0 = 0; q0 < n; q0 += LB * DT) {
     float v[LB];
 #pragma unroll
     for (int u = 0; u < LB; ++u) v[u] = 0.f;
-    for (int sp = 0; sp < ksplit - 1; ++sp) {
-      uint64_t* ps = part + (int64_t)sp * n;
-      uint64_t w[LB];
+    for (int sp0 = 0; sp0 < ksplit - 1; sp0 += SC) {
+      const int nsc = min(SC, ksplit - 1 - sp0);
+      uint64_t w[SC][LB];
 #pragma unroll
-      for (int u = 0; u < LB; ++u) w[u] = ld_agent(ps + min(q0 + u * DT + tid, n - 1));
+      for (int c = 0; c < SC; ++c)
 #pragma unroll
-      for (int u = 0; u < LB; ++u) {
-        const int q = q0 + u * DT + tid;
-        if (q < n) {
-          for (int it = 0; (w[u] >> 32) != ptag && it < spin; ++it) w[u] = ld_agent(ps + q);
-          const int rl = q / M, m = q % M;
-          v[u] += (w[u] >> 32) == ptag
-                      ? __uint_as_float((uint32_t)w[u])
-                      : direct_partial<WDT>(mat, ldm, map_row(min(row0 + rl, nrows - 1), rmap), x, ldx, m, sp * kc,
-                                            kc);
+        for (int u = 0; u < LB; ++u)
+          w[c][u] = c < nsc ? ld_agent(part + (int64_t)(sp0 + c) * n + min(q0 + u * DT + tid, n - 1)) : 0;
+#pragma unroll
+      for (int c = 0; c < SC; ++c) {
+        if (c >= nsc) break;
+        const int sp = sp0 + c;
+        uint64_t* ps = part + (int64_t)sp * n;
+#pragma unroll
+        for (int u = 0; u < LB; ++u) {
+          const int q = q0 + u * DT + tid;
+          if (q < n) {
+            for (int it = 0; (w[c][u] >> 32) != ptag && it < spin; ++it) w[c][u] = ld_agent(ps + q);
+            const int rl = q / M, m = q % M;
+            v[u] += (w[c][u] >> 32) == ptag
+                        ? __uint_as_float((uint32_t)w[c][u])
+                        : direct_partial<WDT>(mat, ldm, map_row(min(row0 + rl, nrows - 1), rmap), x, ldx, m,
+                                              sp * kc, kc);
+          }
         }
       }
     }
@@ -697,8 +739,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums,
                                    NormPrologue{&p, smem, ss, smem + p.nw_off});
     } else {
-      fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct, wave, lane);
-      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums);
+      fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kct / p.kpt, wave, lane);
+      slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums, NoPrologue{},
+                                   RowMap{}, XPasses{p.x, p.ldx, p.kpt});
     }
     const uint64_t tag = late_tag();
     if (split_reduce<kBF16, TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, ks, p.kst, p.M,
@@ -716,7 +759,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     const int kbeg = ks * p.kcy;
     const int row0 = g * ROWS;
     constexpr int RED = (NWV - RBK) * NR * MB * 4 * 64 * 4;
-    const int xs_bytes = p.M * p.kcy * 2;
+    const int xs_bytes = p.M * (p.kcy / p.kpy) * 2;
     const int post = RED + ROWS * MC * 4 + MC * (p.r32 + 8) * 2;
     char* bl = smem + (xs_bytes > post ? xs_bytes : post);
     float* sums = reinterpret_cast<float*>(smem + RED);
@@ -729,9 +772,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums,
                                   NormPrologue{&p, smem, ss, smem + p.nw_off}, p.wmap);
     } else {
-      fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kcy, wave, lane);
+      fill_x(smem, p.x, p.ldx, p.M, kbeg, p.kcy / p.kpy, wave, lane);
       if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
-      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums, NoPrologue{}, p.wmap);
+      slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums, NoPrologue{}, p.wmap,
+                                  XPasses{p.x, p.ldx, p.kpy});
     }
     const uint64_t tag = late_tag();
     if (split_reduce<WDT, ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, ks, p.ksy, p.M,
@@ -853,6 +897,7 @@ struct DecodePlan {
   int mb, nr, kw, rows, trows, r32;
   int gT, kst, kct;
   int gY, ksy, kcy;
+  int kpt, kpy;  // passes over a slice (1: the x slice is filled once)
   size_t off_t, off_pt, off_py, total;
   size_t flag_off, smem;
   bool ok;
@@ -860,7 +905,8 @@ struct DecodePlan {
 
 size_t plan_smem(const DecodePlan& pl, int64_t M, size_t* flag_off) {
   // LDS: max(x slice, reduction + sums + T) + B rows, then the broadcast word.
-  const size_t xs = (size_t)M * (pl.kcy > pl.kct ? pl.kcy : pl.kct) * 2;
+  const size_t xy = (size_t)pl.kcy / pl.kpy, xt = (size_t)pl.kct / pl.kpt;
+  const size_t xs = (size_t)M * (xy > xt ? xy : xt) * 2;
   const size_t red = (size_t)(NWV - NWV / pl.kw) * pl.nr * pl.mb * 4 * 64 * 4;
   const size_t post = red + (size_t)pl.rows * 16 * pl.mb * 4 + (size_t)16 * pl.mb * (pl.r32 + 8) * 2;
   *flag_off = (xs > post ? xs : post) + (size_t)pl.rows * pl.r32 * 2;
@@ -883,11 +929,24 @@ double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
 // fused kernels are built for (one token block).
 enum class Pick { kAll, kFused };
 
+// WSL_DECODE_PASSES: "off" keeps K splits, "on" takes the pass form wherever it applies,
+// anything else the measured rule of plan_decode (read per call: a benchmark or test can
+// switch it).
+enum class PassMode { kAuto, kOff, kOn };
+PassMode pass_mode() {
+  const char* e = std::getenv("WSL_DECODE_PASSES");
+  if (e == nullptr) return PassMode::kAuto;
+  if (std::strcmp(e, "off") == 0) return PassMode::kOff;
+  if (std::strcmp(e, "on") == 0) return PassMode::kOn;
+  return PassMode::kAuto;
+}
+
 // rt: rank rows of the T work (groups * r for a grouped launch; r when negative).
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick pick = Pick::kAll,
                        int64_t rt = -1) {
   if (rt < 0) rt = r;
   DecodePlan pl{};
+  pl.kpt = pl.kpy = 1;
   pl.mb = (int)((M + 15) / 16);
   if (pl.mb < 1) pl.mb = 1;
   pl.nr = pl.mb >= 3 ? 2 : 1;
@@ -943,6 +1002,49 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
       }
     }
     pl.rows = 16 * pl.nr;
+    // The pass form: where x does not fit the LDS whole, one workgroup walks its rows' whole
+    // K in passes (x refilled between them) instead of K splits over several workgroups.
+    // That halves (or more) the workgroups, so a grid that needed two waves of one workgroup
+    // per CU may need one, and drops the split hand-off; each pass boundary costs a refill
+    // round trip. Measured at M = 64 on the Qwen3-1.7B shapes (grouped launches): with two
+    // slices it won everywhere (gate|up 41.7 -> 23.8 us, one wave of workgroups instead of
+    // two; q|k|v 19.7 -> 16.9; o 15.7 -> 15.0), with more it lost (down, six slices: 23.4
+    // against about 30 us; M = 32 down, three slices: 1751 -> 1674 GB/s over the layer). So
+    // it is taken for two slices, with the rows per workgroup the model picks among its own
+    // choices.
+    const int wk = wave_k_of(wdt);
+    const PassMode mode = pass_mode();
+    const int max_slices = mode == PassMode::kOn ? INT_MAX : (mode == PassMode::kOff ? 1 : 2);
+    const bool w_pass = pl.ksy > 1 && pl.ksy <= max_slices && (pl.kcy / wk) % 8 == 0;
+    const bool t_pass = pl.kst > 1 && (pl.kct / wave_k_of(kBF16)) % 8 == 0;
+    if (w_pass && pick == Pick::kAll) {
+      DecodePlan c = pl;
+      c.kpy = pl.ksy;
+      c.ksy = 1;
+      c.kcy = (int)K;
+      if (t_pass) {
+        c.kpt = pl.kst;
+        c.kst = 1;
+        c.kct = (int)K;
+      }
+      double pass_best = 1e30;
+      for (int nr : {1, 2, 4}) {
+        DecodePlan d = c;
+        d.nr = nr;
+        d.rows = 16 * nr;
+        size_t fo;
+        if (plan_smem(d, M, &fo) > (size_t)LDS_MAX) continue;
+        const double cost = plan_cost(d, M, N, nr);
+        if (cost < pass_best) {
+          pass_best = cost;
+          c.nr = nr;
+        }
+      }
+      if (pass_best < 1e30) {
+        c.rows = 16 * c.nr;
+        pl = c;
+      }
+    }
   }
   pl.gY = (int)((N + pl.rows - 1) / pl.rows);
   pl.ok = pl.ksy > 0 && pl.kst > 0 &&
@@ -1095,6 +1197,7 @@ DecodeArgs make_args(const LoraArgs& p, const DecodePlan& pl, char* cnt, char* d
   a.ge2 = p.groups > 3 ? (int)p.gend[2] : INT_MAX;
   a.gT = pl.gT; a.kst = pl.kst; a.kct = pl.kct;
   a.gY = pl.gY; a.ksy = pl.ksy; a.kcy = pl.kcy;
+  a.kpt = pl.kpt; a.kpy = pl.kpy;
   a.flag_off = (int)pl.flag_off;
   a.cnt = reinterpret_cast<unsigned*>(cnt);
   a.tfin = reinterpret_cast<uint64_t*>(data + pl.off_t);
