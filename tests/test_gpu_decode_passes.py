@@ -143,3 +143,31 @@ def test_decode_forms_fp8(gpu, mode, monkeypatch):
     _say(f"  vs fp32 W: {err:.3e}   vs dequantised W: {err_dq:.3e}")
     assert err <= FP8_TOL
     assert err_dq <= BF16_TOL
+
+
+def test_split_partials_are_consumed(gpu, monkeypatch):
+    """After split-form launches (T and W split six ways) the workspace past the counter
+    prefix holds no partial-sum word (bit 63 clear, tag bits set): the last split takes
+    each word, so none can meet a launch whose 31-bit tag repeats its own. T words (bit 63
+    set) stay, as their readers are many."""
+    import ctypes
+    from weightshared_torchtitan_amd import _native as N
+    monkeypatch.setenv("WSL_DECODE_PASSES", "off")
+    M, N_, K, r = 64, 2048, 6144, 64
+    _say(f"[decode split partials consumed] M={M} N={N_} K={K} r={r}")
+    x, W, A, B = (t.to(gpu) for t in _inputs(M, N_, K, r, seed=47))
+    y = torch.empty(M, N_, dtype=torch.bfloat16, device=gpu)
+    nb = N.workspace_bytes(M, N_, K, r, N.WSL_DTYPE_BF16)
+    ws = torch.zeros(nb // 8, dtype=torch.int64, device=gpu)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    for _ in range(3):
+        N.check(N.lib().wsl_lora_linear_fwd(p(x), K, p(W), K, N.WSL_DTYPE_BF16, None, p(A), K, p(B), r, 2.0,
+                                            p(y), N_, M, N_, K, r, p(ws), nb, stream), "wsl_lora_linear_fwd")
+    torch.cuda.synchronize()
+    words = ws[65536 // 8:].cpu()
+    partial = (words >= 0) & ((words >> 32) != 0)  # bit 63 clear, upper half non-zero
+    assert int(partial.sum()) == 0
+    assert int((words < 0).sum()) > 0  # the T words of the launch are there
+    ref = O.lora_linear(_np(x.cpu()), _np(W.cpu()), _np(A.cpu()), _np(B.cpu()), 2.0)
+    assert O.max_rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL

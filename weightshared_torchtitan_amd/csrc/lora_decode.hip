@@ -261,6 +261,10 @@ __device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
 __device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Reads a word and leaves zero in its place (one atomic round trip, like the load).
+__device__ __forceinline__ uint64_t take_agent(uint64_t* p) {
+  return __hip_atomic_exchange(p, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Sums over one K slice of a group of 16*NR rows of `mat` against x (whose fill into
 // smem this wave has issued just before), reduced over the waves into sums[row][m]
@@ -444,7 +448,11 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
   }
   // The words of SC splits are requested together (one memory round trip for up to SC
   // splits, where one split at a time cost a round trip each: M = 64, K = 6144 has six
-  // splits); they are still added in split order.
+  // splits); they are still added in split order. Each word is taken (exchanged with zero)
+  // rather than loaded, so no partial outlives its launch: the 31-bit tag repeats after
+  // 2^31 - 1 launches, and a word left in a region no later launch rewrote could otherwise
+  // match a launch that far ahead. Zero matches no tag; a word taken before its writer
+  // stored it is polled again.
   constexpr int SC = 4;
   for (int q0 = 0; q0 < n; q0 += LB * DT) {
     float v[LB];
@@ -456,8 +464,10 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
 #pragma unroll
       for (int c = 0; c < SC; ++c)
 #pragma unroll
-        for (int u = 0; u < LB; ++u)
-          w[c][u] = c < nsc ? ld_agent(part + (int64_t)(sp0 + c) * n + min(q0 + u * DT + tid, n - 1)) : 0;
+        for (int u = 0; u < LB; ++u) {
+          const int q = q0 + u * DT + tid;
+          w[c][u] = (c < nsc && q < n) ? take_agent(part + (int64_t)(sp0 + c) * n + q) : 0;
+        }
 #pragma unroll
       for (int c = 0; c < SC; ++c) {
         if (c >= nsc) break;
@@ -467,7 +477,7 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
         for (int u = 0; u < LB; ++u) {
           const int q = q0 + u * DT + tid;
           if (q < n) {
-            for (int it = 0; (w[c][u] >> 32) != ptag && it < spin; ++it) w[c][u] = ld_agent(ps + q);
+            for (int it = 0; (w[c][u] >> 32) != ptag && it < spin; ++it) w[c][u] = take_agent(ps + q);
             const int rl = q / M, m = q % M;
             v[u] += (w[c][u] >> 32) == ptag
                         ? __uint_as_float((uint32_t)w[c][u])
