@@ -1,7 +1,8 @@
 """The decode path's two ways to cover a K whose x rows do not fit the LDS at once: K split
 over several workgroups (partials handed to the last split) and the pass form (one workgroup
-walks its rows' whole K, refilling x between passes). Each form, forced with
-WSL_DECODE_PASSES=off / on, against the float64 oracle (1e-2 bf16, 3e-2 fp8 base against
+walks its K range in passes, refilling x between them), and the plan's own mix of the two
+(two passes per split for an even slice count). Each form, forced with WSL_DECODE_PASSES=off
+/ on or left to the plan (auto), against the float64 oracle (1e-2 bf16, 3e-2 fp8 base against
 fp32 W and 1e-2 against the dequantised W), bitwise repeatable, and with the T wait forced
 to its local fallback. The forms sum K in different orders, so they agree with each other
 only to the bar."""
@@ -37,8 +38,9 @@ def _inputs(M, N, K, r, seed):
 CASES = [
     # M, N, K, r: x is M x K bf16, more than one slice of the LDS at these sizes
     (64, 6144, 2048, 64),    # two slices (gate at 1.7B)
-    (64, 2048, 6144, 64),    # six slices (down at 1.7B)
+    (64, 2048, 6144, 64),    # six slices (down at 1.7B; auto: three splits of two passes)
     (48, 1024, 2048, 64),    # three token blocks
+    (48, 1000, 6144, 40),    # six slices at three token blocks, N tail
     (33, 1000, 6144, 24),    # N tail, partial rank group
     (64, 1000, 6144, 24),
     (17, 640, 12288, 8),     # two token blocks, three slices
@@ -47,11 +49,18 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("mode", ["off", "on"])
+def _mode(monkeypatch, mode):
+    if mode == "auto":
+        monkeypatch.delenv("WSL_DECODE_PASSES", raising=False)
+    else:
+        monkeypatch.setenv("WSL_DECODE_PASSES", mode)
+
+
+@pytest.mark.parametrize("mode", ["off", "on", "auto"])
 @pytest.mark.parametrize("M,N,K,r", CASES)
 def test_decode_forms_match_oracle(gpu, M, N, K, r, mode, monkeypatch):
     import weightshared_torchtitan_amd as wsl
-    monkeypatch.setenv("WSL_DECODE_PASSES", mode)
+    _mode(monkeypatch, mode)
     _say(f"[decode {mode}] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=3 * M + N + K + r)
     d = lambda t: None if t is None else t.to(gpu)
@@ -80,12 +89,12 @@ def test_override_reaches_the_plan(gpu, monkeypatch):
     assert ((ys["off"].float() - ys["on"].float()).abs().max() / ys["off"].float().abs().max()).item() < BF16_TOL
 
 
-@pytest.mark.parametrize("mode", ["off", "on"])
+@pytest.mark.parametrize("mode", ["off", "on", "auto"])
 def test_decode_forms_grouped(gpu, mode, monkeypatch):
     """gate|up and q|k|v of Qwen3-1.7B at M = 64 as grouped launches; every group's block
     against the oracle."""
     from weightshared_torchtitan_amd import ops
-    monkeypatch.setenv("WSL_DECODE_PASSES", mode)
+    _mode(monkeypatch, mode)
     M, K, r = 64, 2048, 64
     for group_n in ((6144, 6144), (2048, 1024, 1024)):
         _say(f"[decode grouped {mode}] M={M} K={K} r={r} groups={group_n}")
@@ -105,11 +114,12 @@ def test_decode_forms_grouped(gpu, mode, monkeypatch):
             n0 += n
 
 
-def test_pass_form_t_fallback(gpu, monkeypatch):
-    """The pass form with the T wait bound forced to zero from the host: the W workgroups
+@pytest.mark.parametrize("mode", ["on", "auto"])
+def test_pass_form_t_fallback(gpu, mode, monkeypatch):
+    """The pass forms with the T wait bound forced to zero from the host: the W workgroups
     compute T themselves, within the bar."""
     import weightshared_torchtitan_amd as wsl
-    monkeypatch.setenv("WSL_DECODE_PASSES", "on")
+    _mode(monkeypatch, mode)
     M, N, K, r = 64, 2048, 6144, 64
     _say(f"[decode pass T fallback] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=41)

@@ -939,9 +939,9 @@ double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
 // fused kernels are built for (one token block).
 enum class Pick { kAll, kFused };
 
-// WSL_DECODE_PASSES: "off" keeps K splits, "on" takes the pass form wherever it applies,
-// anything else the measured rule of plan_decode (read per call: a benchmark or test can
-// switch it).
+// WSL_DECODE_PASSES: "off" keeps K splits, "on" walks every split slice in passes (one
+// workgroup per row group), anything else the measured rule of plan_decode (read per call:
+// a benchmark or test can switch it).
 enum class PassMode { kAuto, kOff, kOn };
 PassMode pass_mode() {
   const char* e = std::getenv("WSL_DECODE_PASSES");
@@ -1012,30 +1012,31 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
       }
     }
     pl.rows = 16 * pl.nr;
-    // The pass form: where x does not fit the LDS whole, one workgroup walks its rows' whole
-    // K in passes (x refilled between them) instead of K splits over several workgroups.
+    // The pass form: where x does not fit the LDS whole, one workgroup walks its rows' K
+    // range in passes (x refilled between them) instead of spreading it over more K splits.
     // That halves (or more) the workgroups, so a grid that needed two waves of one workgroup
-    // per CU may need one, and drops the split hand-off; each pass boundary costs a refill
-    // round trip. Measured at M = 64 on the Qwen3-1.7B shapes (grouped launches): with two
-    // slices it won everywhere (gate|up 41.7 -> 23.8 us, one wave of workgroups instead of
-    // two; q|k|v 19.7 -> 16.9; o 15.7 -> 15.0), with more it lost (down, six slices: 23.4
-    // against about 30 us; M = 32 down, three slices: 1751 -> 1674 GB/s over the layer). So
-    // it is taken for two slices, with the rows per workgroup the model picks among its own
-    // choices.
+    // per CU may need one, and shortens the split hand-off; each pass boundary costs a
+    // refill round trip. Measured at M = 64 on the Qwen3-1.7B shapes (grouped launches):
+    // two slices as two passes won everywhere (gate|up 41.7 -> 23.8 us, one wave of
+    // workgroups instead of two; q|k|v 19.7 -> 16.9; o 15.7 -> 15.0); six slices (down) as
+    // three splits of two passes took 22.1 us against 23.9 for six splits, and as six
+    // passes 28.8; three slices (down at M = 32) as passes lost (17.3 -> 19.3). So an even
+    // slice count takes two passes per split, with the rows per workgroup the model picks.
     const int wk = wave_k_of(wdt);
     const PassMode mode = pass_mode();
-    const int max_slices = mode == PassMode::kOn ? INT_MAX : (mode == PassMode::kOff ? 1 : 2);
-    const bool w_pass = pl.ksy > 1 && pl.ksy <= max_slices && (pl.kcy / wk) % 8 == 0;
-    const bool t_pass = pl.kst > 1 && (pl.kct / wave_k_of(kBF16)) % 8 == 0;
+    const bool all_passes = mode == PassMode::kOn;
+    const bool w_pass = mode != PassMode::kOff && pl.ksy > 1 && (all_passes || pl.ksy % 2 == 0) &&
+                        (pl.kcy / wk) % 8 == 0;
+    const bool t_pass = pl.kst > 1 && (all_passes || pl.kst % 2 == 0) && (pl.kct / wave_k_of(kBF16)) % 8 == 0;
     if (w_pass && pick == Pick::kAll) {
       DecodePlan c = pl;
-      c.kpy = pl.ksy;
-      c.ksy = 1;
-      c.kcy = (int)K;
+      c.kpy = all_passes ? pl.ksy : 2;
+      c.ksy = pl.ksy / c.kpy;
+      c.kcy = (int)(K / c.ksy);
       if (t_pass) {
-        c.kpt = pl.kst;
-        c.kst = 1;
-        c.kct = (int)K;
+        c.kpt = all_passes ? pl.kst : 2;
+        c.kst = pl.kst / c.kpt;
+        c.kct = (int)(K / c.kst);
       }
       double pass_best = 1e30;
       for (int nr : {1, 2, 4}) {
