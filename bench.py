@@ -347,37 +347,41 @@ def bench_c3(dev, steps, warmup):
 
 
 def bench_medium(dev, steps, warmup):
-    """Medium M (between the decode path's 64 and a few hundred tokens) at the Qwen3-1.7B
-    projection shapes, r = 64, cold weights (6 rotating copies), 28 layers per graph, grouped
-    q|k|v and gate|up: the prefill path's split-K form (the default for 64 < M <= 256) beside
-    its unsplit tiles (WSL_PREFILL_MEDIUM=off), and M = 64 on the decode path for reference."""
+    """Medium M (above the decode path's fused forms and up to a few hundred tokens) at the
+    Qwen3-1.7B projection shapes, r = 64, cold weights (6 rotating copies), 28 layers per
+    graph, grouped q|k|v and gate|up, each way the library can run them on the same inputs:
+    the decode path (the default up to 128 tokens), the prefill path's split-K form
+    (WSL_DECODE_WIDE=off; the default for 129-160 tokens) and its unsplit tiles (also
+    WSL_PREFILL_MEDIUM=off)."""
     out = {}
-    saved = os.environ.get("WSL_PREFILL_MEDIUM")
+    keys = ("WSL_DECODE_WIDE", "WSL_PREFILL_MEDIUM")
+    saved = {k: os.environ.get(k) for k in keys}
+    ways = (("decode", {}), ("split", {"WSL_DECODE_WIDE": "off"}),
+            ("unsplit", {"WSL_DECODE_WIDE": "off", "WSL_PREFILL_MEDIUM": "off"}))
     try:
-        for M in (64, 65, 96, 128, 192, 256):
+        for M in (64, 65, 96, 128, 160, 192, 256):
             row = {}
-            for label, env in (("split", None), ("unsplit", "off")):
-                if M == 64 and env is not None:
-                    continue
-                if env is None:
-                    os.environ.pop("WSL_PREFILL_MEDIUM", None)
-                else:
-                    os.environ["WSL_PREFILL_MEDIUM"] = env
+            for label, env in ways:
+                if (label == "decode" and M > 128) or (label != "decode" and M <= 64):
+                    continue  # decode runs up to 128 tokens; the prefill forms above 64
+                for k in keys:
+                    os.environ.pop(k, None)
+                os.environ.update(env)
                 st = ProjectionStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
                 st.stack_groups()
                 g = graph_of(st.run_grouped)
                 ms = time_replays(g, steps, warmup)
-                row["decode" if M == 64 else label] = {
-                    "ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
-                    "TFLOP/s": round(st.flops() / ms / 1e9, 1)}
+                row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
+                              "TFLOP/s": round(st.flops() / ms / 1e9, 1)}
                 del g, st
                 torch.cuda.empty_cache()
             out[f"M={M}"] = row
     finally:
-        if saved is None:
-            os.environ.pop("WSL_PREFILL_MEDIUM", None)
-        else:
-            os.environ["WSL_PREFILL_MEDIUM"] = saved
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     return out
 
 

@@ -448,3 +448,15 @@ def test_bwd_weights_workspace_holds_dw_copies_and_partials():
     assert got >= 65536 + 2 * (2 * Nn * K * 2 + 4 * Nn * K * 4)
     assert got < 65536 + 2 * (K + Nn) * M * 2
     assert N.bwd_weights_workspace_bytes(0, Nn, K, r) >= 65536
+
+
+@pytest.mark.parametrize("M,K", [(80, 256), (128, 640), (96, 2048), (65, 6144)])
+def test_workspace_bytes_of_wide_decode_shapes(M, K):
+    """65-128 tokens: the decode plan takes the shape or declines it (K not a multiple of its
+    pass slice); either way the size queries give the bytes of a real path, not a wrapped
+    subtraction."""
+    for r in (0, 32):
+        single = N.workspace_bytes(M, 3072, K, r, N.WSL_DTYPE_BF16)
+        grouped = N.grouped_workspace_bytes(M, K, r, (1024, 512, 512), N.WSL_DTYPE_BF16)
+        for b in (single, grouped):
+            assert 0 < b < (1 << 32)

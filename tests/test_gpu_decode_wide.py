@@ -1,0 +1,113 @@
+"""The decode path from 65 to 128 tokens (plain bf16 launches): five to eight token blocks,
+four waves along K, x walked in pass slices of 512 or 1024 columns, the slices spread over
+the K splits that keep one wave of workgroups. Against the float64 oracle (1e-2), bitwise
+repeatable, with the T wait forced to its local fallback, beside the prefill path's medium
+form (WSL_DECODE_WIDE=off) on the same inputs, and as grouped launches: bit for bit the
+single launches (a grouped launch whose K splits would differ from a group's runs the
+groups one by one)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lora_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _np(t):
+    return None if t is None else t.float().numpy()
+
+
+def _inputs(M, N, K, r, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    A = (torch.randn(r, K, generator=g) * 0.02).bfloat16() if r else None
+    B = (torch.randn(N, r, generator=g) * 0.02).bfloat16() if r else None
+    return x, W, A, B
+
+
+CASES = [
+    # M, N, K, r
+    (65, 2048, 2048, 64),    # 1024-column passes (x of 65 rows fits), o at 1.7B
+    (72, 6144, 2048, 64),    # 512-column passes, 64 rows per workgroup
+    (80, 2048, 6144, 64),    # twelve slices over three K splits (down at 1.7B)
+    (96, 1000, 2048, 24),    # N tail, partial rank group
+    (112, 4096, 1024, 16),
+    (128, 2048, 2048, 64),   # eight token blocks
+    (128, 12288, 2048, 64),  # gate|up at 1.7B, one wave of workgroups
+    (100, 3072, 1024, 0),    # plain linear
+    (127, 640, 4096, 8),     # M one short of 128
+]
+
+
+@pytest.mark.parametrize("M,N,K,r", CASES)
+def test_wide_decode_matches_oracle(gpu, M, N, K, r, monkeypatch):
+    import weightshared_torchtitan_amd as wsl
+    monkeypatch.delenv("WSL_DECODE_WIDE", raising=False)
+    _say(f"[decode wide] M={M} N={N} K={K} r={r}")
+    x, W, A, B = _inputs(M, N, K, r, seed=5 * M + N + K + r)
+    d = lambda t: None if t is None else t.to(gpu)
+    y1 = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0)
+    y2 = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), 2.0)
+    err = O.max_rel_err(y1.float().cpu().numpy(), ref)
+    _say(f"  max_rel_err={err:.3e}")
+    assert np.isfinite(err) and err <= BF16_TOL
+    # the medium form of the prefill path on the same inputs: same bar, a different kernel
+    monkeypatch.setenv("WSL_DECODE_WIDE", "off")
+    y3 = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0)
+    torch.cuda.synchronize()
+    assert O.max_rel_err(y3.float().cpu().numpy(), ref) <= BF16_TOL
+
+
+def test_wide_decode_t_fallback(gpu, monkeypatch):
+    """T wait bound forced to zero from the host: the W workgroups compute T themselves."""
+    import weightshared_torchtitan_amd as wsl
+    monkeypatch.delenv("WSL_DECODE_WIDE", raising=False)
+    M, N, K, r = 96, 2048, 6144, 64
+    _say(f"[decode wide T fallback] M={M} N={N} K={K} r={r}")
+    x, W, A, B = _inputs(M, N, K, r, seed=53)
+    d = lambda t: t.to(gpu)
+    monkeypatch.setenv("WSL_DECODE_SPIN_LIMIT", "0")
+    y = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0).float().cpu().numpy()
+    torch.cuda.synchronize()
+    monkeypatch.delenv("WSL_DECODE_SPIN_LIMIT")
+    ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), 2.0)
+    assert O.max_rel_err(y, ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("M,K,group_n", [
+    (96, 2048, (6144, 6144)),        # gate|up: the groups split K as the grouped launch does
+    (96, 2048, (2048, 1024, 1024)),  # q|k|v: q alone splits K otherwise -> groups one by one
+    (128, 6144, (2048, 2048)),
+    (72, 1024, (3072, 3072, 1024)),
+])
+def test_wide_decode_grouped_matches_single(gpu, M, K, group_n, monkeypatch):
+    import weightshared_torchtitan_amd as wsl
+    from weightshared_torchtitan_amd import ops
+    monkeypatch.delenv("WSL_DECODE_WIDE", raising=False)
+    r = 64
+    _say(f"[decode wide grouped] M={M} K={K} r={r} groups={group_n}")
+    g = torch.Generator().manual_seed(M + K + len(group_n))
+    x = torch.randn(M, K, generator=g).bfloat16().to(gpu)
+    Ws = [(torch.randn(n, K, generator=g) * 0.02).bfloat16().to(gpu) for n in group_n]
+    As = [(torch.randn(r, K, generator=g) * 0.02).bfloat16().to(gpu) for _ in group_n]
+    Bs = [(torch.randn(n, r, generator=g) * 0.02).bfloat16().to(gpu) for n in group_n]
+    y = ops.lora_linear_grouped_op(x, torch.cat(Ws), None, torch.cat(As), torch.cat(Bs), 2.0, list(group_n))
+    n0 = 0
+    for i, n in enumerate(group_n):
+        yi = wsl.lora_linear(x, Ws[i], As[i], Bs[i], 2.0)
+        assert torch.equal(y[:, n0:n0 + n], yi), i
+        n0 += n
+    ref = O.lora_linear(x.float().cpu().numpy(), Ws[0].float().cpu().numpy(), As[0].float().cpu().numpy(),
+                        Bs[0].float().cpu().numpy(), 2.0)
+    assert O.max_rel_err(y[:, :group_n[0]].float().cpu().numpy(), ref) <= BF16_TOL

@@ -923,13 +923,13 @@ size_t plan_smem(const DecodePlan& pl, int64_t M, size_t* flag_off) {
   return *flag_off + 16;  // the broadcast word (the RMSNorm prologue adds its own after it)
 }
 
-// Modelled time of a plan with `nr` row blocks per wave (KW = 8, so 16*nr rows per W
+// Modelled time of a plan with `nr` row blocks per wave (16 * nr * 8 / KW rows per W
 // workgroup), in us: one workgroup per CU (the x slice holds most of the LDS), so the
 // grid runs in ceil(workgroups / 256) waves, each costing a fixed latency plus the
 // workgroup's bytes (W rows and x slice) at the rate one CU streams them. Constants from
 // M = 32 and 64 sweeps over N, K in {1024, 2048, 6144}: 4 us and 40 GB/s per CU.
 double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
-  const int64_t rows = 16 * nr;
+  const int64_t rows = (int64_t)(NWV / pl.kw) * 16 * nr;
   const int64_t wgs = (int64_t)pl.gT * pl.kst + (N + rows - 1) / rows * pl.ksy;
   const double waves = (double)((wgs + 255) / 256);
   return waves * (4.0 + (double)((rows + M) * pl.kcy * 2) / 40e3);
@@ -1057,6 +1057,45 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
       }
     }
   }
+  // Five to eight token blocks (65 <= M <= 128, plain bf16 launches): x is walked in pass
+  // slices of 1024 columns, or 512 where 1024 do not fit the LDS (128 KB at M = 128): eight
+  // or four wave steps, so four waves run along K and two row blocks share a workgroup.
+  // 32 rows per workgroup, or 64 where 32 would take more than one wave of workgroups; the
+  // slices are then spread over the largest number of K splits that keeps the grid within
+  // one wave of workgroups (more workgroups stream faster; passes spare the workgroups a
+  // split hand-off), the rest walked as passes. Every choice depends on M, K and the grid,
+  // and a grouped launch fills its groups' rows as the single launches do.
+  if (pick == Pick::kAll && pl.mb > 4) {
+    pl.ok = false;
+    const int64_t kcp = (M * 1024 * 2 <= XS_MAX && K % 1024 == 0) ? 1024 : 512;
+    if (wdt == kBF16 && K % kcp == 0 && M * kcp * 2 <= XS_MAX) {
+      const int slices = (int)(K / kcp);
+      pl.kw = 4;
+      pl.trows = (NWV / pl.kw) * 16;
+      pl.gT = r > 0 ? (int)((rt + pl.trows - 1) / pl.trows) : 0;
+      pl.nr = 1;
+      pl.rows = (NWV / pl.kw) * 16;
+      if ((N + pl.rows - 1) / pl.rows + pl.gT > 256) {
+        pl.nr = 2;
+        pl.rows *= 2;
+      }
+      const int64_t gy = (N + pl.rows - 1) / pl.rows;
+      int splits = 1;
+      for (int d = 1; d <= slices; ++d)
+        if (slices % d == 0 && (gy + pl.gT) * d <= 256) splits = d;
+      pl.ksy = splits;
+      pl.kpy = slices / splits;
+      pl.kcy = (int)(K / splits);
+      if (r > 0) {
+        pl.kst = splits;
+        pl.kpt = pl.kpy;
+        pl.kct = pl.kcy;
+      }
+      size_t fo;
+      pl.ok = plan_smem(pl, M, &fo) <= (size_t)LDS_MAX;
+    }
+    if (!pl.ok) return pl;
+  }
   pl.gY = (int)((N + pl.rows - 1) / pl.rows);
   pl.ok = pl.ksy > 0 && pl.kst > 0 &&
           (uint64_t)pl.gT * pl.kst + (uint64_t)pl.gY * pl.ksy < kLaunchUnit;
@@ -1117,6 +1156,12 @@ hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t sme
       if (mb == 3) return launch_one<WDT, 1, 3, KW>(a, grid, smem, st);
       if (mb == 4) return launch_one<WDT, 1, 4, KW>(a, grid, smem, st);
     }
+    if constexpr (KW == 4 && WDT == kBF16) {  // 65 <= M <= 128
+      if (mb == 5) return launch_one<WDT, 1, 5, KW>(a, grid, smem, st);
+      if (mb == 6) return launch_one<WDT, 1, 6, KW>(a, grid, smem, st);
+      if (mb == 7) return launch_one<WDT, 1, 7, KW>(a, grid, smem, st);
+      if (mb == 8) return launch_one<WDT, 1, 8, KW>(a, grid, smem, st);
+    }
     return hipErrorInvalidValue;
   }
   if (nr == 2) {
@@ -1130,6 +1175,12 @@ hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t sme
     }
     if (mb == 3) return launch_one<WDT, 2, 3, KW>(a, grid, smem, st);
     if (mb == 4) return launch_one<WDT, 2, 4, KW>(a, grid, smem, st);
+    if constexpr (KW == 4 && WDT == kBF16) {  // 65 <= M <= 128
+      if (mb == 5) return launch_one<WDT, 2, 5, KW>(a, grid, smem, st);
+      if (mb == 6) return launch_one<WDT, 2, 6, KW>(a, grid, smem, st);
+      if (mb == 7) return launch_one<WDT, 2, 7, KW>(a, grid, smem, st);
+      if (mb == 8) return launch_one<WDT, 2, 8, KW>(a, grid, smem, st);
+    }
     return hipErrorInvalidValue;
   }
   if constexpr (KW == 8) {
@@ -1167,7 +1218,14 @@ int spin_limit() {
 }  // namespace
 
 bool decode_supported(const LoraArgs& p) {
-  if (p.M < 1 || p.M > kDecodeMaxM) return false;
+  if (p.M < 1 || p.M > kDecodePlainMaxM) return false;
+  if (p.M > kDecodeMaxM) {
+    if (p.w_dtype != kBF16) return false;  // fp8 base above 64 tokens: the prefill path
+    // WSL_DECODE_WIDE=off keeps 65-128 tokens on the prefill path's medium form (read per
+    // call, for side-by-side timing)
+    const char* e = std::getenv("WSL_DECODE_WIDE");
+    if (e != nullptr && std::strcmp(e, "off") == 0) return false;
+  }
   if (p.w == nullptr) return false;  // the delta-only form runs on the prefill path
   if (p.N > (int64_t)1 << 30 || p.K > (int64_t)1 << 30) return false;
   const bool fp8 = p.w_dtype == kFP8;
@@ -1237,6 +1295,22 @@ bool decode_groups_supported(const LoraArgs& p) {
   return true;
 }
 
+// Whether a grouped launch sums every output in the order its group's single launch does:
+// a row's order depends on the waves along K and the K splits of W and of T (the passes
+// and the rows per workgroup do not change it). The plans below 65 tokens never depend on
+// N; above, the split count fills one wave of workgroups and does.
+bool decode_groups_consistent(const LoraArgs& p) {
+  const DecodePlan pg = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kAll, p.r * p.groups);
+  int64_t n0 = 0;
+  for (int g = 0; g < p.groups; ++g) {
+    const int64_t ng = (g + 1 < p.groups ? p.gend[g] : p.N) - n0;
+    const DecodePlan ps = plan_decode(p.M, ng, p.K, p.r, p.w_dtype);
+    if (ps.kw != pg.kw || ps.ksy != pg.ksy || (p.r > 0 && ps.kst != pg.kst)) return false;
+    n0 += ng;
+  }
+  return true;
+}
+
 size_t decode_grouped_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int groups, int w_dtype) {
   return plan_decode(M, N, K, r, w_dtype, Pick::kAll, r * groups).total;
 }
@@ -1251,7 +1325,7 @@ hipError_t launch_decode(const LoraArgs& p) {
 
 bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
   if (f.fuse < 1 || f.fuse > 7 || ((f.fuse & kFuseAct) && (f.fuse & kFuseRes))) return false;
-  if (!decode_supported(p) || p.w_dtype != kBF16) return false;
+  if (p.M > kDecodeMaxM || !decode_supported(p) || p.w_dtype != kBF16) return false;
   const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kFused);
   if (!pl.ok || pl.kw != 8) return false;
   if (f.fuse & kFuseNorm) {
@@ -1281,7 +1355,7 @@ bool argmax_plan_ok(const DecodePlan& pl) {
 }  // namespace
 
 bool decode_argmax_supported(const LoraArgs& p) {
-  if (p.r != 0 || p.w_dtype != kBF16 || !decode_supported(p)) return false;
+  if (p.M > kDecodeMaxM || p.r != 0 || p.w_dtype != kBF16 || !decode_supported(p)) return false;
   return argmax_plan_ok(plan_decode(p.M, p.N, p.K, 0, kBF16, Pick::kFused));
 }
 

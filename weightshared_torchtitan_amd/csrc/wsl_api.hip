@@ -100,7 +100,7 @@ enum class Path { kNone, kPrefill, kDecode, kGeneric };
 
 Path choose_path(const wsl::LoraArgs& p) {
   if (p.M == 0) return Path::kNone;
-  if (p.M <= wsl::kDecodeMaxM && wsl::decode_supported(p)) return Path::kDecode;
+  if (p.M <= wsl::kDecodePlainMaxM && wsl::decode_supported(p)) return Path::kDecode;
   if (wsl::prefill_supported(p)) return Path::kPrefill;
   return Path::kGeneric;
 }
@@ -121,7 +121,8 @@ size_t layout_bytes(size_t data) { return wsl::kCounterBytes + 2 * align256(data
 size_t decode_data(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype, int groups = 1) {
   const size_t t = groups > 1 ? wsl::decode_grouped_workspace_bytes(M, N, K, r, groups, w_dtype)
                               : wsl::decode_workspace_bytes(M, N, K, r, w_dtype);
-  return t - wsl::kCounterBytes;  // plan offsets start after the counter prefix
+  // plan offsets start after the counter prefix; a shape no decode plan covers needs none
+  return t > wsl::kCounterBytes ? t - wsl::kCounterBytes : 0;
 }
 size_t generic_data(int64_t M, int64_t r) { return (size_t)(M * r * 2); }
 size_t prefill_data(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
@@ -134,7 +135,7 @@ size_t workspace_upper_bound(int64_t M, int64_t N, int64_t K, int64_t r, int w_d
   size_t b = generic_data(M, r);
   const size_t pf = prefill_data(M, N, K, r, w_dtype);
   if (pf > b) b = pf;
-  if (M >= 1 && M <= wsl::kDecodeMaxM) {
+  if (M >= 1 && M <= wsl::kDecodePlainMaxM) {
     const size_t d = decode_data(M, N, K, r, w_dtype);
     if (d > b) b = d;
   }
@@ -284,8 +285,9 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
       medium_agrees =
           medium_agrees && wsl::medium_splits(p.M, group_n[g], p.K, p.r, p.w_dtype, p.w != nullptr, false) == ms;
   }
+  // Likewise the decode path above 64 tokens, whose K splits depend on N.
   if ((path == Path::kPrefill && medium_agrees && wsl::prefill_groups_supported(p)) ||
-      (path == Path::kDecode && wsl::decode_groups_supported(p)))
+      (path == Path::kDecode && wsl::decode_groups_supported(p) && wsl::decode_groups_consistent(p)))
     return run_call(p, workspace, workspace_bytes);
   const int64_t wbytes = (p.w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;
   int64_t n0 = 0;
@@ -386,7 +388,7 @@ int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int
   rc = validate_sizes(M, N, K, r, w_dtype);
   if (rc != WSL_OK) return rc;
   size_t b = layout_bytes(prefill_data(M, N, K, r * n_groups, w_dtype));
-  if (M >= 1 && M <= wsl::kDecodeMaxM) {
+  if (M >= 1 && M <= wsl::kDecodePlainMaxM) {
     const size_t d = layout_bytes(decode_data(M, N, K, r, w_dtype, n_groups));
     if (d > b) b = d;
   }

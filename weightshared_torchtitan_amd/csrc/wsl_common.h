@@ -171,6 +171,8 @@ hipError_t launch_decode(const LoraArgs& p);
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool decode_supported(const LoraArgs& p);
 bool decode_groups_supported(const LoraArgs& p);
+// Whether a grouped decode launch sums each group's outputs as the group's single launch.
+bool decode_groups_consistent(const LoraArgs& p);
 size_t decode_grouped_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int groups, int w_dtype);
 
 // Decode-step fusions of the decode kernel (bit 0: RMSNorm prologue on x, bit 1: SwiGLU
@@ -195,8 +197,11 @@ hipError_t launch_factorized_embedding(const int64_t* ids, int64_t n_ids, const 
                                        int64_t ldp, int64_t hidden, void* out, int64_t ldo,
                                        hipStream_t stream);
 
-// Largest M routed to the decode-shaped (skinny) kernels.
+// Largest M routed to the decode-shaped (skinny) kernels: every form (fused, fp8 base, the
+// greedy head) up to kDecodeMaxM, the plain bf16 form up to kDecodePlainMaxM (eight token
+// blocks, four waves along K, x walked in passes).
 constexpr int64_t kDecodeMaxM = 64;
+constexpr int64_t kDecodePlainMaxM = 128;
 
 // Every workspace starts with this many bytes of counters (a launch counter and arrival
 // counters of the decode path). They must be zero when the workspace is first used;
