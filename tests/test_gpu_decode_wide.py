@@ -2,9 +2,10 @@
 four waves along K, x walked in pass slices of 512 or 1024 columns, the slices spread over
 the K splits that keep one wave of workgroups. Against the float64 oracle (1e-2), bitwise
 repeatable, with the T wait forced to its local fallback, beside the prefill path's medium
-form (WSL_DECODE_WIDE=off) on the same inputs, and as grouped launches: bit for bit the
-single launches (a grouped launch whose K splits would differ from a group's runs the
-groups one by one)."""
+form (WSL_DECODE_WIDE=off) on the same inputs, and as grouped launches. The K split count
+fills one wave of workgroups, so it depends on N: a grouped launch may sum a group's rows in
+another order than the group's single launch, and the two agree within the bar (below 65
+tokens they agree bit for bit)."""
 import numpy as np
 import pytest
 import torch
@@ -86,8 +87,8 @@ def test_wide_decode_t_fallback(gpu, monkeypatch):
 
 
 @pytest.mark.parametrize("M,K,group_n", [
-    (96, 2048, (6144, 6144)),        # gate|up: the groups split K as the grouped launch does
-    (96, 2048, (2048, 1024, 1024)),  # q|k|v: q alone splits K otherwise -> groups one by one
+    (96, 2048, (6144, 6144)),        # gate|up
+    (96, 2048, (2048, 1024, 1024)),  # q|k|v: q alone splits K in two, the grouped launch not
     (128, 6144, (2048, 2048)),
     (72, 1024, (3072, 3072, 1024)),
 ])
@@ -104,10 +105,12 @@ def test_wide_decode_grouped_matches_single(gpu, M, K, group_n, monkeypatch):
     Bs = [(torch.randn(n, r, generator=g) * 0.02).bfloat16().to(gpu) for n in group_n]
     y = ops.lora_linear_grouped_op(x, torch.cat(Ws), None, torch.cat(As), torch.cat(Bs), 2.0, list(group_n))
     n0 = 0
+    xn = x.float().cpu().numpy()
     for i, n in enumerate(group_n):
-        yi = wsl.lora_linear(x, Ws[i], As[i], Bs[i], 2.0)
-        assert torch.equal(y[:, n0:n0 + n], yi), i
+        yi = wsl.lora_linear(x, Ws[i], As[i], Bs[i], 2.0).float()
+        yg = y[:, n0:n0 + n].float()
+        assert ((yg - yi).abs().max() / yi.abs().max()).item() <= BF16_TOL, i
+        ref = O.lora_linear(xn, Ws[i].float().cpu().numpy(), As[i].float().cpu().numpy(),
+                            Bs[i].float().cpu().numpy(), 2.0)
+        assert O.max_rel_err(yg.cpu().numpy(), ref) <= BF16_TOL, i
         n0 += n
-    ref = O.lora_linear(x.float().cpu().numpy(), Ws[0].float().cpu().numpy(), As[0].float().cpu().numpy(),
-                        Bs[0].float().cpu().numpy(), 2.0)
-    assert O.max_rel_err(y[:, :group_n[0]].float().cpu().numpy(), ref) <= BF16_TOL

@@ -1,8 +1,9 @@
-"""The prefill path's medium-M split form (64 < M <= 160: split-K base product, rank
-pre-pass, combine kernel) against the float64 oracle, bar max|y - y_ref| / max|y_ref| <= 1e-2;
-grouped launches against the single calls bit for bit (the groups take one split count or go
-one by one); the shared-base form; and agreement with the decode path across the M = 64 / 65
-cut-over."""
+"""Medium M: 65-128 tokens run on the decode path's wide form and 129-160 on the prefill
+path's split form (split-K base product, rank pre-pass, combine kernel); each against the
+float64 oracle, bar max|y - y_ref| / max|y_ref| <= 1e-2. Grouped launches against the single
+calls: bit for bit on the split form (the groups take one split count or go one by one),
+within the bar on the decode path above 64 tokens (its K splits depend on N). The
+shared-base form, and agreement across the M = 64 / 65 cut-over."""
 import sys
 
 import pytest
@@ -76,7 +77,10 @@ def test_medium_m_grouped_matches_single(gpu, M, K, r, group_n):
     n0 = 0
     for i, n in enumerate(group_n):
         yi = wsl.lora_linear(x, Ws[i], As[i], Bs[i], 2.0)
-        assert torch.equal(y[:, n0:n0 + n], yi), i
+        if M > 128:  # the split form
+            assert torch.equal(y[:, n0:n0 + n], yi), i
+        else:
+            assert ((y[:, n0:n0 + n].float() - yi.float()).abs().max() / yi.float().abs().max()).item() <= BF16_TOL, i
         n0 += n
     ref = O.lora_linear(x.float().cpu().numpy(), Ws[0].float().cpu().numpy(), As[0].float().cpu().numpy(),
                         Bs[0].float().cpu().numpy(), 2.0)

@@ -1063,8 +1063,10 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
   // 32 rows per workgroup, or 64 where 32 would take more than one wave of workgroups; the
   // slices are then spread over the largest number of K splits that keeps the grid within
   // one wave of workgroups (more workgroups stream faster; passes spare the workgroups a
-  // split hand-off), the rest walked as passes. Every choice depends on M, K and the grid,
-  // and a grouped launch fills its groups' rows as the single launches do.
+  // split hand-off), the rest walked as passes. The split count depends on N through the
+  // grid, so above 64 tokens a grouped launch may sum a group's rows in another order than
+  // the group's single launch (within the bar; below 65 tokens every choice that fixes the
+  // order depends on M and K only, and grouped launches match single ones bit for bit).
   if (pick == Pick::kAll && pl.mb > 4) {
     pl.ok = false;
     const int64_t kcp = (M * 1024 * 2 <= XS_MAX && K % 1024 == 0) ? 1024 : 512;
@@ -1292,22 +1294,6 @@ bool decode_groups_supported(const LoraArgs& p) {
   if (!pl.ok) return false;
   for (int g = 0; g + 1 < p.groups; ++g)
     if (p.gend[g] % pl.rows != 0) return false;
-  return true;
-}
-
-// Whether a grouped launch sums every output in the order its group's single launch does:
-// a row's order depends on the waves along K and the K splits of W and of T (the passes
-// and the rows per workgroup do not change it). The plans below 65 tokens never depend on
-// N; above, the split count fills one wave of workgroups and does.
-bool decode_groups_consistent(const LoraArgs& p) {
-  const DecodePlan pg = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kAll, p.r * p.groups);
-  int64_t n0 = 0;
-  for (int g = 0; g < p.groups; ++g) {
-    const int64_t ng = (g + 1 < p.groups ? p.gend[g] : p.N) - n0;
-    const DecodePlan ps = plan_decode(p.M, ng, p.K, p.r, p.w_dtype);
-    if (ps.kw != pg.kw || ps.ksy != pg.ksy || (p.r > 0 && ps.kst != pg.kst)) return false;
-    n0 += ng;
-  }
   return true;
 }
 

@@ -285,9 +285,8 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
       medium_agrees =
           medium_agrees && wsl::medium_splits(p.M, group_n[g], p.K, p.r, p.w_dtype, p.w != nullptr, false) == ms;
   }
-  // Likewise the decode path above 64 tokens, whose K splits depend on N.
   if ((path == Path::kPrefill && medium_agrees && wsl::prefill_groups_supported(p)) ||
-      (path == Path::kDecode && wsl::decode_groups_supported(p) && wsl::decode_groups_consistent(p)))
+      (path == Path::kDecode && wsl::decode_groups_supported(p)))
     return run_call(p, workspace, workspace_bytes);
   const int64_t wbytes = (p.w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;
   int64_t n0 = 0;

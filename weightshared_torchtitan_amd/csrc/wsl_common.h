@@ -171,8 +171,6 @@ hipError_t launch_decode(const LoraArgs& p);
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool decode_supported(const LoraArgs& p);
 bool decode_groups_supported(const LoraArgs& p);
-// Whether a grouped decode launch sums each group's outputs as the group's single launch.
-bool decode_groups_consistent(const LoraArgs& p);
 size_t decode_grouped_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int groups, int w_dtype);
 
 // Decode-step fusions of the decode kernel (bit 0: RMSNorm prologue on x, bit 1: SwiGLU
