@@ -413,3 +413,33 @@ def test_tied_head_argmax_in_graph_replays(gpu):
         torch.cuda.synchronize()
         want = torch.argmax(ops.lora_linear(z, E, None, None, 0.0), dim=-1)
         assert torch.equal(out, want), f"replay {i}"
+
+
+@pytest.mark.parametrize("M,N,K,r", [(8, 1024, 2048, 32), (8, 1024, 3072, 32), (5, 1000, 1024, 24), (64, 512, 1024, 8)])
+def test_fused_residual_in_place(gpu, M, N, K, r):
+    """The residual epilogue with y aliasing the residual (the C ABI allows it): bit-equal
+    to the out-of-place launch, since every workgroup reads the residual words it later
+    overwrites before any of them is written."""
+    import ctypes
+    from weightshared_torchtitan_amd import ops, _native as N_
+    _say(f"[fused residual in place] M={M} N={N} K={K} r={r}")
+    g = torch.Generator(device="cuda").manual_seed(M + N + K + r)
+    x = torch.randn(M, K, device=gpu, generator=g).bfloat16()
+    W = (torch.randn(N, K, device=gpu, generator=g) * K ** -0.5).bfloat16()
+    A = (torch.randn(r, K, device=gpu, generator=g) * K ** -0.5).bfloat16()
+    B = (torch.randn(N, r, device=gpu, generator=g) * 0.3).bfloat16()
+    res = torch.randn(M, N, device=gpu, generator=g).bfloat16()
+    want = ops.lora_linear_fused_op(x, None, 1e-6, W, A, B, 2.0, res, N_.WSL_FUSE_RESIDUAL)
+    h = res.clone()
+    stream = ops._stream(h.device)
+    ws = ops.workspace(h.device, stream, N_.workspace_bytes(M, N, K, r, N_.WSL_DTYPE_BF16))
+    for _ in range(2):  # the second launch adds the delta to the first one's output
+        h_prev = h.clone()
+        rc = N_.lib().wsl_lora_linear_fused_fwd(
+            x.data_ptr(), K, None, 1e-6, W.data_ptr(), K, A.data_ptr(), K, B.data_ptr(), r, 2.0,
+            h.data_ptr(), N, h.data_ptr(), N, M, N, K, r, N_.WSL_FUSE_RESIDUAL, ws.data_ptr(), ws.numel(), stream)
+        N_.check(rc, "wsl_lora_linear_fused_fwd")
+        ref = ops.lora_linear_fused_op(x, None, 1e-6, W, A, B, 2.0, h_prev, N_.WSL_FUSE_RESIDUAL)
+        torch.cuda.synchronize()
+        assert torch.equal(h, ref)
+    assert torch.equal(ops.lora_linear_fused_op(x, None, 1e-6, W, A, B, 2.0, res, N_.WSL_FUSE_RESIDUAL), want)

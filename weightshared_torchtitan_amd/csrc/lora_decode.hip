@@ -774,6 +774,22 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     char* bl = smem + (xs_bytes > post ? xs_bytes : post);
     float* sums = reinterpret_cast<float*>(smem + RED);
     uint16_t* tl = reinterpret_cast<uint16_t*>(smem + RED + ROWS * MC * 4);
+    const int l16 = lane & 15, grp = lane >> 4;
+    // Residual epilogue: the residual words of this wave's output blocks are loaded here, so
+    // their round trip overlaps the W stream instead of following the T gather. Each element
+    // is read and later written by this workgroup only, so y may alias res.
+    constexpr int EPB = ((ROWS / 16) * MB + NWV - 1) / NWV;  // epilogue blocks per wave
+    uint2 rpre[RES ? EPB : 1];
+    if constexpr (RES) {
+#pragma unroll
+      for (int t = 0; t < EPB; ++t) {
+        const int blk = wave + t * NWV, i = blk / MB, m = blk % MB * 16 + l16;
+        const int n0 = row0 + i * 16 + grp * 4;
+        rpre[t] = make_uint2(0u, 0u);
+        if (blk < (ROWS / 16) * MB && m < p.M && n0 + 3 < p.N)
+          rpre[t] = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n0);
+      }
+    }
     if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
@@ -799,9 +815,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
         gather_t<MC, NORM>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
       }
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
-      const int l16 = lane & 15, grp = lane >> 4;
       const int tls = p.r32 + 8;
-      for (int blk = wave; blk < (ROWS / 16) * MB; blk += NWV) {
+#pragma unroll
+      for (int t = 0; t < EPB; ++t) {
+        const int blk = wave + t * NWV;
+        if (blk >= (ROWS / 16) * MB) break;
         const int i = blk / MB, mb = blk % MB;
         f32x4_t d = {0.f, 0.f, 0.f, 0.f};
         for (int j0 = 0; j0 < p.r; j0 += 32) {
@@ -839,7 +857,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
           if constexpr (RES) {  // y = bf16(res + bf16(o)); res may be y itself (read first)
             const uint16_t* rr = p.res + (int64_t)m * p.ldr;
             if (n0 + 3 < p.N) {
-              const uint2 rv = *reinterpret_cast<const uint2*>(rr + n0);
+              const uint2 rv = rpre[t];
               o[0] = bf16_bits_to_f32(rv.x & 0xffffu) + bf16_round(o[0]);
               o[1] = bf16_bits_to_f32(rv.x >> 16) + bf16_round(o[1]);
               o[2] = bf16_bits_to_f32(rv.y & 0xffffu) + bf16_round(o[2]);
