@@ -347,23 +347,26 @@ def bench_c3(dev, steps, warmup):
 
 
 def bench_medium(dev, steps, warmup):
-    """Medium M (above the decode path's fused forms and up to a few hundred tokens) at the
+    """Medium M (above the decode path's fused forms, up to a thousand tokens) at the
     Qwen3-1.7B projection shapes, r = 64, cold weights (6 rotating copies), 28 layers per
     graph, grouped q|k|v and gate|up, each way the library can run them on the same inputs:
-    the decode path (the default up to 128 tokens), the prefill path's split-K form
-    (WSL_DECODE_WIDE=off; the default for 129-160 tokens) and its unsplit tiles (also
-    WSL_PREFILL_MEDIUM=off)."""
+    the decode path's wide form (the default up to 72 tokens), the prefill path's in-launch
+    split-K form (WSL_DECODE_WIDE=off below 129 tokens; the default above), its earlier
+    medium split form (also WSL_PREFILL_SPLIT=off; up to 160 tokens) and its unsplit tiles
+    (also WSL_PREFILL_MEDIUM=off)."""
     out = {}
-    keys = ("WSL_DECODE_WIDE", "WSL_PREFILL_MEDIUM")
+    keys = ("WSL_DECODE_WIDE", "WSL_PREFILL_MEDIUM", "WSL_PREFILL_SPLIT")
     saved = {k: os.environ.get(k) for k in keys}
-    ways = (("decode", {}), ("split", {"WSL_DECODE_WIDE": "off"}),
-            ("unsplit", {"WSL_DECODE_WIDE": "off", "WSL_PREFILL_MEDIUM": "off"}))
+    ways = (("decode", {}),
+            ("split_k", {"WSL_DECODE_WIDE": "off"}),
+            ("medium", {"WSL_DECODE_WIDE": "off", "WSL_PREFILL_SPLIT": "off"}),
+            ("unsplit", {"WSL_DECODE_WIDE": "off", "WSL_PREFILL_SPLIT": "off", "WSL_PREFILL_MEDIUM": "off"}))
     try:
-        for M in (64, 65, 96, 128, 160, 192, 256):
+        for M in (64, 65, 72, 96, 128, 160, 192, 256, 512, 1024):
             row = {}
             for label, env in ways:
-                if (label == "decode" and M > 128) or (label != "decode" and M <= 64):
-                    continue  # decode runs up to 128 tokens; the prefill forms above 64
+                if (label == "decode" and M > 72) or (label != "decode" and M <= 64) or (label == "medium" and M > 160):
+                    continue  # decode runs up to 72 tokens, the medium split form to 160; the prefill forms above 64
                 for k in keys:
                     os.environ.pop(k, None)
                 os.environ.update(env)

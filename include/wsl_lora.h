@@ -141,10 +141,11 @@ int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx,
  * gate/up (qwen3/model/model.py:250-251). The groups run as one launch where every group
  * boundary falls on the launch's work grid: on the prefill path, whole output tiles
  * (multiples of 128; of 256 for ranks 33-64), each tile taking its group's rank block; on
- * the decode path (M <= 64; plain bf16 up to 128), whole row groups of W (multiples of 64
+ * the decode path (M <= 64; plain bf16 up to 72), whole row groups of W (multiples of 64
  * suffice), the T work covering all groups' A rows. Otherwise the groups run as consecutive
- * launches on `stream`. Results are those of the per-group calls, bit for bit, except on
- * the decode path between 65 and 128 tokens, whose K split count depends on N: there the
+ * launches on `stream`. Results are those of the per-group calls, bit for bit, except where
+ * a K split count depends on N (the decode path between 65 and 72 tokens; the prefill
+ * path's in-launch split-K form, taken where 128 x 128 tiles leave CUs idle): there the
  * groups' outputs agree with the per-group calls within the forward's bar.
  */
 #define WSL_MAX_GROUPS 4

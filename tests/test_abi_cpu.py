@@ -460,3 +460,25 @@ def test_workspace_bytes_of_wide_decode_shapes(M, K):
         grouped = N.grouped_workspace_bytes(M, K, r, (1024, 512, 512), N.WSL_DTYPE_BF16)
         for b in (single, grouped):
             assert 0 < b < (1 << 32)
+
+
+@pytest.mark.parametrize("M,Nn,K,r,splits", [
+    (256, 2048, 2048, 64, 4),   # 32 tiles of 128 x 128, 32 K tiles: four splits of eight
+    (256, 2048, 6144, 0, 8),    # 96 K tiles: eight splits fill 256 CUs
+    (129, 1024, 1024, 16, 2),   # 16 K tiles: two splits of eight
+    (160, 12288, 2048, 64, 0),  # 192 tiles: no split
+])
+def test_workspace_bytes_of_split_k_shapes(M, Nn, K, r, splits):
+    """The in-launch split-K form's records (8 waves x 64 lanes x 24 words of 8 bytes per tile
+    and split, 16 words without T) fit in the prefill half of the workspace the size query
+    asks for, single and grouped (the grouped query cannot see the per-group rank, so it
+    counts the T words)."""
+    tiles = ((M + 127) // 128) * ((Nn + 127) // 128)
+    words = 24 if r else 16
+    need = tiles * splits * 8 * 64 * words * 8
+    half = lambda b: ((b - 65536) // 2) & ~255
+    single = N.workspace_bytes(M, Nn, K, r, N.WSL_DTYPE_BF16)
+    assert half(single) >= need
+    if r:
+        grouped = N.grouped_workspace_bytes(M, K, r, (Nn // 2, Nn // 4, Nn // 4), N.WSL_DTYPE_BF16)
+        assert half(grouped) >= tiles * splits * 8 * 64 * 24 * 8

@@ -1,8 +1,8 @@
-"""The decode path from 65 to 128 tokens (plain bf16 launches): five to eight token blocks,
-four waves along K, x walked in pass slices of 512 or 1024 columns, the slices spread over
-the K splits that keep one wave of workgroups. Against the float64 oracle (1e-2), bitwise
-repeatable, with the T wait forced to its local fallback, beside the prefill path's medium
-form (WSL_DECODE_WIDE=off) on the same inputs, and as grouped launches. The K split count
+"""The decode path from 65 to 72 tokens (plain bf16 launches): five token blocks, four
+waves along K, x walked in pass slices of 512 or 1024 columns, the slices spread over the K
+splits that keep one wave of workgroups. Against the float64 oracle (1e-2), bitwise
+repeatable, with the T wait forced to its local fallback, beside the prefill path
+(WSL_DECODE_WIDE=off) on the same inputs, and as grouped launches. The K split count
 fills one wave of workgroups, so it depends on N: a grouped launch may sum a group's rows in
 another order than the group's single launch, and the two agree within the bar (below 65
 tokens they agree bit for bit)."""
@@ -38,13 +38,12 @@ CASES = [
     # M, N, K, r
     (65, 2048, 2048, 64),    # 1024-column passes (x of 65 rows fits), o at 1.7B
     (72, 6144, 2048, 64),    # 512-column passes, 64 rows per workgroup
-    (80, 2048, 6144, 64),    # twelve slices over three K splits (down at 1.7B)
-    (96, 1000, 2048, 24),    # N tail, partial rank group
-    (112, 4096, 1024, 16),
-    (128, 2048, 2048, 64),   # eight token blocks
-    (128, 12288, 2048, 64),  # gate|up at 1.7B, one wave of workgroups
-    (100, 3072, 1024, 0),    # plain linear
-    (127, 640, 4096, 8),     # M one short of 128
+    (72, 2048, 6144, 64),    # twelve slices over K splits and passes (down at 1.7B)
+    (70, 1000, 2048, 24),    # N tail, partial rank group
+    (68, 4096, 1024, 16),
+    (72, 12288, 2048, 64),   # gate|up at 1.7B, one wave of workgroups
+    (66, 3072, 1024, 0),     # plain linear
+    (71, 640, 4096, 8),
 ]
 
 
@@ -74,7 +73,7 @@ def test_wide_decode_t_fallback(gpu, monkeypatch):
     """T wait bound forced to zero from the host: the W workgroups compute T themselves."""
     import weightshared_torchtitan_amd as wsl
     monkeypatch.delenv("WSL_DECODE_WIDE", raising=False)
-    M, N, K, r = 96, 2048, 6144, 64
+    M, N, K, r = 72, 2048, 6144, 64
     _say(f"[decode wide T fallback] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=53)
     d = lambda t: t.to(gpu)
@@ -87,10 +86,10 @@ def test_wide_decode_t_fallback(gpu, monkeypatch):
 
 
 @pytest.mark.parametrize("M,K,group_n", [
-    (96, 2048, (6144, 6144)),        # gate|up
-    (96, 2048, (2048, 1024, 1024)),  # q|k|v: q alone splits K in two, the grouped launch not
-    (128, 6144, (2048, 2048)),
-    (72, 1024, (3072, 3072, 1024)),
+    (72, 2048, (6144, 6144)),        # gate|up
+    (70, 2048, (2048, 1024, 1024)),  # q|k|v
+    (72, 6144, (2048, 2048)),
+    (65, 1024, (3072, 3072, 1024)),
 ])
 def test_wide_decode_grouped_matches_single(gpu, M, K, group_n, monkeypatch):
     import weightshared_torchtitan_amd as wsl

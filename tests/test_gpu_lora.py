@@ -393,7 +393,7 @@ def test_decode_counters_return_to_zero_and_deterministic(gpu):
 
 
 @pytest.mark.parametrize("M,N,K,r", [(4, 1024, 2048, 32), (64, 2048, 6144, 64), (64, 6144, 2048, 64),
-                                     (96, 2048, 6144, 64)])
+                                     (72, 2048, 6144, 64)])
 def test_decode_in_graph_replays_match_eager(gpu, M, N, K, r):
     """Captured decode calls replay correctly several times (counters reset per replay)."""
     import weightshared_torchtitan_amd as wsl

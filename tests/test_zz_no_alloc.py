@@ -68,7 +68,8 @@ def _noalloc(dev, x, W, A, B, s):
 CASES = [
     # (first shape, second smaller shape): M, N, K, r
     ((64, 1024, 4096, 64), (8, 1024, 4096, 64)),      # decode path, K split (partials + T words)
-    ((96, 2048, 6144, 64), (64, 6144, 2048, 64)),     # wide decode form (splits of passes), then two passes
+    ((72, 2048, 6144, 64), (64, 6144, 2048, 64)),     # wide decode form (splits of passes), then two passes
+    ((256, 2048, 2048, 64), (160, 1024, 6144, 32)),   # prefill in-launch split-K (arrival counters in the scratch)
     ((4, 2048, 2048, 32), (1, 2048, 2048, 32)),       # decode path, one slice
     ((1024, 768, 1024, 128), (512, 768, 1024, 128)),  # prefill rank pre-pass with split partials
     ((300, 520, 192, 24), (100, 520, 192, 24)),       # prefill, in-kernel rank

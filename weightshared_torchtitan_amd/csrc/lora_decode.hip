@@ -1075,9 +1075,10 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
       }
     }
   }
-  // Five to eight token blocks (65 <= M <= 128, plain bf16 launches): x is walked in pass
-  // slices of 1024 columns, or 512 where 1024 do not fit the LDS (128 KB at M = 128): eight
-  // or four wave steps, so four waves run along K and two row blocks share a workgroup.
+  // Five token blocks and more (65 <= M <= kDecodePlainMaxM, plain bf16 launches; kernels
+  // are built for five): x is walked in pass slices of 1024 columns, or 512 where 1024 do
+  // not fit the LDS: eight or four wave steps, so four waves run along K and two row
+  // blocks share a workgroup.
   // 32 rows per workgroup, or 64 where 32 would take more than one wave of workgroups; the
   // slices are then spread over the largest number of K splits that keeps the grid within
   // one wave of workgroups (more workgroups stream faster; passes spare the workgroups a
@@ -1176,11 +1177,8 @@ hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t sme
       if (mb == 3) return launch_one<WDT, 1, 3, KW>(a, grid, smem, st);
       if (mb == 4) return launch_one<WDT, 1, 4, KW>(a, grid, smem, st);
     }
-    if constexpr (KW == 4 && WDT == kBF16) {  // 65 <= M <= 128
+    if constexpr (KW == 4 && WDT == kBF16) {  // 65 <= M <= kDecodePlainMaxM
       if (mb == 5) return launch_one<WDT, 1, 5, KW>(a, grid, smem, st);
-      if (mb == 6) return launch_one<WDT, 1, 6, KW>(a, grid, smem, st);
-      if (mb == 7) return launch_one<WDT, 1, 7, KW>(a, grid, smem, st);
-      if (mb == 8) return launch_one<WDT, 1, 8, KW>(a, grid, smem, st);
     }
     return hipErrorInvalidValue;
   }
@@ -1195,11 +1193,8 @@ hipError_t dispatch_kw(const DecodeArgs& a, int mb, int nr, int grid, size_t sme
     }
     if (mb == 3) return launch_one<WDT, 2, 3, KW>(a, grid, smem, st);
     if (mb == 4) return launch_one<WDT, 2, 4, KW>(a, grid, smem, st);
-    if constexpr (KW == 4 && WDT == kBF16) {  // 65 <= M <= 128
+    if constexpr (KW == 4 && WDT == kBF16) {  // 65 <= M <= kDecodePlainMaxM
       if (mb == 5) return launch_one<WDT, 2, 5, KW>(a, grid, smem, st);
-      if (mb == 6) return launch_one<WDT, 2, 6, KW>(a, grid, smem, st);
-      if (mb == 7) return launch_one<WDT, 2, 7, KW>(a, grid, smem, st);
-      if (mb == 8) return launch_one<WDT, 2, 8, KW>(a, grid, smem, st);
     }
     return hipErrorInvalidValue;
   }
@@ -1241,8 +1236,8 @@ bool decode_supported(const LoraArgs& p) {
   if (p.M < 1 || p.M > kDecodePlainMaxM) return false;
   if (p.M > kDecodeMaxM) {
     if (p.w_dtype != kBF16) return false;  // fp8 base above 64 tokens: the prefill path
-    // WSL_DECODE_WIDE=off keeps 65-128 tokens on the prefill path's medium form (read per
-    // call, for side-by-side timing)
+    // WSL_DECODE_WIDE=off keeps 65-72 tokens on the prefill path (read per call, for
+    // side-by-side timing)
     const char* e = std::getenv("WSL_DECODE_WIDE");
     if (e != nullptr && std::strcmp(e, "off") == 0) return false;
   }

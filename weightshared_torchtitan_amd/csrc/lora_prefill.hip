@@ -43,6 +43,7 @@
 //
 // Reference arithmetic being fused: torchtitan/models/llama3/model/model.py:189-192
 // (LoRAModule.forward), :392-398 (base projection + broadcast_add with g = 1).
+#include <algorithm>
 #include <climits>
 #include <cstdlib>
 #include <cstring>
@@ -62,9 +63,10 @@ constexpr int GROUP_M = 4;  // row tiles per XCD group (4 against 8 and 16: +0.9
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int BM_, int BN_, int WNW_, int NW_>
+template <int BM_, int BN_, int WNW_, int NW_, int NS_ = 2>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_;
+  static constexpr int NS = NS_;                      // LDS ring buffers (K tiles in flight + 1)
   static constexpr int NW = NW_, NT = NW_ * 64;     // waves, threads
   static constexpr int WNW = WNW_, WMW = NW_ / WNW_;  // waves along n and m
   static constexpr int TN = BN / WNW, TM = BM / WMW;  // wave tile
@@ -125,6 +127,12 @@ __device__ __forceinline__ void direct_fill(char* lds_tile, int grp, const void*
 
 // s_waitcnt vmcnt(0) with expcnt/lgkmcnt left unconstrained (gfx9 encoding).
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+// s_waitcnt vmcnt(N), N < 64
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
 
 // Workgroup barrier of the K loop. Its vmcnt wait is explicit, so it must not carry the
 // release fence of __syncthreads(), which would also wait for the fill in flight.
@@ -141,6 +149,14 @@ __device__ __forceinline__ void ring_barrier() {
 // range [blockIdx.y * K, (blockIdx.y + 1) * K) of x and W and writes its fp32 partial
 // product to slice blockIdx.y of y (viewed as fp32 [gridDim.y][M][ldy]).
 //
+// RED: split-K fused LoRA linear with the reduction in the launch. Workgroup row
+// blockIdx.y takes the K range [blockIdx.y * K, (blockIdx.y + 1) * K) of x, W and A (K is
+// one split's length); every split writes its fp32 base and T partials to red_part in its
+// accumulators' own lane order, and the split that arrives last at the tile's counter
+// (red_cnt[blockIdx.x], left at zero again) sums all of them in split order and finishes
+// the tile (T, the up-projection, the store) as an unsplit launch would. The sum does not
+// depend on which split arrives last, so the result is repeatable bit for bit.
+//
 // TN: plain GEMM over operands stored with the reduction as rows ("token-major"): x'[m][k] is
 // x[k * ldx + m] and W'[n][k] is w[k * ldw + n], as the weight gradients' dY and x are (a
 // reduction over the tokens). The tiles go into LDS as they lie, [64 k][BM or BN columns]
@@ -148,7 +164,8 @@ __device__ __forceinline__ void ring_barrier() {
 // two transposing LDS reads (lds_read_tr8). K rows from `grows` (the token count, from this
 // split's start) on are read clamped and zeroed in the x' tile after they land. M and N are
 // multiples of 8.
-template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false>
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
+          bool RED = false>
 __global__ void __launch_bounds__(C::NT, 1)
 prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const int64_t* __restrict__ gidx, int64_t grows,
@@ -158,7 +175,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const uint16_t* __restrict__ bm, int64_t ldb, float s, float yscale,
                uint16_t* __restrict__ y, int64_t ldy,
                int M, int N, int K, int r, int tiles_m, int tiles_n,
-               int ge0, int ge1, int ge2, int64_t a_gstride, int t_gstride, RowMap wmap) {
+               int ge0, int ge1, int ge2, int64_t a_gstride, int t_gstride, RowMap wmap,
+               uint64_t* __restrict__ red_part, unsigned* __restrict__ red_cnt) {
   constexpr bool W8 = HAS_W && WDT == kFP8;
   constexpr bool WDIRECT = HAS_W && WDT == kBF16;
   constexpr bool LORA = RB > 0 || EXT_T;
@@ -166,13 +184,21 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   constexpr int AB = RB * 32 * ROWB;         // rank-A slice of a K tile
   constexpr int STAGE = C::XB + C::WB + AB;  // one of the two ring buffers
   constexpr int OS = C::BN * 2 + 16;          // LDS row stride of the staged output tile
-  constexpr int LDS_BYTES = (2 * STAGE > C::BM * OS) ? 2 * STAGE : C::BM * OS;
+  constexpr int LDS_BYTES = (C::NS * STAGE > C::BM * OS) ? C::NS * STAGE : C::BM * OS;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert(C::BM * ROWB <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   static_assert(!SPLIT || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "split-K is a plain bf16 GEMM");
   static_assert(!TN || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "token-major operands: plain bf16 GEMM");
+  static_assert(!RED || (WDT == kBF16 && HAS_W && !EXT_T && !GATHER && !SPLIT && !TN), "in-launch split-K: bf16 W");
+  static_assert(C::NS == 2 || (!W8 && !TN && !GATHER), "deep ring: bf16 W and x as they lie");
   int64_t tok_rem = grows;  // TN: K rows from this workgroup's first one to the end (>= 1)
+  if constexpr (RED) {
+    const int64_t kofs = (int64_t)blockIdx.y * K;
+    x += kofs;
+    w = reinterpret_cast<const uint16_t*>(w) + kofs;
+    if constexpr (RB > 0) a += kofs;
+  }
   if constexpr (SPLIT) {
     const int64_t kofs = (int64_t)blockIdx.y * K;
     if constexpr (TN) {
@@ -316,11 +342,16 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   };
   // TN: K rows past the token count (clamped reads) are zeroed in the x' tile once it has
-  // landed, so they add nothing whatever the W' tile holds there
+  // landed, so they add nothing whatever the W' tile holds there. A thread zeroes chunks
+  // that other waves' fills write, and each wave has only waited for its own fills: the
+  // barrier first lets every fill land, or a late fill would overwrite the zeros with the
+  // clamped row (the weight gradients of a partial token tile then came out wrong now and
+  // then).
   auto tn_zero = [&](int stage, int k0) {
     if constexpr (TN) {
       const int64_t valid = tok_rem - k0;
-      if (valid < 64) {
+      if (valid < 64) {  // the same for every wave
+        ring_barrier();
         char* sx = lds + stage * STAGE;
         const int v0 = valid > 0 ? (int)valid : 0;
         constexpr int CPR = C::BM / 8;
@@ -464,10 +495,10 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   };
 
   const int nk = K / BK;
-  // The last K tile runs from buffer (nk-1)&1; the B slice of the LoRA phase is filled
-  // into the other one while it does.
-  char* lora_t = lds + ((nk - 1) & 1) * STAGE;
-  char* lora_b = lds + (nk & 1) * STAGE;
+  // The last K tile runs from buffer (nk-1) % NS; the B slice of the LoRA phase is filled
+  // into buffer nk % NS, which no later tile uses, while the last tiles run.
+  char* lora_t = lds + ((nk - 1) % C::NS) * STAGE;
+  char* lora_b = lds + (nk % C::NS) * STAGE;
 
   constexpr bool RUN_K = HAS_W || RB > 0;
   // The K loop, instantiated with and without this wave's T work (`do_t`), so the k steps
@@ -524,17 +555,161 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
     __syncthreads();  // every wave is done with the ring before the LDS is reused
   };
+  // The deep ring (NS > 2 buffers, the 128 x 128 tile at one workgroup per CU): NS K tiles
+  // are in flight from the start, and the fill of tile kt+NS goes into tile kt's buffer
+  // once every wave has read it (the barrier in tile kt). Each wait leaves the fills of the
+  // NS-2 younger tiles in flight. With a workgroup alone on its CU, two buffers left every
+  // K tile waiting one fill's latency (about 1.2 us per 128 x 128 x 64 tile at M = 256).
+  auto run_k_deep = [&](auto do_t) {
+    constexpr int NS = C::NS;
+    constexpr int PT = C::NXI + (WDIRECT ? C::NWI : 0);  // fills per K tile of every wave (waves < NAI add one)
+    const int pre = nk < NS ? nk : NS;
+    for (int q = 0; q < pre; ++q) issue(q, q * BK);
+    if constexpr (LORA) {
+      if (nk < NS) issue_b(lora_b, 0);  // buffer nk is never filled with a K tile
+    }
+    if (nk >= NS) wait_vm<(NS - 1) * PT>();  // tile 0 has landed
+    else wait_vm0();
+    ring_barrier();
+    Frags cur;
+    frag_load(do_t, 0, 0, cur);
+    int buf = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int nbuf = buf + 1 == NS ? 0 : buf + 1;
+#pragma unroll
+      for (int kk = 0; kk < KK - 1; ++kk) {
+        Frags nxt;
+        frag_load(do_t, buf, kk + 1, nxt);
+        frag_mma(do_t, cur);
+        interleave(do_t);
+        cur = nxt;
+      }
+      if (kt + 1 < nk) {
+        if (kt + NS - 1 < nk) wait_vm<(NS - 2) * PT>();  // tile kt+1 has landed
+        else wait_vm0();
+        ring_barrier();  // all fragments of tile kt are read; tile kt+1 visible
+      }
+      Frags nxt;
+      frag_load(do_t, nbuf, 0, nxt);
+      frag_mma(do_t, cur);
+      interleave(do_t);
+      cur = nxt;
+      if (kt + NS < nk) {
+        issue(buf, (kt + NS) * BK);
+      } else if constexpr (LORA) {
+        if (kt + NS == nk) issue_b(lora_b, 0);  // buffer `buf` is lora_b
+      }
+      buf = nbuf;
+    }
+    __syncthreads();
+  };
+  auto run = [&](auto do_t) {
+    if constexpr (C::NS == 2) run_k(do_t);
+    else run_k_deep(do_t);
+  };
   if constexpr (RUN_K) {
     if constexpr (RB == 0) {
-      run_k(std::false_type{});
+      run(std::false_type{});
     } else if constexpr (ALL_T) {
-      run_k(std::true_type{});
+      run(std::true_type{});
     } else {
-      if (t_wave) run_k(std::true_type{});
-      else run_k(std::false_type{});
+      if (t_wave) run(std::true_type{});
+      else run(std::false_type{});
     }
   } else if constexpr (LORA) {
     issue_b(lora_b, 0);
+  }
+
+  if constexpr (RED) {
+    // This split's partials: lane-major 8-byte words (two accumulators each), the base
+    // block first, then the T block of a T wave; agent-scope stores, so the reducing
+    // workgroup (on any XCD) reads them from memory rather than from a stale L2 line.
+    constexpr int EB = C::NI * C::MJ * 8;
+    constexpr int ET = RB > 0 ? TPW * 8 : 0;
+    constexpr int EW = EB + ET;
+    const int S = (int)gridDim.y;
+    const int64_t first = (int64_t)blockIdx.x * S;  // the tile's split 0 record
+    auto rec = [&](int q) { return red_part + ((first + q) * C::NW + wave) * (int64_t)(EW * 64) + lane; };
+    auto pk = [](float lo, float hi) {
+      return (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+    };
+    {
+      uint64_t* dst = rec(blockIdx.y);
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::MJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            __hip_atomic_store(dst + ((i * C::MJ + j) * 8 + v) * 64, pk(acc[i][j][2 * v], acc[i][j][2 * v + 1]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (RB > 0) {
+        if (t_wave) {
+#pragma unroll
+          for (int q = 0; q < TPW; ++q)
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+              __hip_atomic_store(dst + (EB + q * 8 + v) * 64, pk(acct[q][2 * v], acct[q][2 * v + 1]),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    // the flag goes in the W area of the buffer the last K tile ran from (idle now; T is
+    // parked below its first BM rows, and a separate __shared__ word would take the
+    // 128 x 128 tile with two rank blocks past half the LDS, one workgroup per CU)
+    volatile int* red_last = reinterpret_cast<volatile int*>(lora_t + C::XB);
+    wait_vm0();  // the records are out before the arrival
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned old = __hip_atomic_fetch_add(red_cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == (unsigned)(S - 1);
+      if (last) __hip_atomic_store(red_cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *red_last = last ? 1 : 0;
+    }
+    __syncthreads();
+    if (*red_last == 0) return;
+    // the last split: every record, in split order (this one's own included), one split's
+    // words in flight at a time
+    for (int q = 0; q < S; ++q) {
+      const uint64_t* src = rec(q);
+      uint64_t wb[EB];
+#pragma unroll
+      for (int e = 0; e < EB; ++e)
+        wb[e] = __hip_atomic_load(const_cast<uint64_t*>(src + e * 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint64_t wt[ET > 0 ? ET : 1];
+      if constexpr (RB > 0) {
+        if (t_wave) {
+#pragma unroll
+          for (int e = 0; e < ET; ++e)
+            wt[e] = __hip_atomic_load(const_cast<uint64_t*>(src + (EB + e) * 64), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::MJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) {
+            const uint64_t u = wb[(i * C::MJ + j) * 8 + v];
+            const float lo = __uint_as_float((uint32_t)u), hi = __uint_as_float((uint32_t)(u >> 32));
+            acc[i][j][2 * v] = q == 0 ? lo : acc[i][j][2 * v] + lo;
+            acc[i][j][2 * v + 1] = q == 0 ? hi : acc[i][j][2 * v + 1] + hi;
+          }
+      if constexpr (RB > 0) {
+        if (t_wave) {
+#pragma unroll
+          for (int qq = 0; qq < TPW; ++qq)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+              const uint64_t u = wt[qq * 8 + v];
+              const float lo = __uint_as_float((uint32_t)u), hi = __uint_as_float((uint32_t)(u >> 32));
+              acct[qq][2 * v] = q == 0 ? lo : acct[qq][2 * v] + lo;
+              acct[qq][2 * v + 1] = q == 0 ? hi : acct[qq][2 * v + 1] + hi;
+            }
+        }
+      }
+    }
   }
 
   // ---- per-output-channel dequantisation scale (fp8 base) ----
@@ -711,6 +886,7 @@ using CfgBig = Cfg<256, 256, 2, 8>;   // 8 waves, 128(n) x 64(m) per wave
 using CfgTall = Cfg<128, 256, 4, 8>;  // 8 waves, 64 x 64 per wave
 using CfgMid = Cfg<256, 192, 2, 8>;   // 8 waves, 96(n) x 64(m) per wave
 using CfgSmall = Cfg<128, 128, 2, 8>;  // 8 waves, 64(n) x 32(m) per wave; also the rank pre-pass (N = r)
+using CfgDeep = Cfg<128, 128, 2, 8, 4>;  // the same tile with four ring buffers: one workgroup per CU
 
 // End column of group g of a grouped launch (INT_MAX past the last group: no tile
 // starts there).
@@ -723,17 +899,19 @@ bool groups_fit(const LoraArgs& p, int bn) {
   return true;
 }
 
-template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false>
-hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1) {
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
+          bool RED = false>
+hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1,
+                      uint64_t* red_part = nullptr, unsigned* red_cnt = nullptr) {
   const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
   const int tiles_n = (int)((p.N + C::BN - 1) / C::BN);
-  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN><<<dim3(tiles_m * tiles_n, splits), dim3(C::NT), 0, p.stream>>>(
+  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN, RED><<<dim3(tiles_m * tiles_n, splits), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
       reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n,
       group_end(p, 0), group_end(p, 1), group_end(p, 2), p.groups > 1 ? p.r * p.lda : 0,
-      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0, p.wmap);
+      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0, p.wmap, red_part, red_cnt);
   return hipGetLastError();
 }
 
@@ -763,17 +941,32 @@ Tile choose_tile(const LoraArgs& p) {
   return tall > big ? Tile::kTall : Tile::kBig;
 }
 
+// 128 x 128 tiles: with at most one workgroup per CU (no more tiles than CUs) the deep ring,
+// else two workgroups per CU on the two-buffer ring (they hide each other's fills).
+template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
+hipError_t launch_small(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+  if constexpr (WDT == kBF16 && !GATHER) {
+    if (((p.M + 127) / 128) * ((p.N + 127) / 128) <= 256) return launch_cfg<CfgDeep, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+  }
+  return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+}
+
 template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER = false>
 hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
   // Ranks 33-64 (two rank blocks) use 128 x 256, whose 64 x 64 wave tile leaves registers
-  // for the second block's T accumulators beside the base accumulators.
+  // for the second block's T accumulators beside the base accumulators, or 128 x 128 (one
+  // rank block per wave) where the wider tiles would leave more CUs idle.
   if constexpr (RB == 2) {
-    return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);  // groups fit 256 (checked)
+    const int64_t tm = (p.M + 127) / 128;
+    const double tall = wave_efficiency(tm * ((p.N + 255) / 256)) * 0.85;  // groups fit 256 (checked)
+    const double small = wave_efficiency(tm * ((p.N + 127) / 128)) * 0.75;
+    if (small > tall) return launch_small<WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
   } else {
     switch (choose_tile(p)) {
       case Tile::kMid: return launch_cfg<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
       case Tile::kTall: return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-      case Tile::kSmall: return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      case Tile::kSmall: return launch_small<WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
       default: return launch_cfg<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
     }
   }
@@ -882,6 +1075,7 @@ bool fp8_matrix_cores(const LoraArgs& p) {
 // while the partials exceed their budget; a grouped call whose groups would take another
 // count alone goes group by group, so grouped outputs stay those of the single calls.
 constexpr int kMediumMaxM = 160;  // measured: the split form wins at M = 65-128, loses at 192-256
+// (since the in-launch split-K form, taken first for ranks up to 64, it serves ranks 65-256)
 constexpr int kMediumMaxSplits = 16;
 constexpr size_t kMediumPartBytes = (size_t)24 << 20;  // with T, within the no-allocation scratch
 
@@ -900,7 +1094,52 @@ int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool
   return s > 1 ? s : 0;
 }
 
+// ---- Split-K in one launch (the RED form of prefill_kernel over 128 x 128 tiles) ----
+// For shapes whose 128 x 128 tiles leave most CUs idle (few rows of tokens, or narrow N),
+// K is cut into S equal parts over a second grid dimension. Each split runs the fused K
+// loop (T included) over its part and leaves fp32 partial records; the last split of a tile
+// sums them in split order and finishes the tile. One launch, no pre-pass: T comes from the
+// same K loops. The split count fills at most one workgroup per CU (the deep ring's LDS
+// takes a whole CU; allowing two per CU measured the same), keeps at least kRedMinTiles K
+// tiles per split, divides the K tile count and keeps the records within their budget (the
+// no-allocation scratch holds them).
+constexpr int kRedMaxSplits = 16;
+constexpr int kRedMinTiles = 8;  // 1.7B layer at M = 129-256: 8 K tiles per split 7-8 % ahead of 4
+constexpr size_t kRedPartBytes = (size_t)24 << 20;
+
+// Bytes of one (tile, split) record: 8 waves x 64 lanes x (16 base words + 8 T words).
+size_t red_record_bytes(bool lora) {
+  return (size_t)CfgDeep::NW * 64 * 8 * (CfgDeep::NI * CfgDeep::MJ * 8 + (lora ? 8 : 0));
+}
+
+int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool gather) {
+  if (!has_w || gather || w_dtype != kBF16 || M < 1) return 0;
+  const int64_t nk = K / BK;
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  if (tiles > kRedMaxTiles) return 0;
+  const char* env = std::getenv("WSL_PREFILL_SPLIT");  // "off", or a forced split count (side-by-side timing)
+  if (env != nullptr) {
+    if (std::strcmp(env, "off") == 0) return 0;
+    const int f = std::atoi(env);
+    if (f >= 2 && f <= kRedMaxSplits && nk % f == 0 && (size_t)(tiles * f) * red_record_bytes(true) <= kRedPartBytes)
+      return f;
+  }
+  int s = 1;
+  while (s * 2 <= kRedMaxSplits && nk % (s * 2) == 0 && nk / (s * 2) >= kRedMinTiles && tiles * s * 2 <= 256) s *= 2;
+  while (s > 1 && (size_t)(tiles * s) * red_record_bytes(true) > kRedPartBytes) s /= 2;
+  return s > 1 ? s : 0;
+}
+
 namespace {
+hipError_t launch_red(const LoraArgs& p, int splits) {
+  LoraArgs q = p;
+  q.K = p.K / splits;
+  uint64_t* part = reinterpret_cast<uint64_t*>(p.ws);
+  if (p.r == 0) return launch_cfg<CfgDeep, kBF16, true, 0, false, false, false, false, true>(q, nullptr, 0, splits, part, p.red_cnt);
+  if (p.r <= 32) return launch_cfg<CfgDeep, kBF16, true, 1, false, false, false, false, true>(q, nullptr, 0, splits, part, p.red_cnt);
+  return launch_cfg<CfgDeep, kBF16, true, 2, false, false, false, false, true>(q, nullptr, 0, splits, part, p.red_cnt);
+}
+
 // y[m][n] = bf16(sum_s part[s][m][n] + sum_j T[m][goff(n) + j] B[n][j]): the partials in split
 // order, then the LoRA up-projection over the bf16 T of the rank pre-pass (s applied there).
 // A workgroup owns 32 rows x 32 columns: it stages their T rows (all rt ranks) and B rows in
@@ -1015,15 +1254,20 @@ hipError_t launch_medium(const LoraArgs& p, int splits) {
 // Workspace of the prefill path: the rank pre-pass region (r > RIN, any rank on the fp8
 // matrix-core path or on the medium-M split path, which take T from the pre-pass), then for
 // an fp8 W the activation codes of the fp8 matrix-core path, or the medium path's partials.
+// With the in-launch split-K form possible (which `r`, the ranks of all groups, does not
+// decide) its records are covered as well.
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
   if (w_dtype == kFP8)
     return (r > 0 ? rank_prepass_bytes(M, K, r) : 0) + prefill_fp8_workspace_bytes(M, K, 2);
+  size_t b = r > RIN ? rank_prepass_bytes(M, K, r) : 0;
   const int ms = medium_splits(M, N, K, r, w_dtype, true, false);
   if (ms > 0) {
     const size_t t_bytes = r > 0 ? ((rank_prepass_bytes(M, K, r) + 255) & ~(size_t)255) : 0;
-    return t_bytes + (size_t)ms * M * N * 4;
+    b = std::max(b, t_bytes + (size_t)ms * M * N * 4);
   }
-  return r > RIN ? rank_prepass_bytes(M, K, r) : 0;
+  const int rs = red_splits(M, N, K, w_dtype, true, false);
+  if (rs > 0) b = std::max(b, (size_t)(((M + 127) / 128) * ((N + 127) / 128) * rs) * red_record_bytes(r > 0));
+  return b;
 }
 
 // Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by the prefill kernel run as a
@@ -1120,6 +1364,10 @@ hipError_t launch_prefill(const LoraArgs& p) {
     }
     char* codes = reinterpret_cast<char*>(p.ws) + (p.r > 0 ? rank_prepass_bytes(p.M, p.K, rt) : 0);
     return launch_prefill_fp8(p, p.r > 0 ? t : nullptr, rt, codes, p.fp8_terms);
+  }
+  if (has_w && p.w_dtype == kBF16 && p.r <= RIN && p.red_cnt != nullptr) {
+    const int rs = red_splits(p.M, p.N, p.K, p.w_dtype, true, false);
+    if (rs > 0) return launch_red(p, rs);
   }
   if (has_w && p.w_dtype == kBF16) {
     const int ms = medium_splits(p.M, p.N, p.K, rt, p.w_dtype, true, false);

@@ -250,6 +250,7 @@ int run_call(wsl::LoraArgs p, void* workspace, size_t workspace_bytes) {
   } else {
     p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes + half;
     p.ws_bytes = half;
+    p.red_cnt = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(workspace) + wsl::kRedCntOff);
   }
   hipError_t e;
   switch (path) {
@@ -277,13 +278,21 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
   const Path path = choose_path(p);
   // The prefill path's medium-M split form must be taken (with the same split count) by the
   // grouped launch exactly when each group alone takes it, so the groups' outputs stay those
-  // of the single calls bit for bit; otherwise the groups go one by one.
+  // of the single calls bit for bit; otherwise the groups go one by one. A grouped launch
+  // that takes the in-launch split-K form runs whole: its split count follows the launch's
+  // tiles, so a group may sum K in another order than its single call (within the bar).
   bool medium_agrees = true;
-  if (path == Path::kPrefill) {
-    const int ms = wsl::medium_splits(p.M, p.N, p.K, p.r * n_groups, p.w_dtype, p.w != nullptr, false);
-    for (int g = 0; g < n_groups; ++g)
-      medium_agrees =
-          medium_agrees && wsl::medium_splits(p.M, group_n[g], p.K, p.r, p.w_dtype, p.w != nullptr, false) == ms;
+  // the medium split form's count for `n` columns of rank rt, 0 where it is not taken (the
+  // in-launch split-K form comes first for ranks up to 64)
+  const auto medium = [&](int64_t n, int64_t rt) {
+    if (p.r <= 64 && wsl::red_splits(p.M, n, p.K, p.w_dtype, p.w != nullptr, false) > 0) return 0;
+    return wsl::medium_splits(p.M, n, p.K, rt, p.w_dtype, p.w != nullptr, false);
+  };
+  const bool red = path == Path::kPrefill && p.r <= 64 &&
+                   wsl::red_splits(p.M, p.N, p.K, p.w_dtype, p.w != nullptr, false) > 0;
+  if (path == Path::kPrefill && !red) {
+    const int ms = medium(p.N, p.r * n_groups);
+    for (int g = 0; g < n_groups; ++g) medium_agrees = medium_agrees && medium(group_n[g], p.r) == ms;
   }
   if ((path == Path::kPrefill && medium_agrees && wsl::prefill_groups_supported(p)) ||
       (path == Path::kDecode && wsl::decode_groups_supported(p)))

@@ -139,6 +139,9 @@ struct LoraArgs {
   // Shared-base forms: W (and w_scale) rows by output column, and W's row count.
   RowMap wmap;
   int64_t wrows = 0;
+  // Arrival counters of the prefill path's in-launch split-K form (the workspace prefix
+  // from kRedCntOff); nullptr keeps that form off.
+  unsigned* red_cnt = nullptr;
 };
 
 // Each launcher returns hipSuccess or the launch error.
@@ -148,6 +151,9 @@ bool prefill_supported(const LoraArgs& p);
 bool prefill_groups_supported(const LoraArgs& p);
 // K splits of the medium-M split form of the prefill path (0: not taken); rt = r * groups.
 int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool has_w, bool gather);
+// K splits of the prefill path's in-launch split-K form over 128 x 128 tiles (0: not taken;
+// it also needs a rank of at most 64 per group).
+int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool gather);
 // Plain bf16 products over a long contiguous K (csrc/lora_prefill.hip) and the rank
 // pre-pass T = bf16(s x . A^T), for the weight gradients (csrc/lora_backward.hip).
 int product_splits(int64_t M, int64_t N, int64_t nk, bool divides);
@@ -196,14 +202,20 @@ hipError_t launch_factorized_embedding(const int64_t* ids, int64_t n_ids, const 
                                        hipStream_t stream);
 
 // Largest M routed to the decode-shaped (skinny) kernels: every form (fused, fp8 base, the
-// greedy head) up to kDecodeMaxM, the plain bf16 form up to kDecodePlainMaxM (eight token
-// blocks, four waves along K, x walked in passes).
+// greedy head) up to kDecodeMaxM, the plain bf16 form up to kDecodePlainMaxM (five token
+// blocks, four waves along K, x walked in passes). Past 72 tokens the prefill path's
+// in-launch split-K form is faster (1.7B layer, grouped: 2.60 against 2.63 ms at 72 tokens,
+// 2.67 against 2.64 at 80, 2.88 against 2.66 at 96).
 constexpr int64_t kDecodeMaxM = 64;
-constexpr int64_t kDecodePlainMaxM = 128;
+constexpr int64_t kDecodePlainMaxM = 72;
 
-// Every workspace starts with this many bytes of counters (a launch counter and arrival
-// counters of the decode path). They must be zero when the workspace is first used;
-// every launch leaves them valid for the next. Path-specific scratch follows the prefix.
+// Every workspace starts with this many bytes of counters: the decode path's launch counter
+// in its first 1 KB, and from kRedCntOff the prefill path's arrival counters of the
+// in-launch split-K form (one 32-bit word per tile). They must be zero when the workspace
+// is first used; every launch leaves them valid (its counters back at zero) for the next.
+// Path-specific scratch follows the prefix.
 constexpr size_t kCounterBytes = 65536;
+constexpr size_t kRedCntOff = 4096;
+constexpr int64_t kRedMaxTiles = (int64_t)((kCounterBytes - kRedCntOff) / 4);
 
 }  // namespace wsl
