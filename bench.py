@@ -351,22 +351,23 @@ def bench_medium(dev, steps, warmup):
     Qwen3-1.7B projection shapes, r = 64, cold weights (6 rotating copies), 28 layers per
     graph, grouped q|k|v and gate|up, each way the library can run them on the same inputs:
     the decode path's wide form (the default up to 72 tokens), the prefill path's in-launch
-    split-K form (WSL_DECODE_WIDE=off below 129 tokens; the default above), its earlier
-    medium split form (also WSL_PREFILL_SPLIT=off; up to 160 tokens) and its unsplit tiles
-    (also WSL_PREFILL_MEDIUM=off)."""
+    split-K form (WSL_DECODE_WIDE=off below 73 tokens; the default above) and its unsplit
+    tiles (also WSL_PREFILL_SPLIT=off and WSL_PREFILL_MEDIUM=off, which keep the split forms
+    off); from 128 tokens also torch.matmul (hipBLASLt) on the same
+    inputs: the plain GEMM on the stacked weights (no LoRA term) and the unfused three-call
+    LoRA linear (the reference's arithmetic)."""
     out = {}
     keys = ("WSL_DECODE_WIDE", "WSL_PREFILL_MEDIUM", "WSL_PREFILL_SPLIT")
     saved = {k: os.environ.get(k) for k in keys}
     ways = (("decode", {}),
             ("split_k", {"WSL_DECODE_WIDE": "off"}),
-            ("medium", {"WSL_DECODE_WIDE": "off", "WSL_PREFILL_SPLIT": "off"}),
             ("unsplit", {"WSL_DECODE_WIDE": "off", "WSL_PREFILL_SPLIT": "off", "WSL_PREFILL_MEDIUM": "off"}))
     try:
         for M in (64, 65, 72, 96, 128, 160, 192, 256, 512, 1024):
             row = {}
             for label, env in ways:
-                if (label == "decode" and M > 72) or (label != "decode" and M <= 64) or (label == "medium" and M > 160):
-                    continue  # decode runs up to 72 tokens, the medium split form to 160; the prefill forms above 64
+                if (label == "decode" and M > 72) or (label != "decode" and M <= 64):
+                    continue  # decode runs up to 72 tokens, the prefill forms above 64
                 for k in keys:
                     os.environ.pop(k, None)
                 os.environ.update(env)
@@ -377,6 +378,18 @@ def bench_medium(dev, steps, warmup):
                 row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
                               "TFLOP/s": round(st.flops() / ms / 1e9, 1)}
                 del g, st
+                torch.cuda.empty_cache()
+            if M >= 128:
+                for k in keys:
+                    os.environ.pop(k, None)
+                st = VendorStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
+                st.stack_groups()
+                for label, fn in (("torch_plain_gemm_grouped", st.run_plain_grouped), ("torch_unfused_lora", st.run_lora)):
+                    g = graph_of(fn)
+                    ms = time_replays(g, steps, warmup)
+                    row[label] = {"ms_per_28_layers": round(ms, 4)}
+                    del g
+                del st
                 torch.cuda.empty_cache()
             out[f"M={M}"] = row
     finally:

@@ -1,5 +1,5 @@
-"""Medium M: 65-128 tokens run on the decode path's wide form, 129 and more on the prefill
-path's in-launch split-K form (ranks up to 64) or, above rank 64 up to 160 tokens, its
+"""Medium M: 65-72 tokens run on the decode path's wide form, more on the prefill path's
+in-launch split-K form (ranks up to 64) or, above rank 64 up to 160 tokens over long K, its
 medium split form (split-K base product, rank pre-pass, combine kernel); each against the
 float64 oracle, bar max|y - y_ref| / max|y_ref| <= 1e-2. Grouped launches against the single
 calls within the bar (the K split counts of both forms above 64 tokens depend on N). The
@@ -40,7 +40,8 @@ CASES = [
     (100, 2048, 2048, 32),
     (128, 1024, 1024, 16),
     (150, 3072, 1024, 32),
-    (160, 1024, 2048, 128),  # r > 64
+    (160, 1024, 2048, 128),  # r > 64: unsplit tiles, T by the rank pre-pass
+    (130, 2048, 6144, 128),  # r > 64 over 96 K tiles: the medium split form
     (65, 200, 512, 8),       # N off every tile grid
     (96, 512, 4096, 0),      # plain linear
 ]

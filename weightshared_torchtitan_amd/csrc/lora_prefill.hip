@@ -1085,7 +1085,10 @@ int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool
   const char* env = std::getenv("WSL_PREFILL_MEDIUM");  // "off": the unsplit tiles, for side-by-side timing
   if (env != nullptr && std::strcmp(env, "off") == 0) return 0;
   const int64_t nk = K / BK;
-  if (nk < 8) return 0;
+  // Since the 128 x 128 tiles' deep ring, the unsplit tiles win below 64 K tiles (rank 128:
+  // 100 x 2048 x 2048 27.6 against 30.9 us, 160 x 6144 x 2048 30.6 against 41.6; rank 96,
+  // 150 x 3072 x 1024 19.3 against 31.9) and lose above (130 x 2048 x 6144: 60.9 against 41.6)
+  if (nk < 64) return 0;
   const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
   if (tiles >= 192) return 0;  // enough workgroups without a split
   int s = 1;
@@ -1124,6 +1127,11 @@ int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool ga
     if (f >= 2 && f <= kRedMaxSplits && nk % f == 0 && (size_t)(tiles * f) * red_record_bytes(true) <= kRedPartBytes)
       return f;
   }
+  // At 97-128 tiles the unsplit launch already covers half the CUs: splitting in two paid
+  // only over long K (M x N x K = 1024 x 2048 x 6144: 52.4 against 62.8 us; 2048 x 1024 x
+  // 1024: 18.1 against 14.1, 1024 x 2048 x 2048: 27.0 against 25.6, 512 x 4096 x 2048: 26.7
+  // against 24.9). At 96 tiles (gate|up at 128 tokens) it still paid.
+  if (tiles > 96 && nk < 64) return 0;
   int s = 1;
   while (s * 2 <= kRedMaxSplits && nk % (s * 2) == 0 && nk / (s * 2) >= kRedMinTiles && tiles * s * 2 <= 256) s *= 2;
   while (s > 1 && (size_t)(tiles * s) * red_record_bytes(true) > kRedPartBytes) s /= 2;
