@@ -164,19 +164,25 @@ __device__ __forceinline__ void ring_barrier() {
 // two transposing LDS reads (lds_read_tr8). K rows from `grows` (the token count, from this
 // split's start) on are read clamped and zeroed in the x' tile after they land. M and N are
 // multiples of 8.
+//
+// PER: persistent strips. Workgroup b owns `tpw` consecutive column tiles of one row block
+// (a strip, all in one group) and runs them one after another. T depends only on the row
+// block and the group, so the first tile's K loop computes it (as an unsplit launch does),
+// parks it in an LDS region of its own, and the strip's later tiles skip the rank MFMAs
+// and the A fills and reuse it.
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
-          bool RED = false>
+          bool RED = false, bool PER = false>
 __global__ void __launch_bounds__(C::NT, 1)
 prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const int64_t* __restrict__ gidx, int64_t grows,
                const void* __restrict__ w, int64_t ldw, const float* __restrict__ w_scale,
-               const uint16_t* __restrict__ a, int64_t lda,
-               const uint16_t* __restrict__ tg, int64_t ldt,
+               const uint16_t* __restrict__ a_arg, int64_t lda,
+               const uint16_t* __restrict__ tg_arg, int64_t ldt,
                const uint16_t* __restrict__ bm, int64_t ldb, float s, float yscale,
                uint16_t* __restrict__ y, int64_t ldy,
                int M, int N, int K, int r, int tiles_m, int tiles_n,
                int ge0, int ge1, int ge2, int64_t a_gstride, int t_gstride, RowMap wmap,
-               uint64_t* __restrict__ red_part, unsigned* __restrict__ red_cnt) {
+               uint64_t* __restrict__ red_part, unsigned* __restrict__ red_cnt, int tpw) {
   constexpr bool W8 = HAS_W && WDT == kFP8;
   constexpr bool WDIRECT = HAS_W && WDT == kBF16;
   constexpr bool LORA = RB > 0 || EXT_T;
@@ -184,8 +190,16 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   constexpr int AB = RB * 32 * ROWB;         // rank-A slice of a K tile
   constexpr int STAGE = C::XB + C::WB + AB;  // one of the two ring buffers
   constexpr int OS = C::BN * 2 + 16;          // LDS row stride of the staged output tile
-  constexpr int LDS_BYTES = (C::NS * STAGE > C::BM * OS) ? C::NS * STAGE : C::BM * OS;
+  // PER: T of the strip's row block, [BM m][r ranks] bf16, past the ring (rows of 64 bytes
+  // for r <= 32, 128 for r <= 64); the staged output tile stays within the ring
+  constexpr int TROW = (PER && RB == 1) ? 64 : ROWB;
+  constexpr int TREG = PER ? C::BM * TROW : 0;
+  constexpr int RING = C::NS * STAGE + TREG;
+  constexpr int LDS_BYTES = (RING > C::BM * OS) ? RING : C::BM * OS;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(!PER || C::BM * OS <= C::NS * STAGE, "staged output clear of the T region");
+  static_assert(!PER || (WDT == kBF16 && HAS_W && RB > 0 && !EXT_T && !GATHER && !SPLIT && !TN && !RED && C::NS == 2),
+                "persistent strips: bf16 W, in-kernel T, two-buffer ring");
   static_assert(C::BM * ROWB <= STAGE && C::BN * ROWB <= STAGE, "LoRA phase fits the ring");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   static_assert(!SPLIT || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "split-K is a plain bf16 GEMM");
@@ -197,7 +211,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int64_t kofs = (int64_t)blockIdx.y * K;
     x += kofs;
     w = reinterpret_cast<const uint16_t*>(w) + kofs;
-    if constexpr (RB > 0) a += kofs;
+    if constexpr (RB > 0) a_arg += kofs;
   }
   if constexpr (SPLIT) {
     const int64_t kofs = (int64_t)blockIdx.y * K;
@@ -220,26 +234,40 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   const int l32 = lane & 31;
   const int lh = lane >> 5;
 
-  // ---- XCD-aware, grouped tile order ----
-  const int G = tiles_m * tiles_n;
+  // Byte offset of 16-byte chunk c of row `row` in the T region: 64-byte rows with the
+  // chunk XORed by row bits 2..3 (16 consecutive rows at one chunk cover all 64 banks), or
+  // the ring's own 128-byte layout.
+  auto t_off = [](int row, int c) {
+    if constexpr (TROW == 64) return row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
+    else return lds_off(row, c);
+  };
+
+  // One output tile: tile tq of this workgroup's strip (always 0 without PER). `first`
+  // (a compile-time bool) is whether it is the strip's first tile, which computes T.
+  auto do_tile = [&](const int tq, auto first) {
+  // ---- XCD-aware, grouped tile order (over strips of tpw column tiles with PER) ----
+  const int SW = PER ? tpw : 1;
+  const int G = tiles_m * tiles_n / SW;
   int t = blockIdx.x;
+  if constexpr (PER) asm volatile("" : "+s"(t));  // recomputed per tile, not kept live across tiles
   if (G % N_XCD == 0) t = (t % N_XCD) * (G / N_XCD) + t / N_XCD;
-  const int group_size = GROUP_M * tiles_n;
+  const int group_size = GROUP_M * (tiles_n / SW);
   const int first_m = (t / group_size) * GROUP_M;
   const int gm = min(tiles_m - first_m, GROUP_M);
   const int tm = first_m + (t % group_size) % gm;
-  const int tn = (t % group_size) / gm;
+  const int tn = ((t % group_size) / gm) * SW + tq;
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
+  // whether this tile computes T in its K loop (every tile but a strip's later ones)
+  constexpr bool t_here = !PER || decltype(first)::value;
   // Grouped launch: output columns [ge_{g-1}, ge_g) are projection g, whose LoRA down
   // factor is rank block g of a (rows g*r..g*r+r-1) and whose T is column block g of the
-  // pre-pass output. Group ends are multiples of BN, so a tile lies in one group; B rows
-  // and W rows are indexed by the output column as in a single projection.
-  {
-    const int grp = (n0 >= ge0) + (n0 >= ge1) + (n0 >= ge2);
-    a += grp * a_gstride;
-    tg += grp * t_gstride;
-  }
+  // pre-pass output. Group ends are multiples of BN (of a strip's width with PER), so a
+  // tile lies in one group; B rows and W rows are indexed by the output column as in a
+  // single projection.
+  const int grp = (n0 >= ge0) + (n0 >= ge1) + (n0 >= ge2);
+  const uint16_t* const a = a_arg + grp * a_gstride;
+  const uint16_t* const tg = tg_arg + grp * t_gstride;
 
   // ---- sources of this wave's direct fills: uniform tile base + 32-bit lane offset ----
   const char* xbase = reinterpret_cast<const char*>(GATHER ? x : x + (int64_t)m0 * ldx);
@@ -318,7 +346,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       for (int i = 0; i < C::NWI; ++i) direct_fill(sw, wave * C::NWI + i, wbase + k0 * 2 + opaque(woff[i]));
     }
     if constexpr (RB > 0) {
-      if (wave < NAI) direct_fill(sa, wave, reinterpret_cast<const char*>(a) + k0 * 2 + opaque(aoff));
+      if (t_here && wave < NAI) direct_fill(sa, wave, reinterpret_cast<const char*>(a) + k0 * 2 + opaque(aoff));
     }
   };
   // B slice [BN][64 ranks from rk0] into `dst`. Lanes past rank r read a finite element
@@ -610,6 +638,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   if constexpr (RUN_K) {
     if constexpr (RB == 0) {
       run(std::false_type{});
+    } else if constexpr (PER && !t_here) {
+      run(std::false_type{});
     } else if constexpr (ALL_T) {
       run(std::true_type{});
     } else {
@@ -731,10 +761,10 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
   // ---- LoRA up-projection: acc[n][m] += sum_j B[n][j] * T[m][j] in 64-rank chunks ----
   if constexpr (LORA) {
-    char* st = lora_t;                   // T chunk [BM m][64 ranks]
+    char* st = PER ? lds + C::NS * STAGE : lora_t;  // T chunk [BM m][64 ranks] (the T region with PER)
     char* sb = lora_b;                   // B chunk [BN n][64 ranks]
     if constexpr (RB > 0) {
-      if (t_wave) {
+      if (t_wave && t_here) {
         // park bf16(s * T): rows wm*TM + tj*32 + l32, ranks trb*32 + 8g + 4*lh + e. Ranks
         // >= r (A rows past r were filled with row r-1) are zeroed here: they meet finite
         // stand-in columns of B in the up-projection.
@@ -750,7 +780,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             uint2 v;
             v.x = pack_bf16x2(t4[0], t4[1]);
             v.y = pack_bf16x2(t4[2], t4[3]);
-            *reinterpret_cast<uint2*>(st + lds_off(mrow, trb[q] * 4 + g) + lh * 8) = v;
+            *reinterpret_cast<uint2*>(st + t_off(mrow, trb[q] * 4 + g) + lh * 8) = v;
           }
         }
       }
@@ -777,7 +807,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         const int c = kk * 2 + lh;
         bf16x8_t tf[C::MJ], bf[C::NI];
 #pragma unroll
-        for (int j = 0; j < C::MJ; ++j) tf[j] = as_bf16x8(lds_read16(st, lds_off(wm * C::TM + j * 32 + l32, c)));
+        for (int j = 0; j < C::MJ; ++j) tf[j] = as_bf16x8(lds_read16(st, t_off(wm * C::TM + j * 32 + l32, c)));
 #pragma unroll
         for (int i = 0; i < C::NI; ++i) bf[i] = as_bf16x8(lds_read16(sb, lds_off(wn * C::TN + i * 32 + l32, c)));
 #pragma unroll
@@ -880,6 +910,21 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       for (int e = 0; e < N - n; ++e) dst[e] = (uint16_t)(v[e >> 1] >> ((e & 1) * 16));
     }
   }
+  };  // do_tile
+
+  if constexpr (PER) {
+    // The first tile (with T) peeled from the rest: the loop then holds only the K loop
+    // without rank work. After each tile every wave has read its share of the staged output
+    // before the next tile's fills land in the ring (the stores stay in flight).
+    do_tile(0, std::true_type{});
+    ring_barrier();
+    for (int tq = 1; tq < tpw; ++tq) {
+      do_tile(tq, std::false_type{});
+      ring_barrier();
+    }
+  } else {
+    do_tile(0, std::true_type{});
+  }
 }
 
 using CfgBig = Cfg<256, 256, 2, 8>;   // 8 waves, 128(n) x 64(m) per wave
@@ -900,19 +945,49 @@ bool groups_fit(const LoraArgs& p, int bn) {
 }
 
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
-          bool RED = false>
+          bool RED = false, bool PER = false>
 hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1,
-                      uint64_t* red_part = nullptr, unsigned* red_cnt = nullptr) {
+                      uint64_t* red_part = nullptr, unsigned* red_cnt = nullptr, int tpw = 1) {
   const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
   const int tiles_n = (int)((p.N + C::BN - 1) / C::BN);
-  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN, RED><<<dim3(tiles_m * tiles_n, splits), dim3(C::NT), 0, p.stream>>>(
+  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN, RED, PER>
+      <<<dim3(tiles_m * tiles_n / (PER ? tpw : 1), splits), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
       reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n,
       group_end(p, 0), group_end(p, 1), group_end(p, 2), p.groups > 1 ? p.r * p.lda : 0,
-      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0, p.wmap, red_part, red_cnt);
+      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0, p.wmap, red_part, red_cnt, PER ? tpw : 1);
   return hipGetLastError();
+}
+
+// Column tiles per persistent strip for a launch of BM x BN tiles, or 1 (one tile per
+// workgroup). Strips are taken where the tiles are a whole number k >= 2 of waves over the
+// 256 CUs: 256 workgroups then run k tiles each, and T, computed in the first, costs one
+// tile's rank MFMAs instead of k. A strip stays in one row of tiles and one group.
+// WSL_PREFILL_STRIPS=off keeps one tile per workgroup (side-by-side timing).
+int strip_tiles(const LoraArgs& p, int bm, int bn) {
+  const char* env = std::getenv("WSL_PREFILL_STRIPS");
+  if (env != nullptr && std::strcmp(env, "off") == 0) return 1;
+  const int64_t tiles_m = (p.M + bm - 1) / bm, tiles_n = (p.N + bn - 1) / bn;
+  const int64_t tiles = tiles_m * tiles_n;
+  if (tiles < 512 || tiles % 256 != 0) return 1;
+  const int64_t k = tiles / 256;
+  if (k > tiles_n || tiles_n % k != 0) return 1;
+  for (int g = 0; g + 1 < p.groups; ++g)
+    if (p.gend[g] % (k * bn) != 0) return 1;
+  return (int)k;
+}
+
+// One tile configuration's launch: persistent strips where strip_tiles takes them (bf16 W
+// with T computed in the kernel, two-buffer ring), else one tile per workgroup.
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
+hipError_t launch_tiles(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+  if constexpr (WDT == kBF16 && HAS_W && RB > 0 && !EXT_T && !GATHER && C::NS == 2) {
+    const int k = strip_tiles(p, C::BM, C::BN);
+    if (k > 1) return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, true>(p, tg, ldt, 1, nullptr, nullptr, k);
+  }
+  return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
 }
 
 // Fraction of the 256 CUs kept busy over the launch's waves of workgroups.
@@ -961,13 +1036,13 @@ hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
     const double tall = wave_efficiency(tm * ((p.N + 255) / 256)) * 0.85;  // groups fit 256 (checked)
     const double small = wave_efficiency(tm * ((p.N + 127) / 128)) * 0.75;
     if (small > tall) return launch_small<WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-    return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
   } else {
     switch (choose_tile(p)) {
-      case Tile::kMid: return launch_cfg<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-      case Tile::kTall: return launch_cfg<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      case Tile::kMid: return launch_tiles<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      case Tile::kTall: return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
       case Tile::kSmall: return launch_small<WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-      default: return launch_cfg<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      default: return launch_tiles<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
     }
   }
 }
