@@ -298,6 +298,58 @@ def bench_c2(dev, steps, warmup, grouped=True, single=True):
     return lora_flops_c2(), ms_grouped, ms_single
 
 
+# Prefill launches of configs 2 and 1.7B for side-by-side timing of the path switches (name,
+# M, group widths, K); every launch at r = 32.
+AB_SHAPES = [("c2 q|k|v", 8192, (2048, 1024, 1024), 1024), ("c2 o", 8192, (1024,), 2048),
+             ("c2 gate|up", 8192, (3072, 3072), 1024), ("c2 down", 8192, (1024,), 3072),
+             ("1.7b q|k|v", 8192, (2048, 1024, 1024), 2048), ("1.7b o", 8192, (2048,), 2048),
+             ("1.7b gate|up", 8192, (6144, 6144), 2048), ("1.7b down", 8192, (2048,), 6144)]
+
+
+def bench_env_ab(dev, modes, names=None, launches=28, rounds=6):
+    """Side-by-side timing of path switches read at launch (WSL_PREFILL_STRIPS,
+    WSL_PREFILL_SPLIT, ...): per launch shape one HIP graph of `launches` launches is captured
+    under each mode's environment, and the graphs are replayed in alternating order over
+    `rounds` rounds (5 replays each, HIP events), so clock drift falls on every mode alike.
+    Returns the median us per launch per mode."""
+    from weightshared_torchtitan_amd import ops
+    out = {}
+    for name, M, ns, K in AB_SHAPES:
+        if names is not None and name not in names:
+            continue
+        r = 32
+        g = torch.Generator(device=dev).manual_seed(M + sum(ns) + K)
+        x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        w = (torch.randn(sum(ns), K, device=dev, generator=g) * 0.02).bfloat16()
+        a = (torch.randn(len(ns) * r, K, device=dev, generator=g) * 0.02).bfloat16()
+        b = (torch.randn(sum(ns), r, device=dev, generator=g) * 0.02).bfloat16()
+        if len(ns) > 1:
+            fn = lambda: ops.lora_linear_grouped_op(x, w, None, a, b, 2.0, list(ns))  # noqa: E731
+        else:
+            fn = lambda: ops.lora_linear_op(x, w, None, a, b, 2.0)  # noqa: E731
+        graphs = {}
+        for mode, env in modes.items():
+            saved = {k: os.environ.get(k) for k in env}
+            os.environ.update(env)
+            try:
+                graphs[mode] = graph_of(lambda: [fn() for _ in range(launches)])
+            finally:
+                for k, v in saved.items():
+                    if v is None:
+                        os.environ.pop(k, None)
+                    else:
+                        os.environ[k] = v
+        times = {m: [] for m in modes}
+        order = list(modes)
+        for it in range(rounds):
+            for m in (order if it % 2 == 0 else order[::-1]):
+                times[m].append(time_replays(graphs[m], 5, 1) * 1e3 / launches)
+        out[name] = {m: round(sorted(v)[len(v) // 2], 2) for m, v in times.items()}
+        del graphs
+    torch.cuda.empty_cache()
+    return out
+
+
 def lora_flops_c2():
     return 28 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_0P6B)
 
@@ -781,10 +833,13 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=("c1", "c2", "c2single", "c2_1p7b", "c3", "c4", "c5", "c5paths", "emb",
-                                       "vendor", "backward", "medium", "shape"), default=None)
+                                       "vendor", "backward", "medium", "shape", "envab"), default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--ab", default='{"default": {}, "strips_off": {"WSL_PREFILL_STRIPS": "off"}}',
+                    help="--only envab: JSON {mode: {ENV: value}} of the settings timed side by side")
+    ap.add_argument("--ab-shapes", default=None, help="--only envab: comma-separated names from AB_SHAPES")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -810,7 +865,9 @@ def main():
               "vendor": lambda: bench_vendor(dev, args.steps, args.warmup),
               "medium": lambda: bench_medium(dev, min(args.steps, 10), min(args.warmup, 3)),
               "backward": lambda: bench_backward(dev, min(args.steps, 10), min(args.warmup, 3)),
-              "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor)}[args.only]
+              "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor),
+              "envab": lambda: bench_env_ab(dev, json.loads(args.ab),
+                                            args.ab_shapes.split(",") if args.ab_shapes else None)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     flops, ms, ms_single = bench_c2(dev, args.steps, args.warmup, grouped=args.only != "c2single",
