@@ -350,6 +350,76 @@ def bench_env_ab(dev, modes, names=None, launches=28, rounds=6):
     return out
 
 
+STAMP_PHASES = ("first_fill", "k_loop", "lora_up", "stage", "store_issue")
+
+
+def bench_stamps(dev, names=None):
+    """Where a prefill tile's time goes, from the instrumented library's per-workgroup
+    wall-clock stamps (WSL_LIB=<repo>/weightshared_torchtitan_amd/libwsl_stamps.so, built by
+    `python -m weightshared_torchtitan_amd.build --stamps`). One launch per shape of
+    AB_SHAPES after three warm-up launches; per tile of a strip (q = 0, 1, ...) the median and
+    maximum over workgroups of each phase's duration (us at the 100 MHz constant clock), the
+    spread of tile starts, and the span from the first start to the last store beside the
+    HIP-event time of the same launch."""
+    import ctypes
+    import numpy as np
+    from weightshared_torchtitan_amd import _native, ops
+    lib = _native.lib()
+    if not hasattr(lib, "wsl_prefill_stamps"):
+        raise SystemExit("--only stamps needs WSL_LIB=<repo>/weightshared_torchtitan_amd/libwsl_stamps.so "
+                         "(python -m weightshared_torchtitan_amd.build --stamps)")
+    lib.wsl_prefill_stamps.restype = ctypes.c_int
+    lib.wsl_prefill_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    recs = 4096
+    buf = np.zeros(recs * 8, dtype=np.uint64)
+    out = {}
+    for name, M, ns, K in AB_SHAPES:
+        if names is not None and name not in names:
+            continue
+        r = 32
+        g = torch.Generator(device=dev).manual_seed(M + sum(ns) + K)
+        x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        w = (torch.randn(sum(ns), K, device=dev, generator=g) * 0.02).bfloat16()
+        a = (torch.randn(len(ns) * r, K, device=dev, generator=g) * 0.02).bfloat16()
+        b = (torch.randn(sum(ns), r, device=dev, generator=g) * 0.02).bfloat16()
+        if len(ns) > 1:
+            fn = lambda: ops.lora_linear_grouped_op(x, w, None, a, b, 2.0, list(ns))  # noqa: E731
+        else:
+            fn = lambda: ops.lora_linear_op(x, w, None, a, b, 2.0)  # noqa: E731
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        lib.wsl_prefill_stamps(buf.ctypes.data, recs)  # clears the stamps
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        rc = lib.wsl_prefill_stamps(buf.ctypes.data, recs)
+        if rc != 0:
+            raise RuntimeError(f"wsl_prefill_stamps failed: {rc}")
+        st = buf.reshape(recs, 8).astype(np.int64)
+        valid = st[:, 0] > 0
+        t0 = st[valid, 0].min()
+        res = {"event_us": round(e0.elapsed_time(e1) * 1e3, 2),
+               "span_us": round((st[valid, 5].max() - t0) / 100.0, 2)}
+        for q in range(4):
+            rows = st[(np.arange(recs) % 4 == q) & valid]
+            if len(rows) == 0:
+                continue
+            d = {"workgroups": int(len(rows)),
+                 "start_after_first_us": [round(float(np.median(rows[:, 0] - t0)) / 100, 2),
+                                          round(float((rows[:, 0] - t0).max()) / 100, 2)]}
+            for k, ph in enumerate(STAMP_PHASES, start=1):
+                dd = (rows[:, k] - rows[:, k - 1]) / 100.0
+                d[ph + "_us"] = [round(float(np.median(dd)), 2), round(float(dd.max()), 2)]
+            res[f"tile{q}"] = d
+        out[name] = res
+        del x, w, a, b
+    return out
+
+
 def lora_flops_c2():
     return 28 * sum(lora_flops(8192, N, K, 32) for _, N, K in QWEN3_0P6B)
 
@@ -833,13 +903,13 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=("c1", "c2", "c2single", "c2_1p7b", "c3", "c4", "c5", "c5paths", "emb",
-                                       "vendor", "backward", "medium", "shape", "envab"), default=None)
+                                       "vendor", "backward", "medium", "shape", "envab", "stamps"), default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--ab", default='{"default": {}, "strips_off": {"WSL_PREFILL_STRIPS": "off"}}',
                     help="--only envab: JSON {mode: {ENV: value}} of the settings timed side by side")
-    ap.add_argument("--ab-shapes", default=None, help="--only envab: comma-separated names from AB_SHAPES")
+    ap.add_argument("--ab-shapes", default=None, help="--only envab / stamps: comma-separated names from AB_SHAPES")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -867,7 +937,8 @@ def main():
               "backward": lambda: bench_backward(dev, min(args.steps, 10), min(args.warmup, 3)),
               "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor),
               "envab": lambda: bench_env_ab(dev, json.loads(args.ab),
-                                            args.ab_shapes.split(",") if args.ab_shapes else None)}[args.only]
+                                            args.ab_shapes.split(",") if args.ab_shapes else None),
+              "stamps": lambda: bench_stamps(dev, args.ab_shapes.split(",") if args.ab_shapes else None)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     flops, ms, ms_single = bench_c2(dev, args.steps, args.warmup, grouped=args.only != "c2single",

@@ -12,7 +12,9 @@ import threading
 
 import torch  # noqa: F401  (loads the HIP runtime libwsl links against)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwsl.so")
+# WSL_LIB names another build of the same library (the instrumented libwsl_stamps.so that
+# `bench.py --only stamps` reads); by default the in-tree libwsl.so.
+LIB_PATH = os.environ.get("WSL_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwsl.so")
 
 WSL_OK = 0
 WSL_E_INVALID_ARG = -1

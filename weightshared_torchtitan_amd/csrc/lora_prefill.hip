@@ -63,6 +63,23 @@ constexpr int GROUP_M = 4;  // row tiles per XCD group (4 against 8 and 16: +0.9
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Phase timestamps, in instrumented builds only (-DWSL_STAMPS, libwsl_stamps.so): record
+// `rec` (workgroup b's tile q of a strip: 4 b + min(q, 3)) slot k gets the 100 MHz constant
+// clock when the workgroup's first thread passes phase k: 0 tile start, 1 first K tile
+// landed, 2 K loop done, 3 LoRA up-projection done, 4 output staged in LDS, 5 stores issued.
+#ifdef WSL_STAMPS
+constexpr int kStampRecs = 4096;
+__device__ unsigned long long g_prefill_stamps[kStampRecs * 8];
+#define WSL_STAMP(rec, k)                                                                  \
+  do {                                                                                     \
+    if (threadIdx.x == 0 && (rec) < kStampRecs) g_prefill_stamps[(rec) * 8 + (k)] = wall_clock64(); \
+  } while (0)
+#else
+#define WSL_STAMP(rec, k) \
+  do {                    \
+  } while (0)
+#endif
+
 template <int BM_, int BN_, int WNW_, int NW_, int NS_ = 2>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_;
@@ -258,6 +275,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   const int tn = ((t % group_size) / gm) * SW + tq;
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
+  const int srec = (int)blockIdx.x * 4 + (tq < 3 ? tq : 3);  // phase-stamp record
+  (void)srec;
+  WSL_STAMP(srec, 0);
   // whether this tile computes T in its K loop (every tile but a strip's later ones)
   constexpr bool t_here = !PER || decltype(first)::value;
   // Grouped launch: output columns [ge_{g-1}, ge_g) are projection g, whose LoRA down
@@ -538,6 +558,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     store_w8(0);
     tn_zero(0, 0);
     ring_barrier();
+    WSL_STAMP(srec, 1);
     if (nk > 1) {
       issue(1, BK);
       load_w8(BK);
@@ -649,6 +670,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   } else if constexpr (LORA) {
     issue_b(lora_b, 0);
   }
+  WSL_STAMP(srec, 2);
 
   if constexpr (RED) {
     // This split's partials: lane-major 8-byte words (two accumulators each), the base
@@ -820,6 +842,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
 
+  WSL_STAMP(srec, 3);
   if constexpr (SPLIT) {
     // fp32 partials straight from the accumulators: lane pairs (lh) cover 8 consecutive
     // n of one row, the four groups g a whole 128-byte line, merged in L2.
@@ -869,6 +892,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
   __syncthreads();
+  WSL_STAMP(srec, 4);
   constexpr int CPR = C::BN / 8;  // 16-byte chunks per tile row
   const bool a16 = ((reinterpret_cast<uintptr_t>(y) & 15u) == 0) && ((ldy & 7) == 0);
   if (a16 && m0 + C::BM <= M && n0 + C::BN <= N) {
@@ -890,6 +914,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       const int q = i * NT + tid;
       __builtin_nontemporal_store(v[i], reinterpret_cast<u32x4_t*>(y + (int64_t)(m0 + q / CPR) * ldy + n0 + (q % CPR) * 8));
     }
+    WSL_STAMP(srec, 5);
     return;
   }
 #pragma unroll 4
@@ -910,6 +935,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       for (int e = 0; e < N - n; ++e) dst[e] = (uint16_t)(v[e >> 1] >> ((e & 1) * 16));
     }
   }
+  WSL_STAMP(srec, 5);
   };  // do_tile
 
   if constexpr (PER) {
@@ -1470,3 +1496,16 @@ hipError_t launch_prefill(const LoraArgs& p) {
 }
 
 }  // namespace wsl
+
+#ifdef WSL_STAMPS
+// Instrumented builds only: copies the first `recs` phase-stamp records (8 words each) to
+// host memory, then clears them on the device. Returns 0 or a HIP error code.
+extern "C" int wsl_prefill_stamps(unsigned long long* host, size_t recs) {
+  if (recs > (size_t)wsl::kStampRecs) recs = wsl::kStampRecs;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(host, HIP_SYMBOL(wsl::g_prefill_stamps), recs * 8 * sizeof(unsigned long long));
+  static unsigned long long zeros[wsl::kStampRecs * 8];
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(wsl::g_prefill_stamps), zeros, sizeof(zeros));
+  return (int)e;
+}
+#endif
