@@ -76,3 +76,39 @@ def test_strips_match_single_tiles_and_oracle(gpu, M, ns, K, r, monkeypatch):
         _say(f"   group {g}: max_rel_err {err:.2e} over {len(rows)} rows")
         assert np.isfinite(err) and err <= BF16_TOL
         c0 += n
+
+
+def test_strips_on_the_shared_base_form(gpu, monkeypatch):
+    """The shared-base launch (wsl::lora_linear_bcast, the reference's head sharing: one base
+    W [1024, 1024] read through the broadcast_add row map by two LoRA pairs of width 2048,
+    g = 8) at M = 8192: 512 tiles, strips of 2. Bit for bit against one tile per workgroup,
+    and against the float64 oracle of broadcast_add on sampled rows."""
+    from weightshared_torchtitan_amd import ops
+    M, N, K, r, base_n, g, G = 8192, 2048, 1024, 32, 1024, 8, 2
+    _say(f"[prefill strips, shared base] M={M} N={N} K={K} r={r} base_n={base_n} g={g} groups={G}")
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(M, K, generator=gen).bfloat16()
+    W = (torch.randn(base_n, K, generator=gen) * 0.02).bfloat16()
+    A = (torch.randn(G * r, K, generator=gen) * 0.02).bfloat16()
+    B = (torch.randn(G * N, r, generator=gen) * 0.02).bfloat16()
+
+    def run():
+        y = ops.lora_linear_bcast_op(x.to(gpu), W.to(gpu), None, A.to(gpu), B.to(gpu), 2.0, g, G)
+        torch.cuda.synchronize()
+        return y.cpu()
+
+    monkeypatch.delenv("WSL_PREFILL_STRIPS", raising=False)
+    y = run()
+    monkeypatch.setenv("WSL_PREFILL_STRIPS", "off")
+    assert torch.equal(y, run()), "strips differ from one tile per workgroup"
+    rows = sorted({min(b + o, M - 1) for b in range(0, M, 256) for o in (0, 255)})
+    xs = x[rows].float().numpy().astype("float64")
+    base = xs @ W.float().numpy().T
+    yf = y[rows].float().numpy()
+    for j in range(G):
+        delta = O.lora_delta(x[rows].float().numpy(), A[j * r:(j + 1) * r].float().numpy(),
+                             B[j * N:(j + 1) * N].float().numpy(), 2.0)
+        ref = O.broadcast_add(base, delta, dim=-1, g=g)
+        err = O.max_rel_err(yf[:, j * N:(j + 1) * N], ref)
+        _say(f"   group {j}: max_rel_err {err:.2e}")
+        assert np.isfinite(err) and err <= BF16_TOL
