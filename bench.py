@@ -417,6 +417,77 @@ def bench_stamps(dev, names=None):
             res[f"tile{q}"] = d
         out[name] = res
         del x, w, a, b
+    if names is None or any(n in names for n, *_ in DECODE_STAMP_SHAPES):
+        out.update(decode_stamps(dev, lib, names))
+    return out
+
+
+# Decode launches (config 3 shapes, r = 64) for the decode kernel's phase stamps: name, M,
+# group widths, K.
+DECODE_STAMP_SHAPES = [("c3 o M=1", 1, (2048,), 2048), ("c3 gate|up M=1", 1, (6144, 6144), 2048),
+                       ("c3 down M=1", 1, (2048,), 6144), ("c3 o M=8", 8, (2048,), 2048),
+                       ("c3 gate|up M=64", 64, (6144, 6144), 2048)]
+
+
+def decode_stamps(dev, lib, names=None, copies=6):
+    """Per-workgroup phase times of one decode launch per shape (cold weights: `copies`
+    weight sets, the first ones for the warm-up launches, the last for the stamped one),
+    in us after the launch's first workgroup start (median / max): T workgroups' T
+    published; W workgroups' W stream and cross-wave reduction done, K-split reduction done,
+    T gathered, outputs stored."""
+    import ctypes
+    import numpy as np
+    from weightshared_torchtitan_amd import ops
+    lib.wsl_decode_stamps.restype = ctypes.c_int
+    lib.wsl_decode_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    recs = 4096
+    buf = np.zeros(recs * 8, dtype=np.uint64)
+    out = {}
+    for name, M, ns, K in DECODE_STAMP_SHAPES:
+        if names is not None and name not in names:
+            continue
+        r = 64
+        g = torch.Generator(device=dev).manual_seed(M + sum(ns) + K)
+        x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        sets = []
+        for _ in range(copies):
+            sets.append(((torch.randn(sum(ns), K, device=dev, generator=g) * 0.02).bfloat16(),
+                         (torch.randn(len(ns) * r, K, device=dev, generator=g) * 0.02).bfloat16(),
+                         (torch.randn(sum(ns), r, device=dev, generator=g) * 0.02).bfloat16()))
+
+        def run(wab):
+            w, a, b = wab
+            if len(ns) > 1:
+                return ops.lora_linear_grouped_op(x, w, None, a, b, 2.0, list(ns))
+            return ops.lora_linear_op(x, w, None, a, b, 2.0)
+
+        for q in range(copies - 1):
+            run(sets[q])
+        torch.cuda.synchronize()
+        lib.wsl_decode_stamps(buf.ctypes.data, recs)  # clears the stamps
+        run(sets[-1])
+        torch.cuda.synchronize()
+        rc = lib.wsl_decode_stamps(buf.ctypes.data, recs)
+        if rc != 0:
+            raise RuntimeError(f"wsl_decode_stamps failed: {rc}")
+        st = buf.reshape(recs, 8).astype(np.int64)
+        kind = st[:, 7]
+        t0 = st[kind > 0, 0].min()
+
+        def mm(v):
+            v = (v - t0) / 100.0
+            return [round(float(np.median(v)), 2), round(float(v.max()), 2)]
+
+        tw, ww = st[kind == 1], st[kind == 2]
+        res = {"t_workgroups": int(len(tw)), "w_workgroups": int(len(ww)),
+               "start": mm(st[kind > 0, 0]),
+               "t_published": mm(tw[tw[:, 2] > 0, 2]) if (tw[:, 2] > 0).any() else None,
+               "w_stream_reduced": mm(ww[:, 1]),
+               "w_split_reduced": mm(ww[ww[:, 2] > 0, 2]) if (ww[:, 2] > 0).any() else None,
+               "w_t_gathered": mm(ww[ww[:, 3] > 0, 3]) if (ww[:, 3] > 0).any() else None,
+               "w_stored": mm(ww[ww[:, 4] > 0, 4]) if (ww[:, 4] > 0).any() else None}
+        out[name] = res
+        del sets, x
     return out
 
 

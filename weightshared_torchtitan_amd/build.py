@@ -89,21 +89,29 @@ STAMPS_LIB_PATH = os.path.join(PKG_DIR, "libwsl_stamps.so")
 
 
 def build_stamps_library(verbose: bool = False) -> str:
-    """libwsl_stamps.so: libwsl with the prefill kernel built with -DWSL_STAMPS (per-phase
-    wall-clock stamps of every workgroup, read back by ``wsl_prefill_stamps``), for
-    ``bench.py --only stamps`` run with WSL_LIB pointing at it. The other objects are the
-    ones of the last ``build_library``; the product library is left as it is."""
+    """libwsl_stamps.so: libwsl with the prefill and decode kernels built with -DWSL_STAMPS
+    (per-phase wall-clock stamps of every workgroup, read back by ``wsl_prefill_stamps`` and
+    ``wsl_decode_stamps``), for ``bench.py --only stamps`` run with WSL_LIB pointing at it.
+    The other objects are the ones of the last ``build_library``; the product library is
+    left as it is."""
     hipcc = _hipcc()
     if not os.path.exists(LIB_PATH):
         build_library(verbose=verbose)
-    src = os.path.join(CSRC, "lora_prefill.hip")
-    obj = os.path.join(BUILD_DIR, "lora_prefill_stamps.o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-DWSL_STAMPS", f"-I{INCLUDE_DIR}", f"-I{CSRC}", "-c", src, "-o", obj]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src}:\n{res.stdout}\n{res.stderr}")
+    inst = ("lora_prefill.hip", "lora_decode.hip")
+
+    def stamped(name: str) -> str:
+        src = os.path.join(CSRC, name)
+        obj = os.path.join(BUILD_DIR, name[:-4] + "_stamps.o")
+        cmd = [hipcc, *HIPCC_FLAGS, "-DWSL_STAMPS", f"-I{INCLUDE_DIR}", f"-I{CSRC}", "-c", src, "-o", obj]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n{res.stdout}\n{res.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=len(inst)) as ex:
+        stamped_objs = list(ex.map(stamped, inst))
     objs = [os.path.join(BUILD_DIR, os.path.basename(s)[:-4] + ".o") for s in sources()
-            if not s.endswith("lora_prefill.hip")] + [obj]
+            if os.path.basename(s) not in inst] + stamped_objs
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", STAMPS_LIB_PATH]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

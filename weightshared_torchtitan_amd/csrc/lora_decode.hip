@@ -79,6 +79,31 @@ constexpr uint64_t kLaunchUnit = 1ull << 20;  // C: what one launch adds to the 
 constexpr uint64_t kTagMask = (1ull << 48) - 1;
 
 constexpr int kDefaultSpin = 1 << 16;  // polls of the T counter before computing T locally
+
+// Phase timestamps, in instrumented builds only (-DWSL_STAMPS, libwsl_stamps.so): record
+// `bid` slot k gets the 100 MHz constant clock when the workgroup's first thread passes phase
+// k. T workgroups: 0 start, 1 partial sums done, 2 T published; W workgroups: 0 start, 1 W
+// stream and cross-wave reduction done, 2 K-split reduction done, 3 T gathered, 4 outputs
+// stored. Slot 7 holds 1 for a T workgroup, 2 for a W workgroup.
+#ifdef WSL_STAMPS
+constexpr int kDecStampRecs = 4096;
+__device__ unsigned long long g_decode_stamps[kDecStampRecs * 8];
+#define WSL_DSTAMP(rec, k)                                                                   \
+  do {                                                                                       \
+    if (threadIdx.x == 0 && (rec) < kDecStampRecs) g_decode_stamps[(rec) * 8 + (k)] = wall_clock64(); \
+  } while (0)
+#define WSL_DKIND(rec, v)                                                                    \
+  do {                                                                                       \
+    if (threadIdx.x == 0 && (rec) < kDecStampRecs) g_decode_stamps[(rec) * 8 + 7] = (v);     \
+  } while (0)
+#else
+#define WSL_DSTAMP(rec, k) \
+  do {                     \
+  } while (0)
+#define WSL_DKIND(rec, v) \
+  do {                    \
+  } while (0)
+#endif
 constexpr int LB = 8;                   // workspace loads a thread keeps in flight
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -738,6 +763,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
 
   if (bid < nT) {
     // ---------------- T workgroup: TROWS rows of A over one K slice
+    WSL_DSTAMP(bid, 0);
+    WSL_DKIND(bid, 1);
     const int g = bid / p.kst, ks = bid % p.kst;
     const int kbeg = ks * p.kct;
     constexpr int RED_T = (NWV - RBK) * MB * 4 * 64 * 4;
@@ -753,6 +780,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, kbeg, p.kct, p.M, smem, sums, NoPrologue{},
                                    RowMap{}, XPasses{p.x, p.ldx, p.kpt});
     }
+    WSL_DSTAMP(bid, 1);
     const uint64_t tag = late_tag();
     if (split_reduce<kBF16, TROWS, MC>(sums, p.tpart + (int64_t)g * p.kst * p.M * TROWS, ks, p.kst, p.M,
                                        ptag_of(tag), p.spin, p.a, p.lda, p.rt, g * TROWS, p.x, p.ldx,
@@ -761,9 +789,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
         const int m = q / TROWS, rl = q % TROWS, j = g * TROWS + rl;
         if (j < p.rt) st_agent(p.tfin + m * p.rt + j, (ttag_of(tag) << 16) | f32_to_bf16_bits(p.s * sums[rl * MC + m]));
       }
+      WSL_DSTAMP(bid, 2);
     }
   } else {
     // ---------------- W workgroup: 16*NR rows of W over one K slice
+    WSL_DSTAMP(bid, 0);
+    WSL_DKIND(bid, 2);
     const int yb = bid - nT;
     const int g = yb / p.ksy, ks = yb % p.ksy;
     const int kbeg = ks * p.kcy;
@@ -803,9 +834,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, kbeg, p.kcy, p.M, smem, sums, NoPrologue{}, p.wmap,
                                   XPasses{p.x, p.ldx, p.kpy});
     }
+    WSL_DSTAMP(bid, 1);
     const uint64_t tag = late_tag();
     if (split_reduce<WDT, ROWS, MC>(sums, p.ypart + (int64_t)g * p.ksy * p.M * ROWS, ks, p.ksy, p.M,
                                     ptag_of(tag), p.spin, p.w, p.ldw, p.N, row0, p.x, p.ldx, p.kcy, p.wmap)) {
+      WSL_DSTAMP(bid, 2);
       if constexpr ((FUSE & kFuseArgmax) != 0) {  // the head's greedy token: no logits written
         argmax_epilogue<ROWS, MC>(p, sums, row0, smem);
         return;
@@ -814,6 +847,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
         const int goff = ((row0 >= p.ge0) + (row0 >= p.ge1) + (row0 >= p.ge2)) * p.r;
         gather_t<MC, NORM>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
       }
+      WSL_DSTAMP(bid, 3);
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
       const int tls = p.r32 + 8;
 #pragma unroll
@@ -881,6 +915,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
           }
         }
       }
+      WSL_DSTAMP(bid, 4);
     }
   }
 }
@@ -1395,3 +1430,16 @@ hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {
 }
 
 }  // namespace wsl
+
+#ifdef WSL_STAMPS
+// Instrumented builds only: copies the first `recs` decode phase-stamp records (8 words
+// each) to host memory, then clears them on the device. Returns 0 or a HIP error code.
+extern "C" int wsl_decode_stamps(unsigned long long* host, size_t recs) {
+  if (recs > (size_t)wsl::kDecStampRecs) recs = wsl::kDecStampRecs;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(host, HIP_SYMBOL(wsl::g_decode_stamps), recs * 8 * sizeof(unsigned long long));
+  static unsigned long long zeros[wsl::kDecStampRecs * 8];
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(wsl::g_decode_stamps), zeros, sizeof(zeros));
+  return (int)e;
+}
+#endif
