@@ -307,9 +307,9 @@ AB_SHAPES = [("c2 q|k|v", 8192, (2048, 1024, 1024), 1024), ("c2 o", 8192, (1024,
 
 
 def bench_env_ab(dev, modes, names=None, launches=28, rounds=6):
-    """Side-by-side timing of path switches read at launch (WSL_PREFILL_STRIPS,
-    WSL_PREFILL_SPLIT, ...): per launch shape one HIP graph of `launches` launches is captured
-    under each mode's environment, and the graphs are replayed in alternating order over
+    """Side-by-side timing of libwsl's path overrides (ops.path_options: prefill_strips,
+    prefill_split, ...): per launch shape one HIP graph of `launches` launches is captured
+    under each mode's overrides, and the graphs are replayed in alternating order over
     `rounds` rounds (5 replays each, HIP events), so clock drift falls on every mode alike.
     Returns the median us per launch per mode."""
     from weightshared_torchtitan_amd import ops
@@ -328,17 +328,9 @@ def bench_env_ab(dev, modes, names=None, launches=28, rounds=6):
         else:
             fn = lambda: ops.lora_linear_op(x, w, None, a, b, 2.0)  # noqa: E731
         graphs = {}
-        for mode, env in modes.items():
-            saved = {k: os.environ.get(k) for k in env}
-            os.environ.update(env)
-            try:
+        for mode, opts in modes.items():
+            with ops.path_options(**opts):
                 graphs[mode] = graph_of(lambda: [fn() for _ in range(launches)])
-            finally:
-                for k, v in saved.items():
-                    if v is None:
-                        os.environ.pop(k, None)
-                    else:
-                        os.environ[k] = v
         times = {m: [] for m in modes}
         order = list(modes)
         for it in range(rounds):
@@ -544,60 +536,48 @@ def bench_medium(dev, steps, warmup):
     Qwen3-1.7B projection shapes, r = 64, cold weights (6 rotating copies), 28 layers per
     graph, grouped q|k|v and gate|up, each way the library can run them on the same inputs:
     the decode path's wide form (the default up to 72 tokens), the prefill path's in-launch
-    split-K form (WSL_DECODE_WIDE=off below 73 tokens; the default above) and its unsplit
-    tiles (also WSL_PREFILL_SPLIT=off and WSL_PREFILL_MEDIUM=off, which keep the split forms
+    split-K form (the decode_wide override at -1 below 73 tokens; the default above) and its
+    unsplit tiles (also prefill_split and prefill_medium at -1, which keep the split forms
     off); from 128 tokens also torch.matmul (hipBLASLt) on the same
     inputs: the plain GEMM on the stacked weights (no LoRA term) and the unfused three-call
     LoRA linear (the reference's arithmetic)."""
+    from weightshared_torchtitan_amd import ops
     out = {}
-    keys = ("WSL_DECODE_WIDE", "WSL_PREFILL_MEDIUM", "WSL_PREFILL_SPLIT")
-    saved = {k: os.environ.get(k) for k in keys}
     ways = (("decode", {}),
-            ("split_k", {"WSL_DECODE_WIDE": "off"}),
-            ("unsplit", {"WSL_DECODE_WIDE": "off", "WSL_PREFILL_SPLIT": "off", "WSL_PREFILL_MEDIUM": "off"}))
-    try:
-        for M in (64, 65, 72, 96, 128, 160, 192, 256, 512, 1024):
-            row = {}
-            for label, env in ways:
-                if (label == "decode" and M > 72) or (label != "decode" and M <= 64):
-                    continue  # decode runs up to 72 tokens, the prefill forms above 64
-                for k in keys:
-                    os.environ.pop(k, None)
-                os.environ.update(env)
+            ("split_k", {"decode_wide": -1}),
+            ("unsplit", {"decode_wide": -1, "prefill_split": -1, "prefill_medium": -1}))
+    for M in (64, 65, 72, 96, 128, 160, 192, 256, 512, 1024):
+        row = {}
+        for label, opts in ways:
+            if (label == "decode" and M > 72) or (label != "decode" and M <= 64):
+                continue  # decode runs up to 72 tokens, the prefill forms above 64
+            with ops.path_options(**opts):
                 st = ProjectionStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
                 st.stack_groups()
                 g = graph_of(st.run_grouped)
+            ms = time_replays(g, steps, warmup)
+            row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
+                          "TFLOP/s": round(st.flops() / ms / 1e9, 1)}
+            del g, st
+            torch.cuda.empty_cache()
+        if M >= 128:
+            st = VendorStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
+            st.stack_groups()
+            for label, fn in (("torch_plain_gemm_grouped", st.run_plain_grouped), ("torch_unfused_lora", st.run_lora)):
+                g = graph_of(fn)
                 ms = time_replays(g, steps, warmup)
-                row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
-                              "TFLOP/s": round(st.flops() / ms / 1e9, 1)}
-                del g, st
-                torch.cuda.empty_cache()
-            if M >= 128:
-                for k in keys:
-                    os.environ.pop(k, None)
-                st = VendorStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=6)
-                st.stack_groups()
-                for label, fn in (("torch_plain_gemm_grouped", st.run_plain_grouped), ("torch_unfused_lora", st.run_lora)):
-                    g = graph_of(fn)
-                    ms = time_replays(g, steps, warmup)
-                    row[label] = {"ms_per_28_layers": round(ms, 4)}
-                    del g
-                del st
-                torch.cuda.empty_cache()
-            out[f"M={M}"] = row
-    finally:
-        for k, v in saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
+                row[label] = {"ms_per_28_layers": round(ms, 4)}
+                del g
+            del st
+            torch.cuda.empty_cache()
+        out[f"M={M}"] = row
     return out
 
 
 def bench_c5_paths(dev, steps, warmup):
     """Config 5 at M = 4096 on each fp8 prefill path, same inputs: the fp8 matrix cores with
     two activation terms (the default), with one term (the opt-in WSL_DTYPE_FP8_E4M3_ACT8),
-    and W decoded onto the bf16 matrix cores (WSL_FP8_PREFILL=weight_only)."""
+    and W decoded onto the bf16 matrix cores (the fp8_prefill override at 1)."""
     from weightshared_torchtitan_amd import ops
     st = ProjectionStack(QWEN3_8B, M=4096, r=128, layers=1, dev=dev, seed=5, copies=1, fp8=True, scale=1.0)
     st.stack_groups()
@@ -605,29 +585,22 @@ def bench_c5_paths(dev, steps, warmup):
     lora = st.flops() - base
     t_min = base / (FP8_PEAK_TFLOPS * 1e12) + lora / (BF16_PEAK_TFLOPS * 1e12)
     out = {}
-    saved = (ops.FP8_ACTIVATIONS, os.environ.get("WSL_FP8_PREFILL"))
+    saved = ops.FP8_ACTIVATIONS
     try:
-        for name, act8, env in (("fp8_mfma_two_term", False, None), ("fp8_mfma_one_term", True, None),
-                                ("weight_only_bf16_mfma", False, "weight_only")):
+        for name, act8, weight_only in (("fp8_mfma_two_term", False, 0), ("fp8_mfma_one_term", True, 0),
+                                        ("weight_only_bf16_mfma", False, 1)):
             ops.FP8_ACTIVATIONS = act8
-            if env is None:
-                os.environ.pop("WSL_FP8_PREFILL", None)
-            else:
-                os.environ["WSL_FP8_PREFILL"] = env
             row = {}
             for label, fn in (("per_projection", st.run), ("grouped_qkv_gateup", st.run_grouped)):
-                g = graph_of(fn)
+                with ops.path_options(fp8_prefill=weight_only):
+                    g = graph_of(fn)
                 ms = time_replays(g, steps, warmup)
                 del g
                 row[label] = {"ms": round(ms, 4), "TFLOP/s": round(st.flops() / ms / 1e9, 1),
                               "frac_mixed_mfma_roofline": round(t_min * 1e3 / ms, 4)}
             out[name] = row
     finally:
-        ops.FP8_ACTIVATIONS = saved[0]
-        if saved[1] is None:
-            os.environ.pop("WSL_FP8_PREFILL", None)
-        else:
-            os.environ["WSL_FP8_PREFILL"] = saved[1]
+        ops.FP8_ACTIVATIONS = saved
     del st
     torch.cuda.empty_cache()
     return out
@@ -978,8 +951,8 @@ def main():
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--ab", default='{"default": {}, "strips_off": {"WSL_PREFILL_STRIPS": "off"}}',
-                    help="--only envab: JSON {mode: {ENV: value}} of the settings timed side by side")
+    ap.add_argument("--ab", default='{"default": {}, "strips_off": {"prefill_strips": -1}}',
+                    help="--only envab: JSON {mode: {option: value}} of the path overrides timed side by side")
     ap.add_argument("--ab-shapes", default=None, help="--only envab / stamps: comma-separated names from AB_SHAPES")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

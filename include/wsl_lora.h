@@ -240,6 +240,70 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
                                  void* out, int64_t ldo,
                                  void* stream);
 
+/*
+ * Path overrides. No counterpart in the reference (whose path is three aten calls with no
+ * choices to make); they exist for side-by-side timing and for tests that pin one form of a
+ * kernel against the oracle. Each option is a process-wide integer that starts at 0, the
+ * library's own choice; the host planning of every later launch reads it. Set them between
+ * calls, never while another thread is launching. Every form computes the same contract
+ * within the forward's bar; the ones marked bit-exact give identical outputs.
+ *   WSL_OPT_PREFILL_STRIPS     0 auto; -1 one output tile per workgroup (bit-exact)
+ *   WSL_OPT_PREFILL_SPLIT      0 auto; -1 never split K inside a launch; n in [2, 16] that
+ *                              split count wherever it divides the K tiles and fits
+ *   WSL_OPT_PREFILL_MEDIUM     0 auto; -1 never take the medium-M split form
+ *   WSL_OPT_FP8_PREFILL        0 fp8 matrix cores; 1 W decoded onto the bf16 matrix cores
+ *   WSL_OPT_DECODE_PASSES      0 auto; -1 K splits only; 1 passes wherever the slices allow
+ *   WSL_OPT_DECODE_WIDE        0 auto; -1 keep 65-72 tokens on the prefill path
+ *   WSL_OPT_DECODE_SPIN_LIMIT  0 the default poll bound of the decode hand-offs; n > 0 that
+ *                              bound; -1 no polling (the local fallback runs at once)
+ * wsl_set_option returns WSL_E_INVALID_ARG for an unknown option or a value out of range.
+ */
+#define WSL_OPT_PREFILL_STRIPS 1
+#define WSL_OPT_PREFILL_SPLIT 2
+#define WSL_OPT_PREFILL_MEDIUM 3
+#define WSL_OPT_FP8_PREFILL 4
+#define WSL_OPT_DECODE_PASSES 5
+#define WSL_OPT_DECODE_WIDE 6
+#define WSL_OPT_DECODE_SPIN_LIMIT 7
+#define WSL_OPT_COUNT 8
+int wsl_set_option(int32_t option, int64_t value);
+int wsl_get_option(int32_t option, int64_t* value);
+
+/*
+ * The plan a grouped (n_groups >= 1) or single call of these sizes takes, for dense,
+ * 256-byte aligned operands (pointer alignment also steers the path). No counterpart in the
+ * reference; it lets tests assert which kernel form their shapes reach. Pure host function.
+ *   path         WSL_PATH_*; WSL_PATH_NONE for M = 0
+ *   launches     calls of the main kernel (a grouped call that cannot run as one launch
+ *                runs group by group: n_groups)
+ *   tile_m/n     output tile of one workgroup on the prefill paths (of the first group's
+ *                launch when the groups run one by one), else 0
+ *   rank_blocks  32-rank blocks of T computed inside the K loop (0: none, or pre-pass T)
+ *   rank_prepass 1 when T comes from the rank pre-pass launch
+ *   strip_tiles  output tiles per workgroup of the persistent strips (1: one per workgroup)
+ *   k_splits     K splits of the split-K forms (1 otherwise)
+ *   workgroups   workgroups of the main launch on the prefill paths (first group's), else 0
+ */
+#define WSL_PATH_NONE 0
+#define WSL_PATH_PREFILL 1
+#define WSL_PATH_PREFILL_SPLITK 2
+#define WSL_PATH_PREFILL_MEDIUM 3
+#define WSL_PATH_PREFILL_FP8 4
+#define WSL_PATH_DECODE 5
+#define WSL_PATH_GENERIC 6
+typedef struct wsl_plan_info {
+  int32_t path;
+  int32_t launches;
+  int32_t tile_m, tile_n;
+  int32_t rank_blocks;
+  int32_t rank_prepass;
+  int32_t strip_tiles;
+  int32_t k_splits;
+  int32_t workgroups;
+} wsl_plan_info;
+int wsl_lora_linear_plan(int64_t M, int64_t K, int64_t r, int32_t n_groups, const int64_t* group_n,
+                         int32_t w_dtype, wsl_plan_info* out);
+
 /* Thread-local, NUL-terminated description of the last error ("" if none). */
 const char* wsl_last_error(void);
 

@@ -56,7 +56,7 @@ def test_library_exports_every_declared_symbol():
 @needs_lib
 def test_version_and_empty_error():
     lib = N.lib()
-    assert lib.wsl_version() == 100
+    assert lib.wsl_version() == 101
     sz = ctypes.c_size_t()
     assert lib.wsl_lora_linear_workspace_bytes(16, 64, 64, 8, 0, ctypes.byref(sz)) == N.WSL_OK
     assert N.last_error() == ""
@@ -482,3 +482,91 @@ def test_workspace_bytes_of_split_k_shapes(M, Nn, K, r, splits):
     if r:
         grouped = N.grouped_workspace_bytes(M, K, r, (Nn // 2, Nn // 4, Nn // 4), N.WSL_DTYPE_BF16)
         assert half(grouped) >= tiles * splits * 8 * 64 * 24 * 8
+
+
+@needs_lib
+def test_options_set_get_and_refuse():
+    """Path overrides: every option round-trips, out-of-range values and unknown options are
+    refused with WSL_E_INVALID_ARG and leave the value as it was."""
+    d = _header_defines()
+    for name, opt in N.OPTIONS.items():
+        assert d["WSL_OPT_" + name.upper()] == opt
+        assert N.get_option(name) == 0
+    try:
+        N.set_option("prefill_split", 4)
+        assert N.get_option("prefill_split") == 4
+        assert N.lib().wsl_set_option(N.OPTIONS["prefill_split"], 17) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(N.OPTIONS["prefill_strips"], 1) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], -1) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(99, 0) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(0, 0) == N.WSL_E_INVALID_ARG
+        assert N.get_option("prefill_split") == 4
+        with pytest.raises(ValueError):
+            N.set_option("decode_passes", 2)
+    finally:
+        for name in N.OPTIONS:
+            N.set_option(name, 0)
+
+
+# Config 2 (Qwen3-0.6B, M = 8192, r = 32) and the 1.7B prefill launches: the tile each takes.
+PLAN_CASES = [
+    # M, K, r, groups, path, tile (m, n), rank blocks, strip tiles, workgroups
+    (8192, 1024, 32, (2048, 1024, 1024), "prefill", (256, 256), 1, 2, 256),   # c2 q|k|v
+    (8192, 2048, 32, (1024,), "prefill", (128, 256), 1, 1, 256),              # c2 o
+    (8192, 1024, 32, (3072, 3072), "prefill", (256, 256), 1, 3, 256),         # c2 gate|up
+    (8192, 3072, 32, (1024,), "prefill", (128, 256), 1, 1, 256),              # c2 down
+    (8192, 2048, 32, (2048, 1024, 1024), "prefill", (256, 256), 1, 2, 256),   # 1.7b q|k|v
+    (8192, 2048, 32, (2048,), "prefill", (256, 256), 1, 1, 256),              # 1.7b o
+    (8192, 6144, 32, (2048,), "prefill", (256, 256), 1, 1, 256),              # 1.7b down
+    (8192, 2048, 32, (6144, 6144), "prefill", (256, 256), 1, 6, 256),         # 1.7b gate|up
+    (8192, 1024, 32, (3072,), "prefill", (256, 192), 1, 2, 256),              # c2 gate alone
+]
+
+
+@needs_lib
+@pytest.mark.parametrize("M,K,r,groups,path,tile,rb,strips,wgs", PLAN_CASES)
+def test_plan_of_benchmark_launches(M, K, r, groups, path, tile, rb, strips, wgs):
+    p = N.plan(M, K, r, groups)
+    assert p["path"] == path and (p["tile_m"], p["tile_n"]) == tile
+    assert p["rank_blocks"] == rb and p["strip_tiles"] == strips and p["workgroups"] == wgs
+    assert p["launches"] == 1 and p["k_splits"] == 1 and p["rank_prepass"] == 0
+
+
+@needs_lib
+def test_plan_follows_overrides():
+    try:
+        N.set_option("prefill_strips", -1)
+        assert N.plan(8192, 1024, 32, (2048, 1024, 1024))["strip_tiles"] == 1
+        N.set_option("prefill_strips", 0)
+        assert N.plan(256, 2048, 64, (2048,))["path"] == "prefill_splitk"
+        N.set_option("prefill_split", -1)
+        assert N.plan(256, 2048, 64, (2048,))["path"] == "prefill"
+        N.set_option("prefill_split", 2)
+        p = N.plan(256, 2048, 64, (2048,))
+        assert p["path"] == "prefill_splitk" and p["k_splits"] == 2
+    finally:
+        for name in N.OPTIONS:
+            N.set_option(name, 0)
+
+
+@needs_lib
+def test_plan_split_form_needs_group_ends_on_its_tiles():
+    """The in-launch split-K form runs 128 x 128 tiles that each compute one group's T. Group
+    ends on multiples of 192 but not 128 must not reach it as one launch: the groups then run
+    one by one (each may take the form alone); ends on multiples of 128 keep one launch."""
+    p = N.plan(256, 4096, 16, (192, 192, 192))
+    assert p["launches"] == 3
+    assert N.plan(256, 4096, 16, (192,))["path"] == "prefill_splitk"
+    p = N.plan(256, 4096, 16, (256, 128, 128))
+    assert p["launches"] == 1 and p["path"] == "prefill_splitk"
+
+
+@needs_lib
+def test_plan_paths_by_size():
+    assert N.plan(0, 1024, 16, (1024,))["path"] == "none"
+    assert N.plan(8, 2048, 64, (2048, 1024, 1024))["path"] == "decode"
+    assert N.plan(100, 1000, 16, (512,))["path"] == "generic"  # K off the 64 grid
+    p = N.plan(4096, 4096, 128, (4096,), N.WSL_DTYPE_FP8_E4M3)
+    assert p["path"] == "prefill_fp8" and p["rank_prepass"] == 1
+    p = N.plan(4096, 4096, 128, (4096,))
+    assert p["path"] == "prefill" and p["rank_prepass"] == 1 and p["rank_blocks"] == 0

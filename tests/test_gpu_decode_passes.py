@@ -1,7 +1,7 @@
 """The decode path's two ways to cover a K whose x rows do not fit the LDS at once: K split
 over several workgroups (partials handed to the last split) and the pass form (one workgroup
 walks its K range in passes, refilling x between them), and the plan's own mix of the two
-(two passes per split for an even slice count). Each form, forced with WSL_DECODE_PASSES=off
+(two passes per split for an even slice count). Each form, forced with the decode_passes override (-1 splits, 1 passes)
 / on or left to the plan (auto), against the float64 oracle (1e-2 bf16, 3e-2 fp8 base against
 fp32 W and 1e-2 against the dequantised W), bitwise repeatable, and with the T wait forced
 to its local fallback. The forms sum K in different orders, so they agree with each other
@@ -49,18 +49,18 @@ CASES = [
 ]
 
 
-def _mode(monkeypatch, mode):
-    if mode == "auto":
-        monkeypatch.delenv("WSL_DECODE_PASSES", raising=False)
-    else:
-        monkeypatch.setenv("WSL_DECODE_PASSES", mode)
+PASS_MODES = {"off": -1, "on": 1, "auto": 0}
+
+
+def _mode(wsl_opts, mode):
+    wsl_opts(decode_passes=PASS_MODES[mode])
 
 
 @pytest.mark.parametrize("mode", ["off", "on", "auto"])
 @pytest.mark.parametrize("M,N,K,r", CASES)
-def test_decode_forms_match_oracle(gpu, M, N, K, r, mode, monkeypatch):
+def test_decode_forms_match_oracle(gpu, M, N, K, r, mode, wsl_opts):
     import weightshared_torchtitan_amd as wsl
-    _mode(monkeypatch, mode)
+    _mode(wsl_opts, mode)
     _say(f"[decode {mode}] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=3 * M + N + K + r)
     d = lambda t: None if t is None else t.to(gpu)
@@ -74,7 +74,7 @@ def test_decode_forms_match_oracle(gpu, M, N, K, r, mode, monkeypatch):
     assert np.isfinite(err) and err <= BF16_TOL
 
 
-def test_override_reaches_the_plan(gpu, monkeypatch):
+def test_override_reaches_the_plan(gpu, wsl_opts):
     """The two forms sum K in different orders, so at a six-slice shape their outputs differ
     in some elements (both within the bar above): the override switched the kernel's form."""
     import weightshared_torchtitan_amd as wsl
@@ -82,7 +82,7 @@ def test_override_reaches_the_plan(gpu, monkeypatch):
     x, W, A, B = (t.to(gpu) for t in _inputs(M, N, K, r, seed=43))
     ys = {}
     for mode in ("off", "on"):
-        monkeypatch.setenv("WSL_DECODE_PASSES", mode)
+        wsl_opts(decode_passes=PASS_MODES[mode])
         ys[mode] = wsl.lora_linear(x, W, A, B, 2.0)
     torch.cuda.synchronize()
     assert not torch.equal(ys["off"], ys["on"])
@@ -90,11 +90,11 @@ def test_override_reaches_the_plan(gpu, monkeypatch):
 
 
 @pytest.mark.parametrize("mode", ["off", "on", "auto"])
-def test_decode_forms_grouped(gpu, mode, monkeypatch):
+def test_decode_forms_grouped(gpu, mode, wsl_opts):
     """gate|up and q|k|v of Qwen3-1.7B at M = 64 as grouped launches; every group's block
     against the oracle."""
     from weightshared_torchtitan_amd import ops
-    _mode(monkeypatch, mode)
+    _mode(wsl_opts, mode)
     M, K, r = 64, 2048, 64
     for group_n in ((6144, 6144), (2048, 1024, 1024)):
         _say(f"[decode grouped {mode}] M={M} K={K} r={r} groups={group_n}")
@@ -115,29 +115,29 @@ def test_decode_forms_grouped(gpu, mode, monkeypatch):
 
 
 @pytest.mark.parametrize("mode", ["on", "auto"])
-def test_pass_form_t_fallback(gpu, mode, monkeypatch):
+def test_pass_form_t_fallback(gpu, mode, wsl_opts):
     """The pass forms with the T wait bound forced to zero from the host: the W workgroups
     compute T themselves, within the bar."""
     import weightshared_torchtitan_amd as wsl
-    _mode(monkeypatch, mode)
+    _mode(wsl_opts, mode)
     M, N, K, r = 64, 2048, 6144, 64
     _say(f"[decode pass T fallback] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=41)
     d = lambda t: t.to(gpu)
-    monkeypatch.setenv("WSL_DECODE_SPIN_LIMIT", "0")
+    wsl_opts(decode_spin_limit=-1)
     y = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0).float().cpu().numpy()
     torch.cuda.synchronize()
-    monkeypatch.delenv("WSL_DECODE_SPIN_LIMIT")
+    wsl_opts(decode_spin_limit=0)
     ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), 2.0)
     assert O.max_rel_err(y, ref) <= BF16_TOL
 
 
 @pytest.mark.parametrize("mode", ["off", "on"])
-def test_decode_forms_fp8(gpu, mode, monkeypatch):
+def test_decode_forms_fp8(gpu, mode, wsl_opts):
     """Config 5's down projection at M = 16 (fp8 base, K = 12288: three x slices)."""
     import weightshared_torchtitan_amd as wsl
     from weightshared_torchtitan_amd import quantize_fp8_per_channel
-    monkeypatch.setenv("WSL_DECODE_PASSES", mode)
+    wsl_opts(decode_passes=PASS_MODES[mode])
     M, N, K, r = 16, 4096, 12288, 128
     _say(f"[decode fp8 {mode}] M={M} N={N} K={K} r={r}")
     g = torch.Generator().manual_seed(5)
@@ -155,14 +155,14 @@ def test_decode_forms_fp8(gpu, mode, monkeypatch):
     assert err_dq <= BF16_TOL
 
 
-def test_split_partials_are_consumed(gpu, monkeypatch):
+def test_split_partials_are_consumed(gpu, wsl_opts):
     """After split-form launches (T and W split six ways) the workspace past the counter
     prefix holds no partial-sum word (bit 63 clear, tag bits set): the last split takes
     each word, so none can meet a launch whose 31-bit tag repeats its own. T words (bit 63
     set) stay, as their readers are many."""
     import ctypes
     from weightshared_torchtitan_amd import _native as N
-    monkeypatch.setenv("WSL_DECODE_PASSES", "off")
+    wsl_opts(decode_passes=-1)
     M, N_, K, r = 64, 2048, 6144, 64
     _say(f"[decode split partials consumed] M={M} N={N_} K={K} r={r}")
     x, W, A, B = (t.to(gpu) for t in _inputs(M, N_, K, r, seed=47))

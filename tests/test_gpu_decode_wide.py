@@ -2,7 +2,7 @@
 waves along K, x walked in pass slices of 512 or 1024 columns, the slices spread over the K
 splits that keep one wave of workgroups. Against the float64 oracle (1e-2), bitwise
 repeatable, with the T wait forced to its local fallback, beside the prefill path
-(WSL_DECODE_WIDE=off) on the same inputs, and as grouped launches. The K split count
+(the decode_wide override at -1) on the same inputs, and as grouped launches. The K split count
 fills one wave of workgroups, so it depends on N: a grouped launch may sum a group's rows in
 another order than the group's single launch, and the two agree within the bar (below 65
 tokens they agree bit for bit)."""
@@ -48,9 +48,9 @@ CASES = [
 
 
 @pytest.mark.parametrize("M,N,K,r", CASES)
-def test_wide_decode_matches_oracle(gpu, M, N, K, r, monkeypatch):
+def test_wide_decode_matches_oracle(gpu, M, N, K, r, wsl_opts):
     import weightshared_torchtitan_amd as wsl
-    monkeypatch.delenv("WSL_DECODE_WIDE", raising=False)
+    wsl_opts(decode_wide=0)
     _say(f"[decode wide] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=5 * M + N + K + r)
     d = lambda t: None if t is None else t.to(gpu)
@@ -63,24 +63,24 @@ def test_wide_decode_matches_oracle(gpu, M, N, K, r, monkeypatch):
     _say(f"  max_rel_err={err:.3e}")
     assert np.isfinite(err) and err <= BF16_TOL
     # the medium form of the prefill path on the same inputs: same bar, a different kernel
-    monkeypatch.setenv("WSL_DECODE_WIDE", "off")
+    wsl_opts(decode_wide=-1)
     y3 = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0)
     torch.cuda.synchronize()
     assert O.max_rel_err(y3.float().cpu().numpy(), ref) <= BF16_TOL
 
 
-def test_wide_decode_t_fallback(gpu, monkeypatch):
+def test_wide_decode_t_fallback(gpu, wsl_opts):
     """T wait bound forced to zero from the host: the W workgroups compute T themselves."""
     import weightshared_torchtitan_amd as wsl
-    monkeypatch.delenv("WSL_DECODE_WIDE", raising=False)
+    wsl_opts(decode_wide=0)
     M, N, K, r = 72, 2048, 6144, 64
     _say(f"[decode wide T fallback] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=53)
     d = lambda t: t.to(gpu)
-    monkeypatch.setenv("WSL_DECODE_SPIN_LIMIT", "0")
+    wsl_opts(decode_spin_limit=-1)
     y = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0).float().cpu().numpy()
     torch.cuda.synchronize()
-    monkeypatch.delenv("WSL_DECODE_SPIN_LIMIT")
+    wsl_opts(decode_spin_limit=0)
     ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), 2.0)
     assert O.max_rel_err(y, ref) <= BF16_TOL
 
@@ -91,10 +91,10 @@ def test_wide_decode_t_fallback(gpu, monkeypatch):
     (72, 6144, (2048, 2048)),
     (65, 1024, (3072, 3072, 1024)),
 ])
-def test_wide_decode_grouped_matches_single(gpu, M, K, group_n, monkeypatch):
+def test_wide_decode_grouped_matches_single(gpu, M, K, group_n, wsl_opts):
     import weightshared_torchtitan_amd as wsl
     from weightshared_torchtitan_amd import ops
-    monkeypatch.delenv("WSL_DECODE_WIDE", raising=False)
+    wsl_opts(decode_wide=0)
     r = 64
     _say(f"[decode wide grouped] M={M} K={K} r={r} groups={group_n}")
     g = torch.Generator().manual_seed(M + K + len(group_n))

@@ -152,7 +152,7 @@ def test_grouped_backward(gpu, M, K, r, group_n):
         assert err <= BF16_TOL, (name, err)
 
 
-def test_grouped_decode_t_wait_fallback(gpu, monkeypatch):
+def test_grouped_decode_t_wait_fallback(gpu, wsl_opts):
     """With the T poll bound at zero every W workgroup computes its group's T columns
     itself from x and the stacked A (the fallback reads rows g*r.. of a): same bits as
     the published path."""
@@ -163,7 +163,7 @@ def test_grouped_decode_t_wait_fallback(gpu, monkeypatch):
     args = [t.to(gpu) for t in (x, torch.cat(Ws).bfloat16(), torch.cat(As), torch.cat(Bs))]
     y0 = ops.lora_linear_grouped_op(args[0], args[1], None, args[2], args[3], 2.0, list(group_n))
     torch.cuda.synchronize()
-    monkeypatch.setenv("WSL_DECODE_SPIN_LIMIT", "0")
+    wsl_opts(decode_spin_limit=-1)
     y1 = ops.lora_linear_grouped_op(args[0], args[1], None, args[2], args[3], 2.0, list(group_n))
     torch.cuda.synchronize()
     assert torch.equal(y0, y1)

@@ -442,7 +442,7 @@ def test_workspace_growth_refused_during_capture(gpu):
 
 
 @pytest.mark.parametrize("M,N,K,r", [(1, 2048, 2048, 64), (40, 1000, 6144, 24)])
-def test_decode_t_wait_fallback(gpu, M, N, K, r, monkeypatch):
+def test_decode_t_wait_fallback(gpu, M, N, K, r, wsl_opts):
     """With the T wait bound forced to zero from the host, every W workgroup computes T
     itself: the result stays within tolerance and the counters still return to zero."""
     import weightshared_torchtitan_amd as wsl
@@ -450,10 +450,10 @@ def test_decode_t_wait_fallback(gpu, M, N, K, r, monkeypatch):
     x, W, A, B = _inputs(M, N, K, r, seed=29)
     xg, Wg, Ag, Bg = (t.to(gpu) for t in (x, W, A, B))
     normal = wsl.lora_linear(xg, Wg, Ag, Bg, 2.0).float()
-    monkeypatch.setenv("WSL_DECODE_SPIN_LIMIT", "0")
+    wsl_opts(decode_spin_limit=-1)
     forced = wsl.lora_linear(xg, Wg, Ag, Bg, 2.0).float()
     torch.cuda.synchronize()
-    monkeypatch.delenv("WSL_DECODE_SPIN_LIMIT")
+    wsl_opts(decode_spin_limit=0)
     ref = O.lora_linear(_np(x), _np(W), _np(A), _np(B), 2.0)
     assert O.max_rel_err(forced.cpu().numpy(), ref) <= BF16_TOL
     assert ((forced - normal).abs().max() / normal.abs().max()).item() < 1e-2

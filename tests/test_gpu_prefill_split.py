@@ -4,7 +4,7 @@ runs the fused K loop (T included) over its part and leaves fp32 partial records
 split that arrives last at the tile's counter sums them in split order and finishes the
 tile. Checked against the float64 oracle (bar max|y - y_ref| / max|y_ref| <= 1e-2), bitwise
 repeatable (the sum does not depend on which split arrives last), at forced split counts
-(WSL_PREFILL_SPLIT) against the unsplit tiles (WSL_PREFILL_SPLIT=off; another summation
+(the prefill_split override) against the unsplit tiles (prefill_split at -1; another summation
 order, so within the bar), in graph replays, with shapes of different tile counts sharing
 one workspace, and with every arrival counter back at zero after the launches."""
 import ctypes
@@ -39,11 +39,11 @@ def _np(t):
     return None if t is None else t.float().numpy()
 
 
-def _mode(monkeypatch, mode):
+def _mode(wsl_opts, mode):
     if mode is None:
-        monkeypatch.delenv("WSL_PREFILL_SPLIT", raising=False)
+        wsl_opts(prefill_split=0)
     else:
-        monkeypatch.setenv("WSL_PREFILL_SPLIT", str(mode))
+        wsl_opts(prefill_split=-1 if mode == "off" else int(mode))
 
 
 CASES = [
@@ -59,9 +59,9 @@ CASES = [
 
 
 @pytest.mark.parametrize("M,N,K,r", CASES)
-def test_split_form_matches_oracle(gpu, M, N, K, r, monkeypatch):
+def test_split_form_matches_oracle(gpu, M, N, K, r, wsl_opts):
     import weightshared_torchtitan_amd as wsl
-    _mode(monkeypatch, None)
+    _mode(wsl_opts, None)
     _say(f"[prefill split] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=7 * M + N + K + r)
     d = lambda t: None if t is None else t.to(gpu)
@@ -74,21 +74,21 @@ def test_split_form_matches_oracle(gpu, M, N, K, r, monkeypatch):
     _say(f"   max_rel_err {err:.2e}")
     assert np.isfinite(err) and err <= BF16_TOL
     # the unsplit tiles on the same inputs: the same bar, another order of the K sum
-    _mode(monkeypatch, "off")
+    _mode(wsl_opts, "off")
     y3 = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0)
     torch.cuda.synchronize()
     assert O.max_rel_err(y3.float().cpu().numpy(), ref) <= BF16_TOL
 
 
 @pytest.mark.parametrize("splits", [2, 4, 8, 16])
-def test_forced_split_counts(gpu, splits, monkeypatch):
+def test_forced_split_counts(gpu, splits, wsl_opts):
     """Every split count the form takes, on one shape (32 K tiles), against the oracle;
     the counts sum K in different orders, so they agree with each other to the bar."""
     import weightshared_torchtitan_amd as wsl
     M, N, K, r = 160, 640, 2048, 64
     _say(f"[prefill split forced] S={splits} M={M} N={N} K={K} r={r}")
     x, W, A, B = (t.to(gpu) for t in _inputs(M, N, K, r, seed=splits))
-    _mode(monkeypatch, splits)
+    _mode(wsl_opts, splits)
     y = wsl.lora_linear(x, W, A, B, 2.0)
     y2 = wsl.lora_linear(x, W, A, B, 2.0)
     torch.cuda.synchronize()
@@ -102,12 +102,12 @@ def test_forced_split_counts(gpu, splits, monkeypatch):
     (150, 2048, 32, (3072, 3072)),        # gate|up: the grouped launch splits in two, each group alone in four
     (300, 1024, 8, (1024, 512, 512)),
 ])
-def test_split_form_grouped(gpu, M, K, r, group_n, monkeypatch):
+def test_split_form_grouped(gpu, M, K, r, group_n, wsl_opts):
     """A grouped launch runs whole; its split count follows its own tiles, so each group
     agrees with its single call within the bar, and with the oracle."""
     import weightshared_torchtitan_amd as wsl
     from weightshared_torchtitan_amd import ops
-    _mode(monkeypatch, None)
+    _mode(wsl_opts, None)
     _say(f"[prefill split grouped] M={M} K={K} r={r} groups={group_n}")
     g = torch.Generator().manual_seed(M + K + r)
     x = torch.randn(M, K, generator=g).bfloat16().to(gpu)
@@ -129,11 +129,11 @@ def test_split_form_grouped(gpu, M, K, r, group_n, monkeypatch):
         n0 += n
 
 
-def test_split_form_graph_replays(gpu, monkeypatch):
+def test_split_form_graph_replays(gpu, wsl_opts):
     """Captured once and replayed with eager work between the replays: every replay equals
     the eager launch (the counters the replays leave behind start the next one at zero)."""
     import weightshared_torchtitan_amd as wsl
-    _mode(monkeypatch, None)
+    _mode(wsl_opts, None)
     M, N, K, r = 256, 2048, 2048, 64
     _say(f"[prefill split graph] M={M} N={N} K={K} r={r}")
     x, W, A, B = (t.to(gpu) for t in _inputs(M, N, K, r, seed=11))
@@ -156,12 +156,12 @@ def test_split_form_graph_replays(gpu, monkeypatch):
         assert other.shape == (200, N)
 
 
-def test_split_counters_return_to_zero(gpu, monkeypatch):
+def test_split_counters_return_to_zero(gpu, wsl_opts):
     """Launches of two tile counts and split counts through one workspace, through the C ABI:
     the arrival counters in the workspace prefix are all zero afterwards, and each output
     equals its launch on a fresh workspace."""
     from weightshared_torchtitan_amd import _native as N_
-    _mode(monkeypatch, None)
+    _mode(wsl_opts, None)
     shapes = [(256, 2048, 2048, 64), (160, 1024, 6144, 32), (256, 2048, 2048, 64)]
     nb = max(N_.workspace_bytes(M, N, K, r, N_.WSL_DTYPE_BF16) for M, N, K, r in shapes)
     ws = torch.zeros(nb // 8, dtype=torch.int64, device=gpu)
@@ -190,11 +190,11 @@ def test_split_counters_return_to_zero(gpu, monkeypatch):
     (200, 16, 512, 0), (200, 100, 64, 0), (200, 1000, 128, 0), (130, 640, 192, 0), (256, 256, 256, 8),
     (300, 384, 320, 16), (129, 2048, 2048, 64), (512, 512, 4096, 40), (24 * 8, 16, 1024, 0),
 ])
-def test_deep_ring_unsplit(gpu, M, N, K, r, monkeypatch):
+def test_deep_ring_unsplit(gpu, M, N, K, r, wsl_opts):
     """The 128 x 128 tile's four-buffer ring (no more tiles than CUs) without the K split,
     every K tile count from one up: against the oracle."""
     import weightshared_torchtitan_amd as wsl
-    _mode(monkeypatch, "off")
+    _mode(wsl_opts, "off")
     _say(f"[deep ring] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=M * 3 + N + K + r)
     d = lambda t: None if t is None else t.to(gpu)

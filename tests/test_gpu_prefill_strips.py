@@ -2,7 +2,7 @@
 waves over the 256 CUs, 256 workgroups each run k consecutive column tiles of one row block
 (one group), and T = bf16(s x A^T), which depends only on the row block and the group, is
 computed in the strip's first K loop and reused by the rest. The arithmetic is that of one
-tile per workgroup, so the outputs are compared bit for bit with WSL_PREFILL_STRIPS=off, and
+tile per workgroup, so the outputs are compared bit for bit with the prefill_strips override at -1, and
 against the float64 oracle on rows sampled from every row block (rows are independent; bar
 max|y - y_ref| / max|y_ref| <= 1e-2)."""
 import sys
@@ -56,12 +56,12 @@ def _run(gpu, x, W, A, B, ns):
 
 
 @pytest.mark.parametrize("M,ns,K,r", CASES)
-def test_strips_match_single_tiles_and_oracle(gpu, M, ns, K, r, monkeypatch):
+def test_strips_match_single_tiles_and_oracle(gpu, M, ns, K, r, wsl_opts):
     _say(f"[prefill strips] M={M} groups={ns} K={K} r={r}")
     x, W, A, B = _inputs(M, ns, K, r, seed=M + sum(ns) + K + r)
-    monkeypatch.delenv("WSL_PREFILL_STRIPS", raising=False)
+    wsl_opts(prefill_strips=0)
     y = _run(gpu, x, W, A, B, ns)
-    monkeypatch.setenv("WSL_PREFILL_STRIPS", "off")
+    wsl_opts(prefill_strips=-1)
     y_off = _run(gpu, x, W, A, B, ns)
     assert torch.equal(y, y_off), "strips differ from one tile per workgroup"
     # oracle on 3 rows of every 128-row block (first, middle, last row present)
@@ -78,7 +78,7 @@ def test_strips_match_single_tiles_and_oracle(gpu, M, ns, K, r, monkeypatch):
         c0 += n
 
 
-def test_strips_on_the_shared_base_form(gpu, monkeypatch):
+def test_strips_on_the_shared_base_form(gpu, wsl_opts):
     """The shared-base launch (wsl::lora_linear_bcast, the reference's head sharing: one base
     W [1024, 1024] read through the broadcast_add row map by two LoRA pairs of width 2048,
     g = 8) at M = 8192: 512 tiles, strips of 2. Bit for bit against one tile per workgroup,
@@ -97,9 +97,9 @@ def test_strips_on_the_shared_base_form(gpu, monkeypatch):
         torch.cuda.synchronize()
         return y.cpu()
 
-    monkeypatch.delenv("WSL_PREFILL_STRIPS", raising=False)
+    wsl_opts(prefill_strips=0)
     y = run()
-    monkeypatch.setenv("WSL_PREFILL_STRIPS", "off")
+    wsl_opts(prefill_strips=-1)
     assert torch.equal(y, run()), "strips differ from one tile per workgroup"
     rows = sorted({min(b + o, M - 1) for b in range(0, M, 256) for o in (0, 255)})
     xs = x[rows].float().numpy().astype("float64")

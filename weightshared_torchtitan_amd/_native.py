@@ -50,6 +50,9 @@ EXPORTED = (
     "wsl_factorized_embedding_fwd",
     "wsl_last_error",
     "wsl_version",
+    "wsl_set_option",
+    "wsl_get_option",
+    "wsl_lora_linear_plan",
     "wsl_rmsnorm_fwd",
     "wsl_qk_norm_rope_fwd",
     "wsl_decode_attention_workspace_bytes",
@@ -78,9 +81,37 @@ class WSLError(RuntimeError):
     """A libwsl call failed on the device side (workspace, device, launch)."""
 
 
+# Path overrides (WSL_OPT_* in include/wsl_lora.h) by name; 0 is the library's own choice.
+OPTIONS = {
+    "prefill_strips": 1,     # -1: one output tile per workgroup
+    "prefill_split": 2,      # -1: no split-K inside a launch; 2..16: that split count
+    "prefill_medium": 3,     # -1: never the medium-M split form
+    "fp8_prefill": 4,        # 1: fp8 W decoded onto the bf16 matrix cores
+    "decode_passes": 5,      # -1: K splits only; 1: passes wherever the slices allow
+    "decode_wide": 6,        # -1: 65-72 tokens on the prefill path
+    "decode_spin_limit": 7,  # n > 0: poll bound of the decode hand-offs; -1: no polling
+}
+
+# wsl_plan_info.path values
+PATHS = {0: "none", 1: "prefill", 2: "prefill_splitk", 3: "prefill_medium", 4: "prefill_fp8", 5: "decode",
+         6: "generic"}
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("path", "launches", "tile_m", "tile_n", "rank_blocks",
+                                               "rank_prepass", "strip_tiles", "k_splits", "workgroups")]
+
+
 def _declare(lib: ctypes.CDLL) -> None:
     lib.wsl_version.restype = ctypes.c_int
     lib.wsl_version.argtypes = []
+    lib.wsl_set_option.restype = ctypes.c_int
+    lib.wsl_set_option.argtypes = [ctypes.c_int32, _c_i64]
+    lib.wsl_get_option.restype = ctypes.c_int
+    lib.wsl_get_option.argtypes = [ctypes.c_int32, ctypes.POINTER(_c_i64)]
+    lib.wsl_lora_linear_plan.restype = ctypes.c_int
+    lib.wsl_lora_linear_plan.argtypes = [_c_i64, _c_i64, _c_i64, ctypes.c_int32, ctypes.POINTER(_c_i64),
+                                         ctypes.c_int32, ctypes.POINTER(PlanInfo)]
     lib.wsl_last_error.restype = ctypes.c_char_p
     lib.wsl_last_error.argtypes = []
     lib.wsl_lora_linear_workspace_bytes.restype = ctypes.c_int
@@ -290,3 +321,25 @@ def bwd_weights_workspace_bytes(M: int, N: int, K: int, r: int) -> int:
     check(lib().wsl_lora_linear_bwd_weights_workspace_bytes(M, N, K, r, ctypes.byref(out)),
           "wsl_lora_linear_bwd_weights_workspace_bytes")
     return int(out.value)
+
+
+def set_option(name: str, value: int) -> None:
+    """Sets a path override (see OPTIONS); 0 restores the library's own choice."""
+    check(lib().wsl_set_option(OPTIONS[name], int(value)), f"wsl_set_option({name})")
+
+
+def get_option(name: str) -> int:
+    out = _c_i64(0)
+    check(lib().wsl_get_option(OPTIONS[name], ctypes.byref(out)), f"wsl_get_option({name})")
+    return int(out.value)
+
+
+def plan(M: int, K: int, r: int, group_n, w_dtype: int = WSL_DTYPE_BF16) -> dict:
+    """The plan a call of these sizes takes (dense, aligned operands): a dict of the
+    wsl_plan_info fields, with `path` by name."""
+    info = PlanInfo()
+    check(lib().wsl_lora_linear_plan(M, K, r, len(group_n), group_array(group_n), w_dtype, ctypes.byref(info)),
+          "wsl_lora_linear_plan")
+    out = {n: int(getattr(info, n)) for n, _ in PlanInfo._fields_}
+    out["path"] = PATHS[out["path"]]
+    return out

@@ -474,10 +474,12 @@ __device__ __forceinline__ bool split_reduce(float* sums, uint64_t* part, int ks
   // The words of SC splits are requested together (one memory round trip for up to SC
   // splits, where one split at a time cost a round trip each: M = 64, K = 6144 has six
   // splits); they are still added in split order. Each word is taken (exchanged with zero)
-  // rather than loaded, so no partial outlives its launch: the 31-bit tag repeats after
-  // 2^31 - 1 launches, and a word left in a region no later launch rewrote could otherwise
-  // match a launch that far ahead. Zero matches no tag; a word taken before its writer
-  // stored it is polled again.
+  // rather than loaded, so a partial does not outlive its launch: the 31-bit tag repeats
+  // after 2^31 - 1 launches, and a word left in a region no later launch rewrote could
+  // otherwise match a launch that far ahead. Zero matches no tag; a word taken before its
+  // writer stored it is polled again. One exception: when the poll bound runs out the
+  // reducer recomputes that split locally (direct_partial), and the late writer's word then
+  // lands after the last take and stays in the workspace, tagged with this launch.
   constexpr int SC = 4;
   for (int q0 = 0; q0 < n; q0 += LB * DT) {
     float v[LB];
@@ -992,16 +994,13 @@ double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
 // fused kernels are built for (one token block).
 enum class Pick { kAll, kFused };
 
-// WSL_DECODE_PASSES: "off" keeps K splits, "on" walks every split slice in passes (one
-// workgroup per row group), anything else the measured rule of plan_decode (read per call:
-// a benchmark or test can switch it).
+// WSL_OPT_DECODE_PASSES: -1 keeps K splits, 1 walks every split slice in passes (one
+// workgroup per row group), 0 the measured rule of plan_decode (read per call: a benchmark
+// or test can switch it).
 enum class PassMode { kAuto, kOff, kOn };
 PassMode pass_mode() {
-  const char* e = std::getenv("WSL_DECODE_PASSES");
-  if (e == nullptr) return PassMode::kAuto;
-  if (std::strcmp(e, "off") == 0) return PassMode::kOff;
-  if (std::strcmp(e, "on") == 0) return PassMode::kOn;
-  return PassMode::kAuto;
+  const int64_t v = option(WSL_OPT_DECODE_PASSES);
+  return v < 0 ? PassMode::kOff : v > 0 ? PassMode::kOn : PassMode::kAuto;
 }
 
 // rt: rank rows of the T work (groups * r for a grouped launch; r when negative).
@@ -1256,13 +1255,12 @@ hipError_t dispatch(const DecodeArgs& a, int mb, int nr, int kw, int grid, size_
 
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
-// Poll bound of the T wait; WSL_DECODE_SPIN_LIMIT overrides it (a test uses 0 to run the
-// local fallback).
+// Poll bound of the hand-off waits; WSL_OPT_DECODE_SPIN_LIMIT overrides it (a test uses -1,
+// no polling, to run the local fallback).
 int spin_limit() {
-  const char* e = std::getenv("WSL_DECODE_SPIN_LIMIT");
-  if (e == nullptr || *e == 0) return kDefaultSpin;
-  const long v = std::strtol(e, nullptr, 10);
-  return v < 0 ? 0 : (v > (1L << 30) ? (1 << 30) : (int)v);
+  const int64_t v = option(WSL_OPT_DECODE_SPIN_LIMIT);
+  if (v == 0) return kDefaultSpin;
+  return v < 0 ? 0 : (int)v;
 }
 
 }  // namespace
@@ -1271,10 +1269,8 @@ bool decode_supported(const LoraArgs& p) {
   if (p.M < 1 || p.M > kDecodePlainMaxM) return false;
   if (p.M > kDecodeMaxM) {
     if (p.w_dtype != kBF16) return false;  // fp8 base above 64 tokens: the prefill path
-    // WSL_DECODE_WIDE=off keeps 65-72 tokens on the prefill path (read per call, for
-    // side-by-side timing)
-    const char* e = std::getenv("WSL_DECODE_WIDE");
-    if (e != nullptr && std::strcmp(e, "off") == 0) return false;
+    // WSL_OPT_DECODE_WIDE = -1 keeps 65-72 tokens on the prefill path (side-by-side timing)
+    if (option(WSL_OPT_DECODE_WIDE) < 0) return false;
   }
   if (p.w == nullptr) return false;  // the delta-only form runs on the prefill path
   if (p.N > (int64_t)1 << 30 || p.K > (int64_t)1 << 30) return false;

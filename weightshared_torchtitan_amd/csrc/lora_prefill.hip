@@ -991,10 +991,9 @@ hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int sp
 // workgroup). Strips are taken where the tiles are a whole number k >= 2 of waves over the
 // 256 CUs: 256 workgroups then run k tiles each, and T, computed in the first, costs one
 // tile's rank MFMAs instead of k. A strip stays in one row of tiles and one group.
-// WSL_PREFILL_STRIPS=off keeps one tile per workgroup (side-by-side timing).
+// WSL_OPT_PREFILL_STRIPS = -1 keeps one tile per workgroup (side-by-side timing).
 int strip_tiles(const LoraArgs& p, int bm, int bn) {
-  const char* env = std::getenv("WSL_PREFILL_STRIPS");
-  if (env != nullptr && std::strcmp(env, "off") == 0) return 1;
+  if (option(WSL_OPT_PREFILL_STRIPS) < 0) return 1;
   const int64_t tiles_m = (p.M + bm - 1) / bm, tiles_n = (p.N + bn - 1) / bn;
   const int64_t tiles = tiles_m * tiles_n;
   if (tiles < 512 || tiles % 256 != 0) return 1;
@@ -1005,13 +1004,14 @@ int strip_tiles(const LoraArgs& p, int bm, int bn) {
   return (int)k;
 }
 
-// One tile configuration's launch: persistent strips where strip_tiles takes them (bf16 W
-// with T computed in the kernel, two-buffer ring), else one tile per workgroup.
+// One tile configuration's launch: persistent strips of `strips` tiles (bf16 W with T
+// computed in the kernel, two-buffer ring), or one tile per workgroup.
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
-hipError_t launch_tiles(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+hipError_t launch_tiles(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int strips) {
   if constexpr (WDT == kBF16 && HAS_W && RB > 0 && !EXT_T && !GATHER && C::NS == 2) {
-    const int k = strip_tiles(p, C::BM, C::BN);
-    if (k > 1) return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, true>(p, tg, ldt, 1, nullptr, nullptr, k);
+    if (strips > 1)
+      return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, true>(p, tg, ldt, 1, nullptr, nullptr,
+                                                                                     strips);
   }
   return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
 }
@@ -1027,7 +1027,8 @@ double wave_efficiency(int64_t tiles) {
 // 128 x 128 on a full chip: 0.81 of 256 x 256 at M = N = 8192, K = 4096, 0.75 at
 // M = N = K = 4096; it wins where the larger tiles leave CUs idle (M = 4096, N = 1024:
 // 256 tiles against 128 of 128 x 256, 642 against 552 TFLOP/s).
-enum class Tile { kBig, kMid, kTall, kSmall };
+// kDeep is the 128 x 128 tile on the four-buffer ring.
+enum class Tile { kBig, kMid, kTall, kSmall, kDeep };
 // A grouped launch only considers configurations whose tile width divides every group
 // boundary (one of 256 and 128 always does: prefill_groups_supported checks it).
 Tile choose_tile(const LoraArgs& p) {
@@ -1042,36 +1043,59 @@ Tile choose_tile(const LoraArgs& p) {
   return tall > big ? Tile::kTall : Tile::kBig;
 }
 
-// 128 x 128 tiles: with at most one workgroup per CU (no more tiles than CUs) the deep ring,
-// else two workgroups per CU on the two-buffer ring (they hide each other's fills).
-template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
-hipError_t launch_small(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
-  if constexpr (WDT == kBF16 && !GATHER) {
-    if (((p.M + 127) / 128) * ((p.N + 127) / 128) <= 256) return launch_cfg<CfgDeep, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+int tile_rows(Tile t) { return (t == Tile::kBig || t == Tile::kMid) ? 256 : 128; }
+int tile_cols(Tile t) { return t == Tile::kMid ? 192 : (t == Tile::kSmall || t == Tile::kDeep) ? 128 : 256; }
+
+// The tile loop's configuration for a launch of the K loop with RB in-loop rank blocks
+// (ext_t: T from the pre-pass), and its persistent strip length.
+struct TilePick {
+  Tile tile;
+  int strips;
+};
+TilePick pick_tiles(const LoraArgs& p, int wdt, bool has_w, int rb, bool ext_t, bool gather) {
+  TilePick t{Tile::kBig, 1};
+  if (rb == 2) {
+    // Ranks 33-64 (two rank blocks) use 128 x 256, whose 64 x 64 wave tile leaves registers
+    // for the second block's T accumulators beside the base accumulators, or 128 x 128 (one
+    // rank block per wave) where the wider tiles would leave more CUs idle.
+    const int64_t tm = (p.M + 127) / 128;
+    const double tall = wave_efficiency(tm * ((p.N + 255) / 256)) * 0.85;  // groups fit 256 (checked)
+    const double small = wave_efficiency(tm * ((p.N + 127) / 128)) * 0.75;
+    t.tile = small > tall ? Tile::kSmall : Tile::kTall;
+  } else {
+    t.tile = choose_tile(p);
   }
-  return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+  // 128 x 128 tiles: with at most one workgroup per CU (no more tiles than CUs) the deep
+  // ring, else two workgroups per CU on the two-buffer ring (they hide each other's fills).
+  if (t.tile == Tile::kSmall && wdt == kBF16 && !gather && ((p.M + 127) / 128) * ((p.N + 127) / 128) <= 256)
+    t.tile = Tile::kDeep;
+  if (wdt == kBF16 && has_w && rb > 0 && !ext_t && !gather && t.tile != Tile::kSmall && t.tile != Tile::kDeep)
+    t.strips = strip_tiles(p, tile_rows(t.tile), tile_cols(t.tile));
+  return t;
 }
 
 template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER = false>
 hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
-  // Ranks 33-64 (two rank blocks) use 128 x 256, whose 64 x 64 wave tile leaves registers
-  // for the second block's T accumulators beside the base accumulators, or 128 x 128 (one
-  // rank block per wave) where the wider tiles would leave more CUs idle.
+  const TilePick t = pick_tiles(p, WDT, HAS_W, RB, EXT_T, GATHER);
+  if constexpr (WDT == kBF16 && !GATHER) {
+    if (t.tile == Tile::kDeep) return launch_cfg<CfgDeep, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+  }
   if constexpr (RB == 2) {
-    const int64_t tm = (p.M + 127) / 128;
-    const double tall = wave_efficiency(tm * ((p.N + 255) / 256)) * 0.85;  // groups fit 256 (checked)
-    const double small = wave_efficiency(tm * ((p.N + 127) / 128)) * 0.75;
-    if (small > tall) return launch_small<WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-    return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    if (t.tile == Tile::kTall) return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
+    return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
   } else {
-    switch (choose_tile(p)) {
-      case Tile::kMid: return launch_tiles<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-      case Tile::kTall: return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-      case Tile::kSmall: return launch_small<WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-      default: return launch_tiles<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    switch (t.tile) {
+      case Tile::kMid: return launch_tiles<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
+      case Tile::kTall: return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
+      case Tile::kSmall:
+      case Tile::kDeep: return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+      default: return launch_tiles<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
     }
   }
 }
+
+// In-loop rank blocks of a launch of rank r (0 above RIN: T from the pre-pass).
+int rank_blocks_of(int64_t r) { return r == 0 ? 0 : r <= 32 ? 1 : r <= RIN ? 2 : 0; }
 
 template <int WDT, bool HAS_W>
 hipError_t launch_rank(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
@@ -1117,6 +1141,8 @@ rank_reduce_kernel(const float* __restrict__ part, int splits, int64_t slice, fl
 
 }  // namespace
 
+bool groups_fit_tiles(const LoraArgs& p, int bn) { return groups_fit(p, bn); }
+
 // A grouped launch needs the prefill path and group ends that whole tiles of one of the
 // configurations its rank takes respect (ranks 33-64 run only on 256-wide tiles).
 bool prefill_groups_supported(const LoraArgs& p) {
@@ -1157,12 +1183,10 @@ size_t rank_prepass_bytes(int64_t M, int64_t K, int64_t rt) {
 
 namespace {
 // Which path an fp8 W takes on prefill shapes: the fp8 matrix cores (activation terms per
-// p.fp8_terms) unless WSL_FP8_PREFILL=weight_only asks for W decoded onto the bf16 matrix
-// cores (kept for side-by-side measurement).
+// p.fp8_terms) unless WSL_OPT_FP8_PREFILL = 1 asks for W decoded onto the bf16 matrix cores
+// (kept for side-by-side measurement).
 bool fp8_matrix_cores(const LoraArgs& p) {
-  const char* e = std::getenv("WSL_FP8_PREFILL");  // read per call: a benchmark can switch it
-  const bool weight_only = e != nullptr && std::strcmp(e, "weight_only") == 0;
-  return !weight_only && p.fp8_terms > 0 && prefill_fp8_supported(p);
+  return option(WSL_OPT_FP8_PREFILL) != 1 && p.fp8_terms > 0 && prefill_fp8_supported(p);
 }
 }  // namespace
 
@@ -1183,8 +1207,7 @@ constexpr size_t kMediumPartBytes = (size_t)24 << 20;  // with T, within the no-
 int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool has_w, bool gather) {
   if (!has_w || gather || w_dtype != kBF16 || M > kMediumMaxM || M < 1) return 0;
   if (rt > 256) return 0;  // the combine kernel stages 32 rows of T (all rt ranks) in LDS
-  const char* env = std::getenv("WSL_PREFILL_MEDIUM");  // "off": the unsplit tiles, for side-by-side timing
-  if (env != nullptr && std::strcmp(env, "off") == 0) return 0;
+  if (option(WSL_OPT_PREFILL_MEDIUM) < 0) return 0;  // the unsplit tiles, for side-by-side timing
   const int64_t nk = K / BK;
   // Since the 128 x 128 tiles' deep ring, the unsplit tiles win below 64 K tiles (rank 128:
   // 100 x 2048 x 2048 27.6 against 30.9 us, 160 x 6144 x 2048 30.6 against 41.6; rank 96,
@@ -1221,13 +1244,10 @@ int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool ga
   const int64_t nk = K / BK;
   const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
   if (tiles > kRedMaxTiles) return 0;
-  const char* env = std::getenv("WSL_PREFILL_SPLIT");  // "off", or a forced split count (side-by-side timing)
-  if (env != nullptr) {
-    if (std::strcmp(env, "off") == 0) return 0;
-    const int f = std::atoi(env);
-    if (f >= 2 && f <= kRedMaxSplits && nk % f == 0 && (size_t)(tiles * f) * red_record_bytes(true) <= kRedPartBytes)
-      return f;
-  }
+  const int64_t f = option(WSL_OPT_PREFILL_SPLIT);  // off, or a forced split count (side-by-side timing)
+  if (f < 0) return 0;
+  if (f >= 2 && f <= kRedMaxSplits && nk % f == 0 && (size_t)(tiles * f) * red_record_bytes(true) <= kRedPartBytes)
+    return (int)f;
   // At 97-128 tiles the unsplit launch already covers half the CUs: splitting in two paid
   // only over long K (M x N x K = 1024 x 2048 x 6144: 52.4 against 62.8 us; 2048 x 1024 x
   // 1024: 18.1 against 14.1, 1024 x 2048 x 2048: 27.0 against 25.6, 512 x 4096 x 2048: 26.7
@@ -1458,6 +1478,57 @@ hipError_t launch_product_tn(const LoraArgs& p, int64_t tokens, float* part, int
   return launch_cfg<CfgSmall, kBF16, true, 0, false, false, true, true>(q, nullptr, 0, splits);
 }
 
+// The form, tile and splits a prefill call takes; launch_prefill follows it.
+PrefillPlan plan_prefill(const LoraArgs& p) {
+  PrefillPlan pl;
+  pl.form = WSL_PATH_PREFILL;
+  const bool has_w = p.w != nullptr;
+  const int64_t rt = p.r * p.groups;
+  const int64_t tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (p.gather != nullptr) {
+    // factorized embedding: gathered x rows, bf16 base, no LoRA term
+    const TilePick t = pick_tiles(p, kBF16, true, 0, false, true);
+    pl.tile_m = tile_rows(t.tile);
+    pl.tile_n = tile_cols(t.tile);
+  } else if (has_w && p.w_dtype == kFP8 && fp8_matrix_cores(p)) {
+    pl.form = WSL_PATH_PREFILL_FP8;
+    pl.prepass = p.r > 0;
+    pl.tile_m = pl.tile_n = 256;
+  } else {
+    // The in-launch split-K form runs 128 x 128 tiles that compute their group's T, so every
+    // group end must fall on a tile boundary.
+    const int rs = (has_w && p.w_dtype == kBF16 && p.r <= RIN && p.red_cnt != nullptr && groups_fit(p, 128))
+                       ? red_splits(p.M, p.N, p.K, p.w_dtype, true, false)
+                       : 0;
+    const int ms = (rs == 0 && has_w && p.w_dtype == kBF16) ? medium_splits(p.M, p.N, p.K, rt, p.w_dtype, true, false)
+                                                             : 0;
+    if (rs > 0) {
+      pl.form = WSL_PATH_PREFILL_SPLITK;
+      pl.tile_m = pl.tile_n = 128;
+      pl.rank_blocks = rank_blocks_of(p.r);
+      pl.splits = rs;
+      pl.workgroups = tiles128 * rs;
+      return pl;
+    }
+    if (ms > 0) {
+      pl.form = WSL_PATH_PREFILL_MEDIUM;
+      pl.tile_m = pl.tile_n = 128;
+      pl.prepass = p.r > 0;
+      pl.splits = ms;
+      pl.workgroups = tiles128 * ms;
+      return pl;
+    }
+    pl.prepass = p.r > RIN;
+    pl.rank_blocks = rank_blocks_of(p.r);
+    const TilePick t = pick_tiles(p, has_w ? (int)p.w_dtype : kBF16, has_w, pl.rank_blocks, pl.prepass, false);
+    pl.tile_m = tile_rows(t.tile);
+    pl.tile_n = tile_cols(t.tile);
+    pl.strips = t.strips;
+  }
+  pl.workgroups = ((p.M + pl.tile_m - 1) / pl.tile_m) * ((p.N + pl.tile_n - 1) / pl.tile_n) / pl.strips;
+  return pl;
+}
+
 hipError_t launch_prefill(const LoraArgs& p) {
   if (p.gather != nullptr) {
     // factorized embedding: gathered x rows, bf16 base, no LoRA term
@@ -1466,7 +1537,8 @@ hipError_t launch_prefill(const LoraArgs& p) {
   const bool has_w = p.w != nullptr;
   const int64_t rt = p.r * p.groups;
   uint16_t* t = reinterpret_cast<uint16_t*>(p.ws);
-  if (has_w && p.w_dtype == kFP8 && fp8_matrix_cores(p)) {
+  const PrefillPlan pl = plan_prefill(p);
+  if (pl.form == WSL_PATH_PREFILL_FP8) {
     if (p.r > 0) {
       const hipError_t e = rank_prepass(p, t);
       if (e != hipSuccess) return e;
@@ -1474,14 +1546,8 @@ hipError_t launch_prefill(const LoraArgs& p) {
     char* codes = reinterpret_cast<char*>(p.ws) + (p.r > 0 ? rank_prepass_bytes(p.M, p.K, rt) : 0);
     return launch_prefill_fp8(p, p.r > 0 ? t : nullptr, rt, codes, p.fp8_terms);
   }
-  if (has_w && p.w_dtype == kBF16 && p.r <= RIN && p.red_cnt != nullptr) {
-    const int rs = red_splits(p.M, p.N, p.K, p.w_dtype, true, false);
-    if (rs > 0) return launch_red(p, rs);
-  }
-  if (has_w && p.w_dtype == kBF16) {
-    const int ms = medium_splits(p.M, p.N, p.K, rt, p.w_dtype, true, false);
-    if (ms > 0) return launch_medium(p, ms);
-  }
+  if (pl.form == WSL_PATH_PREFILL_SPLITK) return launch_red(p, pl.splits);
+  if (pl.form == WSL_PATH_PREFILL_MEDIUM) return launch_medium(p, pl.splits);
   const uint16_t* tg = nullptr;
   int64_t ldt = 0;
   if (p.r > RIN) {

@@ -4,12 +4,24 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 
 #include "../../include/wsl_decode.h"
 #include "../../include/wsl_lora.h"
 #include "wsl_common.h"
+
+namespace wsl {
+namespace {
+// WSL_OPT_* values (include/wsl_lora.h), 0 = the library's own choice.
+std::atomic<int64_t> g_options[WSL_OPT_COUNT];
+}  // namespace
+
+int64_t option(int id) {
+  return (id > 0 && id < WSL_OPT_COUNT) ? g_options[id].load(std::memory_order_relaxed) : 0;
+}
+}  // namespace wsl
 
 namespace {
 
@@ -262,6 +274,34 @@ int run_call(wsl::LoraArgs p, void* workspace, size_t workspace_bytes) {
   return WSL_OK;
 }
 
+// Whether a validated grouped call (p.groups, p.gend set) runs as one launch of its path;
+// otherwise its groups run one by one.
+bool grouped_one_launch(const wsl::LoraArgs& p) {
+  if (p.groups == 1 || p.r == 0) return true;
+  const Path path = choose_path(p);
+  if (path == Path::kDecode) return wsl::decode_groups_supported(p);
+  if (path != Path::kPrefill) return false;
+  // The prefill path's medium-M split form must be taken (with the same split count) by the
+  // grouped launch exactly when each group alone takes it, so the groups' outputs stay those
+  // of the single calls bit for bit; otherwise the groups go one by one. A grouped launch
+  // that takes the in-launch split-K form runs whole: its split count follows the launch's
+  // tiles, so a group may sum K in another order than its single call (within the bar). That
+  // form's 128 x 128 tiles compute their group's T, so its group ends must fall on multiples
+  // of 128; where they do not, the groups go one by one (each may still take the form).
+  const auto medium = [&](int64_t n, int64_t rt) {
+    if (p.r <= 64 && wsl::red_splits(p.M, n, p.K, p.w_dtype, p.w != nullptr, false) > 0) return 0;
+    return wsl::medium_splits(p.M, n, p.K, rt, p.w_dtype, p.w != nullptr, false);
+  };
+  const bool red_shape = p.r <= 64 && wsl::red_splits(p.M, p.N, p.K, p.w_dtype, p.w != nullptr, false) > 0;
+  if (red_shape) return wsl::groups_fit_tiles(p, 128) && wsl::prefill_groups_supported(p);
+  const int ms = medium(p.N, p.r * p.groups);
+  for (int g = 0; g < p.groups; ++g) {
+    const int64_t n = p.gend[g] - (g > 0 ? p.gend[g - 1] : 0);
+    if (medium(n, p.r) != ms) return false;
+  }
+  return wsl::prefill_groups_supported(p);
+}
+
 // A grouped call after validation: one launch when the path's grid respects the group
 // ends, else one launch per group in order on the same stream (the workspace is reused
 // stream-ordered). With `shared_base` every group reads the same W (and w_scale) rows
@@ -275,28 +315,7 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
     p.groups = 1;
     return run_call(p, workspace, workspace_bytes);
   }
-  const Path path = choose_path(p);
-  // The prefill path's medium-M split form must be taken (with the same split count) by the
-  // grouped launch exactly when each group alone takes it, so the groups' outputs stay those
-  // of the single calls bit for bit; otherwise the groups go one by one. A grouped launch
-  // that takes the in-launch split-K form runs whole: its split count follows the launch's
-  // tiles, so a group may sum K in another order than its single call (within the bar).
-  bool medium_agrees = true;
-  // the medium split form's count for `n` columns of rank rt, 0 where it is not taken (the
-  // in-launch split-K form comes first for ranks up to 64)
-  const auto medium = [&](int64_t n, int64_t rt) {
-    if (p.r <= 64 && wsl::red_splits(p.M, n, p.K, p.w_dtype, p.w != nullptr, false) > 0) return 0;
-    return wsl::medium_splits(p.M, n, p.K, rt, p.w_dtype, p.w != nullptr, false);
-  };
-  const bool red = path == Path::kPrefill && p.r <= 64 &&
-                   wsl::red_splits(p.M, p.N, p.K, p.w_dtype, p.w != nullptr, false) > 0;
-  if (path == Path::kPrefill && !red) {
-    const int ms = medium(p.N, p.r * n_groups);
-    for (int g = 0; g < n_groups; ++g) medium_agrees = medium_agrees && medium(group_n[g], p.r) == ms;
-  }
-  if ((path == Path::kPrefill && medium_agrees && wsl::prefill_groups_supported(p)) ||
-      (path == Path::kDecode && wsl::decode_groups_supported(p)))
-    return run_call(p, workspace, workspace_bytes);
+  if (grouped_one_launch(p)) return run_call(p, workspace, workspace_bytes);
   const int64_t wbytes = (p.w_dtype == WSL_DTYPE_FP8_E4M3) ? 1 : 2;
   int64_t n0 = 0;
   for (int g = 0; g < n_groups; ++g) {
@@ -321,7 +340,82 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
 
 extern "C" {
 
-int wsl_version(void) { return 100; }
+int wsl_version(void) { return 101; }
+
+int wsl_set_option(int32_t option, int64_t value) {
+  clear_err();
+  bool ok;
+  switch (option) {
+    case WSL_OPT_PREFILL_STRIPS:
+    case WSL_OPT_PREFILL_MEDIUM:
+    case WSL_OPT_DECODE_WIDE: ok = value == 0 || value == -1; break;
+    case WSL_OPT_PREFILL_SPLIT: ok = value == 0 || value == -1 || (value >= 2 && value <= 16); break;
+    case WSL_OPT_FP8_PREFILL: ok = value == 0 || value == 1; break;
+    case WSL_OPT_DECODE_PASSES: ok = value >= -1 && value <= 1; break;
+    case WSL_OPT_DECODE_SPIN_LIMIT: ok = value >= -1 && value <= ((int64_t)1 << 30); break;
+    default: return fail(WSL_E_INVALID_ARG, "unknown option %d", (int)option);
+  }
+  if (!ok) return fail(WSL_E_INVALID_ARG, "value %lld out of range for option %d", (long long)value, (int)option);
+  wsl::g_options[option].store(value, std::memory_order_relaxed);
+  return WSL_OK;
+}
+
+int wsl_get_option(int32_t option, int64_t* value) {
+  clear_err();
+  if (value == nullptr) return fail(WSL_E_INVALID_ARG, "value must not be NULL");
+  if (option < 1 || option >= WSL_OPT_COUNT) return fail(WSL_E_INVALID_ARG, "unknown option %d", (int)option);
+  *value = wsl::option(option);
+  return WSL_OK;
+}
+
+int wsl_lora_linear_plan(int64_t M, int64_t K, int64_t r, int32_t n_groups, const int64_t* group_n,
+                         int32_t w_dtype_in, wsl_plan_info* out) {
+  clear_err();
+  if (out == nullptr) return fail(WSL_E_INVALID_ARG, "out must not be NULL");
+  int terms;
+  const int32_t w_dtype = kernel_dtype(w_dtype_in, &terms);
+  int64_t N = 0;
+  int rc = validate_groups(n_groups, group_n, &N);
+  if (rc != WSL_OK) return rc;
+  rc = validate_sizes(M, N, K, r, w_dtype);
+  if (rc != WSL_OK) return rc;
+  std::memset(out, 0, sizeof(*out));
+  // dense, 256-byte aligned stand-ins for the operands (only their alignment is read)
+  const void* al = reinterpret_cast<const void*>((uintptr_t)256);
+  wsl::LoraArgs p = make_args(al, K, al, K, w_dtype, w_dtype == WSL_DTYPE_FP8_E4M3 ? reinterpret_cast<const float*>(al)
+                                                                                    : nullptr,
+                              al, K, al, r, 2.f, const_cast<void*>(al), N, M, N, K, r, nullptr);
+  p.fp8_terms = terms;
+  p.red_cnt = reinterpret_cast<unsigned*>(const_cast<void*>(al));
+  p.groups = n_groups;
+  int64_t end = 0;
+  for (int g = 0; g < n_groups; ++g) p.gend[g] = (end += group_n[g]);
+  if (n_groups == 1 || r == 0) p.groups = 1;
+  if (choose_path(p) == Path::kNone) return WSL_OK;
+  out->launches = 1;
+  if (!grouped_one_launch(p)) {  // group by group: the first group's plan
+    out->launches = n_groups;
+    p.groups = 1;
+    p.N = group_n[0];
+  }
+  out->strip_tiles = out->k_splits = 1;
+  switch (choose_path(p)) {
+    case Path::kDecode: out->path = WSL_PATH_DECODE; break;
+    case Path::kGeneric: out->path = WSL_PATH_GENERIC; break;
+    default: {
+      const wsl::PrefillPlan pl = wsl::plan_prefill(p);
+      out->path = pl.form;
+      out->tile_m = pl.tile_m;
+      out->tile_n = pl.tile_n;
+      out->rank_blocks = pl.rank_blocks;
+      out->rank_prepass = pl.prepass ? 1 : 0;
+      out->strip_tiles = pl.strips;
+      out->k_splits = pl.splits;
+      out->workgroups = (int32_t)pl.workgroups;
+    }
+  }
+  return WSL_OK;
+}
 
 const char* wsl_last_error(void) { return g_err; }
 

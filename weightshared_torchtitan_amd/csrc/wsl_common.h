@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "wsl_lora.h"
+
 namespace wsl {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
@@ -144,11 +146,30 @@ struct LoraArgs {
   unsigned* red_cnt = nullptr;
 };
 
+// Path overrides (WSL_OPT_* of include/wsl_lora.h): 0 unless wsl_set_option changed them.
+int64_t option(int id);
+
+// The prefill path's choice for a call (csrc/lora_prefill.hip), shared by the launcher and
+// wsl_lora_linear_plan: form (WSL_PATH_PREFILL*), tile, in-loop rank blocks, pre-pass T,
+// persistent strip length, K splits and the main launch's workgroups.
+struct PrefillPlan {
+  int form = 0;
+  int tile_m = 0, tile_n = 0;
+  int rank_blocks = 0;
+  bool prepass = false;
+  int strips = 1;
+  int splits = 1;
+  int64_t workgroups = 0;
+};
+PrefillPlan plan_prefill(const LoraArgs& p);
+
 // Each launcher returns hipSuccess or the launch error.
 hipError_t launch_prefill(const LoraArgs& p);
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype);
 bool prefill_supported(const LoraArgs& p);
 bool prefill_groups_supported(const LoraArgs& p);
+// Whether every group end of a grouped launch falls on a multiple of bn columns.
+bool groups_fit_tiles(const LoraArgs& p, int bn);
 // K splits of the medium-M split form of the prefill path (0: not taken); rt = r * groups.
 int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool has_w, bool gather);
 // K splits of the prefill path's in-launch split-K form over 128 x 128 tiles (0: not taken;
