@@ -14,6 +14,7 @@ from __future__ import annotations
 from typing import Optional
 
 import collections
+import contextlib
 import ctypes
 import os
 
@@ -29,6 +30,28 @@ _FP8 = torch.float8_e4m3fn
 # an error of about 3.7e-2 against the fp32-weight reference at config-5 shapes, above the
 # 3e-2 bar the default keeps (2.4-2.6e-2).
 FP8_ACTIVATIONS = os.environ.get("WSL_FP8_ACTIVATIONS", "") not in ("", "0")
+
+
+@contextlib.contextmanager
+def path_options(**opts: int):
+    """Forces kernel forms for the duration of the block through libwsl's path overrides
+    (``_native.OPTIONS``: e.g. ``prefill_strips=-1``, ``prefill_split=4``,
+    ``decode_passes=1``), restoring the previous values on exit. The overrides are
+    process-wide; use them for side-by-side timing and tests, not in concurrent code."""
+    saved = {k: _native.get_option(k) for k in opts}
+    try:
+        for k, v in opts.items():
+            _native.set_option(k, v)
+        yield
+    finally:
+        for k, v in saved.items():
+            _native.set_option(k, v)
+
+
+def plan(M: int, K: int, r: int, group_n, fp8: bool = False) -> dict:
+    """The kernel plan libwsl takes for a (grouped) LoRA linear of these sizes on dense,
+    aligned operands: path, launches, tile, in-loop rank blocks, pre-pass, strips, K splits."""
+    return _native.plan(M, K, r, list(group_n), _fp8_code() if fp8 else _native.WSL_DTYPE_BF16)
 
 
 def _fp8_code() -> int:
@@ -75,6 +98,9 @@ _retired: list = []
 
 
 def _retire(key) -> None:
+    """Replaces the workspace of `key` after a failed kernel launch (WSL_E_LAUNCH), which may
+    leave its counters mid-update. Argument, shape and workspace errors return before any
+    launch and keep the buffer."""
     buf = _workspaces.pop(key, None)
     if buf is not None:
         _retired.append(buf)
@@ -167,7 +193,7 @@ def lora_linear_op(x: torch.Tensor, w: Optional[torch.Tensor], w_scale: Optional
                 y.data_ptr(), y.stride(0),
                 M, N, K, r,
                 ws.data_ptr(), ws.numel(), stream)
-        if rc != _native.WSL_OK:
+        if rc == _native.WSL_E_LAUNCH:
             _retire((dev.index, stream, "lora"))  # a failed launch may leave counters mid-update
         _native.check(rc, "wsl_lora_linear_fwd")
     return y.reshape(*lead, N)
@@ -186,7 +212,21 @@ _WT_CACHE: "collections.OrderedDict" = collections.OrderedDict()
 _WT_CACHE_MAX = 16
 
 
+def _has_storage(t: torch.Tensor) -> bool:
+    """False for the fake, functional and meta tensors of tracing (torch.compile, AOT
+    autograd, meta-device init), whose data pointers do not exist."""
+    if t.device.type == "meta":
+        return False
+    try:
+        t.data_ptr()
+    except RuntimeError:
+        return False
+    return True
+
+
 def _transposed(w: torch.Tensor) -> torch.Tensor:
+    if not _has_storage(w) or torch.compiler.is_compiling():
+        return w.t().contiguous()  # traced: a plain transpose in the graph, no cache
     key = (w.data_ptr(), tuple(w.shape), tuple(w.stride()), w.dtype, w.device)
     hit = _WT_CACHE.get(key)
     if hit is not None and hit[1] == w._version:
@@ -404,7 +444,7 @@ def lora_linear_grouped_op(x: torch.Tensor, w: torch.Tensor, w_scale: Optional[t
                 y.data_ptr(), y.stride(0),
                 M, K, r, G, gn,
                 ws.data_ptr(), ws.numel(), stream)
-        if rc != _native.WSL_OK:
+        if rc == _native.WSL_E_LAUNCH:
             _retire((dev.index, stream, "lora"))
         _native.check(rc, "wsl_lora_linear_grouped_fwd")
     return y.reshape(*lead, N)
@@ -472,7 +512,7 @@ def lora_linear_bcast_op(x: torch.Tensor, w: torch.Tensor, w_scale: Optional[tor
                 _dev_ptr(a), a.stride(0) if a is not None else 0, _dev_ptr(b), b.stride(0) if b is not None else 0,
                 float(scale), y.data_ptr(), y.stride(0), M, N, K, r, base_n, int(g), G,
                 ws.data_ptr(), ws.numel(), stream)
-        if rc != _native.WSL_OK:
+        if rc == _native.WSL_E_LAUNCH:
             _retire((dev.index, stream, "lora"))
         _native.check(rc, "wsl_lora_linear_bcast_fwd")
     return y.reshape(*lead, G * N)
@@ -524,8 +564,12 @@ def _lora_linear_bcast_backward(ctx, gy):
     if need_x:
         wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous() if w.dtype == _FP8 else _transposed(w)
         dx = lora_linear_op(gyb, wt, None, None, None, 0.0)
-        if has_lora:
+        if has_lora and G * r <= _native.WSL_MAX_RANK:
             dx = dx + lora_linear_op(gy2, None, None, bd.t().contiguous(), a.t().contiguous(), s)
+        elif has_lora:  # G*r above the kernels' rank limit: one delta launch per group, summed
+            for j in range(G):
+                dx = dx + lora_linear_op(gy2[:, j * N:(j + 1) * N], None, None, b[j * N:(j + 1) * N].t().contiguous(),
+                                         a[j * r:(j + 1) * r].t().contiguous(), s)
         dx = dx.reshape(x.shape)
     dw, _, _ = weight_grads(x2, gyb, None, None, s, need_w and w.dtype == torch.bfloat16, False, False)
     if has_lora and (need_a or need_b):
@@ -928,7 +972,7 @@ def argmax_rows_op(x: torch.Tensor) -> torch.Tensor:
     with torch.cuda.device(dev):
         rc = lib.wsl_argmax_rows_fwd(x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1], out.data_ptr(),
                                      ws.data_ptr(), ws.numel(), stream)
-    if rc != 0:
+    if rc == _native.WSL_E_LAUNCH:
         _retire((dev.index, stream, "argmax"))  # a failed launch may leave keys set
     _native.check(rc, "wsl_argmax_rows_fwd", decode=True)
     return out.view(x.shape[:-1])
@@ -966,7 +1010,7 @@ def decode_attention_step_op(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w
             q2.data_ptr(), q2.stride(0), b, n_heads, n_kv_heads, hd, qw.data_ptr(), kw.data_ptr(), float(eps),
             rope.data_ptr(), pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), L, float(scale),
             out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
-    if rc != _native.WSL_OK:
+    if rc == _native.WSL_E_LAUNCH:
         _retire((dev.index, stream, "attention"))
     _native.check(rc, "wsl_decode_attention_step_fwd", decode=True)
     return out
@@ -1003,7 +1047,7 @@ def tied_head_argmax_op(z: torch.Tensor, emb: torch.Tensor) -> torch.Tensor:
     with torch.cuda.device(dev):
         rc = lib.wsl_tied_head_argmax_fwd(z2.data_ptr(), z2.stride(0), emb.data_ptr(), emb.stride(0), V, K, M,
                                           out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
-    if rc != _native.WSL_OK:
+    if rc == _native.WSL_E_LAUNCH:
         _retire((dev.index, stream, "head_argmax"))  # a failed launch may leave keys set
     _native.check(rc, "wsl_tied_head_argmax_fwd")
     return out
@@ -1047,7 +1091,7 @@ def lora_linear_fused_op(x: torch.Tensor, norm_w: Optional[torch.Tensor], eps: f
             _dev_ptr(a), a.stride(0) if a is not None else 0, _dev_ptr(b), b.stride(0) if b is not None else 0,
             float(scale), _dev_ptr(res), res.stride(0) if res is not None else 0, y.data_ptr(), y.stride(0),
             M, N, K, r, int(fuse), ws.data_ptr(), ws.numel(), stream)
-    if rc != _native.WSL_OK:
+    if rc == _native.WSL_E_LAUNCH:
         _retire((dev.index, stream, "lora"))
     _native.check(rc, "wsl_lora_linear_fused_fwd")
     return y
