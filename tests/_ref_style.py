@@ -41,17 +41,19 @@ class RefSharedAttention(nn.Module):
     """The projection part of the reference's Attention with its sharing switches: base widths
     as its constructor sets them (torchtitan/models/llama3/model/model.py:218-273: one base per
     qkv_sharing group named str(group), GQA off under qkv_sharing; g = grouping templates under
-    head_sharing; k/v bases g / n_rep templates wide) and the composition of its forward
-    (:376-398: every projection is broadcast_add(base, offset, g=self.grouping)). Returns
-    (xq, xk, xv)."""
+    head_sharing; k/v bases g / n_rep templates wide), the two_step offsets (:275-300: one
+    head_offset as wide as q, and per-projection w{q,k,v}_only_offset one head wide) and the
+    composition of its forward (:366-398: under two_step each offset is
+    broadcast_add(w<p>_only_offset(x), head_offset(x)).contiguous(); every projection is
+    broadcast_add(base, offset, g=self.grouping)). Returns (xq, xk, xv)."""
 
     def __init__(self, dim=512, n_heads=16, n_kv_heads=8, rank=8, head_sharing=False, grouping=1,
-                 qkv_sharing=None):
+                 qkv_sharing=None, two_step=False):
         super().__init__()
         self.n_heads, self.n_kv_heads = n_heads, n_kv_heads
         self.qkv_sharing, self.head_sharing = qkv_sharing, head_sharing
         self.grouping = grouping if grouping else 1
-        self.two_step = False
+        self.two_step = two_step
         self.head_dim = dim // n_heads
         self.n_rep = n_heads // n_kv_heads
         if qkv_sharing:
@@ -65,12 +67,27 @@ class RefSharedAttention(nn.Module):
             self.wq_base = nn.Linear(dim, self.head_dim * dim_mult, bias=False)
             self.wk_base = nn.Linear(dim, self.head_dim * kv_dim_mult, bias=False)
             self.wv_base = nn.Linear(dim, self.head_dim * kv_dim_mult, bias=False)
-        self.wq_offset = RefLoRA(dim, n_heads * self.head_dim, rank)
-        self.wk_offset = RefLoRA(dim, self.n_kv_heads * self.head_dim, rank)
-        self.wv_offset = RefLoRA(dim, self.n_kv_heads * self.head_dim, rank)
+        if two_step:
+            self.head_offset = RefLoRA(dim, n_heads * self.head_dim, rank)
+            self.wq_only_offset = RefLoRA(dim, self.head_dim, rank)
+            self.wk_only_offset = RefLoRA(dim, self.head_dim, rank)
+            self.wv_only_offset = RefLoRA(dim, self.head_dim, rank)
+        else:
+            self.wq_offset = RefLoRA(dim, n_heads * self.head_dim, rank)
+            self.wk_offset = RefLoRA(dim, self.n_kv_heads * self.head_dim, rank)
+            self.wv_offset = RefLoRA(dim, self.n_kv_heads * self.head_dim, rank)
 
     def forward(self, x):
-        wq_offset, wk_offset, wv_offset = self.wq_offset(x), self.wk_offset(x), self.wv_offset(x)
+        if self.two_step:
+            head_offset = self.head_offset(x)
+            wq_only_offset = self.wq_only_offset(x)
+            wk_only_offset = self.wk_only_offset(x)
+            wv_only_offset = self.wv_only_offset(x)
+            wq_offset = broadcast_add(wq_only_offset, head_offset).contiguous()
+            wk_offset = broadcast_add(wk_only_offset, head_offset).contiguous()
+            wv_offset = broadcast_add(wv_only_offset, head_offset).contiguous()
+        else:
+            wq_offset, wk_offset, wv_offset = self.wq_offset(x), self.wk_offset(x), self.wv_offset(x)
         if self.qkv_sharing:
             for grp in self.qkv_sharing:
                 val = getattr(self, str(grp))(x)

@@ -53,6 +53,10 @@ SHARING_MODES = [
     ("qkv_sharing [q,k,v]", dict(qkv_sharing=[["q", "k", "v"]])),
     ("qkv_sharing [q,k],[v] + head_sharing g=4", dict(qkv_sharing=[["q", "k"], ["v"]], head_sharing=True,
                                                        grouping=4)),
+    ("two_step", dict(two_step=True)),
+    ("two_step + qkv_sharing [q,k,v]", dict(two_step=True, qkv_sharing=[["q", "k", "v"]])),
+    ("two_step + qkv_sharing [q,k],[v] + head_sharing g=4", dict(two_step=True, qkv_sharing=[["q", "k"], ["v"]],
+                                                                   head_sharing=True, grouping=4)),
 ]
 
 
@@ -80,7 +84,8 @@ def test_sharing_modes_match_reference_forward_and_backward(gpu, mode, kw, M):
     model = copy.deepcopy(ref).to(gpu)
     conv = C.WslLoRAConverter()
     conv.convert(model)
-    assert len(conv.fused) == 3
+    assert len(conv.fused) == (4 if kw.get("two_step") else 3)  # two_step: head_offset and 3 only-offsets
+    assert conv.converted == []
     xg = x.to(gpu).requires_grad_(True)
     outs = model(xg)
     torch.autograd.backward(list(outs), [g.to(gpu) for g in grads])
@@ -98,6 +103,8 @@ def test_sharing_modes_match_reference_forward_and_backward(gpu, mode, kw, M):
 @pytest.mark.parametrize("mode,kw,launches", [
     ("head_sharing g=2", dict(head_sharing=True, grouping=2), 3),
     ("qkv_sharing [q,k,v]", dict(qkv_sharing=[["q", "k", "v"]]), 1),
+    ("two_step", dict(two_step=True), 3),
+    ("two_step + qkv_sharing [q,k,v]", dict(two_step=True, qkv_sharing=[["q", "k", "v"]]), 1),
 ])
 def test_converted_projections_are_one_launch_each(gpu, mode, kw, launches):
     """Inference forward of a converted block: one fused-LoRA kernel per projection (one per
