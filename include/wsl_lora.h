@@ -207,11 +207,12 @@ int wsl_lora_linear_bcast_fwd(const void* x, int64_t ldx,
  * loss.backward() (torchtitan/train.py:456); the reference has no kernel of its own.
  * All tensors bf16 [rows, ld]; x [M, K], gy [M, N], a [r, K], b [N, r]. Any of dw, da, db
  * may be NULL (not computed); da and db need r > 0. Deterministic: split reductions are
- * summed in a fixed order. The layouts taken (wsl_lora_linear_bwd_weights_supported): K and
- * N multiples of 64, r a multiple of 8, x, gy, a, b 16-byte aligned with leading dimensions
- * multiples of 8; anything else returns WSL_E_SHAPE. Workspace (256-byte aligned) from
- * wsl_lora_linear_bwd_weights_workspace_bytes; it may be the forward's workspace (the
- * decode path's counter prefix is left as it is).
+ * summed in a fixed order. wsl_lora_linear_bwd_weights_supported returns 1 for the layouts
+ * the MFMA tile kernels take (K and N multiples of 64, r a multiple of 8, x, gy, a, b 16-byte
+ * aligned with leading dimensions multiples of 8) and 0 for the rest, which run on scalar
+ * kernels with the same contract (dW, dB = gy^T . T and dA = U^T . x over the tokens).
+ * Workspace (256-byte aligned) from wsl_lora_linear_bwd_weights_workspace_bytes; it may be
+ * the forward's workspace (the decode path's counter prefix is left as it is).
  */
 int wsl_lora_linear_bwd_weights_supported(const void* x, int64_t ldx, const void* gy, int64_t ldg,
                                           const void* a, int64_t lda, const void* b, int64_t ldb,

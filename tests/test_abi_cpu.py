@@ -414,8 +414,9 @@ def _bwd_weights(**kw):
     (dict(ldg=127), N.WSL_E_SHAPE),
     (dict(lddb=7), N.WSL_E_SHAPE),
     (dict(dw=P + 1), N.WSL_E_ALIGN),
-    (dict(K=72, ldx=72, lda=72, lddw=72, ldda=72), N.WSL_E_SHAPE),  # K off the 64 grid: not taken
-    (dict(x=P + 2), N.WSL_E_SHAPE),              # x not 16-byte aligned: not taken
+    (dict(x=P + 1), N.WSL_E_ALIGN),              # x not aligned to its element size
+    (dict(K=72, ldx=72, lda=72, lddw=72, ldda=72), N.WSL_E_WORKSPACE),  # K off the grid: taken
+    (dict(x=P + 2), N.WSL_E_WORKSPACE),          # x not 16-byte aligned: taken (scalar kernels)
     (dict(), N.WSL_E_WORKSPACE),                 # no workspace
 ])
 def test_bwd_weights_validation_codes(kw, code):

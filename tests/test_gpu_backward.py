@@ -177,3 +177,33 @@ def test_weight_grads_partial_token_tile_repeats(gpu, M, N, K, r, need_w):
         err = O.max_rel_err(t.float().numpy(), g_ref)
         _say(f"   {name} max_rel_err {err:.2e}")
         assert err <= BF16_TOL, (name, err)
+
+
+def test_off_grid_backward_runs_no_vendor_gemm(gpu):
+    """The backward at a layout off the tile grid (N = 72, K = 136) runs dx on the library's
+    generic forward and dW, dA, dB on its generic weight-gradient kernels: no hipBLASLt or
+    rocBLAS GEMM kernel appears in a trace of the backward."""
+    from torch.profiler import ProfilerActivity, profile
+    import weightshared_torchtitan_amd as wsl
+    M, N, K, r = 100, 72, 136, 8
+    _say(f"[backward, no vendor GEMM] M={M} N={N} K={K} r={r}")
+    g = torch.Generator().manual_seed(3)
+    x, W, A, B = (_leaf(t, gpu) for t in (torch.randn(M, K, generator=g).bfloat16(),
+                                          (torch.randn(N, K, generator=g) * 0.02).bfloat16(),
+                                          (torch.randn(r, K, generator=g) * 0.02).bfloat16(),
+                                          (torch.randn(N, r, generator=g) * 0.02).bfloat16()))
+    gy = torch.randn(M, N, generator=g).bfloat16().to(gpu)
+    wsl.lora_linear(x, W, A, B, 2.0).backward(gy)  # warm-up: workspaces
+    torch.cuda.synchronize()
+    for t in (x, W, A, B):
+        t.grad = None
+    y = wsl.lora_linear(x, W, A, B, 2.0)
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        y.backward(gy)
+        torch.cuda.synchronize()
+    kernels = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+    if not kernels:
+        pytest.skip("the profiler recorded no device activity on this build")
+    vendor = [k for k in kernels if any(s in k for s in ("Cijk", "gemm", "Gemm", "GEMM", "rocblas", "hipblaslt"))]
+    assert vendor == [], vendor
+    assert all(t.grad is not None for t in (x, W, A, B))

@@ -144,6 +144,80 @@ hipError_t transpose_pad(const void* src, int64_t lds_, int64_t R, int64_t C, ui
   return hipGetLastError();
 }
 
+// ---- Layouts the tile kernels do not take (K or N off the 64 grid, r not a multiple of 8,
+// unaligned rows): the token route on scalar kernels, same contract ----
+
+// t[m][j] = bf16(s * sum_k x[m][k] * f[j * fj + k * fk]) for m < M, j < r: T = x . A^T
+// (fj = lda, fk = 1) or U = gy . B (fj = 1, fk = ldb). One thread per (m, j), k in order.
+__global__ void __launch_bounds__(256) generic_rank_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                          const uint16_t* __restrict__ f, int64_t fj, int64_t fk,
+                                                          float s, uint16_t* __restrict__ t, int64_t M, int64_t K,
+                                                          int64_t r) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * r) return;
+  const int64_t m = idx / r, j = idx % r;
+  const uint16_t* xr = x + m * ldx;
+  const uint16_t* fr = f + j * fj;
+  float acc = 0.f;
+  for (int64_t k = 0; k < K; ++k) acc += bf16_bits_to_f32(xr[k]) * bf16_bits_to_f32(fr[k * fk]);
+  t[m * r + j] = f32_to_bf16_bits(s * acc);
+}
+
+// c[i][j] = bf16(sum_m p[m][i] * q[m][j]) over the M token rows of two token-major operands
+// (dW = gy^T . x, dA = U^T . x, dB = gy^T . T). A workgroup owns a 64 x 64 output tile, each
+// thread 4 x 4 outputs; 16 tokens at a time are staged through LDS. Every output is summed
+// by one thread in token order, so the result is deterministic.
+constexpr int GW = 64, GWK = 16;
+__global__ void __launch_bounds__(256) generic_token_product_kernel(const uint16_t* __restrict__ p, int64_t ldp,
+                                                                   const uint16_t* __restrict__ q, int64_t ldq,
+                                                                   int64_t M, int64_t I, int64_t J,
+                                                                   uint16_t* __restrict__ c, int64_t ldc) {
+  __shared__ float ps[GWK][GW + 1];
+  __shared__ float qs[GWK][GW + 1];
+  const int tid = threadIdx.x;
+  const int ti = tid / 16, tj = tid % 16;  // this thread's outputs: rows ti + 16 u, columns tj + 16 v
+  const int64_t i0 = (int64_t)blockIdx.y * GW, j0 = (int64_t)blockIdx.x * GW;
+  float acc[4][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[u][v] = 0.f;
+  for (int64_t m0 = 0; m0 < M; m0 += GWK) {
+    // 16 tokens x 64 columns of each operand: four elements per thread, columns fastest
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = tid + 256 * e, row = idx / GW, col = idx % GW;
+      const int64_t m = m0 + row;
+      ps[row][col] = (m < M && i0 + col < I) ? bf16_bits_to_f32(p[m * ldp + i0 + col]) : 0.f;
+      qs[row][col] = (m < M && j0 + col < J) ? bf16_bits_to_f32(q[m * ldq + j0 + col]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < GWK; ++kk) {
+      float pv[4], qv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pv[u] = ps[kk][ti + 16 * u];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) qv[v] = qs[kk][tj + 16 * v];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[u][v] += pv[u] * qv[v];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = i0 + ti + 16 * u;
+    if (i >= I) continue;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t j = j0 + tj + 16 * v;
+      if (j < J) c[i * ldc + j] = f32_to_bf16_bits(acc[u][v]);
+    }
+  }
+}
+
 size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
@@ -180,9 +254,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t r) {
 
 }  // namespace
 
-// Shapes and layouts the weight-gradient path takes: K and N on the 64-element tile grid
-// (the reductions of the dA and dB products and of the token route's pre-passes), ranks in
-// multiples of 8, 16-byte aligned rows, and sizes within the tile kernel's int range.
+// Shapes and layouts the tile kernels of the weight-gradient path take: K and N on the
+// 64-element tile grid (the reductions of the dA and dB products and of the token route's
+// pre-passes), ranks in multiples of 8, 16-byte aligned rows, and sizes within the tile
+// kernel's int range. Every other layout takes the generic route above.
 bool weight_grads_supported(const LoraArgs& p, const void* gy, int64_t ldg) {
   if (p.M < 1 || p.K % 64 != 0 || p.N % 64 != 0 || p.r % 8 != 0) return false;
   if (p.M > ((int64_t)1 << 22) - 2048 || p.N > ((int64_t)1 << 22) || p.K > ((int64_t)1 << 22)) return false;
@@ -198,6 +273,44 @@ size_t weight_grads_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, 
   return make_plan(M, N, K, need_ab ? r : 0).total;
 }
 
+namespace {
+// The generic route: T = bf16(s x . A^T) and U = bf16(s gy . B) into the workspace's T and U
+// regions, then dW = gy^T . x, dB = gy^T . T and dA = U^T . x over the tokens.
+hipError_t launch_weight_grads_generic(const LoraArgs& p, const void* gy, int64_t ldg, void* dw, int64_t lddw,
+                                       void* da, int64_t ldda, void* db, int64_t lddb, int64_t r, const Plan& L) {
+  const int64_t M = p.M, N = p.N, K = p.K;
+  char* ws = reinterpret_cast<char*>(p.ws);
+  uint16_t* T = reinterpret_cast<uint16_t*>(ws + L.off_t);
+  uint16_t* U = reinterpret_cast<uint16_t*>(ws + L.off_u);
+  const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
+  const uint16_t* g = reinterpret_cast<const uint16_t*>(gy);
+  const hipStream_t st = p.stream;
+  const dim3 rank_grid((unsigned)((M * r + 255) / 256));
+  auto product = [&](const uint16_t* pp, int64_t ldp, int64_t I, const uint16_t* qq, int64_t ldq, int64_t J,
+                     void* dst, int64_t ldd) {
+    const dim3 grid((unsigned)((J + GW - 1) / GW), (unsigned)((I + GW - 1) / GW));
+    generic_token_product_kernel<<<grid, dim3(256), 0, st>>>(pp, ldp, qq, ldq, M, I, J, reinterpret_cast<uint16_t*>(dst),
+                                                             ldd);
+    return hipGetLastError();
+  };
+  hipError_t e = hipSuccess;
+  if (dw != nullptr) e = product(g, ldg, N, x, p.ldx, K, dw, lddw);
+  if (e == hipSuccess && db != nullptr) {
+    generic_rank_kernel<<<rank_grid, dim3(256), 0, st>>>(x, p.ldx, reinterpret_cast<const uint16_t*>(p.a), p.lda, 1,
+                                                         p.scale, T, M, K, r);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = product(g, ldg, N, T, r, r, db, lddb);
+  }
+  if (e == hipSuccess && da != nullptr) {
+    generic_rank_kernel<<<rank_grid, dim3(256), 0, st>>>(g, ldg, reinterpret_cast<const uint16_t*>(p.b), 1, p.ldb,
+                                                         p.scale, U, M, N, r);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = product(U, r, r, x, p.ldx, K, da, ldda);
+  }
+  return e;
+}
+}  // namespace
+
 hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, void* dw, int64_t lddw, void* da,
                                int64_t ldda, void* db, int64_t lddb) {
   const int64_t M = p.M, N = p.N, K = p.K;
@@ -205,6 +318,7 @@ hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, v
   if (r == 0) da = db = nullptr;
   if (dw == nullptr && r == 0) return hipSuccess;
   const Plan L = make_plan(M, N, K, r);
+  if (!weight_grads_supported(p, gy, ldg)) return launch_weight_grads_generic(p, gy, ldg, dw, lddw, da, ldda, db, lddb, r, L);
   char* ws = reinterpret_cast<char*>(p.ws);
   uint16_t* T = reinterpret_cast<uint16_t*>(ws + L.off_t);
   uint16_t* U = reinterpret_cast<uint16_t*>(ws + L.off_u);

@@ -600,13 +600,11 @@ int wsl_lora_linear_bwd_weights(const void* x, int64_t ldx, const void* gy, int6
   if (dw != nullptr && lddw < K) return fail(WSL_E_SHAPE, "lddw (%lld) < K (%lld)", (long long)lddw, (long long)K);
   if (da != nullptr && ldda < K) return fail(WSL_E_SHAPE, "ldda (%lld) < K (%lld)", (long long)ldda, (long long)K);
   if (db != nullptr && lddb < r) return fail(WSL_E_SHAPE, "lddb (%lld) < r (%lld)", (long long)lddb, (long long)r);
-  if (((uintptr_t)dw & 1) || ((uintptr_t)da & 1) || ((uintptr_t)db & 1))
+  if (((uintptr_t)dw & 1) || ((uintptr_t)da & 1) || ((uintptr_t)db & 1) || ((uintptr_t)x & 1) ||
+      ((uintptr_t)gy & 1) || ((uintptr_t)a & 1) || ((uintptr_t)b & 1))
     return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
   wsl::LoraArgs p = make_args(x, ldx, nullptr, 0, WSL_DTYPE_BF16, nullptr, a, lda, b, ldb, scale, nullptr, 0, M, N, K,
                               r, stream);
-  if (!wsl::weight_grads_supported(p, gy, ldg))
-    return fail(WSL_E_SHAPE, "layout not taken by the weight-gradient path (K, N multiples of 64, r of 8, "
-                             "16-byte aligned operands, leading dimensions multiples of 8)");
   const size_t need = wsl::weight_grads_workspace_bytes(M, N, K, r, true, true);
   if (workspace == nullptr || workspace_bytes < layout_bytes(need))
     return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", layout_bytes(need), workspace_bytes);

@@ -244,19 +244,6 @@ def clear_transpose_cache() -> None:
     _WT_CACHE.clear()
 
 
-def _weight_grads_torch(x2, gy2, a, b, s, need_w, need_a, need_b):
-    """The same gradients by torch GEMMs on the device, for layouts the HIP path does not
-    take (K or N off the 64 grid, r not a multiple of 8, unaligned operands)."""
-    dw = torch.mm(gy2.t(), x2) if need_w else None
-    da = db = None
-    zero = torch.zeros((), dtype=torch.bfloat16, device=gy2.device)  # beta = 0: s rides on alpha
-    if need_a:
-        da = torch.addmm(zero, torch.mm(gy2, b).t(), x2, beta=0, alpha=s)
-    if need_b:
-        db = torch.addmm(zero, gy2.t(), torch.mm(x2, a.t().contiguous()), beta=0, alpha=s)
-    return dw, da, db
-
-
 @torch.library.custom_op("wsl::lora_linear_weight_grads", mutates_args=(), device_types="cuda")
 def lora_linear_weight_grads_op(x: torch.Tensor, gy: torch.Tensor, a: Optional[torch.Tensor],
                                 b: Optional[torch.Tensor], scale: float, need_w: bool, need_a: bool,
@@ -264,7 +251,8 @@ def lora_linear_weight_grads_op(x: torch.Tensor, gy: torch.Tensor, a: Optional[t
     """dw = gy^T . x [N, K], da = scale (gy . b)^T . x [r, K], db = scale gy^T . (x . a^T)
     [N, r], each only when asked for (else an empty tensor), bf16 from bf16 x [M, K],
     gy [M, N], a [r, K], b [N, r] (wsl_lora_linear_bwd_weights: dW over the tokens on the
-    fused kernel's tile loop, reading x and gy as they lie; da and db from dW)."""
+    fused kernel's tile loop, reading x and gy as they lie, da and db from dW; layouts off
+    the tile grid on the library's scalar kernels)."""
     dev = _check_device(x, gy, a, b)
     x2 = _row_major(x.reshape(-1, x.shape[-1]), "x")
     gy2 = _row_major(gy.reshape(-1, gy.shape[-1]), "grad_y")
@@ -290,12 +278,6 @@ def lora_linear_weight_grads_op(x: torch.Tensor, gy: torch.Tensor, a: Optional[t
         return (x2.new_zeros(N, K) if need_w else empty(), x2.new_zeros(r, K) if need_a else empty(),
                 x2.new_zeros(N, r) if need_b else empty())
     L = _native.lib()
-    supported = L.wsl_lora_linear_bwd_weights_supported(
-        x2.data_ptr(), x2.stride(0), gy2.data_ptr(), gy2.stride(0), _dev_ptr(a), a.stride(0) if r else 0,
-        _dev_ptr(b), b.stride(0) if r else 0, M, N, K, r)
-    if not supported:
-        dw, da, db = _weight_grads_torch(x2, gy2, a, b, float(scale), need_w, need_a, need_b)
-        return dw if need_w else empty(), da if need_a else empty(), db if need_b else empty()
     dw = torch.empty((N, K), dtype=torch.bfloat16, device=dev) if need_w else None
     da = torch.empty((r, K), dtype=torch.bfloat16, device=dev) if need_a else None
     db = torch.empty((N, r), dtype=torch.bfloat16, device=dev) if need_b else None
