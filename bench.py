@@ -145,6 +145,34 @@ class ProjectionStack:
                 ops.lora_linear_grouped_op(self.x[self.gK[q]], self.gW[c][q], self.gS[c][q], self.gA[l][q],
                                            self.gB[l][q], self.scale, self.gN[q])
 
+    def prepare_chain(self, layers_per_chain=2):
+        """Chains (wsl_lora_linear_chain_fwd) of the grouped launches' projections as
+        independent stages, `layers_per_chain` layers (4 stages each) per launch: the inputs
+        are synthetic, so no stage reads another's output. Outputs are allocated once. False
+        where the library does not take it."""
+        from weightshared_torchtitan_amd import ops
+        self.stack_groups()
+        dev = self.x[self.gK[0]].device
+        self.chains = []
+        st = []
+        for l in range(self.layers):
+            c = l % self.copies
+            for q in range(len(self.GROUPS)):
+                y = torch.empty(self.M, sum(self.gN[q]), dtype=torch.bfloat16, device=dev)
+                st.append(ops.ChainStage(self.x[self.gK[q]], self.gW[c][q], self.gA[l][q], self.gB[l][q], self.scale,
+                                         y, group_n=self.gN[q]))
+            if (l + 1) % layers_per_chain == 0 or l + 1 == self.layers:
+                if self.fp8 or not ops.chain_supported(st, self.M):
+                    return False
+                self.chains.append(st)
+                st = []
+        return True
+
+    def run_chain(self):
+        from weightshared_torchtitan_amd import ops
+        for st in self.chains:
+            ops.lora_linear_chain(st, self.M)
+
     def flops(self):
         return self.layers * sum(lora_flops(self.M, N, K, self.r) for _, N, K in self.shapes)
 
@@ -513,15 +541,25 @@ def c2_1p7b_extra(dev, steps, warmup):
 
 def bench_c3(dev, steps, warmup):
     """Config 3 per M: one launch per projection with cold weights (6 rotating copies) and
-    warm (one copy), and cold with q|k|v and gate|up as grouped launches (4 per layer)."""
+    warm (one copy), cold with q|k|v and gate|up as grouped launches (4 per layer), and cold
+    with two layers' grouped launches as the independent stages of one chain launch (up to 16
+    tokens)."""
     out = {}
     for M in (1, 8, 32, 64):
         row = {}
-        for label, copies, grouped in (("cold", 6, False), ("warm", 1, False), ("cold_grouped", 6, True)):
+        for label, copies, grouped in (("cold", 6, False), ("warm", 1, False), ("cold_grouped", 6, True),
+                                       ("cold_chain", 6, "chain")):
             st = ProjectionStack(QWEN3_1P7B, M=M, r=64, layers=28, dev=dev, seed=3, copies=copies)
-            if grouped:
+            if grouped == "chain":
+                if not st.prepare_chain():
+                    continue
+                fn = st.run_chain
+            elif grouped:
                 st.stack_groups()
-            g = graph_of(st.run_grouped if grouped else st.run)
+                fn = st.run_grouped
+            else:
+                fn = st.run
+            g = graph_of(fn)
             ms = time_replays(g, steps, warmup)
             row[label] = {"ms_per_28_layers": round(ms, 4), "GB/s": round(st.bytes() / ms / 1e6, 1),
                           "frac_hbm": round(st.bytes() / ms / 1e6 / HBM_PEAK_GBS, 4)}
@@ -825,6 +863,12 @@ def bench_c4(dev):
                         "bytes_per_step_every_layer_weights": round(by["every_layer"]),
                         "frac_every_layer_weights": round(by["every_layer"] / step_ms / 1e6 / HBM_PEAK_GBS, 4),
                         "terms_MB": {k: round(v / 1e6, 2) for k, v in by["terms"].items()}}}
+    # the same decode with chains (2 launches per layer: the attention step and one chain of
+    # o, gate|up, down and the next layer's q|k|v) instead of one launch per fused projection
+    model.decode_chain = True
+    _, t2 = model.generate(prompt, n_new)
+    res["with_chain"] = {"decode_tok_s": round(8 * n_new / (t2["decode_ms"] / 1e3), 1),
+                         "ms_per_step": round(t2["decode_ms"] / steps, 4)}
     del model
     torch.cuda.empty_cache()
     return res
@@ -954,6 +998,8 @@ def main():
     ap.add_argument("--ab", default='{"default": {}, "strips_off": {"prefill_strips": -1}}',
                     help="--only envab: JSON {mode: {option: value}} of the path overrides timed side by side")
     ap.add_argument("--ab-shapes", default=None, help="--only envab / stamps: comma-separated names from AB_SHAPES")
+    ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",
+                    help="a libwsl path override for the whole run (ops.path_options names), repeatable")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -963,6 +1009,10 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     import weightshared_torchtitan_amd  # noqa: F401  (loads libwsl; fails loudly if missing)
+    from weightshared_torchtitan_amd import _native
+    for kv in args.opt:
+        name, _, val = kv.partition("=")
+        _native.set_option(name, int(val))
 
     dev = torch.device("cuda:0")
     torch.cuda.synchronize()

@@ -139,6 +139,53 @@ int wsl_tied_head_argmax_supported(int64_t M, int64_t N, int64_t K);
 int wsl_tied_head_argmax_fwd(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t N, int64_t K, int64_t M,
                              int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* A chain of decode-shaped LoRA linears in one persistent launch. No counterpart in the
+ * reference, whose decode re-runs the whole model per token (scripts/generate/_generation.py:35-80)
+ * with one aten call per projection; it replaces the consecutive launches of the projections
+ * of one decode step (torchtitan/experiments/qwen3/model/model.py:184,218,250-251 at M tokens).
+ *
+ * Stage s is wsl_lora_linear_fused_fwd (fuse != 0) or wsl_lora_linear_grouped_fwd (fuse == 0,
+ * n_groups >= 1) on its descriptor, with the same results bit for bit. One workgroup per CU
+ * runs every stage's workgroups in order; a stage with after_previous = 1 reads what an
+ * earlier stage of the chain wrote (its x or residual), so its workgroups wait until every
+ * workgroup of the previous stage has stored its outputs. They issue their first W and A
+ * loads before that wait and fetch x afterwards, so a stage's weight stream overlaps the end
+ * of the stage before it. Stages without after_previous must not read another stage's output.
+ *
+ * Shapes taken (wsl_lora_linear_chain_supported, from the sizes and pointer alignment):
+ * 1 <= M <= 16, bf16 W, 1 <= n_stages <= WSL_CHAIN_MAX_STAGES; each stage the decode path's
+ * one-slice plan (x, A and B rows in one K slice: M * K * 2 bytes within the LDS budget, K a
+ * multiple of 1024), N a multiple of 16 and at most 16384 rows, 16-byte aligned operands.
+ *
+ * Waits are bounded. A stage wait that gives up sets a sticky failure word in the workspace
+ * and the launch still drains (its outputs are then not valid);
+ * wsl_lora_linear_chain_status reads and clears that word (it synchronizes `stream`). The
+ * workspace (wsl_lora_linear_chain_workspace_bytes) is zero-filled before its first use and
+ * kept valid by every call; a workspace used only by chains keeps other launches' hand-off
+ * words out of the chain's stage flags. */
+#define WSL_CHAIN_MAX_STAGES 8
+typedef struct wsl_chain_stage {
+  const void* x; int64_t ldx;    /* input [M, K] bf16 */
+  const void* norm_w; float eps; /* RMSNorm weight [K] (fuse & WSL_FUSE_RMSNORM) */
+  const void* w; int64_t ldw;    /* base [N, K] bf16 */
+  const void* a; int64_t lda;    /* LoRA A [n_groups * r, K] (r = 0: none) */
+  const void* b; int64_t ldb;    /* LoRA B [N, r] */
+  float scale;
+  const void* residual; int64_t ldr; /* fuse & WSL_FUSE_RESIDUAL */
+  void* y; int64_t ldy;          /* output [M, N], or [M, N / 2] with WSL_FUSE_SWIGLU */
+  int64_t N, K, r;
+  int32_t fuse;                  /* WSL_FUSE_* as wsl_lora_linear_fused_fwd, or 0 */
+  int32_t n_groups;              /* fuse == 0: projections side by side (group_n), else 1 */
+  int64_t group_n[4];
+  int32_t after_previous;        /* 1: x or residual is an earlier stage's output */
+} wsl_chain_stage;
+int wsl_lora_linear_chain_supported(int64_t M, int32_t n_stages, const wsl_chain_stage* stages);
+int wsl_lora_linear_chain_workspace_bytes(int64_t M, int32_t n_stages, const wsl_chain_stage* stages,
+                                          size_t* bytes);
+int wsl_lora_linear_chain_fwd(int64_t M, int32_t n_stages, const wsl_chain_stage* stages, void* workspace,
+                              size_t workspace_bytes, void* stream);
+int wsl_lora_linear_chain_status(void* workspace, void* stream, int32_t* failed);
+
 /* Thread-local description of the last failure of an entry point above ("" if none). */
 const char* wsl_decode_last_error(void);
 

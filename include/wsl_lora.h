@@ -257,6 +257,9 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
  *   WSL_OPT_DECODE_WIDE        0 auto; -1 keep 65-72 tokens on the prefill path
  *   WSL_OPT_DECODE_SPIN_LIMIT  0 the default poll bound of the decode hand-offs; n > 0 that
  *                              bound; -1 no polling (the local fallback runs at once)
+ *   WSL_OPT_DECODE_RES_SPLITS  0 auto; n in [2, 8] at least n K splits for the decode step's
+ *                              residual-epilogue launches (wsl_lora_linear_fused_fwd) where
+ *                              the slices keep eight wave steps
  * wsl_set_option returns WSL_E_INVALID_ARG for an unknown option or a value out of range.
  */
 #define WSL_OPT_PREFILL_STRIPS 1
@@ -266,7 +269,8 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
 #define WSL_OPT_DECODE_PASSES 5
 #define WSL_OPT_DECODE_WIDE 6
 #define WSL_OPT_DECODE_SPIN_LIMIT 7
-#define WSL_OPT_COUNT 8
+#define WSL_OPT_DECODE_RES_SPLITS 8
+#define WSL_OPT_COUNT 9
 int wsl_set_option(int32_t option, int64_t value);
 int wsl_get_option(int32_t option, int64_t* value);
 

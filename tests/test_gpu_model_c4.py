@@ -78,3 +78,22 @@ def test_c4_greedy_tokens_match_cpu_oracle(c4):
         tol = LOGIT_TOL * r.abs().max(dim=-1).values
         chosen = r.gather(1, new[seqs, i:i + 1])[:, 0]
         assert bool((chosen >= r.max(dim=-1).values - tol).all()), f"step {i}"
+
+
+def test_c4_chain_decode_equals_separate_launches(gpu, c4):
+    """The same generation with the decode step's chains (one launch for each layer's o,
+    gate|up, down and the next layer's q|k|v): the chains compute what the separate fused
+    launches do bit for bit, so the tokens and the logits they were chosen from are equal."""
+    from weightshared_torchtitan_amd import ops
+    a, m, prompt, new, logits = c4
+    _say("[c4] generate with chains")
+    m.decode_chain = True
+    try:
+        with torch.no_grad():
+            new2, res = m.generate(prompt.to(gpu), N_NEW, use_graph=True, return_logits=True)
+        torch.cuda.synchronize()
+        assert not ops.chain_status(gpu)
+    finally:
+        m.decode_chain = False
+    assert torch.equal(new2.cpu(), new)
+    assert torch.equal(res["logits"], logits)

@@ -68,7 +68,24 @@ EXPORTED = (
     "wsl_tied_head_argmax_workspace_bytes",
     "wsl_tied_head_argmax_supported",
     "wsl_tied_head_argmax_fwd",
+    "wsl_lora_linear_chain_supported",
+    "wsl_lora_linear_chain_workspace_bytes",
+    "wsl_lora_linear_chain_fwd",
+    "wsl_lora_linear_chain_status",
 )
+
+WSL_CHAIN_MAX_STAGES = 8
+
+
+class ChainStage(ctypes.Structure):
+    """wsl_chain_stage (include/wsl_decode.h)."""
+    _fields_ = [("x", ctypes.c_void_p), ("ldx", ctypes.c_int64), ("norm_w", ctypes.c_void_p), ("eps", ctypes.c_float),
+                ("w", ctypes.c_void_p), ("ldw", ctypes.c_int64), ("a", ctypes.c_void_p), ("lda", ctypes.c_int64),
+                ("b", ctypes.c_void_p), ("ldb", ctypes.c_int64), ("scale", ctypes.c_float),
+                ("residual", ctypes.c_void_p), ("ldr", ctypes.c_int64), ("y", ctypes.c_void_p),
+                ("ldy", ctypes.c_int64), ("N", ctypes.c_int64), ("K", ctypes.c_int64), ("r", ctypes.c_int64),
+                ("fuse", ctypes.c_int32), ("n_groups", ctypes.c_int32), ("group_n", ctypes.c_int64 * 4),
+                ("after_previous", ctypes.c_int32)]
 
 _lib = None
 _lock = threading.Lock()
@@ -90,6 +107,7 @@ OPTIONS = {
     "decode_passes": 5,      # -1: K splits only; 1: passes wherever the slices allow
     "decode_wide": 6,        # -1: 65-72 tokens on the prefill path
     "decode_spin_limit": 7,  # n > 0: poll bound of the decode hand-offs; -1: no polling
+    "decode_res_splits": 8,  # 2..8: K splits of the decode step's residual-epilogue launches
 }
 
 # wsl_plan_info.path values
@@ -226,6 +244,16 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, _c_i64, _c_vp, _c_i64,                          # residual, ldr, y, ldy
         _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int32,        # M, N, K, r, fuse
         _c_vp, ctypes.c_size_t, _c_vp]                         # workspace, bytes, stream
+    chain_p = ctypes.POINTER(ChainStage)
+    lib.wsl_lora_linear_chain_supported.restype = ctypes.c_int
+    lib.wsl_lora_linear_chain_supported.argtypes = [_c_i64, ctypes.c_int32, chain_p]
+    lib.wsl_lora_linear_chain_workspace_bytes.restype = ctypes.c_int
+    lib.wsl_lora_linear_chain_workspace_bytes.argtypes = [_c_i64, ctypes.c_int32, chain_p,
+                                                          ctypes.POINTER(ctypes.c_size_t)]
+    lib.wsl_lora_linear_chain_fwd.restype = ctypes.c_int
+    lib.wsl_lora_linear_chain_fwd.argtypes = [_c_i64, ctypes.c_int32, chain_p, _c_vp, ctypes.c_size_t, _c_vp]
+    lib.wsl_lora_linear_chain_status.restype = ctypes.c_int
+    lib.wsl_lora_linear_chain_status.argtypes = [_c_vp, _c_vp, ctypes.POINTER(ctypes.c_int32)]
     lib.wsl_tied_head_argmax_workspace_bytes.restype = ctypes.c_size_t
     lib.wsl_tied_head_argmax_workspace_bytes.argtypes = [_c_i64]
     lib.wsl_tied_head_argmax_supported.restype = ctypes.c_int

@@ -53,6 +53,7 @@
 // arithmetic: the decode loop runs the same projections at small M
 // (scripts/generate/_generation.py:35-80 calling
 // torchtitan/models/llama3/model/model.py:189-192,392-398).
+#include <algorithm>
 #include <climits>
 #include <cstring>
 #include <cstdlib>
@@ -308,11 +309,18 @@ struct XPasses {
   int kp = 1;
 };
 
-template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue>
+// Issued by slice_sums between its first W loads and the wait for the x fill: with
+// NoLate the caller has issued the fills before the call; otherwise `late()` issues them
+// (after whatever wait it needs), so the W loads are in flight while it waits.
+struct NoLate {
+  __device__ __forceinline__ void operator()() const {}
+};
+
+template <int WDT, int NR, int MB, int KW, class Pro = NoPrologue, class Late = NoLate>
 __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t ldm, int nrows, int row0,
                                            int kbeg, int kc, int M, char* smem, float* sums,
                                            const Pro& pro = Pro(), RowMap rmap = RowMap{},
-                                           XPasses xp = XPasses{}) {
+                                           XPasses xp = XPasses{}, const Late& late = Late()) {
   using G = Geo<WDT>;
   constexpr int PD = NR == 1 ? 4 : (NR == 2 ? 2 : 1);  // K steps in flight per wave (NR*4*PD = 16 loads)
   constexpr int LPS = NR * 4;           // loads per step
@@ -350,9 +358,9 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[i][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // The x / B fills were issued before the W loads: wait until only the W loads are
-  // outstanding, then for every wave's fills (and LDS writes made before the call).
-  {
+  if constexpr (std::is_same<Late, NoLate>::value) {
+    // The x / B fills were issued before the W loads: wait until only the W loads are
+    // outstanding, then for every wave's fills (and LDS writes made before the call).
     const int npf = my < PD ? my : PD;
     if (npf == 0) wait_vm<0>();
     else if (npf == 1) wait_vm<LPS>();
@@ -361,6 +369,11 @@ __device__ __forceinline__ void slice_sums(const void* __restrict__ mat, int64_t
       if (npf == 3) wait_vm<3 * LPS>();
       else wait_vm<4 * LPS>();
     }
+  } else {
+    // The fills follow the W loads: wait for all of them (the W steps, issued first, have
+    // had the whole of late()'s wait to land).
+    late();
+    wait_vm<0>();
   }
   lds_barrier();
   pro();  // the x slice computed from what the fills staged (W loads still in flight)
@@ -550,9 +563,16 @@ __device__ __forceinline__ uint32_t ptag_of(uint64_t tag) { return (uint32_t)((t
 // bound computes T itself from x and A.
 // Eight consecutive elements of the projection input x[m][k..k+8): x itself, or with the
 // RMSNorm prologue bf16(x * rsqrt(ss[m] / K + eps) * w_norm).
-template <bool NORM>
+template <bool NORM, bool COH = false>
 __device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, int m, int k, float (&v)[8]) {
-  const u32x4_t xv = ld_global_16(p.x + (int64_t)m * p.ldx + k);
+  u32x4_t xv;
+  if constexpr (COH) {  // x written earlier in this launch (a chain stage), maybe on another XCD
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p.x + (int64_t)m * p.ldx + k);
+    const uint64_t lo = ld_agent(q), hi = ld_agent(q + 1);
+    xv = u32x4_t{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+  } else {
+    xv = ld_global_16(p.x + (int64_t)m * p.ldx + k);
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32((xv[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
   if constexpr (NORM) {
@@ -564,7 +584,7 @@ __device__ __forceinline__ void load_x8(const DecodeArgs& p, const float* ss, in
   }
 }
 
-template <int MC, bool NORM = false>
+template <int MC, bool NORM = false, bool COH = false>
 __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint64_t tag, int* flag,
                                          const float* ss = nullptr, int goff = 0) {
   const int tid = threadIdx.x;
@@ -605,7 +625,7 @@ __device__ __forceinline__ void gather_t(const DecodeArgs& p, uint16_t* tl, uint
       float acc = 0.f;
       for (int k = 0; k < p.K; k += 8) {
         float xv[8];
-        load_x8<NORM>(p, ss, m, k, xv);
+        load_x8<NORM, COH>(p, ss, m, k, xv);
         const u32x4_t av = ld_global_16(ar + k);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += xv[e] * bf16_bits_to_f32((av[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
@@ -738,10 +758,60 @@ __device__ __forceinline__ void argmax_epilogue(const DecodeArgs& p, const float
   if (tid == 0) __hip_atomic_store(p.am_cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- Chains (wsl_lora_linear_chain_fwd): the stages of one persistent launch ----
+// A W workgroup of a chain stage publishes one word per workgroup once its outputs are
+// stored (agent-scope stores, then vmcnt(0)); a stage that reads an earlier stage's output
+// waits, after issuing its first W loads, until every word of the previous stage carries the
+// launch's flag value, and only then fetches x (agent-coherent loads: another XCD wrote it).
+// The flag value's top bits (0x7F5A) are neither a T word's (bit 63 set) nor, for the first
+// 2^30 launches, a partial-sum word's.
+struct ChainCtl {
+  const uint64_t* prev_flags;  // W workgroup words of the stage waited on; nullptr: no wait
+  int prev_n;
+  uint64_t* flags;             // this stage's W workgroup words
+  unsigned* err;               // sticky failure word of the launch (a wait that gave up)
+  int spin;
+};
+__device__ __forceinline__ uint64_t chain_flag_of(uint64_t tag) { return (0x7F5Aull << 48) | (tag & kTagMask); }
+
+// Wave 0 polls the previous stage's words (bounded, with a short sleep between rounds), then
+// every wave passes a barrier: no x or residual load of this workgroup is issued before the
+// previous stage's outputs are out. The barrier carries no fence, so the W loads already in
+// flight stay in flight.
+__device__ __forceinline__ void chain_wait(const ChainCtl* c, uint64_t tag) {
+  if (c->prev_flags == nullptr) return;
+  if (threadIdx.x < 64) {
+    const uint64_t want = chain_flag_of(tag);
+    bool ok = true;
+    for (int i = threadIdx.x; i < c->prev_n; i += 64) {
+      uint64_t v = ld_agent(c->prev_flags + i);
+      for (int it = 0; v != want && it < c->spin; ++it) {
+        __builtin_amdgcn_s_sleep(1);
+        v = ld_agent(c->prev_flags + i);
+      }
+      ok = ok && v == want;
+    }
+    if (!ok) __hip_atomic_fetch_or(c->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  plain_barrier();
+}
+
+// Eight bytes of y: a plain store, or in a chain an agent-scope one (read by other XCDs in
+// the same launch).
+template <bool CH>
+__device__ __forceinline__ void store_out8(uint16_t* q, uint2 v) {
+  if constexpr (CH)
+    st_agent(reinterpret_cast<uint64_t*>(q), ((uint64_t)v.y << 32) | v.x);
+  else
+    *reinterpret_cast<uint2*>(q) = v;
+}
+
 // The work of one workgroup of a decode launch: a T workgroup (bid < gT * kst) or a W
-// workgroup.
-template <int WDT, int NR, int MB, int KW, int FUSE>
-__device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64_t cnt_raw, char* smem) {
+// workgroup. CH: a stage of a chain (ctl), see ChainCtl: its first W (or A) loads are issued
+// before it waits for its input.
+template <int WDT, int NR, int MB, int KW, int FUSE, bool CH = false>
+__device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64_t cnt_raw, char* smem,
+                                            const ChainCtl* ctl = nullptr) {
   constexpr bool NORM = (FUSE & kFuseNorm) != 0;
   constexpr bool ACT = (FUSE & kFuseAct) != 0;
   constexpr bool RES = (FUSE & kFuseRes) != 0;
@@ -771,7 +841,24 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     const int kbeg = ks * p.kct;
     constexpr int RED_T = (NWV - RBK) * MB * 4 * 64 * 4;
     float* sums = reinterpret_cast<float*>(smem + RED_T);
-    if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
+    if constexpr (CH) {  // one K slice, no passes: A loads first, then the wait, then x
+      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
+      const auto late = [&]() {
+        chain_wait(ctl, late_tag());
+        if constexpr (NORM) {
+          fill_x<false, kAgentCoherent>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
+          fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
+        } else {
+          fill_x<true, kAgentCoherent>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
+        }
+      };
+      if constexpr (NORM)
+        slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, 0, p.kct, p.M, smem, sums,
+                                     NormPrologue{&p, smem, ss, smem + p.nw_off}, RowMap{}, XPasses{}, late);
+      else
+        slice_sums<kBF16, 1, MB, KW>(p.a, p.lda, p.rt, g * TROWS, 0, p.kct, p.M, smem, sums, NoPrologue{},
+                                     RowMap{}, XPasses{}, late);
+    } else if constexpr (NORM) {  // one K slice (kst == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
@@ -813,17 +900,44 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
     // is read and later written by this workgroup only, so y may alias res.
     constexpr int EPB = ((ROWS / 16) * MB + NWV - 1) / NWV;  // epilogue blocks per wave
     uint2 rpre[RES ? EPB : 1];
-    if constexpr (RES) {
+    const auto load_res = [&]() {
 #pragma unroll
       for (int t = 0; t < EPB; ++t) {
         const int blk = wave + t * NWV, i = blk / MB, m = blk % MB * 16 + l16;
         const int n0 = row0 + i * 16 + grp * 4;
         rpre[t] = make_uint2(0u, 0u);
-        if (blk < (ROWS / 16) * MB && m < p.M && n0 + 3 < p.N)
-          rpre[t] = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n0);
+        if (blk < (ROWS / 16) * MB && m < p.M && n0 + 3 < p.N) {
+          const uint16_t* q = p.res + (int64_t)m * p.ldr + n0;
+          if constexpr (CH) {  // written earlier in this launch, maybe on another XCD
+            const uint64_t v = ld_agent(reinterpret_cast<const uint64_t*>(q));
+            rpre[t] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+          } else {
+            rpre[t] = *reinterpret_cast<const uint2*>(q);
+          }
+        }
       }
-    }
-    if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
+    };
+    if constexpr (RES && !CH) load_res();
+    if constexpr (CH) {  // one K slice, no passes: W loads first, then the wait, then x, B, res
+      float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
+      const auto late = [&]() {
+        chain_wait(ctl, late_tag());
+        if constexpr (NORM) {
+          fill_x<false, kAgentCoherent>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
+          fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
+        } else {
+          fill_x<true, kAgentCoherent>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
+        }
+        if (p.r > 0) fill_b(bl, p.b, p.ldb, ROWS, row0, p.N, p.r, p.r32, wave, lane);
+        if constexpr (RES) load_res();
+      };
+      if constexpr (NORM)
+        slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, 0, p.kcy, p.M, smem, sums,
+                                    NormPrologue{&p, smem, ss, smem + p.nw_off}, p.wmap, XPasses{}, late);
+      else
+        slice_sums<WDT, NR, MB, KW>(p.w, p.ldw, p.N, row0, 0, p.kcy, p.M, smem, sums, NoPrologue{}, p.wmap,
+                                    XPasses{}, late);
+    } else if constexpr (NORM) {  // one K slice (ksy == 1): the whole rows
       float* ss = reinterpret_cast<float*>(smem + p.flag_off + 16);
       fill_x<false>(smem, p.x, p.ldx, p.M, 0, p.K, wave, lane);
       fill_x<false>(smem + p.nw_off, p.nw, 0, 1, 0, p.K, wave, lane);
@@ -847,7 +961,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
       }
       if (p.r > 0) {
         const int goff = ((row0 >= p.ge0) + (row0 >= p.ge1) + (row0 >= p.ge2)) * p.r;
-        gather_t<MC, NORM>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
+        gather_t<MC, NORM, CH>(p, tl, tag, flag, reinterpret_cast<const float*>(smem + p.flag_off + 16), goff);
       }
       WSL_DSTAMP(bid, 3);
       // Epilogue: wave blk finishes the 16 x 16 output block (rows i, tokens mb).
@@ -879,7 +993,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
             uint2 pk;
             pk.x = pack_bf16x2(o[0] / (1.f + __expf(-o[0])) * u[0], o[1] / (1.f + __expf(-o[1])) * u[1]);
             pk.y = pack_bf16x2(o[2] / (1.f + __expf(-o[2])) * u[2], o[3] / (1.f + __expf(-o[3])) * u[3]);
-            *reinterpret_cast<uint2*>(p.y + (int64_t)m * p.ldy + f0) = pk;
+            store_out8<CH>(p.y + (int64_t)m * p.ldy + f0, pk);
           }
         } else if (m < p.M) {
           float o[4];
@@ -909,13 +1023,18 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& p, int bid, uint64
             uint2 pk;
             pk.x = pack_bf16x2(o[0], o[1]);
             pk.y = pack_bf16x2(o[2], o[3]);
-            *reinterpret_cast<uint2*>(yr + n0) = pk;
+            store_out8<CH>(yr + n0, pk);
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               if (n0 + e < p.N) yr[n0 + e] = f32_to_bf16_bits(o[e]);
           }
         }
+      }
+      if constexpr (CH) {  // every output of this workgroup is out: publish its word
+        wait_vm<0>();
+        plain_barrier();
+        if (tid == 0) st_agent(ctl->flags + g, chain_flag_of(tag));
       }
       WSL_DSTAMP(bid, 4);
     }
@@ -945,6 +1064,64 @@ __global__ void __launch_bounds__(DT) decode_kernel(DecodeArgs p) {
   decode_body<WDT, NR, MB, KW, FUSE>(p, blockIdx.x, launch_count(p.cnt), smem);
   launch_exit(p.cnt, p.gT * p.kst + p.gY * p.ksy);
 }
+
+// ---- The chain kernel: the stages of wsl_lora_linear_chain_fwd in one persistent launch ----
+constexpr int kChainMax = 8;            // WSL_CHAIN_MAX_STAGES
+constexpr int kChainFlagWords = 1024;   // W workgroups per stage
+constexpr size_t kChainErrOff = 2048;   // sticky failure word in the counter prefix (unused by other launches)
+
+struct ChainStage {
+  DecodeArgs a;
+  ChainCtl ctl;
+  int fuse, nr, nvb;  // fusion, row blocks per wave, workgroups (T then W)
+  int rot;            // workgroup v of the stage runs on workgroup (v + rot) mod grid
+};
+struct ChainArgs {
+  ChainStage st[kChainMax];
+  int n;
+  unsigned* cnt;
+};
+
+template <int NR, int FUSE>
+__device__ __forceinline__ void chain_vb(const ChainStage& s, int vb, uint64_t cnt_raw, char* smem) {
+  decode_body<kBF16, NR, 1, 8, FUSE, true>(s.a, vb, cnt_raw, smem, &s.ctl);
+}
+
+// One workgroup per CU walks every stage in order. Stage s's workgroup v runs on workgroup
+// (v + rot_s) mod grid, rot_s being where the stage before it ended (rot_0 = 0), so most of a
+// stage lands on workgroups the stage before left idle: those issue their first W loads at
+// once and wait for the input with them in flight. A stage's T workgroups (v < nT, at most
+// the grid) are in its first round; a workgroup only waits on work of earlier stages or of
+// T workgroups, which never wait themselves within their stage.
+__global__ void __launch_bounds__(DT, 1) chain_kernel(const ChainArgs args) {
+  (void)args;
+  // The arguments read where they lie in the kernel argument segment (the first argument is
+  // at its start): used by name, the compiler copied them to scratch per lane.
+  const ChainArgs& c = *(const ChainArgs*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const uint64_t cnt_raw = launch_count(c.cnt);
+  const int grid = (int)gridDim.x;
+  for (int s = 0; s < c.n; ++s) {
+    const ChainStage& st = c.st[s];
+    const int key = st.fuse * 4 + st.nr;
+    for (int vb = ((int)blockIdx.x - st.rot + grid) % grid; vb < st.nvb; vb += grid) {
+      switch (key) {
+        case 0 * 4 + 1: chain_vb<1, 0>(st, vb, cnt_raw, smem); break;
+        case 0 * 4 + 2: chain_vb<2, 0>(st, vb, cnt_raw, smem); break;
+        case kFuseNorm * 4 + 1: chain_vb<1, kFuseNorm>(st, vb, cnt_raw, smem); break;
+        case kFuseNorm * 4 + 2: chain_vb<2, kFuseNorm>(st, vb, cnt_raw, smem); break;
+        case (kFuseNorm | kFuseAct) * 4 + 1: chain_vb<1, kFuseNorm | kFuseAct>(st, vb, cnt_raw, smem); break;
+        case (kFuseNorm | kFuseAct) * 4 + 2: chain_vb<2, kFuseNorm | kFuseAct>(st, vb, cnt_raw, smem); break;
+        case kFuseRes * 4 + 1: chain_vb<1, kFuseRes>(st, vb, cnt_raw, smem); break;
+        case kFuseRes * 4 + 2: chain_vb<2, kFuseRes>(st, vb, cnt_raw, smem); break;
+        default: break;  // the host plans only the pairs above
+      }
+      lds_barrier();  // the next workgroup's fills reuse the LDS this one read
+    }
+  }
+  launch_exit(c.cnt, gridDim.x);
+}
+static_assert(sizeof(ChainArgs) <= 4096, "kernel arguments");
 
 int wave_k_of(int wdt) { return wdt == kFP8 ? 256 : 128; }
 
@@ -992,7 +1169,7 @@ double plan_cost(const DecodePlan& pl, int64_t M, int64_t N, int nr) {
 
 // Which rows-per-group choices a plan may take: every one (plain launches) or those the
 // fused kernels are built for (one token block).
-enum class Pick { kAll, kFused };
+enum class Pick { kAll, kFused, kChain };
 
 // WSL_OPT_DECODE_PASSES: -1 keeps K splits, 1 walks every split slice in passes (one
 // workgroup per row group), 0 the measured rule of plan_decode (read per call: a benchmark
@@ -1004,8 +1181,10 @@ PassMode pass_mode() {
 }
 
 // rt: rank rows of the T work (groups * r for a grouped launch; r when negative).
+// min_splits: K splits of the W work to take at least, where the slices keep eight or more
+// whole wave steps (more W workgroups for a launch whose rows alone give few).
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick pick = Pick::kAll,
-                       int64_t rt = -1) {
+                       int64_t rt = -1, int min_splits = 1) {
   if (rt < 0) rt = r;
   DecodePlan pl{};
   pl.kpt = pl.kpy = 1;
@@ -1014,6 +1193,14 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
   pl.nr = pl.mb >= 3 ? 2 : 1;
   pl.r32 = (int)((r + 31) / 32 * 32);
   pl.ksy = fit_split(M, K, wave_k_of(wdt));
+  if (pl.ksy > 0 && min_splits > pl.ksy) {
+    const int64_t wk = wave_k_of(wdt);
+    for (int64_t s = min_splits; s > pl.ksy; --s)
+      if (s % pl.ksy == 0 && K % s == 0 && (K / s) % wk == 0 && (K / s) / wk >= 8) {
+        pl.ksy = (int)s;
+        break;
+      }
+  }
   pl.kcy = pl.ksy > 0 ? (int)(K / pl.ksy) : 0;
   if (r > 0) {
     pl.kst = fit_split(M, K, wave_k_of(kBF16));
@@ -1046,12 +1233,12 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t r, int wdt, Pick
   // Whole wave steps along K: rows per workgroup (16, 32 or 64) by the modelled time,
   // among the choices whose LDS fits. (At M = 1 and 8, 6144 x 2048 went 13.0 -> 11.3 us;
   // fp8 at M = 16, 12288 x 4096 went 40.7 -> 20.6 us: one wave of workgroups, not three.)
-  const bool can_pick = pick == Pick::kAll || (pick == Pick::kFused && pl.mb == 1);
+  const bool can_pick = pick == Pick::kAll || (pick != Pick::kAll && pl.mb == 1);
   if (can_pick && pl.kw == 8 && pl.ksy > 0 && pl.kst > 0) {
     double best = plan_cost(pl, M, N, pl.nr);
     const int legacy = pl.nr;
     for (int nr : {1, 2, 4}) {
-      if (nr == legacy) continue;
+      if (nr == legacy || (pick == Pick::kChain && nr > 2)) continue;  // chain kernels: one or two blocks
       DecodePlan c = pl;
       c.nr = nr;
       c.rows = 16 * nr;
@@ -1287,11 +1474,21 @@ bool decode_supported(const LoraArgs& p) {
   return plan_decode(p.M, p.N, p.K, p.r, p.w_dtype).ok;
 }
 
-// Covers the plain and fused launches' plans of the problem.
+// K splits of a fused launch's W work: a residual-epilogue launch (no RMSNorm prologue,
+// which needs whole rows in one slice) may take WSL_OPT_DECODE_RES_SPLITS.
+int fused_min_splits(int fuse) {
+  if (!(fuse & kFuseRes) || (fuse & kFuseNorm)) return 1;
+  const int64_t v = option(WSL_OPT_DECODE_RES_SPLITS);
+  return v > 1 ? (int)v : 1;
+}
+
+// Covers the plain and fused launches' plans of the problem (K splits of a residual
+// launch included).
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
   const size_t a = plan_decode(M, N, K, r, w_dtype).total;
   const size_t b = plan_decode(M, N, K, r, w_dtype, Pick::kFused).total;
-  return a > b ? a : b;
+  const size_t c = plan_decode(M, N, K, r, w_dtype, Pick::kFused, -1, fused_min_splits(kFuseRes)).total;
+  return std::max(a, std::max(b, c));
 }
 
 namespace {
@@ -1356,7 +1553,7 @@ hipError_t launch_decode(const LoraArgs& p) {
 bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f) {
   if (f.fuse < 1 || f.fuse > 7 || ((f.fuse & kFuseAct) && (f.fuse & kFuseRes))) return false;
   if (p.M > kDecodeMaxM || !decode_supported(p) || p.w_dtype != kBF16) return false;
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kFused);
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kFused, -1, fused_min_splits(f.fuse));
   if (!pl.ok || pl.kw != 8) return false;
   if (f.fuse & kFuseNorm) {
     // whole rows in one slice, up to NORM_CH chunks per thread, w_norm staged after the plan's LDS
@@ -1408,7 +1605,7 @@ hipError_t launch_decode_argmax(const LoraArgs& p, void* keys, int64_t* out) {
 }
 
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {
-  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kFused);
+  const DecodePlan pl = plan_decode(p.M, p.N, p.K, p.r, p.w_dtype, Pick::kFused, -1, fused_min_splits(f.fuse));
   DecodeArgs a = make_args(p, pl);
   a.nw = reinterpret_cast<const uint16_t*>(f.nw); a.eps = f.eps;
   a.nw_off = (int)pl.flag_off + 16 + kNormLds;
@@ -1424,6 +1621,152 @@ hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f) {
     default: return hipErrorInvalidValue;
   }
 }
+
+// ---- Chains ----
+namespace {
+struct ChainPlan {
+  DecodePlan pl[kChainMax];
+  size_t data[kChainMax];  // byte offset of stage s's plan region base (its plan offsets add to it)
+  size_t smem = 0, total = 0;
+  int grid = 0;
+  bool ok = false;
+};
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+// The stages' plans (the decode path's one-slice plans of one token block), the workspace
+// layout (counter prefix, the stages' flag words, then each stage's hand-off region) and
+// the LDS. `cus`: CUs of the device (0: the layout only).
+ChainPlan plan_chain(int64_t M, int n, const LoraArgs* ps, const FusedArgs* fs, int cus,
+                     const int* after_prev = nullptr) {
+  ChainPlan c;
+  if (n < 1 || n > kChainMax || M < 1 || M > 16) return c;
+  size_t off = kCounterBytes + (size_t)kChainMax * kChainFlagWords * 8;
+  int max_t = 0;
+  for (int s = 0; s < n; ++s) {
+    const LoraArgs& p = ps[s];
+    const FusedArgs& f = fs[s];
+    const int fuse = f.fuse;
+    if (fuse != 0 && fuse != kFuseNorm && fuse != (kFuseNorm | kFuseAct) && fuse != kFuseRes) return c;
+    if (fuse != 0 && p.groups != 1) return c;
+    if (p.w == nullptr || p.w_dtype != kBF16 || p.w_scale != nullptr || p.wmap.P != 0) return c;
+    if (p.M != M || p.N % 16 != 0 || !decode_supported(p)) return c;
+    const DecodePlan pl = plan_decode(M, p.N, p.K, p.r, kBF16, Pick::kChain, p.r * p.groups);
+    if (!pl.ok || pl.kw != 8 || pl.mb != 1 || pl.nr > 2 || pl.ksy != 1 || pl.kpy != 1) return c;
+    if (p.r > 0 && (pl.kst != 1 || pl.kpt != 1)) return c;
+    if (pl.gY > kChainFlagWords) return c;
+    for (int g = 0; g + 1 < p.groups; ++g)
+      if (p.gend[g] % pl.rows != 0) return c;
+    size_t smem = pl.smem;
+    if (fuse & kFuseNorm) {
+      if (p.M * (p.K / 8) > (int64_t)NORM_CH * DT || f.nw == nullptr || !aligned16(f.nw)) return c;
+      smem += (size_t)kNormLds + (size_t)p.K * 2;
+    }
+    if (fuse & kFuseRes) {
+      if (f.res == nullptr || (reinterpret_cast<uintptr_t>(f.res) & 7u) != 0 || f.ldr % 4 != 0) return c;
+    }
+    if (smem > (size_t)LDS_MAX) return c;
+    c.pl[s] = pl;
+    c.smem = std::max(c.smem, smem);
+    c.data[s] = off - kCounterBytes;
+    off += ((pl.total - kCounterBytes) + 255) & ~(size_t)255;
+    max_t = std::max(max_t, pl.gT * pl.kst);
+  }
+  // Neighbouring stages whose workgroups together exceed the CUs share some workgroups, and
+  // those run the later stage's work only after their own earlier work. In a chain of
+  // independent stages, a one-block stage (16 rows per workgroup) with such a neighbour takes
+  // 32 rows per workgroup if that removes the overlap and fits the LDS (C3, M = 1, two layers
+  // per chain: 3000 against 2514 GB/s with one layer and no widening). With dependent stages
+  // it does not: a wider first stage has no earlier stage to stream behind (config 4's decode
+  // step: 4941 against 5384 tok/s).
+  bool independent = true;
+  for (int q = 1; q < n; ++q) independent = independent && (after_prev == nullptr || after_prev[q] == 0);
+  if (cus > 0) {
+    const auto nvb = [&](int q) { return c.pl[q].gT * c.pl[q].kst + c.pl[q].gY * c.pl[q].ksy; };
+    for (int q = 0; q < n && independent && after_prev != nullptr; ++q) {
+      DecodePlan& pl = c.pl[q];
+      const int prev = q > 0 ? nvb(q - 1) : 0, next = q + 1 < n ? nvb(q + 1) : 0;
+      if (pl.nr != 1 || (prev + nvb(q) <= cus && next + nvb(q) <= cus)) continue;
+      DecodePlan w = pl;
+      w.nr = 2;
+      w.rows = 32;
+      w.gY = (int)((ps[q].N + 31) / 32);
+      const int wv = w.gT * w.kst + w.gY * w.ksy;
+      size_t fo;
+      const size_t sm = plan_smem(w, M, &fo) + ((fs[q].fuse & kFuseNorm) ? (size_t)kNormLds + (size_t)ps[q].K * 2 : 0);
+      bool fits = sm <= (size_t)LDS_MAX;
+      for (int g = 0; g + 1 < ps[q].groups; ++g) fits = fits && ps[q].gend[g] % 32 == 0;
+      if (!fits || prev + wv > cus || next + wv > cus) continue;
+      w.smem = plan_smem(w, M, &w.flag_off);
+      pl = w;  // the hand-off regions do not depend on the rows per workgroup (one K slice)
+      c.smem = std::max(c.smem, sm);
+    }
+    int mv = 0;
+    for (int q = 0; q < n; ++q) mv = std::max(mv, nvb(q));
+    c.grid = std::min(cus, mv);
+    if (c.grid < max_t) return c;  // every T workgroup in the first round
+  }
+  c.total = off;
+  c.ok = true;
+  return c;
+}
+}  // namespace
+
+bool decode_chain_supported(int64_t M, int n, const LoraArgs* ps, const FusedArgs* fs) {
+  return plan_chain(M, n, ps, fs, 0).ok;
+}
+
+size_t decode_chain_workspace_bytes(int64_t M, int n, const LoraArgs* ps, const FusedArgs* fs) {
+  const ChainPlan c = plan_chain(M, n, ps, fs, 0);
+  return c.ok ? c.total : 0;
+}
+
+hipError_t launch_decode_chain(int64_t M, int n, const LoraArgs* ps, const FusedArgs* fs, const int* after_prev,
+                               void* ws, hipStream_t stream) {
+  const ChainPlan c = plan_chain(M, n, ps, fs, device_cus(), after_prev);
+  if (!c.ok || c.grid < 1) return hipErrorInvalidValue;
+  char* base = reinterpret_cast<char*>(ws);
+  uint64_t* flags = reinterpret_cast<uint64_t*>(base + kCounterBytes);
+  ChainArgs a{};
+  a.n = n;
+  a.cnt = reinterpret_cast<unsigned*>(base);
+  for (int s = 0; s < n; ++s) {
+    const DecodePlan& pl = c.pl[s];
+    DecodeArgs d = make_args(ps[s], pl, base, base + c.data[s]);
+    d.nw = reinterpret_cast<const uint16_t*>(fs[s].nw);
+    d.eps = fs[s].eps;
+    d.nw_off = (int)pl.flag_off + 16 + kNormLds;
+    d.res = reinterpret_cast<const uint16_t*>(fs[s].res);
+    d.ldr = fs[s].ldr;
+    ChainStage& st = a.st[s];
+    st.a = d;
+    st.fuse = fs[s].fuse;
+    st.nr = pl.nr;
+    st.nvb = pl.gT * pl.kst + pl.gY * pl.ksy;
+    st.rot = s > 0 ? (a.st[s - 1].rot + a.st[s - 1].nvb) % c.grid : 0;
+    st.ctl.flags = flags + (size_t)s * kChainFlagWords;
+    st.ctl.prev_flags = (s > 0 && after_prev[s]) ? flags + (size_t)(s - 1) * kChainFlagWords : nullptr;
+    st.ctl.prev_n = s > 0 ? c.pl[s - 1].gY : 0;
+    st.ctl.err = reinterpret_cast<unsigned*>(base + kChainErrOff);
+    st.ctl.spin = d.spin;
+  }
+  const hipError_t e = allow_full_lds<chain_kernel>();
+  if (e != hipSuccess) return e;
+  chain_kernel<<<dim3((unsigned)c.grid), dim3(DT), c.smem, stream>>>(a);
+  return hipGetLastError();
+}
+
+size_t decode_chain_err_offset() { return kChainErrOff; }
 
 }  // namespace wsl
 

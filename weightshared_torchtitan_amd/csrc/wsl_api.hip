@@ -353,6 +353,7 @@ int wsl_set_option(int32_t option, int64_t value) {
     case WSL_OPT_FP8_PREFILL: ok = value == 0 || value == 1; break;
     case WSL_OPT_DECODE_PASSES: ok = value >= -1 && value <= 1; break;
     case WSL_OPT_DECODE_SPIN_LIMIT: ok = value >= -1 && value <= ((int64_t)1 << 30); break;
+    case WSL_OPT_DECODE_RES_SPLITS: ok = value == 0 || (value >= 2 && value <= 8); break;
     default: return fail(WSL_E_INVALID_ARG, "unknown option %d", (int)option);
   }
   if (!ok) return fail(WSL_E_INVALID_ARG, "value %lld out of range for option %d", (long long)value, (int)option);
@@ -675,6 +676,124 @@ int wsl_lora_linear_fused_fwd(const void* x, int64_t ldx, const void* norm_w, fl
   p.ws_bytes = wsl::kCounterBytes + half_of(workspace_bytes);
   const hipError_t e = wsl::launch_decode_fused(p, f);
   if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
+}  // extern "C"
+
+namespace {
+// A chain's stages as launch arguments, after the checks that need no plan; the plan's own
+// checks (shapes, alignment) follow in wsl::decode_chain_supported.
+int chain_args(int64_t M, int32_t n, const wsl_chain_stage* st, wsl::LoraArgs* ps, wsl::FusedArgs* fs, int* after) {
+  if (n < 1 || n > WSL_CHAIN_MAX_STAGES)
+    return fail(WSL_E_SHAPE, "n_stages must be in [1, %d] (got %d)", WSL_CHAIN_MAX_STAGES, (int)n);
+  if (st == nullptr) return fail(WSL_E_INVALID_ARG, "stages must not be NULL");
+  if (M < 1 || M > 16) return fail(WSL_E_SHAPE, "chains take 1 <= M <= 16 (got %lld)", (long long)M);
+  for (int s = 0; s < n; ++s) {
+    const wsl_chain_stage& c = st[s];
+    int rc = validate_sizes(M, c.N, c.K, c.r, WSL_DTYPE_BF16);
+    if (rc != WSL_OK) return rc;
+    const int fuse = c.fuse;
+    if (fuse != 0 && fuse != WSL_FUSE_RMSNORM && fuse != (WSL_FUSE_RMSNORM | WSL_FUSE_SWIGLU) &&
+        fuse != WSL_FUSE_RESIDUAL)
+      return fail(WSL_E_INVALID_ARG, "stage %d: fuse must be 0, RMSNORM, RMSNORM|SWIGLU or RESIDUAL", s);
+    if (c.x == nullptr || c.w == nullptr || c.y == nullptr)
+      return fail(WSL_E_INVALID_ARG, "stage %d: x, w and y must not be NULL", s);
+    if (c.r > 0 && (c.a == nullptr || c.b == nullptr)) return fail(WSL_E_INVALID_ARG, "stage %d: r > 0 needs a and b", s);
+    if ((fuse & WSL_FUSE_RMSNORM) && c.norm_w == nullptr) return fail(WSL_E_INVALID_ARG, "stage %d: norm_w is NULL", s);
+    if ((fuse & WSL_FUSE_RESIDUAL) && c.residual == nullptr)
+      return fail(WSL_E_INVALID_ARG, "stage %d: residual is NULL", s);
+    if (c.after_previous != 0 && c.after_previous != 1)
+      return fail(WSL_E_INVALID_ARG, "stage %d: after_previous must be 0 or 1", s);
+    const int g = c.n_groups;
+    if (g < 1 || g > WSL_MAX_GROUPS || (fuse != 0 && g != 1))
+      return fail(WSL_E_SHAPE, "stage %d: n_groups must be 1 with a fusion, 1..%d without", s, WSL_MAX_GROUPS);
+    int64_t end = 0;
+    wsl::LoraArgs p = make_args(c.x, c.ldx, c.w, c.ldw, WSL_DTYPE_BF16, nullptr, c.a, c.lda, c.b, c.ldb, c.scale,
+                                c.y, c.ldy, M, c.N, c.K, c.r, nullptr);
+    p.groups = g;
+    for (int q = 0; q < g; ++q) {
+      if (c.group_n[q] < 1) return fail(WSL_E_SHAPE, "stage %d: group %d has width %lld", s, q, (long long)c.group_n[q]);
+      p.gend[q] = (end += c.group_n[q]);
+    }
+    if (g > 1 && end != c.N) return fail(WSL_E_SHAPE, "stage %d: the group widths sum to %lld, not N", s, (long long)end);
+    const int64_t ny = (fuse & WSL_FUSE_SWIGLU) ? c.N / 2 : c.N;
+    if (c.ldx < c.K || c.ldw < c.K || (c.r > 0 && (c.lda < c.K || c.ldb < c.r)) || c.ldy < ny ||
+        ((fuse & WSL_FUSE_RESIDUAL) && c.ldr < c.N))
+      return fail(WSL_E_SHAPE, "stage %d: leading dimension too small", s);
+    ps[s] = p;
+    fs[s] = wsl::FusedArgs{fuse, c.norm_w, c.eps, c.residual, c.ldr};
+    after[s] = s > 0 ? c.after_previous : 0;
+  }
+  return WSL_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int wsl_lora_linear_chain_supported(int64_t M, int32_t n_stages, const wsl_chain_stage* stages) {
+  wsl::LoraArgs ps[WSL_CHAIN_MAX_STAGES];
+  wsl::FusedArgs fs[WSL_CHAIN_MAX_STAGES];
+  int after[WSL_CHAIN_MAX_STAGES];
+  const bool ok = chain_args(M, n_stages, stages, ps, fs, after) == WSL_OK &&
+                  wsl::decode_chain_supported(M, n_stages, ps, fs);
+  clear_err();  // a query leaves no error behind
+  return ok ? 1 : 0;
+}
+
+int wsl_lora_linear_chain_workspace_bytes(int64_t M, int32_t n_stages, const wsl_chain_stage* stages, size_t* bytes) {
+  clear_err();
+  if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
+  wsl::LoraArgs ps[WSL_CHAIN_MAX_STAGES];
+  wsl::FusedArgs fs[WSL_CHAIN_MAX_STAGES];
+  int after[WSL_CHAIN_MAX_STAGES];
+  const int rc = chain_args(M, n_stages, stages, ps, fs, after);
+  if (rc != WSL_OK) return rc;
+  if (!wsl::decode_chain_supported(M, n_stages, ps, fs))
+    return fail(WSL_E_SHAPE, "a stage's shape or alignment is not taken by chains (wsl_lora_linear_chain_supported)");
+  *bytes = wsl::decode_chain_workspace_bytes(M, n_stages, ps, fs);
+  return WSL_OK;
+}
+
+int wsl_lora_linear_chain_fwd(int64_t M, int32_t n_stages, const wsl_chain_stage* stages, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  clear_err();
+  wsl::LoraArgs ps[WSL_CHAIN_MAX_STAGES];
+  wsl::FusedArgs fs[WSL_CHAIN_MAX_STAGES];
+  int after[WSL_CHAIN_MAX_STAGES];
+  int rc = chain_args(M, n_stages, stages, ps, fs, after);
+  if (rc != WSL_OK) return rc;
+  if (!wsl::decode_chain_supported(M, n_stages, ps, fs))
+    return fail(WSL_E_SHAPE, "a stage's shape or alignment is not taken by chains (wsl_lora_linear_chain_supported)");
+  const size_t need = wsl::decode_chain_workspace_bytes(M, n_stages, ps, fs);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((uintptr_t)workspace & 255) return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
+  rc = check_device();
+  if (rc != WSL_OK) return rc;
+  const hipError_t e = wsl::launch_decode_chain(M, n_stages, ps, fs, after, workspace,
+                                                reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
+int wsl_lora_linear_chain_status(void* workspace, void* stream, int32_t* failed) {
+  clear_err();
+  if (workspace == nullptr || failed == nullptr) return fail(WSL_E_INVALID_ARG, "workspace and failed must not be NULL");
+  const int rc = check_device();
+  if (rc != WSL_OK) return rc;
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  unsigned* word = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(workspace) + wsl::decode_chain_err_offset());
+  unsigned v = 0;
+  hipError_t e = hipMemcpyAsync(&v, word, sizeof(v), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e == hipSuccess && v != 0) {
+    const unsigned zero = 0;
+    e = hipMemcpyAsync(word, &zero, sizeof(zero), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+  }
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "reading the chain status failed: %s", hipGetErrorString(e));
+  *failed = v != 0 ? 1 : 0;
   return WSL_OK;
 }
 

@@ -209,6 +209,15 @@ struct FusedArgs {
 };
 bool decode_fused_supported(const LoraArgs& p, const FusedArgs& f);
 hipError_t launch_decode_fused(const LoraArgs& p, const FusedArgs& f);
+// A chain of decode launches in one persistent launch (n stages, each a LoraArgs with its
+// FusedArgs; fuse 0 is the plain or grouped form). after_prev[s]: stage s waits for stage
+// s - 1. The workspace holds the counter prefix, the stages' flag words and their hand-off
+// regions; its sticky failure word is a 32-bit word at decode_chain_err_offset().
+bool decode_chain_supported(int64_t M, int n, const LoraArgs* ps, const FusedArgs* fs);
+size_t decode_chain_workspace_bytes(int64_t M, int n, const LoraArgs* ps, const FusedArgs* fs);
+hipError_t launch_decode_chain(int64_t M, int n, const LoraArgs* ps, const FusedArgs* fs, const int* after_prev,
+                               void* ws, hipStream_t stream);
+size_t decode_chain_err_offset();
 // The tied output head fused with the greedy argmax: out[m] = argmax_n bf16(x[m] . W[n]),
 // no logits written. `keys` holds one 256-byte slot per token (64-bit key; the slot of
 // token 0 also holds the arrival counter at byte 128), zero before a launch and after it.

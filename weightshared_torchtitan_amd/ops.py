@@ -1084,3 +1084,95 @@ def _lora_linear_fused_fake(x, norm_w, eps, w, a, b, scale, residual, fuse):
     M = x.reshape(-1, x.shape[-1]).shape[0]
     ny = w.shape[0] // 2 if fuse & 2 else w.shape[0]
     return x.new_empty((M, ny), dtype=torch.bfloat16)
+
+
+
+# ------------------------------------------------------------------------------------------
+# Chains: several decode-shaped LoRA linears in one persistent launch
+# (wsl_lora_linear_chain_fwd, include/wsl_decode.h). Inference only (no autograd): the decode
+# step of the weight-shared Qwen3 harness runs o, gate|up, down and the next layer's q|k|v as
+# one chain between two attention steps.
+# ------------------------------------------------------------------------------------------
+class ChainStage:
+    """One stage of a chain: ``y = fused(x; w, a, b, scale)`` as wsl::lora_linear_fused with
+    ``fuse`` (WSL_FUSE_* flags; 0 = the plain or grouped LoRA linear over ``group_n``).
+    ``y`` is written in place (allocate it before the call); ``after_previous`` marks a stage
+    whose x or residual is an earlier stage's y."""
+
+    def __init__(self, x, w, a, b, scale, y, fuse=0, norm_w=None, eps=0.0, residual=None, group_n=None,
+                 after_previous=False):
+        self.x, self.w, self.a, self.b, self.scale, self.y = x, w, a, b, float(scale), y
+        self.fuse, self.norm_w, self.eps, self.residual = int(fuse), norm_w, float(eps), residual
+        self.group_n = list(group_n) if group_n else [w.shape[0]]
+        self.after_previous = bool(after_previous)
+
+    def _c(self, M: int) -> "_native.ChainStage":
+        c = _native.ChainStage()
+        x2 = self.x.reshape(M, -1)
+        c.x, c.ldx = x2.data_ptr(), x2.stride(0)
+        c.norm_w = _dev_ptr(self.norm_w)
+        c.eps = self.eps
+        c.w, c.ldw = self.w.data_ptr(), self.w.stride(0)
+        r = 0
+        if self.a is not None:
+            r = self.b.shape[1]
+            c.a, c.lda, c.b, c.ldb = self.a.data_ptr(), self.a.stride(0), self.b.data_ptr(), self.b.stride(0)
+        c.scale = self.scale
+        if self.residual is not None:
+            res2 = self.residual.reshape(M, -1)
+            c.residual, c.ldr = res2.data_ptr(), res2.stride(0)
+        y2 = self.y.reshape(M, -1)
+        c.y, c.ldy = y2.data_ptr(), y2.stride(0)
+        c.N, c.K, c.r = self.w.shape[0], self.w.shape[1], r
+        c.fuse = self.fuse
+        c.n_groups = len(self.group_n)
+        for i, n in enumerate(self.group_n):
+            c.group_n[i] = int(n)
+        c.after_previous = 1 if self.after_previous else 0
+        return c
+
+
+def _chain_array(stages, M):
+    arr = (_native.ChainStage * len(stages))(*[st._c(M) for st in stages])
+    return arr
+
+
+def chain_supported(stages, M: int) -> bool:
+    """Whether one chain launch takes these stages at M tokens (wsl_lora_linear_chain_supported)."""
+    if not 1 <= len(stages) <= _native.WSL_CHAIN_MAX_STAGES:
+        return False
+    return bool(_native.lib().wsl_lora_linear_chain_supported(M, len(stages), _chain_array(stages, M)))
+
+
+def lora_linear_chain(stages, M: int) -> None:
+    """Runs the stages as one persistent launch on the current stream (each stage's y is
+    written; results equal the per-stage fused or grouped calls bit for bit). Raises if the
+    chain is not supported (chain_supported)."""
+    dev = _check_device(*[st.x for st in stages], *[st.y for st in stages])
+    arr = _chain_array(stages, M)
+    L = _native.lib()
+    need = ctypes.c_size_t(0)
+    _native.check(L.wsl_lora_linear_chain_workspace_bytes(M, len(stages), arr, ctypes.byref(need)),
+                  "wsl_lora_linear_chain_workspace_bytes")
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = workspace(dev, stream, int(need.value), kind="chain")
+    with torch.cuda.device(dev):
+        rc = L.wsl_lora_linear_chain_fwd(M, len(stages), arr, ws.data_ptr(), ws.numel(), stream)
+    if rc == _native.WSL_E_LAUNCH:
+        _retire((dev.index, stream, "chain"))
+    _native.check(rc, "wsl_lora_linear_chain_fwd")
+
+
+def chain_status(dev: Optional[torch.device] = None) -> bool:
+    """True when a chain launch on the current stream's workspace gave up a stage wait since
+    the last call (the sticky failure word, then cleared); synchronizes the stream."""
+    dev = dev or torch.device("cuda", torch.cuda.current_device())
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = _workspaces.get((dev.index, stream, "chain"))
+    if ws is None:
+        return False
+    failed = ctypes.c_int32(0)
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().wsl_lora_linear_chain_status(ws.data_ptr(), stream, ctypes.byref(failed)),
+                      "wsl_lora_linear_chain_status")
+    return bool(failed.value)

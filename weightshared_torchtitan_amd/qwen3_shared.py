@@ -393,11 +393,83 @@ class SharedQwen3(nn.Module):
 
     decode_fusion = True  # use the fused decode-step launches where _fusion_plan allows
 
+    # Run each layer's o, gate|up and down projections and the next layer's q|k|v (the head's
+    # first factor after the last layer) as one chain launch between two attention steps,
+    # where the library takes the chain (wsl_lora_linear_chain_fwd; same results bit for bit):
+    # 58 launches per step instead of 142. Off by default: at config 4 it measured at parity
+    # with the separate launches (5409 against 5440 tok/s, one box), the stage waits inside
+    # the launch costing about what the launch boundaries did.
+    decode_chain = False
+
+    def _chain_layer_stages(self, l, o, h, nxt, pk, outs):
+        """The chain of layer l: o (+ residual h) -> gate|up (RMSNorm, SwiGLU) -> down
+        (+ residual) -> `nxt` = (x-consuming weights of the next launch: the next layer's
+        q|k|v with its RMSNorm, or the head's first factor with the final RMSNorm)."""
+        from ._native import WSL_FUSE_RESIDUAL as RES, WSL_FUSE_RMSNORM as NORM, WSL_FUSE_SWIGLU as ACT
+        a = self.args
+        blk = self.base_blocks[a.block_of(l)]
+        lo = self.layer_loras[l]
+        h1, act, h2, y4 = outs
+        Ag, Bg, sg = pk["l_gu_il"][l]
+        S = ops.ChainStage
+        nw, w, A, B, sc = nxt
+        return [S(o, blk.base("wo").weight, lo.wo.w_a.weight, lo.wo.w_b.weight, lo.wo.scale, h1, fuse=RES,
+                  residual=h),
+                S(h1, pk["w_gu_il"][a.block_of(l)], Ag, Bg, sg, act, fuse=NORM | ACT, norm_w=blk.ffn_norm.weight,
+                  eps=a.norm_eps, after_previous=True),
+                S(act, blk.base("w2").weight, lo.w2.w_a.weight, lo.w2.w_b.weight, lo.w2.scale, h2, fuse=RES,
+                  residual=h1, after_previous=True),
+                S(h2, w, A, B, sc, y4, fuse=NORM, norm_w=nw, eps=a.norm_eps, after_previous=True)]
+
+    def _decode_step_chain(self, h, pos, cache, pk, rope):
+        """The fused decode step with chain launches: q|k|v of layer 0, then per layer the
+        attention step and one chain (o, gate|up, down, and the next layer's q|k|v or the
+        head's first factor). Returns None where the library does not take the chain."""
+        a = self.args
+        b = h.shape[0]
+        sm_scale = a.head_dim ** -0.5
+        fl = ops.lora_linear_fused_op
+        dev = h.device
+        qkv_n = (a.n_heads + 2 * a.n_kv_heads) * a.head_dim
+
+        def nxt_of(l):
+            if l + 1 < a.n_layers:
+                A, B, sc = pk["l_qkv"][l + 1]
+                nb = self.base_blocks[a.block_of(l + 1)]
+                return nb.attention_norm.weight, pk["w_qkv"][a.block_of(l + 1)], A, B, sc
+            return self.norm.weight, self.tok_embeddings.proj_t(), None, None, 0.0
+
+        def outs_of(l):
+            e = lambda n: torch.empty(b, n, dtype=torch.bfloat16, device=dev)  # noqa: E731
+            return e(a.dim), e(a.hidden_dim), e(a.dim), e(qkv_n if l + 1 < a.n_layers else a.embed_rank)
+
+        o_probe = torch.empty(b, a.n_heads * a.head_dim, dtype=torch.bfloat16, device=dev)
+        for l in (0, a.n_layers - 1):  # every layer's chain has one of these two shapes
+            if not ops.chain_supported(self._chain_layer_stages(l, o_probe, h, nxt_of(l), pk, outs_of(l)), b):
+                return None
+        blk = self.base_blocks[a.block_of(0)]
+        A, B, sc = pk["l_qkv"][0]
+        qkv = fl(h, blk.attention_norm.weight, a.norm_eps, pk["w_qkv"][a.block_of(0)], A, B, sc, None, 1)
+        for l in range(a.n_layers):
+            blk = self.base_blocks[a.block_of(l)]
+            o = ops.decode_attention_step_op(qkv, blk.attention.q_norm.weight, blk.attention.k_norm.weight,
+                                             a.norm_eps, rope, pos, cache.k[l], cache.v[l], a.n_heads,
+                                             a.n_kv_heads, sm_scale)
+            outs = outs_of(l)
+            ops.lora_linear_chain(self._chain_layer_stages(l, o, h, nxt_of(l), pk, outs), b)
+            h, qkv = outs[2], outs[3]
+        return qkv  # after the last layer: z = rmsnorm(h) . P
+
     def _decode_step_fused(self, h, pos, cache, pk, rope) -> torch.Tensor:
         """The decode step in fused launches up to the head input z = rmsnorm(h) . P [b, k]:
         q|k|v (RMSNorm prologue), the fused attention step, o projection (+ residual),
         gate|up (RMSNorm prologue, SwiGLU epilogue), down projection (+ residual); then the
-        head's first factor with the final RMSNorm."""
+        head's first factor with the final RMSNorm. With decode_chain, the projections
+        between two attention steps run as one chain launch."""
+        if self.decode_chain:
+            z = self._decode_step_chain(h, pos, cache, pk, rope)
+            if z is not None:
+                return z
         a = self.args
         b = h.shape[0]
         sm_scale = a.head_dim ** -0.5
