@@ -154,8 +154,10 @@ int wsl_tied_head_argmax_fwd(const void* x, int64_t ldx, const void* w, int64_t 
  *
  * Shapes taken (wsl_lora_linear_chain_supported, from the sizes and pointer alignment):
  * 1 <= M <= 16, bf16 W, 1 <= n_stages <= WSL_CHAIN_MAX_STAGES; each stage the decode path's
- * one-slice plan (x, A and B rows in one K slice: M * K * 2 bytes within the LDS budget, K a
- * multiple of 1024), N a multiple of 16 and at most 16384 rows, 16-byte aligned operands.
+ * one-slice plan (x, A and B rows in one K slice: M * K * 2 bytes within the LDS budget; K a
+ * multiple of 128 and at least 1024), N a multiple of 16 and at most 1024 output row blocks
+ * (16 or 32 rows each, 16384 rows at least), 16-byte aligned operands. Errors are reported
+ * by wsl_last_error().
  *
  * Waits are bounded. A stage wait that gives up sets a sticky failure word in the workspace
  * and the launch still drains (its outputs are then not valid);
