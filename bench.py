@@ -752,6 +752,15 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
                      "frac_mfma": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
     from weightshared_torchtitan_amd import ops
 
+    def torch_weight_grads(x2, gy2, a, b, s):
+        """The same three products on torch GEMMs (hipBLASLt), the vendor comparison:
+        dW = gy^T x, dA = s (gy B)^T x, dB = s gy^T (x A^T)."""
+        gt = gy2.t()
+        dw = gt @ x2
+        da = ((gy2 @ b) * s).t() @ x2
+        db = gt @ ((x2 @ a.t()) * s)
+        return dw, da, db
+
     def wg_ms(fn):
         for _ in range(warmup):
             fn()
@@ -770,7 +779,7 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
         x2, gy2 = xs[0][K].detach(), gys[i]
         a, b = lor[0][i][0].detach(), lor[0][i][1].detach()
         hip = wg_ms(lambda: ops.lora_linear_weight_grads_op(x2, gy2, a, b, 2.0, True, True, True))
-        tch = wg_ms(lambda: ops._weight_grads_torch(x2, gy2, a, b, 2.0, True, True, True))
+        tch = wg_ms(lambda: torch_weight_grads(x2, gy2, a, b, 2.0))
         fl = 2.0 * M * (N * K + r * (N + K)) + 2.0 * M * r * (N + K)  # dW, dA, dB + the T, U pre-passes
         wg[name] = {"N": N, "K": K, "hip_ms": round(hip, 4), "torch_ms": round(tch, 4),
                     "hip_TFLOP/s": round(fl / hip / 1e9, 1), "torch_TFLOP/s": round(fl / tch / 1e9, 1)}
@@ -782,7 +791,7 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
     a = (torch.randn(r, 4096, device=dev, generator=g) * 0.02).bfloat16()
     b = (torch.randn(4096, r, device=dev, generator=g) * 0.02).bfloat16()
     hip = wg_ms(lambda: ops.lora_linear_weight_grads_op(x2, gy2, a, b, 2.0, True, True, True))
-    tch = wg_ms(lambda: ops._weight_grads_torch(x2, gy2, a, b, 2.0, True, True, True))
+    tch = wg_ms(lambda: torch_weight_grads(x2, gy2, a, b, 2.0))
     fl = 2.0 * M * (4096 * 4096 + r * 8192) + 2.0 * M * r * 8192
     out["weight_grads"] = {"per_projection": wg, "layer_hip_ms": round(tot_hip, 4),
                            "layer_torch_ms": round(tot_torch, 4),

@@ -782,14 +782,26 @@ __device__ __forceinline__ void chain_wait(const ChainCtl* c, uint64_t tag) {
   if (c->prev_flags == nullptr) return;
   if (threadIdx.x < 64) {
     const uint64_t want = chain_flag_of(tag);
+    // up to 8 flags per lane requested together (one round trip for 512 flags), then each
+    // one not yet set is polled
+    constexpr int FB = 8;
     bool ok = true;
-    for (int i = threadIdx.x; i < c->prev_n; i += 64) {
-      uint64_t v = ld_agent(c->prev_flags + i);
-      for (int it = 0; v != want && it < c->spin; ++it) {
-        __builtin_amdgcn_s_sleep(1);
-        v = ld_agent(c->prev_flags + i);
+    for (int i0 = 0; i0 < c->prev_n; i0 += 64 * FB) {
+      uint64_t v[FB];
+#pragma unroll
+      for (int u = 0; u < FB; ++u) {
+        const int i = i0 + u * 64 + (int)threadIdx.x;
+        v[u] = i < c->prev_n ? ld_agent(c->prev_flags + i) : want;
       }
-      ok = ok && v == want;
+#pragma unroll
+      for (int u = 0; u < FB; ++u) {
+        const int i = i0 + u * 64 + (int)threadIdx.x;
+        for (int it = 0; v[u] != want && it < c->spin; ++it) {
+          __builtin_amdgcn_s_sleep(1);
+          v[u] = ld_agent(c->prev_flags + i);
+        }
+        ok = ok && v[u] == want;
+      }
     }
     if (!ok) __hip_atomic_fetch_or(c->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
