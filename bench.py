@@ -334,6 +334,52 @@ AB_SHAPES = [("c2 q|k|v", 8192, (2048, 1024, 1024), 1024), ("c2 o", 8192, (1024,
              ("1.7b gate|up", 8192, (6144, 6144), 2048), ("1.7b down", 8192, (2048,), 6144)]
 
 
+def bench_data(dev, names=("c2 q|k|v", "1.7b gate|up", "1.7b down"), launches=28, rounds=6):
+    """The same prefill launches (the fused op, and torch.mm on hipBLASLt for the base GEMM
+    alone) on operands of different value statistics and identical shapes, layouts and
+    memory traffic: x ~ N(0, 1) and W ~ N(0, 0.02^2) as every benchmark here uses, x zero,
+    W zero, x all ones, half of x's rows zero. The chip's clock is set by its power budget,
+    and the power drawn depends on how many operand bits switch, so these times differ while
+    the work does not. One HIP graph of `launches` launches per variant, the graphs
+    replayed in alternating order, the median of `rounds` rounds (us per launch)."""
+    from weightshared_torchtitan_amd import ops
+    out = {}
+    for name, M, ns, K in AB_SHAPES:
+        if name not in names:
+            continue
+        r = 32
+        g = torch.Generator(device=dev).manual_seed(M + sum(ns) + K)
+        xr = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        wr = (torch.randn(sum(ns), K, device=dev, generator=g) * 0.02).bfloat16()
+        a = (torch.randn(len(ns) * r, K, device=dev, generator=g) * 0.02).bfloat16()
+        b = (torch.randn(sum(ns), r, device=dev, generator=g) * 0.02).bfloat16()
+        half = (torch.rand(M, 1, device=dev, generator=g) < 0.5).bfloat16()
+        data = {"randn": (xr, wr), "x_zero": (torch.zeros_like(xr), wr), "w_zero": (xr, torch.zeros_like(wr)),
+                "x_ones": (torch.ones_like(xr), wr), "x_half_rows_zero": (xr * half, wr)}
+        graphs = {}
+        for v, (x, w) in data.items():
+            if len(ns) > 1:
+                fn = lambda x=x, w=w: ops.lora_linear_grouped_op(x, w, None, a, b, 2.0, list(ns))  # noqa: E731
+            else:
+                fn = lambda x=x, w=w: ops.lora_linear_op(x, w, None, a, b, 2.0)  # noqa: E731
+            graphs["wsl " + v] = graph_of(lambda fn=fn: [fn() for _ in range(launches)])
+            if v in ("randn", "x_zero"):
+                wt = w.t()
+                graphs["hipblaslt_base_gemm " + v] = graph_of(lambda x=x, wt=wt: [torch.mm(x, wt) for _ in range(launches)])
+        times = {k: [] for k in graphs}
+        for _ in range(rounds):
+            for k, gr in graphs.items():
+                times[k].append(time_replays(gr, 3, 1) * 1e3 / launches)
+        fl = sum(lora_flops(M, n, K, r) for n in ns)  # the base GEMM alone: r = 0
+        flb = sum(lora_flops(M, n, K, 0) for n in ns)
+        out[name] = {k: {"us": round(sorted(t)[len(t) // 2], 2),
+                         "TFLOP/s": round((flb if k.startswith("hipblaslt") else fl) / (sorted(t)[len(t) // 2] * 1e-6) / 1e12, 1)}
+                     for k, t in times.items()}
+        del graphs, data, xr, wr, a, b
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_env_ab(dev, modes, names=None, launches=28, rounds=6):
     """Side-by-side timing of libwsl's path overrides (ops.path_options: prefill_strips,
     prefill_split, ...): per launch shape one HIP graph of `launches` launches is captured
@@ -1000,7 +1046,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=("c1", "c2", "c2single", "c2_1p7b", "c3", "c4", "c5", "c5paths", "emb",
-                                       "vendor", "backward", "medium", "shape", "envab", "stamps"), default=None)
+                                       "vendor", "backward", "medium", "shape", "envab", "stamps", "data"), default=None)
     ap.add_argument("--shape", default="8192,2048,6144,0", help="M,N,K,r for --only shape")
     ap.add_argument("--vendor", action="store_true", help="--only shape: torch.matmul instead of the fused op")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -1041,7 +1087,8 @@ def main():
               "shape": lambda: run_shape(dev, tuple(int(v) for v in args.shape.split(",")), args.vendor),
               "envab": lambda: bench_env_ab(dev, json.loads(args.ab),
                                             args.ab_shapes.split(",") if args.ab_shapes else None),
-              "stamps": lambda: bench_stamps(dev, args.ab_shapes.split(",") if args.ab_shapes else None)}[args.only]
+              "stamps": lambda: bench_stamps(dev, args.ab_shapes.split(",") if args.ab_shapes else None),
+              "data": lambda: bench_data(dev)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
     flops, ms, ms_single = bench_c2(dev, args.steps, args.warmup, grouped=args.only != "c2single",
