@@ -659,9 +659,11 @@ def bench_medium(dev, steps, warmup):
 
 
 def bench_c5_paths(dev, steps, warmup):
-    """Config 5 at M = 4096 on each fp8 prefill path, same inputs: the fp8 matrix cores with
-    two activation terms (the default), with one term (the opt-in WSL_DTYPE_FP8_E4M3_ACT8),
-    and W decoded onto the bf16 matrix cores (the fp8_prefill override at 1)."""
+    """Config 5 at M = 4096 on each fp8 prefill path, same inputs: the default (two activation
+    terms on the fp8 matrix cores for launches wider than one wave of 256 x 256 tiles, W
+    decoded onto the bf16 matrix cores for the rest), every launch on the fp8 matrix cores
+    with two terms (the fp8_prefill override at 2), with one term (the opt-in
+    WSL_DTYPE_FP8_E4M3_ACT8), and every launch with W decoded (the override at 1)."""
     from weightshared_torchtitan_amd import ops
     st = ProjectionStack(QWEN3_8B, M=4096, r=128, layers=1, dev=dev, seed=5, copies=1, fp8=True, scale=1.0)
     st.stack_groups()
@@ -671,8 +673,8 @@ def bench_c5_paths(dev, steps, warmup):
     out = {}
     saved = ops.FP8_ACTIVATIONS
     try:
-        for name, act8, weight_only in (("fp8_mfma_two_term", False, 0), ("fp8_mfma_one_term", True, 0),
-                                        ("weight_only_bf16_mfma", False, 1)):
+        for name, act8, weight_only in (("default", False, 0), ("fp8_mfma_two_term", False, 2),
+                                        ("fp8_mfma_one_term", True, 0), ("weight_only_bf16_mfma", False, 1)):
             ops.FP8_ACTIVATIONS = act8
             row = {}
             for label, fn in (("per_projection", st.run), ("grouped_qkv_gateup", st.run_grouped)):

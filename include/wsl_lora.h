@@ -145,8 +145,10 @@ int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx,
  * suffice), the T work covering all groups' A rows. Otherwise the groups run as consecutive
  * launches on `stream`. Results are those of the per-group calls, bit for bit, except where
  * a K split count depends on N (the decode path between 65 and 72 tokens; the prefill
- * path's in-launch split-K form, taken where 128 x 128 tiles leave CUs idle): there the
- * groups' outputs agree with the per-group calls within the forward's bar.
+ * path's in-launch split-K form, taken where 128 x 128 tiles leave CUs idle) or, for an fp8
+ * W on prefill shapes, where the choice between the fp8 matrix cores and W decoded onto the
+ * bf16 matrix cores depends on the launch's width (WSL_OPT_FP8_PREFILL): there the groups'
+ * outputs agree with the per-group calls within the forward's bar.
  */
 #define WSL_MAX_GROUPS 4
 int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int32_t n_groups,
@@ -252,7 +254,10 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
  *   WSL_OPT_PREFILL_SPLIT      0 auto; -1 never split K inside a launch; n in [2, 16] that
  *                              split count wherever it divides the K tiles and fits
  *   WSL_OPT_PREFILL_MEDIUM     0 auto; -1 never take the medium-M split form
- *   WSL_OPT_FP8_PREFILL        0 fp8 matrix cores; 1 W decoded onto the bf16 matrix cores
+ *   WSL_OPT_FP8_PREFILL        0 auto (two activation terms on the fp8 matrix cores where
+ *                              the launch has more 256 x 256 tiles than CUs, else W decoded
+ *                              onto the bf16 matrix cores); 1 always decoded; 2 always the
+ *                              fp8 matrix cores
  *   WSL_OPT_DECODE_PASSES      0 auto; -1 K splits only; 1 passes wherever the slices allow
  *   WSL_OPT_DECODE_WIDE        0 auto; -1 keep 65-72 tokens on the prefill path
  *   WSL_OPT_DECODE_SPIN_LIMIT  0 the default poll bound of the decode hand-offs; n > 0 that

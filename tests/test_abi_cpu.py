@@ -499,6 +499,7 @@ def test_options_set_get_and_refuse():
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_split"], 17) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_strips"], 1) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], -1) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], 3) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(99, 0) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(0, 0) == N.WSL_E_INVALID_ARG
         assert N.get_option("prefill_split") == 4
@@ -567,7 +568,19 @@ def test_plan_paths_by_size():
     assert N.plan(0, 1024, 16, (1024,))["path"] == "none"
     assert N.plan(8, 2048, 64, (2048, 1024, 1024))["path"] == "decode"
     assert N.plan(100, 1000, 16, (512,))["path"] == "generic"  # K off the 64 grid
-    p = N.plan(4096, 4096, 128, (4096,), N.WSL_DTYPE_FP8_E4M3)
+    p = N.plan(4096, 4096, 128, (12288,), N.WSL_DTYPE_FP8_E4M3)  # 768 tiles of 256 x 256
     assert p["path"] == "prefill_fp8" and p["rank_prepass"] == 1
+    # one wave of 256 x 256 tiles or less: W decoded onto the bf16 matrix cores, unless forced
+    assert N.plan(4096, 4096, 128, (4096,), N.WSL_DTYPE_FP8_E4M3)["path"] == "prefill"
+    assert N.plan(4096, 4096, 128, (1024,), N.WSL_DTYPE_FP8_E4M3)["path"] == "prefill"
+    assert N.plan(4096, 4096, 128, (1024,), N.WSL_DTYPE_FP8_E4M3_ACT8)["path"] == "prefill_fp8"
+    assert N.plan(4096, 4096, 128, (4096, 1024, 1024), N.WSL_DTYPE_FP8_E4M3)["path"] == "prefill_fp8"
+    try:
+        N.set_option("fp8_prefill", 2)
+        assert N.plan(4096, 4096, 128, (1024,), N.WSL_DTYPE_FP8_E4M3)["path"] == "prefill_fp8"
+        N.set_option("fp8_prefill", 1)
+        assert N.plan(4096, 4096, 128, (12288,), N.WSL_DTYPE_FP8_E4M3)["path"] == "prefill"
+    finally:
+        N.set_option("fp8_prefill", 0)
     p = N.plan(4096, 4096, 128, (4096,))
     assert p["path"] == "prefill" and p["rank_prepass"] == 1 and p["rank_blocks"] == 0

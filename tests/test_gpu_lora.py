@@ -213,8 +213,43 @@ def test_fp8_base_parity_c5_shapes(gpu, M, N, K):
     assert err_dq <= BF16_TOL
 
 
+@pytest.mark.parametrize("path", [1, 2], ids=["decoded_w", "fp8_matrix_cores"])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (4096, 12288)])  # q/o, k/v, down at 8B
+def test_fp8_base_parity_c5_forced_paths(gpu, N, K, path, wsl_opts):
+    """Config 5's one-wave fp8 launches (M = 4096) on each path, forced (by default the
+    launch width picks W decoded onto the bf16 matrix cores for these; wider launches take
+    the fp8 matrix cores, test_fp8_base_parity_c5_shapes), so both stay pinned at these
+    shapes. Every 16th row against the float64 oracle: within the
+    bf16 bar of the exact product on the dequantised W, and against the fp32 W no more than
+    2e-3 above the per-channel e4m3 quantiser's own error on these inputs (2.5-3.1e-2 for
+    N(0, 0.02^2) weights at these shapes, whatever the kernel)."""
+    from weightshared_torchtitan_amd import _native, quantize_fp8_per_channel
+    M = 4096
+    wsl_opts(fp8_prefill=path)
+    p = _native.plan(M, K, 128, (N,), _native.WSL_DTYPE_FP8_E4M3)
+    assert p["path"] == ("prefill_fp8" if path == 2 else "prefill")
+    _say(f"[fp8 c5 forced] path={p['path']} M={M} N={N} K={K} r=128 s=1")
+    g = torch.Generator().manual_seed(N + K + M)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    Wf = torch.randn(N, K, generator=g) * 0.02
+    A = (torch.randn(128, K, generator=g) * 0.02).bfloat16()
+    B = (torch.randn(N, 128, generator=g) * 0.02).bfloat16()
+    q, sc = quantize_fp8_per_channel(Wf)
+    y = _run(gpu, x, q, A, B, 1.0, w_scale=sc).float().numpy()
+    rows = np.arange(0, M, 16)
+    ref = O.lora_linear(_np(x)[rows], Wf.numpy(), _np(A), _np(B), 1.0)
+    err = O.max_rel_err(y[rows], ref)
+    wdq = O.dequantize_fp8(q.view(torch.uint8).numpy(), sc.numpy())
+    exact_dq = O.lora_linear(_np(x)[rows], wdq, _np(A), _np(B), 1.0)
+    err_dq = O.max_rel_err(y[rows], exact_dq)
+    q_err = O.max_rel_err(exact_dq, ref)  # the quantiser's share
+    _say(f"  vs fp32 W: {err:.3e} (quantiser alone {q_err:.3e})   vs dequantised W: {err_dq:.3e}")
+    assert err_dq <= BF16_TOL
+    assert err <= q_err + 2e-3
+
+
 @pytest.mark.parametrize("terms", [2, 1])
-def test_fp8_activation_split_pinned_by_identity_weight(gpu, terms, monkeypatch):
+def test_fp8_activation_split_pinned_by_identity_weight(gpu, terms, monkeypatch, wsl_opts):
     """The fp8 matrix-core path with W = I (code 1.0 on the diagonal, scale 1): y is the
     activations the kernel multiplied, 2^e (hi + lo/16) (or 2^e hi), rounded to bf16. It must
     equal the oracle's split (oracle.fp8_split_activations) bit for bit: exponent choice, the
@@ -222,6 +257,7 @@ def test_fp8_activation_split_pinned_by_identity_weight(gpu, terms, monkeypatch)
     from 1e-6 to 1e6 and include maxima on both sides of the 1.75 * 2^k boundary."""
     from weightshared_torchtitan_amd import ops
     monkeypatch.setattr(ops, "FP8_ACTIVATIONS", terms == 1)
+    wsl_opts(fp8_prefill=2)  # one 256 x 256 tile: the fp8 matrix cores only when forced
     _say(f"[fp8 split] terms={terms}")
     M, K = 256, 256
     g = torch.Generator().manual_seed(17)

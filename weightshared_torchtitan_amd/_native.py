@@ -103,7 +103,7 @@ OPTIONS = {
     "prefill_strips": 1,     # -1: one output tile per workgroup
     "prefill_split": 2,      # -1: no split-K inside a launch; 2..16: that split count
     "prefill_medium": 3,     # -1: never the medium-M split form
-    "fp8_prefill": 4,        # 1: fp8 W decoded onto the bf16 matrix cores
+    "fp8_prefill": 4,        # 0: by launch width; 1: fp8 W decoded onto the bf16 matrix cores; 2: fp8 matrix cores
     "decode_passes": 5,      # -1: K splits only; 1: passes wherever the slices allow
     "decode_wide": 6,        # -1: 65-72 tokens on the prefill path
     "decode_spin_limit": 7,  # n > 0: poll bound of the decode hand-offs; -1: no polling

@@ -1182,11 +1182,23 @@ size_t rank_prepass_bytes(int64_t M, int64_t K, int64_t rt) {
 }
 
 namespace {
-// Which path an fp8 W takes on prefill shapes: the fp8 matrix cores (activation terms per
-// p.fp8_terms) unless WSL_OPT_FP8_PREFILL = 1 asks for W decoded onto the bf16 matrix cores
-// (kept for side-by-side measurement).
+// Which path an fp8 W takes on prefill shapes. Two activation terms on the fp8 matrix cores
+// do the MFMA work of the bf16 product and add the activation split (a read and a write of
+// x); the fp8 kernel has only 256 x 256 tiles, where the bf16 path also has narrower tiles
+// and split forms. They pay where the launch has more 256 x 256 tiles than the 256 CUs;
+// narrower launches decode W onto the bf16 matrix cores. Config 5 at M = 4096 (graphs of
+// 10 launches, one box; fp8 matrix cores with the split against decoded W): gate (768
+// tiles) 353.9 against 371.5 us, q|k|v grouped (384) 235.7 against 249.2, gate|up grouped
+// 683.7 against 730.4; q and o (256 tiles) 141.9 / 141.3 against 140.8 / 140.0, down
+// (4096 x 12288, the split of a 12288-wide x costing 31 us) 366.2 against 360.8, k and v
+// (1024 x 4096, 64 tiles) 116.4 against 68.6. One activation term
+// (WSL_DTYPE_FP8_E4M3_ACT8) always takes the fp8 matrix cores. WSL_OPT_FP8_PREFILL = 1
+// decodes W for every shape, 2 takes the fp8 matrix cores for every shape.
 bool fp8_matrix_cores(const LoraArgs& p) {
-  return option(WSL_OPT_FP8_PREFILL) != 1 && p.fp8_terms > 0 && prefill_fp8_supported(p);
+  const int64_t o = option(WSL_OPT_FP8_PREFILL);
+  if (o == 1 || p.fp8_terms <= 0 || !prefill_fp8_supported(p)) return false;
+  if (o == 2 || p.fp8_terms == 1) return true;
+  return ((p.M + 255) / 256) * ((p.N + 255) / 256) > 256;
 }
 }  // namespace
 
@@ -1402,8 +1414,10 @@ size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w
 // Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by the prefill kernel run as a
 // plain GEMM with A in the place of W (N = r) and s applied before rounding. With few row
 // tiles (N = r is one or two tiles wide) K is split over grid rows into fp32 partials that
-// a second kernel sums in split order, scales and rounds. A grouped launch runs one pre-pass
-// over all groups' A blocks (N = groups * r).
+// a second kernel sums in split order, scales and rounds; the splits run on the four-buffer
+// ring (one workgroup per CU, three K tiles in flight), whose partial sums are those of the
+// two-buffer form (the same K tiles and k steps in the same order). A grouped launch runs
+// one pre-pass over all groups' A blocks (N = groups * r).
 hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
   const int64_t rt = p.r * p.groups;
   LoraArgs q = p;
@@ -1415,7 +1429,7 @@ hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
   if (splits > 1) {
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(t) + (((size_t)(p.M * rt * 2) + 255) & ~(size_t)255));
     q.y = part; q.K = p.K / splits;
-    hipError_t e = launch_cfg<CfgSmall, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
+    hipError_t e = launch_cfg<CfgDeep, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
     if (e != hipSuccess) return e;
     const int64_t slice = p.M * rt;
     rank_reduce_kernel<<<dim3((unsigned)((slice / 8 + 255) / 256)), dim3(256), 0, p.stream>>>(part, splits, slice, p.scale, t);
