@@ -604,7 +604,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
     __syncthreads();  // every wave is done with the ring before the LDS is reused
   };
-  // The deep ring (NS > 2 buffers, the 128 x 128 tile at one workgroup per CU): NS K tiles
+  // The deep ring (NS > 2 buffers: the 128 x 128 tile and the one-wave 128 x 256 tile, at
+  // one workgroup per CU): NS K tiles
   // are in flight from the start, and the fill of tile kt+NS goes into tile kt's buffer
   // once every wave has read it (the barrier in tile kt). Each wait leaves the fills of the
   // NS-2 younger tiles in flight. With a workgroup alone on its CU, two buffers left every
@@ -955,6 +956,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
 using CfgBig = Cfg<256, 256, 2, 8>;   // 8 waves, 128(n) x 64(m) per wave
 using CfgTall = Cfg<128, 256, 4, 8>;  // 8 waves, 64 x 64 per wave
+using CfgTall3 = Cfg<128, 256, 4, 8, 3>;  // the same tile on a three-buffer ring (one wave of tiles)
 using CfgMid = Cfg<256, 192, 2, 8>;   // 8 waves, 96(n) x 64(m) per wave
 using CfgSmall = Cfg<128, 128, 2, 8>;  // 8 waves, 64(n) x 32(m) per wave; also the rank pre-pass (N = r)
 using CfgDeep = Cfg<128, 128, 2, 8, 4>;  // the same tile with four ring buffers: one workgroup per CU
@@ -1005,9 +1007,16 @@ int strip_tiles(const LoraArgs& p, int bm, int bn) {
 }
 
 // One tile configuration's launch: persistent strips of `strips` tiles (bf16 W with T
-// computed in the kernel, two-buffer ring), or one tile per workgroup.
+// computed in the kernel, two-buffer ring), or one tile per workgroup. 128 x 256 tiles
+// without strips (config 2's o and down: one tile per CU) run on a three-buffer ring, two K
+// tiles in flight, where a rank block leaves room for it (156 KB of LDS): same box,
+// alternating, o 41.1 / 41.3 against 41.8 / 42.0 us and down 56.5 / 56.4 against 58.9 /
+// 57.6.
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
 hipError_t launch_tiles(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int strips) {
+  if constexpr (std::is_same_v<C, CfgTall> && WDT == kBF16 && !GATHER && RB <= 1) {
+    if (strips <= 1) return launch_cfg<CfgTall3, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+  }
   if constexpr (WDT == kBF16 && HAS_W && RB > 0 && !EXT_T && !GATHER && C::NS == 2) {
     if (strips > 1)
       return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, true>(p, tg, ldt, 1, nullptr, nullptr,
