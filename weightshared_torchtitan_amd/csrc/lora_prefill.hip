@@ -430,9 +430,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   constexpr int TBLK = C::MJ * RB;
   constexpr bool ALL_T = RB > 0 && TBLK >= C::WNW;
   constexpr int TPW = (RB == 0) ? 0 : (ALL_T ? TBLK / C::WNW : 1);  // blocks per T wave
-  constexpr int TG = (RB == 0 || ALL_T) ? 1 : C::WNW / TBLK;        // wave groups per row
-  static_assert(RB == 0 || TBLK % C::WNW == 0 || C::WNW % TBLK == 0, "T split");
   constexpr int TBLKX = TBLK > 0 ? TBLK : 1;  // RB == 0: no T blocks (keeps % and / defined)
+  constexpr int TG = (RB == 0 || ALL_T) ? 1 : C::WNW / TBLKX;       // wave groups per row
+  static_assert(RB == 0 || TBLK % C::WNW == 0 || C::WNW % TBLK == 0, "T split");
   const int t_first = ALL_T ? wn * TPW : wn % TBLKX;  // first T block of this wave
   const bool t_wave = RB > 0 && (ALL_T || (wn / TBLKX) == (wm % TG));
 
