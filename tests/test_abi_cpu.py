@@ -451,6 +451,53 @@ def test_bwd_weights_workspace_holds_dw_copies_and_partials():
     assert N.bwd_weights_workspace_bytes(0, Nn, K, r) >= 65536
 
 
+def _bwd_input(**kw):
+    a = dict(gy=P, ldg=128, w=P, ldw=64, a=P, lda=64, b=P, ldb=8, scale=2.0, dx=P, lddx=64, M=4, N=128, K=64, r=8,
+             ws=None, ws_bytes=0, stream=None)
+    a.update(kw)
+    return N.lib().wsl_lora_linear_bwd_input(a["gy"], a["ldg"], a["w"], a["ldw"], a["a"], a["lda"], a["b"], a["ldb"],
+                                             a["scale"], a["dx"], a["lddx"], a["M"], a["N"], a["K"], a["r"], a["ws"],
+                                             a["ws_bytes"], a["stream"])
+
+
+@needs_lib
+@pytest.mark.parametrize("kw,code", [
+    (dict(gy=None), N.WSL_E_INVALID_ARG),
+    (dict(w=None), N.WSL_E_INVALID_ARG),
+    (dict(b=None), N.WSL_E_INVALID_ARG),
+    (dict(ldg=127), N.WSL_E_SHAPE),
+    (dict(ldw=63), N.WSL_E_SHAPE),
+    (dict(lddx=63), N.WSL_E_SHAPE),
+    (dict(ldb=7), N.WSL_E_SHAPE),
+    (dict(dx=P + 1), N.WSL_E_ALIGN),
+    (dict(N=72, ldg=72), N.WSL_E_SHAPE),         # the reduction off the 64 grid: not taken
+    (dict(gy=P + 8), N.WSL_E_SHAPE),             # gy rows not 16-byte aligned: not taken
+    (dict(r=12, ldb=12), N.WSL_E_SHAPE),         # rank off 8
+    (dict(), N.WSL_E_WORKSPACE),                 # no workspace
+])
+def test_bwd_input_validation_codes(kw, code):
+    """Every refusal happens on the host, before any device is touched."""
+    assert _bwd_input(**kw) == code
+    assert N.last_error() != ""
+
+
+@needs_lib
+def test_bwd_input_empty_batch_and_queries():
+    L = N.lib()
+    assert _bwd_input(M=0, gy=None, dx=None) == N.WSL_OK
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, P, 64, P, 8, P, 64, 4, 128, 64, 8) == 1
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, None, 0, None, 0, P, 64, 4, 128, 64, 0) == 1
+    assert L.wsl_lora_linear_bwd_input_supported(P, 100, P, 64, P, 64, P, 8, P, 64, 4, 100, 64, 8) == 0
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, P, 64, P, 8, P, 64, 4, 128, 60, 8) == 0
+    assert N.last_error() == ""
+    # the prefill scratch of the [M, K] outputs plus the transposed factors, and nothing the
+    # size of W (read where it lies)
+    M, Nn, K, r = 8192, 4096, 1024, 32
+    got = N.bwd_input_workspace_bytes(M, Nn, K, r)
+    assert got >= 65536 + 2 * (r * (Nn + K) * 2)
+    assert got < 65536 + 2 * (Nn * K * 2)
+
+
 @pytest.mark.parametrize("M,K", [(80, 256), (128, 640), (96, 2048), (65, 6144)])
 def test_workspace_bytes_of_wide_decode_shapes(M, K):
     """65-128 tokens: the decode plan takes the shape or declines it (K not a multiple of its

@@ -120,9 +120,9 @@ def test_lora_linear_module_trains(gpu):
     assert loss_fn().item() < loss.item()
 
 
-def test_shared_weight_transpose_follows_updates(gpu):
-    # dx of layers sharing one W reuses W^T; an in-place update of W must be seen by the
-    # next backward
+def test_shared_weight_updates_seen_by_next_backward(gpu):
+    # dx of two layers sharing one W reads W where it lies; an in-place update of W between
+    # steps must be seen by the next backward
     import weightshared_torchtitan_amd as wsl
     M, N, K, r = 256, 512, 384, 16
     g = torch.Generator().manual_seed(21)

@@ -3,9 +3,9 @@ compiles every transformer block with torch.compile(..., fullgraph=True)
 (torchtitan/models/llama3/infra/parallelize.py:348-357) and builds its model on the meta
 device before materialising it (torchtitan/train.py:156-157). Here:
 
-- torch.library.opcheck on wsl::lora_linear, wsl::lora_linear_grouped, wsl::lora_linear_bcast
-  and wsl::factorized_embedding: schema, fake (meta) kernels, autograd registration and AOT
-  dispatch, forward and backward;
+- torch.library.opcheck on wsl::lora_linear, wsl::lora_linear_grouped, wsl::lora_linear_bcast,
+  wsl::factorized_embedding and wsl::lora_linear_bwd_input: schema, fake (meta) kernels,
+  autograd registration and AOT dispatch, forward and backward;
 - a block of LoRALinear projections (grouped q|k|v, o, SwiGLU MLP) under
   torch.compile(fullgraph=True): no graph break, outputs and every gradient equal to eager;
 - the same block built on the meta device, materialised with to_empty and initialised, runs
@@ -71,6 +71,17 @@ def test_opcheck_factorized_embedding(gpu):
     ids = torch.randint(0, 1000, (4, 33), generator=g).to(gpu)
     args = (ids, _t(1000, 64, g=g, grad=False), _t(256, 64, g=g, grad=False))
     torch.library.opcheck(torch.ops.wsl.factorized_embedding.default, args,
+                          test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
+
+
+def test_opcheck_lora_linear_bwd_input(gpu):
+    """The input-gradient op the backward formulas call (no autograd of its own)."""
+    _say("[opcheck] wsl::lora_linear_bwd_input")
+    g = torch.Generator().manual_seed(5)
+    M, N, K, r = 256, 512, 256, 16
+    args = (_t(M, N, g=g, grad=False), _t(N, K, g=g, scale=0.02, grad=False), _t(r, K, g=g, scale=0.02, grad=False),
+            _t(N, r, g=g, scale=0.02, grad=False), 2.0)
+    torch.library.opcheck(torch.ops.wsl.lora_linear_bwd_input.default, args,
                           test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
 
 

@@ -47,6 +47,9 @@ EXPORTED = (
     "wsl_lora_linear_bwd_weights_supported",
     "wsl_lora_linear_bwd_weights_workspace_bytes",
     "wsl_lora_linear_bwd_weights",
+    "wsl_lora_linear_bwd_input_supported",
+    "wsl_lora_linear_bwd_input_workspace_bytes",
+    "wsl_lora_linear_bwd_input",
     "wsl_factorized_embedding_fwd",
     "wsl_last_error",
     "wsl_version",
@@ -208,6 +211,25 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_vp, ctypes.c_size_t,          # workspace, bytes
         _c_vp,                           # stream
     ]
+    lib.wsl_lora_linear_bwd_input_supported.restype = ctypes.c_int
+    lib.wsl_lora_linear_bwd_input_supported.argtypes = [
+        _c_vp, _c_i64, _c_vp, _c_i64,    # gy, ldg, w, ldw
+        _c_vp, _c_i64, _c_vp, _c_i64,    # a, lda, b, ldb
+        _c_vp, _c_i64,                   # dx, lddx
+        _c_i64, _c_i64, _c_i64, _c_i64]  # M, N, K, r
+    lib.wsl_lora_linear_bwd_input_workspace_bytes.restype = ctypes.c_int
+    lib.wsl_lora_linear_bwd_input_workspace_bytes.argtypes = [_c_i64, _c_i64, _c_i64, _c_i64,
+                                                              ctypes.POINTER(ctypes.c_size_t)]
+    lib.wsl_lora_linear_bwd_input.restype = ctypes.c_int
+    lib.wsl_lora_linear_bwd_input.argtypes = [
+        _c_vp, _c_i64, _c_vp, _c_i64,    # gy, ldg, w, ldw
+        _c_vp, _c_i64, _c_vp, _c_i64,    # a, lda, b, ldb
+        ctypes.c_float,                  # scale
+        _c_vp, _c_i64,                   # dx, lddx
+        _c_i64, _c_i64, _c_i64, _c_i64,  # M, N, K, r
+        _c_vp, ctypes.c_size_t,          # workspace, bytes
+        _c_vp,                           # stream
+    ]
     lib.wsl_decode_last_error.restype = ctypes.c_char_p
     lib.wsl_decode_last_error.argtypes = []
     lib.wsl_rmsnorm_fwd.restype = ctypes.c_int
@@ -341,6 +363,13 @@ def grouped_workspace_bytes(M: int, K: int, r: int, group_n, w_dtype: int) -> in
     check(lib().wsl_lora_linear_grouped_workspace_bytes(M, K, r, len(group_n), group_array(group_n), w_dtype,
                                                         ctypes.byref(out)),
           "wsl_lora_linear_grouped_workspace_bytes")
+    return int(out.value)
+
+
+def bwd_input_workspace_bytes(M: int, N: int, K: int, r: int) -> int:
+    out = ctypes.c_size_t(0)
+    check(lib().wsl_lora_linear_bwd_input_workspace_bytes(M, N, K, r, ctypes.byref(out)),
+          "wsl_lora_linear_bwd_input_workspace_bytes")
     return int(out.value)
 
 

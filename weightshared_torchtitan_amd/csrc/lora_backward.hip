@@ -311,6 +311,57 @@ hipError_t launch_weight_grads_generic(const LoraArgs& p, const void* gy, int64_
 }
 }  // namespace
 
+// ---- Input gradient: dX = dY . W + s (dY . B) . A, W read where it lies ----
+// The forward-shaped problem of dX (x' = dY, reduction K' = N, N' = K output columns) runs
+// on the prefill kernel's WT form: W's rows are the reduction, so its tiles go into LDS as
+// they lie and its fragments are transposing reads; no copy of W. The rank factors take the
+// places of the forward's: A' = B^T [r, N] and B' = A^T [K, r], transposed into the
+// workspace after the prefill scratch (r (N + K) bf16).
+namespace {
+LoraArgs wt_problem(const LoraArgs& p) {
+  LoraArgs q = p;
+  q.K = p.N;
+  q.N = p.K;
+  return q;
+}
+size_t a256b(size_t v) { return (v + 255) & ~(size_t)255; }
+}  // namespace
+
+bool bwd_input_supported(const LoraArgs& p) {
+  if (p.r > 0 && (p.N % 8 != 0 || p.K % 8 != 0 || !al16(p.a) || p.lda % 8 != 0 || !al16(p.b) || p.ldb % 8 != 0))
+    return false;
+  LoraArgs q = wt_problem(p);
+  // the transposed factors stand in for a and b (aligned, tight leading dimensions)
+  static char kAligned[16] __attribute__((aligned(16))) = {0};
+  q.a = p.r > 0 ? kAligned : nullptr;
+  q.lda = p.N;
+  q.b = p.r > 0 ? kAligned : nullptr;
+  q.ldb = p.r;
+  return prefill_wt_supported(q);
+}
+
+size_t bwd_input_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r) {
+  return a256b(prefill_workspace_bytes(M, K, N, r, kBF16)) + a256b((size_t)r * N * 2) + (size_t)K * r * 2;
+}
+
+hipError_t launch_bwd_input(const LoraArgs& p) {
+  LoraArgs q = wt_problem(p);
+  hipError_t e = hipSuccess;
+  if (p.r > 0) {
+    char* base = reinterpret_cast<char*>(p.ws) + a256b(prefill_workspace_bytes(p.M, p.K, p.N, p.r, kBF16));
+    uint16_t* bt = reinterpret_cast<uint16_t*>(base);
+    uint16_t* at = reinterpret_cast<uint16_t*>(base + a256b((size_t)p.r * p.N * 2));
+    e = transpose_pad(p.b, p.ldb, p.N, p.r, bt, p.N, p.N, p.stream);  // B [N, r] -> B^T [r, N]
+    if (e == hipSuccess) e = transpose_pad(p.a, p.lda, p.r, p.K, at, p.r, p.r, p.stream);  // A [r, K] -> A^T [K, r]
+    q.a = bt;
+    q.lda = p.N;
+    q.b = at;
+    q.ldb = p.r;
+  }
+  if (e == hipSuccess) e = launch_prefill_wt(q);
+  return e;
+}
+
 hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, void* dw, int64_t lddw, void* da,
                                int64_t ldda, void* db, int64_t lddb) {
   const int64_t M = p.M, N = p.N, K = p.K;

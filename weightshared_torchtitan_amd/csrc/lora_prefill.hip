@@ -187,8 +187,15 @@ __device__ __forceinline__ void ring_barrier() {
 // block and the group, so the first tile's K loop computes it (as an unsplit launch does),
 // parks it in an LDS region of its own, and the strip's later tiles skip the rank MFMAs
 // and the A fills and reuse it.
+//
+// WT: W' alone token-major, W'[n][k] = w[k * ldw + n] (x', A' and B' as they lie, the rank
+// work and epilogue unchanged): the input gradient dX = dY . W + s (dY . B) . A of a linear
+// whose W [N, K] is read where it lies, K being the reduction of the forward's output
+// columns. The W' tile goes into LDS as [64 k][BN] like the TN operands (every K row is
+// in range: K % 64 == 0), and its fragments are the same two transposing reads, whose k
+// order (16 kk + 8 (lane / 32) + 0..7) is that of x's plain fragments.
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
-          bool RED = false, bool PER = false>
+          bool RED = false, bool PER = false, bool WT = false>
 __global__ void __launch_bounds__(C::NT, 1)
 prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const int64_t* __restrict__ gidx, int64_t grows,
@@ -223,6 +230,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   static_assert(!TN || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "token-major operands: plain bf16 GEMM");
   static_assert(!RED || (WDT == kBF16 && HAS_W && !EXT_T && !GATHER && !SPLIT && !TN), "in-launch split-K: bf16 W");
   static_assert(C::NS == 2 || (!W8 && !TN && !GATHER), "deep ring: bf16 W and x as they lie");
+  static_assert(!WT || (WDT == kBF16 && HAS_W && !TN && !GATHER && !SPLIT && !RED && !PER && C::NS == 2 &&
+                        C::BN % 128 == 0),
+                "token-major W': bf16, x as it lies, two-buffer ring, 128-column multiples");
   int64_t tok_rem = grows;  // TN: K rows from this workgroup's first one to the end (>= 1)
   if constexpr (RED) {
     const int64_t kofs = (int64_t)blockIdx.y * K;
@@ -361,7 +371,12 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       if constexpr (GATHER) direct_fill(sx, wave * C::NXI + i, xg[i] + k0);
       else direct_fill(sx, wave * C::NXI + i, xbase + k0 * 2 + opaque(xoff[i]));
     }
-    if constexpr (WDIRECT) {
+    if constexpr (WT) {
+      constexpr int QW = 64 * C::BN * 2 / 1024 / C::NW;
+#pragma unroll
+      for (int i = 0; i < QW; ++i)
+        tn_fill(sw, C::BN, wave * QW + i, reinterpret_cast<const uint16_t*>(w), ldw, n0, N, k0);
+    } else if constexpr (WDIRECT) {
 #pragma unroll
       for (int i = 0; i < C::NWI; ++i) direct_fill(sw, wave * C::NWI + i, wbase + k0 * 2 + opaque(woff[i]));
     }
@@ -489,7 +504,10 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int c = kk * 2 + lh;
 #pragma unroll
     for (int j = 0; j < C::MJ; ++j) f.x[j] = lds_read16(sx, lds_off(wm * C::TM + j * 32 + l32, c));
-    if constexpr (HAS_W) {
+    if constexpr (WT) {
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i) f.w[i] = tn_frag(sw, C::BN, wn * C::TN + i * 32, kk);
+    } else if constexpr (HAS_W) {
 #pragma unroll
       for (int i = 0; i < C::NI; ++i) f.w[i] = lds_read16(sw, lds_off(wn * C::TN + i * 32 + l32, c));
     }
@@ -531,7 +549,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   auto interleave = [&](auto do_t) {
     constexpr int TT = decltype(do_t)::value ? TPW : 0;
     constexpr int NMF = (HAS_W ? C::NI * C::MJ : 0) + TT;
-    constexpr int NRD = (C::MJ + (HAS_W ? C::NI : 0)) * (TN ? 2 : 1) + TT * (ALL_T ? 1 : 2);
+    constexpr int NRD = (C::MJ + (HAS_W ? C::NI : 0)) * (TN ? 2 : 1) + (WT ? C::NI : 0) + TT * (ALL_T ? 1 : 2);
     constexpr int PAIRS = NMF < NRD ? NMF : NRD;
 #pragma unroll
     for (int q = 0; q < PAIRS; ++q) {
@@ -973,12 +991,12 @@ bool groups_fit(const LoraArgs& p, int bn) {
 }
 
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
-          bool RED = false, bool PER = false>
+          bool RED = false, bool PER = false, bool WT = false>
 hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1,
                       uint64_t* red_part = nullptr, unsigned* red_cnt = nullptr, int tpw = 1) {
   const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
   const int tiles_n = (int)((p.N + C::BN - 1) / C::BN);
-  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN, RED, PER>
+  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN, RED, PER, WT>
       <<<dim3(tiles_m * tiles_n / (PER ? tpw : 1), splits), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
@@ -1550,6 +1568,57 @@ PrefillPlan plan_prefill(const LoraArgs& p) {
   }
   pl.workgroups = ((p.M + pl.tile_m - 1) / pl.tile_m) * ((p.N + pl.tile_n - 1) / pl.tile_n) / pl.strips;
   return pl;
+}
+
+// ---- The input gradient with W read where it lies (the WT form) ----
+// q is the forward-shaped problem of dX = dY . W + s (dY . B) . A for a linear with W [N, K]:
+// x = dY [M, K'] (K' = N, the reduction), w = W with ldw its row stride (W'[n][k] =
+// w[k * ldw + n]; N' = K output columns), a = B^T [r, K'], b = A^T [N', r], y = dX.
+bool prefill_wt_supported(const LoraArgs& q) {
+  if (q.groups != 1 || q.wmap.P != 0 || q.w == nullptr || q.w_dtype != kBF16 || q.gather != nullptr) return false;
+  return q.M >= 1 && q.N % 8 == 0 && q.r <= WSL_MAX_RANK && prefill_supported(q);
+}
+
+namespace {
+template <class C, int RB, bool EXT_T>
+hipError_t launch_wt_cfg(const LoraArgs& q, const uint16_t* tg, int64_t ldt) {
+  return launch_cfg<C, kBF16, true, RB, EXT_T, false, false, false, false, false, true>(q, tg, ldt);
+}
+
+template <class C>
+hipError_t launch_wt_rank(const LoraArgs& q, const uint16_t* tg, int64_t ldt) {
+  if (tg != nullptr) return launch_wt_cfg<C, 0, true>(q, tg, ldt);
+  const int rb = rank_blocks_of(q.r);
+  if (rb == 1) return launch_wt_cfg<C, 1, false>(q, nullptr, 0);
+  if constexpr (C::BM == 128) {
+    if (rb == 2) return launch_wt_cfg<C, 2, false>(q, nullptr, 0);
+  }
+  return launch_wt_cfg<C, 0, false>(q, nullptr, 0);
+}
+}  // namespace
+
+// Tiles as the forward chooses them by how they fill the CUs, without the 192-wide one (the
+// token-major W' tile needs whole 128-column chunks); ranks 33-64 take 128-row tiles. Ranks
+// above 64 take T = s dY . B from the rank pre-pass in the workspace.
+hipError_t launch_prefill_wt(const LoraArgs& q_in) {
+  LoraArgs q = q_in;
+  q.gather_rows = q.K;  // every reduction row of W' is in range: no clamping in its fills
+  const uint16_t* tg = nullptr;
+  int64_t ldt = 0;
+  if (q.r > RIN) {
+    uint16_t* t = reinterpret_cast<uint16_t*>(q.ws);
+    const hipError_t e = rank_prepass(q, t);
+    if (e != hipSuccess) return e;
+    tg = t;
+    ldt = q.r;
+  }
+  const int rb = tg != nullptr ? 0 : rank_blocks_of(q.r);
+  const double big = rb == 2 ? -1.0 : wave_efficiency(((q.M + 255) / 256) * ((q.N + 255) / 256));
+  const double tall = wave_efficiency(((q.M + 127) / 128) * ((q.N + 255) / 256)) * 0.85;
+  const double small = wave_efficiency(((q.M + 127) / 128) * ((q.N + 127) / 128)) * 0.75;
+  if (small > big && small > tall) return launch_wt_rank<CfgSmall>(q, tg, ldt);
+  if (tall > big) return launch_wt_rank<CfgTall>(q, tg, ldt);
+  return launch_wt_rank<CfgBig>(q, tg, ldt);
 }
 
 hipError_t launch_prefill(const LoraArgs& p) {

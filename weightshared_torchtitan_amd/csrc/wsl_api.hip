@@ -336,6 +336,14 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
   return WSL_OK;
 }
 
+// The input gradient's problem in the linear's terms: x = gy [M, N], w = W [N, K], a = A,
+// b = B, y = dx [M, K].
+wsl::LoraArgs bwd_input_args(const void* gy, int64_t ldg, const void* w, int64_t ldw, const void* a, int64_t lda,
+                             const void* b, int64_t ldb, float scale, void* dx, int64_t lddx, int64_t M, int64_t N,
+                             int64_t K, int64_t r, void* stream) {
+  return make_args(gy, ldg, w, ldw, WSL_DTYPE_BF16, nullptr, a, lda, b, ldb, scale, dx, lddx, M, N, K, r, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -616,6 +624,61 @@ int wsl_lora_linear_bwd_weights(const void* x, int64_t ldx, const void* gy, int6
   p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes + half;
   p.ws_bytes = half;
   const hipError_t e = wsl::launch_weight_grads(p, gy, ldg, dw, lddw, da, ldda, db, lddb);
+  if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return WSL_OK;
+}
+
+int wsl_lora_linear_bwd_input_supported(const void* gy, int64_t ldg, const void* w, int64_t ldw, const void* a,
+                                        int64_t lda, const void* b, int64_t ldb, const void* dx, int64_t lddx,
+                                        int64_t M, int64_t N, int64_t K, int64_t r) {
+  const bool sizes_ok = validate_sizes(M, N, K, r, WSL_DTYPE_BF16) == WSL_OK && M >= 1;
+  clear_err();  // a query leaves no error behind
+  if (!sizes_ok || gy == nullptr || w == nullptr || dx == nullptr || (r > 0 && (a == nullptr || b == nullptr)))
+    return 0;
+  const wsl::LoraArgs p = bwd_input_args(gy, ldg, w, ldw, a, lda, b, ldb, 1.f, const_cast<void*>(dx), lddx, M, N, K,
+                                         r, nullptr);
+  return wsl::bwd_input_supported(p) ? 1 : 0;
+}
+
+int wsl_lora_linear_bwd_input_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, size_t* bytes) {
+  clear_err();
+  if (bytes == nullptr) return fail(WSL_E_INVALID_ARG, "bytes must not be NULL");
+  const int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
+  if (rc != WSL_OK) return rc;
+  *bytes = layout_bytes(M > 0 ? wsl::bwd_input_workspace_bytes(M, N, K, r) : 0);
+  return WSL_OK;
+}
+
+int wsl_lora_linear_bwd_input(const void* gy, int64_t ldg, const void* w, int64_t ldw, const void* a, int64_t lda,
+                              const void* b, int64_t ldb, float scale, void* dx, int64_t lddx, int64_t M, int64_t N,
+                              int64_t K, int64_t r, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_err();
+  int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
+  if (rc != WSL_OK) return rc;
+  if (M == 0) return WSL_OK;
+  if (gy == nullptr || w == nullptr || dx == nullptr) return fail(WSL_E_INVALID_ARG, "gy, w and dx must not be NULL");
+  if (r > 0 && (a == nullptr || b == nullptr)) return fail(WSL_E_INVALID_ARG, "r > 0 needs a and b");
+  if (ldg < N) return fail(WSL_E_SHAPE, "ldg (%lld) < N (%lld)", (long long)ldg, (long long)N);
+  if (ldw < K) return fail(WSL_E_SHAPE, "ldw (%lld) < K (%lld)", (long long)ldw, (long long)K);
+  if (lddx < K) return fail(WSL_E_SHAPE, "lddx (%lld) < K (%lld)", (long long)lddx, (long long)K);
+  if (r > 0 && lda < K) return fail(WSL_E_SHAPE, "lda (%lld) < K (%lld)", (long long)lda, (long long)K);
+  if (r > 0 && ldb < r) return fail(WSL_E_SHAPE, "ldb (%lld) < r (%lld)", (long long)ldb, (long long)r);
+  if (((uintptr_t)gy & 1) || ((uintptr_t)w & 1) || ((uintptr_t)dx & 1) || ((uintptr_t)a & 1) || ((uintptr_t)b & 1))
+    return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
+  wsl::LoraArgs p = bwd_input_args(gy, ldg, w, ldw, a, lda, b, ldb, scale, dx, lddx, M, N, K, r, stream);
+  if (!wsl::bwd_input_supported(p))
+    return fail(WSL_E_SHAPE, "layout not taken (N %% 64, K %% 8, r %% 8, 16-byte aligned rows): multiply by W^T");
+  const size_t need = wsl::bwd_input_workspace_bytes(M, N, K, r);
+  if (workspace == nullptr || workspace_bytes < layout_bytes(need))
+    return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", layout_bytes(need), workspace_bytes);
+  if ((uintptr_t)workspace & 255) return fail(WSL_E_ALIGN, "workspace must be 256-byte aligned");
+  rc = check_device();
+  if (rc != WSL_OK) return rc;
+  const size_t half = half_of(workspace_bytes);
+  p.ws = reinterpret_cast<char*>(workspace) + wsl::kCounterBytes + half;
+  p.ws_bytes = half;
+  p.red_cnt = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(workspace) + wsl::kRedCntOff);
+  const hipError_t e = wsl::launch_bwd_input(p);
   if (e != hipSuccess) return fail(WSL_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return WSL_OK;
 }

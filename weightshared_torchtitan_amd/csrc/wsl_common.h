@@ -187,6 +187,16 @@ bool weight_grads_supported(const LoraArgs& p, const void* gy, int64_t ldg);
 size_t weight_grads_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, bool need_w, bool need_ab);
 hipError_t launch_weight_grads(const LoraArgs& p, const void* gy, int64_t ldg, void* dw, int64_t lddw, void* da,
                                int64_t ldda, void* db, int64_t lddb);
+// The input gradient dX = dY . W + s (dY . B) . A with W [N, K] read where it lies: the
+// prefill kernel's WT form on the forward-shaped problem q (x = dY, K' = N, N' = K, a = B^T,
+// b = A^T; csrc/lora_prefill.hip), and its driver from the linear's own operands (p: x =
+// dY [M, N], w = W [N, K], a = A [r, K], b = B [N, r], y = dX [M, K]; p.N and p.K are the
+// linear's), which transposes A and B into the workspace (csrc/lora_backward.hip).
+bool prefill_wt_supported(const LoraArgs& q);
+hipError_t launch_prefill_wt(const LoraArgs& q);
+bool bwd_input_supported(const LoraArgs& p);
+size_t bwd_input_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r);
+hipError_t launch_bwd_input(const LoraArgs& p);
 
 // fp8 matrix-core prefill path (csrc/lora_prefill_fp8.hip): T from the rank pre-pass, the
 // activation codes and per-token scales in `scratch` (prefill_fp8_workspace_bytes).

@@ -13,7 +13,6 @@ from __future__ import annotations
 
 from typing import Optional
 
-import collections
 import contextlib
 import ctypes
 import os
@@ -205,43 +204,65 @@ def _lora_linear_fake(x, w, w_scale, a, b, scale):
     return x.new_empty((*x.shape[:-1], N), dtype=torch.bfloat16)
 
 
-# W^T of a bf16 base weight, reused by the backward of every layer that shares W (the
-# weight-shared model runs one W in up to 7 layers). An entry holds W itself, so its memory
-# cannot be reused while cached; a changed W (an optimizer step bumps _version) misses.
-_WT_CACHE: "collections.OrderedDict" = collections.OrderedDict()
-_WT_CACHE_MAX = 16
+@torch.library.custom_op("wsl::lora_linear_bwd_input", mutates_args=(), device_types="cuda")
+def lora_linear_bwd_input_op(gy: torch.Tensor, w: torch.Tensor, a: Optional[torch.Tensor],
+                             b: Optional[torch.Tensor], scale: float) -> torch.Tensor:
+    """dx [M, K] = gy . w + scale * (gy . b) . a for bf16 gy [M, N], w [N, K], a [r, K] and
+    b [N, r] as the forward takes them (a and b None: r = 0): wsl_lora_linear_bwd_input,
+    the fused kernel reading W where it lies as the reduction rows of its tiles. Layouts that
+    entry point does not take (N off the 64 grid, K or r off 8, unaligned rows) run the
+    forward op on a transposed copy of w."""
+    dev = _check_device(gy, w, a, b)
+    gy2 = _row_major(gy.reshape(-1, gy.shape[-1]), "grad_y")
+    w = _row_major(w, "w")
+    M, N = gy2.shape
+    if w.dim() != 2 or w.shape[0] != N:
+        raise ValueError(f"w {tuple(w.shape)} does not match grad_y's {N} columns")
+    K = w.shape[1]
+    if gy2.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("grad_y and w must be bfloat16")
+    r = 0
+    if a is not None or b is not None:
+        if a is None or b is None:
+            raise ValueError("a and b go together")
+        a = _row_major(a, "a")
+        b = _row_major(b, "b")
+        r = a.shape[0]
+        if a.shape[1] != K or b.shape != (N, r):
+            raise ValueError(f"LoRA shapes a {tuple(a.shape)}, b {tuple(b.shape)} do not match K={K}, N={N}")
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    if M == 0:
+        return dx
+    L = _native.lib()
+    if not L.wsl_lora_linear_bwd_input_supported(gy2.data_ptr(), gy2.stride(0), w.data_ptr(), w.stride(0),
+                                                 _dev_ptr(a), a.stride(0) if r else 0, _dev_ptr(b),
+                                                 b.stride(0) if r else 0, dx.data_ptr(), K, M, N, K, r):
+        return lora_linear_op(gy2, w.t().contiguous(), None, b.t().contiguous() if r else None,
+                              a.t().contiguous() if r else None, float(scale))
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = workspace(dev, stream, _native.bwd_input_workspace_bytes(M, N, K, r))
+    with torch.cuda.device(dev):
+        rc = L.wsl_lora_linear_bwd_input(gy2.data_ptr(), gy2.stride(0), w.data_ptr(), w.stride(0),
+                                         _dev_ptr(a), a.stride(0) if r else 0, _dev_ptr(b), b.stride(0) if r else 0,
+                                         float(scale), dx.data_ptr(), K, M, N, K, r, ws.data_ptr(), ws.numel(),
+                                         stream)
+    _native.check(rc, "wsl_lora_linear_bwd_input")
+    return dx
 
 
-def _has_storage(t: torch.Tensor) -> bool:
-    """False for the fake, functional and meta tensors of tracing (torch.compile, AOT
-    autograd, meta-device init), whose data pointers do not exist."""
-    if t.device.type == "meta":
-        return False
-    try:
-        t.data_ptr()
-    except RuntimeError:
-        return False
-    return True
+@lora_linear_bwd_input_op.register_fake
+def _lora_linear_bwd_input_fake(gy, w, a, b, scale):
+    return gy.new_empty((gy.numel() // gy.shape[-1], w.shape[1]), dtype=torch.bfloat16)
 
 
-def _transposed(w: torch.Tensor) -> torch.Tensor:
-    if not _has_storage(w) or torch.compiler.is_compiling():
-        return w.t().contiguous()  # traced: a plain transpose in the graph, no cache
-    key = (w.data_ptr(), tuple(w.shape), tuple(w.stride()), w.dtype, w.device)
-    hit = _WT_CACHE.get(key)
-    if hit is not None and hit[1] == w._version:
-        _WT_CACHE.move_to_end(key)
-        return hit[2]
-    wt = w.t().contiguous()
-    _WT_CACHE[key] = (w.detach(), w._version, wt)
-    while len(_WT_CACHE) > _WT_CACHE_MAX:
-        _WT_CACHE.popitem(last=False)
-    return wt
-
-
-def clear_transpose_cache() -> None:
-    """Drops the cached W^T copies (and the references they hold to their weights)."""
-    _WT_CACHE.clear()
+def _input_grad(gy2, w, w_scale, a, b, s):
+    """dx = gy . W + s (gy . b) . a: bf16 W read where it lies; an fp8 W through its
+    dequantised transpose on the forward kernel (a and b None: the base term alone)."""
+    if w.dtype == _FP8:
+        wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous()
+        return lora_linear_op(gy2, wt, None, b.t().contiguous() if b is not None else None,
+                              a.t().contiguous() if a is not None else None, s)
+    return lora_linear_bwd_input_op(gy2, w, a, b, float(s))
 
 
 @torch.library.custom_op("wsl::lora_linear_weight_grads", mutates_args=(), device_types="cuda")
@@ -321,9 +342,9 @@ def _lora_linear_setup(ctx, inputs, output):
 def _lora_linear_backward(ctx, gy):
     """Backward of ``wsl::lora_linear``. With T = x . a^T and U = gy . b:
 
-        dx = gy . W + scale * U . a     one launch of the fused kernel, as the forward of
-                                        the same op on (gy, W^T, b^T, a^T): the fused
-                                        kernel's K is the forward's N
+        dx = gy . W + scale * U . a     one wsl::lora_linear_bwd_input launch: the fused
+                                        kernel on (gy, b^T, a^T) with W's rows as the
+                                        reduction of its tiles, read where they lie
         dW = gy^T . x                   one wsl::lora_linear_weight_grads call: dW over the
         da = scale * U^T . x            tokens on the fused kernel's tile loop (operands
         db = scale * gy^T . T           read as they lie), da and db from dW
@@ -343,15 +364,10 @@ def _lora_linear_backward(ctx, gy):
     has_lora = a is not None and a.shape[0] > 0
     dx = dw = da = db = None
     if need_x:
-        wt = None
-        if w is not None and w.dtype == _FP8:
-            wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous()
-        elif w is not None:
-            wt = _transposed(w)
-        if has_lora:
-            dx = lora_linear_op(gy2, wt, None, b.t().contiguous(), a.t().contiguous(), s)
-        elif wt is not None:
-            dx = lora_linear_op(gy2, wt, None, None, None, s)
+        if w is not None:
+            dx = _input_grad(gy2, w, w_scale, a if has_lora else None, b if has_lora else None, s)
+        elif has_lora:  # the delta alone: s (gy . b) . a on the fused kernel's delta form
+            dx = lora_linear_op(gy2, None, None, b.t().contiguous(), a.t().contiguous(), s)
         else:
             dx = torch.zeros_like(x2)
         dx = dx.reshape(x.shape)
@@ -544,8 +560,7 @@ def _lora_linear_bcast_backward(ctx, gy):
     bd = _block_diag_rows(b, [N] * G, r) if has_lora else None
     dx = dw = da = db = None
     if need_x:
-        wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous() if w.dtype == _FP8 else _transposed(w)
-        dx = lora_linear_op(gyb, wt, None, None, None, 0.0)
+        dx = _input_grad(gyb, w, w_scale, None, None, 0.0)
         if has_lora and G * r <= _native.WSL_MAX_RANK:
             dx = dx + lora_linear_op(gy2, None, None, bd.t().contiguous(), a.t().contiguous(), s)
         elif has_lora:  # G*r above the kernels' rank limit: one delta launch per group, summed
@@ -620,23 +635,17 @@ def _lora_linear_grouped_backward(ctx, gy):
     bd = _block_diag_rows(b, gn, r) if has_lora else None
     dx = dw = da = db = None
     if need_x:
-        if w.dtype == _FP8:
-            wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous()
-        else:
-            wt = _transposed(w)
         if has_lora and len(gn) * r <= _native.WSL_MAX_RANK:
-            dx = lora_linear_op(gy2, wt, None, bd.t().contiguous(), a.t().contiguous(), s)
-        elif has_lora:  # G*r above the kernels' rank limit: one dx launch per group, summed
-            dx = None
+            dx = _input_grad(gy2, w, w_scale, a, bd, s)
+        elif has_lora:  # G*r above the kernels' rank limit: the base term, then one delta per group
+            dx = _input_grad(gy2, w, w_scale, None, None, s)
             n0 = 0
             for g, n in enumerate(gn):
-                ag = a[g * r:(g + 1) * r]
-                d = lora_linear_op(gy2[:, n0:n0 + n], wt[:, n0:n0 + n], None, b[n0:n0 + n].t().contiguous(),
-                                   ag.t().contiguous(), s)
-                dx = d if dx is None else dx + d
+                dx = dx + lora_linear_op(gy2[:, n0:n0 + n], None, None, b[n0:n0 + n].t().contiguous(),
+                                         a[g * r:(g + 1) * r].t().contiguous(), s)
                 n0 += n
         else:
-            dx = lora_linear_op(gy2, wt, None, None, None, s)
+            dx = _input_grad(gy2, w, w_scale, None, None, s)
         dx = dx.reshape(x.shape)
     # one weight-gradient call over all groups (x and gy read once): da from Bd, db as the
     # diagonal blocks of the [N, G*r] product (the off-diagonal blocks are a few GFLOP,
