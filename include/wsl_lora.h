@@ -228,29 +228,31 @@ int wsl_lora_linear_bwd_weights(const void* x, int64_t ldx, const void* gy, int6
                                 void* stream);
 
 /*
- * Input gradient of the fused LoRA linear (bf16 W):
+ * Input gradient of the fused LoRA linear:
  *
- *   dx [M, K] = gy [M, N] . W [N, K] + scale * (gy . B) . A
+ *   dx [M, K] = gy [M, N] . W [N, K] (. diag(w_scale) folded per row of W) + scale * (gy . B) . A
  *
- * with W [N, K], A [r, K], B [N, r] the operands as wsl_lora_linear_fwd takes them: W is
- * read where it lies (no transposed copy), as the reduction rows of the fused kernel's
- * token-major W tiles. Replaces the dx half of torch autograd's backward of the reference's
+ * with W [N, K] (bf16, or e4m3 with w_scale [N] fp32: WSL_DTYPE_FP8_E4M3 or _ACT8), A [r, K],
+ * B [N, r] the operands as wsl_lora_linear_fwd takes them: W is read where it lies (no
+ * transposed copy), as the reduction rows of the fused kernel's token-major W tiles; an fp8
+ * W is decoded to bf16(code * w_scale[n]) as its tiles are staged (the dequantised W). Replaces the dx half of torch autograd's backward of the reference's
  * LoRA linear (LoRAModule.forward, torchtitan/models/llama3/model/model.py:189-192, plus
  * the base nn.Linear, :257-273), run by loss.backward() (torchtitan/train.py:456).
  * wsl_lora_linear_bwd_input_supported returns 1 for the layouts taken: N a multiple of 64,
- * K and r multiples of 8, r <= WSL_MAX_RANK, gy, W, A, B and dx 16-byte aligned with leading
- * dimensions multiples of 8 (dx: 8-byte aligned, ldd a multiple of 4); the rest return
- * WSL_E_SHAPE (or WSL_E_ALIGN), and a caller multiplies by a transposed copy of W instead.
+ * K and r multiples of 8 (K of 16 for fp8), r <= WSL_MAX_RANK, gy, W, A, B and dx 16-byte
+ * aligned with leading dimensions multiples of 8 (fp8 ldw of 16; dx: 8-byte aligned, ldd a
+ * multiple of 4); the rest return WSL_E_SHAPE (or WSL_E_ALIGN), and a caller multiplies by
+ * a transposed copy of W instead.
  * Workspace (256-byte aligned) from wsl_lora_linear_bwd_input_workspace_bytes: the forward's
  * prefill scratch for [M, K] outputs plus the transposed A and B. fp32 accumulation, T =
  * bf16(scale * gy . B) rounded once, as the forward.
  */
-int wsl_lora_linear_bwd_input_supported(const void* gy, int64_t ldg, const void* w, int64_t ldw,
-                                        const void* a, int64_t lda, const void* b, int64_t ldb,
+int wsl_lora_linear_bwd_input_supported(const void* gy, int64_t ldg, const void* w, int64_t ldw, int32_t w_dtype,
+                                        const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
                                         const void* dx, int64_t lddx, int64_t M, int64_t N, int64_t K, int64_t r);
 int wsl_lora_linear_bwd_input_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, size_t* bytes);
-int wsl_lora_linear_bwd_input(const void* gy, int64_t ldg, const void* w, int64_t ldw,
-                              const void* a, int64_t lda, const void* b, int64_t ldb,
+int wsl_lora_linear_bwd_input(const void* gy, int64_t ldg, const void* w, int64_t ldw, int32_t w_dtype,
+                              const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
                               float scale, void* dx, int64_t lddx,
                               int64_t M, int64_t N, int64_t K, int64_t r,
                               void* workspace, size_t workspace_bytes, void* stream);

@@ -452,12 +452,12 @@ def test_bwd_weights_workspace_holds_dw_copies_and_partials():
 
 
 def _bwd_input(**kw):
-    a = dict(gy=P, ldg=128, w=P, ldw=64, a=P, lda=64, b=P, ldb=8, scale=2.0, dx=P, lddx=64, M=4, N=128, K=64, r=8,
-             ws=None, ws_bytes=0, stream=None)
+    a = dict(gy=P, ldg=128, w=P, ldw=64, w_dtype=N.WSL_DTYPE_BF16, w_scale=None, a=P, lda=64, b=P, ldb=8, scale=2.0,
+             dx=P, lddx=64, M=4, N=128, K=64, r=8, ws=None, ws_bytes=0, stream=None)
     a.update(kw)
-    return N.lib().wsl_lora_linear_bwd_input(a["gy"], a["ldg"], a["w"], a["ldw"], a["a"], a["lda"], a["b"], a["ldb"],
-                                             a["scale"], a["dx"], a["lddx"], a["M"], a["N"], a["K"], a["r"], a["ws"],
-                                             a["ws_bytes"], a["stream"])
+    return N.lib().wsl_lora_linear_bwd_input(a["gy"], a["ldg"], a["w"], a["ldw"], a["w_dtype"], a["w_scale"], a["a"],
+                                             a["lda"], a["b"], a["ldb"], a["scale"], a["dx"], a["lddx"], a["M"], a["N"],
+                                             a["K"], a["r"], a["ws"], a["ws_bytes"], a["stream"])
 
 
 @needs_lib
@@ -473,6 +473,11 @@ def _bwd_input(**kw):
     (dict(N=72, ldg=72), N.WSL_E_SHAPE),         # the reduction off the 64 grid: not taken
     (dict(gy=P + 8), N.WSL_E_SHAPE),             # gy rows not 16-byte aligned: not taken
     (dict(r=12, ldb=12), N.WSL_E_SHAPE),         # rank off 8
+    (dict(w_dtype=7), N.WSL_E_DTYPE),
+    (dict(w_dtype=N.WSL_DTYPE_FP8_E4M3), N.WSL_E_INVALID_ARG),              # fp8 without its scales
+    (dict(w_dtype=N.WSL_DTYPE_FP8_E4M3, w_scale=P + 2), N.WSL_E_ALIGN),
+    (dict(w_dtype=N.WSL_DTYPE_FP8_E4M3, w_scale=P, K=56, ldw=64, lda=64, lddx=64), N.WSL_E_SHAPE),  # K % 16
+    (dict(w_dtype=N.WSL_DTYPE_FP8_E4M3, w_scale=P), N.WSL_E_WORKSPACE),     # fp8 taken
     (dict(), N.WSL_E_WORKSPACE),                 # no workspace
 ])
 def test_bwd_input_validation_codes(kw, code):
@@ -485,10 +490,15 @@ def test_bwd_input_validation_codes(kw, code):
 def test_bwd_input_empty_batch_and_queries():
     L = N.lib()
     assert _bwd_input(M=0, gy=None, dx=None) == N.WSL_OK
-    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, P, 64, P, 8, P, 64, 4, 128, 64, 8) == 1
-    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, None, 0, None, 0, P, 64, 4, 128, 64, 0) == 1
-    assert L.wsl_lora_linear_bwd_input_supported(P, 100, P, 64, P, 64, P, 8, P, 64, 4, 100, 64, 8) == 0
-    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, P, 64, P, 8, P, 64, 4, 128, 60, 8) == 0
+    bf = N.WSL_DTYPE_BF16
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, bf, None, P, 64, P, 8, P, 64, 4, 128, 64, 8) == 1
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, bf, None, None, 0, None, 0, P, 64, 4, 128, 64, 0) == 1
+    assert L.wsl_lora_linear_bwd_input_supported(P, 100, P, 64, bf, None, P, 64, P, 8, P, 64, 4, 100, 64, 8) == 0
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, bf, None, P, 64, P, 8, P, 64, 4, 128, 60, 8) == 0
+    f8 = N.WSL_DTYPE_FP8_E4M3
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, f8, P, P, 64, P, 8, P, 64, 4, 128, 64, 8) == 1
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 64, f8, None, P, 64, P, 8, P, 64, 4, 128, 64, 8) == 0
+    assert L.wsl_lora_linear_bwd_input_supported(P, 128, P, 56, f8, P, P, 56, P, 8, P, 56, 4, 128, 56, 8) == 0
     assert N.last_error() == ""
     # the prefill scratch of the [M, K] outputs plus the transposed factors, and nothing the
     # size of W (read where it lies)

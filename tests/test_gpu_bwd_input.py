@@ -66,8 +66,8 @@ def test_bwd_input_matches_oracle(gpu, M, N, K, r):
     _say(f"[bwd input] M={M} N={N} K={K} r={r}")
     gy, W, A, B = _inputs(M, N, K, r, seed=M + N + K + r)
     dev = lambda t: t.to(gpu) if t is not None else None  # noqa: E731
-    dx = ops.lora_linear_bwd_input_op(dev(gy), dev(W), dev(A), dev(B), 2.0)
-    dx2 = ops.lora_linear_bwd_input_op(dev(gy), dev(W), dev(A), dev(B), 2.0)
+    dx = ops.lora_linear_bwd_input_op(dev(gy), dev(W), None, dev(A), dev(B), 2.0)
+    dx2 = ops.lora_linear_bwd_input_op(dev(gy), dev(W), None, dev(A), dev(B), 2.0)
     torch.cuda.synchronize()
     assert torch.equal(dx, dx2)
     rows = np.arange(M) if M <= 1024 else np.unique(np.concatenate([np.arange(0, M, 64), np.arange(63, M, 64)]))
@@ -90,15 +90,17 @@ def test_bwd_input_through_the_c_abi_and_views(gpu):
     out = torch.full((M, K + 40), 7.0, dtype=torch.bfloat16, device=gpu)
     L = _native.lib()
     Wd, Ad, Bd = W.to(gpu), A.to(gpu), B.to(gpu)
-    assert L.wsl_lora_linear_bwd_input_supported(gyv.data_ptr(), gyv.stride(0), Wd.data_ptr(), K, Ad.data_ptr(), K,
-                                                 Bd.data_ptr(), r, out.data_ptr(), out.stride(0), M, N, K, r) == 1
+    bf = _native.WSL_DTYPE_BF16
+    assert L.wsl_lora_linear_bwd_input_supported(gyv.data_ptr(), gyv.stride(0), Wd.data_ptr(), K, bf, None,
+                                                 Ad.data_ptr(), K, Bd.data_ptr(), r, out.data_ptr(), out.stride(0),
+                                                 M, N, K, r) == 1
     ws = torch.zeros(_native.bwd_input_workspace_bytes(M, N, K, r), dtype=torch.uint8, device=gpu)
     stream = torch.cuda.current_stream().cuda_stream
-    rc = L.wsl_lora_linear_bwd_input(gyv.data_ptr(), gyv.stride(0), Wd.data_ptr(), K, Ad.data_ptr(), K,
+    rc = L.wsl_lora_linear_bwd_input(gyv.data_ptr(), gyv.stride(0), Wd.data_ptr(), K, bf, None, Ad.data_ptr(), K,
                                      Bd.data_ptr(), r, 2.0, out.data_ptr(), out.stride(0), M, N, K, r,
                                      ws.data_ptr(), ws.numel(), stream)
     assert rc == 0, _native.last_error()
-    want = ops.lora_linear_bwd_input_op(gy.to(gpu), Wd, Ad, Bd, 2.0)
+    want = ops.lora_linear_bwd_input_op(gy.to(gpu), Wd, None, Ad, Bd, 2.0)
     torch.cuda.synchronize()
     assert torch.equal(out[:, :K], want)
     assert torch.all(out[:, K:] == 7.0)
@@ -114,15 +116,45 @@ def test_bwd_input_unsupported_layout_falls_back(gpu):
     Wd = W.to(gpu)
     gyd = gy.to(gpu)
     dx = torch.empty(M, K, dtype=torch.bfloat16, device=gpu)
-    assert L.wsl_lora_linear_bwd_input_supported(gyd.data_ptr(), N, Wd.data_ptr(), K, None, 0, None, 0,
+    bf = _native.WSL_DTYPE_BF16
+    assert L.wsl_lora_linear_bwd_input_supported(gyd.data_ptr(), N, Wd.data_ptr(), K, bf, None, None, 0, None, 0,
                                                  dx.data_ptr(), K, M, N, K, 0) == 0
     ws = torch.zeros(_native.bwd_input_workspace_bytes(M, N, K, 0), dtype=torch.uint8, device=gpu)
-    rc = L.wsl_lora_linear_bwd_input(gyd.data_ptr(), N, Wd.data_ptr(), K, None, 0, None, 0, 1.0, dx.data_ptr(), K,
-                                     M, N, K, 0, ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    rc = L.wsl_lora_linear_bwd_input(gyd.data_ptr(), N, Wd.data_ptr(), K, bf, None, None, 0, None, 0, 1.0,
+                                     dx.data_ptr(), K, M, N, K, 0, ws.data_ptr(), ws.numel(),
+                                     torch.cuda.current_stream().cuda_stream)
     assert rc == _native.WSL_E_SHAPE
-    got = ops.lora_linear_bwd_input_op(gyd, Wd, A.to(gpu), B.to(gpu), 2.0)
+    got = ops.lora_linear_bwd_input_op(gyd, Wd, None, A.to(gpu), B.to(gpu), 2.0)
     err = O.max_rel_err(_np(got), _ref_dx(gy, W, A, B, 2.0))
     assert err <= BF16_TOL
+
+
+FP8_CASES = [(4096, 4096, 4096, 128), (2048, 1024, 4096, 32), (512, 12288, 4096, 0), (300, 512, 784, 16)]
+
+
+@pytest.mark.parametrize("M,N,K,r", FP8_CASES, ids=[f"M{c[0]}_N{c[1]}_K{c[2]}_r{c[3]}" for c in FP8_CASES])
+def test_bwd_input_fp8_base(gpu, M, N, K, r):
+    """An fp8 W (e4m3 codes, per-row scales, config 5's shapes among them): decoded to
+    bf16(code * scale) as its tiles are staged. Against the float64 oracle on that
+    dequantised W (the bf16 bar), and bit for bit against the bf16 entry point given the
+    same dequantised W."""
+    from weightshared_torchtitan_amd import ops, quantize_fp8_per_channel
+    _say(f"[bwd input fp8] M={M} N={N} K={K} r={r}")
+    g = torch.Generator().manual_seed(M + N + K + r + 1)
+    gy = torch.randn(M, N, generator=g).bfloat16()
+    q, sc = quantize_fp8_per_channel(torch.randn(N, K, generator=g) * 0.02)
+    A = (torch.randn(r, K, generator=g) * 0.02).bfloat16() if r else None
+    B = (torch.randn(N, r, generator=g) * 0.02).bfloat16() if r else None
+    wdq = (q.float() * sc[:, None]).bfloat16()  # the dequantised W, rounded as the kernel rounds it
+    dev = lambda t: t.to(gpu) if t is not None else None  # noqa: E731
+    dx = ops.lora_linear_bwd_input_op(dev(gy), dev(q), dev(sc), dev(A), dev(B), 1.0)
+    want = ops.lora_linear_bwd_input_op(dev(gy), dev(wdq), None, dev(A), dev(B), 1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(dx, want)
+    rows = np.arange(0, M, max(1, M // 256))
+    err = O.max_rel_err(_np(dx)[rows], _ref_dx(gy[rows], wdq, A, B, 1.0))
+    _say(f"   max_rel_err {err:.2e}")
+    assert np.isfinite(err) and err <= BF16_TOL
 
 
 def test_backward_calls_no_transpose_of_w(gpu):

@@ -79,8 +79,8 @@ def test_opcheck_lora_linear_bwd_input(gpu):
     _say("[opcheck] wsl::lora_linear_bwd_input")
     g = torch.Generator().manual_seed(5)
     M, N, K, r = 256, 512, 256, 16
-    args = (_t(M, N, g=g, grad=False), _t(N, K, g=g, scale=0.02, grad=False), _t(r, K, g=g, scale=0.02, grad=False),
-            _t(N, r, g=g, scale=0.02, grad=False), 2.0)
+    args = (_t(M, N, g=g, grad=False), _t(N, K, g=g, scale=0.02, grad=False), None,
+            _t(r, K, g=g, scale=0.02, grad=False), _t(N, r, g=g, scale=0.02, grad=False), 2.0)
     torch.library.opcheck(torch.ops.wsl.lora_linear_bwd_input.default, args,
                           test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
 

@@ -214,6 +214,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.wsl_lora_linear_bwd_input_supported.restype = ctypes.c_int
     lib.wsl_lora_linear_bwd_input_supported.argtypes = [
         _c_vp, _c_i64, _c_vp, _c_i64,    # gy, ldg, w, ldw
+        ctypes.c_int32, _c_vp,           # w_dtype, w_scale
         _c_vp, _c_i64, _c_vp, _c_i64,    # a, lda, b, ldb
         _c_vp, _c_i64,                   # dx, lddx
         _c_i64, _c_i64, _c_i64, _c_i64]  # M, N, K, r
@@ -223,6 +224,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.wsl_lora_linear_bwd_input.restype = ctypes.c_int
     lib.wsl_lora_linear_bwd_input.argtypes = [
         _c_vp, _c_i64, _c_vp, _c_i64,    # gy, ldg, w, ldw
+        ctypes.c_int32, _c_vp,           # w_dtype, w_scale
         _c_vp, _c_i64, _c_vp, _c_i64,    # a, lda, b, ldb
         ctypes.c_float,                  # scale
         _c_vp, _c_i64,                   # dx, lddx

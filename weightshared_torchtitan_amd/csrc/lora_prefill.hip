@@ -230,9 +230,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   static_assert(!TN || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "token-major operands: plain bf16 GEMM");
   static_assert(!RED || (WDT == kBF16 && HAS_W && !EXT_T && !GATHER && !SPLIT && !TN), "in-launch split-K: bf16 W");
   static_assert(C::NS == 2 || (!W8 && !TN && !GATHER), "deep ring: bf16 W and x as they lie");
-  static_assert(!WT || (WDT == kBF16 && HAS_W && !TN && !GATHER && !SPLIT && !RED && !PER && C::NS == 2 &&
-                        C::BN % 128 == 0),
-                "token-major W': bf16, x as it lies, two-buffer ring, 128-column multiples");
+  static_assert(!WT || (HAS_W && !TN && !GATHER && !SPLIT && !RED && !PER && C::NS == 2 && C::BN % 128 == 0 &&
+                        (64 * C::BN / 16) % C::NT == 0),
+                "token-major W': x as it lies, two-buffer ring, 128-column multiples");
   int64_t tok_rem = grows;  // TN: K rows from this workgroup's first one to the end (>= 1)
   if constexpr (RED) {
     const int64_t kofs = (int64_t)blockIdx.y * K;
@@ -331,9 +331,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   uint32_t aoff = 0;
   if constexpr (RB > 0) aoff = (uint32_t)(min(wave * 8 + (lane >> 3), r - 1) * lda * 2 + fill_chunk(lane, wave) * 16);
   // fp8 W: BN rows x 64 B per K tile, 16 fp8 per chunk
-  constexpr int W8C = W8 ? C::BN * 4 / NT : 1;  // chunks per thread
+  constexpr int W8C = (W8 && !WT) ? C::BN * 4 / NT : 1;  // chunks per thread
   const uint8_t* w8row[W8C];
-  if constexpr (W8) {
+  if constexpr (W8 && !WT) {
 #pragma unroll
     for (int i = 0; i < W8C; ++i) {
       const int id = i * NT + tid;
@@ -371,7 +371,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       if constexpr (GATHER) direct_fill(sx, wave * C::NXI + i, xg[i] + k0);
       else direct_fill(sx, wave * C::NXI + i, xbase + k0 * 2 + opaque(xoff[i]));
     }
-    if constexpr (WT) {
+    if constexpr (WT && !W8) {
       constexpr int QW = 64 * C::BN * 2 / 1024 / C::NW;
 #pragma unroll
       for (int i = 0; i < QW; ++i)
@@ -398,8 +398,22 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   };
 
   u32x4_t w8stage[W8C];
+  // WT with an fp8 W: 64 K rows x BN columns of e4m3 bytes per K tile, 16-byte chunks
+  // (row id / (BN / 16), column chunk id % (BN / 16)); each row's scale is that of its
+  // reduction index (the linear's output channel), applied as it is decoded
+  constexpr int W8T = (W8 && WT) ? 64 * C::BN / 16 / NT : 1;  // chunks per thread
+  u32x4_t w8t[W8T];
+  float w8s[W8T];
   auto load_w8 = [&](int k0) {
-    if constexpr (W8) {
+    if constexpr (W8 && WT) {
+#pragma unroll
+      for (int i = 0; i < W8T; ++i) {
+        const int id = i * NT + tid, row = id / (C::BN / 16), c16 = id % (C::BN / 16);
+        const int col = min(n0 + c16 * 16, N - 16);  // N % 16 == 0: columns past N read a valid chunk
+        w8t[i] = ld_global_16(reinterpret_cast<const uint8_t*>(w) + (int64_t)(k0 + row) * ldw + col);
+        w8s[i] = w_scale[k0 + row];
+      }
+    } else if constexpr (W8) {
 #pragma unroll
       for (int i = 0; i < W8C; ++i) w8stage[i] = ld_global_16(w8row[i] + k0);
     }
@@ -423,7 +437,26 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   };
   auto store_w8 = [&](int stage) {
-    if constexpr (W8) {
+    if constexpr (W8 && WT) {
+      // bf16(code * scale) of each element, into the token-major tile's swizzled chunks
+      char* sw = lds + stage * STAGE + C::XB;
+#pragma unroll
+      for (int i = 0; i < W8T; ++i) {
+        const int id = i * NT + tid, row = id / (C::BN / 16), c16 = id % (C::BN / 16);
+        const float sc = w8s[i];
+        uint32_t o[8];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const auto lo2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w8t[i][d], false);
+          const auto hi2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w8t[i][d], true);
+          o[2 * d] = pack_bf16x2(lo2[0] * sc, lo2[1] * sc);
+          o[2 * d + 1] = pack_bf16x2(hi2[0] * sc, hi2[1] * sc);
+        }
+        const int sw4 = (row & 3) << 2;
+        lds_write16(sw, row * C::BN * 2 + (((c16 * 2) ^ sw4) << 4), u32x4_t{o[0], o[1], o[2], o[3]});
+        lds_write16(sw, row * C::BN * 2 + (((c16 * 2 + 1) ^ sw4) << 4), u32x4_t{o[4], o[5], o[6], o[7]});
+      }
+    } else if constexpr (W8) {
       char* sw = lds + stage * STAGE + C::XB;
 #pragma unroll
       for (int i = 0; i < W8C; ++i) {
@@ -783,8 +816,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
 
-  // ---- per-output-channel dequantisation scale (fp8 base) ----
-  if constexpr (W8) {
+  // ---- per-output-channel dequantisation scale (fp8 base; WT applied it when decoding) ----
+  if constexpr (W8 && !WT) {
 #pragma unroll
     for (int i = 0; i < C::NI; ++i) {
 #pragma unroll
@@ -1575,31 +1608,48 @@ PrefillPlan plan_prefill(const LoraArgs& p) {
 // x = dY [M, K'] (K' = N, the reduction), w = W with ldw its row stride (W'[n][k] =
 // w[k * ldw + n]; N' = K output columns), a = B^T [r, K'], b = A^T [N', r], y = dX.
 bool prefill_wt_supported(const LoraArgs& q) {
-  if (q.groups != 1 || q.wmap.P != 0 || q.w == nullptr || q.w_dtype != kBF16 || q.gather != nullptr) return false;
+  if (q.groups != 1 || q.wmap.P != 0 || q.w == nullptr || q.gather != nullptr) return false;
+  if (q.w_dtype == kFP8) {
+    if (q.w_scale == nullptr || q.N % 16 != 0) return false;  // 16-byte chunks of e4m3 columns
+  } else if (q.w_dtype != kBF16) {
+    return false;
+  }
   return q.M >= 1 && q.N % 8 == 0 && q.r <= WSL_MAX_RANK && prefill_supported(q);
 }
 
 namespace {
-template <class C, int RB, bool EXT_T>
+template <class C, int WDT, int RB, bool EXT_T>
 hipError_t launch_wt_cfg(const LoraArgs& q, const uint16_t* tg, int64_t ldt) {
-  return launch_cfg<C, kBF16, true, RB, EXT_T, false, false, false, false, false, true>(q, tg, ldt);
+  return launch_cfg<C, WDT, true, RB, EXT_T, false, false, false, false, false, true>(q, tg, ldt);
 }
 
-template <class C>
+template <class C, int WDT>
 hipError_t launch_wt_rank(const LoraArgs& q, const uint16_t* tg, int64_t ldt) {
-  if (tg != nullptr) return launch_wt_cfg<C, 0, true>(q, tg, ldt);
+  if (tg != nullptr) return launch_wt_cfg<C, WDT, 0, true>(q, tg, ldt);
   const int rb = rank_blocks_of(q.r);
-  if (rb == 1) return launch_wt_cfg<C, 1, false>(q, nullptr, 0);
+  if (rb == 1) return launch_wt_cfg<C, WDT, 1, false>(q, nullptr, 0);
   if constexpr (C::BM == 128) {
-    if (rb == 2) return launch_wt_cfg<C, 2, false>(q, nullptr, 0);
+    if (rb == 2) return launch_wt_cfg<C, WDT, 2, false>(q, nullptr, 0);
   }
-  return launch_wt_cfg<C, 0, false>(q, nullptr, 0);
+  return launch_wt_cfg<C, WDT, 0, false>(q, nullptr, 0);
+}
+
+template <int WDT>
+hipError_t launch_wt_tiles(const LoraArgs& q, int rb, const uint16_t* tg, int64_t ldt) {
+  const double big = rb == 2 ? -1.0 : wave_efficiency(((q.M + 255) / 256) * ((q.N + 255) / 256));
+  const double tall = wave_efficiency(((q.M + 127) / 128) * ((q.N + 255) / 256)) * 0.85;
+  const double small = wave_efficiency(((q.M + 127) / 128) * ((q.N + 127) / 128)) * 0.75;
+  if (small > big && small > tall) return launch_wt_rank<CfgSmall, WDT>(q, tg, ldt);
+  if (tall > big) return launch_wt_rank<CfgTall, WDT>(q, tg, ldt);
+  return launch_wt_rank<CfgBig, WDT>(q, tg, ldt);
 }
 }  // namespace
 
 // Tiles as the forward chooses them by how they fill the CUs, without the 192-wide one (the
 // token-major W' tile needs whole 128-column chunks); ranks 33-64 take 128-row tiles. Ranks
-// above 64 take T = s dY . B from the rank pre-pass in the workspace.
+// above 64 take T = s dY . B from the rank pre-pass in the workspace. An fp8 W is decoded
+// through registers with each row's scale (bf16(code * scale), the values of the
+// dequantised W) into the same token-major tiles.
 hipError_t launch_prefill_wt(const LoraArgs& q_in) {
   LoraArgs q = q_in;
   q.gather_rows = q.K;  // every reduction row of W' is in range: no clamping in its fills
@@ -1613,12 +1663,8 @@ hipError_t launch_prefill_wt(const LoraArgs& q_in) {
     ldt = q.r;
   }
   const int rb = tg != nullptr ? 0 : rank_blocks_of(q.r);
-  const double big = rb == 2 ? -1.0 : wave_efficiency(((q.M + 255) / 256) * ((q.N + 255) / 256));
-  const double tall = wave_efficiency(((q.M + 127) / 128) * ((q.N + 255) / 256)) * 0.85;
-  const double small = wave_efficiency(((q.M + 127) / 128) * ((q.N + 127) / 128)) * 0.75;
-  if (small > big && small > tall) return launch_wt_rank<CfgSmall>(q, tg, ldt);
-  if (tall > big) return launch_wt_rank<CfgTall>(q, tg, ldt);
-  return launch_wt_rank<CfgBig>(q, tg, ldt);
+  if (q.w_dtype == kFP8) return launch_wt_tiles<kFP8>(q, rb, tg, ldt);
+  return launch_wt_tiles<kBF16>(q, rb, tg, ldt);
 }
 
 hipError_t launch_prefill(const LoraArgs& p) {

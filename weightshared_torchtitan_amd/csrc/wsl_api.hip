@@ -338,10 +338,10 @@ int run_grouped(wsl::LoraArgs p, int n_groups, const int64_t* group_n, bool shar
 
 // The input gradient's problem in the linear's terms: x = gy [M, N], w = W [N, K], a = A,
 // b = B, y = dx [M, K].
-wsl::LoraArgs bwd_input_args(const void* gy, int64_t ldg, const void* w, int64_t ldw, const void* a, int64_t lda,
-                             const void* b, int64_t ldb, float scale, void* dx, int64_t lddx, int64_t M, int64_t N,
-                             int64_t K, int64_t r, void* stream) {
-  return make_args(gy, ldg, w, ldw, WSL_DTYPE_BF16, nullptr, a, lda, b, ldb, scale, dx, lddx, M, N, K, r, stream);
+wsl::LoraArgs bwd_input_args(const void* gy, int64_t ldg, const void* w, int64_t ldw, int32_t w_dtype,
+                             const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb, float scale,
+                             void* dx, int64_t lddx, int64_t M, int64_t N, int64_t K, int64_t r, void* stream) {
+  return make_args(gy, ldg, w, ldw, w_dtype, w_scale, a, lda, b, ldb, scale, dx, lddx, M, N, K, r, stream);
 }
 
 }  // namespace
@@ -628,15 +628,18 @@ int wsl_lora_linear_bwd_weights(const void* x, int64_t ldx, const void* gy, int6
   return WSL_OK;
 }
 
-int wsl_lora_linear_bwd_input_supported(const void* gy, int64_t ldg, const void* w, int64_t ldw, const void* a,
-                                        int64_t lda, const void* b, int64_t ldb, const void* dx, int64_t lddx,
-                                        int64_t M, int64_t N, int64_t K, int64_t r) {
-  const bool sizes_ok = validate_sizes(M, N, K, r, WSL_DTYPE_BF16) == WSL_OK && M >= 1;
+int wsl_lora_linear_bwd_input_supported(const void* gy, int64_t ldg, const void* w, int64_t ldw, int32_t w_dtype,
+                                        const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb,
+                                        const void* dx, int64_t lddx, int64_t M, int64_t N, int64_t K, int64_t r) {
+  int terms;
+  const int32_t kdt = kernel_dtype(w_dtype, &terms);
+  const bool sizes_ok = validate_sizes(M, N, K, r, kdt) == WSL_OK && M >= 1;
   clear_err();  // a query leaves no error behind
   if (!sizes_ok || gy == nullptr || w == nullptr || dx == nullptr || (r > 0 && (a == nullptr || b == nullptr)))
     return 0;
-  const wsl::LoraArgs p = bwd_input_args(gy, ldg, w, ldw, a, lda, b, ldb, 1.f, const_cast<void*>(dx), lddx, M, N, K,
-                                         r, nullptr);
+  if (kdt == WSL_DTYPE_FP8_E4M3 && w_scale == nullptr) return 0;
+  const wsl::LoraArgs p = bwd_input_args(gy, ldg, w, ldw, kdt, w_scale, a, lda, b, ldb, 1.f, const_cast<void*>(dx),
+                                         lddx, M, N, K, r, nullptr);
   return wsl::bwd_input_supported(p) ? 1 : 0;
 }
 
@@ -649,25 +652,32 @@ int wsl_lora_linear_bwd_input_workspace_bytes(int64_t M, int64_t N, int64_t K, i
   return WSL_OK;
 }
 
-int wsl_lora_linear_bwd_input(const void* gy, int64_t ldg, const void* w, int64_t ldw, const void* a, int64_t lda,
-                              const void* b, int64_t ldb, float scale, void* dx, int64_t lddx, int64_t M, int64_t N,
-                              int64_t K, int64_t r, void* workspace, size_t workspace_bytes, void* stream) {
+int wsl_lora_linear_bwd_input(const void* gy, int64_t ldg, const void* w, int64_t ldw, int32_t w_dtype,
+                              const float* w_scale, const void* a, int64_t lda, const void* b, int64_t ldb, float scale,
+                              void* dx, int64_t lddx, int64_t M, int64_t N, int64_t K, int64_t r, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   clear_err();
-  int rc = validate_sizes(M, N, K, r, WSL_DTYPE_BF16);
+  int terms;
+  const int32_t kdt = kernel_dtype(w_dtype, &terms);
+  int rc = validate_sizes(M, N, K, r, kdt);
   if (rc != WSL_OK) return rc;
   if (M == 0) return WSL_OK;
   if (gy == nullptr || w == nullptr || dx == nullptr) return fail(WSL_E_INVALID_ARG, "gy, w and dx must not be NULL");
+  if (kdt == WSL_DTYPE_FP8_E4M3 && w_scale == nullptr)
+    return fail(WSL_E_INVALID_ARG, "an fp8 w needs w_scale");
   if (r > 0 && (a == nullptr || b == nullptr)) return fail(WSL_E_INVALID_ARG, "r > 0 needs a and b");
   if (ldg < N) return fail(WSL_E_SHAPE, "ldg (%lld) < N (%lld)", (long long)ldg, (long long)N);
   if (ldw < K) return fail(WSL_E_SHAPE, "ldw (%lld) < K (%lld)", (long long)ldw, (long long)K);
   if (lddx < K) return fail(WSL_E_SHAPE, "lddx (%lld) < K (%lld)", (long long)lddx, (long long)K);
   if (r > 0 && lda < K) return fail(WSL_E_SHAPE, "lda (%lld) < K (%lld)", (long long)lda, (long long)K);
   if (r > 0 && ldb < r) return fail(WSL_E_SHAPE, "ldb (%lld) < r (%lld)", (long long)ldb, (long long)r);
-  if (((uintptr_t)gy & 1) || ((uintptr_t)w & 1) || ((uintptr_t)dx & 1) || ((uintptr_t)a & 1) || ((uintptr_t)b & 1))
+  if (((uintptr_t)gy & 1) || ((uintptr_t)dx & 1) || ((uintptr_t)a & 1) || ((uintptr_t)b & 1) ||
+      (kdt == WSL_DTYPE_BF16 && ((uintptr_t)w & 1)) || ((uintptr_t)w_scale & 3))
     return fail(WSL_E_ALIGN, "pointers must be aligned to their element size");
-  wsl::LoraArgs p = bwd_input_args(gy, ldg, w, ldw, a, lda, b, ldb, scale, dx, lddx, M, N, K, r, stream);
+  wsl::LoraArgs p = bwd_input_args(gy, ldg, w, ldw, kdt, w_scale, a, lda, b, ldb, scale, dx, lddx, M, N, K, r, stream);
   if (!wsl::bwd_input_supported(p))
-    return fail(WSL_E_SHAPE, "layout not taken (N %% 64, K %% 8, r %% 8, 16-byte aligned rows): multiply by W^T");
+    return fail(WSL_E_SHAPE, "layout not taken (N %% 64, K %% 8 (16 for fp8), r %% 8, 16-byte aligned rows): "
+                             "multiply by W^T");
   const size_t need = wsl::bwd_input_workspace_bytes(M, N, K, r);
   if (workspace == nullptr || workspace_bytes < layout_bytes(need))
     return fail(WSL_E_WORKSPACE, "workspace of %zu bytes required (got %zu)", layout_bytes(need), workspace_bytes);

@@ -205,22 +205,28 @@ def _lora_linear_fake(x, w, w_scale, a, b, scale):
 
 
 @torch.library.custom_op("wsl::lora_linear_bwd_input", mutates_args=(), device_types="cuda")
-def lora_linear_bwd_input_op(gy: torch.Tensor, w: torch.Tensor, a: Optional[torch.Tensor],
-                             b: Optional[torch.Tensor], scale: float) -> torch.Tensor:
-    """dx [M, K] = gy . w + scale * (gy . b) . a for bf16 gy [M, N], w [N, K], a [r, K] and
-    b [N, r] as the forward takes them (a and b None: r = 0): wsl_lora_linear_bwd_input,
-    the fused kernel reading W where it lies as the reduction rows of its tiles. Layouts that
-    entry point does not take (N off the 64 grid, K or r off 8, unaligned rows) run the
-    forward op on a transposed copy of w."""
-    dev = _check_device(gy, w, a, b)
+def lora_linear_bwd_input_op(gy: torch.Tensor, w: torch.Tensor, w_scale: Optional[torch.Tensor],
+                             a: Optional[torch.Tensor], b: Optional[torch.Tensor], scale: float) -> torch.Tensor:
+    """dx [M, K] = gy . W + scale * (gy . b) . a for bf16 gy [M, N], w [N, K] (bf16, or
+    float8_e4m3fn with w_scale [N] fp32: W = bf16(w * w_scale[:, None]) row by row),
+    a [r, K] and b [N, r] as the forward takes them (a and b None: r = 0):
+    wsl_lora_linear_bwd_input, the fused kernel reading w where it lies as the reduction rows
+    of its tiles. Layouts that entry point does not take (N off the 64 grid, K or r off 8,
+    unaligned rows) run the forward op on a transposed copy of W."""
+    dev = _check_device(gy, w, w_scale, a, b)
     gy2 = _row_major(gy.reshape(-1, gy.shape[-1]), "grad_y")
     w = _row_major(w, "w")
     M, N = gy2.shape
     if w.dim() != 2 or w.shape[0] != N:
         raise ValueError(f"w {tuple(w.shape)} does not match grad_y's {N} columns")
     K = w.shape[1]
-    if gy2.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
-        raise TypeError("grad_y and w must be bfloat16")
+    fp8 = w.dtype == _FP8
+    if gy2.dtype != torch.bfloat16 or (w.dtype != torch.bfloat16 and not fp8):
+        raise TypeError("grad_y must be bfloat16 and w bfloat16 or float8_e4m3fn")
+    if fp8 and (w_scale is None or w_scale.dtype != torch.float32 or w_scale.shape != (N,)):
+        raise ValueError("an fp8 w needs w_scale [N] float32")
+    if fp8:
+        w_scale = w_scale.contiguous()
     r = 0
     if a is not None or b is not None:
         if a is None or b is None:
@@ -234,15 +240,18 @@ def lora_linear_bwd_input_op(gy: torch.Tensor, w: torch.Tensor, a: Optional[torc
     if M == 0:
         return dx
     L = _native.lib()
-    if not L.wsl_lora_linear_bwd_input_supported(gy2.data_ptr(), gy2.stride(0), w.data_ptr(), w.stride(0),
-                                                 _dev_ptr(a), a.stride(0) if r else 0, _dev_ptr(b),
+    wdt = _native.WSL_DTYPE_FP8_E4M3 if fp8 else _native.WSL_DTYPE_BF16
+    ws_ptr = w_scale.data_ptr() if fp8 else None
+    if not L.wsl_lora_linear_bwd_input_supported(gy2.data_ptr(), gy2.stride(0), w.data_ptr(), w.stride(0), wdt,
+                                                 ws_ptr, _dev_ptr(a), a.stride(0) if r else 0, _dev_ptr(b),
                                                  b.stride(0) if r else 0, dx.data_ptr(), K, M, N, K, r):
-        return lora_linear_op(gy2, w.t().contiguous(), None, b.t().contiguous() if r else None,
-                              a.t().contiguous() if r else None, float(scale))
+        wt = ((w.float() * w_scale[:, None]).to(torch.bfloat16) if fp8 else w).t().contiguous()
+        return lora_linear_op(gy2, wt, None, b.t().contiguous() if r else None, a.t().contiguous() if r else None,
+                              float(scale))
     stream = torch.cuda.current_stream(dev).cuda_stream
     ws = workspace(dev, stream, _native.bwd_input_workspace_bytes(M, N, K, r))
     with torch.cuda.device(dev):
-        rc = L.wsl_lora_linear_bwd_input(gy2.data_ptr(), gy2.stride(0), w.data_ptr(), w.stride(0),
+        rc = L.wsl_lora_linear_bwd_input(gy2.data_ptr(), gy2.stride(0), w.data_ptr(), w.stride(0), wdt, ws_ptr,
                                          _dev_ptr(a), a.stride(0) if r else 0, _dev_ptr(b), b.stride(0) if r else 0,
                                          float(scale), dx.data_ptr(), K, M, N, K, r, ws.data_ptr(), ws.numel(),
                                          stream)
@@ -251,18 +260,14 @@ def lora_linear_bwd_input_op(gy: torch.Tensor, w: torch.Tensor, a: Optional[torc
 
 
 @lora_linear_bwd_input_op.register_fake
-def _lora_linear_bwd_input_fake(gy, w, a, b, scale):
+def _lora_linear_bwd_input_fake(gy, w, w_scale, a, b, scale):
     return gy.new_empty((gy.numel() // gy.shape[-1], w.shape[1]), dtype=torch.bfloat16)
 
 
 def _input_grad(gy2, w, w_scale, a, b, s):
-    """dx = gy . W + s (gy . b) . a: bf16 W read where it lies; an fp8 W through its
-    dequantised transpose on the forward kernel (a and b None: the base term alone)."""
-    if w.dtype == _FP8:
-        wt = (w.float() * w_scale[:, None]).to(torch.bfloat16).t().contiguous()
-        return lora_linear_op(gy2, wt, None, b.t().contiguous() if b is not None else None,
-                              a.t().contiguous() if a is not None else None, s)
-    return lora_linear_bwd_input_op(gy2, w, a, b, float(s))
+    """dx = gy . W + s (gy . b) . a with W read where it lies (an fp8 W decoded with its
+    per-row scale as it is staged; a and b None: the base term alone)."""
+    return lora_linear_bwd_input_op(gy2, w, w_scale if w.dtype == _FP8 else None, a, b, float(s))
 
 
 @torch.library.custom_op("wsl::lora_linear_weight_grads", mutates_args=(), device_types="cuda")
