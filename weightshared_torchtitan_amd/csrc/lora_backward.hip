@@ -24,6 +24,8 @@
 // The reference has no backward of its own: torch autograd differentiates LoRAModule.forward
 // (torchtitan/models/llama3/model/model.py:189-192) and the base nn.Linear (:257-273)
 // composed by broadcast_add (:392-398); the trainer runs it at torchtitan/train.py:456.
+#include <algorithm>
+
 #include "wsl_common.h"
 
 namespace wsl {
@@ -35,12 +37,20 @@ constexpr int TS = TT + 2;   // its LDS row stride in bf16 (odd word count: spre
 
 // dst[c][i] = src[i][c] for i < R and 0 for R <= i < Rp, c < C (B^T and dW^T here, Rp = R).
 // 16-byte global accesses both ways (C % 8 == 0, Rp % 8 == 0, 16-byte aligned rows).
-__global__ void __launch_bounds__(256) transpose_pad_kernel(const uint16_t* __restrict__ src, int64_t lds_,
-                                                           int64_t R, int64_t C, uint16_t* __restrict__ dst,
-                                                           int64_t ldd, int64_t Rp) {
-  __shared__ uint32_t tile[TT * TS / 2];
+struct TransposeJob {
+  const uint16_t* src;
+  int64_t lds_, R, C;
+  uint16_t* dst;
+  int64_t ldd, Rp;
+};
+
+// The 64 x 64 tile (bx, by) of one job, staged through `tile`.
+__device__ __forceinline__ void transpose_tile(const TransposeJob& j, int64_t bx, int64_t by, uint32_t* tile) {
+  const uint16_t* __restrict__ src = j.src;
+  uint16_t* __restrict__ dst = j.dst;
+  const int64_t lds_ = j.lds_, R = j.R, C = j.C, ldd = j.ldd, Rp = j.Rp;
   const uint16_t* t16 = reinterpret_cast<const uint16_t*>(tile);
-  const int64_t r0 = (int64_t)blockIdx.y * TT, c0 = (int64_t)blockIdx.x * TT;
+  const int64_t r0 = by * TT, c0 = bx * TT;
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -62,6 +72,19 @@ __global__ void __launch_bounds__(256) transpose_pad_kernel(const uint16_t* __re
       w[j] = (uint32_t)t16[(q * 8 + 2 * j) * TS + c] | ((uint32_t)t16[(q * 8 + 2 * j + 1) * TS + c] << 16);
     *reinterpret_cast<u32x4_t*>(dst + (c0 + c) * ldd + r0 + q * 8) = u32x4_t{w[0], w[1], w[2], w[3]};
   }
+}
+
+__global__ void __launch_bounds__(256) transpose_pad_kernel(const TransposeJob j) {
+  __shared__ uint32_t tile[TT * TS / 2];
+  transpose_tile(j, blockIdx.x, blockIdx.y, tile);
+}
+
+// Two jobs in one launch (blockIdx.z picks the job; tiles past a job's extent exit).
+__global__ void __launch_bounds__(256) transpose_pair_kernel(const TransposeJob j0, const TransposeJob j1) {
+  __shared__ uint32_t tile[TT * TS / 2];
+  const TransposeJob& j = blockIdx.z == 0 ? j0 : j1;
+  if ((int64_t)blockIdx.x * TT >= j.C || (int64_t)blockIdx.y * TT >= j.Rp) return;
+  transpose_tile(j, blockIdx.x, blockIdx.y, tile);
 }
 
 // Four bf16 of row-major `d` (8-byte pieces when `vec`).
@@ -140,7 +163,16 @@ hipError_t transpose_pad(const void* src, int64_t lds_, int64_t R, int64_t C, ui
                          int64_t Rp, hipStream_t st) {
   if (C == 0 || Rp == 0) return hipSuccess;
   const dim3 grid((unsigned)((C + TT - 1) / TT), (unsigned)((Rp + TT - 1) / TT));
-  transpose_pad_kernel<<<grid, dim3(256), 0, st>>>(reinterpret_cast<const uint16_t*>(src), lds_, R, C, dst, ldd, Rp);
+  transpose_pad_kernel<<<grid, dim3(256), 0, st>>>(TransposeJob{reinterpret_cast<const uint16_t*>(src), lds_, R, C,
+                                                                dst, ldd, Rp});
+  return hipGetLastError();
+}
+
+// Both transposes of the input gradient's rank factors in one launch.
+hipError_t transpose_pair(const TransposeJob& j0, const TransposeJob& j1, hipStream_t st) {
+  const int64_t gx = std::max((j0.C + TT - 1) / TT, (j1.C + TT - 1) / TT);
+  const int64_t gy = std::max((j0.Rp + TT - 1) / TT, (j1.Rp + TT - 1) / TT);
+  transpose_pair_kernel<<<dim3((unsigned)gx, (unsigned)gy, 2), dim3(256), 0, st>>>(j0, j1);
   return hipGetLastError();
 }
 
@@ -351,8 +383,9 @@ hipError_t launch_bwd_input(const LoraArgs& p) {
     char* base = reinterpret_cast<char*>(p.ws) + a256b(prefill_workspace_bytes(p.M, p.K, p.N, p.r, kBF16));
     uint16_t* bt = reinterpret_cast<uint16_t*>(base);
     uint16_t* at = reinterpret_cast<uint16_t*>(base + a256b((size_t)p.r * p.N * 2));
-    e = transpose_pad(p.b, p.ldb, p.N, p.r, bt, p.N, p.N, p.stream);  // B [N, r] -> B^T [r, N]
-    if (e == hipSuccess) e = transpose_pad(p.a, p.lda, p.r, p.K, at, p.r, p.r, p.stream);  // A [r, K] -> A^T [K, r]
+    // B [N, r] -> B^T [r, N] and A [r, K] -> A^T [K, r], one launch
+    e = transpose_pair(TransposeJob{reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.N, p.r, bt, p.N, p.N},
+                       TransposeJob{reinterpret_cast<const uint16_t*>(p.a), p.lda, p.r, p.K, at, p.r, p.r}, p.stream);
     q.a = bt;
     q.lda = p.N;
     q.b = at;

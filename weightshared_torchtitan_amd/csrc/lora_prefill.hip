@@ -230,9 +230,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   static_assert(!TN || (WDT == kBF16 && HAS_W && RB == 0 && !EXT_T && !GATHER), "token-major operands: plain bf16 GEMM");
   static_assert(!RED || (WDT == kBF16 && HAS_W && !EXT_T && !GATHER && !SPLIT && !TN), "in-launch split-K: bf16 W");
   static_assert(C::NS == 2 || (!W8 && !TN && !GATHER), "deep ring: bf16 W and x as they lie");
-  static_assert(!WT || (HAS_W && !TN && !GATHER && !SPLIT && !RED && !PER && C::NS == 2 && C::BN % 128 == 0 &&
-                        (64 * C::BN / 16) % C::NT == 0),
-                "token-major W': x as it lies, two-buffer ring, 128-column multiples");
+  static_assert(!WT || (HAS_W && !TN && !GATHER && !SPLIT && !RED && C::BN % 128 == 0 &&
+                        (WDT == kBF16 || (C::NS == 2 && (64 * C::BN / 16) % C::NT == 0))),
+                "token-major W': x as it lies, 128-column multiples (fp8: two-buffer ring)");
   int64_t tok_rem = grows;  // TN: K rows from this workgroup's first one to the end (>= 1)
   if constexpr (RED) {
     const int64_t kofs = (int64_t)blockIdx.y * K;
@@ -325,6 +325,23 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int row = (wave * C::NWI + i) * 8 + (lane >> 3);
     woff[i] = (uint32_t)((map_row(min(n0 + row, N - 1), wmap) - wrow0) * ldw * 2 + fill_chunk(lane, wave * C::NWI + i) * 16);
   }
+  // WT: the W' tile's direct fills, [64 k][BN] as the TN operands lie: fill q of this wave
+  // writes lane i's 16 bytes at 1024 q + 16 i of the tile, row (1024 q + 16 i) / (2 BN), and
+  // takes W's column chunk held there (chunk c at physical chunk c ^ 4 (row & 3); columns
+  // past N read the last full chunk, their outputs are not stored). The byte offset within
+  // a K tile's 64 rows fits 32 bits; the K tile's base is uniform.
+  constexpr int QWT = WT ? 64 * C::BN * 2 / 1024 / C::NW : 1;
+  uint32_t wtoff[QWT];
+  if constexpr (WT && !W8) {
+#pragma unroll
+    for (int i = 0; i < QWT; ++i) {
+      const int q = wave * QWT + i;
+      const int row = (q * 1024 + lane * 16) / (C::BN * 2);
+      const int c = (lane % (C::BN / 8)) ^ ((row & 3) << 2);
+      const int f = min(n0 + c * 8, N - 8);
+      wtoff[i] = (uint32_t)(((int64_t)row * ldw + f) * 2);
+    }
+  }
   // rank-A slice: RB*32 rows = RB*4 fills, one per wave for waves < RB*4 (rows >= r read
   // row r-1; their T ranks are zeroed when T is parked)
   constexpr int NAI = RB * 4;
@@ -372,10 +389,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       else direct_fill(sx, wave * C::NXI + i, xbase + k0 * 2 + opaque(xoff[i]));
     }
     if constexpr (WT && !W8) {
-      constexpr int QW = 64 * C::BN * 2 / 1024 / C::NW;
+      const char* wk = reinterpret_cast<const char*>(w) + (int64_t)k0 * ldw * 2;  // K rows k0..k0+63
 #pragma unroll
-      for (int i = 0; i < QW; ++i)
-        tn_fill(sw, C::BN, wave * QW + i, reinterpret_cast<const uint16_t*>(w), ldw, n0, N, k0);
+      for (int i = 0; i < QWT; ++i) direct_fill(sw, wave * QWT + i, wk + opaque(wtoff[i]));
     } else if constexpr (WDIRECT) {
 #pragma unroll
       for (int i = 0; i < C::NWI; ++i) direct_fill(sw, wave * C::NWI + i, wbase + k0 * 2 + opaque(woff[i]));
@@ -1063,17 +1079,18 @@ int strip_tiles(const LoraArgs& p, int bm, int bn) {
 // tiles in flight, where a rank block leaves room for it (156 KB of LDS): same box,
 // alternating, o 41.1 / 41.3 against 41.8 / 42.0 us and down 56.5 / 56.4 against 58.9 /
 // 57.6.
-template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER>
+template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool WT = false>
 hipError_t launch_tiles(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int strips) {
   if constexpr (std::is_same_v<C, CfgTall> && WDT == kBF16 && !GATHER && RB <= 1) {
-    if (strips <= 1) return launch_cfg<CfgTall3, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    if (strips <= 1)
+      return launch_cfg<CfgTall3, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, false, WT>(p, tg, ldt);
   }
   if constexpr (WDT == kBF16 && HAS_W && RB > 0 && !EXT_T && !GATHER && C::NS == 2) {
     if (strips > 1)
-      return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, true>(p, tg, ldt, 1, nullptr, nullptr,
-                                                                                     strips);
+      return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, true, WT>(p, tg, ldt, 1, nullptr,
+                                                                                         nullptr, strips);
   }
-  return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+  return launch_cfg<C, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, false, WT>(p, tg, ldt);
 }
 
 // Fraction of the 256 CUs kept busy over the launch's waves of workgroups.
@@ -1091,9 +1108,10 @@ double wave_efficiency(int64_t tiles) {
 enum class Tile { kBig, kMid, kTall, kSmall, kDeep };
 // A grouped launch only considers configurations whose tile width divides every group
 // boundary (one of 256 and 128 always does: prefill_groups_supported checks it).
-Tile choose_tile(const LoraArgs& p) {
+// no_mid: the token-major W' tile of the input gradient needs whole 128-column chunks.
+Tile choose_tile(const LoraArgs& p, bool no_mid = false) {
   const int64_t tm = (p.M + 255) / 256;
-  const bool f256 = groups_fit(p, 256), f192 = groups_fit(p, 192), f128 = groups_fit(p, 128);
+  const bool f256 = groups_fit(p, 256), f192 = groups_fit(p, 192) && !no_mid, f128 = groups_fit(p, 128);
   const double big = f256 ? wave_efficiency(tm * ((p.N + 255) / 256)) : -1.0;
   const double mid = f192 ? wave_efficiency(tm * ((p.N + 191) / 192)) * 0.95 : -1.0;
   const double tall = f256 ? wave_efficiency(((p.M + 127) / 128) * ((p.N + 255) / 256)) * 0.85 : -1.0;
@@ -1112,7 +1130,7 @@ struct TilePick {
   Tile tile;
   int strips;
 };
-TilePick pick_tiles(const LoraArgs& p, int wdt, bool has_w, int rb, bool ext_t, bool gather) {
+TilePick pick_tiles(const LoraArgs& p, int wdt, bool has_w, int rb, bool ext_t, bool gather, bool wt = false) {
   TilePick t{Tile::kBig, 1};
   if (rb == 2) {
     // Ranks 33-64 (two rank blocks) use 128 x 256, whose 64 x 64 wave tile leaves registers
@@ -1123,7 +1141,7 @@ TilePick pick_tiles(const LoraArgs& p, int wdt, bool has_w, int rb, bool ext_t, 
     const double small = wave_efficiency(tm * ((p.N + 127) / 128)) * 0.75;
     t.tile = small > tall ? Tile::kSmall : Tile::kTall;
   } else {
-    t.tile = choose_tile(p);
+    t.tile = choose_tile(p, wt);
   }
   // 128 x 128 tiles: with at most one workgroup per CU (no more tiles than CUs) the deep
   // ring, else two workgroups per CU on the two-buffer ring (they hide each other's fills).
@@ -1134,22 +1152,26 @@ TilePick pick_tiles(const LoraArgs& p, int wdt, bool has_w, int rb, bool ext_t, 
   return t;
 }
 
-template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER = false>
+template <int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER = false, bool WT = false>
 hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
-  const TilePick t = pick_tiles(p, WDT, HAS_W, RB, EXT_T, GATHER);
+  const TilePick t = pick_tiles(p, WDT, HAS_W, RB, EXT_T, GATHER, WT);
   if constexpr (WDT == kBF16 && !GATHER) {
-    if (t.tile == Tile::kDeep) return launch_cfg<CfgDeep, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    if (t.tile == Tile::kDeep)
+      return launch_cfg<CfgDeep, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, false, WT>(p, tg, ldt);
   }
   if constexpr (RB == 2) {
-    if (t.tile == Tile::kTall) return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
-    return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
+    if (t.tile == Tile::kTall) return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER, WT>(p, tg, ldt, t.strips);
+    return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, false, WT>(p, tg, ldt);
   } else {
     switch (t.tile) {
-      case Tile::kMid: return launch_tiles<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
-      case Tile::kTall: return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
+      case Tile::kMid:
+        if constexpr (!WT) return launch_tiles<CfgMid, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
+        else return hipErrorInvalidValue;  // not picked for WT (no_mid)
+      case Tile::kTall: return launch_tiles<CfgTall, WDT, HAS_W, RB, EXT_T, GATHER, WT>(p, tg, ldt, t.strips);
       case Tile::kSmall:
-      case Tile::kDeep: return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt);
-      default: return launch_tiles<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER>(p, tg, ldt, t.strips);
+      case Tile::kDeep:
+        return launch_cfg<CfgSmall, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, false, WT>(p, tg, ldt);
+      default: return launch_tiles<CfgBig, WDT, HAS_W, RB, EXT_T, GATHER, WT>(p, tg, ldt, t.strips);
     }
   }
 }
@@ -1618,38 +1640,21 @@ bool prefill_wt_supported(const LoraArgs& q) {
 }
 
 namespace {
-template <class C, int WDT, int RB, bool EXT_T>
-hipError_t launch_wt_cfg(const LoraArgs& q, const uint16_t* tg, int64_t ldt) {
-  return launch_cfg<C, WDT, true, RB, EXT_T, false, false, false, false, false, true>(q, tg, ldt);
-}
-
-template <class C, int WDT>
-hipError_t launch_wt_rank(const LoraArgs& q, const uint16_t* tg, int64_t ldt) {
-  if (tg != nullptr) return launch_wt_cfg<C, WDT, 0, true>(q, tg, ldt);
-  const int rb = rank_blocks_of(q.r);
-  if (rb == 1) return launch_wt_cfg<C, WDT, 1, false>(q, nullptr, 0);
-  if constexpr (C::BM == 128) {
-    if (rb == 2) return launch_wt_cfg<C, WDT, 2, false>(q, nullptr, 0);
-  }
-  return launch_wt_cfg<C, WDT, 0, false>(q, nullptr, 0);
-}
-
 template <int WDT>
-hipError_t launch_wt_tiles(const LoraArgs& q, int rb, const uint16_t* tg, int64_t ldt) {
-  const double big = rb == 2 ? -1.0 : wave_efficiency(((q.M + 255) / 256) * ((q.N + 255) / 256));
-  const double tall = wave_efficiency(((q.M + 127) / 128) * ((q.N + 255) / 256)) * 0.85;
-  const double small = wave_efficiency(((q.M + 127) / 128) * ((q.N + 127) / 128)) * 0.75;
-  if (small > big && small > tall) return launch_wt_rank<CfgSmall, WDT>(q, tg, ldt);
-  if (tall > big) return launch_wt_rank<CfgTall, WDT>(q, tg, ldt);
-  return launch_wt_rank<CfgBig, WDT>(q, tg, ldt);
+hipError_t launch_wt_rank(const LoraArgs& q, const uint16_t* tg, int64_t ldt) {
+  if (tg != nullptr) return launch_variant<WDT, true, 0, true, false, true>(q, tg, ldt);
+  if (q.r == 0) return launch_variant<WDT, true, 0, false, false, true>(q, nullptr, 0);
+  if (q.r <= 32) return launch_variant<WDT, true, 1, false, false, true>(q, nullptr, 0);
+  return launch_variant<WDT, true, 2, false, false, true>(q, nullptr, 0);
 }
 }  // namespace
 
-// Tiles as the forward chooses them by how they fill the CUs, without the 192-wide one (the
-// token-major W' tile needs whole 128-column chunks); ranks 33-64 take 128-row tiles. Ranks
-// above 64 take T = s dY . B from the rank pre-pass in the workspace. An fp8 W is decoded
-// through registers with each row's scale (bf16(code * scale), the values of the
-// dequantised W) into the same token-major tiles.
+// The forward's tile forms (tiles by how they fill the CUs, persistent strips, the three-
+// and four-buffer rings), without the 192-wide tile (the token-major W' tile needs whole
+// 128-column chunks). Ranks above 64 take T = s dY . B from the rank pre-pass in the
+// workspace. An fp8 W is decoded through registers with each row's scale (bf16(code *
+// scale), the values of the dequantised W) into the same token-major tiles (two-buffer
+// ring, no strips).
 hipError_t launch_prefill_wt(const LoraArgs& q_in) {
   LoraArgs q = q_in;
   q.gather_rows = q.K;  // every reduction row of W' is in range: no clamping in its fills
@@ -1662,9 +1667,8 @@ hipError_t launch_prefill_wt(const LoraArgs& q_in) {
     tg = t;
     ldt = q.r;
   }
-  const int rb = tg != nullptr ? 0 : rank_blocks_of(q.r);
-  if (q.w_dtype == kFP8) return launch_wt_tiles<kFP8>(q, rb, tg, ldt);
-  return launch_wt_tiles<kBF16>(q, rb, tg, ldt);
+  if (q.w_dtype == kFP8) return launch_wt_rank<kFP8>(q, tg, ldt);
+  return launch_wt_rank<kBF16>(q, tg, ldt);
 }
 
 hipError_t launch_prefill(const LoraArgs& p) {
