@@ -360,6 +360,24 @@ def test_tied_head_argmax_equals_argmax_of_logits(gpu, M):
     assert bool((chosen >= ref.max(-1).values - 2 ** -7 * ref.abs().max(-1).values).all())
 
 
+@pytest.mark.parametrize("M,V", [(8, 40000), (40, 33000), (2, 32768)])
+def test_tied_head_argmax_other_vocab_sizes(gpu, M, V):
+    """Vocabularies whose workgroup count is not a multiple of the arrival groups (and whose
+    last workgroup is partial): the same bit-for-bit bar, twice in a row."""
+    from weightshared_torchtitan_amd import ops
+    _say(f"[head argmax] M={M} V={V}")
+    g = torch.Generator(device="cuda").manual_seed(V + M)
+    k = 256
+    E = (torch.randn(V, k, device=gpu, generator=g) * 0.02).bfloat16()
+    z = torch.randn(M, k, device=gpu, generator=g).bfloat16()
+    assert ops.tied_head_argmax_supported(M, V, k)
+    want = torch.argmax(ops.lora_linear(z, E, None, None, 0.0), dim=-1)
+    for _ in range(2):
+        got = ops.tied_head_argmax_op(z, E)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+
+
 def test_tied_head_argmax_ties_and_nan(gpu):
     """Ties give the first index and NaN counts as largest (the first NaN wins), as
     torch.argmax; placed in different workgroups' rows so the cross-workgroup merge decides."""

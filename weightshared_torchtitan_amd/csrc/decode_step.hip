@@ -418,8 +418,11 @@ __global__ void __launch_bounds__(AM_T) argmax_kernel(const uint16_t* __restrict
 // Split argmax: a row's chunks are reduced by separate workgroups and merged with a 64-bit
 // atomic max on a key that orders (value, then the lower index) as am_better does: the
 // value's order-preserving bits (NaN above everything, -0 folded into +0) over the
-// complemented index. The last chunk of a row (arrival counter) writes the index and
-// returns the key and the counter to zero. Workspace: per row, the key and the counter on
+// complemented index. The last chunk of a row (arrival counter) takes the key with an
+// atomic exchange, writes the index and returns the counter to zero. The atomics are
+// relaxed (each chunk waits for its maximum to be performed before it arrives, and the key
+// is read by an atomic at the same scope): a release/acquire pair would add an L2
+// write-back and invalidate to every chunk. Workspace: per row, the key and the counter on
 // lines of their own (AMS_ROW bytes).
 constexpr int AMS_T = 256;
 constexpr int64_t AMS_CHUNK = 4096;  // elements per workgroup (at least)
@@ -468,11 +471,10 @@ __global__ void __launch_bounds__(AMS_T) argmax_split_kernel(const uint16_t* __r
     uint64_t* key = reinterpret_cast<uint64_t*>(ws + (size_t)row * AMS_ROW);
     unsigned* cnt = reinterpret_cast<unsigned*>(ws + (size_t)row * AMS_ROW + 128);
     if (bi != INT64_MAX) __hip_atomic_fetch_max(key, am_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == (unsigned)(nsplit - 1)) {  // every chunk's key is in
-      const uint64_t kv = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      out[row] = am_index(kv);
-      __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the maximum is performed before the arrival
+    const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (unsigned)(nsplit - 1)) {  // every chunk's key is in: take it, leaving zero
+      out[row] = am_index(__hip_atomic_exchange(key, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
       __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }

@@ -709,9 +709,16 @@ struct NormPrologue {
 
 // Greedy-token epilogue of a W workgroup: no output is written. Each token's logits over
 // this workgroup's rows are rounded to bf16 (the values the unfused head would store), and
-// the best (value, lowest index) key per token goes into a 64-bit atomic max. The last
-// workgroup to arrive writes each token's index and returns the keys and the counter to
-// zero, so every completed launch leaves them zero.
+// the best (value, lowest index) key per token goes into a 64-bit atomic max. Once this
+// workgroup's maxima are performed (vmcnt) it arrives at the counter; the last workgroup to
+// arrive takes every key with an atomic exchange (performed where the maxima were, after
+// all of them, and leaving zero behind), writes each token's index and returns the counter
+// to zero, so every completed launch leaves the keys and the counter zero. The atomics are
+// relaxed: the data passed on are the keys themselves, read by atomics at the same scope,
+// so no release or acquire is needed, and each of those (an L2 write-back or invalidate)
+// cost about 3 us on the launch (C4 head, 396 workgroups: 27.8 against 30.8 us; the GEMV
+// without the epilogue 21.8). Spreading the arrivals over 32 counters and a top counter
+// was slower still (one more round trip for the last workgroup).
 template <int ROWS, int MC>
 __device__ __forceinline__ void argmax_epilogue(const DecodeArgs& p, const float* sums, int row0, char* smem) {
   constexpr int RG = DT / MC;  // row groups
@@ -744,17 +751,12 @@ __device__ __forceinline__ void argmax_epilogue(const DecodeArgs& p, const float
   wait_vm<0>();     // every maximum of this workgroup is performed
   __syncthreads();  // ... before its arrival
   if (tid == 0) {
-    const unsigned old = __hip_atomic_fetch_add(p.am_cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned old = __hip_atomic_fetch_add(p.am_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *last = old == (unsigned)(p.am_total - 1);
   }
   __syncthreads();
   if (!*last) return;
-  if (tid < p.M) {
-    uint64_t* key = p.am_keys + (size_t)tid * kAmStride;
-    const uint64_t kv = __hip_atomic_load(key, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-    p.am_out[tid] = am_index(kv);
-    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (tid < p.M) p.am_out[tid] = am_index(take_agent(p.am_keys + (size_t)tid * kAmStride));
   if (tid == 0) __hip_atomic_store(p.am_cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1597,6 +1599,10 @@ bool decode_argmax_supported(const LoraArgs& p) {
   if (p.M > kDecodeMaxM || p.r != 0 || p.w_dtype != kBF16 || !decode_supported(p)) return false;
   return argmax_plan_ok(plan_decode(p.M, p.N, p.K, 0, kBF16, Pick::kFused));
 }
+
+// One 256-byte slot per token: the 64-bit key at its start; the slot of token 0 also holds
+// the arrival counter, at byte 128.
+size_t decode_argmax_keys_bytes(int64_t M) { return (size_t)(M > 1 ? M : 1) * 256; }
 
 hipError_t launch_decode_argmax(const LoraArgs& p, void* keys, int64_t* out) {
   const DecodePlan pl = plan_decode(p.M, p.N, p.K, 0, kBF16, Pick::kFused);

@@ -871,7 +871,7 @@ int wsl_lora_linear_chain_status(void* workspace, void* stream, int32_t* failed)
 }
 
 size_t wsl_tied_head_argmax_workspace_bytes(int64_t M) {
-  return wsl::kCounterBytes + (size_t)(M > 1 ? M : 1) * 256;
+  return wsl::kCounterBytes + wsl::decode_argmax_keys_bytes(M);
 }
 
 int wsl_tied_head_argmax_supported(int64_t M, int64_t N, int64_t K) {

@@ -229,9 +229,10 @@ hipError_t launch_decode_chain(int64_t M, int n, const LoraArgs* ps, const Fused
                                void* ws, hipStream_t stream);
 size_t decode_chain_err_offset();
 // The tied output head fused with the greedy argmax: out[m] = argmax_n bf16(x[m] . W[n]),
-// no logits written. `keys` holds one 256-byte slot per token (64-bit key; the slot of
-// token 0 also holds the arrival counter at byte 128), zero before a launch and after it.
+// no logits written. `keys` (decode_argmax_keys_bytes(M) bytes) holds the 64-bit keys of
+// the arrival groups and their counters, zero before a launch and after it.
 bool decode_argmax_supported(const LoraArgs& p);
+size_t decode_argmax_keys_bytes(int64_t M);
 hipError_t launch_decode_argmax(const LoraArgs& p, void* keys, int64_t* out);
 
 hipError_t launch_generic(const LoraArgs& p);
