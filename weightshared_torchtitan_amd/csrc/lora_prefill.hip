@@ -1268,13 +1268,21 @@ bool prefill_supported(const LoraArgs& p) {
   return true;
 }
 
+// Whether a split rank pre-pass of rank rt takes the in-launch reduction: whole 128-column
+// tiles (a split's record is a whole tile's accumulators, 4x the partials of rank 32) and
+// an arrival counter per tile.
+bool prepass_in_launch(int64_t M, int64_t rt) {
+  return rt % 128 == 0 && ((M + 127) / 128) * (rt / 128) <= kRedMaxTiles;
+}
+
 // Bytes of the rank pre-pass region for M rows of rank rt: T [M][rt] bf16, then, when K is
-// split, the fp32 partials at the next 256-byte boundary: one 128 x 128 tile's worth per
-// (tile, split), the in-launch records' size and at least [splits][M][rt].
+// split, the fp32 partials [splits][M][rt] at the next 256-byte boundary (M rounded up to
+// whole 128-row tiles for the in-launch reduction's records).
 size_t rank_prepass_bytes(int64_t M, int64_t K, int64_t rt) {
   const size_t t_bytes = ((size_t)(M * rt * 2) + 255) & ~(size_t)255;
   const int splits = rank_splits(M, K, rt);
-  return t_bytes + (splits > 1 ? (size_t)splits * ((M + 127) / 128 * 128) * ((rt + 127) / 128 * 128) * 4 : 0);
+  const int64_t rows = prepass_in_launch(M, rt) ? (M + 127) / 128 * 128 : M;
+  return t_bytes + (splits > 1 ? (size_t)splits * rows * rt * 4 : 0);
 }
 
 namespace {
@@ -1511,10 +1519,11 @@ size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w
 // plain GEMM with A in the place of W (N = r) and s applied before rounding. With few row
 // tiles (N = r is one or two tiles wide) K is split over grid rows on the four-buffer ring
 // (one workgroup per CU, three K tiles in flight), whose partial sums are those of the
-// two-buffer form (the same K tiles and k steps in the same order). The split's last
-// workgroup of a tile to arrive sums the fp32 records in split order, scales and rounds
-// (the in-launch reduction of the RED form), or, without arrival counters, a second kernel
-// sums fp32 partials in the same order: T is the same bit for bit. One launch instead of
+// two-buffer form (the same K tiles and k steps in the same order). At ranks of whole
+// 128-column tiles the split's last workgroup of a tile to arrive sums the fp32 records in
+// split order, scales and rounds (the in-launch reduction of the RED form); otherwise (or
+// without arrival counters) a second kernel sums fp32 partials in the same order: T is the
+// same bit for bit. One launch instead of
 // two, in the same time at config 5 (M = 4096, r = 128, K = 4096: 21-25 us against 18.7
 // for the split product plus 5.1 for the sum). A grouped launch runs one pre-pass over all
 // groups' A blocks (N = groups * r).
@@ -1528,8 +1537,7 @@ hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
   const int splits = rank_splits(p.M, p.K, rt);
   if (splits > 1) {
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(t) + (((size_t)(p.M * rt * 2) + 255) & ~(size_t)255));
-    const int64_t tiles = ((p.M + 127) / 128) * ((rt + 127) / 128);
-    if (p.red_cnt != nullptr && tiles <= kRedMaxTiles) {
+    if (p.red_cnt != nullptr && prepass_in_launch(p.M, rt)) {
       q.K = p.K / splits;
       return launch_cfg<CfgDeep, kBF16, true, 0, false, false, false, false, true>(
           q, nullptr, 0, splits, reinterpret_cast<uint64_t*>(part), p.red_cnt);
