@@ -788,58 +788,45 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
     __syncthreads();
     if (*red_last == 0) return;
-    // the last split: every record, in split order (this one's own included). QB records'
-    // words are in flight at a time (as many as the registers beside the accumulators
-    // take), each batch one memory round trip.
-    constexpr int QB = (EW <= 16) ? 4 : 2;
-    for (int q0 = 0; q0 < S; q0 += QB) {
-      uint64_t wb[QB][EB];
-      uint64_t wt[QB][ET > 0 ? ET : 1];
+    // the last split: every record, in split order (this one's own included), one split's
+    // words in flight at a time
+    for (int q = 0; q < S; ++q) {
+      const uint64_t* src = rec(q);
+      uint64_t wb[EB];
 #pragma unroll
-      for (int b = 0; b < QB; ++b) {
-        if (q0 + b < S) {
-          const uint64_t* src = rec(q0 + b);
+      for (int e = 0; e < EB; ++e)
+        wb[e] = __hip_atomic_load(const_cast<uint64_t*>(src + e * 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint64_t wt[ET > 0 ? ET : 1];
+      if constexpr (RB > 0) {
+        if (t_wave) {
 #pragma unroll
-          for (int e = 0; e < EB; ++e)
-            wb[b][e] = __hip_atomic_load(const_cast<uint64_t*>(src + e * 64), __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-          if constexpr (RB > 0) {
-            if (t_wave) {
-#pragma unroll
-              for (int e = 0; e < ET; ++e)
-                wt[b][e] = __hip_atomic_load(const_cast<uint64_t*>(src + (EB + e) * 64), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-            }
-          }
+          for (int e = 0; e < ET; ++e)
+            wt[e] = __hip_atomic_load(const_cast<uint64_t*>(src + (EB + e) * 64), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
         }
       }
 #pragma unroll
-      for (int b = 0; b < QB; ++b) {
-        if (q0 + b >= S) break;
-        const bool first_rec = q0 + b == 0;
+      for (int i = 0; i < C::NI; ++i)
 #pragma unroll
-        for (int i = 0; i < C::NI; ++i)
+        for (int j = 0; j < C::MJ; ++j)
 #pragma unroll
-          for (int j = 0; j < C::MJ; ++j)
+          for (int v = 0; v < 8; ++v) {
+            const uint64_t u = wb[(i * C::MJ + j) * 8 + v];
+            const float lo = __uint_as_float((uint32_t)u), hi = __uint_as_float((uint32_t)(u >> 32));
+            acc[i][j][2 * v] = q == 0 ? lo : acc[i][j][2 * v] + lo;
+            acc[i][j][2 * v + 1] = q == 0 ? hi : acc[i][j][2 * v + 1] + hi;
+          }
+      if constexpr (RB > 0) {
+        if (t_wave) {
+#pragma unroll
+          for (int qq = 0; qq < TPW; ++qq)
 #pragma unroll
             for (int v = 0; v < 8; ++v) {
-              const uint64_t u = wb[b][(i * C::MJ + j) * 8 + v];
+              const uint64_t u = wt[qq * 8 + v];
               const float lo = __uint_as_float((uint32_t)u), hi = __uint_as_float((uint32_t)(u >> 32));
-              acc[i][j][2 * v] = first_rec ? lo : acc[i][j][2 * v] + lo;
-              acc[i][j][2 * v + 1] = first_rec ? hi : acc[i][j][2 * v + 1] + hi;
+              acct[qq][2 * v] = q == 0 ? lo : acct[qq][2 * v] + lo;
+              acct[qq][2 * v + 1] = q == 0 ? hi : acct[qq][2 * v + 1] + hi;
             }
-        if constexpr (RB > 0) {
-          if (t_wave) {
-#pragma unroll
-            for (int qq = 0; qq < TPW; ++qq)
-#pragma unroll
-              for (int v = 0; v < 8; ++v) {
-                const uint64_t u = wt[b][qq * 8 + v];
-                const float lo = __uint_as_float((uint32_t)u), hi = __uint_as_float((uint32_t)(u >> 32));
-                acct[qq][2 * v] = first_rec ? lo : acct[qq][2 * v] + lo;
-                acct[qq][2 * v + 1] = first_rec ? hi : acct[qq][2 * v + 1] + hi;
-              }
-          }
         }
       }
     }
@@ -1268,21 +1255,12 @@ bool prefill_supported(const LoraArgs& p) {
   return true;
 }
 
-// Whether a split rank pre-pass of rank rt takes the in-launch reduction: whole 128-column
-// tiles (a split's record is a whole tile's accumulators, 4x the partials of rank 32) and
-// an arrival counter per tile.
-bool prepass_in_launch(int64_t M, int64_t rt) {
-  return rt % 128 == 0 && ((M + 127) / 128) * (rt / 128) <= kRedMaxTiles;
-}
-
 // Bytes of the rank pre-pass region for M rows of rank rt: T [M][rt] bf16, then, when K is
-// split, the fp32 partials [splits][M][rt] at the next 256-byte boundary (M rounded up to
-// whole 128-row tiles for the in-launch reduction's records).
+// split, the fp32 partials [splits][M][rt] at the next 256-byte boundary.
 size_t rank_prepass_bytes(int64_t M, int64_t K, int64_t rt) {
   const size_t t_bytes = ((size_t)(M * rt * 2) + 255) & ~(size_t)255;
   const int splits = rank_splits(M, K, rt);
-  const int64_t rows = prepass_in_launch(M, rt) ? (M + 127) / 128 * 128 : M;
-  return t_bytes + (splits > 1 ? (size_t)splits * rows * rt * 4 : 0);
+  return t_bytes + (splits > 1 ? (size_t)splits * M * rt * 4 : 0);
 }
 
 namespace {
@@ -1517,16 +1495,11 @@ size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w
 
 // Pre-pass: T = bf16(s * x . A^T) [M, r] into the workspace, by the prefill kernel run as a
 // plain GEMM with A in the place of W (N = r) and s applied before rounding. With few row
-// tiles (N = r is one or two tiles wide) K is split over grid rows on the four-buffer ring
-// (one workgroup per CU, three K tiles in flight), whose partial sums are those of the
-// two-buffer form (the same K tiles and k steps in the same order). At ranks of whole
-// 128-column tiles the split's last workgroup of a tile to arrive sums the fp32 records in
-// split order, scales and rounds (the in-launch reduction of the RED form); otherwise (or
-// without arrival counters) a second kernel sums fp32 partials in the same order: T is the
-// same bit for bit. One launch instead of
-// two, in the same time at config 5 (M = 4096, r = 128, K = 4096: 21-25 us against 18.7
-// for the split product plus 5.1 for the sum). A grouped launch runs one pre-pass over all
-// groups' A blocks (N = groups * r).
+// tiles (N = r is one or two tiles wide) K is split over grid rows into fp32 partials that
+// a second kernel sums in split order, scales and rounds; the splits run on the four-buffer
+// ring (one workgroup per CU, three K tiles in flight), whose partial sums are those of the
+// two-buffer form (the same K tiles and k steps in the same order). A grouped launch runs
+// one pre-pass over all groups' A blocks (N = groups * r).
 hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
   const int64_t rt = p.r * p.groups;
   LoraArgs q = p;
@@ -1537,11 +1510,6 @@ hipError_t rank_prepass(const LoraArgs& p, uint16_t* t) {
   const int splits = rank_splits(p.M, p.K, rt);
   if (splits > 1) {
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(t) + (((size_t)(p.M * rt * 2) + 255) & ~(size_t)255));
-    if (p.red_cnt != nullptr && prepass_in_launch(p.M, rt)) {
-      q.K = p.K / splits;
-      return launch_cfg<CfgDeep, kBF16, true, 0, false, false, false, false, true>(
-          q, nullptr, 0, splits, reinterpret_cast<uint64_t*>(part), p.red_cnt);
-    }
     q.y = part; q.K = p.K / splits;
     hipError_t e = launch_cfg<CfgDeep, kBF16, true, 0, false, false, true>(q, nullptr, 0, splits);
     if (e != hipSuccess) return e;
