@@ -145,7 +145,8 @@ int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx,
  * suffice), the T work covering all groups' A rows. Otherwise the groups run as consecutive
  * launches on `stream`. Results are those of the per-group calls, bit for bit, except where
  * a K split count depends on N (the decode path between 65 and 72 tokens; the prefill
- * path's in-launch split-K form, taken where 128 x 128 tiles leave CUs idle) or, for an fp8
+ * path's in-launch split-K form, taken where 128 x 128 tiles leave CUs idle), where the
+ * column tiles of a launch share T (WSL_OPT_PREFILL_SHARED_T; one wave of tiles) or, for an fp8
  * W on prefill shapes, where the choice between the fp8 matrix cores and W decoded onto the
  * bf16 matrix cores depends on the launch's width (WSL_OPT_FP8_PREFILL): there the groups'
  * outputs agree with the per-group calls within the forward's bar.
@@ -295,6 +296,12 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
  *   WSL_OPT_DECODE_RES_SPLITS  0 auto; n in [2, 8] at least n K splits for the decode step's
  *                              residual-epilogue launches (wsl_lora_linear_fused_fwd) where
  *                              the slices keep eight wave steps
+ *   WSL_OPT_PREFILL_SHARED_T   0 auto (one-wave launches of one in-loop rank block over
+ *                              K >= 4096 share T between the column tiles of each row
+ *                              block); -1 T in every
+ *                              tile; 1 shared, with every tile taking the no-wait path (it
+ *                              computes the classes of T from global memory: bit-exact
+ *                              with 0)
  * wsl_set_option returns WSL_E_INVALID_ARG for an unknown option or a value out of range.
  */
 #define WSL_OPT_PREFILL_STRIPS 1
@@ -305,14 +312,16 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
 #define WSL_OPT_DECODE_WIDE 6
 #define WSL_OPT_DECODE_SPIN_LIMIT 7
 #define WSL_OPT_DECODE_RES_SPLITS 8
-#define WSL_OPT_COUNT 9
+#define WSL_OPT_PREFILL_SHARED_T 9
+#define WSL_OPT_COUNT 10
 int wsl_set_option(int32_t option, int64_t value);
 int wsl_get_option(int32_t option, int64_t* value);
 
 /*
  * The plan a grouped (n_groups >= 1) or single call of these sizes takes, for dense,
  * 256-byte aligned operands (pointer alignment also steers the path). No counterpart in the
- * reference; it lets tests assert which kernel form their shapes reach. Pure host function.
+ * reference; it lets tests assert which kernel form their shapes reach. Host function: it
+ * launches nothing (shared_t reads the current device's CU count; 0 without a device).
  *   path         WSL_PATH_*; WSL_PATH_NONE for M = 0
  *   launches     calls of the main kernel (a grouped call that cannot run as one launch
  *                runs group by group: n_groups)
@@ -323,6 +332,9 @@ int wsl_get_option(int32_t option, int64_t* value);
  *   strip_tiles  output tiles per workgroup of the persistent strips (1: one per workgroup)
  *   k_splits     K splits of the split-K forms (1 otherwise)
  *   workgroups   workgroups of the main launch on the prefill paths (first group's), else 0
+ *   shared_t     1 when the column tiles of each row block share T (a launch of one wave of
+ *                tiles on this device over K >= 4096: each group's first four tiles compute
+ *                one class of T's k steps each, the other tiles none)
  */
 #define WSL_PATH_NONE 0
 #define WSL_PATH_PREFILL 1
@@ -340,6 +352,7 @@ typedef struct wsl_plan_info {
   int32_t strip_tiles;
   int32_t k_splits;
   int32_t workgroups;
+  int32_t shared_t;
 } wsl_plan_info;
 int wsl_lora_linear_plan(int64_t M, int64_t K, int64_t r, int32_t n_groups, const int64_t* group_n,
                          int32_t w_dtype, wsl_plan_info* out);

@@ -6,6 +6,9 @@ tile form each takes asserted through wsl_lora_linear_plan:
 - Qwen3-1.7B o (8192 x 2048 -> 2048) and down (8192 x 6144 -> 2048): 256 x 256 tiles, one
   rank block, one tile per workgroup.
 
+All four are one wave of tiles; over K >= 4096 (the 1.7B down) their column tiles share T
+(tests/test_gpu_shared_t.py).
+
 Rows are independent, so the float64 oracle runs on rows sampled from every 128-row block
 (first, middle, last) of the GPU output (bar max|y - y_ref| / max|y_ref| <= 1e-2). Also the
 grouped in-launch split-K case whose group ends fall on 192 but not 128 columns, which must
@@ -45,6 +48,7 @@ def test_one_wave_launches_match_oracle(gpu, name, M, N, K, r, tile):
     p = ops.plan(M, K, r, [N])
     assert p["path"] == "prefill" and (p["tile_m"], p["tile_n"]) == tile
     assert p["rank_blocks"] == 1 and p["strip_tiles"] == 1 and p["k_splits"] == 1 and p["launches"] == 1
+    assert p["shared_t"] == (1 if K >= 4096 else 0)  # T shared by the column tiles over a long K
     g = torch.Generator().manual_seed(M + N + K + r)
     x = torch.randn(M, K, generator=g).bfloat16()
     W = (torch.randn(N, K, generator=g) * 0.02).bfloat16()

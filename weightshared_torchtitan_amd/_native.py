@@ -111,6 +111,7 @@ OPTIONS = {
     "decode_wide": 6,        # -1: 65-72 tokens on the prefill path
     "decode_spin_limit": 7,  # n > 0: poll bound of the decode hand-offs; -1: no polling
     "decode_res_splits": 8,  # 2..8: K splits of the decode step's residual-epilogue launches
+    "prefill_shared_t": 9,   # -1: T in every tile; 1: shared T with every tile on the no-wait path
 }
 
 # wsl_plan_info.path values
@@ -120,7 +121,8 @@ PATHS = {0: "none", 1: "prefill", 2: "prefill_splitk", 3: "prefill_medium", 4: "
 
 class PlanInfo(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("path", "launches", "tile_m", "tile_n", "rank_blocks",
-                                               "rank_prepass", "strip_tiles", "k_splits", "workgroups")]
+                                               "rank_prepass", "strip_tiles", "k_splits", "workgroups",
+                                               "shared_t")]
 
 
 def _declare(lib: ctypes.CDLL) -> None:

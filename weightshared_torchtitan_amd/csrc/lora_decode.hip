@@ -1650,18 +1650,6 @@ struct ChainPlan {
   bool ok = false;
 };
 
-int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = v;
-  }
-  return cus[dev];
-}
-
 // The stages' plans (the decode path's one-slice plans of one token block), the workspace
 // layout (counter prefix, the stages' flag words, then each stage's hand-off region) and
 // the LDS. `cus`: CUs of the device (0: the layout only).

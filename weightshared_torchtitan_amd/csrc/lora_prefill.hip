@@ -44,6 +44,7 @@
 // Reference arithmetic being fused: torchtitan/models/llama3/model/model.py:189-192
 // (LoRAModule.forward), :392-398 (base projection + broadcast_add with g = 1).
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cstdlib>
 #include <cstring>
@@ -60,6 +61,7 @@ constexpr int ROWB = 128; // bytes per LDS row (BK bf16)
 constexpr int KK = 4;     // MFMA k steps per K tile
 constexpr int N_XCD = 8;
 constexpr int GROUP_M = 4;  // row tiles per XCD group (4 against 8 and 16: +0.9 % at config 2 grouped)
+constexpr int kShareClasses = KK;  // shared T (SKT): classes of T's k steps, k step c of every K tile
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -162,6 +164,16 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Calls f(std::integral_constant<int, I>{}) for I = B .. E-1: the k steps of a K tile as
+// compile-time indices.
+template <int B, int E, class F>
+__device__ __forceinline__ void for_ct(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    for_ct<B + 1, E>(f);
+  }
+}
+
 // SPLIT: split-K plain GEMM for the rank pre-pass. Workgroup row blockIdx.y takes the K
 // range [blockIdx.y * K, (blockIdx.y + 1) * K) of x and W and writes its fp32 partial
 // product to slice blockIdx.y of y (viewed as fp32 [gridDim.y][M][ldy]).
@@ -194,8 +206,19 @@ __device__ __forceinline__ void ring_barrier() {
 // columns. The W' tile goes into LDS as [64 k][BN] like the TN operands (every K row is
 // in range: K % 64 == 0), and its fragments are the same two transposing reads, whose k
 // order (16 kk + 8 (lane / 32) + 0..7) is that of x's plain fragments.
+//
+// SKT: T shared by the column tiles of a row block and group (launches of one wave of tiles,
+// every workgroup resident at once). The group's first kShareClasses tiles each compute one
+// class of T's k steps (class c: k step c of every K tile), publish the fp32 partial
+// (red_part, lane-major words as RED's records) and arrive at the row block's counter
+// (red_cnt[2 rbg]); the other tiles of the group do no rank work. Every tile then waits for
+// all the classes, sums them in class order (so every tile of the row block holds the same
+// T) and goes on as if it had computed T itself. A wait that runs past skt_spin polls
+// computes the classes it has not seen from x and A in global memory (the same k steps in
+// the same order: the same bits), so the launch ends whatever the residency; the last
+// tile to pass (red_cnt[2 rbg + 1]) returns both counters to zero.
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
-          bool RED = false, bool PER = false, bool WT = false>
+          bool RED = false, bool PER = false, bool WT = false, bool SKT = false>
 __global__ void __launch_bounds__(C::NT, 1)
 prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                const int64_t* __restrict__ gidx, int64_t grows,
@@ -206,7 +229,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                uint16_t* __restrict__ y, int64_t ldy,
                int M, int N, int K, int r, int tiles_m, int tiles_n,
                int ge0, int ge1, int ge2, int64_t a_gstride, int t_gstride, RowMap wmap,
-               uint64_t* __restrict__ red_part, unsigned* __restrict__ red_cnt, int tpw) {
+               uint64_t* __restrict__ red_part, unsigned* __restrict__ red_cnt, int tpw, int skt_spin) {
   constexpr bool W8 = HAS_W && WDT == kFP8;
   constexpr bool WDIRECT = HAS_W && WDT == kBF16;
   constexpr bool LORA = RB > 0 || EXT_T;
@@ -233,6 +256,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   static_assert(!WT || (HAS_W && !TN && !GATHER && !SPLIT && !RED && C::BN % 128 == 0 &&
                         (WDT == kBF16 || (C::NS == 2 && (64 * C::BN / 16) % C::NT == 0))),
                 "token-major W': x as it lies, 128-column multiples (fp8: two-buffer ring)");
+  static_assert(!SKT || (WDT == kBF16 && HAS_W && RB == 1 && !EXT_T && !GATHER && !SPLIT && !TN && !RED && !PER && !WT),
+                "shared T: one in-loop rank block, bf16 W, one tile per workgroup");
   int64_t tok_rem = grows;  // TN: K rows from this workgroup's first one to the end (>= 1)
   if constexpr (RED) {
     const int64_t kofs = (int64_t)blockIdx.y * K;
@@ -298,6 +323,18 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   const int grp = (n0 >= ge0) + (n0 >= ge1) + (n0 >= ge2);
   const uint16_t* const a = a_arg + grp * a_gstride;
   const uint16_t* const tg = tg_arg + grp * t_gstride;
+  // SKT: the tile's row block and group (rbg), the group's tile count and the tile's class
+  // of T's k steps (its column index in the group; -1 past the classes: no rank work)
+  int skt_cls = -1, skt_rbg = 0, skt_ntiles = 1;
+  if constexpr (SKT) {
+    const int gstart = grp == 0 ? 0 : grp == 1 ? ge0 : grp == 2 ? ge1 : ge2;
+    const int gend = grp == 0 ? ge0 : grp == 1 ? ge1 : grp == 2 ? ge2 : INT_MAX;
+    skt_ntiles = ((gend < N ? gend : N) - gstart + C::BN - 1) / C::BN;
+    const int ngroups = 1 + (ge0 != INT_MAX) + (ge1 != INT_MAX) + (ge2 != INT_MAX);
+    skt_rbg = tm * ngroups + grp;
+    const int local = (n0 - gstart) / C::BN;
+    skt_cls = local < kShareClasses ? local : -1;
+  }
 
   // ---- sources of this wave's direct fills: uniform tile base + 32-bit lane offset ----
   const char* xbase = reinterpret_cast<const char*>(GATHER ? x : x + (int64_t)m0 * ldx);
@@ -397,7 +434,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       for (int i = 0; i < C::NWI; ++i) direct_fill(sw, wave * C::NWI + i, wbase + k0 * 2 + opaque(woff[i]));
     }
     if constexpr (RB > 0) {
-      if (t_here && wave < NAI) direct_fill(sa, wave, reinterpret_cast<const char*>(a) + k0 * 2 + opaque(aoff));
+      if (t_here && wave < NAI && (!SKT || skt_cls >= 0))
+        direct_fill(sa, wave, reinterpret_cast<const char*>(a) + k0 * 2 + opaque(aoff));
     }
   };
   // B slice [BN][64 ranks from rk0] into `dst`. Lanes past rank r read a finite element
@@ -595,10 +633,12 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   // Interleave the MFMAs of the current k step with the LDS reads of the next one, so
   // the reads are issued early and their latency hides behind the MFMAs (left to
   // itself the scheduler sinks each read next to its use).
-  auto interleave = [&](auto do_t) {
-    constexpr int TT = decltype(do_t)::value ? TPW : 0;
-    constexpr int NMF = (HAS_W ? C::NI * C::MJ : 0) + TT;
-    constexpr int NRD = (C::MJ + (HAS_W ? C::NI : 0)) * (TN ? 2 : 1) + (WT ? C::NI : 0) + TT * (ALL_T ? 1 : 2);
+  // t_mma: this step's MFMAs include the rank work; t_load: the next step's reads do.
+  auto interleave = [&](auto t_mma, auto t_load) {
+    constexpr int TTM = decltype(t_mma)::value ? TPW : 0;
+    constexpr int TTL = decltype(t_load)::value ? TPW : 0;
+    constexpr int NMF = (HAS_W ? C::NI * C::MJ : 0) + TTM;
+    constexpr int NRD = (C::MJ + (HAS_W ? C::NI : 0)) * (TN ? 2 : 1) + (WT ? C::NI : 0) + TTL * (ALL_T ? 1 : 2);
     constexpr int PAIRS = NMF < NRD ? NMF : NRD;
 #pragma unroll
     for (int q = 0; q < PAIRS; ++q) {
@@ -616,9 +656,18 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   char* lora_b = lds + (nk % C::NS) * STAGE;
 
   constexpr bool RUN_K = HAS_W || RB > 0;
-  // The K loop, instantiated with and without this wave's T work (`do_t`), so the k steps
-  // carry no per-step branch and the MFMAs interleave with the next step's LDS reads.
-  auto run_k = [&](auto do_t) {
+  // Rank work at compile-time k step kc of a K tile: every step with do_t, or only step
+  // `cls` (a shared-T class; -1: every step).
+  auto t_at = [](auto do_t, auto cls, auto kc) {
+    return std::bool_constant<decltype(do_t)::value &&
+                              (decltype(cls)::value < 0 || decltype(cls)::value == decltype(kc)::value)>{};
+  };
+  using K0 = std::integral_constant<int, 0>;
+  using KL = std::integral_constant<int, KK - 1>;
+  // The K loop, instantiated with and without this wave's T work (`do_t`, at the k steps of
+  // `cls`), so the k steps carry no per-step branch and the MFMAs interleave with the next
+  // step's LDS reads.
+  auto run_k = [&](auto do_t, auto cls) {
     issue(0, 0);
     load_w8(0);
     wait_vm0();
@@ -634,17 +683,17 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       if (nk == 1) issue_b(lora_b, 0);
     }
     Frags cur;
-    frag_load(do_t, 0, 0, cur);
+    frag_load(t_at(do_t, cls, K0{}), 0, 0, cur);
     for (int kt = 0; kt < nk; ++kt) {
       const int buf = kt & 1;
-#pragma unroll
-      for (int kk = 0; kk < KK - 1; ++kk) {
+      for_ct<0, KK - 1>([&](auto kc) {
+        using KN = std::integral_constant<int, decltype(kc)::value + 1>;
         Frags nxt;
-        frag_load(do_t, buf, kk + 1, nxt);
-        frag_mma(do_t, cur);
-        interleave(do_t);
+        frag_load(t_at(do_t, cls, KN{}), buf, KN::value, nxt);
+        frag_mma(t_at(do_t, cls, kc), cur);
+        interleave(t_at(do_t, cls, kc), t_at(do_t, cls, KN{}));
         cur = nxt;
-      }
+      });
       if (kt + 1 < nk) {
         wait_vm0();          // tile kt+1 has landed (the only fill in flight)
         store_w8(buf ^ 1);   // fp8 base: decoded tile kt+1 into its buffer
@@ -656,9 +705,9 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       // The fill of tile kt+2 goes out after these MFMAs, so the MFMA pipes restart at
       // once after the barrier.
       Frags nxt;
-      frag_load(do_t, buf ^ 1, 0, nxt);
-      frag_mma(do_t, cur);
-      interleave(do_t);
+      frag_load(t_at(do_t, cls, K0{}), buf ^ 1, 0, nxt);
+      frag_mma(t_at(do_t, cls, KL{}), cur);
+      interleave(t_at(do_t, cls, KL{}), t_at(do_t, cls, K0{}));
       cur = nxt;
       if (kt + 1 < nk) {
         if (kt + 2 < nk) {
@@ -677,7 +726,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   // once every wave has read it (the barrier in tile kt). Each wait leaves the fills of the
   // NS-2 younger tiles in flight. With a workgroup alone on its CU, two buffers left every
   // K tile waiting one fill's latency (about 1.2 us per 128 x 128 x 64 tile at M = 256).
-  auto run_k_deep = [&](auto do_t) {
+  auto run_k_deep = [&](auto do_t, auto cls) {
     constexpr int NS = C::NS;
     constexpr int PT = C::NXI + (WDIRECT ? C::NWI : 0);  // fills per K tile of every wave (waves < NAI add one)
     const int pre = nk < NS ? nk : NS;
@@ -689,27 +738,27 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     else wait_vm0();
     ring_barrier();
     Frags cur;
-    frag_load(do_t, 0, 0, cur);
+    frag_load(t_at(do_t, cls, K0{}), 0, 0, cur);
     int buf = 0;
     for (int kt = 0; kt < nk; ++kt) {
       const int nbuf = buf + 1 == NS ? 0 : buf + 1;
-#pragma unroll
-      for (int kk = 0; kk < KK - 1; ++kk) {
+      for_ct<0, KK - 1>([&](auto kc) {
+        using KN = std::integral_constant<int, decltype(kc)::value + 1>;
         Frags nxt;
-        frag_load(do_t, buf, kk + 1, nxt);
-        frag_mma(do_t, cur);
-        interleave(do_t);
+        frag_load(t_at(do_t, cls, KN{}), buf, KN::value, nxt);
+        frag_mma(t_at(do_t, cls, kc), cur);
+        interleave(t_at(do_t, cls, kc), t_at(do_t, cls, KN{}));
         cur = nxt;
-      }
+      });
       if (kt + 1 < nk) {
         if (kt + NS - 1 < nk) wait_vm<(NS - 2) * PT>();  // tile kt+1 has landed
         else wait_vm0();
         ring_barrier();  // all fragments of tile kt are read; tile kt+1 visible
       }
       Frags nxt;
-      frag_load(do_t, nbuf, 0, nxt);
-      frag_mma(do_t, cur);
-      interleave(do_t);
+      frag_load(t_at(do_t, cls, K0{}), nbuf, 0, nxt);
+      frag_mma(t_at(do_t, cls, KL{}), cur);
+      interleave(t_at(do_t, cls, KL{}), t_at(do_t, cls, K0{}));
       cur = nxt;
       if (kt + NS < nk) {
         issue(buf, (kt + NS) * BK);
@@ -720,25 +769,130 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
     __syncthreads();
   };
-  auto run = [&](auto do_t) {
-    if constexpr (C::NS == 2) run_k(do_t);
-    else run_k_deep(do_t);
+  auto run = [&](auto do_t, auto cls) {
+    if constexpr (C::NS == 2) run_k(do_t, cls);
+    else run_k_deep(do_t, cls);
   };
+  using EVERY = std::integral_constant<int, -1>;
   if constexpr (RUN_K) {
     if constexpr (RB == 0) {
-      run(std::false_type{});
+      run(std::false_type{}, EVERY{});
     } else if constexpr (PER && !t_here) {
-      run(std::false_type{});
+      run(std::false_type{}, EVERY{});
+    } else if constexpr (SKT) {
+      static_assert(kShareClasses == 4, "shared-T classes are the four k steps of a K tile");
+      if (!t_wave || skt_cls < 0) run(std::false_type{}, EVERY{});
+      else if (skt_cls == 0) run(std::true_type{}, std::integral_constant<int, 0>{});
+      else if (skt_cls == 1) run(std::true_type{}, std::integral_constant<int, 1>{});
+      else if (skt_cls == 2) run(std::true_type{}, std::integral_constant<int, 2>{});
+      else run(std::true_type{}, std::integral_constant<int, 3>{});
     } else if constexpr (ALL_T) {
-      run(std::true_type{});
+      run(std::true_type{}, EVERY{});
     } else {
-      if (t_wave) run(std::true_type{});
-      else run(std::false_type{});
+      if (t_wave) run(std::true_type{}, EVERY{});
+      else run(std::false_type{}, EVERY{});
     }
   } else if constexpr (LORA) {
     issue_b(lora_b, 0);
   }
   WSL_STAMP(srec, 2);
+
+  if constexpr (SKT) {
+    // Shared T: publish this tile's class, wait for every class of the row block, sum them
+    // in class order into acct. Records are lane-major 8-byte words (two accumulators
+    // each), one [8][64] block per wave, for every (rbg, class).
+    constexpr int CL = kShareClasses;
+    static_assert(TPW == 1, "shared T: one T block per T wave");
+    auto part_of = [&](int c) { return red_part + (((int64_t)skt_rbg * CL + c) * C::NW + wave) * (8 * 64) + lane; };
+    unsigned* const pub = red_cnt + 2 * skt_rbg;
+    unsigned* const done = pub + 1;
+    // broadcast word: the W area of the buffer the last K tile ran from (idle now; T is
+    // parked below its first BM rows)
+    volatile int* skt_seen = reinterpret_cast<volatile int*>(lora_t + C::XB);
+    if (skt_cls >= 0) {
+      if (t_wave) {
+        uint64_t* dst = part_of(skt_cls);
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+          __hip_atomic_store(dst + v * 64,
+                             (uint64_t)__float_as_uint(acct[0][2 * v]) |
+                                 ((uint64_t)__float_as_uint(acct[0][2 * v + 1]) << 32),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      wait_vm0();  // the class is out before the arrival
+      __syncthreads();
+      if (tid == 0) __hip_atomic_fetch_add(pub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0) {
+      int seen = 0;
+      for (int it = 0; it < skt_spin; ++it) {
+        if (__hip_atomic_load(pub, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= (unsigned)CL) {
+          seen = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      *skt_seen = seen;
+    }
+    __syncthreads();
+    const bool seen = *skt_seen != 0;
+    if (t_wave) {
+      if (seen) {
+        uint64_t w[CL][8];
+#pragma unroll
+        for (int c = 0; c < CL; ++c)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            w[c][v] = __hip_atomic_load(const_cast<uint64_t*>(part_of(c) + v * 64), __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          float lo = __uint_as_float((uint32_t)w[0][v]), hi = __uint_as_float((uint32_t)(w[0][v] >> 32));
+#pragma unroll
+          for (int c = 1; c < CL; ++c) {
+            lo += __uint_as_float((uint32_t)w[c][v]);
+            hi += __uint_as_float((uint32_t)(w[c][v] >> 32));
+          }
+          acct[0][2 * v] = lo;
+          acct[0][2 * v + 1] = hi;
+        }
+      } else {
+        // Every class from global memory: the fragments the K loop reads from LDS (A rows
+        // past r read row r - 1, x rows past M row M - 1), the same k steps in the same order.
+        const uint16_t* arow = a + (int64_t)min(trb[0] * 32 + l32, r - 1) * lda + lh * 8;
+        const uint16_t* xrow = x + (int64_t)min(m0 + wm * C::TM + tj[0] * 32 + l32, M - 1) * ldx + lh * 8;
+        f32x16_t tc[CL];
+#pragma unroll
+        for (int c = 0; c < CL; ++c)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) tc[c][v] = 0.f;
+        for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+          for (int c = 0; c < CL; ++c) {
+            const int k = kt * BK + c * 16;
+            tc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ld_global_16(arow + k)),
+                                                             as_bf16x8(ld_global_16(xrow + k)), tc[c], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          float t = tc[0][v];
+#pragma unroll
+          for (int c = 1; c < CL; ++c) t += tc[c][v];
+          acct[0][v] = t;
+        }
+      }
+    }
+    wait_vm0();  // every read of the classes has returned
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == (unsigned)(skt_ntiles - 1)) {  // the row block's last: counters back to zero
+        __hip_atomic_store(pub, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
 
   if constexpr (RED) {
     // This split's partials: lane-major 8-byte words (two accumulators each), the base
@@ -1040,20 +1194,70 @@ bool groups_fit(const LoraArgs& p, int bn) {
 }
 
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool SPLIT = false, bool TN = false,
-          bool RED = false, bool PER = false, bool WT = false>
+          bool RED = false, bool PER = false, bool WT = false, bool SKT = false>
 hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int splits = 1,
-                      uint64_t* red_part = nullptr, unsigned* red_cnt = nullptr, int tpw = 1) {
+                      uint64_t* red_part = nullptr, unsigned* red_cnt = nullptr, int tpw = 1, int skt_spin = 0) {
   const int tiles_m = (int)((p.M + C::BM - 1) / C::BM);
   const int tiles_n = (int)((p.N + C::BN - 1) / C::BN);
-  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN, RED, PER, WT>
+  prefill_kernel<C, WDT, HAS_W, RB, EXT_T, GATHER, SPLIT, TN, RED, PER, WT, SKT>
       <<<dim3(tiles_m * tiles_n / (PER ? tpw : 1), splits), dim3(C::NT), 0, p.stream>>>(
       reinterpret_cast<const uint16_t*>(p.x), p.ldx, p.gather, p.gather_rows, p.w, p.ldw, p.w_scale,
       reinterpret_cast<const uint16_t*>(p.a), p.lda, tg, ldt,
       reinterpret_cast<const uint16_t*>(p.b), p.ldb, p.scale, p.yscale,
       reinterpret_cast<uint16_t*>(p.y), p.ldy, (int)p.M, (int)p.N, (int)p.K, (int)p.r, tiles_m, tiles_n,
       group_end(p, 0), group_end(p, 1), group_end(p, 2), p.groups > 1 ? p.r * p.lda : 0,
-      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0, p.wmap, red_part, red_cnt, PER ? tpw : 1);
+      (p.groups > 1 && tg != nullptr) ? (int)p.r : 0, p.wmap, red_part, red_cnt, PER ? tpw : 1, skt_spin);
   return hipGetLastError();
+}
+
+// ---- Shared T (the SKT form) ----
+// Records of one row block and group: kShareClasses classes x 8 waves x 64 lanes x 8 words.
+constexpr size_t kSktRbgBytes = (size_t)kShareClasses * 8 * 64 * 8 * 8;
+constexpr int kSktSpin = 1 << 16;  // polls of the row block's counter before a tile computes T itself
+// K tiles from which sharing pays: the exchange (the classes out and arrived, the counter
+// seen, the classes read: about 3.5 us with the tiles' skew) against three quarters of T's
+// MFMAs (1/9 of the loop's). Alternating graphs of 28 launches, shared against T in every
+// tile: 8192 x 6144 -> 2048 (96 K tiles) 163.2 against 173.4 us; 8192 x 3072 -> 1024 (48)
+// 55.5 / 55.9; 8192 x 2048 -> 2048 (32) 65.4 / 65.3; 8192 x 2048 -> 1024 (32) 40.9 / 40.0.
+constexpr int kSktMinKTiles = 64;
+
+// Row-block groups of a launch of BM x BN tiles that shares T between the column tiles of
+// each row block, or 0 where it does not: a long K (kSktMinKTiles), one wave of tiles on
+// this device (every workgroup resident at once, so the wait for the other tiles' classes
+// is short), at least kShareClasses tiles in every group, the arrival counters, and room in
+// the workspace for the records. WSL_OPT_PREFILL_SHARED_T = -1 keeps T in every tile.
+int64_t shared_t_rbgs(const LoraArgs& p, int bm, int bn) {
+  if (option(WSL_OPT_PREFILL_SHARED_T) < 0 || p.red_cnt == nullptr || p.ws == nullptr) return 0;
+  if (p.K / BK < kSktMinKTiles) return 0;
+  const int64_t tiles_m = (p.M + bm - 1) / bm, tiles_n = (p.N + bn - 1) / bn;
+  const int cus = device_cus();
+  if (cus <= 0 || tiles_m * tiles_n > cus) return 0;
+  int64_t start = 0;
+  for (int g = 0; g < p.groups; ++g) {
+    const int64_t end = g + 1 < p.groups ? p.gend[g] : p.N;
+    if ((end - start + bn - 1) / bn < kShareClasses) return 0;
+    start = end;
+  }
+  const int64_t rbgs = tiles_m * p.groups;
+  if (2 * rbgs > kRedMaxTiles || (size_t)rbgs * kSktRbgBytes > p.ws_bytes) return 0;
+  return rbgs;
+}
+
+// Workspace bytes the shared-T records of an M x N launch can take: at most a quarter of
+// its 128 x 256 tiles are row-block groups (every group has at least four tiles), and only
+// when those tiles are one wave on this device.
+size_t shared_t_bytes(int64_t M, int64_t N, int64_t K) {
+  if (K / BK < kSktMinKTiles) return 0;
+  const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256);
+  const int cus = device_cus();
+  return (cus > 0 && tiles <= cus) ? (size_t)((tiles + kShareClasses - 1) / kShareClasses) * kSktRbgBytes : 0;
+}
+
+template <class C>
+hipError_t launch_skt(const LoraArgs& p) {
+  const int spin = option(WSL_OPT_PREFILL_SHARED_T) == 1 ? 0 : kSktSpin;
+  return launch_cfg<C, kBF16, true, 1, false, false, false, false, false, false, false, true>(
+      p, nullptr, 0, 1, reinterpret_cast<uint64_t*>(p.ws), p.red_cnt, 1, spin);
 }
 
 // Column tiles per persistent strip for a launch of BM x BN tiles, or 1 (one tile per
@@ -1081,9 +1285,17 @@ int strip_tiles(const LoraArgs& p, int bm, int bn) {
 // 57.6.
 template <class C, int WDT, bool HAS_W, int RB, bool EXT_T, bool GATHER, bool WT = false>
 hipError_t launch_tiles(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int strips) {
+  constexpr bool SKT_FORM = WDT == kBF16 && HAS_W && RB == 1 && !EXT_T && !GATHER && !WT;
   if constexpr (std::is_same_v<C, CfgTall> && WDT == kBF16 && !GATHER && RB <= 1) {
-    if (strips <= 1)
+    if (strips <= 1) {
+      if constexpr (SKT_FORM) {
+        if (shared_t_rbgs(p, CfgTall3::BM, CfgTall3::BN) > 0) return launch_skt<CfgTall3>(p);
+      }
       return launch_cfg<CfgTall3, WDT, HAS_W, RB, EXT_T, GATHER, false, false, false, false, WT>(p, tg, ldt);
+    }
+  }
+  if constexpr (std::is_same_v<C, CfgBig> && SKT_FORM) {
+    if (strips <= 1 && shared_t_rbgs(p, C::BM, C::BN) > 0) return launch_skt<CfgBig>(p);
   }
   if constexpr (WDT == kBF16 && HAS_W && RB > 0 && !EXT_T && !GATHER && C::NS == 2) {
     if (strips > 1)
@@ -1490,6 +1702,8 @@ size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w
   }
   const int rs = red_splits(M, N, K, w_dtype, true, false);
   if (rs > 0) b = std::max(b, (size_t)(((M + 127) / 128) * ((N + 127) / 128) * rs) * red_record_bytes(r > 0));
+  // shared T: one rank block per group (r here is the groups' total rank)
+  if (r > 0 && r <= 32 * kMaxGroups) b = std::max(b, shared_t_bytes(M, N, K));
   return b;
 }
 
@@ -1574,6 +1788,18 @@ hipError_t launch_product_tn(const LoraArgs& p, int64_t tokens, float* part, int
   return launch_cfg<CfgSmall, kBF16, true, 0, false, false, true, true>(q, nullptr, 0, splits);
 }
 
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int v = cus[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 // The form, tile and splits a prefill call takes; launch_prefill follows it.
 PrefillPlan plan_prefill(const LoraArgs& p) {
   PrefillPlan pl;
@@ -1620,6 +1846,8 @@ PrefillPlan plan_prefill(const LoraArgs& p) {
     pl.tile_m = tile_rows(t.tile);
     pl.tile_n = tile_cols(t.tile);
     pl.strips = t.strips;
+    pl.shared_t = has_w && p.w_dtype == kBF16 && pl.rank_blocks == 1 && !pl.prepass && t.strips <= 1 &&
+                  (t.tile == Tile::kBig || t.tile == Tile::kTall) && shared_t_rbgs(p, pl.tile_m, pl.tile_n) > 0;
   }
   pl.workgroups = ((p.M + pl.tile_m - 1) / pl.tile_m) * ((p.N + pl.tile_n - 1) / pl.tile_n) / pl.strips;
   return pl;

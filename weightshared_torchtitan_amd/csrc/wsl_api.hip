@@ -362,6 +362,7 @@ int wsl_set_option(int32_t option, int64_t value) {
     case WSL_OPT_DECODE_PASSES: ok = value >= -1 && value <= 1; break;
     case WSL_OPT_DECODE_SPIN_LIMIT: ok = value >= -1 && value <= ((int64_t)1 << 30); break;
     case WSL_OPT_DECODE_RES_SPLITS: ok = value == 0 || (value >= 2 && value <= 8); break;
+    case WSL_OPT_PREFILL_SHARED_T: ok = value >= -1 && value <= 1; break;
     default: return fail(WSL_E_INVALID_ARG, "unknown option %d", (int)option);
   }
   if (!ok) return fail(WSL_E_INVALID_ARG, "value %lld out of range for option %d", (long long)value, (int)option);
@@ -396,6 +397,8 @@ int wsl_lora_linear_plan(int64_t M, int64_t K, int64_t r, int32_t n_groups, cons
                               al, K, al, r, 2.f, const_cast<void*>(al), N, M, N, K, r, nullptr);
   p.fp8_terms = terms;
   p.red_cnt = reinterpret_cast<unsigned*>(const_cast<void*>(al));
+  p.ws = const_cast<void*>(al);  // a workspace of the size the size query reports
+  p.ws_bytes = SIZE_MAX;
   p.groups = n_groups;
   int64_t end = 0;
   for (int g = 0; g < n_groups; ++g) p.gend[g] = (end += group_n[g]);
@@ -418,6 +421,7 @@ int wsl_lora_linear_plan(int64_t M, int64_t K, int64_t r, int32_t n_groups, cons
       out->tile_n = pl.tile_n;
       out->rank_blocks = pl.rank_blocks;
       out->rank_prepass = pl.prepass ? 1 : 0;
+      out->shared_t = pl.shared_t ? 1 : 0;
       out->strip_tiles = pl.strips;
       out->k_splits = pl.splits;
       out->workgroups = (int32_t)pl.workgroups;

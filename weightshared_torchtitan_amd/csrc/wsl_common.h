@@ -149,6 +149,9 @@ struct LoraArgs {
 // Path overrides (WSL_OPT_* of include/wsl_lora.h): 0 unless wsl_set_option changed them.
 int64_t option(int id);
 
+// Compute units of the current device (cached per device; 0 when it cannot be read).
+int device_cus();
+
 // The prefill path's choice for a call (csrc/lora_prefill.hip), shared by the launcher and
 // wsl_lora_linear_plan: form (WSL_PATH_PREFILL*), tile, in-loop rank blocks, pre-pass T,
 // persistent strip length, K splits and the main launch's workgroups.
@@ -160,6 +163,7 @@ struct PrefillPlan {
   int strips = 1;
   int splits = 1;
   int64_t workgroups = 0;
+  bool shared_t = false;
 };
 PrefillPlan plan_prefill(const LoraArgs& p);
 
