@@ -1213,7 +1213,10 @@ hipError_t launch_cfg(const LoraArgs& p, const uint16_t* tg, int64_t ldt, int sp
 // ---- Shared T (the SKT form) ----
 // Records of one row block and group: kShareClasses classes x 8 waves x 64 lanes x 8 words.
 constexpr size_t kSktRbgBytes = (size_t)kShareClasses * 8 * 64 * 8 * 8;
-constexpr int kSktSpin = 1 << 16;  // polls of the row block's counter before a tile computes T itself
+// Polls of the row block's counter (each a memory round trip and a short sleep, 1 us or
+// more) before a tile computes T itself: milliseconds, against the few microseconds the
+// tiles of one wave finish apart.
+constexpr int kSktSpin = 1 << 12;
 // K tiles from which sharing pays: the exchange (the classes out and arrived, the counter
 // seen, the classes read: about 3.5 us with the tiles' skew) against three quarters of T's
 // MFMAs (1/9 of the loop's). Alternating graphs of 28 launches, shared against T in every
