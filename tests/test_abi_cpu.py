@@ -557,6 +557,10 @@ def test_options_set_get_and_refuse():
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_strips"], 1) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], -1) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], 3) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(N.OPTIONS["prefill_shared_t"], 2) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(N.OPTIONS["prefill_shared_t"], -2) == N.WSL_E_INVALID_ARG
+        N.set_option("prefill_shared_t", 1)
+        assert N.get_option("prefill_shared_t") == 1
         assert N.lib().wsl_set_option(99, 0) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(0, 0) == N.WSL_E_INVALID_ARG
         assert N.get_option("prefill_split") == 4
@@ -589,6 +593,18 @@ def test_plan_of_benchmark_launches(M, K, r, groups, path, tile, rb, strips, wgs
     assert p["path"] == path and (p["tile_m"], p["tile_n"]) == tile
     assert p["rank_blocks"] == rb and p["strip_tiles"] == strips and p["workgroups"] == wgs
     assert p["launches"] == 1 and p["k_splits"] == 1 and p["rank_prepass"] == 0
+
+
+@needs_lib
+def test_plan_shared_t_needs_a_device():
+    """Shared T is taken for one wave of tiles on the current device, so the plan reads the
+    device's CU count: on a host without a GPU it is never reported (the GPU tests assert
+    where it is taken)."""
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is visible: tests/test_gpu_shared_t.py covers the plan there")
+    assert N.plan(8192, 6144, 32, (2048,))["shared_t"] == 0
+    assert N.plan(8192, 4096, 32, (1024,))["shared_t"] == 0
 
 
 @needs_lib
