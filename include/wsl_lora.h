@@ -301,7 +301,7 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
  *                              block); -1 T in every
  *                              tile; 1 shared, with every tile taking the no-wait path (it
  *                              computes the classes of T from global memory: bit-exact
- *                              with 0)
+ *                              with 0); 2 shared at any K (one-wave launches)
  * wsl_set_option returns WSL_E_INVALID_ARG for an unknown option or a value out of range.
  */
 #define WSL_OPT_PREFILL_STRIPS 1

@@ -557,7 +557,7 @@ def test_options_set_get_and_refuse():
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_strips"], 1) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], -1) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], 3) == N.WSL_E_INVALID_ARG
-        assert N.lib().wsl_set_option(N.OPTIONS["prefill_shared_t"], 2) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(N.OPTIONS["prefill_shared_t"], 3) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_shared_t"], -2) == N.WSL_E_INVALID_ARG
         N.set_option("prefill_shared_t", 1)
         assert N.get_option("prefill_shared_t") == 1

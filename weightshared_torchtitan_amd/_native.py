@@ -111,7 +111,7 @@ OPTIONS = {
     "decode_wide": 6,        # -1: 65-72 tokens on the prefill path
     "decode_spin_limit": 7,  # n > 0: poll bound of the decode hand-offs; -1: no polling
     "decode_res_splits": 8,  # 2..8: K splits of the decode step's residual-epilogue launches
-    "prefill_shared_t": 9,   # -1: T in every tile; 1: shared T with every tile on the no-wait path
+    "prefill_shared_t": 9,   # -1: T in every tile; 1: shared T, every tile on the no-wait path; 2: at any K
 }
 
 # wsl_plan_info.path values

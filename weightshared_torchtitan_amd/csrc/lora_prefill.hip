@@ -821,11 +821,14 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       }
       wait_vm0();  // the class is out before the arrival
       __syncthreads();
-      if (tid == 0) __hip_atomic_fetch_add(pub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (tid == 0) {
       int seen = 0;
-      for (int it = 0; it < skt_spin; ++it) {
+      // a publisher that arrives last has seen every class arrive before its own
+      if (skt_cls >= 0)
+        seen = __hip_atomic_fetch_add(pub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(CL - 1) &&
+               skt_spin > 0;
+      for (int it = 0; !seen && it < skt_spin; ++it) {
         if (__hip_atomic_load(pub, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= (unsigned)CL) {
           seen = 1;
           break;
@@ -883,15 +886,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         }
       }
     }
-    wait_vm0();  // every read of the classes has returned
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == (unsigned)(skt_ntiles - 1)) {  // the row block's last: counters back to zero
-        __hip_atomic_store(pub, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    (void)done;  // passed at the end of the tile (skt_pass), off the path to the stores
   }
 
   if constexpr (RED) {
@@ -1087,6 +1082,22 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     return;
   }
 
+  // SKT: this tile is past its reads of the classes (they returned before T was parked);
+  // the row block's last tile to pass returns both counters to zero. Thread 0 waits for the
+  // counter's round trip after its stores are issued, where nothing waits on it.
+  auto skt_pass = [&]() {
+    if constexpr (SKT) {
+      if (tid == 0) {
+        unsigned* const pub = red_cnt + 2 * skt_rbg;
+        const unsigned old = __hip_atomic_fetch_add(pub + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == (unsigned)(skt_ntiles - 1)) {
+          __hip_atomic_store(pub, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(pub + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  };
+
   // ---- store. The accumulators hold 4 consecutive n of one m per lane and group, i.e.
   // 16-byte pieces of 32 different rows per wave instruction; written straight to y
   // they reach L2 as partial lines. The tile is staged through LDS (row stride OS) and
@@ -1137,6 +1148,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
       __builtin_nontemporal_store(v[i], reinterpret_cast<u32x4_t*>(y + (int64_t)(m0 + q / CPR) * ldy + n0 + (q % CPR) * 8));
     }
     WSL_STAMP(srec, 5);
+    skt_pass();
     return;
   }
 #pragma unroll 4
@@ -1158,6 +1170,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
   WSL_STAMP(srec, 5);
+  skt_pass();
   };  // do_tile
 
   if constexpr (PER) {
@@ -1218,20 +1231,24 @@ constexpr size_t kSktRbgBytes = (size_t)kShareClasses * 8 * 64 * 8 * 8;
 // tiles of one wave finish apart.
 constexpr int kSktSpin = 1 << 12;
 // K tiles from which sharing pays: the exchange (the classes out and arrived, the counter
-// seen, the classes read: about 3.5 us with the tiles' skew) against three quarters of T's
+// seen, the classes read: about 3 us with the tiles' skew) against three quarters of T's
 // MFMAs (1/9 of the loop's). Alternating graphs of 28 launches, shared against T in every
-// tile: 8192 x 6144 -> 2048 (96 K tiles) 163.2 against 173.4 us; 8192 x 3072 -> 1024 (48)
-// 55.5 / 55.9; 8192 x 2048 -> 2048 (32) 65.4 / 65.3; 8192 x 2048 -> 1024 (32) 40.9 / 40.0.
+// tile, two orders on one box: 8192 x 6144 -> 2048 (96 K tiles) 164.0 / 163.2 against
+// 172.5 / 173.3 us; 8192 x 3072 -> 1024 (48) 55.4 / 56.2 against 56.8 / 56.2; 8192 x 2048
+// -> 2048 (32) 63.1 / 63.4 against 63.5 / 63.6; 8192 x 2048 -> 1024 (32) 40.0 / 40.1
+// against 39.5 / 39.3.
 constexpr int kSktMinKTiles = 64;
 
 // Row-block groups of a launch of BM x BN tiles that shares T between the column tiles of
 // each row block, or 0 where it does not: a long K (kSktMinKTiles), one wave of tiles on
 // this device (every workgroup resident at once, so the wait for the other tiles' classes
 // is short), at least kShareClasses tiles in every group, the arrival counters, and room in
-// the workspace for the records. WSL_OPT_PREFILL_SHARED_T = -1 keeps T in every tile.
+// the workspace for the records. WSL_OPT_PREFILL_SHARED_T = -1 keeps T in every tile; 2
+// drops the K bound (side-by-side timing of the shorter launches).
 int64_t shared_t_rbgs(const LoraArgs& p, int bm, int bn) {
-  if (option(WSL_OPT_PREFILL_SHARED_T) < 0 || p.red_cnt == nullptr || p.ws == nullptr) return 0;
-  if (p.K / BK < kSktMinKTiles) return 0;
+  const int64_t opt = option(WSL_OPT_PREFILL_SHARED_T);
+  if (opt < 0 || p.red_cnt == nullptr || p.ws == nullptr) return 0;
+  if (p.K / BK < kSktMinKTiles && opt != 2) return 0;
   const int64_t tiles_m = (p.M + bm - 1) / bm, tiles_n = (p.N + bn - 1) / bn;
   const int cus = device_cus();
   if (cus <= 0 || tiles_m * tiles_n > cus) return 0;
@@ -1250,7 +1267,7 @@ int64_t shared_t_rbgs(const LoraArgs& p, int bm, int bn) {
 // its 128 x 256 tiles are row-block groups (every group has at least four tiles), and only
 // when those tiles are one wave on this device.
 size_t shared_t_bytes(int64_t M, int64_t N, int64_t K) {
-  if (K / BK < kSktMinKTiles) return 0;
+  if (K / BK < kSktMinKTiles && option(WSL_OPT_PREFILL_SHARED_T) != 2) return 0;
   const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256);
   const int cus = device_cus();
   return (cus > 0 && tiles <= cus) ? (size_t)((tiles + kShareClasses - 1) / kShareClasses) * kSktRbgBytes : 0;

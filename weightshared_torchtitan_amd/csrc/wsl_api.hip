@@ -362,7 +362,7 @@ int wsl_set_option(int32_t option, int64_t value) {
     case WSL_OPT_DECODE_PASSES: ok = value >= -1 && value <= 1; break;
     case WSL_OPT_DECODE_SPIN_LIMIT: ok = value >= -1 && value <= ((int64_t)1 << 30); break;
     case WSL_OPT_DECODE_RES_SPLITS: ok = value == 0 || (value >= 2 && value <= 8); break;
-    case WSL_OPT_PREFILL_SHARED_T: ok = value >= -1 && value <= 1; break;
+    case WSL_OPT_PREFILL_SHARED_T: ok = value >= -1 && value <= 2; break;
     default: return fail(WSL_E_INVALID_ARG, "unknown option %d", (int)option);
   }
   if (!ok) return fail(WSL_E_INVALID_ARG, "value %lld out of range for option %d", (long long)value, (int)option);
