@@ -140,3 +140,25 @@ def test_shared_t_graph_replays(gpu):
         assert torch.equal(out, want), f"replay {i}"
         _run(gpu, x2, W2, A2, B2, 2.0)  # another shared-T launch between replays
         torch.cuda.synchronize()
+
+
+def test_shared_t_at_any_k_for_timing(gpu):
+    """WSL_OPT_PREFILL_SHARED_T = 2 takes the shared form below 4096 too (the side-by-side
+    timings of config 2's o): the plan reports it, and the output is within the bar of T in
+    every tile and of the oracle."""
+    from weightshared_torchtitan_amd import _native, ops
+    M, N, K, r = 8192, 1024, 2048, 32
+    assert ops.plan(M, K, r, [N])["shared_t"] == 0
+    _native.set_option("prefill_shared_t", 2)
+    try:
+        assert ops.plan(M, K, r, [N])["shared_t"] == 1
+    finally:
+        _native.set_option("prefill_shared_t", 0)
+    x, Ws, As, Bs = _inputs(M, (N,), K, r, seed=17)
+    y = _with_option(2, lambda: _run(gpu, x, Ws, As, Bs, 2.0))
+    y_every = _with_option(-1, lambda: _run(gpu, x, Ws, As, Bs, 2.0))
+    assert O.max_rel_err(y.cpu().float().numpy(), y_every.cpu().float().numpy()) <= BF16_TOL
+    rows = sorted({min(b + o, M - 1) for b in range(0, M, 128) for o in (0, 127)})
+    f = lambda t: t.float().numpy()  # noqa: E731
+    ref = O.lora_linear(f(x[rows]), f(Ws[0]), f(As[0]), f(Bs[0]), 2.0)
+    assert O.max_rel_err(f(y.cpu()[rows]), ref) <= BF16_TOL
