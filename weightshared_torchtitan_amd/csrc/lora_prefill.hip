@@ -804,8 +804,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     constexpr int CL = kShareClasses;
     static_assert(TPW == 1, "shared T: one T block per T wave");
     auto part_of = [&](int c) { return red_part + (((int64_t)skt_rbg * CL + c) * C::NW + wave) * (8 * 64) + lane; };
-    unsigned* const pub = red_cnt + 2 * skt_rbg;
-    unsigned* const done = pub + 1;
+    unsigned* const pub = red_cnt + 2 * skt_rbg;  // the arrivals; pub + 1 counts the passes (skt_pass)
     // broadcast word: the W area of the buffer the last K tile ran from (idle now; T is
     // parked below its first BM rows)
     volatile int* skt_seen = reinterpret_cast<volatile int*>(lora_t + C::XB);
@@ -886,7 +885,6 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         }
       }
     }
-    (void)done;  // passed at the end of the tile (skt_pass), off the path to the stores
   }
 
   if constexpr (RED) {
