@@ -66,6 +66,7 @@ CASES = [
     ("ragged M, rank 24", 8000, (1024,), 4096, 24, (128, 256)),
     ("two groups", 4096, (1024, 1024), 4096, 32, (128, 256)),
     ("q|k|v-like groups", 2048, (2048, 1024, 1024), 4096, 16, (128, 256)),
+    ("four groups, rank 8", 2048, (1024, 1024, 1024, 1024), 4096, 8, (128, 256)),
 ]
 
 
