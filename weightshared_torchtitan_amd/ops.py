@@ -49,7 +49,8 @@ def path_options(**opts: int):
 
 def plan(M: int, K: int, r: int, group_n, fp8: bool = False) -> dict:
     """The kernel plan libwsl takes for a (grouped) LoRA linear of these sizes on dense,
-    aligned operands: path, launches, tile, in-loop rank blocks, pre-pass, strips, K splits."""
+    aligned operands: path, launches, tile, in-loop rank blocks, pre-pass, strips, K splits,
+    workgroups, and whether the column tiles share T (shared_t)."""
     return _native.plan(M, K, r, list(group_n), _fp8_code() if fp8 else _native.WSL_DTYPE_BF16)
 
 
