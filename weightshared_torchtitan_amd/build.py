@@ -86,42 +86,58 @@ def build_library(verbose: bool = False, jobs: int | None = None, incremental: b
 
 
 STAMPS_LIB_PATH = os.path.join(PKG_DIR, "libwsl_stamps.so")
+TEMPORAL_LIB_PATH = os.path.join(PKG_DIR, "libwsl_temporal.so")
 
 
-def build_stamps_library(verbose: bool = False) -> str:
-    """libwsl_stamps.so: libwsl with the prefill and decode kernels built with -DWSL_STAMPS
-    (per-phase wall-clock stamps of every workgroup, read back by ``wsl_prefill_stamps`` and
-    ``wsl_decode_stamps``), for ``bench.py --only stamps`` run with WSL_LIB pointing at it.
-    The other objects are the ones of the last ``build_library``; the product library is
-    left as it is."""
+def _variant_library(define: str, names: tuple, suffix: str, out: str, verbose: bool) -> str:
+    """libwsl with the sources `names` compiled with -D`define` (objects `<name>_<suffix>.o`)
+    and the other objects of the last ``build_library``; the product library is left as it is."""
     hipcc = _hipcc()
     if not os.path.exists(LIB_PATH):
         build_library(verbose=verbose)
-    inst = ("lora_prefill.hip", "lora_decode.hip")
 
-    def stamped(name: str) -> str:
+    def compiled(name: str) -> str:
         src = os.path.join(CSRC, name)
-        obj = os.path.join(BUILD_DIR, name[:-4] + "_stamps.o")
-        cmd = [hipcc, *HIPCC_FLAGS, "-DWSL_STAMPS", f"-I{INCLUDE_DIR}", f"-I{CSRC}", "-c", src, "-o", obj]
+        obj = os.path.join(BUILD_DIR, name[:-4] + f"_{suffix}.o")
+        cmd = [hipcc, *HIPCC_FLAGS, f"-D{define}", f"-I{INCLUDE_DIR}", f"-I{CSRC}", "-c", src, "-o", obj]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src}:\n{res.stdout}\n{res.stderr}")
         return obj
 
-    with ThreadPoolExecutor(max_workers=len(inst)) as ex:
-        stamped_objs = list(ex.map(stamped, inst))
+    with ThreadPoolExecutor(max_workers=len(names)) as ex:
+        variant_objs = list(ex.map(compiled, names))
     objs = [os.path.join(BUILD_DIR, os.path.basename(s)[:-4] + ".o") for s in sources()
-            if os.path.basename(s) not in inst] + stamped_objs
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", STAMPS_LIB_PATH]
+            if os.path.basename(s) not in names] + variant_objs
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", out]
+    if verbose:
+        print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    return STAMPS_LIB_PATH
+    return out
+
+
+def build_stamps_library(verbose: bool = False) -> str:
+    """libwsl_stamps.so: libwsl with the prefill and decode kernels built with -DWSL_STAMPS
+    (per-phase wall-clock stamps of every workgroup, read back by ``wsl_prefill_stamps`` and
+    ``wsl_decode_stamps``), for ``bench.py --only stamps`` run with WSL_LIB pointing at it."""
+    return _variant_library("WSL_STAMPS", ("lora_prefill.hip", "lora_decode.hip"), "stamps", STAMPS_LIB_PATH,
+                            verbose)
+
+
+def build_temporal_library(verbose: bool = False) -> str:
+    """libwsl_temporal.so: libwsl with the prefill kernel's output stores through the caches
+    (-DWSL_TEMPORAL_STORES) instead of non-temporal, for side-by-side timing with WSL_LIB
+    pointing at it."""
+    return _variant_library("WSL_TEMPORAL_STORES", ("lora_prefill.hip",), "temporal", TEMPORAL_LIB_PATH, verbose)
 
 
 if __name__ == "__main__":
     if "--stamps" in sys.argv:
         print(build_stamps_library(verbose="-v" in sys.argv))
+    elif "--temporal-stores" in sys.argv:
+        print(build_temporal_library(verbose="-v" in sys.argv))
     else:
         path = build_library(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv)
         print(path)

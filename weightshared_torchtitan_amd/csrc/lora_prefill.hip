@@ -129,6 +129,18 @@ __device__ __forceinline__ void lds_write16(char* base, int off, u32x4_t v) {
   *reinterpret_cast<u32x4_t*>(base + off) = v;
 }
 
+// A 16-byte chunk of the output: a non-temporal store (y is written once and not read by
+// the launch; streamed past the caches it leaves the lines the next launch reads in place).
+// Builds with -DWSL_TEMPORAL_STORES (libwsl_temporal.so, for side-by-side timing) store it
+// through the caches instead.
+__device__ __forceinline__ void store_y16(u32x4_t v, u32x4_t* p) {
+#ifdef WSL_TEMPORAL_STORES
+  *p = v;
+#else
+  __builtin_nontemporal_store(v, p);
+#endif
+}
+
 // A lane offset the compiler must treat as computed here: left visible, the loop-invariant
 // zero-extension of each 32-bit offset is hoisted into a live 64-bit register pair, and
 // every fill then adds it with a 64-bit VALU op instead of using the uniform-base +
@@ -1143,7 +1155,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int q = i * NT + tid;
-      __builtin_nontemporal_store(v[i], reinterpret_cast<u32x4_t*>(y + (int64_t)(m0 + q / CPR) * ldy + n0 + (q % CPR) * 8));
+      store_y16(v[i], reinterpret_cast<u32x4_t*>(y + (int64_t)(m0 + q / CPR) * ldy + n0 + (q % CPR) * 8));
     }
     WSL_STAMP(srec, 5);
     skt_pass();
@@ -1158,7 +1170,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     uint16_t* dst = y + (int64_t)m * ldy + n;
     if (n + 8 <= N) {
       if (a16) {
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
+        store_y16(v, reinterpret_cast<u32x4_t*>(dst));
       } else {
         reinterpret_cast<uint2*>(dst)[0] = uint2{v[0], v[1]};
         reinterpret_cast<uint2*>(dst)[1] = uint2{v[2], v[3]};
