@@ -619,17 +619,17 @@ def bench_medium(dev, steps, warmup):
     """Medium M (above the decode path's fused forms, up to a thousand tokens) at the
     Qwen3-1.7B projection shapes, r = 64, cold weights (6 rotating copies), 28 layers per
     graph, grouped q|k|v and gate|up, each way the library can run them on the same inputs:
-    the decode path's wide form (the default up to 72 tokens), the prefill path's in-launch
-    split-K form (the decode_wide override at -1 below 73 tokens; the default above) and its
-    unsplit tiles (also prefill_split and prefill_medium at -1, which keep the split forms
-    off); from 128 tokens also torch.matmul (hipBLASLt) on the same
+    the decode path (the default up to 64 tokens; its wide form from 65 to 72 with the
+    decode_wide override at 1), the prefill path's in-launch split-K form (the default from 65
+    tokens) and its unsplit tiles (prefill_split and prefill_medium at -1, which keep the
+    split forms off); from 128 tokens also torch.matmul (hipBLASLt) on the same
     inputs: the plain GEMM on the stacked weights (no LoRA term) and the unfused three-call
     LoRA linear (the reference's arithmetic)."""
     from weightshared_torchtitan_amd import ops
     out = {}
-    ways = (("decode", {}),
-            ("split_k", {"decode_wide": -1}),
-            ("unsplit", {"decode_wide": -1, "prefill_split": -1, "prefill_medium": -1}))
+    ways = (("decode", {"decode_wide": 1}),
+            ("split_k", {}),
+            ("unsplit", {"prefill_split": -1, "prefill_medium": -1}))
     for M in (64, 65, 72, 96, 128, 160, 192, 256, 512, 1024):
         row = {}
         for label, opts in ways:

@@ -141,10 +141,10 @@ int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx,
  * gate/up (qwen3/model/model.py:250-251). The groups run as one launch where every group
  * boundary falls on the launch's work grid: on the prefill path, whole output tiles
  * (multiples of 128; of 256 for ranks 33-64), each tile taking its group's rank block; on
- * the decode path (M <= 64; plain bf16 up to 72), whole row groups of W (multiples of 64
+ * the decode path (M <= 64; plain bf16 up to 72 with WSL_OPT_DECODE_WIDE), whole row groups of W (multiples of 64
  * suffice), the T work covering all groups' A rows. Otherwise the groups run as consecutive
  * launches on `stream`. Results are those of the per-group calls, bit for bit, except where
- * a K split count depends on N (the decode path between 65 and 72 tokens; the prefill
+ * a K split count depends on N (the decode path's wide form; the prefill
  * path's in-launch split-K form, taken where 128 x 128 tiles leave CUs idle), where the
  * column tiles of a launch share T (WSL_OPT_PREFILL_SHARED_T; one wave of tiles) or, for an fp8
  * W on prefill shapes, where the choice between the fp8 matrix cores and W decoded onto the
@@ -290,7 +290,8 @@ int wsl_factorized_embedding_fwd(const int64_t* ids, int64_t n_ids,
  *                              onto the bf16 matrix cores); 1 always decoded; 2 always the
  *                              fp8 matrix cores
  *   WSL_OPT_DECODE_PASSES      0 auto; -1 K splits only; 1 passes wherever the slices allow
- *   WSL_OPT_DECODE_WIDE        0 auto; -1 keep 65-72 tokens on the prefill path
+ *   WSL_OPT_DECODE_WIDE        0 or -1: 65-72 tokens on the prefill path (the default); 1 the
+ *                              decode path's wide form for plain bf16 launches of 65-72 tokens
  *   WSL_OPT_DECODE_SPIN_LIMIT  0 the default poll bound of the decode hand-offs; n > 0 that
  *                              bound; -1 no polling (the local fallback runs at once)
  *   WSL_OPT_DECODE_RES_SPLITS  0 auto; n in [2, 8] at least n K splits for the decode step's

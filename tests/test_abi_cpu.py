@@ -527,19 +527,17 @@ def test_workspace_bytes_of_wide_decode_shapes(M, K):
     (160, 12288, 2048, 64, 0),  # 192 tiles: no split
 ])
 def test_workspace_bytes_of_split_k_shapes(M, Nn, K, r, splits):
-    """The in-launch split-K form's records (8 waves x 64 lanes x 24 words of 8 bytes per tile
-    and split, 16 words without T) fit in the prefill half of the workspace the size query
-    asks for, single and grouped (the grouped query cannot see the per-group rank, so it
-    counts the T words)."""
+    """The in-launch split-K form's records (8 waves x 64 lanes x 16 words of 8 bytes per tile
+    and split: the output partial, the LoRA term included) fit in the prefill half of the
+    workspace the size query asks for, single and grouped."""
     tiles = ((M + 127) // 128) * ((Nn + 127) // 128)
-    words = 24 if r else 16
-    need = tiles * splits * 8 * 64 * words * 8
+    need = tiles * splits * 8 * 64 * 16 * 8
     half = lambda b: ((b - 65536) // 2) & ~255
     single = N.workspace_bytes(M, Nn, K, r, N.WSL_DTYPE_BF16)
     assert half(single) >= need
     if r:
         grouped = N.grouped_workspace_bytes(M, K, r, (Nn // 2, Nn // 4, Nn // 4), N.WSL_DTYPE_BF16)
-        assert half(grouped) >= tiles * splits * 8 * 64 * 24 * 8
+        assert half(grouped) >= need
 
 
 @needs_lib
@@ -555,6 +553,9 @@ def test_options_set_get_and_refuse():
         assert N.get_option("prefill_split") == 4
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_split"], 17) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_strips"], 1) == N.WSL_E_INVALID_ARG
+        assert N.lib().wsl_set_option(N.OPTIONS["decode_wide"], 2) == N.WSL_E_INVALID_ARG
+        N.set_option("decode_wide", 1)
+        assert N.get_option("decode_wide") == 1
         assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], -1) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["fp8_prefill"], 3) == N.WSL_E_INVALID_ARG
         assert N.lib().wsl_set_option(N.OPTIONS["prefill_shared_t"], 3) == N.WSL_E_INVALID_ARG

@@ -1,8 +1,9 @@
-"""The decode path from 65 to 72 tokens (plain bf16 launches): five token blocks, four
-waves along K, x walked in pass slices of 512 or 1024 columns, the slices spread over the K
-splits that keep one wave of workgroups. Against the float64 oracle (1e-2), bitwise
-repeatable, with the T wait forced to its local fallback, beside the prefill path
-(the decode_wide override at -1) on the same inputs, and as grouped launches. The K split count
+"""The decode path's wide form from 65 to 72 tokens (plain bf16 launches, taken with the
+decode_wide override at 1; by default these shapes run on the prefill path's split-K form):
+five token blocks, four waves along K, x walked in pass slices of 512 or 1024 columns, the
+slices spread over the K splits that keep one wave of workgroups. Against the float64 oracle
+(1e-2), bitwise repeatable, with the T wait forced to its local fallback, beside the prefill
+path (the default) on the same inputs, and as grouped launches. The K split count
 fills one wave of workgroups, so it depends on N: a grouped launch may sum a group's rows in
 another order than the group's single launch, and the two agree within the bar (below 65
 tokens they agree bit for bit)."""
@@ -50,7 +51,7 @@ CASES = [
 @pytest.mark.parametrize("M,N,K,r", CASES)
 def test_wide_decode_matches_oracle(gpu, M, N, K, r, wsl_opts):
     import weightshared_torchtitan_amd as wsl
-    wsl_opts(decode_wide=0)
+    wsl_opts(decode_wide=1)
     _say(f"[decode wide] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=5 * M + N + K + r)
     d = lambda t: None if t is None else t.to(gpu)
@@ -62,8 +63,8 @@ def test_wide_decode_matches_oracle(gpu, M, N, K, r, wsl_opts):
     err = O.max_rel_err(y1.float().cpu().numpy(), ref)
     _say(f"  max_rel_err={err:.3e}")
     assert np.isfinite(err) and err <= BF16_TOL
-    # the medium form of the prefill path on the same inputs: same bar, a different kernel
-    wsl_opts(decode_wide=-1)
+    # the prefill path's split-K form (the default) on the same inputs: same bar, a different kernel
+    wsl_opts(decode_wide=0)
     y3 = wsl.lora_linear(d(x), d(W), d(A), d(B), 2.0)
     torch.cuda.synchronize()
     assert O.max_rel_err(y3.float().cpu().numpy(), ref) <= BF16_TOL
@@ -72,7 +73,7 @@ def test_wide_decode_matches_oracle(gpu, M, N, K, r, wsl_opts):
 def test_wide_decode_t_fallback(gpu, wsl_opts):
     """T wait bound forced to zero from the host: the W workgroups compute T themselves."""
     import weightshared_torchtitan_amd as wsl
-    wsl_opts(decode_wide=0)
+    wsl_opts(decode_wide=1)
     M, N, K, r = 72, 2048, 6144, 64
     _say(f"[decode wide T fallback] M={M} N={N} K={K} r={r}")
     x, W, A, B = _inputs(M, N, K, r, seed=53)
@@ -94,7 +95,7 @@ def test_wide_decode_t_fallback(gpu, wsl_opts):
 def test_wide_decode_grouped_matches_single(gpu, M, K, group_n, wsl_opts):
     import weightshared_torchtitan_amd as wsl
     from weightshared_torchtitan_amd import ops
-    wsl_opts(decode_wide=0)
+    wsl_opts(decode_wide=1)
     r = 64
     _say(f"[decode wide grouped] M={M} K={K} r={r} groups={group_n}")
     g = torch.Generator().manual_seed(M + K + len(group_n))

@@ -430,9 +430,12 @@ def test_decode_counters_return_to_zero_and_deterministic(gpu):
 
 @pytest.mark.parametrize("M,N,K,r", [(4, 1024, 2048, 32), (64, 2048, 6144, 64), (64, 6144, 2048, 64),
                                      (72, 2048, 6144, 64)])
-def test_decode_in_graph_replays_match_eager(gpu, M, N, K, r):
-    """Captured decode calls replay correctly several times (counters reset per replay)."""
+def test_decode_in_graph_replays_match_eager(gpu, M, N, K, r, wsl_opts):
+    """Captured decode calls replay correctly several times (counters reset per replay);
+    72 tokens on the decode path's wide form (the decode_wide override at 1)."""
     import weightshared_torchtitan_amd as wsl
+    if M > 64:
+        wsl_opts(decode_wide=1)
     _say(f"[decode graph] M={M} N={N} K={K} r={r}, 3 replays")
     x, W, A, B = (t.to(gpu) for t in _inputs(M, N, K, r, seed=23))
     eager = wsl.lora_linear(x, W, A, B, 2.0)

@@ -68,7 +68,7 @@ def _noalloc(dev, x, W, A, B, s):
 CASES = [
     # (first shape, second smaller shape): M, N, K, r
     ((64, 1024, 4096, 64), (8, 1024, 4096, 64)),      # decode path, K split (partials + T words)
-    ((72, 2048, 6144, 64), (64, 6144, 2048, 64)),     # wide decode form (splits of passes), then two passes
+    ((72, 2048, 6144, 64), (64, 6144, 2048, 64)),     # prefill split-K at 72 tokens, then two decode passes
     ((256, 2048, 2048, 64), (160, 1024, 6144, 32)),   # prefill in-launch split-K (arrival counters in the scratch)
     ((4, 2048, 2048, 32), (1, 2048, 2048, 32)),       # decode path, one slice
     ((1024, 768, 1024, 128), (512, 768, 1024, 128)),  # prefill rank pre-pass with split partials
@@ -103,3 +103,15 @@ def test_noalloc_repeated_decode_calls_stay_equal(gpu):
     for it in range(30):
         dev_t, want = data[it % len(data)]
         assert torch.equal(_noalloc(gpu, *dev_t, 2.0), want), f"call {it}"
+
+
+def test_noalloc_wide_decode_form(gpu, wsl_opts):
+    """The decode path's wide form (72 tokens, taken with the decode_wide override at 1:
+    splits of passes, their partials and T words in the scratch), then a smaller call."""
+    wsl_opts(decode_wide=1)
+    for i, (M, N_, K, r) in enumerate(((72, 2048, 6144, 64), (66, 3072, 1024, 16))):
+        _say(f"[noalloc wide] call {i}: M={M} N={N_} K={K} r={r}")
+        x, W, A, B = _inputs(M, N_, K, r, seed=3 * M + K)
+        xd, Wd, Ad, Bd = (t.to(gpu) for t in (x, W, A, B))
+        want = _with_workspace(gpu, xd, Wd, Ad, Bd, 2.0)
+        assert torch.equal(_noalloc(gpu, xd, Wd, Ad, Bd, 2.0), want)

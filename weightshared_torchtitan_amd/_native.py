@@ -108,7 +108,7 @@ OPTIONS = {
     "prefill_medium": 3,     # -1: never the medium-M split form
     "fp8_prefill": 4,        # 0: by launch width; 1: fp8 W decoded onto the bf16 matrix cores; 2: fp8 matrix cores
     "decode_passes": 5,      # -1: K splits only; 1: passes wherever the slices allow
-    "decode_wide": 6,        # -1: 65-72 tokens on the prefill path
+    "decode_wide": 6,        # 1: 65-72 tokens on the decode path's wide form
     "decode_spin_limit": 7,  # n > 0: poll bound of the decode hand-offs; -1: no polling
     "decode_res_splits": 8,  # 2..8: K splits of the decode step's residual-epilogue launches
     "prefill_shared_t": 9,   # -1: T in every tile; 1: shared T, every tile on the no-wait path; 2: at any K

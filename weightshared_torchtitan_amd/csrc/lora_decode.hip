@@ -1470,8 +1470,9 @@ bool decode_supported(const LoraArgs& p) {
   if (p.M < 1 || p.M > kDecodePlainMaxM) return false;
   if (p.M > kDecodeMaxM) {
     if (p.w_dtype != kBF16) return false;  // fp8 base above 64 tokens: the prefill path
-    // WSL_OPT_DECODE_WIDE = -1 keeps 65-72 tokens on the prefill path (side-by-side timing)
-    if (option(WSL_OPT_DECODE_WIDE) < 0) return false;
+    // 65-72 tokens run on the prefill path's split-K form; WSL_OPT_DECODE_WIDE = 1 takes
+    // the wide form here instead (side-by-side timing)
+    if (option(WSL_OPT_DECODE_WIDE) <= 0) return false;
   }
   if (p.w == nullptr) return false;  // the delta-only form runs on the prefill path
   if (p.N > (int64_t)1 << 30 || p.K > (int64_t)1 << 30) return false;

@@ -66,9 +66,11 @@ constexpr int kShareClasses = KK;  // shared T (SKT): classes of T's k steps, k 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Phase timestamps, in instrumented builds only (-DWSL_STAMPS, libwsl_stamps.so): record
-// `rec` (workgroup b's tile q of a strip: 4 b + min(q, 3)) slot k gets the 100 MHz constant
+// `rec` (workgroup b's tile q of a strip: 4 b + min(q, 3), b counting the splits of a
+// split-K launch as blockIdx.x * gridDim.y + blockIdx.y) slot k gets the 100 MHz constant
 // clock when the workgroup's first thread passes phase k: 0 tile start, 1 first K tile
-// landed, 2 K loop done, 3 LoRA up-projection done, 4 output staged in LDS, 5 stores issued.
+// landed, 2 K loop done, 3 LoRA up-projection done (split-K: before the reduction), 4 output
+// staged in LDS, 5 stores issued.
 #ifdef WSL_STAMPS
 constexpr int kStampRecs = 4096;
 __device__ unsigned long long g_prefill_stamps[kStampRecs * 8];
@@ -322,7 +324,8 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   const int tn = ((t % group_size) / gm) * SW + tq;
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
-  const int srec = (int)blockIdx.x * 4 + (tq < 3 ? tq : 3);  // phase-stamp record
+  // phase-stamp record (split-K launches: one per tile and split)
+  const int srec = ((int)blockIdx.x * (int)gridDim.y + (int)blockIdx.y) * 4 + (tq < 3 ? tq : 3);
   (void)srec;
   WSL_STAMP(srec, 0);
   // whether this tile computes T in its K loop (every tile but a strip's later ones)
@@ -899,98 +902,6 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
   }
 
-  if constexpr (RED) {
-    // This split's partials: lane-major 8-byte words (two accumulators each), the base
-    // block first, then the T block of a T wave; agent-scope stores, so the reducing
-    // workgroup (on any XCD) reads them from memory rather than from a stale L2 line.
-    constexpr int EB = C::NI * C::MJ * 8;
-    constexpr int ET = RB > 0 ? TPW * 8 : 0;
-    constexpr int EW = EB + ET;
-    const int S = (int)gridDim.y;
-    const int64_t first = (int64_t)blockIdx.x * S;  // the tile's split 0 record
-    auto rec = [&](int q) { return red_part + ((first + q) * C::NW + wave) * (int64_t)(EW * 64) + lane; };
-    auto pk = [](float lo, float hi) {
-      return (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
-    };
-    {
-      uint64_t* dst = rec(blockIdx.y);
-#pragma unroll
-      for (int i = 0; i < C::NI; ++i)
-#pragma unroll
-        for (int j = 0; j < C::MJ; ++j)
-#pragma unroll
-          for (int v = 0; v < 8; ++v)
-            __hip_atomic_store(dst + ((i * C::MJ + j) * 8 + v) * 64, pk(acc[i][j][2 * v], acc[i][j][2 * v + 1]),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if constexpr (RB > 0) {
-        if (t_wave) {
-#pragma unroll
-          for (int q = 0; q < TPW; ++q)
-#pragma unroll
-            for (int v = 0; v < 8; ++v)
-              __hip_atomic_store(dst + (EB + q * 8 + v) * 64, pk(acct[q][2 * v], acct[q][2 * v + 1]),
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
-    // the flag goes in the W area of the buffer the last K tile ran from (idle now; T is
-    // parked below its first BM rows, and a separate __shared__ word would take the
-    // 128 x 128 tile with two rank blocks past half the LDS, one workgroup per CU)
-    volatile int* red_last = reinterpret_cast<volatile int*>(lora_t + C::XB);
-    wait_vm0();  // the records are out before the arrival
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned old = __hip_atomic_fetch_add(red_cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const bool last = old == (unsigned)(S - 1);
-      if (last) __hip_atomic_store(red_cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *red_last = last ? 1 : 0;
-    }
-    __syncthreads();
-    if (*red_last == 0) return;
-    // the last split: every record, in split order (this one's own included), one split's
-    // words in flight at a time
-    for (int q = 0; q < S; ++q) {
-      const uint64_t* src = rec(q);
-      uint64_t wb[EB];
-#pragma unroll
-      for (int e = 0; e < EB; ++e)
-        wb[e] = __hip_atomic_load(const_cast<uint64_t*>(src + e * 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      uint64_t wt[ET > 0 ? ET : 1];
-      if constexpr (RB > 0) {
-        if (t_wave) {
-#pragma unroll
-          for (int e = 0; e < ET; ++e)
-            wt[e] = __hip_atomic_load(const_cast<uint64_t*>(src + (EB + e) * 64), __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < C::NI; ++i)
-#pragma unroll
-        for (int j = 0; j < C::MJ; ++j)
-#pragma unroll
-          for (int v = 0; v < 8; ++v) {
-            const uint64_t u = wb[(i * C::MJ + j) * 8 + v];
-            const float lo = __uint_as_float((uint32_t)u), hi = __uint_as_float((uint32_t)(u >> 32));
-            acc[i][j][2 * v] = q == 0 ? lo : acc[i][j][2 * v] + lo;
-            acc[i][j][2 * v + 1] = q == 0 ? hi : acc[i][j][2 * v + 1] + hi;
-          }
-      if constexpr (RB > 0) {
-        if (t_wave) {
-#pragma unroll
-          for (int qq = 0; qq < TPW; ++qq)
-#pragma unroll
-            for (int v = 0; v < 8; ++v) {
-              const uint64_t u = wt[qq * 8 + v];
-              const float lo = __uint_as_float((uint32_t)u), hi = __uint_as_float((uint32_t)(u >> 32));
-              acct[qq][2 * v] = q == 0 ? lo : acct[qq][2 * v] + lo;
-              acct[qq][2 * v + 1] = q == 0 ? hi : acct[qq][2 * v + 1] + hi;
-            }
-        }
-      }
-    }
-  }
-
   // ---- per-output-channel dequantisation scale (fp8 base; WT applied it when decoding) ----
   if constexpr (W8 && !WT) {
 #pragma unroll
@@ -1070,6 +981,83 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
   }
 
   WSL_STAMP(srec, 3);
+  if constexpr (RED) {
+    // This split's output partial (its K part of the base product and of the LoRA term, the
+    // latter through its own part of T: the up-projection is linear in T) as lane-major
+    // 8-byte words, two accumulators each; agent-scope stores, so the reducing workgroup
+    // (on any XCD) reads them from memory rather than from a stale L2 line.
+    constexpr int EB = C::NI * C::MJ * 8;
+    const int S = (int)gridDim.y;
+    const int own = (int)blockIdx.y;
+    const int64_t first = (int64_t)blockIdx.x * S;  // the tile's split 0 record
+    auto rec = [&](int q) { return red_part + ((first + q) * C::NW + wave) * (int64_t)(EB * 64) + lane; };
+    {
+      uint64_t* dst = rec(own);
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::MJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            __hip_atomic_store(dst + ((i * C::MJ + j) * 8 + v) * 64,
+                               (uint64_t)__float_as_uint(acc[i][j][2 * v]) |
+                                   ((uint64_t)__float_as_uint(acc[i][j][2 * v + 1]) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // the flag goes in the ring (idle: the up-projection's last barrier ended its use)
+    volatile int* red_last = reinterpret_cast<volatile int*>(lds);
+    wait_vm0();  // the record is out before the arrival
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned old = __hip_atomic_fetch_add(red_cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == (unsigned)(S - 1);
+      if (last) __hip_atomic_store(red_cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *red_last = last ? 1 : 0;
+    }
+    __syncthreads();
+    const bool last = *red_last != 0;
+    __syncthreads();  // every wave has the flag before the output staging reuses its word
+    if (!last) return;
+    // the last split: every split's partial in split order, its own from the registers
+    // (the same values it stored), the others' one record's words in flight at a time
+    f32x16_t sum[C::NI][C::MJ];
+    for (int q = 0; q < S; ++q) {
+      f32x16_t part[C::NI][C::MJ];
+      if (q == own) {
+#pragma unroll
+        for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+          for (int j = 0; j < C::MJ; ++j) part[i][j] = acc[i][j];
+      } else {
+        const uint64_t* src = rec(q);
+        uint64_t wb[EB];
+#pragma unroll
+        for (int e = 0; e < EB; ++e)
+          wb[e] = __hip_atomic_load(const_cast<uint64_t*>(src + e * 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+          for (int j = 0; j < C::MJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+              const uint64_t u = wb[(i * C::MJ + j) * 8 + v];
+              part[i][j][2 * v] = __uint_as_float((uint32_t)u);
+              part[i][j][2 * v + 1] = __uint_as_float((uint32_t)(u >> 32));
+            }
+      }
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::MJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sum[i][j][v] = q == 0 ? part[i][j][v] : sum[i][j][v] + part[i][j][v];
+    }
+#pragma unroll
+    for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+      for (int j = 0; j < C::MJ; ++j) acc[i][j] = sum[i][j];
+  }
+
   if constexpr (SPLIT) {
     // fp32 partials straight from the accumulators: lane pairs (lh) cover 8 consecutive
     // n of one row, the four groups g a whole 128-byte line, merged in L2.
@@ -1560,9 +1548,10 @@ int medium_splits(int64_t M, int64_t N, int64_t K, int64_t rt, int w_dtype, bool
 // ---- Split-K in one launch (the RED form of prefill_kernel over 128 x 128 tiles) ----
 // For shapes whose 128 x 128 tiles leave most CUs idle (few rows of tokens, or narrow N),
 // K is cut into S equal parts over a second grid dimension. Each split runs the fused K
-// loop (T included) over its part and leaves fp32 partial records; the last split of a tile
-// sums them in split order and finishes the tile. One launch, no pre-pass: T comes from the
-// same K loops. The split count fills at most one workgroup per CU (the deep ring's LDS
+// loop (T included) over its part, applies its part of T through B (the up-projection is
+// linear in T) and leaves an fp32 record of its output partial; the last split of a tile
+// sums the partials in split order (its own from registers) and stores the tile. One
+// launch, no pre-pass: T comes from the same K loops. The split count fills at most one workgroup per CU (the deep ring's LDS
 // takes a whole CU; allowing two per CU measured the same), keeps at least kRedMinTiles K
 // tiles per split, divides the K tile count and keeps the records within their budget (the
 // no-allocation scratch holds them).
@@ -1570,10 +1559,8 @@ constexpr int kRedMaxSplits = 16;
 constexpr int kRedMinTiles = 8;  // 1.7B layer at M = 129-256: 8 K tiles per split 7-8 % ahead of 4
 constexpr size_t kRedPartBytes = (size_t)24 << 20;
 
-// Bytes of one (tile, split) record: 8 waves x 64 lanes x (16 base words + 8 T words).
-size_t red_record_bytes(bool lora) {
-  return (size_t)CfgDeep::NW * 64 * 8 * (CfgDeep::NI * CfgDeep::MJ * 8 + (lora ? 8 : 0));
-}
+// Bytes of one (tile, split) record: 8 waves x 64 lanes x 16 words (the output partial).
+size_t red_record_bytes() { return (size_t)CfgDeep::NW * 64 * 8 * (CfgDeep::NI * CfgDeep::MJ * 8); }
 
 int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool gather) {
   if (!has_w || gather || w_dtype != kBF16 || M < 1) return 0;
@@ -1582,7 +1569,7 @@ int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool ga
   if (tiles > kRedMaxTiles) return 0;
   const int64_t f = option(WSL_OPT_PREFILL_SPLIT);  // off, or a forced split count (side-by-side timing)
   if (f < 0) return 0;
-  if (f >= 2 && f <= kRedMaxSplits && nk % f == 0 && (size_t)(tiles * f) * red_record_bytes(true) <= kRedPartBytes)
+  if (f >= 2 && f <= kRedMaxSplits && nk % f == 0 && (size_t)(tiles * f) * red_record_bytes() <= kRedPartBytes)
     return (int)f;
   // At 97-128 tiles the unsplit launch already covers half the CUs: splitting in two paid
   // only over long K (M x N x K = 1024 x 2048 x 6144: 52.4 against 62.8 us; 2048 x 1024 x
@@ -1591,7 +1578,7 @@ int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool ga
   if (tiles > 96 && nk < 64) return 0;
   int s = 1;
   while (s * 2 <= kRedMaxSplits && nk % (s * 2) == 0 && nk / (s * 2) >= kRedMinTiles && tiles * s * 2 <= 256) s *= 2;
-  while (s > 1 && (size_t)(tiles * s) * red_record_bytes(true) > kRedPartBytes) s /= 2;
+  while (s > 1 && (size_t)(tiles * s) * red_record_bytes() > kRedPartBytes) s /= 2;
   return s > 1 ? s : 0;
 }
 
@@ -1731,7 +1718,7 @@ size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w
     b = std::max(b, t_bytes + (size_t)ms * M * N * 4);
   }
   const int rs = red_splits(M, N, K, w_dtype, true, false);
-  if (rs > 0) b = std::max(b, (size_t)(((M + 127) / 128) * ((N + 127) / 128) * rs) * red_record_bytes(r > 0));
+  if (rs > 0) b = std::max(b, (size_t)(((M + 127) / 128) * ((N + 127) / 128) * rs) * red_record_bytes());
   // shared T: one rank block per group (r here is the groups' total rank)
   if (r > 0 && r <= 32 * kMaxGroups) b = std::max(b, shared_t_bytes(M, N, K));
   return b;

@@ -355,8 +355,8 @@ int wsl_set_option(int32_t option, int64_t value) {
   bool ok;
   switch (option) {
     case WSL_OPT_PREFILL_STRIPS:
-    case WSL_OPT_PREFILL_MEDIUM:
-    case WSL_OPT_DECODE_WIDE: ok = value == 0 || value == -1; break;
+    case WSL_OPT_PREFILL_MEDIUM: ok = value == 0 || value == -1; break;
+    case WSL_OPT_DECODE_WIDE: ok = value >= -1 && value <= 1; break;
     case WSL_OPT_PREFILL_SPLIT: ok = value == 0 || value == -1 || (value >= 2 && value <= 16); break;
     case WSL_OPT_FP8_PREFILL: ok = value >= 0 && value <= 2; break;
     case WSL_OPT_DECODE_PASSES: ok = value >= -1 && value <= 1; break;

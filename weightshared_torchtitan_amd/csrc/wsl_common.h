@@ -247,10 +247,10 @@ hipError_t launch_factorized_embedding(const int64_t* ids, int64_t n_ids, const 
                                        hipStream_t stream);
 
 // Largest M routed to the decode-shaped (skinny) kernels: every form (fused, fp8 base, the
-// greedy head) up to kDecodeMaxM, the plain bf16 form up to kDecodePlainMaxM (five token
-// blocks, four waves along K, x walked in passes). Past 72 tokens the prefill path's
-// in-launch split-K form is faster (1.7B layer, grouped: 2.60 against 2.63 ms at 72 tokens,
-// 2.67 against 2.64 at 80, 2.88 against 2.66 at 96).
+// greedy head) up to kDecodeMaxM; the plain bf16 wide form (five token blocks, four waves
+// along K, x walked in passes) up to kDecodePlainMaxM only when WSL_OPT_DECODE_WIDE asks for
+// it: the prefill path's in-launch split-K form is faster from 65 tokens (1.7B layer,
+// grouped: 2.24 against 2.46 ms at 65 tokens, 2.25 against 2.61 at 72).
 constexpr int64_t kDecodeMaxM = 64;
 constexpr int64_t kDecodePlainMaxM = 72;
 
