@@ -423,7 +423,8 @@ def bench_stamps(dev, names=None):
     """Where a prefill tile's time goes, from the instrumented library's per-workgroup
     wall-clock stamps (WSL_LIB=<repo>/weightshared_torchtitan_amd/libwsl_stamps.so, built by
     `python -m weightshared_torchtitan_amd.build --stamps`). One launch per shape of
-    AB_SHAPES after three warm-up launches; per tile of a strip (q = 0, 1, ...) the median and
+    AB_SHAPES (and of MEDIUM_STAMP_SHAPES) after three warm-up launches; per tile of a strip
+    (q = 0, 1, ...), or for split-K launches per last split and other splits, the median and
     maximum over workgroups of each phase's duration (us at the 100 MHz constant clock), the
     spread of tile starts, and the span from the first start to the last store beside the
     HIP-event time of the same launch."""
@@ -439,10 +440,9 @@ def bench_stamps(dev, names=None):
     recs = 4096
     buf = np.zeros(recs * 8, dtype=np.uint64)
     out = {}
-    for name, M, ns, K in AB_SHAPES:
+    for name, M, ns, K, r in [(*sh, 32) for sh in AB_SHAPES] + MEDIUM_STAMP_SHAPES:
         if names is not None and name not in names:
             continue
-        r = 32
         g = torch.Generator(device=dev).manual_seed(M + sum(ns) + K)
         x = torch.randn(M, K, device=dev, generator=g).bfloat16()
         w = (torch.randn(sum(ns), K, device=dev, generator=g) * 0.02).bfloat16()
@@ -468,24 +468,39 @@ def bench_stamps(dev, names=None):
         st = buf.reshape(recs, 8).astype(np.int64)
         valid = st[:, 0] > 0
         t0 = st[valid, 0].min()
-        res = {"event_us": round(e0.elapsed_time(e1) * 1e3, 2),
+        plan = ops.plan(M, K, r, list(ns))
+        res = {"plan": {k: plan[k] for k in ("path", "tile_m", "tile_n", "k_splits", "workgroups")},
+               "event_us": round(e0.elapsed_time(e1) * 1e3, 2),
                "span_us": round((st[valid, 5].max() - t0) / 100.0, 2)}
-        for q in range(4):
-            rows = st[(np.arange(recs) % 4 == q) & valid]
+        if plan["k_splits"] > 1:
+            # split-K: the last split of each tile runs every phase (the reduction falls in
+            # "stage"); the others stop after the up-projection of their own part
+            groups = [("last_split", valid & (st[:, 5] > 0), len(STAMP_PHASES)),
+                      ("other_splits", valid & (st[:, 5] == 0), 3)]
+        else:
+            groups = [(f"tile{q}", (np.arange(recs) % 4 == q) & valid, len(STAMP_PHASES)) for q in range(4)]
+        for label, sel, nph in groups:
+            rows = st[sel]
             if len(rows) == 0:
                 continue
             d = {"workgroups": int(len(rows)),
                  "start_after_first_us": [round(float(np.median(rows[:, 0] - t0)) / 100, 2),
                                           round(float((rows[:, 0] - t0).max()) / 100, 2)]}
-            for k, ph in enumerate(STAMP_PHASES, start=1):
+            for k, ph in enumerate(STAMP_PHASES[:nph], start=1):
                 dd = (rows[:, k] - rows[:, k - 1]) / 100.0
                 d[ph + "_us"] = [round(float(np.median(dd)), 2), round(float(dd.max()), 2)]
-            res[f"tile{q}"] = d
+            res[label] = d
         out[name] = res
         del x, w, a, b
     if names is None or any(n in names for n, *_ in DECODE_STAMP_SHAPES):
         out.update(decode_stamps(dev, lib, names))
     return out
+
+
+# Medium-M launches (1.7B shapes, r = 64, the in-launch split-K form) for the prefill
+# kernel's phase stamps: name, M, group widths, K, rank.
+MEDIUM_STAMP_SHAPES = [("1.7b q|k|v M=256", 256, (2048, 1024, 1024), 2048, 64),
+                       ("1.7b down M=512", 512, (2048,), 6144, 64)]
 
 
 # Decode launches (config 3 shapes, r = 64) for the decode kernel's phase stamps: name, M,
@@ -1054,7 +1069,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--ab", default='{"default": {}, "strips_off": {"prefill_strips": -1}}',
                     help="--only envab: JSON {mode: {option: value}} of the path overrides timed side by side")
-    ap.add_argument("--ab-shapes", default=None, help="--only envab / stamps: comma-separated names from AB_SHAPES")
+    ap.add_argument("--ab-shapes", default=None, help="--only envab / stamps: comma-separated names from AB_SHAPES (stamps: also "
+                         "MEDIUM_STAMP_SHAPES, DECODE_STAMP_SHAPES)")
     ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",
                     help="a libwsl path override for the whole run (ops.path_options names), repeatable")
     args = ap.parse_args()

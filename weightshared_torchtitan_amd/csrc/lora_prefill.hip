@@ -752,6 +752,7 @@ prefill_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     if (nk >= NS) wait_vm<(NS - 1) * PT>();  // tile 0 has landed
     else wait_vm0();
     ring_barrier();
+    WSL_STAMP(srec, 1);
     Frags cur;
     frag_load(t_at(do_t, cls, K0{}), 0, 0, cur);
     int buf = 0;
