@@ -806,6 +806,40 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
                 total += e0.elapsed_time(e1)
         return total / steps
 
+    def graphed(fwd, grads):
+        """The GPU time of the backward without the host's launch work: forward + backward
+        captured as one HIP graph and the forward alone as another (both after eager warm-ups
+        on the capture stream, gradients allocated by the capture); the backward is the
+        difference of their mean replay times."""
+        def step():
+            ys = fwd()
+            torch.autograd.backward(ys, [grads[i % len(grads)] for i in range(len(ys))])
+
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                for t in params:
+                    t.grad = None
+                step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        for t in params:
+            t.grad = None
+        g_fb, g_f = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_fb, stream=s):
+            step()
+        with torch.cuda.graph(g_f, stream=s):
+            fwd()
+        torch.cuda.synchronize()
+        t_fb = time_replays(g_fb, steps, warmup)
+        t_f = time_replays(g_f, steps, warmup)
+        del g_fb, g_f
+        for t in params:
+            t.grad = None
+        torch.cuda.synchronize()
+        return t_fb - t_f, t_f
+
     fl = layers * sum(lora_backward_flops(M, N, K, r) for _, N, K in QWEN3_0P6B)
     out = {"layers": layers, "M": M, "r": r}
     for name, fwd, grads in (("wsl_fused", fused, gys), ("wsl_grouped_qkv_gateup", grouped, ggys),
@@ -813,6 +847,14 @@ def bench_backward(dev, steps, warmup, layers=4, M=8192, r=32):
         ms = timed(fwd, grads)
         out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
                      "frac_mfma": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+        try:
+            gms, fms = graphed(fwd, grads)
+            out[name].update({"graph_ms": round(gms, 4), "graph_TFLOP/s": round(fl / gms / 1e9, 1),
+                              "graph_frac_mfma": round(fl / gms / 1e9 / BF16_PEAK_TFLOPS, 4),
+                              "graph_forward_ms": round(fms, 4)})
+        except RuntimeError as e:  # a capture the path does not support: the eager figure stands
+            torch.cuda.synchronize()
+            out[name]["graph_error"] = str(e)[:200]
     from weightshared_torchtitan_amd import ops
 
     def torch_weight_grads(x2, gy2, a, b, s):
