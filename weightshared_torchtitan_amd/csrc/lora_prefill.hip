@@ -1572,11 +1572,12 @@ int red_splits(int64_t M, int64_t N, int64_t K, int w_dtype, bool has_w, bool ga
   if (f < 0) return 0;
   if (f >= 2 && f <= kRedMaxSplits && nk % f == 0 && (size_t)(tiles * f) * red_record_bytes() <= kRedPartBytes)
     return (int)f;
-  // At 97-128 tiles the unsplit launch already covers half the CUs: splitting in two paid
-  // only over long K (M x N x K = 1024 x 2048 x 6144: 52.4 against 62.8 us; 2048 x 1024 x
-  // 1024: 18.1 against 14.1, 1024 x 2048 x 2048: 27.0 against 25.6, 512 x 4096 x 2048: 26.7
-  // against 24.9). At 96 tiles (gate|up at 128 tokens) it still paid.
-  if (tiles > 96 && nk < 64) return 0;
+  // At 97-128 tiles the unsplit launch already covers half the CUs: splitting in two pays
+  // from 24 K tiles (1.7B shapes, r = 64, us per launch in graphs of 28, cold weights:
+  // M x N x K = 1024 x 2048 x 2048 21.8 against 23.8 unsplit, 896 x 2048 x 2048 21.2 against
+  // 23.8, 1024 x 2048 x 1536 18.8 against 19.5; 1024 x 2048 x 1024 16.2 against 14.9 and
+  // 2048 x 1024 x 1024 16.0 against 14.9). At 96 tiles (gate|up at 128 tokens) it pays.
+  if (tiles > 96 && nk < 24) return 0;
   int s = 1;
   while (s * 2 <= kRedMaxSplits && nk % (s * 2) == 0 && nk / (s * 2) >= kRedMinTiles && tiles * s * 2 <= 256) s *= 2;
   while (s > 1 && (size_t)(tiles * s) * red_record_bytes() > kRedPartBytes) s /= 2;
