@@ -146,10 +146,12 @@ int wsl_lora_linear_fwd_noalloc(const void* x, int64_t ldx,
  * launches on `stream`. Results are those of the per-group calls, bit for bit, except where
  * a K split count depends on N (the decode path's wide form; the prefill
  * path's in-launch split-K form, taken where 128 x 128 tiles leave CUs idle), where the
- * column tiles of a launch share T (WSL_OPT_PREFILL_SHARED_T; one wave of tiles) or, for an fp8
- * W on prefill shapes, where the choice between the fp8 matrix cores and W decoded onto the
- * bf16 matrix cores depends on the launch's width (WSL_OPT_FP8_PREFILL): there the groups'
- * outputs agree with the per-group calls within the forward's bar.
+ * column tiles of a launch share T (WSL_OPT_PREFILL_SHARED_T; one wave of tiles), where T
+ * comes from the rank pre-pass (ranks above 64, and ranks 33-64 where it frees a tile wider
+ * than 128 x 128, which depends on N; its K split count follows all groups' ranks) or, for an
+ * fp8 W on prefill shapes, where the choice between the fp8 matrix cores and W decoded onto
+ * the bf16 matrix cores depends on the launch's width (WSL_OPT_FP8_PREFILL): there the
+ * groups' outputs agree with the per-group calls within the forward's bar.
  */
 #define WSL_MAX_GROUPS 4
 int wsl_lora_linear_grouped_workspace_bytes(int64_t M, int64_t K, int64_t r, int32_t n_groups,

@@ -658,3 +658,22 @@ def test_plan_paths_by_size():
         N.set_option("fp8_prefill", 0)
     p = N.plan(4096, 4096, 128, (4096,))
     assert p["path"] == "prefill" and p["rank_prepass"] == 1 and p["rank_blocks"] == 0
+
+
+@needs_lib
+@pytest.mark.parametrize("M,K,r,groups,prepass,tile", [
+    (8192, 2048, 64, (6144, 6144), 1, (256, 256)),   # 1.7B gate|up: T from the pre-pass frees 256 x 256
+    (1024, 2048, 64, (6144, 6144), 1, (256, 192)),
+    (512, 2048, 48, (6144, 6144), 1, (128, 256)),
+    (256, 2048, 64, (6144, 6144), 0, (128, 128)),    # 128 x 128 either way: T in the loop
+    (1024, 2048, 64, (2048, 1024, 1024), 0, (128, 128)),
+    (8192, 2048, 32, (6144, 6144), 0, (256, 256)),   # one rank block: always in the loop
+])
+def test_plan_rank_33_to_64_takes_the_prepass_for_wider_tiles(M, K, r, groups, prepass, tile):
+    """Ranks 33-64 take T from the rank pre-pass wherever that lets the launch use a tile
+    wider than 128 x 128 (two in-loop rank blocks fit only 128 x 256 and 128 x 128)."""
+    p = N.plan(M, K, r, groups)
+    assert p["path"] == "prefill" and p["rank_prepass"] == prepass and (p["tile_m"], p["tile_n"]) == tile
+    assert p["rank_blocks"] == (0 if prepass else (1 if r <= 32 else 2))
+    if prepass:  # the size query covers the pre-pass's T and split partials
+        assert N.grouped_workspace_bytes(M, K, r, groups, N.WSL_DTYPE_BF16) >= 65536 + 2 * M * r * len(groups) * 2

@@ -126,3 +126,43 @@ def test_bcast_backward_above_rank_limit(gpu):
         err = O.max_rel_err(got.grad.float().cpu().numpy(), want.grad.numpy())
         _say(f"   {name}: max_rel_err {err:.2e}")
         assert np.isfinite(err) and err <= BF16_TOL, name
+
+
+@pytest.mark.parametrize("M,K,r,group_n", [
+    (8192, 2048, 64, (6144, 6144)),        # 1.7B gate|up, 256 x 256 tiles
+    (1024, 2048, 64, (6144, 6144)),        # 256 x 192 tiles
+    (2000, 1024, 40, (2048, 1024, 1024)),  # ragged M, rank 40
+])
+def test_rank_33_to_64_from_the_prepass(gpu, M, K, r, group_n):
+    """Ranks 33-64 on tiles wider than 128 x 128: T from the rank pre-pass over all groups,
+    the K loop without rank work. Each group against the oracle on rows of every 128-row
+    block, and the grouped launch against the single-group calls within the bar."""
+    from weightshared_torchtitan_amd import ops
+    _say(f"[rank 33-64 pre-pass] M={M} K={K} r={r} groups={group_n}")
+    p = ops.plan(M, K, r, list(group_n))
+    assert p["path"] == "prefill" and p["rank_prepass"] == 1 and p["rank_blocks"] == 0 and p["launches"] == 1
+    g = torch.Generator().manual_seed(M + K + r)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    Ws = [(torch.randn(n, K, generator=g) * 0.02).bfloat16() for n in group_n]
+    As = [(torch.randn(r, K, generator=g) * 0.02).bfloat16() for _ in group_n]
+    Bs = [(torch.randn(n, r, generator=g) * 0.02).bfloat16() for n in group_n]
+    d = lambda t: t.to(gpu)  # noqa: E731
+    y = ops.lora_linear_grouped_op(d(x), d(torch.cat(Ws)), None, d(torch.cat(As)), d(torch.cat(Bs)), 2.0,
+                                   list(group_n))
+    y2 = ops.lora_linear_grouped_op(d(x), d(torch.cat(Ws)), None, d(torch.cat(As)), d(torch.cat(Bs)), 2.0,
+                                    list(group_n))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    rows = sorted({min(b + o, M - 1) for b in range(0, M, 128) for o in (0, 61, 127)})
+    f = lambda t: t.float().numpy()  # noqa: E731
+    yc = y.cpu()
+    n0 = 0
+    for i, n in enumerate(group_n):
+        ref = O.lora_linear(f(x[rows]), f(Ws[i]), f(As[i]), f(Bs[i]), 2.0)
+        err = O.max_rel_err(f(yc[rows, n0:n0 + n]), ref)
+        ys = ops.lora_linear_op(d(x), d(Ws[i]), None, d(As[i]), d(Bs[i]), 2.0).cpu()
+        e_single = O.max_rel_err(f(yc[:, n0:n0 + n]), f(ys).astype("float64"))
+        _say(f"   group {i}: max_rel_err {err:.2e}, against the single call {e_single:.2e}")
+        assert np.isfinite(err) and err <= BF16_TOL
+        assert e_single <= BF16_TOL
+        n0 += n

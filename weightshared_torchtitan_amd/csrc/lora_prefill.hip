@@ -1407,15 +1407,34 @@ hipError_t launch_variant(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
   }
 }
 
-// In-loop rank blocks of a launch of rank r (0 above RIN: T from the pre-pass).
-int rank_blocks_of(int64_t r) { return r == 0 ? 0 : r <= 32 ? 1 : r <= RIN ? 2 : 0; }
+// Whether a launch's T comes from the rank pre-pass instead of its K loop: always above
+// RIN; for ranks 33-64 (two in-loop rank blocks, which fit only the 128 x 256 and 128 x 128
+// tiles and add a quarter or a half to their MFMAs) wherever T from the pre-pass lets the
+// launch take a wider tile than 128 x 128 (1.7B gate|up, r = 64, us per launch in graphs of
+// 28, cold weights: M = 8192 406.7 against 515.4 in the loop, 2048 123.2 against 132.5,
+// 1024 68.3 against 85.3 (256 x 192 tiles), 512 45.9 against 48.7 (128 x 256 both ways);
+// where both ways take 128 x 128 tiles the loop wins: M = 256 28.8 against 35.8, q|k|v at
+// 1024 30.3 against 36.7).
+bool prepass_rank(const LoraArgs& p) {
+  if (p.r > RIN) return true;
+  if (p.r <= 32 || p.w == nullptr || p.gather != nullptr) return false;
+  const Tile t = pick_tiles(p, (int)p.w_dtype, true, 0, true, false).tile;
+  return t != Tile::kSmall && t != Tile::kDeep;
+}
 
+// In-loop rank blocks of a launch (0 with T from the pre-pass).
+int rank_blocks_of(const LoraArgs& p) {
+  if (p.r == 0 || prepass_rank(p)) return 0;
+  return p.r <= 32 ? 1 : 2;
+}
+
+// tg: T from the pre-pass (prepass_rank), else nullptr and T in the K loop
 template <int WDT, bool HAS_W>
 hipError_t launch_rank(const LoraArgs& p, const uint16_t* tg, int64_t ldt) {
+  if (tg != nullptr) return launch_variant<WDT, HAS_W, 0, true>(p, tg, ldt);
   if (p.r == 0) return launch_variant<WDT, HAS_W, 0, false>(p, nullptr, 0);
   if (p.r <= 32) return launch_variant<WDT, HAS_W, 1, false>(p, nullptr, 0);
-  if (p.r <= RIN) return launch_variant<WDT, HAS_W, 2, false>(p, nullptr, 0);
-  return launch_variant<WDT, HAS_W, 0, true>(p, tg, ldt);
+  return launch_variant<WDT, HAS_W, 2, false>(p, nullptr, 0);
 }
 
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
@@ -1705,15 +1724,16 @@ hipError_t launch_medium(const LoraArgs& p, int splits) {
 }
 }  // namespace
 
-// Workspace of the prefill path: the rank pre-pass region (r > RIN, any rank on the fp8
-// matrix-core path or on the medium-M split path, which take T from the pre-pass), then for
+// Workspace of the prefill path: the rank pre-pass region (r > 32, where prepass_rank may
+// take it; any rank on the fp8 matrix-core path or on the medium-M split path, which take T
+// from the pre-pass), then for
 // an fp8 W the activation codes of the fp8 matrix-core path, or the medium path's partials.
 // With the in-launch split-K form possible (which `r`, the ranks of all groups, does not
 // decide) its records are covered as well.
 size_t prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t r, int w_dtype) {
   if (w_dtype == kFP8)
     return (r > 0 ? rank_prepass_bytes(M, K, r) : 0) + prefill_fp8_workspace_bytes(M, K, 2);
-  size_t b = r > RIN ? rank_prepass_bytes(M, K, r) : 0;
+  size_t b = r > 32 ? rank_prepass_bytes(M, K, r) : 0;
   const int ms = medium_splits(M, N, K, r, w_dtype, true, false);
   if (ms > 0) {
     const size_t t_bytes = r > 0 ? ((rank_prepass_bytes(M, K, r) + 255) & ~(size_t)255) : 0;
@@ -1846,7 +1866,7 @@ PrefillPlan plan_prefill(const LoraArgs& p) {
     if (rs > 0) {
       pl.form = WSL_PATH_PREFILL_SPLITK;
       pl.tile_m = pl.tile_n = 128;
-      pl.rank_blocks = rank_blocks_of(p.r);
+      pl.rank_blocks = p.r == 0 ? 0 : p.r <= 32 ? 1 : 2;
       pl.splits = rs;
       pl.workgroups = tiles128 * rs;
       return pl;
@@ -1859,8 +1879,8 @@ PrefillPlan plan_prefill(const LoraArgs& p) {
       pl.workgroups = tiles128 * ms;
       return pl;
     }
-    pl.prepass = p.r > RIN;
-    pl.rank_blocks = rank_blocks_of(p.r);
+    pl.prepass = p.r > 0 && prepass_rank(p);
+    pl.rank_blocks = rank_blocks_of(p);
     const TilePick t = pick_tiles(p, has_w ? (int)p.w_dtype : kBF16, has_w, pl.rank_blocks, pl.prepass, false);
     pl.tile_m = tile_rows(t.tile);
     pl.tile_n = tile_cols(t.tile);
@@ -1939,7 +1959,7 @@ hipError_t launch_prefill(const LoraArgs& p) {
   if (pl.form == WSL_PATH_PREFILL_MEDIUM) return launch_medium(p, pl.splits);
   const uint16_t* tg = nullptr;
   int64_t ldt = 0;
-  if (p.r > RIN) {
+  if (pl.prepass) {
     const hipError_t e = rank_prepass(p, t);
     if (e != hipSuccess) return e;
     tg = t;
