@@ -51,7 +51,9 @@ CASES = [
     (8192, 1024, 2048, 32),   # config 2 o
     (8192, 3072, 1024, 32),   # config 2 gate
     (8192, 1024, 3072, 32),   # config 2 down
-    (4096, 2048, 2048, 64),   # rank 33-64: two rank blocks, 128-row tiles
+    (4096, 2048, 2048, 64),   # rank 33-64 on 128 x 256 tiles: T from the rank pre-pass
+    (1024, 2048, 2048, 64),   # rank 33-64 on 128 x 128 tiles: two in-loop rank blocks
+    (8192, 6144, 2048, 48),   # rank 33-64 on 256 x 256 tiles (1.7B gate's dx): the pre-pass
     (2048, 1024, 1024, 128),  # T from the rank pre-pass
     (512, 1024, 1024, 0),     # no LoRA term
     (384, 512, 512, 16),      # 128 x 128 tiles

@@ -1927,7 +1927,14 @@ hipError_t launch_prefill_wt(const LoraArgs& q_in) {
   q.gather_rows = q.K;  // every reduction row of W' is in range: no clamping in its fills
   const uint16_t* tg = nullptr;
   int64_t ldt = 0;
-  if (q.r > RIN) {
+  // T from the pre-pass above RIN, and for ranks 33-64 where it frees a tile wider than
+  // 128 x 128 (as the forward's prepass_rank)
+  bool pre = q.r > RIN;
+  if (!pre && q.r > 32) {
+    const Tile t = pick_tiles(q, (int)q.w_dtype, true, 0, true, false, true).tile;
+    pre = t != Tile::kSmall && t != Tile::kDeep;
+  }
+  if (pre) {
     uint16_t* t = reinterpret_cast<uint16_t*>(q.ws);
     const hipError_t e = rank_prepass(q, t);
     if (e != hipSuccess) return e;
