@@ -1,8 +1,9 @@
 """Medium M: from 65 tokens the prefill path's in-launch split-K form (ranks up to 64)
-or, above rank 64 up to 160 tokens over long K, its medium split form (split-K base product, rank pre-pass, combine kernel); each against the
-float64 oracle, bar max|y - y_ref| / max|y_ref| <= 1e-2. Grouped launches against the single
-calls within the bar (the K split counts of both forms above 64 tokens depend on N). The
-shared-base form, and agreement across the M = 64 / 65 cut-over."""
+or, above rank 64 up to 160 tokens over long K, its medium split form (split-K base
+product, rank pre-pass, combine kernel); each against the float64 oracle, bar
+max|y - y_ref| / max|y_ref| <= 1e-2. Grouped launches against the single calls within the
+bar (the K split counts of both forms above 64 tokens depend on N). The shared-base form,
+and agreement across the M = 64 / 65 cut-over."""
 import sys
 
 import pytest
